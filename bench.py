@@ -1,0 +1,268 @@
+#!/usr/bin/env python
+"""SandMuon optimizer step on one MI355X: BASELINE cfg4 (103M GPT, 54 matrices).
+
+One "step" is the optimizer's whole hot path for one effective batch:
+the statistics hooks of 8 microbatches (16 x 1024 tokens each) followed by
+step() (finish statistics, AdamW on the 39.5M auxiliary parameters, and for
+the 54 matrices momentum -> whiten -> S8 -> mapback -> graft -> update).
+
+The hook bodies are driven directly with synthetic activations and
+cotangents of the shapes and dtypes a bf16-autocast GPT forward/backward
+hands them (LayerNorm-fed q/c_fc inputs in fp32, attention/GELU outputs and
+every cotangent in bf16), rotating over two sets of 4 GB so HBM, not the
+256 MB MALL, serves them.  Gradients are synthetic fp32.  No model forward
+or backward is timed.
+
+Prints one JSON line (driver contract) with `roofline` (dominant kernel) and
+`cpu_baseline` (the CPU oracle on a bounded sample, rank 0, N=1 only).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+METRIC = "optimizer step ms (103M GPT, 54 mats) + S8 GEMM MFMA %peak, 1 GPU"
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+BF16_PEAK = 2.5e15         # dense BF16 MFMA, FLOP/s
+FP32_PEAK = 157.3e12       # FP32 MFMA, FLOP/s
+TILE = 256
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="gpt103m", choices=["gpt103m", "gpt2048"])
+    ap.add_argument("--s8-mode", default="comp_bf16", choices=["comp_bf16", "fp32"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0: all cores in the affinity mask")
+    return ap.parse_args()
+
+
+# ------------------------------------------------------------ workload ---
+def build(cfg_name, mode, device):
+    from sandmuon_amd import RankOneAWeightedPE
+    from sandmuon_amd.workloads import GPT, GPT_103M, GPT_2048, transformer_filter
+    cfg = GPT_103M if cfg_name == "gpt103m" else GPT_2048
+    micro, mb_batch = (8, 16) if cfg_name == "gpt103m" else (4, 8)
+    model = GPT(cfg).to(device)
+    model.init_weights(1337)
+    opt = RankOneAWeightedPE(model, lr=1e-2, module_filter=transformer_filter, s8_mode=mode)
+    g = torch.Generator(device=device).manual_seed(1337)
+    for p in model.parameters():
+        p.grad = torch.randn(p.shape, generator=g, device=device) * 1e-3
+    rows = mb_batch * cfg.ctx
+    w, m = cfg.width, cfg.mlp
+    sets = []
+    for s in range(2):
+        a, b = [], []
+        for blk in model.transformer.h:
+            # Hook inputs under bf16 autocast: LayerNorm outputs stay fp32,
+            # the attention output and the GELU output are bf16.
+            a.append((blk.attn.q_proj.weight, torch.randn(rows, w, generator=g, device=device)))
+            a.append((blk.attn.c_proj.weight, torch.randn(rows, w, generator=g, device=device).bfloat16()))
+            a.append((blk.mlp.c_fc.weight, torch.randn(rows, w, generator=g, device=device)))
+            a.append((blk.mlp.c_proj.weight, torch.randn(rows, m, generator=g, device=device).bfloat16()))
+            for lin, width in ((blk.attn.q_proj, w), (blk.attn.k_proj, w), (blk.attn.v_proj, w),
+                               (blk.attn.c_proj, w), (blk.mlp.c_fc, m), (blk.mlp.c_proj, w)):
+                b.append((lin.weight, (torch.randn(rows, width, generator=g, device=device) * 1e-3).bfloat16()))
+        sets.append((a, b))
+    stat_bytes = sum(t.numel() * t.element_size() for _, t in sets[0][0] + sets[0][1]) * micro
+    return model, opt, sets, micro, stat_bytes
+
+
+def run_hooks(opt, sets, micro):
+    for k in range(micro):
+        a, b = sets[k % 2]
+        for p, x in a:
+            opt._accumulate_a(p, x)
+        for p, d in b:
+            opt._accumulate_b(p, d)
+
+
+def s8_flops(opt, mode):
+    """Logical S8 FLOPs 5(4 r^2 c + 2 r^3) and MFMA FLOPs the kernels issue."""
+    logical = issued = 0
+    for p in opt.named_matrices.values():
+        r, c = sorted(p.shape)
+        logical += 5 * (4 * r * r * c + 2 * r ** 3)
+        tm, tn = math.ceil(r / TILE), math.ceil(c / TILE)
+        rp, cp = tm * TILE, tn * TILE
+        sym = tm * (tm + 1) // 2
+        per_stage = 2 * TILE * TILE * (sym * cp + sym * rp + tm * tn * rp)
+        issued += 5 * per_stage * (3 if mode == "comp_bf16" else 1)
+    return logical, issued
+
+
+def time_events(fn, reps=1):
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def s8_only_time(opt, mode, device):
+    """One S8 pass over the step's matrices (same shape classes and
+    orientation), timed on the current stream."""
+    from sandmuon_amd import _native
+    from sandmuon_amd.optimizer import _s8_fp32
+    groups = {}
+    for p in opt.named_matrices.values():
+        groups.setdefault(tuple(p.shape), 0)
+        groups[tuple(p.shape)] += 1
+    xs = [torch.randn(n, *shape, device=device) for shape, n in groups.items()]
+    run = lambda: [_s8_fp32(x, mode=mode) for x in xs]
+    run()
+    torch.cuda.synchronize()
+    return time_events(run, reps=3)
+
+
+def stats_kernel_time(opt, sets):
+    """Sum of per-launch durations (events around each hook launch) for one
+    microbatch, and its bytes."""
+    a, b = sets[0]
+    evs = []
+    for p, x in a:
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(); opt._accumulate_a(p, x); e.record(); evs.append((s, e, x.numel() * x.element_size()))
+    for p, d in b:
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(); opt._accumulate_b(p, d); e.record(); evs.append((s, e, d.numel() * d.element_size()))
+    torch.cuda.synchronize()
+    ms = sum(s.elapsed_time(e) for s, e, _ in evs)
+    return ms, sum(n for *_, n in evs), len(evs)
+
+
+# -------------------------------------------------------- CPU baseline ---
+def cpu_baseline(cfg_name, threads):
+    """The CPU oracle (eager FP32 restatement of the reference) on a bounded
+    sample of the same workload, scaled to one step."""
+    from oracle import sandmuon_oracle as O
+    from sandmuon_amd.workloads import GPT, GPT_103M, GPT_2048, transformer_filter
+    torch.set_num_threads(threads)
+    cfg = GPT_103M if cfg_name == "gpt103m" else GPT_2048
+    micro, mb_rows = (8, 16 * 1024) if cfg_name == "gpt103m" else (4, 8 * 1024)
+    sample_rows = 2048
+    model = GPT(cfg)
+    model.init_weights(1337)
+    ora = O.OracleOptimizer(model, 1e-2, rank_one_a=True, module_filter=transformer_filter, hooks=False)
+    g = torch.Generator().manual_seed(7)
+    for p in model.parameters():
+        p.grad = torch.randn(p.shape, generator=g) * 1e-3
+    # Hooks: one microbatch sample of `sample_rows` rows per hooked tensor.
+    t_hooks = 0.0
+    for name, p in ora.matrices.items():
+        own = ora.a_source[id(p)] is p
+        x = torch.randn(sample_rows, p.shape[1], generator=g)
+        if "c_proj" in name:
+            x = x.bfloat16()
+        d = torch.randn(sample_rows, p.shape[0], generator=g).bfloat16()
+        t0 = time.perf_counter()
+        ora.feed(name, x=x if own else None, delta=d)
+        t_hooks += time.perf_counter() - t0
+    hooks_per_step = t_hooks * (mb_rows / sample_rows) * micro
+    t0 = time.perf_counter()
+    ora.step()
+    t_step = time.perf_counter() - t0
+    sample = (f"hook statistics on {sample_rows} rows of every hooked tensor (scaled x{mb_rows // sample_rows * micro} "
+              f"to {micro} microbatches of {mb_rows} rows) + one full oracle step() on all {len(ora.matrices)} "
+              f"matrices and the AdamW parameters")
+    return (hooks_per_step + t_step) * 1e3, hooks_per_step * 1e3, t_step * 1e3, sample
+
+
+def cpu_model_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---------------------------------------------------------------- main ---
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "bench.py measures one GPU only: the optimizer step is run and reported "
+                                   "on a single MI355X (multi-GPU sharding is a design note, not built)",
+                          "n_gpus_requested": args.gpus}))
+        sys.exit(2)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    model, opt, sets, micro, stat_bytes = build(args.config, args.s8_mode, device)
+
+    def one_step():
+        run_hooks(opt, sets, micro)
+        opt.step()
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        one_step()
+    end.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms = start.elapsed_time(end) / args.steps
+
+    # Phase breakdown (untimed above): hooks of one step, step() alone.
+    hooks_ms = time_events(lambda: run_hooks(opt, sets, micro))
+    step_ms = time_events(opt.step)
+    stats_ms_1, stats_bytes_1, stats_launches = stats_kernel_time(opt, sets)
+    s8_ms = s8_only_time(opt, args.s8_mode, device)
+    logical, issued = s8_flops(opt, args.s8_mode)
+    peak_mfma = BF16_PEAK if args.s8_mode == "comp_bf16" else FP32_PEAK
+
+    stats_gbs = stats_bytes_1 / (stats_ms_1 * 1e-3) / 1e9
+    s8_issued_tfs = issued / (s8_ms * 1e-3) / 1e12
+    s8_logical_tfs = logical / (s8_ms * 1e-3) / 1e12
+    roof_stats = {"bound": "hbm", "achieved": round(stats_gbs, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                  "frac": round(stats_gbs / (HBM_PEAK / 1e9), 4), "traffic": None,
+                  "kernel": "stats_accumulate_kernel", "launches_timed": stats_launches,
+                  "bytes_per_step": stat_bytes, "ms_per_step_kernels": round(stats_ms_1 * micro, 3)}
+    roof_s8 = {"bound": "mfma", "achieved": round(s8_issued_tfs, 1), "peak": peak_mfma / 1e12, "unit": "TFLOP/s",
+               "frac": round(s8_issued_tfs / (peak_mfma / 1e12), 4), "traffic": None,
+               "kernel": "s8_stage_kernel (gram/square/apply)", "issued_flops_per_step": issued,
+               "logical_flops_per_step": logical, "logical_tflops": round(s8_logical_tfs, 1),
+               "ms_per_step": round(s8_ms, 3)}
+    dominant = roof_stats if stats_ms_1 * micro >= s8_ms else roof_s8
+    out = {
+        "metric": METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16" if args.s8_mode == "comp_bf16" else "fp32", "data": "synthetic",
+        "config": {"workload": ("cfg4: 103M GPT SandMuon step = hook statistics of 8 microbatches x 16x1024 tokens + "
+                                "step() on 54 matrices + AdamW on 39.5M params") if args.config == "gpt103m" else
+                   "cfg5: 2048-wide 24-layer GPT, 144 matrices, 4 microbatches x 8x1024 tokens",
+                   "s8_mode": args.s8_mode, "matrices": len(opt.named_matrices), "microbatches": micro},
+        "roofline": dominant,
+        "roofline_stats": roof_stats,
+        "roofline_s8": roof_s8,
+        "phases_ms": {"hooks": round(hooks_ms, 3), "step": round(step_ms, 3), "host_wall_per_step": round(wall, 3)},
+    }
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or len(os.sched_getaffinity(0))
+        total, hooks, step, sample = cpu_baseline(args.config, threads)
+        out["cpu_baseline"] = {"value": round(total, 1), "unit": "ms", "cores": threads, "kind": "port",
+                               "sample": sample, "hooks_ms": round(hooks, 1), "step_ms": round(step, 1),
+                               "cpu": cpu_model_name()}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,209 @@
+/*
+ * sandmuon_amd.h -- C ABI of libsandmuon_amd.so, the MI355X (gfx950) HIP
+ * implementation of the SandMuon optimizer step.
+ *
+ * Every entry point is extern "C", takes plain pointers and sizes, and
+ * enqueues work on the explicit `stream` (a hipStream_t passed as void*).
+ * No entry point allocates or frees device memory, synchronises the device
+ * or copies device data to the host.  Device buffers (including workspaces)
+ * belong to the caller.  Descriptor tables (smx_*_desc) are HOST arrays:
+ * the library copies them into kernel arguments by value at launch, so the
+ * caller may reuse or free them as soon as the call returns.
+ *
+ * Return value: SMX_OK (0) on success; a negative SMX_E* code for invalid
+ * arguments (shape, dtype, alignment, workspace size); SMX_ELAUNCH when a
+ * kernel launch fails.  smx_last_error() returns a thread-local message for
+ * the last failure on the calling thread.
+ *
+ * The reference interface each entry point replaces is cited as
+ * path:line under pxike/SandMuon.
+ */
+#ifndef SANDMUON_AMD_H
+#define SANDMUON_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMX_ABI_VERSION 1
+
+enum smx_status {
+  SMX_OK = 0,
+  SMX_EINVAL = -1,      /* null pointer, bad count or enum          */
+  SMX_ESHAPE = -2,      /* unsupported or inconsistent shape         */
+  SMX_EDTYPE = -3,      /* unsupported element type                  */
+  SMX_EALIGN = -4,      /* pointer or stride alignment               */
+  SMX_EWORKSPACE = -5,  /* workspace too small                       */
+  SMX_ELAUNCH = -6      /* kernel launch failed (see smx_last_error) */
+};
+
+enum smx_dtype { SMX_F32 = 0, SMX_BF16 = 1, SMX_F16 = 2 };
+
+/* Arithmetic of the S8 polar map.
+ * SMX_S8_FP32: every product on FP32 MFMA (v_mfma_f32_32x32x2_f32), FP32
+ *   intermediates.  Restates sandmuon/optimizer.py:69-93.
+ * SMX_S8_COMP_BF16: every product as three BF16 MFMAs on hi/lo splits
+ *   (hi*lo + lo*hi + hi*hi, FP32 accumulation), FP32 intermediates.  The
+ *   compensated-product scheme of reproduction/odl/ops/
+ *   bf16_compensated_mm_fast.py:18-68, applied to all five stages. */
+enum smx_s8_mode { SMX_S8_FP32 = 0, SMX_S8_COMP_BF16 = 1 };
+
+int smx_abi_version(void);
+const char *smx_last_error(void);
+
+/* ------------------------------------------------------------------ *
+ * Statistics (forward hook A-capture and cotangent hook B-capture).
+ * Replaces the hook bodies at sandmuon/optimizer.py:156-168 (A: sum of
+ * x^2, and sum of x for the rank-one variant) and :171-177 (B: sum of
+ * delta^2).
+ *
+ * x is a [rows, cols] view with unit column stride and row stride
+ * `row_stride` elements, of type `dtype`.  The per-channel partial sums are
+ * added into `n_slots` slot rows: slots_sq[p*cols + c] (and slots_first)
+ * for p in [0, n_slots).  Each slot row is owned by one row chunk, so the
+ * accumulation is deterministic and needs no atomics.  The slot rows are
+ * folded into the running sums by smx_stats_fold / smx_stats_finish.
+ * slots_first may be NULL (B side, diagonal A).
+ * ------------------------------------------------------------------ */
+int smx_stats_accumulate(const void *x, int dtype, int64_t rows, int64_t cols,
+                         int64_t row_stride, float *slots_sq,
+                         float *slots_first, int32_t n_slots, void *stream);
+
+/* Fold: sum[c] += sum_p slots[p*n + c] (in FP64), then zero the slots.
+ * Used when the running sums must be materialised outside a step (for
+ * example before state_dict()).  first_* may be NULL. */
+int smx_stats_fold(float *sum_sq, float *slots_sq, float *sum_first,
+                   float *slots_first, int64_t n, int32_t n_slots,
+                   void *stream);
+
+/* One vector to finish.  kind: 0 = diagonal A factor, 1 = rank-one A
+ * factor, 2 = B factor (relative cotangent shape). */
+typedef struct smx_finish_desc {
+  float *sum_sq;      /* [n] running sum of squares; zeroed on return     */
+  float *slots_sq;    /* [n_slots*n] pending slot rows; zeroed on return  */
+  float *sum_first;   /* [n] running sum (kind 1) or NULL; zeroed         */
+  float *slots_first; /* [n_slots*n] (kind 1) or NULL; zeroed             */
+  float *ema;         /* [n] a_ema / b_ema, updated                       */
+  float *mean_ema;    /* [n] a_mean_ema (kind 1) or NULL                  */
+  float *inv;         /* [n] out: diagonal inverse square root            */
+  float *z;           /* [n] out: rank-one vector (kind 1) or NULL        */
+  float *kappa;       /* [1] out: rank-one coefficient (kind 1) or NULL   */
+  int64_t n;
+  int64_t count;      /* rows accumulated (host count, >= 1)              */
+  int32_t n_slots;
+  int32_t kind;
+  int32_t first;      /* 1: EMA starts as a copy (first step)             */
+  int32_t pad_;
+} smx_finish_desc;
+
+/* Batched _finish_a / _finish_b: sandmuon/optimizer.py:182-222 with
+ * rank1_inverse_sqrt (:27-35) and diagonal_inverse_sqrt (:19-24).
+ * `descs` is a host array of n_desc descriptors (device pointers inside). */
+int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc,
+                     float beta, void *stream);
+
+/* ------------------------------------------------------------------ *
+ * AdamW on the auxiliary parameters: sandmuon/optimizer.py:268-281.
+ * ------------------------------------------------------------------ */
+typedef struct smx_adamw_desc {
+  float *param;        /* [n] fp32                                  */
+  const void *grad;    /* [n] of grad_dtype                         */
+  float *exp_avg;      /* [n]                                       */
+  float *exp_avg_sq;   /* [n]                                       */
+  int64_t n;
+  int64_t offset;      /* exclusive prefix sum of n over the table   */
+  float bias1;         /* 1 - beta1^step (this tensor's step)        */
+  float bias2;         /* 1 - beta2^step                             */
+  int32_t grad_dtype;
+  int32_t pad_;
+} smx_adamw_desc;
+
+int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t total,
+              float lr, float beta1, float beta2, float eps,
+              float weight_decay, void *stream);
+
+/* ------------------------------------------------------------------ *
+ * Matrix update: Nesterov momentum -> whiten -> S8 -> mapback -> graft ->
+ * W -= lr * direction.  sandmuon/optimizer.py:244-264 and :283-315, with
+ * rank1_whiten (:38-45), _s8_fp32 (:69-93), rank1_mapback (:48-60) and
+ * _graft_direction (:63-66).
+ *
+ * In parameter layout (W is [rows, cols], input channels are columns) the
+ * A factor acts on columns and the B factor on rows for both orientations:
+ *   S = beta*m' + (1-beta)*g,      m' = beta*m + (1-beta)*g
+ *   V = (D_b S D_a)(I + kappa z z^T)            (whiten)
+ *   Q = S8(V)    (computed on the r<=c orientation of V)
+ *   U = D_b Q (I + kappa z z^T) D_a             (mapback)
+ *   W -= lr * sqrt(rows) * U / max(||U||_F, FLT_MIN)
+ * The diagonal variant has z = NULL (kappa ignored).
+ * ------------------------------------------------------------------ */
+typedef struct smx_matrix_desc {
+  float *param;          /* [rows, cols] fp32                         */
+  const void *grad;      /* [rows, cols] of grad_dtype                */
+  float *momentum;       /* [rows, cols] fp32, updated in place       */
+  const float *inv_row;  /* [rows] B factor                           */
+  const float *inv_col;  /* [cols] A factor diagonal                  */
+  const float *z;        /* [cols] A rank-one vector or NULL          */
+  const float *kappa;    /* [1] A rank-one coefficient or NULL        */
+  int64_t rows, cols;
+  float lr;
+  float momentum_beta;
+  int32_t grad_dtype;
+  int32_t pad_;
+} smx_matrix_desc;
+
+/* Device workspace needed for one smx_matrix_step call over the given
+ * matrices (rows[i], cols[i] are host arrays of parameter shapes). */
+size_t smx_matrix_step_workspace_bytes(const int64_t *rows,
+                                       const int64_t *cols, int32_t n,
+                                       int mode);
+
+/* Runs the whole matrix update for the n matrices of the host table
+ * `descs`.  The workspace (256-byte aligned, at least
+ * smx_matrix_step_workspace_bytes) holds the S8 iterates; its contents on
+ * entry are irrelevant. */
+int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode,
+                    void *workspace, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------------ *
+ * Stand-alone S8 polar map on a batch: _s8_fp32, sandmuon/optimizer.py:
+ * 69-93.  x and out are [batch, rows, cols] fp32 with the given strides
+ * (elements); out may alias x.  A matrix that is entirely zero maps to
+ * zero.  (The reference returns zeros only when the whole batch is zero
+ * and NaN for a zero matrix inside a non-zero batch.)
+ * ------------------------------------------------------------------ */
+size_t smx_s8_workspace_bytes(int64_t batch, int64_t rows, int64_t cols,
+                              int mode);
+int smx_s8(const float *x, float *out, int64_t batch, int64_t rows,
+           int64_t cols, int64_t batch_stride, int64_t row_stride,
+           int64_t col_stride, int mode, void *workspace,
+           size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------------ *
+ * Module-level helpers.
+ * smx_rank1_apply: rank1_whiten (sandmuon/optimizer.py:38-45, order 0) and
+ * rank1_mapback (:48-60, order 1) on a contiguous fp32 batch
+ * [batch, rows, cols]; both sides may carry a rank-one term.  li/lz are
+ * [batch, rows], ri/rz [batch, cols], lc/rc [batch] (device).  `work`
+ * holds batch*(rows+cols) floats.  out must not alias x.
+ * smx_graft: _graft_direction (:63-66) on n contiguous fp32 values:
+ * out = x*sqrt(output_rows)/max(||x||_F, FLT_MIN); a zero input gives a
+ * zero output (the reference returns NaN for a zero input once
+ * sqrt(rows)/FLT_MIN overflows).  `work` holds work_len doubles (>= 1).
+ * ------------------------------------------------------------------ */
+int smx_rank1_apply(const float *x, float *out, int64_t batch, int64_t rows,
+                    int64_t cols, const float *li, const float *lz,
+                    const float *lc, const float *ri, const float *rz,
+                    const float *rc, int order, float *work, void *stream);
+
+int smx_graft(const float *x, float *out, int64_t n, int64_t output_rows,
+              double *work, int32_t work_len, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SANDMUON_AMD_H */

@@ -1,0 +1,207 @@
+"""ctypes binding of libsandmuon_amd.so (the C ABI in include/sandmuon_amd.h).
+
+The library is the only compute path of this package: if it cannot be
+loaded, every entry point raises.  There is no CPU or eager-PyTorch fallback.
+Device tensors are passed by data pointer; every call enqueues on the
+current HIP stream of the tensor's device.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+from typing import Optional, Sequence
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libsandmuon_amd.so"
+ABI_VERSION = 1
+
+SMX_F32, SMX_BF16, SMX_F16 = 0, 1, 2
+S8_FP32, S8_COMP_BF16 = 0, 1
+S8_MODES = {"fp32": S8_FP32, "comp_bf16": S8_COMP_BF16}
+
+_DTYPES = {torch.float32: SMX_F32, torch.bfloat16: SMX_BF16, torch.float16: SMX_F16}
+
+_STATUS = {
+    -1: "SMX_EINVAL", -2: "SMX_ESHAPE", -3: "SMX_EDTYPE", -4: "SMX_EALIGN",
+    -5: "SMX_EWORKSPACE", -6: "SMX_ELAUNCH",
+}
+
+
+class NativeError(RuntimeError):
+    """A libsandmuon_amd entry point returned an error status."""
+
+
+class FinishDesc(ctypes.Structure):
+    _fields_ = [("sum_sq", c_void_p), ("slots_sq", c_void_p), ("sum_first", c_void_p),
+                ("slots_first", c_void_p), ("ema", c_void_p), ("mean_ema", c_void_p),
+                ("inv", c_void_p), ("z", c_void_p), ("kappa", c_void_p),
+                ("n", c_int64), ("count", c_int64), ("n_slots", c_int32), ("kind", c_int32),
+                ("first", c_int32), ("pad_", c_int32)]
+
+
+class AdamwDesc(ctypes.Structure):
+    _fields_ = [("param", c_void_p), ("grad", c_void_p), ("exp_avg", c_void_p),
+                ("exp_avg_sq", c_void_p), ("n", c_int64), ("offset", c_int64),
+                ("bias1", c_float), ("bias2", c_float), ("grad_dtype", c_int32), ("pad_", c_int32)]
+
+
+class MatrixDesc(ctypes.Structure):
+    _fields_ = [("param", c_void_p), ("grad", c_void_p), ("momentum", c_void_p),
+                ("inv_row", c_void_p), ("inv_col", c_void_p), ("z", c_void_p), ("kappa", c_void_p),
+                ("rows", c_int64), ("cols", c_int64), ("lr", c_float), ("momentum_beta", c_float),
+                ("grad_dtype", c_int32), ("pad_", c_int32)]
+
+
+# name -> (restype, argtypes); every symbol include/sandmuon_amd.h declares.
+SIGNATURES = {
+    "smx_abi_version": (c_int, []),
+    "smx_last_error": (ctypes.c_char_p, []),
+    "smx_stats_accumulate": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+                                     c_int32, c_void_p]),
+    "smx_stats_fold": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
+    "smx_stats_finish": (c_int, [ctypes.POINTER(FinishDesc), c_int32, c_float, c_void_p]),
+    "smx_adamw": (c_int, [ctypes.POINTER(AdamwDesc), c_int32, c_int64, c_float, c_float, c_float, c_float,
+                          c_float, c_void_p]),
+    "smx_matrix_step_workspace_bytes": (c_size_t, [ctypes.POINTER(c_int64), ctypes.POINTER(c_int64),
+                                                   c_int32, c_int]),
+    "smx_matrix_step": (c_int, [ctypes.POINTER(MatrixDesc), c_int32, c_int, c_void_p, c_size_t, c_void_p]),
+    "smx_s8_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int]),
+    "smx_s8": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int,
+                       c_void_p, c_size_t, c_void_p]),
+    "smx_rank1_apply": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+                                c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+    "smx_graft": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+_lock = threading.Lock()
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library once; raise loudly if it is missing or stale."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise ImportError(
+                    f"{LIB_PATH} is missing: build it with `python -m sandmuon_amd.build` "
+                    "(hipcc, gfx950). sandmuon_amd has no fallback path.")
+            handle = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            version = handle.smx_abi_version()
+            if version != ABI_VERSION:
+                raise ImportError(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}; rebuild it")
+            _lib = handle
+    return _lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().smx_last_error().decode(errors="replace")
+        kind = _STATUS.get(rc, str(rc))
+        if rc in (-1, -2, -3, -4, -5):
+            raise ValueError(f"{what}: {kind}: {msg}")
+        raise NativeError(f"{what}: {kind}: {msg}")
+
+
+def require_gpu(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{what}: sandmuon_amd runs on ROCm GPU tensors only (got {t.device})")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float16") from None
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+# ------------------------------------------------------------ wrappers ---
+def stats_accumulate(rows2d: torch.Tensor, slots_sq: torch.Tensor, slots_first: Optional[torch.Tensor]) -> None:
+    rc = lib().smx_stats_accumulate(rows2d.data_ptr(), dtype_code(rows2d.dtype), rows2d.shape[0],
+                                    rows2d.shape[1], rows2d.stride(0), slots_sq.data_ptr(),
+                                    ptr(slots_first), slots_sq.shape[0], stream_of(rows2d.device))
+    _check(rc, "smx_stats_accumulate")
+
+
+def stats_fold(sum_sq, slots_sq, sum_first, slots_first) -> None:
+    rc = lib().smx_stats_fold(sum_sq.data_ptr(), slots_sq.data_ptr(), ptr(sum_first), ptr(slots_first),
+                              sum_sq.numel(), slots_sq.shape[0], stream_of(sum_sq.device))
+    _check(rc, "smx_stats_fold")
+
+
+def stats_finish(descs: Sequence[FinishDesc], beta: float, device: torch.device) -> None:
+    if not descs:
+        return
+    arr = (FinishDesc * len(descs))(*descs)
+    _check(lib().smx_stats_finish(arr, len(descs), beta, stream_of(device)), "smx_stats_finish")
+
+
+def adamw(descs: Sequence[AdamwDesc], total: int, lr: float, beta1: float, beta2: float, eps: float,
+          weight_decay: float, device: torch.device) -> None:
+    if not descs:
+        return
+    arr = (AdamwDesc * len(descs))(*descs)
+    _check(lib().smx_adamw(arr, len(descs), total, lr, beta1, beta2, eps, weight_decay, stream_of(device)),
+           "smx_adamw")
+
+
+def matrix_step_workspace_bytes(shapes: Sequence[tuple], mode: int) -> int:
+    n = len(shapes)
+    rows = (c_int64 * n)(*[s[0] for s in shapes])
+    cols = (c_int64 * n)(*[s[1] for s in shapes])
+    return int(lib().smx_matrix_step_workspace_bytes(rows, cols, n, mode))
+
+
+def matrix_step(descs: Sequence[MatrixDesc], mode: int, workspace: torch.Tensor) -> None:
+    if not descs:
+        return
+    arr = (MatrixDesc * len(descs))(*descs)
+    _check(lib().smx_matrix_step(arr, len(descs), mode, workspace.data_ptr(), workspace.numel(),
+                                 stream_of(workspace.device)), "smx_matrix_step")
+
+
+def s8(x: torch.Tensor, out: torch.Tensor, mode: int) -> None:
+    """x, out: [batch, rows, cols] float32 on the GPU (any strides)."""
+    b, r, c = x.shape
+    nbytes = int(lib().smx_s8_workspace_bytes(b, r, c, mode))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    if out.stride() != x.stride():
+        raise ValueError("s8: out must have the strides of x")
+    rc = lib().smx_s8(x.data_ptr(), out.data_ptr(), b, r, c, x.stride(0), x.stride(1), x.stride(2), mode,
+                      ws.data_ptr(), ws.numel(), stream_of(x.device))
+    _check(rc, "smx_s8")
+
+
+def rank1_apply(x: torch.Tensor, out: torch.Tensor, left, right, order: int) -> None:
+    b, r, c = x.shape
+    li, lz, lc = left
+    ri, rz, rc_ = right
+    work = torch.empty(max(b * (r + c), 1), dtype=torch.float32, device=x.device)
+    rc = lib().smx_rank1_apply(x.data_ptr(), out.data_ptr(), b, r, c, li.data_ptr(), lz.data_ptr(),
+                               lc.data_ptr(), ri.data_ptr(), rz.data_ptr(), rc_.data_ptr(), order,
+                               work.data_ptr(), stream_of(x.device))
+    _check(rc, "smx_rank1_apply")
+
+
+def graft(x: torch.Tensor, out: torch.Tensor, output_rows: int) -> None:
+    work = torch.empty(1024, dtype=torch.float64, device=x.device)
+    rc = lib().smx_graft(x.data_ptr(), out.data_ptr(), x.numel(), output_rows, work.data_ptr(), 1024,
+                         stream_of(x.device))
+    _check(rc, "smx_graft")

@@ -1,0 +1,72 @@
+"""Build libsandmuon_amd.so (gfx950) in-tree with hipcc.
+
+Usage: python -m sandmuon_amd.build   (or sandmuon_amd.build.build())
+Each .hip file under csrc/ is compiled to an object in parallel, then the
+objects are linked into sandmuon_amd/libsandmuon_amd.so.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+LIB = HERE / "libsandmuon_amd.so"
+ARCH = os.environ.get("SANDMUON_AMD_ARCH", "gfx950")
+
+# -packed-fp32-ops: keep the compiler from emitting packed FP32 VALU ops.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found; set HIPCC or install ROCm")
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    hipcc = _hipcc()
+    srcs = sources()
+    with tempfile.TemporaryDirectory(prefix="smx_build_") as tmp:
+        objs = [Path(tmp) / (s.stem + ".o") for s in srcs]
+
+        def compile_one(pair):
+            src, obj = pair
+            cmd = [hipcc, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+            res = subprocess.run(cmd, capture_output=True, text=True)
+            out = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
+                            if "packed-fp32-ops" not in l)
+            if res.returncode != 0:
+                raise RuntimeError(f"hipcc failed on {src.name}:\n{out}")
+            if verbose and out.strip():
+                print(out, file=sys.stderr)
+            return obj
+
+        workers = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
+        with ThreadPoolExecutor(max_workers=workers) as ex:
+            list(ex.map(compile_one, zip(srcs, objs)))
+        tmp_lib = Path(tmp) / LIB.name
+        cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp_lib), *map(str, objs)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
+        shutil.move(str(tmp_lib), str(LIB))
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

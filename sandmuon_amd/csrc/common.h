@@ -1,0 +1,78 @@
+// Shared device/host helpers for the SandMuon gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/sandmuon_amd.h"
+
+namespace smx {
+
+// ------------------------------------------------------------ errors ---
+void set_error(const std::string &msg);
+int fail(int code, const std::string &msg);
+int check_launch(const char *what);
+
+#define SMX_REQUIRE(cond, code, msg)                                        \
+  do {                                                                      \
+    if (!(cond)) return ::smx::fail((code), (msg));                         \
+  } while (0)
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+// ------------------------------------------------------- element I/O ---
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even FP32 -> BF16 bits (finite inputs; NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  _Float16 v;
+  __builtin_memcpy(&v, &h, sizeof(v));
+  return static_cast<float>(v);
+}
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const void *p, int64_t i) {
+  if constexpr (DT == SMX_F32) {
+    return static_cast<const float *>(p)[i];
+  } else if constexpr (DT == SMX_BF16) {
+    return bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+  } else {
+    return f16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+  }
+}
+
+// ---------------------------------------------------- wave reductions ---
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Block-wide sum; every thread receives the result.  `scratch` must hold
+// one T per wave (blockDim.x / 64 <= 16).
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T *scratch) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nw = (blockDim.x + 63) >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  T t = 0;
+  for (int w = 0; w < nw; ++w) t += scratch[w];
+  return t;
+}
+
+}  // namespace smx

@@ -1,0 +1,401 @@
+// Matrix update around the S8 map (parameter layout, W is rows x cols):
+//
+//   whiten  (sandmuon/optimizer.py:244-248, :249-264, :290-296, rank1_whiten
+//            :38-45): m' = b m + (1-b) g;  S = b m' + (1-b) g;
+//            V = (D_b S D_a)(I + kappa z z^T)
+//   mapback (rank1_mapback :48-60, _graft_direction :63-66, update :314-315):
+//            U = D_b Q (I + kappa z z^T) D_a;
+//            W -= lr * sqrt(rows) * U / max(||U||_F, FLT_MIN)
+//
+// In parameter layout the A factor always acts on columns (input channels)
+// and B on rows, whichever orientation the S8 map uses; the oriented copies
+// X (r x c, r <= c) and X^T are written by the whiten tile pass.
+//
+// whiten_rows  one pass per row: momentum update, u_i = b_i sum_j S_ij a_j z_j
+//              and the row's ||V_i||^2 in closed form
+//              (||V_i||^2 = b_i^2 sum_j (S_ij a_j)^2 + (2 kappa + kappa^2 |z|^2) u_i^2).
+// whiten_tiles 64x64 tiles: V from (g, m', u), stored to the parameter-layout
+//              buffer and, transposed through LDS, to the other buffer.
+// mapback_rows u_i = sum_j Q_ij z_j and ||U_i||^2 in closed form.
+// mapback_apply W -= lr * scale * U.
+#include "s8.h"
+
+#include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <memory>
+#include <vector>
+
+namespace smx {
+
+struct MatJob {
+  smx_matrix_desc d;
+  float *pl;         // parameter-layout buffer [prow_pad][pcol_pad]
+  float *tl;         // transposed buffer [pcol_pad][prow_pad] (whiten)
+  float *u;          // [rows] rank-one row coefficients
+  double *part;      // [ceil(rows/kRowsPerPart)] partial sums
+  int64_t prow_pad, pcol_pad;
+  int32_t blk0;      // first block of this job in the launch
+  int32_t pad_;
+};
+
+constexpr int kMatBatch = 12;
+struct MatPack {
+  MatJob j[kMatBatch];
+  int32_t n;
+  int32_t total_blocks;
+};
+
+__device__ __forceinline__ int find_job(const MatPack &p, int b) {
+  int k = 0;
+  while (k + 1 < p.n && b >= p.j[k + 1].blk0) ++k;
+  return k;
+}
+
+__device__ __forceinline__ float load_grad(const void *g, int dt, int64_t i) {
+  if (dt == SMX_F32) return static_cast<const float *>(g)[i];
+  if (dt == SMX_BF16) return load_elem<SMX_BF16>(g, i);
+  return load_elem<SMX_F16>(g, i);
+}
+
+// Sum of z^2 (or of (a z)^2 when `a` is given) over n entries; block-wide.
+__device__ double sum_sq_vec(const float *z, const float *a, int64_t n, double *scratch) {
+  double s = 0.0;
+  for (int64_t j = threadIdx.x; j < n; j += blockDim.x) {
+    const double v = a ? static_cast<double>(a[j]) * z[j] : static_cast<double>(z[j]);
+    s += v * v;
+  }
+  return block_sum(s, scratch);
+}
+
+// ------------------------------------------------------------- whiten ---
+// block = 256 threads (4 waves); kRowsPerPart rows per block, one wave per row.
+__global__ void __launch_bounds__(256) whiten_rows_kernel(MatPack pack) {
+  __shared__ double scratch[16];
+  __shared__ double wave_part[4];
+  const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
+  const smx_matrix_desc &d = J.d;
+  const int blk = blockIdx.x - J.blk0;
+  const bool r1 = d.z != nullptr;
+  const double zz = r1 ? sum_sq_vec(d.z, nullptr, d.cols, scratch) : 0.0;
+  const float kappa = r1 ? d.kappa[0] : 0.f;
+  const double corr = r1 ? 2.0 * kappa + static_cast<double>(kappa) * kappa * zz : 0.0;
+  const float beta = d.momentum_beta, omb = 1.0f - d.momentum_beta;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool vec = d.grad_dtype == SMX_F32 && (d.cols % 4 == 0) &&
+                   (reinterpret_cast<uintptr_t>(d.grad) % 16 == 0) &&
+                   (reinterpret_cast<uintptr_t>(d.momentum) % 16 == 0);
+  double part = 0.0;
+  for (int rr = wave; rr < kRowsPerPart; rr += 4) {
+    const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + rr;
+    if (i >= d.rows) break;
+    float y2 = 0.f, yz = 0.f;
+    float *mrow = d.momentum + i * d.cols;
+    if (vec) {
+      const float4 *g4 = reinterpret_cast<const float4 *>(static_cast<const float *>(d.grad) + i * d.cols);
+      float4 *m4 = reinterpret_cast<float4 *>(mrow);
+      for (int64_t q = lane; q < d.cols / 4; q += 64) {
+        const float4 g = g4[q];
+        float4 m = m4[q];
+        m.x = fmaf(m.x, beta, g.x * omb); m.y = fmaf(m.y, beta, g.y * omb);
+        m.z = fmaf(m.z, beta, g.z * omb); m.w = fmaf(m.w, beta, g.w * omb);
+        m4[q] = m;
+        const float gs[4] = {g.x, g.y, g.z, g.w}, ms[4] = {m.x, m.y, m.z, m.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t j = q * 4 + e;
+          const float y = fmaf(ms[e], beta, gs[e] * omb) * d.inv_col[j];
+          y2 = fmaf(y, y, y2);
+          if (r1) yz = fmaf(y, d.z[j], yz);
+        }
+      }
+    } else {
+      for (int64_t j = lane; j < d.cols; j += 64) {
+        const float g = load_grad(d.grad, d.grad_dtype, i * d.cols + j);
+        const float m = fmaf(mrow[j], beta, g * omb);
+        mrow[j] = m;
+        const float y = fmaf(m, beta, g * omb) * d.inv_col[j];
+        y2 = fmaf(y, y, y2);
+        if (r1) yz = fmaf(y, d.z[j], yz);
+      }
+    }
+    const double Y2 = wave_sum(static_cast<double>(y2));
+    const double YZ = wave_sum(static_cast<double>(yz));
+    const double b = d.inv_row[i];
+    const double u = b * YZ;
+    if (lane == 0) {
+      J.u[i] = static_cast<float>(u);
+      part += b * b * Y2 + corr * u * u;
+    }
+  }
+  if (lane == 0) wave_part[wave] = part;
+  __syncthreads();
+  if (threadIdx.x == 0) J.part[blk] = wave_part[0] + wave_part[1] + wave_part[2] + wave_part[3];
+}
+
+// block = 256 threads, one 64x64 tile of the padded parameter layout.
+__global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
+  __shared__ float tile[64][65];
+  const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
+  const smx_matrix_desc &d = J.d;
+  const int64_t tiles_c = J.pcol_pad / 64;
+  const int64_t tb = blockIdx.x - J.blk0;
+  const int64_t i0 = (tb / tiles_c) * 64, j0 = (tb % tiles_c) * 64;
+  const bool r1 = d.z != nullptr;
+  const float kappa = r1 ? d.kappa[0] : 0.f;
+  const float beta = d.momentum_beta, omb = 1.0f - d.momentum_beta;
+  const int t = threadIdx.x;
+  const int lc = (t & 15) * 4;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int lr = (t >> 4) + 16 * q;
+    const int64_t i = i0 + lr;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t j = j0 + lc + e;
+      float val = 0.f;
+      if (i < d.rows && j < d.cols) {
+        const float g = load_grad(d.grad, d.grad_dtype, i * d.cols + j);
+        const float s = fmaf(d.momentum[i * d.cols + j], beta, g * omb);
+        val = (s * d.inv_row[i]) * d.inv_col[j];
+        if (r1) val = fmaf(kappa * J.u[i], d.z[j], val);
+      }
+      v[e] = val;
+      tile[lr][lc + e] = val;
+    }
+    *reinterpret_cast<float4 *>(J.pl + i * J.pcol_pad + j0 + lc) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int lr = (t >> 4) + 16 * q;  // transposed row = parameter column
+    *reinterpret_cast<float4 *>(J.tl + (j0 + lr) * J.prow_pad + i0 + lc) =
+        make_float4(tile[lc][lr], tile[lc + 1][lr], tile[lc + 2][lr], tile[lc + 3][lr]);
+  }
+}
+
+// ------------------------------------------------------------ mapback ---
+__global__ void __launch_bounds__(256) mapback_rows_kernel(MatPack pack) {
+  __shared__ double scratch[16];
+  __shared__ double wave_part[4];
+  const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
+  const smx_matrix_desc &d = J.d;
+  const int blk = blockIdx.x - J.blk0;
+  const bool r1 = d.z != nullptr;
+  const double cz = r1 ? sum_sq_vec(d.z, d.inv_col, d.cols, scratch) : 0.0;
+  const double kappa = r1 ? d.kappa[0] : 0.0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  double part = 0.0;
+  for (int rr = wave; rr < kRowsPerPart; rr += 4) {
+    const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + rr;
+    if (i >= d.rows) break;
+    const float *q = J.pl + i * J.pcol_pad;
+    float su = 0.f, sa = 0.f, sb = 0.f;
+    for (int64_t j = lane; j < d.cols; j += 64) {
+      const float a = d.inv_col[j];
+      const float aq = a * q[j];
+      sa = fmaf(aq, aq, sa);
+      if (r1) {
+        su = fmaf(q[j], d.z[j], su);
+        sb = fmaf(aq, a * d.z[j], sb);
+      }
+    }
+    const double U = wave_sum(static_cast<double>(su));
+    const double A = wave_sum(static_cast<double>(sa));
+    const double B = wave_sum(static_cast<double>(sb));
+    if (lane == 0) {
+      const double b = d.inv_row[i];
+      J.u[i] = static_cast<float>(U);
+      part += b * b * (A + 2.0 * kappa * U * B + kappa * kappa * U * U * cz);
+    }
+  }
+  if (lane == 0) wave_part[wave] = part;
+  __syncthreads();
+  if (threadIdx.x == 0) J.part[blk] = wave_part[0] + wave_part[1] + wave_part[2] + wave_part[3];
+}
+
+// block = 256 threads over kRowsPerPart rows of the parameter.
+__global__ void __launch_bounds__(256) mapback_apply_kernel(MatPack pack) {
+  __shared__ double bcast;
+  const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
+  const smx_matrix_desc &d = J.d;
+  const int blk = blockIdx.x - J.blk0;
+  if (threadIdx.x < 64) {
+    double s = 0.0;
+    const int np = static_cast<int>(ceil_div(d.rows, kRowsPerPart));
+    for (int k = threadIdx.x; k < np; k += 64) s += J.part[k];
+    s = wave_sum(s);
+    if (threadIdx.x == 0) bcast = s;
+  }
+  __syncthreads();
+  const double n2 = bcast;
+  const float norm = static_cast<float>(sqrt(n2));
+  // _graft_direction: sqrt(rows) / max(||U||, FLT_MIN); a zero direction
+  // gives a zero update.
+  const float scale = n2 > 0.0 ? static_cast<float>(sqrt(static_cast<double>(d.rows))) / fmaxf(norm, FLT_MIN) : 0.f;
+  const float nlr = -d.lr;
+  const bool r1 = d.z != nullptr;
+  const float kappa = r1 ? d.kappa[0] : 0.f;
+  for (int rr = 0; rr < kRowsPerPart; ++rr) {
+    const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + rr;
+    if (i >= d.rows) break;
+    const float *q = J.pl + i * J.pcol_pad;
+    float *w = d.param + i * d.cols;
+    const float b = d.inv_row[i];
+    const float ku = r1 ? kappa * J.u[i] : 0.f;
+    for (int64_t j = threadIdx.x; j < d.cols; j += 256) {
+      float v = q[j];
+      if (r1) v = fmaf(ku, d.z[j], v);
+      const float U = (v * b) * d.inv_col[j];
+      w[j] = fmaf(nlr, U * scale, w[j]);
+    }
+  }
+}
+
+// --------------------------------------------------------------- host ---
+struct Planned {
+  S8Plan plan;
+  std::vector<int32_t> cls, slot;
+};
+
+static bool oriented(const smx_matrix_desc &d, int64_t &r, int64_t &c, bool &flip) {
+  flip = d.rows > d.cols;
+  r = flip ? d.cols : d.rows;
+  c = flip ? d.rows : d.cols;
+  return true;
+}
+
+// Groups of matrices with at most kMaxClasses distinct oriented shapes,
+// formed greedily in table order.
+static std::vector<std::vector<int32_t>> shape_groups(const int64_t *rows, const int64_t *cols, int32_t n) {
+  std::vector<std::vector<int32_t>> groups;
+  std::vector<std::pair<int64_t, int64_t>> shapes;
+  for (int32_t i = 0; i < n; ++i) {
+    const std::pair<int64_t, int64_t> s(std::min(rows[i], cols[i]), std::max(rows[i], cols[i]));
+    if (groups.empty() || (std::find(shapes.begin(), shapes.end(), s) == shapes.end() &&
+                           static_cast<int>(shapes.size()) == kMaxClasses)) {
+      groups.emplace_back();
+      shapes.clear();
+    }
+    if (std::find(shapes.begin(), shapes.end(), s) == shapes.end()) shapes.push_back(s);
+    groups.back().push_back(i);
+  }
+  return groups;
+}
+
+static size_t group_bytes(const int64_t *rows, const int64_t *cols, const std::vector<int32_t> &g, int mode) {
+  const int32_t m = static_cast<int32_t>(g.size());
+  std::vector<int64_t> r(m), c(m);
+  std::unique_ptr<bool[]> fl(new bool[m]);
+  for (int32_t k = 0; k < m; ++k) {
+    r[k] = std::min(rows[g[k]], cols[g[k]]);
+    c[k] = std::max(rows[g[k]], cols[g[k]]);
+    fl[k] = rows[g[k]] > cols[g[k]];
+  }
+  S8Plan plan;
+  std::vector<int32_t> cls(m), slot(m);
+  plan_s8(r.data(), c.data(), fl.get(), m, mode, nullptr, plan, cls.data(), slot.data());
+  return plan.bytes;
+}
+
+template <typename KernelFn>
+static int launch_jobs(std::vector<MatJob> &jobs, int64_t (*blocks_of)(const MatJob &), KernelFn kernel,
+                       const char *what, hipStream_t st) {
+  for (size_t b = 0; b < jobs.size(); b += kMatBatch) {
+    MatPack pack{};
+    pack.n = static_cast<int32_t>(std::min<size_t>(kMatBatch, jobs.size() - b));
+    int64_t total = 0;
+    for (int k = 0; k < pack.n; ++k) {
+      pack.j[k] = jobs[b + k];
+      pack.j[k].blk0 = static_cast<int32_t>(total);
+      total += blocks_of(pack.j[k]);
+    }
+    pack.total_blocks = static_cast<int32_t>(total);
+    if (total == 0) continue;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(total)), dim3(256), 0, st, pack);
+    const int rc = check_launch(what);
+    if (rc) return rc;
+  }
+  return SMX_OK;
+}
+
+static int64_t row_blocks(const MatJob &j) { return ceil_div(j.d.rows, kRowsPerPart); }
+static int64_t tile_blocks(const MatJob &j) { return (j.prow_pad / 64) * (j.pcol_pad / 64); }
+
+}  // namespace smx
+
+using namespace smx;
+
+extern "C" size_t smx_matrix_step_workspace_bytes(const int64_t *rows, const int64_t *cols, int32_t n,
+                                                  int mode) {
+  if (n <= 0 || !rows || !cols) return 0;
+  size_t best = 0;
+  for (const auto &g : shape_groups(rows, cols, n)) best = std::max(best, group_bytes(rows, cols, g, mode));
+  return best;
+}
+
+extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode, void *workspace,
+                               size_t workspace_bytes, void *stream) {
+  SMX_REQUIRE(n >= 0, SMX_EINVAL, "matrix_step: n < 0");
+  if (n == 0) return SMX_OK;
+  SMX_REQUIRE(descs && workspace, SMX_EINVAL, "matrix_step: null descriptor table or workspace");
+  SMX_REQUIRE(mode == SMX_S8_FP32 || mode == SMX_S8_COMP_BF16, SMX_EINVAL, "matrix_step: unknown S8 mode");
+  std::vector<int64_t> rows(n), cols(n);
+  for (int32_t i = 0; i < n; ++i) {
+    const smx_matrix_desc &d = descs[i];
+    SMX_REQUIRE(d.param && d.grad && d.momentum && d.inv_row && d.inv_col, SMX_EINVAL,
+                "matrix_step: param, grad, momentum, inv_row and inv_col are required");
+    SMX_REQUIRE((d.z == nullptr) == (d.kappa == nullptr), SMX_EINVAL,
+                "matrix_step: z and kappa must both be set or both NULL");
+    SMX_REQUIRE(d.rows >= 1 && d.cols >= 1, SMX_ESHAPE, "matrix_step: rows and cols must be >= 1");
+    SMX_REQUIRE(d.grad_dtype == SMX_F32 || d.grad_dtype == SMX_BF16 || d.grad_dtype == SMX_F16, SMX_EDTYPE,
+                "matrix_step: grad dtype must be f32, bf16 or f16");
+    rows[i] = d.rows;
+    cols[i] = d.cols;
+  }
+  const size_t need = smx_matrix_step_workspace_bytes(rows.data(), cols.data(), n, mode);
+  SMX_REQUIRE(workspace_bytes >= need, SMX_EWORKSPACE, "matrix_step: workspace too small");
+  SMX_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, SMX_EALIGN,
+              "matrix_step: workspace must be 256-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  for (const auto &g : shape_groups(rows.data(), cols.data(), n)) {
+    const int32_t m = static_cast<int32_t>(g.size());
+    std::vector<int64_t> r(m), c(m);
+    std::unique_ptr<bool[]> fl(new bool[m]);
+    for (int32_t k = 0; k < m; ++k) {
+      bool f;
+      oriented(descs[g[k]], r[k], c[k], f);
+      fl[k] = f;
+    }
+    S8Plan plan;
+    std::vector<int32_t> cls(m), slot(m);
+    if (!plan_s8(r.data(), c.data(), fl.get(), m, mode, static_cast<char *>(workspace), plan, cls.data(),
+                 slot.data()))
+      return fail(SMX_EINVAL, "matrix_step: internal shape grouping error");
+    std::vector<MatJob> ping(m), fin(m);
+    for (int32_t k = 0; k < m; ++k) {
+      const S8Mat M{plan.layout.cls[cls[k]], slot[k]};
+      MatJob j{};
+      j.d = descs[g[k]];
+      j.u = M.u();
+      j.prow_pad = M.prow_pad();
+      j.pcol_pad = M.pcol_pad();
+      j.pl = M.flip() ? M.xt0() : M.x0();
+      j.tl = M.flip() ? M.x0() : M.xt0();
+      j.part = M.fro();
+      ping[k] = j;
+      j.pl = M.flip() ? M.xt1() : M.x1();
+      j.tl = nullptr;
+      j.part = M.mb();
+      fin[k] = j;
+    }
+    int rc = launch_jobs(ping, row_blocks, whiten_rows_kernel, "whiten_rows", st);
+    if (!rc) rc = launch_jobs(ping, tile_blocks, whiten_tiles_kernel, "whiten_tiles", st);
+    if (!rc) rc = run_s8_stages(plan.layout, st);
+    if (!rc) rc = launch_jobs(fin, row_blocks, mapback_rows_kernel, "mapback_rows", st);
+    if (!rc) rc = launch_jobs(fin, row_blocks, mapback_apply_kernel, "mapback_apply", st);
+    if (rc) return rc;
+  }
+  return SMX_OK;
+}

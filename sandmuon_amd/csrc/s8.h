@@ -1,0 +1,91 @@
+// Workspace layout shared by the matrix-step kernels (whiten, S8 GEMMs,
+// mapback).  Matrices are grouped in classes of equal oriented shape
+// (r <= c); every class buffer is padded to multiples of kTile so that the
+// GEMM tiles never need bounds checks.  Padding holds zeros.
+#pragma once
+
+#include "common.h"
+
+namespace smx {
+
+constexpr int kTile = 256;        // GEMM macro tile (M and N) and padding
+constexpr int kMaxClasses = 8;    // shape classes per GEMM launch
+constexpr int kRowsPerPart = 16;  // param rows per whiten/mapback partial
+
+// Fixed S8 recipe: sandmuon/coefficients.py:3-11.
+constexpr double kS8Margin = 1.35;
+constexpr double kS8Coefficients[5][3] = {
+    {11.062126275847973, -56.051653229128085, 72.32081107619855},
+    {4.100720073616268, -2.9324183165353577, 0.5339692084282731},
+    {3.930310192522361, -2.873509793709714, 0.5366557527206212},
+    {3.280567968245866, -2.414925589994015, 0.48635134757825227},
+    {2.282741575232451, -1.6302296637355072, 0.40275720810675486},
+};
+
+struct S8Class {
+  int64_t r, c;        // oriented logical dims, r <= c
+  int64_t rp, cp;      // padded dims
+  int32_t count;       // matrices in the class
+  int32_t n_flip;      // slots [0, n_flip) hold transposed parameters
+  int32_t tiles_m;     // rp / kTile
+  int32_t tiles_n;     // cp / kTile
+  int32_t parts;       // partial slots per matrix: ceil(cp / kRowsPerPart)
+  int32_t pad_;
+  float *x0, *xt0;     // [count][rp][cp], [count][cp][rp]  (ping)
+  float *x1, *xt1;     // pong; after stage 5 the result is in x1/xt1
+  float *g, *p;        // [count][rp][rp]
+  float *u;            // [count][cp] per param-row rank-one coefficient
+  double *fro;         // [count][parts] whiten: partial sum of V^2
+  double *mb;          // [count][parts] mapback: partial sum of U^2
+  double *sch;         // [count][tiles_m*(tiles_m+1)/2] Schatten partials
+};
+
+struct S8Layout {
+  S8Class cls[kMaxClasses];
+  int32_t n_classes;
+  int32_t mode;
+};
+
+__host__ __device__ inline int64_t sym_tiles(int64_t t) { return t * (t + 1) / 2; }
+
+// Per-matrix views of a class slot.
+struct S8Mat {
+  S8Class k_;
+  int32_t slot;
+  __host__ __device__ const S8Class *kp() const { return &k_; }
+  __host__ __device__ bool flip() const { return slot < kp()->n_flip; }
+  __host__ __device__ float *x0() const { return kp()->x0 + slot * kp()->rp * kp()->cp; }
+  __host__ __device__ float *xt0() const { return kp()->xt0 + slot * kp()->rp * kp()->cp; }
+  __host__ __device__ float *x1() const { return kp()->x1 + slot * kp()->rp * kp()->cp; }
+  __host__ __device__ float *xt1() const { return kp()->xt1 + slot * kp()->rp * kp()->cp; }
+  __host__ __device__ float *g() const { return kp()->g + slot * kp()->rp * kp()->rp; }
+  __host__ __device__ float *p() const { return kp()->p + slot * kp()->rp * kp()->rp; }
+  __host__ __device__ float *u() const { return kp()->u + slot * kp()->cp; }
+  __host__ __device__ double *fro() const { return kp()->fro + static_cast<int64_t>(slot) * kp()->parts; }
+  __host__ __device__ double *mb() const { return kp()->mb + static_cast<int64_t>(slot) * kp()->parts; }
+  __host__ __device__ double *sch() const { return kp()->sch + slot * sym_tiles(kp()->tiles_m); }
+  // Parameter layout: rows x cols; the parameter-layout buffer of the
+  // ping side is xt0 for transposed parameters and x0 otherwise.
+  __host__ __device__ int64_t prow() const { return flip() ? kp()->c : kp()->r; }
+  __host__ __device__ int64_t pcol() const { return flip() ? kp()->r : kp()->c; }
+  __host__ __device__ int64_t prow_pad() const { return flip() ? kp()->cp : kp()->rp; }
+  __host__ __device__ int64_t pcol_pad() const { return flip() ? kp()->rp : kp()->cp; }
+};
+
+// Host-side planning of a set of matrices into classes.
+struct S8Plan {
+  S8Layout layout;
+  size_t bytes = 0;
+};
+
+// Compute the class layout for oriented shapes; `flips[i]` marks matrices
+// whose parameter layout is the transpose of the oriented shape.  Fills
+// class/slot of each matrix.  Returns false if more than kMaxClasses shapes.
+bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, int mode,
+             char *base, S8Plan &plan, int32_t *cls_of, int32_t *slot_of);
+
+// Run the five S8 stages on a planned layout whose x0/xt0 (and fro
+// partials) are filled.  The result is in x1/xt1.
+int run_s8_stages(const S8Layout &layout, hipStream_t st);
+
+}  // namespace smx

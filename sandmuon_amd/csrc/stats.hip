@@ -1,0 +1,367 @@
+// Per-channel statistics for the SandMuon hooks and their step-time finish.
+//
+//  * stats_accumulate: the hook bodies of sandmuon/optimizer.py:156-168 and
+//    :171-177 (sum of x^2, and sum of x for the rank-one A variant), as one
+//    HBM pass.  Each block owns a (row chunk, column tile) and adds its FP32
+//    partial into slot row `chunk`, so the result is deterministic and no
+//    atomics or tail combine are needed in the hook.
+//  * stats_fold: sum += sum over slot rows (FP64), slots zeroed.
+//  * stats_finish: _finish_a/_finish_b (sandmuon/optimizer.py:182-222) with
+//    rank1_inverse_sqrt (:27-35) and diagonal_inverse_sqrt (:19-24).
+#include "common.h"
+
+#include <algorithm>
+#include <cfloat>
+#include <vector>
+
+namespace smx {
+
+constexpr int kStatsThreads = 512;
+constexpr int kStatsWaves = kStatsThreads / 64;
+
+template <int DT, int VEC>
+struct VecLoad;
+
+template <>
+struct VecLoad<SMX_F32, 4> {
+  __device__ __forceinline__ static void load(const void *p, int64_t i, float *v) {
+    float4 q = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  }
+};
+
+template <int DT>
+struct VecLoad2B8 {
+  __device__ __forceinline__ static void load(const void *p, int64_t i, float *v) {
+    uint4 q = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
+    uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (DT == SMX_BF16) {
+        v[2 * k] = __uint_as_float(w[k] << 16);
+        v[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+      } else {
+        v[2 * k] = f16_bits_to_f32(static_cast<uint16_t>(w[k] & 0xffffu));
+        v[2 * k + 1] = f16_bits_to_f32(static_cast<uint16_t>(w[k] >> 16));
+      }
+    }
+  }
+};
+template <>
+struct VecLoad<SMX_BF16, 8> : VecLoad2B8<SMX_BF16> {};
+template <>
+struct VecLoad<SMX_F16, 8> : VecLoad2B8<SMX_F16> {};
+
+template <int DT>
+struct VecLoad1 {
+  __device__ __forceinline__ static void load(const void *p, int64_t i, float *v) {
+    v[0] = load_elem<DT>(p, i);
+  }
+};
+template <>
+struct VecLoad<SMX_F32, 1> : VecLoad1<SMX_F32> {};
+template <>
+struct VecLoad<SMX_BF16, 1> : VecLoad1<SMX_BF16> {};
+template <>
+struct VecLoad<SMX_F16, 1> : VecLoad1<SMX_F16> {};
+
+// grid = (column tiles, row chunks); block = kStatsThreads.
+// A column tile is CT lanes x VEC channels; a wave covers 64/CT rows per
+// step, the block kStatsWaves*64/CT rows per step.
+template <int DT, int VEC, int CT, bool FIRST>
+__global__ void __launch_bounds__(kStatsThreads)
+stats_accumulate_kernel(const void *__restrict__ x, int64_t rows, int64_t cols,
+                        int64_t row_stride, int64_t rows_per_chunk,
+                        float *__restrict__ slots_sq, float *__restrict__ slots_first) {
+  constexpr int RPW = 64 / CT;                 // rows per wave step
+  constexpr int GROUPS = kStatsWaves * RPW;    // row groups per block
+  constexpr int TW = CT * VEC;                 // channels per tile
+  __shared__ float red_sq[GROUPS][TW];
+  __shared__ float red_first[FIRST ? GROUPS : 1][FIRST ? TW : 1];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int group = wave * RPW + lane / CT;
+  const int64_t vcol = static_cast<int64_t>(blockIdx.x) * CT + (lane % CT);
+  const int64_t col0 = vcol * VEC;
+  const int64_t r_begin = static_cast<int64_t>(blockIdx.y) * rows_per_chunk;
+  const int64_t r_end = min(rows, r_begin + rows_per_chunk);
+  if (r_begin >= r_end) return;  // whole block: nothing to add
+  const bool active = col0 < cols;
+
+  float acc_sq[VEC], acc_first[VEC];
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) { acc_sq[k] = 0.f; acc_first[k] = 0.f; }
+
+  if (active) {
+    constexpr int U = 4;
+    int64_t r = r_begin + group;
+    for (; r + (U - 1) * GROUPS < r_end; r += U * GROUPS) {
+      float v[U][VEC];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        VecLoad<DT, VEC>::load(x, (r + u * GROUPS) * row_stride + col0, v[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          acc_sq[k] = fmaf(v[u][k], v[u][k], acc_sq[k]);
+          if constexpr (FIRST) acc_first[k] += v[u][k];
+        }
+    }
+    for (; r < r_end; r += GROUPS) {
+      float v[VEC];
+      VecLoad<DT, VEC>::load(x, r * row_stride + col0, v);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        acc_sq[k] = fmaf(v[k], v[k], acc_sq[k]);
+        if constexpr (FIRST) acc_first[k] += v[k];
+      }
+    }
+  }
+  const int cl = (lane % CT) * VEC;
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    red_sq[group][cl + k] = acc_sq[k];
+    if constexpr (FIRST) red_first[group][cl + k] = acc_first[k];
+  }
+  __syncthreads();
+  const int64_t tile_col0 = static_cast<int64_t>(blockIdx.x) * TW;
+  float *slot_sq = slots_sq + static_cast<int64_t>(blockIdx.y) * cols + tile_col0;
+  float *slot_first = FIRST ? slots_first + static_cast<int64_t>(blockIdx.y) * cols + tile_col0 : nullptr;
+  for (int c = threadIdx.x; c < TW; c += kStatsThreads) {
+    if (tile_col0 + c >= cols) break;
+    float s = 0.f, f = 0.f;
+#pragma unroll
+    for (int g = 0; g < GROUPS; ++g) {
+      s += red_sq[g][c];
+      if constexpr (FIRST) f += red_first[g][c];
+    }
+    slot_sq[c] += s;
+    if constexpr (FIRST) slot_first[c] += f;
+  }
+}
+
+template <int DT, int VEC, int CT>
+static void launch_acc(const void *x, int64_t rows, int64_t cols, int64_t row_stride,
+                       float *slots_sq, float *slots_first, int32_t n_slots, hipStream_t st) {
+  const int64_t vcols = ceil_div(cols, VEC);
+  dim3 grid(static_cast<unsigned>(ceil_div(vcols, CT)), static_cast<unsigned>(n_slots));
+  const int64_t rpc = ceil_div(rows, n_slots);
+  if (slots_first)
+    hipLaunchKernelGGL((stats_accumulate_kernel<DT, VEC, CT, true>), grid, dim3(kStatsThreads), 0, st,
+                       x, rows, cols, row_stride, rpc, slots_sq, slots_first);
+  else
+    hipLaunchKernelGGL((stats_accumulate_kernel<DT, VEC, CT, false>), grid, dim3(kStatsThreads), 0, st,
+                       x, rows, cols, row_stride, rpc, slots_sq, slots_first);
+}
+
+template <int DT, int VEC>
+static void dispatch_ct(const void *x, int64_t rows, int64_t cols, int64_t row_stride,
+                        float *slots_sq, float *slots_first, int32_t n_slots, hipStream_t st) {
+  const int64_t vcols = ceil_div(cols, VEC);
+  if (vcols % 64 == 0 || vcols > 256)
+    launch_acc<DT, VEC, 64>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+  else if (vcols % 32 == 0 || vcols > 16)
+    launch_acc<DT, VEC, 32>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+  else
+    launch_acc<DT, VEC, 16>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+}
+
+// ------------------------------------------------------------- fold ---
+// grid = ceil(n / 256) blocks of 256: sum[c] += sum_p slots[p][c] (FP64).
+__device__ __forceinline__ void fold_channel(float *sum, float *slots, int64_t n, int32_t n_slots,
+                                             int64_t c) {
+  double t = 0.0;
+  for (int p = 0; p < n_slots; ++p) {
+    float *s = slots + static_cast<int64_t>(p) * n + c;
+    t += static_cast<double>(*s);
+    *s = 0.f;
+  }
+  sum[c] = static_cast<float>(static_cast<double>(sum[c]) + t);
+}
+
+__global__ void __launch_bounds__(256)
+stats_fold_kernel(float *sum_sq, float *slots_sq, float *sum_first, float *slots_first, int64_t n,
+                  int32_t n_slots) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= n) return;
+  fold_channel(sum_sq, slots_sq, n, n_slots, c);
+  if (sum_first) fold_channel(sum_first, slots_first, n, n_slots, c);
+}
+
+// ----------------------------------------------------------- finish ---
+constexpr int kFinishBatch = 24;  // descriptors per launch (by value)
+struct FinishPack {
+  smx_finish_desc d[kFinishBatch];
+  int32_t n;
+};
+
+// Fold pass over a batch of descriptors: grid.x enumerates 256-channel
+// chunks of every vector, grid.y = descriptor.
+__global__ void __launch_bounds__(256) finish_fold_kernel(FinishPack pack) {
+  const smx_finish_desc &d = pack.d[blockIdx.y];
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= d.n) return;
+  fold_channel(d.sum_sq, d.slots_sq, d.n, d.n_slots, c);
+  if (d.kind == 1) fold_channel(d.sum_first, d.slots_first, d.n, d.n_slots, c);
+}
+
+__device__ __forceinline__ float ema_update(float e, float x, float beta) {
+  // e.mul_(beta).add_(x, alpha=1-beta)
+  return e * beta + x * (1.0f - beta);
+}
+
+// One block per descriptor.
+__global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta) {
+  __shared__ double scratch[16];
+  const smx_finish_desc &d = pack.d[blockIdx.x];
+  const int64_t n = d.n;
+  const float cnt = static_cast<float>(d.count);
+  const int t = threadIdx.x;
+  if (d.kind == 2) {
+    // b = sum/count; b /= max(mean(b), tiny); EMA; diagonal inverse sqrt.
+    double part = 0.0;
+    for (int64_t c = t; c < n; c += 256) part += static_cast<double>(d.sum_sq[c] / cnt);
+    const float bmean = static_cast<float>(block_sum(part, scratch) / static_cast<double>(n));
+    const float den = fmaxf(bmean, FLT_MIN);
+    double epart = 0.0;
+    for (int64_t c = t; c < n; c += 256) {
+      const float b = (d.sum_sq[c] / cnt) / den;
+      const float e = d.first ? b : ema_update(d.ema[c], b, beta);
+      d.ema[c] = e;
+      epart += static_cast<double>(e);
+    }
+    const float em = static_cast<float>(block_sum(epart, scratch) / static_cast<double>(n));
+    const float emc = fmaxf(em, FLT_MIN);
+    for (int64_t c = t; c < n; c += 256) {
+      const float r = fmaxf(d.ema[c], em * 1e-6f) / emc;
+      d.inv[c] = rsqrtf(fmaxf(r, 1e-6f));
+      d.sum_sq[c] = 0.f;
+    }
+    return;
+  }
+  // A side: second = sum/count; EMA (first copies); factor.
+  double epart = 0.0;
+  for (int64_t c = t; c < n; c += 256) {
+    const float second = d.sum_sq[c] / cnt;
+    const float e = d.first ? second : ema_update(d.ema[c], second, beta);
+    d.ema[c] = e;
+    epart += static_cast<double>(e);
+    if (d.kind == 1) {
+      const float mean = d.sum_first[c] / cnt;
+      d.mean_ema[c] = d.first ? mean : ema_update(d.mean_ema[c], mean, beta);
+      d.sum_first[c] = 0.f;
+    }
+    d.sum_sq[c] = 0.f;
+  }
+  const float em = static_cast<float>(block_sum(epart, scratch) / static_cast<double>(n));
+  if (d.kind == 0) {
+    const float emc = fmaxf(em, FLT_MIN);
+    for (int64_t c = t; c < n; c += 256) {
+      const float r = fmaxf(d.ema[c], em * 1e-6f) / emc;
+      d.inv[c] = rsqrtf(fmaxf(r, 1e-6f));
+    }
+    return;
+  }
+  // rank-one: q = max(mean(e), tiny); var = max(e - m^2, 0);
+  // inv = rsqrt(max(var/q, 1e-6)); z = inv*m/sqrt(q); rho = sqrt(1+|z|^2);
+  // kappa = -1/(rho(rho+1)).
+  const float q = fmaxf(em, FLT_MIN);
+  const float sq = sqrtf(q);
+  double zpart = 0.0;
+  for (int64_t c = t; c < n; c += 256) {
+    const float m = d.mean_ema[c];
+    const float var = fmaxf(d.ema[c] - m * m, 0.f);
+    const float inv = rsqrtf(fmaxf(var / q, 1e-6f));
+    const float z = inv * (m / sq);
+    d.inv[c] = inv;
+    d.z[c] = z;
+    zpart += static_cast<double>(z) * static_cast<double>(z);
+  }
+  const double zz = block_sum(zpart, scratch);
+  if (t == 0) {
+    const float rho = sqrtf(1.0f + static_cast<float>(zz));
+    d.kappa[0] = -1.0f / (rho * (rho + 1.0f));
+  }
+}
+
+}  // namespace smx
+
+using namespace smx;
+
+extern "C" int smx_stats_accumulate(const void *x, int dtype, int64_t rows, int64_t cols,
+                                    int64_t row_stride, float *slots_sq, float *slots_first,
+                                    int32_t n_slots, void *stream) {
+  SMX_REQUIRE(rows >= 0 && cols >= 1, SMX_ESHAPE, "stats_accumulate: need rows >= 0 and cols >= 1");
+  if (rows == 0) return SMX_OK;  // empty microbatch: nothing to add
+  SMX_REQUIRE(x && slots_sq, SMX_EINVAL, "stats_accumulate: null pointer");
+  SMX_REQUIRE(row_stride >= cols || rows == 1, SMX_ESHAPE, "stats_accumulate: row_stride must be >= cols");
+  SMX_REQUIRE(n_slots >= 1 && n_slots <= 65535, SMX_EINVAL, "stats_accumulate: n_slots in [1, 65535]");
+  SMX_REQUIRE(dtype == SMX_F32 || dtype == SMX_BF16 || dtype == SMX_F16, SMX_EDTYPE,
+              "stats_accumulate: dtype must be f32, bf16 or f16");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(x);
+  if (dtype == SMX_F32) {
+    if (cols % 4 == 0 && row_stride % 4 == 0 && addr % 16 == 0)
+      dispatch_ct<SMX_F32, 4>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+    else
+      dispatch_ct<SMX_F32, 1>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+  } else {
+    const bool v8 = cols % 8 == 0 && row_stride % 8 == 0 && addr % 16 == 0;
+    if (dtype == SMX_BF16) {
+      if (v8) dispatch_ct<SMX_BF16, 8>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+      else dispatch_ct<SMX_BF16, 1>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+    } else {
+      if (v8) dispatch_ct<SMX_F16, 8>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+      else dispatch_ct<SMX_F16, 1>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+    }
+  }
+  return check_launch("stats_accumulate");
+}
+
+extern "C" int smx_stats_fold(float *sum_sq, float *slots_sq, float *sum_first, float *slots_first,
+                              int64_t n, int32_t n_slots, void *stream) {
+  SMX_REQUIRE(sum_sq && slots_sq, SMX_EINVAL, "stats_fold: null pointer");
+  SMX_REQUIRE((sum_first == nullptr) == (slots_first == nullptr), SMX_EINVAL,
+              "stats_fold: sum_first and slots_first must both be set or both NULL");
+  SMX_REQUIRE(n >= 1 && n_slots >= 1, SMX_ESHAPE, "stats_fold: n >= 1 and n_slots >= 1");
+  hipLaunchKernelGGL(stats_fold_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), sum_sq, slots_sq, sum_first, slots_first, n,
+                     n_slots);
+  return check_launch("stats_fold");
+}
+
+extern "C" int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc, float beta,
+                                void *stream) {
+  SMX_REQUIRE(n_desc >= 0, SMX_EINVAL, "stats_finish: n_desc < 0");
+  SMX_REQUIRE(n_desc == 0 || descs, SMX_EINVAL, "stats_finish: null descriptor table");
+  for (int32_t i = 0; i < n_desc; ++i) {
+    const smx_finish_desc &d = descs[i];
+    SMX_REQUIRE(d.kind >= 0 && d.kind <= 2, SMX_EINVAL, "stats_finish: kind must be 0, 1 or 2");
+    SMX_REQUIRE(d.n >= 1 && d.count >= 1 && d.n_slots >= 1, SMX_ESHAPE,
+                "stats_finish: need n >= 1, count >= 1, n_slots >= 1");
+    SMX_REQUIRE(d.sum_sq && d.slots_sq && d.ema && d.inv, SMX_EINVAL,
+                "stats_finish: sum_sq, slots_sq, ema and inv are required");
+    if (d.kind == 1)
+      SMX_REQUIRE(d.sum_first && d.slots_first && d.mean_ema && d.z && d.kappa, SMX_EINVAL,
+                  "stats_finish: rank-one descriptor needs sum_first, slots_first, mean_ema, z, kappa");
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  for (int32_t b = 0; b < n_desc; b += kFinishBatch) {
+    FinishPack pack{};
+    pack.n = std::min<int32_t>(kFinishBatch, n_desc - b);
+    int64_t nmax = 1;
+    for (int i = 0; i < pack.n; ++i) {
+      pack.d[i] = descs[b + i];
+      nmax = std::max<int64_t>(nmax, pack.d[i].n);
+    }
+    hipLaunchKernelGGL(finish_fold_kernel, dim3(static_cast<unsigned>(ceil_div(nmax, 256)), pack.n),
+                       dim3(256), 0, st, pack);
+    int rc = check_launch("stats_finish(fold)");
+    if (rc) return rc;
+    hipLaunchKernelGGL(finish_kernel, dim3(pack.n), dim3(256), 0, st, pack, beta);
+    rc = check_launch("stats_finish");
+    if (rc) return rc;
+  }
+  return SMX_OK;
+}

@@ -1,0 +1,473 @@
+"""SandMuon optimizer on MI355X: the public API of sandmuon/optimizer.py with
+every tensor operation of the hooks and of step() running in the gfx950 HIP
+kernels of libsandmuon_amd.so.
+
+Drop-in surface (sandmuon/optimizer.py:96-328): DiagonalWeightedPE,
+RankOneAWeightedPE, module_filter, the forward/cotangent hooks, step(),
+state_dict()/load_state_dict() (inherited, same state keys and types) and
+close().  The module-level helpers imported by the reference tests
+(_s8_fp32, diagonal_inverse_sqrt, _graft_direction, rank1_inverse_sqrt,
+rank1_mapback, rank1_whiten) are GPU-backed here as well.
+
+Added keyword (default keeps the production recipe): ``s8_mode`` selects the
+arithmetic of the S8 products, "comp_bf16" (compensated BF16 MFMA, FP32
+intermediates) or "fp32" (FP32 MFMA).
+"""
+from __future__ import annotations
+
+import math
+import re
+from typing import Callable, Dict, List, Optional, Tuple
+
+import torch
+from torch import nn
+from torch.optim import Optimizer
+
+from . import _native
+from .coefficients import S8_COEFFICIENTS, S8_MARGIN, S8_MULTIPLIER
+
+__all__ = [
+    "DiagonalWeightedPE", "RankOneAWeightedPE", "diagonal_inverse_sqrt", "rank1_inverse_sqrt",
+    "rank1_whiten", "rank1_mapback", "_graft_direction", "_s8_fp32",
+]
+
+# q/k/v activation-statistic sharing rule (sandmuon/optimizer.py:129-135).
+_QKV_SHARE = re.compile(r"^(transformer\.h\.\d+\.attn\.)[kv]_proj\.weight$")
+
+_KIND_DIAG_A, _KIND_RANK1_A, _KIND_B = 0, 1, 2
+
+
+# --------------------------------------------------------------- helpers ---
+def _to_gpu_f32(t: torch.Tensor) -> torch.Tensor:
+    if t.device.type != "cuda":
+        if not torch.cuda.is_available():
+            raise RuntimeError("sandmuon_amd needs a ROCm GPU; none is available")
+        t = t.to(torch.device("cuda", torch.cuda.current_device()))
+    return t.to(torch.float32).contiguous()
+
+
+def _finish_vector(kind: int, second: torch.Tensor, first: Optional[torch.Tensor]):
+    """Runs the batched finish kernel on one vector with count 1 (EMA copy)."""
+    dev = second.device
+    n = second.numel()
+    sum_sq = second.clone()
+    slots_sq = torch.zeros(1, n, dtype=torch.float32, device=dev)
+    ema = torch.empty(n, dtype=torch.float32, device=dev)
+    inv = torch.empty(n, dtype=torch.float32, device=dev)
+    d = _native.FinishDesc(sum_sq=sum_sq.data_ptr(), slots_sq=slots_sq.data_ptr(), ema=ema.data_ptr(),
+                           inv=inv.data_ptr(), n=n, count=1, n_slots=1, kind=kind, first=1)
+    z = kappa = None
+    if kind == _KIND_RANK1_A:
+        sum_first = first.clone()
+        slots_first = torch.zeros(1, n, dtype=torch.float32, device=dev)
+        mean_ema = torch.empty(n, dtype=torch.float32, device=dev)
+        z = torch.empty(n, dtype=torch.float32, device=dev)
+        kappa = torch.empty(1, dtype=torch.float32, device=dev)
+        d.sum_first, d.slots_first = sum_first.data_ptr(), slots_first.data_ptr()
+        d.mean_ema, d.z, d.kappa = mean_ema.data_ptr(), z.data_ptr(), kappa.data_ptr()
+    _native.stats_finish([d], 1.0, dev)
+    return inv, z, kappa
+
+
+def diagonal_inverse_sqrt(value: torch.Tensor) -> torch.Tensor:
+    """Mean-normalised diagonal inverse square root (sandmuon/optimizer.py:19-24)."""
+    v = _to_gpu_f32(value).reshape(-1)
+    if v.numel() == 0:
+        return value.new_empty(value.shape)
+    inv, _, _ = _finish_vector(_KIND_DIAG_A, v, None)
+    return inv.reshape(value.shape).to(value.device, value.dtype)
+
+
+def rank1_inverse_sqrt(second: torch.Tensor, mean: torch.Tensor):
+    """D^-1/2 and the Sherman-Morrison rank-one (z, kappa) (sandmuon/optimizer.py:27-35)."""
+    s = _to_gpu_f32(second).reshape(-1)
+    m = _to_gpu_f32(mean).reshape(-1)
+    inv, z, kappa = _finish_vector(_KIND_RANK1_A, s, m)
+    out = lambda t: t.to(second.device, second.dtype)
+    return out(inv), out(z), out(kappa.reshape(()))
+
+
+def _batched_factor(f, batch_shape, n, device):
+    vec = _to_gpu_f32(f[0]).expand(*batch_shape, n).reshape(-1, n).contiguous()
+    z = _to_gpu_f32(f[1]).expand(*batch_shape, n).reshape(-1, n).contiguous()
+    c = _to_gpu_f32(torch.as_tensor(f[2])).expand(*batch_shape).reshape(-1).contiguous()
+    return vec.to(device), z.to(device), c.to(device)
+
+
+def _rank1(matrix: torch.Tensor, left, right, order: int) -> torch.Tensor:
+    x = _to_gpu_f32(matrix)
+    r, c = x.shape[-2], x.shape[-1]
+    batch_shape = x.shape[:-2]
+    xb = x.reshape(-1, r, c)
+    out = torch.empty_like(xb)
+    lf = _batched_factor(left, batch_shape, r, x.device)
+    rf = _batched_factor(right, batch_shape, c, x.device)
+    _native.rank1_apply(xb, out, lf, rf, order)
+    res = out.reshape(x.shape)
+    return res.to(matrix.device, torch.promote_types(matrix.dtype, torch.float32))
+
+
+def rank1_whiten(matrix: torch.Tensor, left, right) -> torch.Tensor:
+    """Dense left/right rank-one whiteners without forming matrices (sandmuon/optimizer.py:38-45)."""
+    return _rank1(matrix, left, right, 0)
+
+
+def rank1_mapback(value: torch.Tensor, left, right) -> torch.Tensor:
+    """Rank-one factors, then diagonals (sandmuon/optimizer.py:48-60)."""
+    return _rank1(value, left, right, 1)
+
+
+def _graft_direction(value: torch.Tensor, output_rows: int) -> torch.Tensor:
+    """Frobenius graft to sqrt(output_rows) (sandmuon/optimizer.py:63-66)."""
+    v = _to_gpu_f32(value)
+    out = torch.empty_like(v)
+    _native.graft(v, out, int(output_rows))
+    return out.to(value.device)
+
+
+def _s8_fp32(x: torch.Tensor, mode: str = "fp32") -> torch.Tensor:
+    """S8 polar map on [..., rows, cols] (sandmuon/optimizer.py:69-93), FP32 MFMA by default."""
+    v = _to_gpu_f32(x)
+    r, c = v.shape[-2], v.shape[-1]
+    vb = v.reshape(-1, r, c)
+    out = torch.empty_like(vb)
+    _native.s8(vb, out, _native.S8_MODES[mode])
+    return (out.reshape(v.shape) * S8_MULTIPLIER).to(x.device)
+
+
+def select_matrices(model: nn.Module, module_filter=None):
+    """Selected matrices and their modules, in named_modules() order.
+
+    sandmuon/optimizer.py:106-118: every module accepted by the filter
+    (default: every nn.Linear) whose `.weight` is a trainable 2-D Parameter.
+    """
+    choose = module_filter or (lambda name, module: isinstance(module, nn.Linear))
+    matrices: Dict[str, nn.Parameter] = {}
+    modules: Dict[str, nn.Module] = {}
+    for name, module in dict(model.named_modules()).items():
+        if name and choose(name, module):
+            parameter = getattr(module, "weight", None)
+            if isinstance(parameter, nn.Parameter) and parameter.requires_grad and parameter.ndim == 2:
+                matrices[name + ".weight"] = parameter
+                modules[name + ".weight"] = module
+    if not matrices:
+        raise ValueError("No eligible trainable linear weights found")
+    return matrices, modules
+
+
+def shared_source(name: str, matrices: Dict[str, nn.Parameter]) -> str:
+    """Name of the matrix whose activation statistic `name` uses.
+
+    sandmuon/optimizer.py:128-135: transformer.h.N.attn.{k,v}_proj share the
+    statistic of the same block's q_proj when it is selected; every other
+    matrix is its own source.
+    """
+    match = _QKV_SHARE.match(name)
+    if match and (match.group(1) + "q_proj.weight") in matrices:
+        return match.group(1) + "q_proj.weight"
+    return name
+
+
+def _rows2d(t: torch.Tensor) -> torch.Tensor:
+    """[..., d] -> [N, d] view with unit column stride (hook input layout)."""
+    _native.require_gpu(t, "statistics hook")
+    rows = t.detach().reshape(-1, t.shape[-1])
+    if rows.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        rows = rows.float()
+    if rows.shape[1] > 1 and rows.stride(1) != 1:
+        rows = rows.contiguous()
+    return rows
+
+
+# ------------------------------------------------------------- optimizer ---
+class DiagonalWeightedPE(Optimizer):
+    """S8 directions weighted by activation and output-cotangent diagonals.
+
+    Mirrors sandmuon/optimizer.py:96-321.  Statistics are accumulated from
+    every forward/backward microbatch between optimizer steps; defaults
+    match the 103M run (beta .97, momentum .8, S8 margin 1.35, AdamW LR
+    ratio .1 and decay .01).
+    """
+
+    # Slot rows per statistics vector: each hook launch spreads its rows over
+    # this many row chunks, each chunk owning one slot row.
+    STAT_SLOTS = 128
+
+    def __init__(self, model: nn.Module, lr: float, *, rank_one_a: bool = False,
+                 module_filter: Optional[Callable[[str, nn.Module], bool]] = None,
+                 s8_mode: str = "comp_bf16"):
+        matrices, modules = select_matrices(model, module_filter)
+        if s8_mode not in _native.S8_MODES:
+            raise ValueError(f"s8_mode must be one of {sorted(_native.S8_MODES)}")
+        _native.lib()  # fails loudly without the HIP library
+
+        self.named_matrices = matrices
+        self.parameter_names = {id(p): name for name, p in matrices.items()}
+        self.rank_one_a = bool(rank_one_a)
+        self.statistic_beta = .97
+        self.s8_coefficients = S8_COEFFICIENTS
+        self.s8_margin = S8_MARGIN
+        self.s8_mode = s8_mode
+        self._group_constants = {}
+
+        self.a_sources = {id(p): matrices[shared_source(name, matrices)] for name, p in matrices.items()}
+
+        matrix_ids = {id(p) for p in matrices.values()}
+        auxiliary = [p for p in model.parameters() if p.requires_grad and id(p) not in matrix_ids]
+        for p in list(matrices.values()) + auxiliary:
+            if p.device.type != "cuda":
+                raise RuntimeError("sandmuon_amd runs on ROCm GPU parameters only; move the model to the GPU "
+                                   f"before constructing the optimizer (got {p.device})")
+            if p.dtype != torch.float32:
+                raise TypeError(f"sandmuon_amd expects float32 parameters (got {p.dtype})")
+        defaults = dict(lr=float(lr), use_muon=True, momentum=.8, weight_decay=0.,
+                        adamw_lr_ratio=.1, adamw_betas=(.9, .999), adamw_eps=1e-8)
+        groups = [dict(params=list(matrices.values()), use_muon=True)]
+        if auxiliary:
+            groups.append(dict(params=auxiliary, use_muon=False, weight_decay=.01))
+        super().__init__(groups, defaults)
+        # Pending per-chunk partial sums of the hooks, folded into a_sum /
+        # b_sum by step() (or before state_dict()).  Not optimizer state.
+        self._slots: Dict[Tuple[int, str], Tuple[nn.Parameter, torch.Tensor, Optional[torch.Tensor]]] = {}
+        self._workspace: Optional[torch.Tensor] = None
+        self.register_state_dict_pre_hook(DiagonalWeightedPE._flush_slots)
+        self.register_load_state_dict_post_hook(DiagonalWeightedPE._drop_slots)
+        self.handles = []
+        for name, module in modules.items():
+            parameter = matrices[name]
+            self.handles.append(module.register_forward_hook(
+                self._capture(parameter, capture_a=self.a_sources[id(parameter)] is parameter)))
+
+    # ------------------------------------------------------------ hooks ---
+    def _slot_pair(self, parameter, side: str, n: int, device, first: bool):
+        key = (id(parameter), side)
+        entry = self._slots.get(key)
+        if entry is None or entry[1].shape[1] != n:
+            sq = torch.zeros(self.STAT_SLOTS, n, dtype=torch.float32, device=device)
+            fs = torch.zeros_like(sq) if first else None
+            entry = (parameter, sq, fs)
+            self._slots[key] = entry
+        return entry[1], entry[2]
+
+    def _accumulate_a(self, parameter, x: torch.Tensor, state: Optional[dict] = None) -> None:
+        """Forward-hook body (sandmuon/optimizer.py:156-168): a_sum += sum x^2,
+        a_first_sum += sum x (rank-one), a_count += rows."""
+        state = self.state[parameter] if state is None else state
+        rows = _rows2d(x)
+        if "a_sum" not in state:
+            state["a_sum"] = torch.zeros(rows.shape[-1], device=rows.device, dtype=torch.float32)
+            state["a_count"] = 0
+            if self.rank_one_a:
+                state["a_first_sum"] = torch.zeros_like(state["a_sum"])
+        sq, fs = self._slot_pair(parameter, "a", rows.shape[-1], rows.device, self.rank_one_a)
+        _native.stats_accumulate(rows, sq, fs)
+        state["a_count"] += rows.shape[0]
+
+    def _accumulate_b(self, parameter, delta: torch.Tensor, state: Optional[dict] = None) -> None:
+        """Cotangent-hook body (sandmuon/optimizer.py:171-177): b_sum += sum delta^2."""
+        state = self.state[parameter] if state is None else state
+        rows = _rows2d(delta)
+        if "b_sum" not in state:
+            state["b_sum"] = torch.zeros(rows.shape[-1], device=rows.device, dtype=torch.float32)
+            state["b_count"] = 0
+        sq, _ = self._slot_pair(parameter, "b", rows.shape[-1], rows.device, False)
+        _native.stats_accumulate(rows, sq, None)
+        state["b_count"] += rows.shape[0]
+
+    def _capture(self, parameter, *, capture_a):
+        def hook(module, inputs, output):
+            if (not module.training or not torch.is_grad_enabled() or
+                    not isinstance(output, torch.Tensor) or not output.requires_grad):
+                return
+            state = self.state[parameter]
+            if capture_a:
+                self._accumulate_a(parameter, inputs[0], state)
+
+            def cotangent_hook(gradient):
+                self._accumulate_b(parameter, gradient, state)
+                return gradient
+            output.register_hook(cotangent_hook)
+        return hook
+
+    @staticmethod
+    def _flush_slots(self) -> None:
+        """Folds pending hook partials into a_sum / b_sum (before state_dict())."""
+        for (pid, side), (parameter, sq, fs) in self._slots.items():
+            state = self.state.get(parameter, {})
+            total = state.get(f"{side}_sum")
+            if total is None:
+                continue
+            first = state.get("a_first_sum") if side == "a" and fs is not None else None
+            _native.stats_fold(total, sq, first, fs if first is not None else None)
+
+    @staticmethod
+    def _drop_slots(self) -> None:
+        """Loaded sums are authoritative: pending partials are discarded."""
+        self._slots.clear()
+
+    # ------------------------------------------------------------- step ---
+    def _finish_a_check(self, parameter) -> int:
+        state = self.state[parameter]
+        if state.get("a_count", 0) < 1:
+            raise RuntimeError(f"Missing activation statistics: {self.parameter_names[id(parameter)]}")
+        return state["a_count"]
+
+    def _finish_b_check(self, parameter, expected_count: int) -> None:
+        state = self.state[parameter]
+        if state.get("b_count", 0) != expected_count:
+            raise RuntimeError(f"Missing or mismatched cotangent statistics: {self.parameter_names[id(parameter)]}; "
+                               f"expected {expected_count}, got {state.get('b_count', 0)}")
+
+    def _finish_desc(self, parameter, side: str, count: int, out: Dict[str, torch.Tensor]) -> _native.FinishDesc:
+        state = self.state[parameter]
+        total = state[f"{side}_sum"]
+        n = total.numel()
+        rank1 = side == "a" and self.rank_one_a
+        sq, fs = self._slot_pair(parameter, side, n, total.device, rank1)
+        ema_key = f"{side}_ema"
+        first = ema_key not in state
+        if first:
+            state[ema_key] = torch.empty(n, dtype=torch.float32, device=total.device)
+            if rank1:
+                state["a_mean_ema"] = torch.empty(n, dtype=torch.float32, device=total.device)
+        kind = _KIND_B if side == "b" else (_KIND_RANK1_A if rank1 else _KIND_DIAG_A)
+        d = _native.FinishDesc(sum_sq=total.data_ptr(), slots_sq=sq.data_ptr(), ema=state[ema_key].data_ptr(),
+                               inv=out["inv"].data_ptr(), n=n, count=int(count), n_slots=sq.shape[0],
+                               kind=kind, first=int(first))
+        if rank1:
+            d.sum_first, d.slots_first = state["a_first_sum"].data_ptr(), fs.data_ptr()
+            d.mean_ema = state["a_mean_ema"].data_ptr()
+            d.z, d.kappa = out["z"].data_ptr(), out["kappa"].data_ptr()
+        return d
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        if closure is None:
+            loss = None
+        else:
+            with torch.enable_grad():
+                loss = closure()
+        matrix_items, auxiliary_items = [], []
+        a_counts: Dict[int, int] = {}
+        for group in self.param_groups:
+            for parameter in group["params"]:
+                if parameter.grad is None:
+                    continue
+                if group.get("use_muon", True):
+                    source = self.a_sources[id(parameter)]
+                    if id(source) not in a_counts:
+                        a_counts[id(source)] = self._finish_a_check(source)
+                    self._finish_b_check(parameter, a_counts[id(source)])
+                    matrix_items.append((parameter, source, group))
+                else:
+                    auxiliary_items.append((parameter, group))
+        if matrix_items:
+            self._matrix_update(matrix_items, a_counts)
+        self._auxiliary_update(auxiliary_items)
+        return loss
+
+    def _matrix_update(self, items, a_counts) -> None:
+        device = items[0][0].device
+        sources = []
+        seen = set()
+        for parameter, source, _ in items:
+            if id(source) not in seen:
+                seen.add(id(source))
+                sources.append(source)
+        # One flat buffer for every factor of this step.
+        sizes = []
+        for s in sources:
+            d = self.state[s]["a_sum"].numel()
+            sizes += [d, d, 1] if self.rank_one_a else [d]
+        for parameter, _, _ in items:
+            sizes.append(parameter.shape[0])
+        flat = torch.empty(sum(sizes), dtype=torch.float32, device=device)
+        views = iter(torch.split(flat, sizes))
+        a_out, b_out, descs = {}, {}, []
+        for s in sources:
+            out = {"inv": next(views)}
+            if self.rank_one_a:
+                out["z"], out["kappa"] = next(views), next(views)
+            a_out[id(s)] = out
+            descs.append(self._finish_desc(s, "a", a_counts[id(s)], out))
+        for parameter, source, _ in items:
+            out = {"inv": next(views)}
+            b_out[id(parameter)] = out
+            descs.append(self._finish_desc(parameter, "b", a_counts[id(source)], out))
+        _native.stats_finish(descs, self.statistic_beta, device)
+        for s in sources:
+            self.state[s]["a_count"] = 0
+        for parameter, _, _ in items:
+            self.state[parameter]["b_count"] = 0
+
+        mdescs, shapes = [], []
+        for parameter, source, group in items:
+            state = self.state[parameter]
+            if "momentum_buffer" not in state:
+                state["momentum_buffer"] = torch.zeros_like(parameter, dtype=torch.float32)
+            grad = parameter.grad
+            if grad.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                grad = grad.float()
+            grad = grad.contiguous()
+            a = a_out[id(source)]
+            md = _native.MatrixDesc(param=parameter.data_ptr(), grad=grad.data_ptr(),
+                                    momentum=state["momentum_buffer"].data_ptr(),
+                                    inv_row=b_out[id(parameter)]["inv"].data_ptr(), inv_col=a["inv"].data_ptr(),
+                                    rows=parameter.shape[0], cols=parameter.shape[1], lr=float(group["lr"]),
+                                    momentum_beta=float(group["momentum"]),
+                                    grad_dtype=_native.dtype_code(grad.dtype))
+            if self.rank_one_a:
+                md.z, md.kappa = a["z"].data_ptr(), a["kappa"].data_ptr()
+            mdescs.append(md)
+            shapes.append(tuple(parameter.shape))
+        mode = _native.S8_MODES[self.s8_mode]
+        need = _native.matrix_step_workspace_bytes(shapes, mode)
+        if self._workspace is None or self._workspace.numel() < need or self._workspace.device != device:
+            self._workspace = None
+            self._workspace = torch.empty(need, dtype=torch.uint8, device=device)
+        _native.matrix_step(mdescs, mode, self._workspace)
+
+    def _auxiliary_update(self, items) -> None:
+        by_group: Dict[int, list] = {}
+        for parameter, group in items:
+            by_group.setdefault(id(group), []).append((parameter, group))
+        for entries in by_group.values():
+            group = entries[0][1]
+            b1, b2 = group["adamw_betas"]
+            descs, offset = [], 0
+            device = entries[0][0].device
+            for parameter, _ in entries:
+                state = self.state[parameter]
+                if "exp_avg" not in state:
+                    state["exp_avg"] = torch.zeros_like(parameter, dtype=torch.float32)
+                    state["exp_avg_sq"] = torch.zeros_like(parameter, dtype=torch.float32)
+                    state["step"] = 0
+                state["step"] = int(state["step"]) + 1
+                grad = parameter.grad
+                if grad.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                    grad = grad.float()
+                grad = grad.contiguous()
+                n = parameter.numel()
+                descs.append(_native.AdamwDesc(
+                    param=parameter.data_ptr(), grad=grad.data_ptr(), exp_avg=state["exp_avg"].data_ptr(),
+                    exp_avg_sq=state["exp_avg_sq"].data_ptr(), n=n, offset=offset,
+                    bias1=1 - b1 ** state["step"], bias2=1 - b2 ** state["step"],
+                    grad_dtype=_native.dtype_code(grad.dtype)))
+                offset += n
+            lr = group["lr"] * group["adamw_lr_ratio"]
+            _native.adamw(descs, offset, lr, b1, b2, group["adamw_eps"], group["weight_decay"], device)
+
+    def close(self):
+        for handle in self.handles:
+            handle.remove()
+        self.handles.clear()
+
+
+class RankOneAWeightedPE(DiagonalWeightedPE):
+    """Production SAND variant with exact rank-one activation mean correction
+    (sandmuon/optimizer.py:324-328)."""
+
+    def __init__(self, model: nn.Module, lr: float, *,
+                 module_filter: Optional[Callable[[str, nn.Module], bool]] = None,
+                 s8_mode: str = "comp_bf16"):
+        super().__init__(model, lr, rank_one_a=True, module_filter=module_filter, s8_mode=s8_mode)

@@ -1,0 +1,103 @@
+"""CPU checks of the C ABI: the library loads without a GPU, exports every
+function include/sandmuon_amd.h declares, its struct layouts match the
+ctypes mirrors, and argument validation fails cleanly before any GPU work."""
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from sandmuon_amd import _native
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "sandmuon_amd.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(smx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_reports_abi_version():
+    lib = _native.lib()
+    assert lib.smx_abi_version() == _native.ABI_VERSION
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _native.lib()
+    names = declared_functions()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _native.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_native.SIGNATURES) == set(names)
+    nm = shutil.which("nm")
+    if nm:
+        out = subprocess.run([nm, "-D", "--defined-only", str(_native.LIB_PATH)], capture_output=True, text=True).stdout
+        exported = set(re.findall(r"\bT (smx_[a-z0-9_]+)", out))
+        assert set(names) <= exported
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc missing")
+def test_struct_layouts_match_header(tmp_path):
+    src = tmp_path / "layout.c"
+    fields = {
+        "smx_finish_desc": _native.FinishDesc,
+        "smx_adamw_desc": _native.AdamwDesc,
+        "smx_matrix_desc": _native.MatrixDesc,
+    }
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "sandmuon_amd.h"', "int main(void){"]
+    for cname, cls in fields.items():
+        lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0;}")
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], capture_output=True, text=True).stdout.split("\n") if l)
+    for cname, cls in fields.items():
+        assert int(got[cname]) == ctypes.sizeof(cls), cname
+        for f, _ in cls._fields_:
+            assert int(got[f"{cname}.{f}"]) == getattr(cls, f).offset, (cname, f)
+
+
+def test_validation_errors_return_before_gpu_work():
+    lib = _native.lib()
+    # bad dtype
+    rc = lib.smx_stats_accumulate(ctypes.c_void_p(16), 9, 4, 4, 4, ctypes.c_void_p(16), None, 1, None)
+    assert rc == -3
+    assert b"dtype" in lib.smx_last_error()
+    # empty input is a no-op even with null pointers
+    assert lib.smx_stats_accumulate(None, 0, 0, 4, 4, None, None, 1, None) == 0
+    # matrix step: workspace too small
+    d = _native.MatrixDesc(param=16, grad=16, momentum=16, inv_row=16, inv_col=16, rows=64, cols=32,
+                           lr=1e-3, momentum_beta=.8, grad_dtype=0)
+    arr = (_native.MatrixDesc * 1)(d)
+    assert lib.smx_matrix_step(arr, 1, 1, ctypes.c_void_p(256), 1024, None) == -5
+    # rank-one z without kappa
+    d.z = 16
+    arr = (_native.MatrixDesc * 1)(d)
+    assert lib.smx_matrix_step(arr, 1, 1, ctypes.c_void_p(256), 1 << 40, None) == -1
+    # unknown S8 mode
+    assert lib.smx_s8(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 4, 4, 16, 4, 1, 7, ctypes.c_void_p(256), 1 << 20,
+                      None) == -1
+    # finish: bad kind
+    f = _native.FinishDesc(sum_sq=16, slots_sq=16, ema=16, inv=16, n=4, count=1, n_slots=1, kind=5)
+    assert lib.smx_stats_finish((_native.FinishDesc * 1)(f), 1, .97, None) == -1
+    # adamw: offsets must be prefix sums
+    a = _native.AdamwDesc(param=16, grad=16, exp_avg=16, exp_avg_sq=16, n=4, offset=3, bias1=.1, bias2=.1)
+    assert lib.smx_adamw((_native.AdamwDesc * 1)(a), 1, 4, 1e-3, .9, .999, 1e-8, .01, None) == -2
+
+
+def test_workspace_sizes_are_consistent():
+    # 103M GPT matrices: 36 of 768x768 and 18 of 768x3072 (9 of them transposed).
+    shapes = [(768, 768)] * 36 + [(3072, 768)] * 9 + [(768, 3072)] * 9
+    for mode in (0, 1):
+        ws = _native.matrix_step_workspace_bytes(shapes, mode)
+        # four iterate planes of r x c plus two r x r planes per matrix (fp32)
+        dense = 4 * (36 * 768 * 768 + 18 * 768 * 3072) * 4 + 2 * 54 * 768 * 768 * 4
+        assert dense <= ws <= dense * 1.01
+    assert _native.lib().smx_s8_workspace_bytes(2, 7, 3, 0) > 0

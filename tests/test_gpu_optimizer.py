@@ -1,0 +1,193 @@
+"""End-to-end GPU parity of RankOneAWeightedPE / DiagonalWeightedPE against
+the CPU oracle on identical inputs.
+
+The GPU model runs forward/backward; every hooked activation and cotangent
+and every gradient is captured and fed to the oracle, so both sides see the
+same numbers.  Gates (north star): statistics/EMA state rel. error <= 1e-6;
+per-matrix update direction rel. Frobenius error <= 1e-4 (fp32 mode) and
+<= 1e-2 (comp_bf16 mode).  AdamW parameters: elementwise FP32 (<= 1e-6).
+"""
+import copy
+import math
+
+import pytest
+import torch
+from torch import nn
+
+from oracle import sandmuon_oracle as O
+from sandmuon_amd import DiagonalWeightedPE, RankOneAWeightedPE
+from sandmuon_amd.workloads import GPT, GPT_TINY, rng, transformer_filter
+
+pytestmark = pytest.mark.gpu
+
+DIR_TOL = {"fp32": 1e-4, "comp_bf16": 1e-2}
+STATS_TOL = 1e-6
+
+
+def rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-300)).item()
+
+
+class Capture:
+    """Records the inputs and output cotangents of the selected modules."""
+
+    def __init__(self, model, names):
+        self.records = []
+        self.handles = []
+        modules = dict(model.named_modules())
+        for name in names:
+            mod = modules[name[: -len(".weight")]]
+            self.handles.append(mod.register_forward_hook(self._hook(name)))
+
+    def _hook(self, name):
+        def hook(module, inputs, output):
+            self.records.append((name, "a", inputs[0].detach().float().cpu().clone()))
+
+            def th(grad):
+                self.records.append((name, "b", grad.detach().float().cpu().clone()))
+                return grad
+            output.register_hook(th)
+        return hook
+
+    def drain(self):
+        out, self.records = self.records, []
+        return out
+
+    def close(self):
+        for h in self.handles:
+            h.remove()
+
+
+def run_pair(device, model, batches, loss_fn, opt_cls, mode, lr, steps, module_filter=None):
+    gpu_model = model.to(device)
+    cpu_model = copy.deepcopy(model).cpu()
+    opt = opt_cls(gpu_model, lr, module_filter=module_filter, s8_mode=mode)
+    ora = O.OracleOptimizer(cpu_model, lr, rank_one_a=opt.rank_one_a, module_filter=module_filter, hooks=False)
+    assert list(opt.named_matrices) == list(ora.matrices)
+    cap = Capture(gpu_model, opt.named_matrices)
+    gparams = dict(gpu_model.named_parameters())
+    cparams = dict(cpu_model.named_parameters())
+    name_of = {id(p): n for n, p in gparams.items()}
+    history = []
+    for _ in range(steps):
+        opt.zero_grad(set_to_none=True)
+        for x, y in batches:
+            loss_fn(gpu_model, x.to(device), y.to(device)).backward()
+        for name, kind, t in cap.drain():
+            ora.feed(name, x=t if kind == "a" else None, delta=t if kind == "b" else None)
+        with torch.no_grad():
+            for n, p in gparams.items():
+                cparams[n].copy_(p.detach().cpu())
+                cparams[n].grad = None if p.grad is None else p.grad.detach().cpu().clone()
+        before = {n: p.detach().clone() for n, p in gparams.items()}
+        opt.step()
+        ora.step()
+        torch.cuda.synchronize()
+        history.append((before, {n: p.detach().clone() for n, p in gparams.items()},
+                        {n: p.detach().clone() for n, p in cparams.items()}))
+        # state comparisons
+        for n, p in opt.named_matrices.items():
+            gs, cs = opt.state[p], ora.st(ora.matrices[n])
+            for key in ("a_ema", "a_mean_ema", "b_ema"):
+                if key in cs:
+                    assert key in gs, (n, key)
+                    assert rel(gs[key], cs[key]) <= STATS_TOL, (n, key, rel(gs[key], cs[key]))
+            for key in ("a_count", "b_count"):
+                if key in cs:
+                    assert gs[key] == cs[key] == 0
+            assert rel(gs["momentum_buffer"], cs["momentum_buffer"]) <= 1e-6
+    cap.close()
+    opt.close()
+    return history, opt, ora
+
+
+def check_directions(history, opt, lr, mode):
+    worst = 0.0
+    for before, after_g, after_c in history:
+        for n in opt.named_matrices:
+            dg = (before[n] - after_g[n]).double().cpu() / lr
+            dc = (before[n].cpu() - after_c[n]).double() / lr
+            e = rel(dg, dc)
+            worst = max(worst, e)
+            assert e <= DIR_TOL[mode], (n, e)
+            # Frobenius graft: ||dW|| / lr = sqrt(rows) (tests/test_optimizer.py:215-237)
+            assert abs(dg.norm().item() - math.sqrt(before[n].shape[0])) <= 1e-4 * math.sqrt(before[n].shape[0])
+    return worst
+
+
+def check_aux(history, opt, ora=None):
+    # AdamW is elementwise FP32: parameters agree to a few ulp.  (The update
+    # delta itself is not compared: for weights near 1 one ulp of p is
+    # ~1e-4 of a 1e-3-scale step.)
+    for before, after_g, after_c in history:
+        for n, p in after_g.items():
+            if n in opt.named_matrices:
+                continue
+            assert rel(after_g[n], after_c[n]) <= 1e-6, n
+    if ora is not None:
+        for p_g, p_c in zip(opt.param_groups[-1]["params"], ora.aux):
+            gs, cs = opt.state[p_g], ora.st(p_c)
+            assert gs["step"] == cs["step"] and isinstance(gs["step"], int)
+            assert rel(gs["exp_avg"], cs["exp_avg"]) <= 1e-6
+            assert rel(gs["exp_avg_sq"], cs["exp_avg_sq"]) <= 1e-6
+
+
+def mse(model, x, y):
+    return (model(x) - y).square().mean()
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+def test_cfg1_single_linear_768(device, mode):
+    """BASELINE cfg1: fp32 Linear 768->768, W ~ N(0, .02), bias 0, lr 1e-2,
+    4 microbatches of 16x1024 tokens, x = N(0,1) + mu_c (mu_c ~ N(0, .5)),
+    MSE against N(0,1) targets."""
+    r = rng(1001)
+    model = nn.Linear(768, 768)
+    with torch.no_grad():
+        model.weight.copy_(torch.from_numpy(r.normal(0, 0.02, (768, 768))).float())
+        model.bias.zero_()
+    mu = torch.from_numpy(r.normal(0, 0.5, 768)).float()
+    batches = []
+    for _ in range(4):
+        x = torch.from_numpy(r.standard_normal((16, 1024, 768))).float() + mu
+        y = torch.from_numpy(r.standard_normal((16, 1024, 768))).float()
+        batches.append((x, y))
+
+    class Wrap(nn.Module):
+        def __init__(self, lin):
+            super().__init__()
+            self.proj = lin
+
+        def forward(self, x):
+            return self.proj(x)
+
+    loss = lambda m, x, y: (m(x) - y).square().mean() / 4
+    hist, opt, _ = run_pair(device, Wrap(model), batches, loss, RankOneAWeightedPE, mode, 1e-2, steps=1)
+    worst = check_directions(hist, opt, 1e-2, mode)
+    print(f"cfg1 {mode}: worst direction rel err {worst:.3e}")
+    check_aux(hist, opt)
+
+
+@pytest.mark.parametrize("opt_cls", [RankOneAWeightedPE, DiagonalWeightedPE])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+def test_tiny_gpt_two_steps(device, opt_cls, mode):
+    torch.manual_seed(21)
+    model = GPT(GPT_TINY)
+    model.init_weights(21)
+    g = torch.Generator().manual_seed(22)
+    batches = []
+    for mb in range(3):
+        idx = torch.randint(0, GPT_TINY.vocab, (2 + mb, GPT_TINY.ctx), generator=g)
+        tgt = torch.randint(0, GPT_TINY.vocab, (2 + mb, GPT_TINY.ctx), generator=g)
+        batches.append((idx, tgt))
+    loss = lambda m, x, y: m(x, y) / 3
+    hist, opt, ora = run_pair(device, model, batches, loss, opt_cls, mode, 3e-3, steps=2,
+                              module_filter=transformer_filter)
+    # q/k/v share the q activation statistic (sandmuon/optimizer.py:128-135)
+    blk = opt.named_matrices
+    assert opt.a_sources[id(blk["transformer.h.0.attn.k_proj.weight"])] is blk["transformer.h.0.attn.q_proj.weight"]
+    assert "a_ema" not in opt.state[blk["transformer.h.0.attn.k_proj.weight"]]
+    worst = check_directions(hist, opt, 3e-3, mode)
+    print(f"tiny gpt {opt_cls.__name__} {mode}: worst direction rel err {worst:.3e}")
+    check_aux(hist, opt, ora)

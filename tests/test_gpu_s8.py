@@ -1,0 +1,67 @@
+"""GPU parity of the S8 polar map (both arithmetic modes) against the oracle.
+
+Gates (north star): per-matrix relative Frobenius error vs the eager FP32
+restatement <= 1e-4 in FP32-MFMA mode and <= 1e-2 in compensated-BF16 mode.
+The FP64 SVD closed form U f(S) V^T is checked alongside.
+"""
+import pytest
+import torch
+
+from oracle import sandmuon_oracle as O
+from sandmuon_amd import _native
+from sandmuon_amd.optimizer import _s8_fp32
+from sandmuon_amd.workloads import s8_cfg2_batch
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"fp32": 1e-4, "comp_bf16": 1e-2}
+
+
+def per_matrix_rel(a, b):
+    a = a.double().cpu()
+    b = b.double().cpu()
+    return ((a - b).flatten(-2).norm(dim=-1) / b.flatten(-2).norm(dim=-1)).tolist()
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("shape", [(2, 7, 3), (2, 3, 7), (2, 4, 4), (3, 64, 96), (2, 300, 200), (1, 257, 513)])
+def test_s8_small_shapes(device, mode, shape):
+    torch.manual_seed(sum(shape))
+    x = torch.randn(*shape)
+    out = _s8_fp32(x.to(device), mode=mode)
+    assert out.shape == x.shape and torch.isfinite(out).all()
+    ref = O.s8(x)
+    assert max(per_matrix_rel(out, ref)) <= TOL[mode]
+    svd = O.s8_svd(x)
+    assert max(per_matrix_rel(out, svd)) <= TOL[mode]
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("shape", [(2, 768, 768), (1, 768, 3072), (1, 3072, 768)])
+def test_s8_cfg2_inputs(device, mode, shape):
+    x = s8_cfg2_batch(1002 + shape[1] + shape[2], *shape)
+    out = _s8_fp32(x.to(device), mode=mode)
+    ref = O.s8(x)
+    errs = per_matrix_rel(out, ref)
+    print(mode, shape, "rel err vs fp32 oracle", errs)
+    assert max(errs) <= TOL[mode]
+
+
+def test_s8_zero_matrix_is_zero_and_batch_neighbours_unaffected(device):
+    torch.manual_seed(3)
+    x = torch.randn(3, 40, 24)
+    x[1] = 0
+    out = _s8_fp32(x.to(device))
+    assert torch.equal(out[1].cpu(), torch.zeros(40, 24))
+    ref = O.s8(x[[0, 2]])
+    assert max(per_matrix_rel(out[[0, 2]], ref)) <= 1e-4
+    zero = _s8_fp32(torch.zeros(1, 4, 3, device=device))
+    assert torch.equal(zero.cpu(), torch.zeros(1, 4, 3))
+
+
+def test_s8_orientation_transpose_equivariance(device):
+    torch.manual_seed(5)
+    x = torch.randn(2, 48, 80, device=device)
+    a = _s8_fp32(x)
+    b = _s8_fp32(x.transpose(-2, -1).contiguous())
+    assert max(per_matrix_rel(b.transpose(-2, -1), a)) <= 1e-5

@@ -1,0 +1,90 @@
+"""Host-side logic of the drop-in API that runs without a GPU: matrix
+selection, q/k/v sharing, constructor errors and the loud failure on CPU
+parameters (the HIP library is the only compute path)."""
+import pytest
+import torch
+from torch import nn
+
+from sandmuon_amd import DiagonalWeightedPE, RankOneAWeightedPE, S8_COEFFICIENTS, S8_MARGIN, S8_MULTIPLIER
+from sandmuon_amd.optimizer import select_matrices, shared_source
+from sandmuon_amd.workloads import GPT, GPT_103M, GPT_TINY, transformer_filter
+
+
+class Attention(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.q_proj = nn.Linear(4, 4, bias=False)
+        self.k_proj = nn.Linear(4, 4, bias=False)
+        self.v_proj = nn.Linear(4, 4, bias=False)
+
+
+class Block(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.attn = Attention()
+        self.cross_attn = Attention()
+
+
+class Model(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.transformer = nn.Module()
+        self.transformer.h = nn.ModuleList([Block(), Block()])
+
+
+def test_qkv_sharing_only_for_production_attention_names():
+    # tests/test_optimizer.py:152-193 (selection part)
+    matrices, _ = select_matrices(Model())
+    src = {n: shared_source(n, matrices) for n in matrices}
+    for i in (0, 1):
+        q = f"transformer.h.{i}.attn.q_proj.weight"
+        assert src[f"transformer.h.{i}.attn.k_proj.weight"] == q
+        assert src[f"transformer.h.{i}.attn.v_proj.weight"] == q
+        assert src[q] == q
+        for p in ("q", "k", "v"):
+            n = f"transformer.h.{i}.cross_attn.{p}_proj.weight"
+            assert src[n] == n
+
+
+def test_k_without_q_is_unshared():
+    matrices, _ = select_matrices(Model(), lambda n, m: isinstance(m, nn.Linear) and "q_proj" not in n)
+    assert shared_source("transformer.h.0.attn.k_proj.weight", matrices) == "transformer.h.0.attn.k_proj.weight"
+
+
+def test_selection_default_and_filter():
+    m = nn.Sequential(nn.Linear(4, 5), nn.Tanh(), nn.Linear(5, 2))
+    mats, mods = select_matrices(m)
+    assert list(mats) == ["0.weight", "2.weight"]
+    frozen = nn.Sequential(nn.Linear(4, 5))
+    frozen[0].weight.requires_grad_(False)
+    with pytest.raises(ValueError, match="No eligible trainable linear weights found"):
+        select_matrices(frozen)
+
+
+def test_gpt_103m_layout():
+    # BASELINE cfg4: 103,176,192 parameters; 54 selected matrices holding 63,700,992.
+    with torch.device("meta"):
+        model = GPT(GPT_103M)
+    assert sum(p.numel() for p in model.parameters()) == 103_176_192
+    mats, _ = select_matrices(model, transformer_filter)
+    assert len(mats) == 54
+    assert sum(p.numel() for p in mats.values()) == 63_700_992
+    sources = {shared_source(n, mats) for n in mats}
+    assert len(sources) == 36
+
+
+def test_constructor_errors():
+    with pytest.raises(ValueError, match="No eligible"):
+        RankOneAWeightedPE(nn.Sequential(nn.Tanh()), 1e-3)
+    # A bare module has no named submodule: nothing is selected (as in the
+    # reference, whose selection skips the root module).
+    with pytest.raises(ValueError, match="No eligible"):
+        RankOneAWeightedPE(nn.Linear(4, 3), 1e-3)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        RankOneAWeightedPE(nn.Sequential(nn.Linear(4, 3)), 1e-3)  # CPU parameters: no fallback
+    with pytest.raises(ValueError, match="s8_mode"):
+        DiagonalWeightedPE(nn.Sequential(nn.Linear(4, 3)), 1e-3, s8_mode="fp16")
+
+
+def test_public_exports():
+    assert S8_MARGIN == 1.35 and S8_MULTIPLIER == 1.0 and len(S8_COEFFICIENTS) == 5

@@ -1,0 +1,331 @@
+"""Pins of the CPU oracle that do not retype its formulas: dense-matrix
+identities, closed forms, the SVD form of S8, a library AdamW, float64
+brute force, the reference's own test intents (tests/test_optimizer.py), and
+planted mistakes that each pin must catch."""
+import copy
+import math
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import sandmuon_oracle as O
+
+# paper/main.tex:196-205 table and reproduction/paper/s8/data/completed/
+# s8_manifest.json:79-108 (second source for the coefficient schedule).
+MANIFEST_COEFFICIENTS = [
+    [11.062126275847973, -56.051653229128085, 72.32081107619855],
+    [4.100720073616268, -2.9324183165353577, 0.5339692084282731],
+    [3.930310192522361, -2.873509793709714, 0.5366557527206212],
+    [3.280567968245866, -2.414925589994015, 0.48635134757825227],
+    [2.282741575232451, -1.6302296637355072, 0.40275720810675486],
+]
+
+
+def test_coefficients_match_manifest():
+    assert [list(c) for c in O.S8_COEFFICIENTS] == MANIFEST_COEFFICIENTS
+    assert O.S8_MARGIN == 1.35 and O.S8_MULTIPLIER == 1.0
+    import sandmuon_amd.coefficients as C
+    assert C.S8_COEFFICIENTS == O.S8_COEFFICIENTS and C.S8_MARGIN == O.S8_MARGIN
+
+
+# ------------------------------------------------------------ factors ---
+def dense_whitener(second, mean, fn=O.rank1_inverse_sqrt):
+    inv, z, k = fn(second, mean)
+    return (torch.eye(second.numel(), dtype=second.dtype) + k * torch.outer(z, z)) @ torch.diag(inv)
+
+
+def covariance_identity(fn=O.rank1_inverse_sqrt):
+    # tests/test_optimizer.py:24-33: W (A / mean(second)) W^T = I.
+    torch.manual_seed(7)
+    x = torch.randn(500, 6, dtype=torch.float64) + torch.randn(6, dtype=torch.float64)
+    second, mean = x.square().mean(0), x.mean(0)
+    w = dense_whitener(second, mean, fn)
+    cov = torch.diag(second - mean.square()) + torch.outer(mean, mean)
+    torch.testing.assert_close(w @ (cov / second.mean()) @ w.T, torch.eye(6, dtype=torch.float64),
+                               atol=1e-10, rtol=1e-10)
+
+
+def test_rank1_inverse_sqrt_whitens_dense_covariance():
+    covariance_identity()
+
+
+def test_planted_kappa_sign_error_is_caught():
+    def wrong(second, mean):
+        inv, z, k = O.rank1_inverse_sqrt(second, mean)
+        return inv, z, -k
+    with pytest.raises(AssertionError):
+        covariance_identity(wrong)
+
+
+def test_diagonal_inverse_sqrt_closed_form_and_zero_signal():
+    v = torch.tensor([4.0, 1.0, 0.0, 1e-9], dtype=torch.float64)
+    m = v.mean().item()  # 1.25
+    expect = torch.tensor([(4 / m) ** -.5, (1 / m) ** -.5, 1e-6 ** -.5, 1e-6 ** -.5], dtype=torch.float64)
+    torch.testing.assert_close(O.diagonal_inverse_sqrt(v), expect)
+    assert torch.isfinite(O.diagonal_inverse_sqrt(torch.zeros(4))).all()
+
+
+# --------------------------------------------------- whiten / mapback ---
+def test_rank1_whiten_equals_dense_two_sided_product():
+    # tests/test_optimizer.py:35-43
+    torch.manual_seed(7)
+    x = torch.randn(500, 6, dtype=torch.float64) + torch.randn(6, dtype=torch.float64)
+    second, mean = x.square().mean(0), x.mean(0)
+    left = O.rank1_inverse_sqrt(second, mean)
+    right = O.rank1_inverse_sqrt(second[:4], mean[:4])
+    src = torch.randn(2, 6, 4, dtype=torch.float64)
+    out = O.rank1_whiten(src, tuple(t.expand(2, *t.shape) if t.ndim else t.expand(2) for t in left),
+                         tuple(t.expand(2, *t.shape) if t.ndim else t.expand(2) for t in right))
+    wl, wr = dense_whitener(second, mean), dense_whitener(second[:4], mean[:4])
+    torch.testing.assert_close(out, torch.stack([wl @ m @ wr.T for m in src]), atol=1e-10, rtol=1e-10)
+
+
+def test_rank1_mapback_equals_dense_product():
+    # tests/test_optimizer.py:46-54
+    torch.manual_seed(8)
+    q = torch.randn(5, 3, dtype=torch.float64)
+    li, lz, lc = O.rank1_inverse_sqrt(torch.rand(5, dtype=torch.float64) + .3, torch.randn(5, dtype=torch.float64) * .1)
+    ri, rz, rc = O.rank1_inverse_sqrt(torch.rand(3, dtype=torch.float64) + .3, torch.randn(3, dtype=torch.float64) * .1)
+    expect = (torch.diag(li) @ (torch.eye(5, dtype=q.dtype) + lc * torch.outer(lz, lz)) @ q
+              @ (torch.eye(3, dtype=q.dtype) + rc * torch.outer(rz, rz)) @ torch.diag(ri))
+    torch.testing.assert_close(O.rank1_mapback(q, (li, lz, lc), (ri, rz, rc)), expect)
+
+
+def test_graft_norm_and_reference_zero_behaviour():
+    v = torch.randn(7, 3)
+    assert abs(O.graft_direction(v, 7).norm().item() - math.sqrt(7)) < 1e-5
+    assert torch.equal(O.graft_direction(torch.zeros(3, 4), 3), torch.zeros(3, 4))
+    # sandmuon/optimizer.py:63-66: for >= 16 rows sqrt(rows)/FLT_MIN overflows
+    # and a zero direction becomes NaN (a reference edge case, not copied
+    # by the GPU build).
+    assert torch.isnan(O.graft_direction(torch.zeros(16, 4), 16)).all()
+
+
+# ------------------------------------------------------------------ S8 ---
+def test_stage_polynomial_via_numpy_polyval():
+    # The scalar composition against numpy's polynomial evaluator:
+    # p(t) = t (a + b t^2 + c t^4) as coefficients [c, 0, b, 0, a, 0].
+    t = np.linspace(1e-4, 1 / 1.35, 50)
+    ref = t.copy()
+    for a, b, c in MANIFEST_COEFFICIENTS:
+        ref = np.polyval([c, 0, b, 0, a, 0], ref)
+    sigma = torch.from_numpy(t * 1.35)
+    got = O.s8_scalar(sigma, torch.ones((), dtype=torch.float64), O.S8_COEFFICIENTS, O.S8_MARGIN).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-12)
+
+
+def test_s8_diagonal_input_maps_singular_values():
+    # X = diag(sigma) (padded): S8(X) = diag(f(sigma)).
+    sigma = torch.tensor([3.0, 1.0, 0.5, 1e-3], dtype=torch.float64)
+    x = torch.zeros(4, 6, dtype=torch.float64)
+    x[range(4), range(4)] = sigma
+    sensor = (sigma ** 8).sum() ** 0.125
+    f = O.s8_scalar(sigma, sensor)
+    expect = torch.zeros(4, 6, dtype=torch.float64)
+    expect[range(4), range(4)] = f
+    torch.testing.assert_close(O.s8(x), expect, atol=1e-12, rtol=1e-10)
+
+
+@pytest.mark.parametrize("shape", [(2, 7, 3), (2, 3, 7), (2, 4, 4), (1, 40, 64)])
+def test_s8_matches_svd_closed_form(shape):
+    torch.manual_seed(13)
+    x = torch.randn(*shape, dtype=torch.float64)
+    torch.testing.assert_close(O.s8(x), O.s8_svd(x), atol=1e-10, rtol=1e-9)
+    y32 = O.s8(x.float())
+    assert ((y32.double() - O.s8_svd(x)).norm() / O.s8_svd(x).norm()) < 1e-4
+
+
+def test_planted_transposed_gram_is_caught():
+    # A stage built on X^T X (the wrong Gram) applied from the left: valid
+    # shapes for a square input, wrong map.  The SVD closed form rejects it.
+    def wrong(x):
+        x = x / torch.linalg.matrix_norm(x, keepdim=True)
+        g = x.transpose(-2, -1) @ x
+        g2 = g @ g
+        s = O.S8_MARGIN * torch.linalg.matrix_norm(g2, keepdim=True) ** .25
+        eye = torch.eye(x.shape[-1], dtype=x.dtype)
+        a, b, c = O.S8_COEFFICIENTS[0]
+        x = ((a * eye + b * g / s ** 2 + c * g2 / s ** 4) @ x) / s
+        for a, b, c in O.S8_COEFFICIENTS[1:]:
+            g = x.transpose(-2, -1) @ x
+            x = (a * eye + b * g + c * g @ g) @ x
+        return x
+    torch.manual_seed(2)
+    x = torch.randn(1, 6, 6, dtype=torch.float64)
+    assert not torch.allclose(wrong(x), O.s8_svd(x), atol=1e-3)
+    torch.testing.assert_close(O.s8(x), O.s8_svd(x), atol=1e-10, rtol=1e-9)
+
+
+def test_planted_missing_schatten_scale_is_caught():
+    def no_scale(x):
+        saved = O.S8_MARGIN
+        try:
+            return O.s8(x, margin=1.0 / 1e6)  # margin slip: wrong sensor scaling
+        finally:
+            assert saved == O.S8_MARGIN
+    x = torch.randn(1, 6, 9, dtype=torch.float64)
+    assert not torch.allclose(no_scale(x), O.s8_svd(x), atol=1e-6)
+
+
+def test_s8_orientation_and_zero():
+    # tests/test_optimizer.py:140-149
+    torch.manual_seed(13)
+    for shape in ((7, 3), (3, 7), (4, 4)):
+        x = torch.randn(2, *shape)
+        y = O.s8(x)
+        assert y.shape == x.shape and torch.isfinite(y).all()
+        torch.testing.assert_close(O.s8(x.transpose(-2, -1)).transpose(-2, -1), y)
+    assert torch.equal(O.s8(torch.zeros(1, 4, 3)), torch.zeros(1, 4, 3))
+
+
+# --------------------------------------------------------------- stats ---
+def test_accumulate_rows_float64_brute_force():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(4, 37, 19, generator=g) * 3 + 1
+    sq, fs = torch.zeros(19), torch.zeros(19)
+    n = O.accumulate_rows(x, sq, fs)
+    assert n == 4 * 37
+    flat = x.reshape(-1, 19).double()
+    torch.testing.assert_close(sq.double(), (flat ** 2).sum(0), rtol=1e-6, atol=0)
+    torch.testing.assert_close(fs.double(), flat.sum(0), rtol=1e-5, atol=1e-5)
+
+
+def test_nesterov_closed_form():
+    m, g = torch.randn(5, 3), torch.randn(5, 3)
+    m0 = m.clone()
+    src = O.nesterov(m, g, .8)
+    torch.testing.assert_close(m, .8 * m0 + .2 * g)
+    torch.testing.assert_close(src, .8 * (.8 * m0 + .2 * g) + .2 * g)
+
+
+def test_adamw_matches_torch_optim_adamw():
+    torch.manual_seed(4)
+    p1 = torch.randn(50, requires_grad=False)
+    p2 = nn.Parameter(p1.clone())
+    ref = torch.optim.AdamW([p2], lr=1e-3, betas=(.9, .999), eps=1e-8, weight_decay=.01)
+    st = {}
+    for _ in range(3):
+        g = torch.randn(50)
+        O.adamw(p1, g, st, 1e-3)
+        p2.grad = g.clone()
+        ref.step()
+        torch.testing.assert_close(p1, p2.detach(), rtol=1e-6, atol=1e-7)
+    assert st["step"] == 3 and isinstance(st["step"], int)
+
+
+class Proj(nn.Module):
+    def __init__(self, rows, cols):
+        super().__init__()
+        self.proj = nn.Linear(cols, rows, bias=False)
+
+    def forward(self, x):
+        return self.proj(x)
+
+
+def test_statistics_over_uneven_microbatches_analytic():
+    # tests/test_optimizer.py:57-85
+    torch.manual_seed(10)
+    model = Proj(3, 4)
+    x, target = torch.randn(9, 4), torch.randn(9, 3)
+    pred0 = model(x).detach()
+    expect_b = (2 * (pred0 - target) / 9).square().mean(0)
+    expect_b = expect_b / expect_b.mean()
+    opt = O.OracleOptimizer(model, 1e-3)
+    for a, b in ((0, 2), (2, 6), (6, 9)):
+        ((model(x[a:b]) - target[a:b]).square().sum() / 9).backward()
+    before = model.proj.weight.detach().clone()
+    opt.step()
+    st = opt.st(model.proj.weight)
+    torch.testing.assert_close(st["a_ema"], x.square().mean(0))
+    torch.testing.assert_close(st["b_ema"], expect_b)
+    assert st["a_count"] == st["b_count"] == 0
+    assert not torch.equal(before, model.proj.weight)
+
+
+def test_planted_ema_slip_is_caught():
+    st = {"a_sum": torch.tensor([2.0, 4.0]), "a_count": 2, "a_ema": torch.tensor([1.0, 1.0])}
+    O.finish_a(st, rank_one=False)
+    # 0.97*1 + 0.03*(sum/count) in closed form
+    torch.testing.assert_close(st["a_ema"], torch.tensor([0.97 + 0.03 * 1.0, 0.97 + 0.03 * 2.0]))
+    st2 = {"a_sum": torch.tensor([2.0, 4.0]), "a_count": 2, "a_ema": torch.tensor([1.0, 1.0])}
+    O.finish_a(st2, rank_one=False, beta=0.9)  # a wrong beta must not pass the same check
+    with pytest.raises(AssertionError):
+        torch.testing.assert_close(st2["a_ema"], st["a_ema"])
+
+
+@pytest.mark.parametrize("rank_one", [True, False])
+@pytest.mark.parametrize("shape", [(4, 4), (7, 3), (3, 7)])
+def test_update_norm_is_sqrt_rows(rank_one, shape):
+    # tests/test_optimizer.py:215-237
+    torch.manual_seed(15)
+    rows, cols = shape
+    model = Proj(rows, cols)
+    opt = O.OracleOptimizer(model, 1e-3, rank_one_a=rank_one)
+    before = model.proj.weight.detach().clone()
+    (model(torch.randn(12, cols)) - torch.randn(12, rows)).square().mean().backward()
+    opt.step()
+    norm = (model.proj.weight.detach() - before).norm() / 1e-3
+    assert abs(norm.item() - rows ** .5) <= 2e-5 * rows ** .5 + 2e-5
+
+
+def test_state_resume_matches_continuous():
+    # tests/test_optimizer.py:95-113, on the oracle's state dict.
+    torch.manual_seed(11)
+    a = nn.Sequential(nn.Linear(4, 5), nn.Tanh(), nn.Linear(5, 2))
+    b = copy.deepcopy(a)
+    oa = O.OracleOptimizer(a, 2e-3)
+    x, y = torch.randn(8, 4), torch.randn(8, 2)
+
+    def one(model, opt):
+        for p in model.parameters():
+            p.grad = None
+        (model(x) - y).square().mean().backward()
+        opt.step()
+    one(a, oa)
+    ob = O.OracleOptimizer(b, 2e-3)
+    b.load_state_dict(a.state_dict())
+    ids_a = {n: id(p) for n, p in a.named_parameters()}
+    ids_b = {n: id(p) for n, p in b.named_parameters()}
+    ob.state = {ids_b[n]: copy.deepcopy(oa.state[ids_a[n]]) for n in ids_a if ids_a[n] in oa.state}
+    one(a, oa)
+    one(b, ob)
+    for pa, pb in zip(a.parameters(), b.parameters()):
+        torch.testing.assert_close(pa, pb)
+
+
+def test_zero_signal_finite():
+    # tests/test_optimizer.py:116-137
+    model = Proj(3, 4)
+    opt = O.OracleOptimizer(model, 1e-3)
+    (model(torch.zeros(6, 4)) * 0).sum().backward()
+    opt.step()
+    assert torch.isfinite(model.proj.weight).all()
+    st = opt.st(model.proj.weight)
+    for k in ("a_ema", "a_mean_ema", "b_ema"):
+        assert torch.isfinite(st[k]).all()
+
+
+def test_comp_bf16_model_is_within_gate_on_cfg2_like_input():
+    # Budget check of the compensated mode's rounding model (all five stages
+    # compensated, FP32 intermediates) against the FP32 oracle.
+    from sandmuon_amd.workloads import s8_cfg2_batch
+    x = s8_cfg2_batch(7, 1, 96, 160)
+    ref = O.s8(x)
+    # A stage-by-stage compensated product model: hi*lo + lo*hi + hi*hi.
+    def comp_mm(a, b):
+        return O._mm_comp(a, b)
+    xx = x / torch.linalg.matrix_norm(x, keepdim=True)
+    eye = torch.eye(96)
+    for k, (a, b, c) in enumerate(O.S8_COEFFICIENTS):
+        g = comp_mm(xx, xx.transpose(-2, -1))
+        g2 = comp_mm(g, g)
+        if k == 0:
+            s = O.S8_MARGIN * torch.linalg.matrix_norm(g2, keepdim=True) ** .25
+            p = a * eye + b * g / s ** 2 + c * g2 / s ** 4
+            xx = comp_mm(p, xx) / s
+        else:
+            xx = comp_mm(a * eye + b * g + c * g2, xx)
+    err = ((xx - ref).norm() / ref.norm()).item()
+    assert err < 1e-3, err
