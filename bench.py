@@ -190,6 +190,10 @@ def cpu_model_name():
     return "unknown"
 
 
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 # ---------------------------------------------------------------- main ---
 def main():
     args = parse()
@@ -202,7 +206,9 @@ def main():
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    log(f"building {args.config} ({args.s8_mode})")
     model, opt, sets, micro, stat_bytes = build(args.config, args.s8_mode, device)
+    log(f"built: {len(opt.named_matrices)} matrices, {stat_bytes / 1e9:.2f} GB of hook input per step")
 
     def one_step():
         run_hooks(opt, sets, micro)
@@ -211,6 +217,7 @@ def main():
     for _ in range(args.warmup):
         one_step()
     torch.cuda.synchronize()
+    log("warmup done")
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
@@ -220,6 +227,7 @@ def main():
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / args.steps
     ms = start.elapsed_time(end) / args.steps
+    log(f"timed {args.steps} steps: {ms:.3f} ms/step")
 
     # Phase breakdown (untimed above): hooks of one step, step() alone.
     hooks_ms = time_events(lambda: run_hooks(opt, sets, micro))
@@ -255,7 +263,9 @@ def main():
         "roofline_s8": roof_s8,
         "phases_ms": {"hooks": round(hooks_ms, 3), "step": round(step_ms, 3), "host_wall_per_step": round(wall, 3)},
     }
+    log(f"breakdown: hooks {hooks_ms:.3f} ms, step {step_ms:.3f} ms, s8 {s8_ms:.3f} ms")
     if not args.no_cpu_baseline:
+        log("cpu baseline")
         threads = args.cpu_threads or len(os.sched_getaffinity(0))
         total, hooks, step, sample = cpu_baseline(args.config, threads)
         out["cpu_baseline"] = {"value": round(total, 1), "unit": "ms", "cores": threads, "kind": "port",

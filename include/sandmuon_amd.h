@@ -101,9 +101,12 @@ typedef struct smx_finish_desc {
 
 /* Batched _finish_a / _finish_b: sandmuon/optimizer.py:182-222 with
  * rank1_inverse_sqrt (:27-35) and diagonal_inverse_sqrt (:19-24).
+ * Scalar hyperparameters are passed in double: the FP32 coefficients beta
+ * and 1 - beta are both rounded from double, as the reference's
+ * mul_(beta).add_(x, alpha=1-beta) rounds two Python floats.
  * `descs` is a host array of n_desc descriptors (device pointers inside). */
 int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc,
-                     float beta, void *stream);
+                     double beta, void *stream);
 
 /* ------------------------------------------------------------------ *
  * AdamW on the auxiliary parameters: sandmuon/optimizer.py:268-281.
@@ -122,8 +125,8 @@ typedef struct smx_adamw_desc {
 } smx_adamw_desc;
 
 int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t total,
-              float lr, float beta1, float beta2, float eps,
-              float weight_decay, void *stream);
+              double lr, double beta1, double beta2, double eps,
+              double weight_decay, void *stream);
 
 /* ------------------------------------------------------------------ *
  * Matrix update: Nesterov momentum -> whiten -> S8 -> mapback -> graft ->
@@ -149,8 +152,8 @@ typedef struct smx_matrix_desc {
   const float *z;        /* [cols] A rank-one vector or NULL          */
   const float *kappa;    /* [1] A rank-one coefficient or NULL        */
   int64_t rows, cols;
-  float lr;
-  float momentum_beta;
+  double lr;
+  double momentum_beta;
   int32_t grad_dtype;
   int32_t pad_;
 } smx_matrix_desc;

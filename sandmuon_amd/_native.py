@@ -51,7 +51,7 @@ class AdamwDesc(ctypes.Structure):
 class MatrixDesc(ctypes.Structure):
     _fields_ = [("param", c_void_p), ("grad", c_void_p), ("momentum", c_void_p),
                 ("inv_row", c_void_p), ("inv_col", c_void_p), ("z", c_void_p), ("kappa", c_void_p),
-                ("rows", c_int64), ("cols", c_int64), ("lr", c_float), ("momentum_beta", c_float),
+                ("rows", c_int64), ("cols", c_int64), ("lr", c_double), ("momentum_beta", c_double),
                 ("grad_dtype", c_int32), ("pad_", c_int32)]
 
 
@@ -62,9 +62,9 @@ SIGNATURES = {
     "smx_stats_accumulate": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                      c_int32, c_void_p]),
     "smx_stats_fold": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
-    "smx_stats_finish": (c_int, [ctypes.POINTER(FinishDesc), c_int32, c_float, c_void_p]),
-    "smx_adamw": (c_int, [ctypes.POINTER(AdamwDesc), c_int32, c_int64, c_float, c_float, c_float, c_float,
-                          c_float, c_void_p]),
+    "smx_stats_finish": (c_int, [ctypes.POINTER(FinishDesc), c_int32, c_double, c_void_p]),
+    "smx_adamw": (c_int, [ctypes.POINTER(AdamwDesc), c_int32, c_int64, c_double, c_double, c_double, c_double,
+                          c_double, c_void_p]),
     "smx_matrix_step_workspace_bytes": (c_size_t, [ctypes.POINTER(c_int64), ctypes.POINTER(c_int64),
                                                    c_int32, c_int]),
     "smx_matrix_step": (c_int, [ctypes.POINTER(MatrixDesc), c_int32, c_int, c_void_p, c_size_t, c_void_p]),

@@ -50,8 +50,8 @@ __global__ void __launch_bounds__(256) adamw_kernel(AdamPack pk) {
 
 using namespace smx;
 
-extern "C" int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t total, float lr, float beta1,
-                         float beta2, float eps, float weight_decay, void *stream) {
+extern "C" int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t total, double lr, double beta1,
+                         double beta2, double eps, double weight_decay, void *stream) {
   SMX_REQUIRE(n_desc >= 0 && (n_desc == 0 || descs), SMX_EINVAL, "adamw: bad descriptor table");
   int64_t sum = 0;
   for (int32_t i = 0; i < n_desc; ++i) {
@@ -74,13 +74,15 @@ extern "C" int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t to
       pk.d[i].offset -= base;
     }
     pk.total = pk.d[pk.n - 1].offset + pk.d[pk.n - 1].n;
-    pk.neg_lr = -lr;
-    pk.decay = static_cast<float>(1.0 - static_cast<double>(lr) * static_cast<double>(weight_decay));
-    pk.b1 = beta1;
-    pk.omb1 = static_cast<float>(1.0 - static_cast<double>(beta1));
-    pk.b2 = beta2;
-    pk.omb2 = static_cast<float>(1.0 - static_cast<double>(beta2));
-    pk.eps = eps;
+    // Each FP32 coefficient is rounded from the double the reference
+    // computes in Python (1 - lr*wd, 1 - beta, -lr).
+    pk.neg_lr = static_cast<float>(-lr);
+    pk.decay = static_cast<float>(1.0 - lr * weight_decay);
+    pk.b1 = static_cast<float>(beta1);
+    pk.omb1 = static_cast<float>(1.0 - beta1);
+    pk.b2 = static_cast<float>(beta2);
+    pk.omb2 = static_cast<float>(1.0 - beta2);
+    pk.eps = static_cast<float>(eps);
     if (pk.total == 0) continue;
     hipLaunchKernelGGL(adamw_kernel, dim3(static_cast<unsigned>(ceil_div(pk.total, kAdamChunk))), dim3(256),
                        0, st, pk);

@@ -80,7 +80,7 @@ __global__ void __launch_bounds__(256) whiten_rows_kernel(MatPack pack) {
   const double zz = r1 ? sum_sq_vec(d.z, nullptr, d.cols, scratch) : 0.0;
   const float kappa = r1 ? d.kappa[0] : 0.f;
   const double corr = r1 ? 2.0 * kappa + static_cast<double>(kappa) * kappa * zz : 0.0;
-  const float beta = d.momentum_beta, omb = 1.0f - d.momentum_beta;
+  const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bool vec = d.grad_dtype == SMX_F32 && (d.cols % 4 == 0) &&
                    (reinterpret_cast<uintptr_t>(d.grad) % 16 == 0) &&
@@ -143,7 +143,7 @@ __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
   const int64_t i0 = (tb / tiles_c) * 64, j0 = (tb % tiles_c) * 64;
   const bool r1 = d.z != nullptr;
   const float kappa = r1 ? d.kappa[0] : 0.f;
-  const float beta = d.momentum_beta, omb = 1.0f - d.momentum_beta;
+  const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
   const int t = threadIdx.x;
   const int lc = (t & 15) * 4;
 #pragma unroll
@@ -234,7 +234,7 @@ __global__ void __launch_bounds__(256) mapback_apply_kernel(MatPack pack) {
   // _graft_direction: sqrt(rows) / max(||U||, FLT_MIN); a zero direction
   // gives a zero update.
   const float scale = n2 > 0.0 ? static_cast<float>(sqrt(static_cast<double>(d.rows))) / fmaxf(norm, FLT_MIN) : 0.f;
-  const float nlr = -d.lr;
+  const float nlr = static_cast<float>(-d.lr);
   const bool r1 = d.z != nullptr;
   const float kappa = r1 ? d.kappa[0] : 0.f;
   for (int rr = 0; rr < kRowsPerPart; ++rr) {

@@ -206,13 +206,13 @@ __global__ void __launch_bounds__(256) finish_fold_kernel(FinishPack pack) {
   if (d.kind == 1) fold_channel(d.sum_first, d.slots_first, d.n, d.n_slots, c);
 }
 
-__device__ __forceinline__ float ema_update(float e, float x, float beta) {
-  // e.mul_(beta).add_(x, alpha=1-beta)
-  return e * beta + x * (1.0f - beta);
+__device__ __forceinline__ float ema_update(float e, float x, float beta, float omb) {
+  // e.mul_(beta).add_(x, alpha=1-beta), both coefficients rounded from double
+  return e * beta + x * omb;
 }
 
 // One block per descriptor.
-__global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta) {
+__global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta, float omb) {
   __shared__ double scratch[16];
   const smx_finish_desc &d = pack.d[blockIdx.x];
   const int64_t n = d.n;
@@ -227,7 +227,7 @@ __global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta
     double epart = 0.0;
     for (int64_t c = t; c < n; c += 256) {
       const float b = (d.sum_sq[c] / cnt) / den;
-      const float e = d.first ? b : ema_update(d.ema[c], b, beta);
+      const float e = d.first ? b : ema_update(d.ema[c], b, beta, omb);
       d.ema[c] = e;
       epart += static_cast<double>(e);
     }
@@ -244,12 +244,12 @@ __global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta
   double epart = 0.0;
   for (int64_t c = t; c < n; c += 256) {
     const float second = d.sum_sq[c] / cnt;
-    const float e = d.first ? second : ema_update(d.ema[c], second, beta);
+    const float e = d.first ? second : ema_update(d.ema[c], second, beta, omb);
     d.ema[c] = e;
     epart += static_cast<double>(e);
     if (d.kind == 1) {
       const float mean = d.sum_first[c] / cnt;
-      d.mean_ema[c] = d.first ? mean : ema_update(d.mean_ema[c], mean, beta);
+      d.mean_ema[c] = d.first ? mean : ema_update(d.mean_ema[c], mean, beta, omb);
       d.sum_first[c] = 0.f;
     }
     d.sum_sq[c] = 0.f;
@@ -331,7 +331,7 @@ extern "C" int smx_stats_fold(float *sum_sq, float *slots_sq, float *sum_first, 
   return check_launch("stats_fold");
 }
 
-extern "C" int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc, float beta,
+extern "C" int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc, double beta,
                                 void *stream) {
   SMX_REQUIRE(n_desc >= 0, SMX_EINVAL, "stats_finish: n_desc < 0");
   SMX_REQUIRE(n_desc == 0 || descs, SMX_EINVAL, "stats_finish: null descriptor table");
@@ -359,7 +359,8 @@ extern "C" int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc, fl
                        dim3(256), 0, st, pack);
     int rc = check_launch("stats_finish(fold)");
     if (rc) return rc;
-    hipLaunchKernelGGL(finish_kernel, dim3(pack.n), dim3(256), 0, st, pack, beta);
+    hipLaunchKernelGGL(finish_kernel, dim3(pack.n), dim3(256), 0, st, pack, static_cast<float>(beta),
+                       static_cast<float>(1.0 - beta));
     rc = check_launch("stats_finish");
     if (rc) return rc;
   }
