@@ -36,7 +36,7 @@ struct MatJob {
   double *part;      // [ceil(rows/kRowsPerPart)] partial sums
   int64_t prow_pad, pcol_pad;
   int32_t blk0;      // first block of this job in the launch
-  int32_t pad_;
+  int32_t planes;    // whiten: write X, X^T as BF16 hi/lo planes (comp mode)
 };
 
 constexpr int kMatBatch = 12;
@@ -146,6 +146,7 @@ __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
   const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
   const int t = threadIdx.x;
   const int lc = (t & 15) * 4;
+  const int64_t n = J.prow_pad * J.pcol_pad;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int lr = (t >> 4) + 16 * q;
@@ -164,14 +165,14 @@ __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
       v[e] = val;
       tile[lr][lc + e] = val;
     }
-    *reinterpret_cast<float4 *>(J.pl + i * J.pcol_pad + j0 + lc) = make_float4(v[0], v[1], v[2], v[3]);
+    put_operand4(J.pl, n, i * J.pcol_pad + j0 + lc, v, J.planes != 0);
   }
   __syncthreads();
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int lr = (t >> 4) + 16 * q;  // transposed row = parameter column
-    *reinterpret_cast<float4 *>(J.tl + (j0 + lr) * J.prow_pad + i0 + lc) =
-        make_float4(tile[lc][lr], tile[lc + 1][lr], tile[lc + 2][lr], tile[lc + 3][lr]);
+    const float v[4] = {tile[lc][lr], tile[lc + 1][lr], tile[lc + 2][lr], tile[lc + 3][lr]};
+    put_operand4(J.tl, n, (j0 + lr) * J.prow_pad + i0 + lc, v, J.planes != 0);
   }
 }
 
@@ -384,10 +385,12 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
       j.pl = M.flip() ? M.xt0() : M.x0();
       j.tl = M.flip() ? M.x0() : M.xt0();
       j.part = M.fro();
+      j.planes = mode == SMX_S8_COMP_BF16;
       ping[k] = j;
       j.pl = M.flip() ? M.xt1() : M.x1();
       j.tl = nullptr;
       j.part = M.mb();
+      j.planes = 0;
       fin[k] = j;
     }
     int rc = launch_jobs(ping, row_blocks, whiten_rows_kernel, "whiten_rows", st);

@@ -24,8 +24,12 @@
 //                     60-66, applied in all five stages with FP32 storage
 //                     of every intermediate).
 //
-// Block: 256x256 output tile, 8 waves (2 x 4), each wave 128x64 (4 x 2
-// MFMA 32x32 tiles); K step 32, double-buffered LDS (2 x 64 KB).
+// Block: 256x256 output tile, 4 waves (2 x 2, one per SIMD), each wave
+// 128x128 (4 x 4 MFMA 32x32 tiles, 256 accumulators).  Operands stream into a 4-stage LDS ring (K = 16 per
+// stage, 32 KB) with direct-to-LDS 16-byte loads issued three stages ahead.
+// In compensated mode every operand is stored by its producer as BF16
+// hi/lo planes (put_operand), so the inner loop is LDS reads + MFMAs; only
+// the stage-1 polynomial operand is formed and split in registers.
 #include "s8.h"
 
 #include <algorithm>
@@ -38,9 +42,18 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 512;
-constexpr int kBK = 32;
-constexpr int kLdsBuf = 65536;  // bytes per pipeline buffer
+constexpr int kThreads = 256;     // 4 waves, one per SIMD
+constexpr int kWaves = kThreads / 64;
+constexpr int kSubM = 4, kSubN = 4; // 32x32 MFMA tiles per wave (128 x 128)
+constexpr int kBK = 16;            // K per pipeline stage
+constexpr int kF32Tile = 16384;    // 256 x 16 FP32 operand tile
+constexpr int kB16Tile = 8192;     // 256 x 16 BF16 plane tile
+constexpr int kStages = 4;         // LDS ring depth (3 stages in flight)
+constexpr int kPolyStages = 3;     // ring depth when A is formed from (G, G2)
+constexpr int kStageBytes = 2 * kF32Tile;          // A + B (FP32, or 4 BF16 planes)
+constexpr int kPolyStageBytes = 3 * kF32Tile;      // G + G2 + B
+constexpr int kRingBytes = kStages * kStageBytes > kPolyStages * kPolyStageBytes ? kStages * kStageBytes
+                                                                                 : kPolyStages * kPolyStageBytes;
 
 enum Phase { kGram = 0, kSquare = 1, kApply = 2 };
 
@@ -53,193 +66,314 @@ struct StageArgs {
   float a, b, c;
 };
 
-// ---------------------------------------------------------- operands ---
 struct PolyArgs {
   float a, b, c;     // stage-1 coefficients
   float is2, is4;    // 1/s^2, 1/s^4
   int64_t r;         // logical rows (identity only on real rows)
+  int64_t row0;      // first global row of the A tile
 };
 
-// Loads the kThreads-share of a 256 x 32 FP32 tile starting at (row0, k0):
-// thread t reads rows t/8 + 64q, columns (t%8)*4 .. +3.
-template <bool POLY>
-__device__ __forceinline__ void load_a_tile(const float *__restrict__ A, const float *__restrict__ A2,
-                                            int64_t ld, int64_t row0, int64_t k0, const PolyArgs &pa,
-                                            float4 (&out)[4]) {
-  const int t = threadIdx.x;
-  const int64_t col = k0 + (t & 7) * 4;
+// A K-contiguous GEMM operand: FP32 rows of `ld` elements, or BF16 hi/lo
+// planes (lo at hi + plane elements).
+struct Opnd {
+  const void *p;
+  int64_t ld;
+  int64_t plane;
+};
+
+// ------------------------------------------------------- LDS layouts ---
+// FP32 tile [256][16]: four 16-byte chunks per row, logical chunk kc at
+// slot kc ^ swz4(r).  BF16 plane tile [256][16]: two chunks per row, slot
+// c ^ swz2(r).  Both make the fragment reads (8 or 16 consecutive rows, one
+// chunk) conflict-free for 32- and 64-bank LDS.
+__device__ __forceinline__ int swz4(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+__device__ __forceinline__ int swz2(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
+__device__ __forceinline__ int f32_off(int r, int kc) { return (r * 4 + (kc ^ swz4(r))) << 4; }
+__device__ __forceinline__ int b16_off(int r, int c) { return (r * 2 + (c ^ swz2(r))) << 4; }
+
+// One 16-byte direct-to-LDS load per lane: lane l writes LDS[m0 + 16 l].
+// Issued from asm so the compiler does not treat later LDS reads as
+// aliasing the in-flight load (it would wait for every outstanding load);
+// the ring's waits are explicit (wait_vm).  M0 is an input operand.
+__device__ __forceinline__ void dma16(const void *src, char *lds_wave_base) {
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_wave_base));
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+
+// This wave's share of an FP32 tile (rows row0.., K k0..k0+15): LDS chunk
+// p = (wave*N+i)*64 + lane is stored slot p&3 of row p>>2.
+__device__ __forceinline__ void dma_f32(const float *__restrict__ M, int64_t ld, int64_t row0, int64_t k0,
+                                        char *tile) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr int N = 16 / kWaves;  // 1 KB loads per wave
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int64_t row = row0 + (t >> 3) + 64 * q;
-    float4 v = *reinterpret_cast<const float4 *>(A + row * ld + col);
-    if constexpr (POLY) {
-      // P1 = a I + (b G)/s^2 + (c G2)/s^4, evaluated left to right.
-      const float4 w = *reinterpret_cast<const float4 *>(A2 + row * ld + col);
-      float g[4] = {v.x, v.y, v.z, v.w}, g2[4] = {w.x, w.y, w.z, w.w};
-      float p[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float eye = (row == col + e && row < pa.r) ? pa.a : 0.f;
-        p[e] = (eye + (pa.b * g[e]) * pa.is2) + (pa.c * g2[e]) * pa.is4;
-      }
-      v = make_float4(p[0], p[1], p[2], p[3]);
-    }
-    out[q] = v;
+  for (int i = 0; i < N; ++i) {
+    const int p = (wave * N + i) * 64 + lane;
+    const int row = p >> 2;
+    const int kc = (p & 3) ^ swz4(row);
+    dma16(M + (row0 + row) * ld + k0 + kc * 4, tile + (wave * N + i) * 1024);
   }
 }
 
-__device__ __forceinline__ void load_b_tile(const float *__restrict__ B, int64_t ld, int64_t row0,
-                                            int64_t k0, float4 (&out)[4]) {
-  const int t = threadIdx.x;
-  const int64_t col = k0 + (t & 7) * 4;
+// This wave's share of a BF16 plane tile: LDS chunk p = (wave*N+i)*64 +
+// lane is stored slot p&1 of row p>>1.
+__device__ __forceinline__ void dma_b16(const uint16_t *__restrict__ M, int64_t ld, int64_t row0, int64_t k0,
+                                        char *tile) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr int N = 8 / kWaves;  // 1 KB loads per wave
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int64_t row = row0 + (t >> 3) + 64 * q;
-    out[q] = *reinterpret_cast<const float4 *>(B + row * ld + col);
+  for (int i = 0; i < N; ++i) {
+    const int p = (wave * N + i) * 64 + lane;
+    const int row = p >> 1;
+    const int c = (p & 1) ^ swz2(row);
+    dma16(M + (row0 + row) * ld + k0 + c * 8, tile + (wave * N + i) * 1024);
   }
 }
 
-// ------------------------------------------------------ LDS staging ---
-// COMP layout of one buffer: planes Ah, Al, Bh, Bl of [256][32] bf16 (64 B
-// rows, four 16-B chunks; chunk index XOR ((row>>1)&3)).
-// FP32 layout: planes A, B of [256][32] f32 (128 B rows, eight chunks;
-// chunk index XOR (row&7)).
-__device__ __forceinline__ int comp_off(int row, int ch) { return row * 64 + ((ch ^ ((row >> 1) & 3)) << 4); }
-__device__ __forceinline__ int f32_off(int row, int ch) { return row * 128 + ((ch ^ (row & 7)) << 4); }
-
-__device__ __forceinline__ void split4(float4 v, uint2 &hi, uint2 &lo) {
-  float x[4] = {v.x, v.y, v.z, v.w};
-  uint16_t h[4], l[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    h[e] = f32_to_bf16_bits(x[e]);
-    l[e] = f32_to_bf16_bits(x[e] - bf16_bits_to_f32(h[e]));
-  }
-  hi = make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
-  lo = make_uint2(l[0] | (static_cast<uint32_t>(l[1]) << 16), l[2] | (static_cast<uint32_t>(l[3]) << 16));
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if constexpr (N == 24) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else if constexpr (N == 36) asm volatile("s_waitcnt vmcnt(36)" ::: "memory");
+  else static_assert(N == 0, "unsupported vmcnt");
 }
 
-template <int MODE>
-__device__ __forceinline__ void store_tiles(char *buf, const float4 (&ra)[4], const float4 (&rb)[4]) {
-  const int t = threadIdx.x;
-  if constexpr (MODE == SMX_S8_COMP_BF16) {
-    const int ch = (t & 7) >> 1, half = (t & 1) * 8;
+__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// The 8 consecutive K values (k = 8h .. 8h+7 of the stage) of row r.
+__device__ __forceinline__ void read8(const char *tile, int r, int h, float (&v)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4 *>(tile + f32_off(r, 2 * h));
+  const f32x4 b = *reinterpret_cast<const f32x4 *>(tile + f32_off(r, 2 * h + 1));
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+__device__ __forceinline__ bf16x8 read_b16(const char *tile, int r, int h) {
+  return *reinterpret_cast<const bf16x8 *>(tile + b16_off(r, h));
+}
+
+__device__ __forceinline__ void split8(const float (&v)[8], bf16x8 &hi, bf16x8 &lo) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int row = (t >> 3) + 64 * q;
-      const int off = comp_off(row, ch) + half;
-      uint2 h, l;
-      split4(ra[q], h, l);
-      *reinterpret_cast<uint2 *>(buf + 0 * 16384 + off) = h;
-      *reinterpret_cast<uint2 *>(buf + 1 * 16384 + off) = l;
-      split4(rb[q], h, l);
-      *reinterpret_cast<uint2 *>(buf + 2 * 16384 + off) = h;
-      *reinterpret_cast<uint2 *>(buf + 3 * 16384 + off) = l;
-    }
-  } else {
-    const int ch = t & 7;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int row = (t >> 3) + 64 * q;
-      const int off = f32_off(row, ch);
-      *reinterpret_cast<float4 *>(buf + off) = ra[q];
-      *reinterpret_cast<float4 *>(buf + 32768 + off) = rb[q];
-    }
+  for (int e = 0; e < 8; ++e) {
+    const __bf16 h = static_cast<__bf16>(v[e]);
+    hi[e] = h;
+    lo[e] = static_cast<__bf16>(v[e] - static_cast<float>(h));
   }
 }
 
 // ----------------------------------------------------------- compute ---
+// Register fragments of one 16-deep K stage for this wave's 128 x 128
+// sub-tile: BF16 hi/lo pairs (compensated mode) or FP32 (FP32 mode).  The
+// A fragments of row block i are dead once row i's MFMAs are issued and are
+// reloaded in place with the next stage; the B fragments, used by every
+// row, are double-buffered.
 template <int MODE>
-__device__ __forceinline__ void compute_tile(const char *buf, int wm, int wn, f32x16 (&acc)[4][2]) {
+struct AFrag;
+template <>
+struct AFrag<SMX_S8_COMP_BF16> {
+  bf16x8 h, l;
+};
+template <>
+struct AFrag<SMX_S8_FP32> {
+  float v[8];
+};
+template <int MODE>
+struct BFrags;
+template <>
+struct BFrags<SMX_S8_COMP_BF16> {
+  bf16x8 h[kSubN], l[kSubN];
+};
+template <>
+struct BFrags<SMX_S8_FP32> {
+  float v[kSubN][8];
+};
+
+// LDS -> registers, A row block i of one stage.
+//  COMP, plain: BF16 hi/lo planes.
+//  POLY       : A = P1 = a I + (b G)/s^2 + (c G2)/s^4 formed from FP32 G and
+//               G2 tiles (and split in compensated mode).
+//  FP32       : FP32 tile.
+template <int MODE, bool POLY>
+__device__ __forceinline__ void load_a(const char *st, int wm, int i, int64_t k0, const PolyArgs &pa,
+                                       AFrag<MODE> &f) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
-  if constexpr (MODE == SMX_S8_COMP_BF16) {
+  const int r = wm * (32 * kSubM) + i * 32 + lr;
+  if constexpr (MODE == SMX_S8_FP32 || POLY) {
+    float av[8];
+    read8(st, r, lh, av);
+    if constexpr (POLY) {
+      float w[8];
+      read8(st + kF32Tile, r, lh, w);
+      const int64_t grow = pa.row0 + r;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int ch = s * 2 + lh;
-      bf16x8 ah[4], al[4], bh[2], bl[2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int off = comp_off(wm * 128 + i * 32 + lr, ch);
-        ah[i] = *reinterpret_cast<const bf16x8 *>(buf + off);
-        al[i] = *reinterpret_cast<const bf16x8 *>(buf + 16384 + off);
+      for (int e = 0; e < 8; ++e) {
+        const int64_t gk = k0 + 8 * lh + e;
+        const float eye = (grow == gk && grow < pa.r) ? pa.a : 0.f;
+        av[e] = (eye + (pa.b * av[e]) * pa.is2) + (pa.c * w[e]) * pa.is4;
       }
+    }
+    if constexpr (MODE == SMX_S8_COMP_BF16) {
+      split8(av, f.h, f.l);
+    } else {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int off = comp_off(wn * 64 + j * 32 + lr, ch);
-        bh[j] = *reinterpret_cast<const bf16x8 *>(buf + 32768 + off);
-        bl[j] = *reinterpret_cast<const bf16x8 *>(buf + 49152 + off);
-      }
-      // Corrections first, then hi*hi (per K step).
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+      for (int e = 0; e < 8; ++e) f.v[e] = av[e];
     }
   } else {
-#pragma unroll
-    for (int kg = 0; kg < 4; ++kg) {
-      const int ch = kg * 2 + lh;
-      f32x4 av[4], bv[2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        av[i] = *reinterpret_cast<const f32x4 *>(buf + f32_off(wm * 128 + i * 32 + lr, ch));
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bv[j] = *reinterpret_cast<const f32x4 *>(buf + 32768 + f32_off(wn * 64 + j * 32 + lr, ch));
-      // Lane half h supplies k = 8kg + 4h + q to MFMA q: the same K
-      // permutation for both operands, so every k is paired exactly once.
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][q], bv[j][q], acc[i][j], 0, 0, 0);
-    }
+    f.h = read_b16(st, r, lh);
+    f.l = read_b16(st + kB16Tile, r, lh);
   }
 }
 
 template <int MODE, bool POLY>
-__device__ __forceinline__ void gemm_256(const float *__restrict__ A, const float *__restrict__ A2,
-                                         const float *__restrict__ B, int64_t K, int64_t arow0,
-                                         int64_t brow0, const PolyArgs &pa, char *smem,
-                                         f32x16 (&acc)[4][2]) {
+__device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) {
+  const int lane = threadIdx.x & 63;
+  const int lr = lane & 31, lh = lane >> 5;
+  constexpr bool A_F32 = MODE == SMX_S8_FP32 || POLY;
+  const char *bt = st + (POLY ? 2 * kF32Tile : (A_F32 ? kF32Tile : 2 * kB16Tile));
+#pragma unroll
+  for (int j = 0; j < kSubN; ++j) {
+    const int r = wn * (32 * kSubN) + j * 32 + lr;
+    if constexpr (MODE == SMX_S8_COMP_BF16) {
+      f.h[j] = read_b16(bt, r, lh);
+      f.l[j] = read_b16(bt + kB16Tile, r, lh);
+    } else {
+      read8(bt, r, lh, f.v[j]);
+    }
+  }
+}
+
+// MFMAs of row block i: acc[i][j] += A_i B_j^T over the stage's 16 K.
+template <int MODE>
+__device__ __forceinline__ void mma_row(const AFrag<MODE> &a, const BFrags<MODE> &b, f32x16 (&acc)[kSubN]) {
+  if constexpr (MODE == SMX_S8_COMP_BF16) {
+    // Corrections first, then hi*hi.
+#pragma unroll
+    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.l[j], acc[j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.l, b.h[j], acc[j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.h[j], acc[j], 0, 0, 0);
+  } else {
+    // Lane half h supplies k = 8h + q to MFMA q (the same permutation for
+    // both operands, so every k is paired exactly once).
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+#pragma unroll
+      for (int j = 0; j < kSubN; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.v[q], b.v[j][q], acc[j], 0, 0, 0);
+  }
+}
+
+// Issues one stage: A (or G, G2 in POLY) and B into the ring slot.
+template <int MODE, bool POLY>
+__device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &A2, const Opnd &B, int64_t arow0,
+                                            int64_t brow0, int64_t k0, char *st) {
+  if constexpr (MODE == SMX_S8_FP32 || POLY) {
+    dma_f32(static_cast<const float *>(A.p), A.ld, arow0, k0, st);
+    if constexpr (POLY) dma_f32(static_cast<const float *>(A2.p), A2.ld, arow0, k0, st + kF32Tile);
+  } else {
+    const uint16_t *a = static_cast<const uint16_t *>(A.p);
+    dma_b16(a, A.ld, arow0, k0, st);
+    dma_b16(a + A.plane, A.ld, arow0, k0, st + kB16Tile);
+  }
+  char *bt = st + (POLY ? 2 * kF32Tile : (MODE == SMX_S8_FP32 ? kF32Tile : 2 * kB16Tile));
+  if constexpr (MODE == SMX_S8_FP32) {
+    dma_f32(static_cast<const float *>(B.p), B.ld, brow0, k0, bt);
+  } else {
+    const uint16_t *b = static_cast<const uint16_t *>(B.p);
+    dma_b16(b, B.ld, brow0, k0, bt);
+    dma_b16(b + B.plane, B.ld, brow0, k0, bt + kB16Tile);
+  }
+}
+
+// Waits until at most `pending` stages of this wave's loads are in flight
+// (each stage is L loads; loads complete in issue order).
+template <int L>
+__device__ __forceinline__ void wait_stages(int pending) {
+  if (pending >= 3) wait_vm<3 * L>();
+  else if (pending == 2) wait_vm<2 * L>();
+  else if (pending == 1) wait_vm<L>();
+  else wait_vm<0>();
+}
+
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// C[256 x 256] = A[arow0.., :K] * B[brow0.., :K]^T.
+//
+// Two pipelines overlap the MFMAs:
+//  * a ring of S LDS slots filled by direct-to-LDS loads, S stages ahead of
+//    the fragment reads;
+//  * register fragments: while the MFMAs of stage kt run, the fragments of
+//    stage kt+1 are read from LDS (B into the other buffer up front, each A
+//    row block right after its last MFMA of stage kt).
+// Iteration kt: wait for this wave's loads of stage kt+1 and for its own
+// outstanding LDS reads (those of stage kt, so slot kt is free); a block
+// barrier makes every wave's loads of kt+1 visible and every wave's reads
+// of kt finished; refill slot kt with stage kt+S; MFMAs of stage kt
+// interleaved with the reads of stage kt+1.
+template <int MODE, bool POLY, int PAR>
+__device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &A2, const Opnd &B, int64_t arow0,
+                                          int64_t brow0, const PolyArgs &pa, char *smem, int kt, int nk, int wm,
+                                          int wn, AFrag<MODE> (&af)[kSubM], BFrags<MODE> (&bf)[2],
+                                          f32x16 (&acc)[kSubM][kSubN]) {
+  constexpr int S = POLY ? kPolyStages : kStages;
+  constexpr int SB = POLY ? kPolyStageBytes : kStageBytes;
+  constexpr int L = POLY ? 12 : 8;
+  const bool more = kt + 1 < nk;
+  if (more) wait_stages<L>(min(S - 2, nk - 2 - kt));
+  wait_lds();
+  block_barrier();
+  if (kt + S < nk)
+    issue_stage<MODE, POLY>(A, A2, B, arow0, brow0, static_cast<int64_t>(kt + S) * kBK, smem + (kt % S) * SB);
+  const char *nxt = smem + ((kt + 1) % S) * SB;
+  const int64_t k1 = static_cast<int64_t>(kt + 1) * kBK;
+  if (more) load_b<MODE, POLY>(nxt, wn, bf[PAR ^ 1]);
+#pragma unroll
+  for (int i = 0; i < kSubM; ++i) {
+    mma_row<MODE>(af[i], bf[PAR], acc[i]);
+    if (more) load_a<MODE, POLY>(nxt, wm, i, k1, pa, af[i]);
+  }
+}
+
+template <int MODE, bool POLY>
+__device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &A2, const Opnd &B, int64_t K, int64_t arow0,
+                                         int64_t brow0, PolyArgs pa, char *smem, f32x16 (&acc)[kSubM][kSubN]) {
+  constexpr int S = POLY ? kPolyStages : kStages;
+  constexpr int SB = POLY ? kPolyStageBytes : kStageBytes;
+  constexpr int L = POLY ? 12 : 8;
   const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave >> 1, wn = wave & 1;
+  pa.row0 = arow0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kSubM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < kSubN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
   const int nk = static_cast<int>(K / kBK);
-  float4 ra[4], rb[4];
-  load_a_tile<POLY>(A, A2, K, arow0, 0, pa, ra);
-  load_b_tile(B, K, brow0, 0, rb);
-  store_tiles<MODE>(smem, ra, rb);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    if (more) {
-      load_a_tile<POLY>(A, A2, K, arow0, static_cast<int64_t>(kt + 1) * kBK, pa, ra);
-      load_b_tile(B, K, brow0, static_cast<int64_t>(kt + 1) * kBK, rb);
-    }
-    compute_tile<MODE>(smem + (kt & 1) * kLdsBuf, wm, wn, acc);
-    if (more) store_tiles<MODE>(smem + ((kt + 1) & 1) * kLdsBuf, ra, rb);
-    __syncthreads();
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+    if (s < nk) issue_stage<MODE, POLY>(A, A2, B, arow0, brow0, static_cast<int64_t>(s) * kBK, smem + s * SB);
+  wait_stages<L>(min(S - 1, nk - 1));
+  block_barrier();
+  AFrag<MODE> af[kSubM];
+  BFrags<MODE> bf[2];
+  load_b<MODE, POLY>(smem, wn, bf[0]);
+#pragma unroll
+  for (int i = 0; i < kSubM; ++i) load_a<MODE, POLY>(smem, wm, i, 0, pa, af[i]);
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    pipe_iter<MODE, POLY, 0>(A, A2, B, arow0, brow0, pa, smem, kt, nk, wm, wn, af, bf, acc);
+    pipe_iter<MODE, POLY, 1>(A, A2, B, arow0, brow0, pa, smem, kt + 1, nk, wm, wn, af, bf, acc);
   }
+  if (kt < nk) pipe_iter<MODE, POLY, 0>(A, A2, B, arow0, brow0, pa, smem, kt, nk, wm, wn, af, bf, acc);
+  block_barrier();
 }
 
 // ---------------------------------------------------------- scalars ---
@@ -263,10 +397,12 @@ __device__ __forceinline__ int fro_parts_used(const S8Mat &m) {
 
 // ------------------------------------------------------------ kernel ---
 template <int MODE, int PHASE>
-__global__ void __launch_bounds__(kThreads) s8_stage_kernel(StageArgs args) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * kLdsBuf];
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+s8_stage_kernel(StageArgs args) {
+  __shared__ __attribute__((aligned(16))) char smem[kRingBytes];
   __shared__ double dscratch[16];
   __shared__ double bcast;
+  constexpr bool PL = MODE == SMX_S8_COMP_BF16;  // operands stored as BF16 planes
 
   // Segment (class) of this block and its XCD-contiguous tile index.
   const int b = blockIdx.x;
@@ -297,19 +433,24 @@ __global__ void __launch_bounds__(kThreads) s8_stage_kernel(StageArgs args) {
   float *xt_in = odd ? M.xt0() : M.xt1();
   float *x_out = odd ? M.x1() : M.x0();
   float *xt_out = odd ? M.xt1() : M.xt0();
+  const int64_t nx = K.rp * K.cp, ng = K.rp * K.rp;
 
-  f32x16 acc[4][2];
+  f32x16 acc[kSubM][kSubN];
   PolyArgs pa{};
   float scale = 1.f;
+  const Opnd none{nullptr, 0, 0};
   if constexpr (PHASE == kGram) {
     if (stage == 1) {
       const double f = sum_parts(M.fro(), fro_parts_used(M), &bcast);
       scale = f > 0.0 ? static_cast<float>(1.0 / f) : 0.f;
     }
-    gemm_256<MODE, false>(x_in, nullptr, x_in, K.cp, tm * kTile, tn * kTile, pa, smem, acc);
+    const Opnd X{x_in, K.cp, nx};
+    gemm_256<MODE, false>(X, none, X, K.cp, tm * kTile, tn * kTile, pa, smem, acc);
   } else if constexpr (PHASE == kSquare) {
-    gemm_256<MODE, false>(M.g(), nullptr, M.g(), K.rp, tm * kTile, tn * kTile, pa, smem, acc);
+    const Opnd G{PL ? M.gs() : M.g(), K.rp, ng};
+    gemm_256<MODE, false>(G, none, G, K.rp, tm * kTile, tn * kTile, pa, smem, acc);
   } else {
+    const Opnd XT{xt_in, K.rp, nx};
     if (stage == 1) {
       const double f = sum_parts(M.fro(), fro_parts_used(M), &bcast);
       const double sq = sum_parts(M.sch(), static_cast<int>(sym_tiles(K.tiles_m)), &bcast);
@@ -324,26 +465,27 @@ __global__ void __launch_bounds__(kThreads) s8_stage_kernel(StageArgs args) {
       } else {
         pa.is2 = 0.f; pa.is4 = 0.f; scale = 0.f;
       }
-      gemm_256<MODE, true>(M.g(), M.p(), xt_in, K.rp, tm * kTile, tn * kTile, pa, smem, acc);
+      gemm_256<MODE, true>(Opnd{M.g(), K.rp, 0}, Opnd{M.p(), K.rp, 0}, XT, K.rp, tm * kTile, tn * kTile, pa,
+                           smem, acc);
     } else {
-      gemm_256<MODE, false>(M.p(), nullptr, xt_in, K.rp, tm * kTile, tn * kTile, pa, smem, acc);
+      gemm_256<MODE, false>(Opnd{M.p(), K.rp, ng}, none, XT, K.rp, tm * kTile, tn * kTile, pa, smem, acc);
     }
   }
 
   // ------------------------------------------------------- epilogue ---
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
   const int64_t R0 = tm * kTile, C0 = tn * kTile;
   float sq_local = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kSubM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = C0 + wn * 64 + j * 32 + lr;
+    for (int j = 0; j < kSubN; ++j) {
+      const int64_t col = C0 + wn * (32 * kSubN) + j * 32 + lr;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int64_t row = R0 + wm * 128 + i * 32 + 8 * k + 4 * lh;  // rows row..row+3
+        const int64_t row = R0 + wm * (32 * kSubM) + i * 32 + 8 * k + 4 * lh;  // rows row..row+3
         float v[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = acc[i][j][4 * k + q];
@@ -353,10 +495,15 @@ __global__ void __launch_bounds__(kThreads) s8_stage_kernel(StageArgs args) {
           for (int q = 0; q < 4; ++q) {
             v[q] *= scale;
             G[(row + q) * K.rp + col] = v[q];
+            if constexpr (PL) put_operand(M.gs(), ng, (row + q) * K.rp + col, v[q], true);
           }
-          if (tm != tn) *reinterpret_cast<float4 *>(G + col * K.rp + row) = make_float4(v[0], v[1], v[2], v[3]);
+          if (tm != tn) {
+            *reinterpret_cast<float4 *>(G + col * K.rp + row) = make_float4(v[0], v[1], v[2], v[3]);
+            if constexpr (PL) put_operand4(M.gs(), ng, col * K.rp + row, v, true);
+          }
         } else if constexpr (PHASE == kSquare) {
           float *P = M.p();
+          const bool planes = PL && stage != 1;  // stage 1 keeps FP32 G2
           if (stage == 1) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) sq_local = fmaf(v[q], v[q], sq_local);
@@ -370,20 +517,23 @@ __global__ void __launch_bounds__(kThreads) s8_stage_kernel(StageArgs args) {
             }
           }
 #pragma unroll
-          for (int q = 0; q < 4; ++q) P[(row + q) * K.rp + col] = v[q];
-          if (tm != tn) *reinterpret_cast<float4 *>(P + col * K.rp + row) = make_float4(v[0], v[1], v[2], v[3]);
+          for (int q = 0; q < 4; ++q) put_operand(P, ng, (row + q) * K.rp + col, v[q], planes);
+          if (tm != tn) put_operand4(P, ng, col * K.rp + row, v, planes);
         } else {
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] *= scale;
           const bool last = stage == 5;
+          // The stage-5 result is FP32 in parameter layout only.
           if (!last || !M.flip()) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) x_out[(row + q) * K.cp + col] = v[q];
+            for (int q = 0; q < 4; ++q) put_operand(x_out, nx, (row + q) * K.cp + col, v[q], PL && !last);
           }
-          if (!last || M.flip())
-            *reinterpret_cast<float4 *>(xt_out + col * K.rp + row) = make_float4(v[0], v[1], v[2], v[3]);
+          if (!last || M.flip()) put_operand4(xt_out, nx, col * K.rp + row, v, PL && !last);
         }
       }
+      // Keep the scheduler from hoisting every accumulator read to the top
+      // of the epilogue (256 values would not fit in the VGPRs).
+      __builtin_amdgcn_sched_barrier(0);
     }
   if constexpr (PHASE == kSquare) {
     if (stage == 1) {
@@ -494,6 +644,7 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.x1 = reinterpret_cast<float *>(take(xs));
     C.xt1 = reinterpret_cast<float *>(take(xs));
     C.g = reinterpret_cast<float *>(take(gs));
+    C.gs = reinterpret_cast<float *>(take(gs));
     C.p = reinterpret_cast<float *>(take(gs));
     C.u = reinterpret_cast<float *>(take(static_cast<size_t>(C.count) * C.cp * sizeof(float)));
     C.fro = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));

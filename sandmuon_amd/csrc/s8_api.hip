@@ -13,6 +13,7 @@ struct S8IoArgs {
   float *out;
   int64_t rows, cols;          // input (= output) shape per matrix
   int64_t sb, sr, sc;          // element strides: batch, row, col
+  int32_t planes;              // iterate stored as BF16 planes (comp mode)
 };
 
 // Row pass: per kRowsPerPart input rows, the sum of squares -> fro partial.
@@ -59,14 +60,14 @@ __global__ void __launch_bounds__(256) s8_load_tiles_kernel(S8IoArgs a) {
       v[e] = (i < a.rows && j < a.cols) ? x[i * a.sr + j * a.sc] : 0.f;
       tile[lr][lc + e] = v[e];
     }
-    *reinterpret_cast<float4 *>(pl + i * ppad + j0 + lc) = make_float4(v[0], v[1], v[2], v[3]);
+    put_operand4(pl, ppad * rpad, i * ppad + j0 + lc, v, a.planes != 0);
   }
   __syncthreads();
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int lr = (t >> 4) + 16 * q;
-    *reinterpret_cast<float4 *>(tl + (j0 + lr) * rpad + i0 + lc) =
-        make_float4(tile[lc][lr], tile[lc + 1][lr], tile[lc + 2][lr], tile[lc + 3][lr]);
+    const float v[4] = {tile[lc][lr], tile[lc + 1][lr], tile[lc + 2][lr], tile[lc + 3][lr]};
+    put_operand4(tl, ppad * rpad, (j0 + lr) * rpad + i0 + lc, v, a.planes != 0);
   }
 }
 
@@ -125,6 +126,7 @@ extern "C" int smx_s8(const float *x, float *out, int64_t batch, int64_t rows, i
   a.sb = batch_stride;
   a.sr = row_stride;
   a.sc = col_stride;
+  a.planes = mode == SMX_S8_COMP_BF16;
   const S8Mat M0{a.k, 0};
   const unsigned tiles = static_cast<unsigned>((M0.prow_pad() / 64) * (M0.pcol_pad() / 64));
   hipLaunchKernelGGL(s8_load_rows_kernel, dim3(static_cast<unsigned>(ceil_div(rows, kRowsPerPart)), batch),
