@@ -146,7 +146,6 @@ __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
   const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
   const int t = threadIdx.x;
   const int lc = (t & 15) * 4;
-  const int64_t n = J.prow_pad * J.pcol_pad;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int lr = (t >> 4) + 16 * q;
@@ -165,14 +164,14 @@ __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
       v[e] = val;
       tile[lr][lc + e] = val;
     }
-    put_operand4(J.pl, n, i * J.pcol_pad + j0 + lc, v, J.planes != 0);
+    put_operand4(J.pl, i * J.pcol_pad + j0 + lc, v, J.planes != 0);
   }
   __syncthreads();
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int lr = (t >> 4) + 16 * q;  // transposed row = parameter column
     const float v[4] = {tile[lc][lr], tile[lc + 1][lr], tile[lc + 2][lr], tile[lc + 3][lr]};
-    put_operand4(J.tl, n, (j0 + lr) * J.prow_pad + i0 + lc, v, J.planes != 0);
+    put_operand4(J.tl, (j0 + lr) * J.prow_pad + i0 + lc, v, J.planes != 0);
   }
 }
 

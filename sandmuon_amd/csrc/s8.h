@@ -32,12 +32,11 @@ struct S8Class {
   int32_t parts;       // partial slots per matrix: ceil(cp / kRowsPerPart)
   int32_t pad_;
   // Iterate buffers (4 bytes per element).  In SMX_S8_FP32 mode they hold
-  // FP32; in SMX_S8_COMP_BF16 mode two BF16 planes (hi, then lo, each of
-  // rows*cols elements), except the stage-5 result, which is FP32.
+  // FP32; in SMX_S8_COMP_BF16 mode interleaved BF16 hi/lo (put_operand),
+  // except the stage-5 result, which is FP32.
   float *x0, *xt0;     // [count][rp][cp], [count][cp][rp]  (ping)
   float *x1, *xt1;     // pong; after stage 5 the result is in x1/xt1
-  float *g;            // [count][rp][rp] FP32 Gram
-  float *gs;           // [count][rp][rp] Gram as BF16 planes (comp mode)
+  float *g;            // [count][rp][rp] Gram (FP32, or planes in comp mode)
   float *p;            // [count][rp][rp] stage 1: FP32 G2; later: P (planes in comp mode)
   float *u;            // [count][cp] per param-row rank-one coefficient
   double *fro;         // [count][parts] whiten: partial sum of V^2
@@ -64,7 +63,6 @@ struct S8Mat {
   __host__ __device__ float *x1() const { return kp()->x1 + slot * kp()->rp * kp()->cp; }
   __host__ __device__ float *xt1() const { return kp()->xt1 + slot * kp()->rp * kp()->cp; }
   __host__ __device__ float *g() const { return kp()->g + slot * kp()->rp * kp()->rp; }
-  __host__ __device__ float *gs() const { return kp()->gs + slot * kp()->rp * kp()->rp; }
   __host__ __device__ float *p() const { return kp()->p + slot * kp()->rp * kp()->rp; }
   __host__ __device__ float *u() const { return kp()->u + slot * kp()->cp; }
   __host__ __device__ double *fro() const { return kp()->fro + static_cast<int64_t>(slot) * kp()->parts; }
@@ -78,35 +76,59 @@ struct S8Mat {
   __host__ __device__ int64_t pcol_pad() const { return flip() ? kp()->rp : kp()->cp; }
 };
 
-// Store of one element of a GEMM operand buffer of n elements: FP32, or
-// (planes) BF16 hi at [idx] and lo at [idx + n] with hi = bf16(v),
-// lo = bf16(v - hi), both round-to-nearest-even.
-__device__ __forceinline__ void put_operand(float *base, int64_t n, int64_t idx, float v, bool planes) {
+// GEMM operand buffers are row-major with K contiguous and rows padded to
+// multiples of kTile.  In compensated mode an element v is stored as two
+// BF16 values, hi = bf16(v) and lo = bf16(v - hi) (round to nearest even),
+// interleaved per 16-element K group: 16 hi values, then the 16 matching lo
+// values.  The buffer has the byte size of its FP32 form and a 16-deep K
+// slice of a row is one contiguous 64-byte run in both forms.  `idx` is the
+// FP32 element index (row * ld + k).
+__device__ __forceinline__ int64_t plane_hi(int64_t idx) { return 2 * (idx & ~int64_t{15}) + (idx & 15); }
+
+__device__ __forceinline__ uint16_t bf16_bits(float v) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v)); }
+__device__ __forceinline__ uint16_t bf16_lo_bits(float v) {
+  return bf16_bits(v - static_cast<float>(static_cast<__bf16>(v)));
+}
+
+__device__ __forceinline__ void put_operand(float *base, int64_t idx, float v, bool planes) {
   if (planes) {
-    uint16_t *h = reinterpret_cast<uint16_t *>(base);
-    const __bf16 hi = static_cast<__bf16>(v);
-    h[idx] = __builtin_bit_cast(uint16_t, hi);
-    h[idx + n] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v - static_cast<float>(hi)));
+    uint16_t *h = reinterpret_cast<uint16_t *>(base) + plane_hi(idx);
+    h[0] = bf16_bits(v);
+    h[16] = bf16_lo_bits(v);
   } else {
     base[idx] = v;
   }
 }
 
 // Four consecutive elements starting at idx (idx % 4 == 0).
-__device__ __forceinline__ void put_operand4(float *base, int64_t n, int64_t idx, const float (&v)[4], bool planes) {
+__device__ __forceinline__ void put_operand4(float *base, int64_t idx, const float (&v)[4], bool planes) {
   if (planes) {
-    uint16_t hb[4], lb[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const __bf16 hi = static_cast<__bf16>(v[e]);
-      hb[e] = __builtin_bit_cast(uint16_t, hi);
-      lb[e] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v[e] - static_cast<float>(hi)));
-    }
-    uint16_t *h = reinterpret_cast<uint16_t *>(base);
-    *reinterpret_cast<uint2 *>(h + idx) = make_uint2(hb[0] | (uint32_t(hb[1]) << 16), hb[2] | (uint32_t(hb[3]) << 16));
-    *reinterpret_cast<uint2 *>(h + idx + n) = make_uint2(lb[0] | (uint32_t(lb[1]) << 16), lb[2] | (uint32_t(lb[3]) << 16));
+    uint16_t *h = reinterpret_cast<uint16_t *>(base) + plane_hi(idx);
+    *reinterpret_cast<uint2 *>(h) = make_uint2(bf16_bits(v[0]) | (uint32_t(bf16_bits(v[1])) << 16),
+                                               bf16_bits(v[2]) | (uint32_t(bf16_bits(v[3])) << 16));
+    *reinterpret_cast<uint2 *>(h + 16) = make_uint2(bf16_lo_bits(v[0]) | (uint32_t(bf16_lo_bits(v[1])) << 16),
+                                                    bf16_lo_bits(v[2]) | (uint32_t(bf16_lo_bits(v[3])) << 16));
   } else {
     *reinterpret_cast<float4 *>(base + idx) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+// Eight consecutive elements starting at idx (idx % 8 == 0): one 16-byte
+// store per BF16 half, or two for FP32.
+__device__ __forceinline__ void put_operand8(float *base, int64_t idx, const float (&v)[8], bool planes) {
+  if (planes) {
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hw[e] = bf16_bits(v[2 * e]) | (static_cast<uint32_t>(bf16_bits(v[2 * e + 1])) << 16);
+      lw[e] = bf16_lo_bits(v[2 * e]) | (static_cast<uint32_t>(bf16_lo_bits(v[2 * e + 1])) << 16);
+    }
+    uint16_t *h = reinterpret_cast<uint16_t *>(base) + plane_hi(idx);
+    *reinterpret_cast<uint4 *>(h) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *reinterpret_cast<uint4 *>(h + 16) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  } else {
+    *reinterpret_cast<float4 *>(base + idx) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4 *>(base + idx + 4) = make_float4(v[4], v[5], v[6], v[7]);
   }
 }
 

@@ -5,31 +5,33 @@
 // its squared Frobenius norm as partials in `fro`) and stage k = 1..5:
 //   GRAM    G  = X X^T                 (stage 1: times 1/||V||^2)
 //   SQUARE  stage 1: G2 = G G  -> p buffer, plus Schatten-8 partials
-//           stage k: P  = a I + b G + c (G G)            -> p buffer
-//   APPLY   stage 1: X' = P1 V / (||V|| s),  P1 = a I + b G/s^2 + c G2/s^4
-//                    formed in the A-operand loader; s = 1.35 ||G2||_F^(1/4)
-//           stage k: X' = P X
+//           stage k: P  = c (G G + (b/c) G) + a I             -> p buffer
+//   POLY1   stage 1 only: P1 = a I + b G/s^2 + c G2/s^4 -> p buffer,
+//           s = max(1.35 ||G2||_F^(1/4), 1e-30) (elementwise kernel)
+//   APPLY   stage 1: X' = P1 V / (||V|| s);  stage k: X' = P X
 // Every product is C = A B^T with A, B row-major and K contiguous: the
 // Gram uses X twice, the square uses the symmetric G twice, the apply uses
 // P and X^T.  The apply epilogue therefore writes the new iterate in both
 // layouts (X and X^T).  Gram and square only compute upper-triangle tiles
-// and store each off-diagonal tile twice (tile and mirror).
+// and store each off-diagonal tile twice (tile and mirror).  The (b/c) G
+// term of the square is accumulated by extra MFMAs from the B fragments
+// (one_hot), so no epilogue reads G.
 //
 // Arithmetic modes:
-//   SMX_S8_FP32       v_mfma_f32_32x32x2_f32, FP32 operands in LDS.
-//   SMX_S8_COMP_BF16  each FP32 operand is split into BF16 hi + lo when it
-//                     is staged to LDS; acc += hi*lo + lo*hi + hi*hi with
+//   SMX_S8_FP32       v_mfma_f32_32x32x2_f32 on FP32 operands.
+//   SMX_S8_COMP_BF16  every operand is stored by its producer as BF16 hi +
+//                     lo (put_operand); acc += hi*lo + lo*hi + hi*hi with
 //                     v_mfma_f32_32x32x16_bf16 (the compensated product of
 //                     reproduction/odl/ops/bf16_compensated_mm_fast.py:
-//                     60-66, applied in all five stages with FP32 storage
-//                     of every intermediate).
+//                     60-66, applied in all five stages with FP32
+//                     accumulation of every intermediate).
 //
 // Block: 256x256 output tile, 4 waves (2 x 2, one per SIMD), each wave
-// 128x128 (4 x 4 MFMA 32x32 tiles, 256 accumulators).  Operands stream into a 4-stage LDS ring (K = 16 per
-// stage, 32 KB) with direct-to-LDS 16-byte loads issued three stages ahead.
-// In compensated mode every operand is stored by its producer as BF16
-// hi/lo planes (put_operand), so the inner loop is LDS reads + MFMAs; only
-// the stage-1 polynomial operand is formed and split in registers.
+// 128x128 (4 x 4 MFMA 32x32 tiles, 256 AGPR accumulators).  Operands stream
+// into a 4-stage LDS ring (K = 16 per stage, 32 KB; 64 contiguous bytes
+// per row and operand in both modes) with direct-to-LDS 16-byte loads
+// issued three stages ahead.  The epilogue stages each 32x32 accumulator
+// block through LDS in both orientations and writes row vectors.
 #include "s8.h"
 
 #include <algorithm>
@@ -46,16 +48,13 @@ constexpr int kThreads = 256;     // 4 waves, one per SIMD
 constexpr int kWaves = kThreads / 64;
 constexpr int kSubM = 4, kSubN = 4; // 32x32 MFMA tiles per wave (128 x 128)
 constexpr int kBK = 16;            // K per pipeline stage
-constexpr int kF32Tile = 16384;    // 256 x 16 FP32 operand tile
-constexpr int kB16Tile = 8192;     // 256 x 16 BF16 plane tile
+constexpr int kOpTile = 16384;     // 256 x 16 operand tile (4 bytes per element)
 constexpr int kStages = 4;         // LDS ring depth (3 stages in flight)
-constexpr int kPolyStages = 3;     // ring depth when A is formed from (G, G2)
-constexpr int kStageBytes = 2 * kF32Tile;          // A + B (FP32, or 4 BF16 planes)
-constexpr int kPolyStageBytes = 3 * kF32Tile;      // G + G2 + B
-constexpr int kRingBytes = kStages * kStageBytes > kPolyStages * kPolyStageBytes ? kStages * kStageBytes
-                                                                                 : kPolyStages * kPolyStageBytes;
+constexpr int kStageBytes = 2 * kOpTile;           // A + B
+constexpr int kRingBytes = kStages * kStageBytes;
+constexpr int kLoadsPerStage = 2 * (kOpTile / 1024) / kWaves;  // 1 KB loads per wave and stage
 
-enum Phase { kGram = 0, kSquare = 1, kApply = 2 };
+enum Phase { kGram = 0, kSquare = 1, kApply = 2, kPoly1 = 3 };
 
 struct StageArgs {
   S8Layout L;
@@ -64,32 +63,24 @@ struct StageArgs {
   int32_t n_seg;
   int32_t stage;  // 1..5
   float a, b, c;
+  float b_over_c;
 };
 
-struct PolyArgs {
-  float a, b, c;     // stage-1 coefficients
-  float is2, is4;    // 1/s^2, 1/s^4
-  int64_t r;         // logical rows (identity only on real rows)
-  int64_t row0;      // first global row of the A tile
-};
-
-// A K-contiguous GEMM operand: FP32 rows of `ld` elements, or BF16 hi/lo
-// planes (lo at hi + plane elements).
+// A K-contiguous GEMM operand with rows of `ld` elements: FP32, or BF16
+// hi/lo interleaved per 16-element K group (put_operand).
 struct Opnd {
   const void *p;
   int64_t ld;
-  int64_t plane;
 };
 
 // ------------------------------------------------------- LDS layouts ---
-// FP32 tile [256][16]: four 16-byte chunks per row, logical chunk kc at
-// slot kc ^ swz4(r).  BF16 plane tile [256][16]: two chunks per row, slot
-// c ^ swz2(r).  Both make the fragment reads (8 or 16 consecutive rows, one
-// chunk) conflict-free for 32- and 64-bank LDS.
+// Operand tile [256 rows][16 K]: four 16-byte chunks per row (FP32: k 0-3,
+// 4-7, 8-11, 12-15; interleaved BF16: hi k 0-7, hi k 8-15, lo k 0-7, lo k
+// 8-15), logical chunk kc at slot kc ^ swz4(r).  Fragment reads (one chunk
+// of 32 consecutive rows per lane half) are conflict-free for 32- and
+// 64-bank LDS.
 __device__ __forceinline__ int swz4(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
-__device__ __forceinline__ int swz2(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
 __device__ __forceinline__ int f32_off(int r, int kc) { return (r * 4 + (kc ^ swz4(r))) << 4; }
-__device__ __forceinline__ int b16_off(int r, int c) { return (r * 2 + (c ^ swz2(r))) << 4; }
 
 // One 16-byte direct-to-LDS load per lane: lane l writes LDS[m0 + 16 l].
 // Issued from asm so the compiler does not treat later LDS reads as
@@ -100,12 +91,14 @@ __device__ __forceinline__ void dma16(const void *src, char *lds_wave_base) {
   asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 
-// This wave's share of an FP32 tile (rows row0.., K k0..k0+15): LDS chunk
-// p = (wave*N+i)*64 + lane is stored slot p&3 of row p>>2.
-__device__ __forceinline__ void dma_f32(const float *__restrict__ M, int64_t ld, int64_t row0, int64_t k0,
-                                        char *tile) {
+// This wave's share of an operand tile (rows row0.., K k0..k0+15; `ld` and
+// k0 in 4-byte elements): LDS chunk p = (wave*N+i)*64 + lane is stored slot
+// p&3 of row p>>2.
+__device__ __forceinline__ void dma_tile(const void *__restrict__ src, int64_t ld, int64_t row0, int64_t k0,
+                                         char *tile) {
+  const float *M = static_cast<const float *>(src);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  constexpr int N = 16 / kWaves;  // 1 KB loads per wave
+  constexpr int N = (kOpTile / 1024) / kWaves;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const int p = (wave * N + i) * 64 + lane;
@@ -115,37 +108,18 @@ __device__ __forceinline__ void dma_f32(const float *__restrict__ M, int64_t ld,
   }
 }
 
-// This wave's share of a BF16 plane tile: LDS chunk p = (wave*N+i)*64 +
-// lane is stored slot p&1 of row p>>1.
-__device__ __forceinline__ void dma_b16(const uint16_t *__restrict__ M, int64_t ld, int64_t row0, int64_t k0,
-                                        char *tile) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  constexpr int N = 8 / kWaves;  // 1 KB loads per wave
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const int p = (wave * N + i) * 64 + lane;
-    const int row = p >> 1;
-    const int c = (p & 1) ^ swz2(row);
-    dma16(M + (row0 + row) * ld + k0 + c * 8, tile + (wave * N + i) * 1024);
-  }
-}
-
 template <int N>
 __device__ __forceinline__ void wait_vm() {
   if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
   else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
   else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
   else if constexpr (N == 24) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
-  else if constexpr (N == 36) asm volatile("s_waitcnt vmcnt(36)" ::: "memory");
   else static_assert(N == 0, "unsupported vmcnt");
 }
 
 __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// The 8 consecutive K values (k = 8h .. 8h+7 of the stage) of row r.
+// The 8 consecutive K values (k = 8h .. 8h+7 of the stage) of row r (FP32).
 __device__ __forceinline__ void read8(const char *tile, int r, int h, float (&v)[8]) {
   const f32x4 a = *reinterpret_cast<const f32x4 *>(tile + f32_off(r, 2 * h));
   const f32x4 b = *reinterpret_cast<const f32x4 *>(tile + f32_off(r, 2 * h + 1));
@@ -153,17 +127,9 @@ __device__ __forceinline__ void read8(const char *tile, int r, int h, float (&v)
   v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-__device__ __forceinline__ bf16x8 read_b16(const char *tile, int r, int h) {
-  return *reinterpret_cast<const bf16x8 *>(tile + b16_off(r, h));
-}
-
-__device__ __forceinline__ void split8(const float (&v)[8], bf16x8 &hi, bf16x8 &lo) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const __bf16 h = static_cast<__bf16>(v[e]);
-    hi[e] = h;
-    lo[e] = static_cast<__bf16>(v[e] - static_cast<float>(h));
-  }
+// Chunk kc of row r as 8 BF16 values.
+__device__ __forceinline__ bf16x8 read_b16(const char *tile, int r, int kc) {
+  return *reinterpret_cast<const bf16x8 *>(tile + f32_off(r, kc));
 }
 
 // ----------------------------------------------------------- compute ---
@@ -193,55 +159,33 @@ struct BFrags<SMX_S8_FP32> {
   float v[kSubN][8];
 };
 
-// LDS -> registers, A row block i of one stage.
-//  COMP, plain: BF16 hi/lo planes.
-//  POLY       : A = P1 = a I + (b G)/s^2 + (c G2)/s^4 formed from FP32 G and
-//               G2 tiles (and split in compensated mode).
-//  FP32       : FP32 tile.
-template <int MODE, bool POLY>
-__device__ __forceinline__ void load_a(const char *st, int wm, int i, int64_t k0, const PolyArgs &pa,
-                                       AFrag<MODE> &f) {
+// LDS -> registers: A row block i, and the four B column blocks, of one
+// stage.  Lane (r, h) takes K = 8h .. 8h+7 of its row: chunks h (hi) and
+// 2 + h (lo) of the interleaved form, chunks 2h and 2h + 1 of FP32.
+template <int MODE>
+__device__ __forceinline__ void load_a(const char *st, int wm, int i, AFrag<MODE> &f) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
   const int r = wm * (32 * kSubM) + i * 32 + lr;
-  if constexpr (MODE == SMX_S8_FP32 || POLY) {
-    float av[8];
-    read8(st, r, lh, av);
-    if constexpr (POLY) {
-      float w[8];
-      read8(st + kF32Tile, r, lh, w);
-      const int64_t grow = pa.row0 + r;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int64_t gk = k0 + 8 * lh + e;
-        const float eye = (grow == gk && grow < pa.r) ? pa.a : 0.f;
-        av[e] = (eye + (pa.b * av[e]) * pa.is2) + (pa.c * w[e]) * pa.is4;
-      }
-    }
-    if constexpr (MODE == SMX_S8_COMP_BF16) {
-      split8(av, f.h, f.l);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) f.v[e] = av[e];
-    }
-  } else {
+  if constexpr (MODE == SMX_S8_COMP_BF16) {
     f.h = read_b16(st, r, lh);
-    f.l = read_b16(st + kB16Tile, r, lh);
+    f.l = read_b16(st, r, 2 + lh);
+  } else {
+    read8(st, r, lh, f.v);
   }
 }
 
-template <int MODE, bool POLY>
+template <int MODE>
 __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
-  constexpr bool A_F32 = MODE == SMX_S8_FP32 || POLY;
-  const char *bt = st + (POLY ? 2 * kF32Tile : (A_F32 ? kF32Tile : 2 * kB16Tile));
+  const char *bt = st + kOpTile;
 #pragma unroll
   for (int j = 0; j < kSubN; ++j) {
     const int r = wn * (32 * kSubN) + j * 32 + lr;
     if constexpr (MODE == SMX_S8_COMP_BF16) {
       f.h[j] = read_b16(bt, r, lh);
-      f.l[j] = read_b16(bt + kB16Tile, r, lh);
+      f.l[j] = read_b16(bt, r, 2 + lh);
     } else {
       read8(bt, r, lh, f.v[j]);
     }
@@ -270,32 +214,44 @@ __device__ __forceinline__ void mma_row(const AFrag<MODE> &a, const BFrags<MODE>
   }
 }
 
-// Issues one stage: A (or G, G2 in POLY) and B into the ring slot.
-template <int MODE, bool POLY>
-__device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &A2, const Opnd &B, int64_t arow0,
-                                            int64_t brow0, int64_t k0, char *st) {
-  if constexpr (MODE == SMX_S8_FP32 || POLY) {
-    dma_f32(static_cast<const float *>(A.p), A.ld, arow0, k0, st);
-    if constexpr (POLY) dma_f32(static_cast<const float *>(A2.p), A2.ld, arow0, k0, st + kF32Tile);
+// acc += s G over this wave's own output rows (square phase of stages 2-5,
+// whose product is P = a I + b G + c G G = c (G G + (b/c) G) + a I).  The
+// Gram is symmetric, so the B fragments of the stage whose K range covers
+// rows R..R+15 of the wave hold G[R + k][col] in accumulator layout; an A
+// fragment that is s on the diagonal k = row - R (a scaled one-hot row)
+// adds s G to those accumulator rows with the ordinary (compensated) MFMAs.
+template <int MODE>
+__device__ __forceinline__ AFrag<MODE> one_hot(float s, int r0) {
+  const int lane = threadIdx.x & 63;
+  const int e = (lane & 31) - r0 - 8 * (lane >> 5);  // position of k = row - R in this lane's 8
+  AFrag<MODE> f;
+  if constexpr (MODE == SMX_S8_COMP_BF16) {
+    const __bf16 sh = static_cast<__bf16>(s);
+    const __bf16 sl = static_cast<__bf16>(s - static_cast<float>(sh));
+    const __bf16 z = static_cast<__bf16>(0.f);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      f.h[q] = q == e ? sh : z;
+      f.l[q] = q == e ? sl : z;
+    }
   } else {
-    const uint16_t *a = static_cast<const uint16_t *>(A.p);
-    dma_b16(a, A.ld, arow0, k0, st);
-    dma_b16(a + A.plane, A.ld, arow0, k0, st + kB16Tile);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) f.v[q] = q == e ? s : 0.f;
   }
-  char *bt = st + (POLY ? 2 * kF32Tile : (MODE == SMX_S8_FP32 ? kF32Tile : 2 * kB16Tile));
-  if constexpr (MODE == SMX_S8_FP32) {
-    dma_f32(static_cast<const float *>(B.p), B.ld, brow0, k0, bt);
-  } else {
-    const uint16_t *b = static_cast<const uint16_t *>(B.p);
-    dma_b16(b, B.ld, brow0, k0, bt);
-    dma_b16(b + B.plane, B.ld, brow0, k0, bt + kB16Tile);
-  }
+  return f;
+}
+
+// Issues one stage (A and B tiles) into a ring slot.
+__device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, int64_t arow0, int64_t brow0,
+                                            int64_t k0, char *st) {
+  dma_tile(A.p, A.ld, arow0, k0, st);
+  dma_tile(B.p, B.ld, brow0, k0, st + kOpTile);
 }
 
 // Waits until at most `pending` stages of this wave's loads are in flight
-// (each stage is L loads; loads complete in issue order).
-template <int L>
+// (loads complete in issue order).
 __device__ __forceinline__ void wait_stages(int pending) {
+  constexpr int L = kLoadsPerStage;
   if (pending >= 3) wait_vm<3 * L>();
   else if (pending == 2) wait_vm<2 * L>();
   else if (pending == 1) wait_vm<L>();
@@ -307,49 +263,46 @@ __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)"
 // C[256 x 256] = A[arow0.., :K] * B[brow0.., :K]^T.
 //
 // Two pipelines overlap the MFMAs:
-//  * a ring of S LDS slots filled by direct-to-LDS loads, S stages ahead of
-//    the fragment reads;
+//  * a ring of kStages LDS slots filled by direct-to-LDS loads, kStages
+//    stages ahead of the fragment reads;
 //  * register fragments: while the MFMAs of stage kt run, the fragments of
 //    stage kt+1 are read from LDS (B into the other buffer up front, each A
 //    row block right after its last MFMA of stage kt).
 // Iteration kt: wait for this wave's loads of stage kt+1 and for its own
 // outstanding LDS reads (those of stage kt, so slot kt is free); a block
 // barrier makes every wave's loads of kt+1 visible and every wave's reads
-// of kt finished; refill slot kt with stage kt+S; MFMAs of stage kt
+// of kt finished; refill slot kt with stage kt+kStages; MFMAs of stage kt
 // interleaved with the reads of stage kt+1.
-template <int MODE, bool POLY, int PAR>
-__device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &A2, const Opnd &B, int64_t arow0,
-                                          int64_t brow0, const PolyArgs &pa, char *smem, int kt, int nk, int wm,
-                                          int wn, AFrag<MODE> (&af)[kSubM], BFrags<MODE> (&bf)[2],
-                                          f32x16 (&acc)[kSubM][kSubN]) {
-  constexpr int S = POLY ? kPolyStages : kStages;
-  constexpr int SB = POLY ? kPolyStageBytes : kStageBytes;
-  constexpr int L = POLY ? 12 : 8;
+// SEL >= 0: this stage is stage SEL of the wave's 8-stage one_hot window
+// (rows 16 SEL .. 16 SEL + 15 of the wave, accumulator block SEL / 2).
+template <int MODE, int SEL, int PAR>
+__device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, int64_t arow0, int64_t brow0, float sel_s,
+                                          char *smem, int kt, int nk, int wm, int wn, AFrag<MODE> (&af)[kSubM],
+                                          BFrags<MODE> (&bf)[2], f32x16 (&acc)[kSubM][kSubN]) {
+  constexpr int S = kStages;
   const bool more = kt + 1 < nk;
-  if (more) wait_stages<L>(min(S - 2, nk - 2 - kt));
+  if (more) wait_stages(min(S - 2, nk - 2 - kt));
   wait_lds();
   block_barrier();
-  if (kt + S < nk)
-    issue_stage<MODE, POLY>(A, A2, B, arow0, brow0, static_cast<int64_t>(kt + S) * kBK, smem + (kt % S) * SB);
-  const char *nxt = smem + ((kt + 1) % S) * SB;
-  const int64_t k1 = static_cast<int64_t>(kt + 1) * kBK;
-  if (more) load_b<MODE, POLY>(nxt, wn, bf[PAR ^ 1]);
+  if (kt + S < nk) issue_stage(A, B, arow0, brow0, static_cast<int64_t>(kt + S) * kBK, smem + (kt % S) * kStageBytes);
+  const char *nxt = smem + ((kt + 1) % S) * kStageBytes;
+  if (more) load_b<MODE>(nxt, wn, bf[PAR ^ 1]);
 #pragma unroll
   for (int i = 0; i < kSubM; ++i) {
     mma_row<MODE>(af[i], bf[PAR], acc[i]);
-    if (more) load_a<MODE, POLY>(nxt, wm, i, k1, pa, af[i]);
+    if (more) load_a<MODE>(nxt, wm, i, af[i]);
   }
+  if constexpr (SEL >= 0) mma_row<MODE>(one_hot<MODE>(sel_s, (SEL & 1) * 16), bf[PAR], acc[SEL >> 1]);
 }
 
-template <int MODE, bool POLY>
-__device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &A2, const Opnd &B, int64_t K, int64_t arow0,
-                                         int64_t brow0, PolyArgs pa, char *smem, f32x16 (&acc)[kSubM][kSubN]) {
-  constexpr int S = POLY ? kPolyStages : kStages;
-  constexpr int SB = POLY ? kPolyStageBytes : kStageBytes;
-  constexpr int L = POLY ? 12 : 8;
-  const int wave = threadIdx.x >> 6;
+// ACCG: also accumulate sel_s * G over the wave's rows (square phase; A and
+// B are the same symmetric G, K = rows of G).
+template <int MODE, bool ACCG>
+__device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &B, int64_t K, int64_t arow0, int64_t brow0,
+                                         float sel_s, char *smem, f32x16 (&acc)[kSubM][kSubN]) {
+  static_assert(kSubM == 4 && kBK == 16, "the one_hot window is 8 stages of 16 rows");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int wm = wave >> 1, wn = wave & 1;
-  pa.row0 = arow0;
 #pragma unroll
   for (int i = 0; i < kSubM; ++i)
 #pragma unroll
@@ -358,21 +311,42 @@ __device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &A2, const Op
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
   const int nk = static_cast<int>(K / kBK);
 #pragma unroll
-  for (int s = 0; s < S; ++s)
-    if (s < nk) issue_stage<MODE, POLY>(A, A2, B, arow0, brow0, static_cast<int64_t>(s) * kBK, smem + s * SB);
-  wait_stages<L>(min(S - 1, nk - 1));
+  for (int s = 0; s < kStages; ++s)
+    if (s < nk) issue_stage(A, B, arow0, brow0, static_cast<int64_t>(s) * kBK, smem + s * kStageBytes);
+  wait_stages(min(kStages - 1, nk - 1));
   block_barrier();
   AFrag<MODE> af[kSubM];
   BFrags<MODE> bf[2];
-  load_b<MODE, POLY>(smem, wn, bf[0]);
+  load_b<MODE>(smem, wn, bf[0]);
 #pragma unroll
-  for (int i = 0; i < kSubM; ++i) load_a<MODE, POLY>(smem, wm, i, 0, pa, af[i]);
+  for (int i = 0; i < kSubM; ++i) load_a<MODE>(smem, wm, i, af[i]);
+#define SMX_PIPE(SEL, PAR, KT) \
+  pipe_iter<MODE, SEL, PAR>(A, B, arow0, brow0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
   int kt = 0;
-  for (; kt + 1 < nk; kt += 2) {
-    pipe_iter<MODE, POLY, 0>(A, A2, B, arow0, brow0, pa, smem, kt, nk, wm, wn, af, bf, acc);
-    pipe_iter<MODE, POLY, 1>(A, A2, B, arow0, brow0, pa, smem, kt + 1, nk, wm, wn, af, bf, acc);
+  if constexpr (ACCG) {
+    // The wave's rows are K stages kt0 .. kt0 + 7 (kt0 = first row / 16, a
+    // multiple of 8, so the stage parity matches the unrolled pairs).
+    const int kt0 = static_cast<int>((arow0 + wm * (32 * kSubM)) / kBK);
+    for (; kt < kt0; kt += 2) {
+      SMX_PIPE(-1, 0, kt);
+      SMX_PIPE(-1, 1, kt + 1);
+    }
+    SMX_PIPE(0, 0, kt0);
+    SMX_PIPE(1, 1, kt0 + 1);
+    SMX_PIPE(2, 0, kt0 + 2);
+    SMX_PIPE(3, 1, kt0 + 3);
+    SMX_PIPE(4, 0, kt0 + 4);
+    SMX_PIPE(5, 1, kt0 + 5);
+    SMX_PIPE(6, 0, kt0 + 6);
+    SMX_PIPE(7, 1, kt0 + 7);
+    kt = kt0 + 8;
   }
-  if (kt < nk) pipe_iter<MODE, POLY, 0>(A, A2, B, arow0, brow0, pa, smem, kt, nk, wm, wn, af, bf, acc);
+  for (; kt + 1 < nk; kt += 2) {
+    SMX_PIPE(-1, 0, kt);
+    SMX_PIPE(-1, 1, kt + 1);
+  }
+  if (kt < nk) SMX_PIPE(-1, 0, kt);
+#undef SMX_PIPE
   block_barrier();
 }
 
@@ -395,6 +369,52 @@ __device__ __forceinline__ int fro_parts_used(const S8Mat &m) {
   return static_cast<int>(ceil_div(m.prow(), kRowsPerPart));
 }
 
+// Stage-1 scalars of a matrix: ||V||^2 (sum of the whiten partials) and the
+// Schatten scale s = max(1.35 ||G2||_F^(1/4), 1e-30) of the normalised G2
+// (sandmuon/optimizer.py:80-84).  ok = false for a zero matrix.
+struct Stage1Scalars {
+  double fro2;
+  float s;
+  bool ok;
+};
+__device__ Stage1Scalars stage1_scalars(const S8Mat &M, double *bcast) {
+  Stage1Scalars r;
+  r.fro2 = sum_parts(M.fro(), fro_parts_used(M), bcast);
+  const double sq = sum_parts(M.sch(), static_cast<int>(sym_tiles(M.kp()->tiles_m)), bcast);
+  r.ok = r.fro2 > 0.0 && sq > 0.0;
+  r.s = r.ok ? fmaxf(static_cast<float>(kS8Margin * pow(sq, 0.125)), 1e-30f) : 1.f;
+  return r;
+}
+
+// Block -> (class, XCD-contiguous tile index).  Blocks are dealt to the
+// XCDs round robin, so consecutive logical tiles (the tiles of one matrix)
+// share an L2 when L = (jb % 8) * per + jb / 8.
+struct TileRef {
+  const S8Class *k;
+  int64_t L;
+};
+__device__ __forceinline__ TileRef tile_of(const StageArgs &args) {
+  const int b = blockIdx.x;
+  int seg = 0;
+  while (seg + 1 < args.n_seg && b >= args.seg_off[seg + 1]) ++seg;
+  const int jb = b - args.seg_off[seg];
+  const int per = (args.seg_off[seg + 1] - args.seg_off[seg]) / 8;
+  return TileRef{&args.L.cls[args.seg_cls[seg]], static_cast<int64_t>(jb % 8) * per + jb / 8};
+}
+
+// Epilogue staging: a 32 x 32 FP32 block per orientation per wave, rows
+// padded to 36 floats (16-byte aligned row vectors).
+constexpr int kEpStride = 36;
+constexpr int kEpBlock = 32 * kEpStride;
+static_assert(kWaves * 2 * kEpBlock * 4 <= kRingBytes, "epilogue staging must fit in the operand ring");
+
+__device__ __forceinline__ void ep_read8(const float *s, int row, int col, float (&w)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4 *>(s + row * kEpStride + col);
+  const f32x4 b = *reinterpret_cast<const f32x4 *>(s + row * kEpStride + col + 4);
+  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+
 // ------------------------------------------------------------ kernel ---
 template <int MODE, int PHASE>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -402,20 +422,14 @@ s8_stage_kernel(StageArgs args) {
   __shared__ __attribute__((aligned(16))) char smem[kRingBytes];
   __shared__ double dscratch[16];
   __shared__ double bcast;
-  constexpr bool PL = MODE == SMX_S8_COMP_BF16;  // operands stored as BF16 planes
+  constexpr bool PL = MODE == SMX_S8_COMP_BF16;  // operands stored as interleaved BF16
 
-  // Segment (class) of this block and its XCD-contiguous tile index.
-  const int b = blockIdx.x;
-  int seg = 0;
-  while (seg + 1 < args.n_seg && b >= args.seg_off[seg + 1]) ++seg;
-  const S8Class K = args.L.cls[args.seg_cls[seg]];
-  const int jb = b - args.seg_off[seg];
-  const int per = (args.seg_off[seg + 1] - args.seg_off[seg]) / 8;
-  const int64_t L = static_cast<int64_t>(jb % 8) * per + jb / 8;
+  const TileRef ref = tile_of(args);
+  const S8Class &K = *ref.k;
   const int64_t tpm = PHASE == kApply ? static_cast<int64_t>(K.tiles_m) * K.tiles_n : sym_tiles(K.tiles_m);
-  if (L >= tpm * K.count) return;
-  const int slot = static_cast<int>(L / tpm);
-  const int64_t tix = L % tpm;
+  if (ref.L >= tpm * K.count) return;
+  const int slot = static_cast<int>(ref.L / tpm);
+  const int64_t tix = ref.L % tpm;
   int64_t tm, tn;
   if constexpr (PHASE == kApply) {
     tm = tix / K.tiles_n;
@@ -433,113 +447,177 @@ s8_stage_kernel(StageArgs args) {
   float *xt_in = odd ? M.xt0() : M.xt1();
   float *x_out = odd ? M.x1() : M.x0();
   float *xt_out = odd ? M.xt1() : M.xt0();
-  const int64_t nx = K.rp * K.cp, ng = K.rp * K.rp;
 
   f32x16 acc[kSubM][kSubN];
-  PolyArgs pa{};
   float scale = 1.f;
-  const Opnd none{nullptr, 0, 0};
   if constexpr (PHASE == kGram) {
     if (stage == 1) {
       const double f = sum_parts(M.fro(), fro_parts_used(M), &bcast);
       scale = f > 0.0 ? static_cast<float>(1.0 / f) : 0.f;
     }
-    const Opnd X{x_in, K.cp, nx};
-    gemm_256<MODE, false>(X, none, X, K.cp, tm * kTile, tn * kTile, pa, smem, acc);
+    const Opnd X{x_in, K.cp};
+    gemm_256<MODE, false>(X, X, K.cp, tm * kTile, tn * kTile, 0.f, smem, acc);
   } else if constexpr (PHASE == kSquare) {
-    const Opnd G{PL ? M.gs() : M.g(), K.rp, ng};
-    gemm_256<MODE, false>(G, none, G, K.rp, tm * kTile, tn * kTile, pa, smem, acc);
-  } else {
-    const Opnd XT{xt_in, K.rp, nx};
+    const Opnd G{M.g(), K.rp};
     if (stage == 1) {
-      const double f = sum_parts(M.fro(), fro_parts_used(M), &bcast);
-      const double sq = sum_parts(M.sch(), static_cast<int>(sym_tiles(K.tiles_m)), &bcast);
-      pa.a = args.a; pa.b = args.b; pa.c = args.c; pa.r = K.r;
-      if (f > 0.0 && sq > 0.0) {
-        // s = max(1.35 * ||G2||_F^(1/4), 1e-30) on the normalised G2.
-        const float s = fmaxf(static_cast<float>(kS8Margin * pow(sq, 0.125)), 1e-30f);
-        const float s2 = s * s;
-        pa.is2 = 1.0f / s2;
-        pa.is4 = 1.0f / (s2 * s2);
-        scale = static_cast<float>(1.0 / (sqrt(f) * static_cast<double>(s)));
-      } else {
-        pa.is2 = 0.f; pa.is4 = 0.f; scale = 0.f;
-      }
-      gemm_256<MODE, true>(Opnd{M.g(), K.rp, 0}, Opnd{M.p(), K.rp, 0}, XT, K.rp, tm * kTile, tn * kTile, pa,
-                           smem, acc);
+      gemm_256<MODE, false>(G, G, K.rp, tm * kTile, tn * kTile, 0.f, smem, acc);
     } else {
-      gemm_256<MODE, false>(Opnd{M.p(), K.rp, ng}, none, XT, K.rp, tm * kTile, tn * kTile, pa, smem, acc);
+      // acc = G G + (b/c) G; the epilogue forms P = c acc + a I.
+      scale = args.c;
+      gemm_256<MODE, true>(G, G, K.rp, tm * kTile, tn * kTile, args.b_over_c, smem, acc);
     }
+  } else {
+    if (stage == 1) {
+      // X' = P1 V / (||V|| s)
+      const Stage1Scalars sc = stage1_scalars(M, &bcast);
+      scale = sc.ok ? static_cast<float>(1.0 / (sqrt(sc.fro2) * static_cast<double>(sc.s))) : 0.f;
+    }
+    gemm_256<MODE, false>(Opnd{M.p(), K.rp}, Opnd{xt_in, K.rp}, K.rp, tm * kTile, tn * kTile, 0.f, smem, acc);
   }
 
   // ------------------------------------------------------- epilogue ---
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // Each 32x32 accumulator block goes through wave-private LDS in both
+  // orientations (T row-major, U column-major), so that the tile and its
+  // transpose are written as row vectors of 8 elements per lane.
+  //   GRAM    tile -> G, transpose -> G (off-diagonal tiles)
+  //   SQUARE  stage 1: G2 (FP32) -> p; stage k: P = c acc + a I -> p
+  //   APPLY   tile -> X', transpose -> X'^T (stage 5: parameter layout only)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
-  const int64_t R0 = tm * kTile, C0 = tn * kTile;
+  const int rr = lane >> 2, cc = (lane & 3) * 8;  // read-back: rows rr, rr + 16; cols cc..cc+7
+  const int64_t R0 = tm * kTile + wm * (32 * kSubM), C0 = tn * kTile + wn * (32 * kSubN);
+  const bool last = stage == 5;
+  float *dst_t, *dst_m;
+  int64_t ld_t, ld_m;
+  bool pl_t, pl_m, do_t, do_m;
+  if constexpr (PHASE == kApply) {
+    dst_t = x_out; ld_t = K.cp;
+    dst_m = xt_out; ld_m = K.rp;
+    pl_t = pl_m = PL && !last;
+    do_t = !last || !M.flip();
+    do_m = !last || M.flip();
+  } else {
+    dst_t = dst_m = PHASE == kGram ? M.g() : M.p();
+    ld_t = ld_m = K.rp;
+    pl_t = pl_m = PL && (PHASE == kGram || stage != 1);
+    do_t = true;
+    do_m = tm != tn;
+  }
+  const bool eye = PHASE == kSquare && stage != 1;  // add a I on the diagonal
+  float *const T = reinterpret_cast<float *>(smem) + wave * 2 * kEpBlock;
+  float *const U = T + kEpBlock;
   float sq_local = 0.f;
+  auto add_eye = [&](int64_t row, int64_t col0, float(&w)[8]) {
 #pragma unroll
-  for (int i = 0; i < kSubM; ++i)
+    for (int e = 0; e < 8; ++e)
+      if (row == col0 + e && row < K.r) w[e] += args.a;
+  };
 #pragma unroll
-    for (int j = 0; j < kSubN; ++j) {
-      const int64_t col = C0 + wn * (32 * kSubN) + j * 32 + lr;
+  for (int blk = 0; blk < kSubM * kSubN; ++blk) {
+    const int i = blk / kSubN, j = blk % kSubN;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int64_t row = R0 + wm * (32 * kSubM) + i * 32 + 8 * k + 4 * lh;  // rows row..row+3
-        float v[4];
+    for (int k = 0; k < 4; ++k) {
+      f32x4 v;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = acc[i][j][4 * k + q];
-        if constexpr (PHASE == kGram) {
-          float *G = M.g();
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            v[q] *= scale;
-            G[(row + q) * K.rp + col] = v[q];
-            if constexpr (PL) put_operand(M.gs(), ng, (row + q) * K.rp + col, v[q], true);
-          }
-          if (tm != tn) {
-            *reinterpret_cast<float4 *>(G + col * K.rp + row) = make_float4(v[0], v[1], v[2], v[3]);
-            if constexpr (PL) put_operand4(M.gs(), ng, col * K.rp + row, v, true);
-          }
-        } else if constexpr (PHASE == kSquare) {
-          float *P = M.p();
-          const bool planes = PL && stage != 1;  // stage 1 keeps FP32 G2
-          if (stage == 1) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) sq_local = fmaf(v[q], v[q], sq_local);
-          } else {
-            const float *G = M.g();
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int64_t rr = row + q;
-              const float eye = (rr == col && rr < K.r) ? args.a : 0.f;
-              v[q] = (eye + args.b * G[rr * K.rp + col]) + args.c * v[q];
-            }
-          }
-#pragma unroll
-          for (int q = 0; q < 4; ++q) put_operand(P, ng, (row + q) * K.rp + col, v[q], planes);
-          if (tm != tn) put_operand4(P, ng, col * K.rp + row, v, planes);
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] *= scale;
-          const bool last = stage == 5;
-          // The stage-5 result is FP32 in parameter layout only.
-          if (!last || !M.flip()) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) put_operand(x_out, nx, (row + q) * K.cp + col, v[q], PL && !last);
-          }
-          if (!last || M.flip()) put_operand4(xt_out, nx, col * K.rp + row, v, PL && !last);
-        }
+      for (int q = 0; q < 4; ++q) {
+        v[q] = acc[i][j][4 * k + q] * scale;
+        if constexpr (PHASE == kSquare) sq_local = fmaf(v[q], v[q], sq_local);  // used in stage 1
+        T[(8 * k + 4 * lh + q) * kEpStride + lr] = v[q];
       }
-      // Keep the scheduler from hoisting every accumulator read to the top
-      // of the epilogue (256 values would not fit in the VGPRs).
-      __builtin_amdgcn_sched_barrier(0);
+      *reinterpret_cast<f32x4 *>(U + lr * kEpStride + 8 * k + 4 * lh) = v;
     }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int row = rr + 16 * q;
+      if (do_t) {
+        float w[8];
+        ep_read8(T, row, cc, w);
+        const int64_t gr = R0 + i * 32 + row, gc = C0 + j * 32 + cc;
+        if (eye) add_eye(gr, gc, w);
+        put_operand8(dst_t, gr * ld_t + gc, w, pl_t);
+      }
+      if (do_m) {
+        float w[8];
+        ep_read8(U, row, cc, w);
+        const int64_t gr = C0 + j * 32 + row, gc = R0 + i * 32 + cc;
+        if (eye) add_eye(gr, gc, w);
+        put_operand8(dst_m, gr * ld_m + gc, w, pl_m);
+      }
+    }
+    // Keep the scheduler from hoisting every accumulator read to the top
+    // of the epilogue (256 values would not fit in the VGPRs).
+    __builtin_amdgcn_sched_barrier(0);
+  }
   if constexpr (PHASE == kSquare) {
     if (stage == 1) {
       const double s = block_sum(static_cast<double>(sq_local), dscratch);
       if (threadIdx.x == 0) M.sch()[tix] = (tm == tn ? 1.0 : 2.0) * s;
     }
+  }
+}
+
+// Stage-1 polynomial operand (sandmuon/optimizer.py:84-86), one 256x256
+// tile of one matrix per block: P1 = a I + (b G)/s^2 + (c G2)/s^4 from the
+// normalised G and the FP32 G2 of the square phase, written over G2 in the
+// p buffer in operand form.  Each thread handles whole 16-element groups,
+// whose FP32 and interleaved BF16 forms occupy the same 64 bytes.
+template <int MODE>
+__global__ void __launch_bounds__(256) s8_poly1_kernel(StageArgs args) {
+  __shared__ double bcast;
+  constexpr bool PL = MODE == SMX_S8_COMP_BF16;
+  const TileRef ref = tile_of(args);
+  const S8Class &K = *ref.k;
+  const int64_t tpm = static_cast<int64_t>(K.tiles_m) * K.tiles_m;
+  if (ref.L >= tpm * K.count) return;
+  const S8Mat M{K, static_cast<int>(ref.L / tpm)};
+  const int64_t tix = ref.L % tpm;
+  const int64_t r0 = (tix / K.tiles_m) * kTile, c0 = (tix % K.tiles_m) * kTile;
+  const Stage1Scalars sc = stage1_scalars(M, &bcast);
+  const float s2 = sc.s * sc.s;
+  const float is2 = sc.ok ? 1.0f / s2 : 0.f, is4 = sc.ok ? 1.0f / (s2 * s2) : 0.f;
+  const float *G = M.g();
+  float *P = M.p();
+  constexpr int kGroups = kTile * kTile / 16;
+  for (int q = threadIdx.x; q < kGroups; q += 256) {
+    const int64_t row = r0 + q / (kTile / 16), col = c0 + (q % (kTile / 16)) * 16;
+    const int64_t idx = row * K.rp + col;
+    float g[16], w[16];
+    const float4 *w4 = reinterpret_cast<const float4 *>(P + idx);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float4 t = w4[e];
+      w[4 * e] = t.x; w[4 * e + 1] = t.y; w[4 * e + 2] = t.z; w[4 * e + 3] = t.w;
+    }
+    if constexpr (PL) {
+      const uint4 *g4 = reinterpret_cast<const uint4 *>(G + idx);  // 16 hi, then 16 lo
+      const uint4 h0 = g4[0], h1 = g4[1], l0 = g4[2], l1 = g4[3];
+      const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+      const uint32_t lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        g[2 * e] = __uint_as_float(hw[e] << 16) + __uint_as_float(lw[e] << 16);
+        g[2 * e + 1] = __uint_as_float(hw[e] & 0xffff0000u) + __uint_as_float(lw[e] & 0xffff0000u);
+      }
+    } else {
+      const float4 *g4 = reinterpret_cast<const float4 *>(G + idx);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float4 t = g4[e];
+        g[4 * e] = t.x; g[4 * e + 1] = t.y; g[4 * e + 2] = t.z; g[4 * e + 3] = t.w;
+      }
+    }
+    float v[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float eye = (row == col + e && row < K.r) ? args.a : 0.f;
+      v[e] = (eye + (args.b * g[e]) * is2) + (args.c * w[e]) * is4;
+    }
+    float lo8[8], hi8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { lo8[e] = v[e]; hi8[e] = v[8 + e]; }
+    put_operand8(P, idx, lo8, PL);
+    put_operand8(P, idx + 8, hi8, PL);
   }
 }
 
@@ -553,6 +631,7 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
   a.a = static_cast<float>(co[0]);
   a.b = static_cast<float>(co[1]);
   a.c = static_cast<float>(co[2]);
+  a.b_over_c = static_cast<float>(co[1] / co[2]);
   // Order classes by per-tile cost (K length), most expensive first.
   std::vector<int> order(Lay.n_classes);
   for (int i = 0; i < Lay.n_classes; ++i) order[i] = i;
@@ -566,7 +645,9 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
   for (int ci : order) {
     const S8Class &k = Lay.cls[ci];
     if (k.count == 0) continue;
-    const int64_t tpm = PHASE == kApply ? static_cast<int64_t>(k.tiles_m) * k.tiles_n : sym_tiles(k.tiles_m);
+    const int64_t tpm = PHASE == kApply   ? static_cast<int64_t>(k.tiles_m) * k.tiles_n
+                        : PHASE == kPoly1 ? static_cast<int64_t>(k.tiles_m) * k.tiles_m
+                                          : sym_tiles(k.tiles_m);
     const int64_t nt = round_up(tpm * k.count, 8);
     a.seg_off[a.n_seg] = off;
     a.seg_cls[a.n_seg] = ci;
@@ -575,17 +656,27 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
   }
   a.seg_off[a.n_seg] = off;
   if (off == 0) return SMX_OK;
-  if (Lay.mode == SMX_S8_COMP_BF16)
-    hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_COMP_BF16, PHASE>), dim3(off), dim3(kThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_FP32, PHASE>), dim3(off), dim3(kThreads), 0, st, a);
-  return check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : "s8 apply");
+  const bool comp = Lay.mode == SMX_S8_COMP_BF16;
+  if constexpr (PHASE == kPoly1) {
+    if (comp)
+      hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_COMP_BF16>, dim3(off), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_FP32>, dim3(off), dim3(256), 0, st, a);
+    return check_launch("s8 stage-1 polynomial");
+  } else {
+    if (comp)
+      hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_COMP_BF16, PHASE>), dim3(off), dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_FP32, PHASE>), dim3(off), dim3(kThreads), 0, st, a);
+    return check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : "s8 apply");
+  }
 }
 
 int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
   for (int stage = 1; stage <= 5; ++stage) {
     int rc = launch_phase<kGram>(Lay, stage, st);
     if (!rc) rc = launch_phase<kSquare>(Lay, stage, st);
+    if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, stage, st);
     if (!rc) rc = launch_phase<kApply>(Lay, stage, st);
     if (rc) return rc;
   }
@@ -644,7 +735,6 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.x1 = reinterpret_cast<float *>(take(xs));
     C.xt1 = reinterpret_cast<float *>(take(xs));
     C.g = reinterpret_cast<float *>(take(gs));
-    C.gs = reinterpret_cast<float *>(take(gs));
     C.p = reinterpret_cast<float *>(take(gs));
     C.u = reinterpret_cast<float *>(take(static_cast<size_t>(C.count) * C.cp * sizeof(float)));
     C.fro = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));

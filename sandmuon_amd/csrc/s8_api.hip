@@ -60,14 +60,14 @@ __global__ void __launch_bounds__(256) s8_load_tiles_kernel(S8IoArgs a) {
       v[e] = (i < a.rows && j < a.cols) ? x[i * a.sr + j * a.sc] : 0.f;
       tile[lr][lc + e] = v[e];
     }
-    put_operand4(pl, ppad * rpad, i * ppad + j0 + lc, v, a.planes != 0);
+    put_operand4(pl, i * ppad + j0 + lc, v, a.planes != 0);
   }
   __syncthreads();
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int lr = (t >> 4) + 16 * q;
     const float v[4] = {tile[lc][lr], tile[lc + 1][lr], tile[lc + 2][lr], tile[lc + 3][lr]};
-    put_operand4(tl, ppad * rpad, (j0 + lr) * rpad + i0 + lc, v, a.planes != 0);
+    put_operand4(tl, (j0 + lr) * rpad + i0 + lc, v, a.planes != 0);
   }
 }
 
