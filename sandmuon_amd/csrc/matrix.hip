@@ -34,17 +34,19 @@ struct MatJob {
   float *tl;         // transposed buffer [pcol_pad][prow_pad] (whiten)
   float *u;          // [rows] rank-one row coefficients
   double *part;      // [ceil(rows/kRowsPerPart)] partial sums
+  double *cst;       // [2]: sum z^2, sum (a z)^2 (matrix_consts_kernel)
   int64_t prow_pad, pcol_pad;
   int32_t blk0;      // first block of this job in the launch
   int32_t planes;    // whiten: write X, X^T as BF16 hi/lo planes (comp mode)
 };
 
-constexpr int kMatBatch = 12;
+constexpr int kMatBatch = 24;
 struct MatPack {
   MatJob j[kMatBatch];
   int32_t n;
   int32_t total_blocks;
 };
+static_assert(sizeof(MatPack) <= 4000, "MatPack is passed by value in the kernel arguments");
 
 __device__ __forceinline__ int find_job(const MatPack &p, int b) {
   int k = 0;
@@ -58,33 +60,50 @@ __device__ __forceinline__ float load_grad(const void *g, int dt, int64_t i) {
   return load_elem<SMX_F16>(g, i);
 }
 
-// Sum of z^2 (or of (a z)^2 when `a` is given) over n entries; block-wide.
-__device__ double sum_sq_vec(const float *z, const float *a, int64_t n, double *scratch) {
-  double s = 0.0;
-  for (int64_t j = threadIdx.x; j < n; j += blockDim.x) {
-    const double v = a ? static_cast<double>(a[j]) * z[j] : static_cast<double>(z[j]);
-    s += v * v;
+__device__ __forceinline__ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+__device__ __forceinline__ float4 ld4(const float *p, int64_t q) { return reinterpret_cast<const float4 *>(p)[q]; }
+__device__ __forceinline__ void st4(float *p, int64_t q, float4 v) { reinterpret_cast<float4 *>(p)[q] = v; }
+
+// One block per job: the rank-one constants of the matrix,
+// cst = {sum_j z_j^2, sum_j (a_j z_j)^2} (FP64), used by the row kernels.
+__global__ void __launch_bounds__(256) matrix_consts_kernel(MatPack pack) {
+  __shared__ double scratch[16];
+  const MatJob &J = pack.j[blockIdx.x];
+  const smx_matrix_desc &d = J.d;
+  if (d.z == nullptr) return;
+  double zz = 0.0, az = 0.0;
+  for (int64_t j = threadIdx.x; j < d.cols; j += blockDim.x) {
+    const double z = d.z[j], a = d.inv_col[j];
+    zz += z * z;
+    az += (a * z) * (a * z);
   }
-  return block_sum(s, scratch);
+  zz = block_sum(zz, scratch);
+  az = block_sum(az, scratch);
+  if (threadIdx.x == 0) {
+    J.cst[0] = zz;
+    J.cst[1] = az;
+  }
 }
 
+// Per-row reductions use FP32 lane partials and an FP32 wave sum; rows are
+// accumulated in FP64.  kRowsPerPart rows per block, one wave per row.
+
 // ------------------------------------------------------------- whiten ---
-// block = 256 threads (4 waves); kRowsPerPart rows per block, one wave per row.
+// Momentum update m' = b m + (1-b) g (in place), u_i = b_i sum_j S_ij a_j z_j
+// and the row's ||V_i||^2 (closed form), for S = b m' + (1-b) g.
 __global__ void __launch_bounds__(256) whiten_rows_kernel(MatPack pack) {
-  __shared__ double scratch[16];
   __shared__ double wave_part[4];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
   const int blk = blockIdx.x - J.blk0;
   const bool r1 = d.z != nullptr;
-  const double zz = r1 ? sum_sq_vec(d.z, nullptr, d.cols, scratch) : 0.0;
+  const double zz = r1 ? J.cst[0] : 0.0;
   const float kappa = r1 ? d.kappa[0] : 0.f;
   const double corr = r1 ? 2.0 * kappa + static_cast<double>(kappa) * kappa * zz : 0.0;
   const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool vec = d.grad_dtype == SMX_F32 && (d.cols % 4 == 0) &&
-                   (reinterpret_cast<uintptr_t>(d.grad) % 16 == 0) &&
-                   (reinterpret_cast<uintptr_t>(d.momentum) % 16 == 0);
+  const bool vec = d.grad_dtype == SMX_F32 && d.cols % 4 == 0 && aligned16(d.grad) && aligned16(d.momentum) &&
+                   aligned16(d.inv_col) && (!r1 || aligned16(d.z));
   double part = 0.0;
   for (int rr = wave; rr < kRowsPerPart; rr += 4) {
     const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + rr;
@@ -92,21 +111,22 @@ __global__ void __launch_bounds__(256) whiten_rows_kernel(MatPack pack) {
     float y2 = 0.f, yz = 0.f;
     float *mrow = d.momentum + i * d.cols;
     if (vec) {
-      const float4 *g4 = reinterpret_cast<const float4 *>(static_cast<const float *>(d.grad) + i * d.cols);
-      float4 *m4 = reinterpret_cast<float4 *>(mrow);
-      for (int64_t q = lane; q < d.cols / 4; q += 64) {
-        const float4 g = g4[q];
-        float4 m = m4[q];
+      const float *grow = static_cast<const float *>(d.grad) + i * d.cols;
+      const int64_t n4 = d.cols / 4;
+#pragma unroll 4
+      for (int64_t q = lane; q < n4; q += 64) {
+        const float4 g = ld4(grow, q);
+        float4 m = ld4(mrow, q);
+        const float4 a = ld4(d.inv_col, q);
         m.x = fmaf(m.x, beta, g.x * omb); m.y = fmaf(m.y, beta, g.y * omb);
         m.z = fmaf(m.z, beta, g.z * omb); m.w = fmaf(m.w, beta, g.w * omb);
-        m4[q] = m;
-        const float gs[4] = {g.x, g.y, g.z, g.w}, ms[4] = {m.x, m.y, m.z, m.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t j = q * 4 + e;
-          const float y = fmaf(ms[e], beta, gs[e] * omb) * d.inv_col[j];
-          y2 = fmaf(y, y, y2);
-          if (r1) yz = fmaf(y, d.z[j], yz);
+        st4(mrow, q, m);
+        const float y0 = fmaf(m.x, beta, g.x * omb) * a.x, y1 = fmaf(m.y, beta, g.y * omb) * a.y;
+        const float y2_ = fmaf(m.z, beta, g.z * omb) * a.z, y3 = fmaf(m.w, beta, g.w * omb) * a.w;
+        y2 = fmaf(y0, y0, fmaf(y1, y1, fmaf(y2_, y2_, fmaf(y3, y3, y2))));
+        if (r1) {
+          const float4 z = ld4(d.z, q);
+          yz = fmaf(y0, z.x, fmaf(y1, z.y, fmaf(y2_, z.z, fmaf(y3, z.w, yz))));
         }
       }
     } else {
@@ -119,8 +139,8 @@ __global__ void __launch_bounds__(256) whiten_rows_kernel(MatPack pack) {
         if (r1) yz = fmaf(y, d.z[j], yz);
       }
     }
-    const double Y2 = wave_sum(static_cast<double>(y2));
-    const double YZ = wave_sum(static_cast<double>(yz));
+    const double Y2 = wave_sum(y2);
+    const double YZ = wave_sum(yz);
     const double b = d.inv_row[i];
     const double u = b * YZ;
     if (lane == 0) {
@@ -130,10 +150,12 @@ __global__ void __launch_bounds__(256) whiten_rows_kernel(MatPack pack) {
   }
   if (lane == 0) wave_part[wave] = part;
   __syncthreads();
-  if (threadIdx.x == 0) J.part[blk] = wave_part[0] + wave_part[1] + wave_part[2] + wave_part[3];
+  if (threadIdx.x == 0) J.part[blk] = (wave_part[0] + wave_part[1]) + (wave_part[2] + wave_part[3]);
 }
 
-// block = 256 threads, one 64x64 tile of the padded parameter layout.
+// block = 256 threads, one 64x64 tile of the padded parameter layout:
+// V = b_i S_ij a_j + kappa u_i z_j, stored to the parameter-layout buffer and,
+// transposed through LDS, to the other buffer (operand form).
 __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
   __shared__ float tile[64][65];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
@@ -144,27 +166,49 @@ __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
   const bool r1 = d.z != nullptr;
   const float kappa = r1 ? d.kappa[0] : 0.f;
   const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
+  const bool vec = d.grad_dtype == SMX_F32 && d.cols % 4 == 0 && aligned16(d.grad) && aligned16(d.momentum) &&
+                   aligned16(d.inv_col) && (!r1 || aligned16(d.z));
   const int t = threadIdx.x;
   const int lc = (t & 15) * 4;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int lr = (t >> 4) + 16 * q;
-    const int64_t i = i0 + lr;
-    float v[4];
+    const int64_t i = i0 + lr, j = j0 + lc;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (i < d.rows) {
+      const float b = d.inv_row[i];
+      const float ku = r1 ? kappa * J.u[i] : 0.f;
+      if (vec && j + 3 < d.cols) {
+        const int64_t e4 = (i * d.cols + j) / 4;
+        const float4 g = ld4(static_cast<const float *>(d.grad), e4), m = ld4(d.momentum, e4);
+        const float4 a = ld4(d.inv_col, j / 4);
+        const float gs[4] = {g.x, g.y, g.z, g.w}, ms[4] = {m.x, m.y, m.z, m.w}, as[4] = {a.x, a.y, a.z, a.w};
+        float zs[4] = {0.f, 0.f, 0.f, 0.f};
+        if (r1) {
+          const float4 z = ld4(d.z, j / 4);
+          zs[0] = z.x; zs[1] = z.y; zs[2] = z.z; zs[3] = z.w;
+        }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int64_t j = j0 + lc + e;
-      float val = 0.f;
-      if (i < d.rows && j < d.cols) {
-        const float g = load_grad(d.grad, d.grad_dtype, i * d.cols + j);
-        const float s = fmaf(d.momentum[i * d.cols + j], beta, g * omb);
-        val = (s * d.inv_row[i]) * d.inv_col[j];
-        if (r1) val = fmaf(kappa * J.u[i], d.z[j], val);
+        for (int e = 0; e < 4; ++e) {
+          const float s = fmaf(ms[e], beta, gs[e] * omb);
+          v[e] = (s * b) * as[e];
+          if (r1) v[e] = fmaf(ku, zs[e], v[e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (j + e < d.cols) {
+            const float g = load_grad(d.grad, d.grad_dtype, i * d.cols + j + e);
+            const float s = fmaf(d.momentum[i * d.cols + j + e], beta, g * omb);
+            v[e] = (s * b) * d.inv_col[j + e];
+            if (r1) v[e] = fmaf(ku, d.z[j + e], v[e]);
+          }
+        }
       }
-      v[e] = val;
-      tile[lr][lc + e] = val;
     }
-    put_operand4(J.pl, i * J.pcol_pad + j0 + lc, v, J.planes != 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[lr][lc + e] = v[e];
+    put_operand4(J.pl, i * J.pcol_pad + j, v, J.planes != 0);
   }
   __syncthreads();
 #pragma unroll
@@ -176,34 +220,51 @@ __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
 }
 
 // ------------------------------------------------------------ mapback ---
+// u_i = sum_j Q_ij z_j and ||U_i||^2 in closed form:
+// b_i^2 (sum (a Q)^2 + 2 kappa u_i sum (a Q)(a z) + kappa^2 u_i^2 sum (a z)^2).
 __global__ void __launch_bounds__(256) mapback_rows_kernel(MatPack pack) {
-  __shared__ double scratch[16];
   __shared__ double wave_part[4];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
   const int blk = blockIdx.x - J.blk0;
   const bool r1 = d.z != nullptr;
-  const double cz = r1 ? sum_sq_vec(d.z, d.inv_col, d.cols, scratch) : 0.0;
+  const double cz = r1 ? J.cst[1] : 0.0;
   const double kappa = r1 ? d.kappa[0] : 0.0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool vec = d.cols % 4 == 0 && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
   double part = 0.0;
   for (int rr = wave; rr < kRowsPerPart; rr += 4) {
     const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + rr;
     if (i >= d.rows) break;
     const float *q = J.pl + i * J.pcol_pad;
     float su = 0.f, sa = 0.f, sb = 0.f;
-    for (int64_t j = lane; j < d.cols; j += 64) {
-      const float a = d.inv_col[j];
-      const float aq = a * q[j];
-      sa = fmaf(aq, aq, sa);
-      if (r1) {
-        su = fmaf(q[j], d.z[j], su);
-        sb = fmaf(aq, a * d.z[j], sb);
+    if (vec) {
+      const int64_t n4 = d.cols / 4;
+#pragma unroll 4
+      for (int64_t k = lane; k < n4; k += 64) {
+        const float4 qv = ld4(q, k), a = ld4(d.inv_col, k);
+        const float aq0 = a.x * qv.x, aq1 = a.y * qv.y, aq2 = a.z * qv.z, aq3 = a.w * qv.w;
+        sa = fmaf(aq0, aq0, fmaf(aq1, aq1, fmaf(aq2, aq2, fmaf(aq3, aq3, sa))));
+        if (r1) {
+          const float4 z = ld4(d.z, k);
+          su = fmaf(qv.x, z.x, fmaf(qv.y, z.y, fmaf(qv.z, z.z, fmaf(qv.w, z.w, su))));
+          sb = fmaf(aq0, a.x * z.x, fmaf(aq1, a.y * z.y, fmaf(aq2, a.z * z.z, fmaf(aq3, a.w * z.w, sb))));
+        }
+      }
+    } else {
+      for (int64_t j = lane; j < d.cols; j += 64) {
+        const float a = d.inv_col[j];
+        const float aq = a * q[j];
+        sa = fmaf(aq, aq, sa);
+        if (r1) {
+          su = fmaf(q[j], d.z[j], su);
+          sb = fmaf(aq, a * d.z[j], sb);
+        }
       }
     }
-    const double U = wave_sum(static_cast<double>(su));
-    const double A = wave_sum(static_cast<double>(sa));
-    const double B = wave_sum(static_cast<double>(sb));
+    const double U = wave_sum(su);
+    const double A = wave_sum(sa);
+    const double B = wave_sum(sb);
     if (lane == 0) {
       const double b = d.inv_row[i];
       J.u[i] = static_cast<float>(U);
@@ -212,10 +273,11 @@ __global__ void __launch_bounds__(256) mapback_rows_kernel(MatPack pack) {
   }
   if (lane == 0) wave_part[wave] = part;
   __syncthreads();
-  if (threadIdx.x == 0) J.part[blk] = wave_part[0] + wave_part[1] + wave_part[2] + wave_part[3];
+  if (threadIdx.x == 0) J.part[blk] = (wave_part[0] + wave_part[1]) + (wave_part[2] + wave_part[3]);
 }
 
-// block = 256 threads over kRowsPerPart rows of the parameter.
+// W -= lr * sqrt(rows) / max(||U||_F, FLT_MIN) * U over kRowsPerPart rows
+// (one wave per row).
 __global__ void __launch_bounds__(256) mapback_apply_kernel(MatPack pack) {
   __shared__ double bcast;
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
@@ -237,18 +299,39 @@ __global__ void __launch_bounds__(256) mapback_apply_kernel(MatPack pack) {
   const float nlr = static_cast<float>(-d.lr);
   const bool r1 = d.z != nullptr;
   const float kappa = r1 ? d.kappa[0] : 0.f;
-  for (int rr = 0; rr < kRowsPerPart; ++rr) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool vec = d.cols % 4 == 0 && aligned16(d.param) && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
+  for (int rr = wave; rr < kRowsPerPart; rr += 4) {
     const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + rr;
     if (i >= d.rows) break;
     const float *q = J.pl + i * J.pcol_pad;
     float *w = d.param + i * d.cols;
     const float b = d.inv_row[i];
     const float ku = r1 ? kappa * J.u[i] : 0.f;
-    for (int64_t j = threadIdx.x; j < d.cols; j += 256) {
-      float v = q[j];
-      if (r1) v = fmaf(ku, d.z[j], v);
-      const float U = (v * b) * d.inv_col[j];
-      w[j] = fmaf(nlr, U * scale, w[j]);
+    if (vec) {
+      const int64_t n4 = d.cols / 4;
+#pragma unroll 4
+      for (int64_t k = lane; k < n4; k += 64) {
+        float4 v = ld4(q, k);
+        const float4 a = ld4(d.inv_col, k);
+        float4 wv = ld4(w, k);
+        if (r1) {
+          const float4 z = ld4(d.z, k);
+          v.x = fmaf(ku, z.x, v.x); v.y = fmaf(ku, z.y, v.y); v.z = fmaf(ku, z.z, v.z); v.w = fmaf(ku, z.w, v.w);
+        }
+        wv.x = fmaf(nlr, ((v.x * b) * a.x) * scale, wv.x);
+        wv.y = fmaf(nlr, ((v.y * b) * a.y) * scale, wv.y);
+        wv.z = fmaf(nlr, ((v.z * b) * a.z) * scale, wv.z);
+        wv.w = fmaf(nlr, ((v.w * b) * a.w) * scale, wv.w);
+        st4(w, k, wv);
+      }
+    } else {
+      for (int64_t j = lane; j < d.cols; j += 64) {
+        float v = q[j];
+        if (r1) v = fmaf(ku, d.z[j], v);
+        const float U = (v * b) * d.inv_col[j];
+        w[j] = fmaf(nlr, U * scale, w[j]);
+      }
     }
   }
 }
@@ -320,6 +403,7 @@ static int launch_jobs(std::vector<MatJob> &jobs, int64_t (*blocks_of)(const Mat
   return SMX_OK;
 }
 
+static int64_t one_block(const MatJob &) { return 1; }
 static int64_t row_blocks(const MatJob &j) { return ceil_div(j.d.rows, kRowsPerPart); }
 static int64_t tile_blocks(const MatJob &j) { return (j.prow_pad / 64) * (j.pcol_pad / 64); }
 
@@ -384,6 +468,7 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
       j.pl = M.flip() ? M.xt0() : M.x0();
       j.tl = M.flip() ? M.x0() : M.xt0();
       j.part = M.fro();
+      j.cst = M.cst();
       j.planes = mode == SMX_S8_COMP_BF16;
       ping[k] = j;
       j.pl = M.flip() ? M.xt1() : M.x1();
@@ -392,7 +477,8 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
       j.planes = 0;
       fin[k] = j;
     }
-    int rc = launch_jobs(ping, row_blocks, whiten_rows_kernel, "whiten_rows", st);
+    int rc = launch_jobs(ping, one_block, matrix_consts_kernel, "matrix_consts", st);
+    if (!rc) rc = launch_jobs(ping, row_blocks, whiten_rows_kernel, "whiten_rows", st);
     if (!rc) rc = launch_jobs(ping, tile_blocks, whiten_tiles_kernel, "whiten_tiles", st);
     if (!rc) rc = run_s8_stages(plan.layout, st);
     if (!rc) rc = launch_jobs(fin, row_blocks, mapback_rows_kernel, "mapback_rows", st);

@@ -10,7 +10,7 @@ namespace smx {
 
 constexpr int kTile = 256;        // GEMM macro tile (M and N) and padding
 constexpr int kMaxClasses = 8;    // shape classes per GEMM launch
-constexpr int kRowsPerPart = 16;  // param rows per whiten/mapback partial
+constexpr int kRowsPerPart = 16;  // param rows per whiten/mapback partial (one block)
 
 // Fixed S8 recipe: sandmuon/coefficients.py:3-11.
 constexpr double kS8Margin = 1.35;
@@ -42,6 +42,7 @@ struct S8Class {
   double *fro;         // [count][parts] whiten: partial sum of V^2
   double *mb;          // [count][parts] mapback: partial sum of U^2
   double *sch;         // [count][tiles_m*(tiles_m+1)/2] Schatten partials
+  double *cst;         // [count][2] matrix-step constants: sum z^2, sum (a z)^2
 };
 
 struct S8Layout {
@@ -68,6 +69,7 @@ struct S8Mat {
   __host__ __device__ double *fro() const { return kp()->fro + static_cast<int64_t>(slot) * kp()->parts; }
   __host__ __device__ double *mb() const { return kp()->mb + static_cast<int64_t>(slot) * kp()->parts; }
   __host__ __device__ double *sch() const { return kp()->sch + slot * sym_tiles(kp()->tiles_m); }
+  __host__ __device__ double *cst() const { return kp()->cst + 2 * static_cast<int64_t>(slot); }
   // Parameter layout: rows x cols; the parameter-layout buffer of the
   // ping side is xt0 for transposed parameters and x0 otherwise.
   __host__ __device__ int64_t prow() const { return flip() ? kp()->c : kp()->r; }

@@ -740,6 +740,7 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.fro = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));
     C.mb = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));
     C.sch = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * sym_tiles(C.tiles_m) * sizeof(double)));
+    C.cst = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * 2 * sizeof(double)));
   }
   plan.bytes = off;
   return true;

@@ -190,20 +190,46 @@ stats_fold_kernel(float *sum_sq, float *slots_sq, float *sum_first, float *slots
 }
 
 // ----------------------------------------------------------- finish ---
-constexpr int kFinishBatch = 24;  // descriptors per launch (by value)
+constexpr int kFinishBatch = 32;  // descriptors per launch (by value)
 struct FinishPack {
   smx_finish_desc d[kFinishBatch];
   int32_t n;
 };
+static_assert(sizeof(FinishPack) <= 4000, "FinishPack is passed by value in the kernel arguments");
 
-// Fold pass over a batch of descriptors: grid.x enumerates 256-channel
-// chunks of every vector, grid.y = descriptor.
+// Fold pass over a batch of descriptors: grid.x enumerates 64-channel
+// chunks of every vector, grid.y = descriptor.  Wave w sums slots w, w+4, ...
+// of the chunk (coalesced 256-byte rows, several loads in flight) and zeroes
+// them; the four wave partials are combined in a fixed order (FP64).
 __global__ void __launch_bounds__(256) finish_fold_kernel(FinishPack pack) {
+  __shared__ double part[2][4][64];
   const smx_finish_desc &d = pack.d[blockIdx.y];
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (c >= d.n) return;
-  fold_channel(d.sum_sq, d.slots_sq, d.n, d.n_slots, c);
-  if (d.kind == 1) fold_channel(d.sum_first, d.slots_first, d.n, d.n_slots, c);
+  if (static_cast<int64_t>(blockIdx.x) * 64 >= d.n) return;  // uniform per block
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  const bool ok = c < d.n;
+  const int nv = d.kind == 1 ? 2 : 1;
+  for (int v = 0; v < nv; ++v) {
+    float *slots = v ? d.slots_first : d.slots_sq;
+    double t = 0.0;
+    if (ok) {
+#pragma unroll 8
+      for (int p = wave; p < d.n_slots; p += 4) {
+        float *s = slots + static_cast<int64_t>(p) * d.n + c;
+        t += static_cast<double>(*s);
+        *s = 0.f;
+      }
+    }
+    part[v][wave][lane] = t;
+  }
+  __syncthreads();
+  if (wave == 0 && ok) {
+    for (int v = 0; v < nv; ++v) {
+      float *sum = v ? d.sum_first : d.sum_sq;
+      const double t = (part[v][0][lane] + part[v][1][lane]) + (part[v][2][lane] + part[v][3][lane]);
+      sum[c] = static_cast<float>(static_cast<double>(sum[c]) + t);
+    }
+  }
 }
 
 __device__ __forceinline__ float ema_update(float e, float x, float beta, float omb) {
@@ -355,7 +381,7 @@ extern "C" int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc, do
       pack.d[i] = descs[b + i];
       nmax = std::max<int64_t>(nmax, pack.d[i].n);
     }
-    hipLaunchKernelGGL(finish_fold_kernel, dim3(static_cast<unsigned>(ceil_div(nmax, 256)), pack.n),
+    hipLaunchKernelGGL(finish_fold_kernel, dim3(static_cast<unsigned>(ceil_div(nmax, 64)), pack.n),
                        dim3(256), 0, st, pack);
     int rc = check_launch("stats_finish(fold)");
     if (rc) return rc;

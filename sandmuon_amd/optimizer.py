@@ -374,15 +374,17 @@ class DiagonalWeightedPE(Optimizer):
             if id(source) not in seen:
                 seen.add(id(source))
                 sources.append(source)
-        # One flat buffer for every factor of this step.
-        sizes = []
+        # One flat buffer for every factor of this step; each vector starts on
+        # a 16-byte boundary (the kernels' vector loads).
+        sizes, lengths = [], []
         for s in sources:
             d = self.state[s]["a_sum"].numel()
-            sizes += [d, d, 1] if self.rank_one_a else [d]
+            lengths += [d, d, 1] if self.rank_one_a else [d]
         for parameter, _, _ in items:
-            sizes.append(parameter.shape[0])
+            lengths.append(parameter.shape[0])
+        sizes = [-(-n // 4) * 4 for n in lengths]
         flat = torch.empty(sum(sizes), dtype=torch.float32, device=device)
-        views = iter(torch.split(flat, sizes))
+        views = iter(v[:n] for v, n in zip(torch.split(flat, sizes), lengths))
         a_out, b_out, descs = {}, {}, []
         for s in sources:
             out = {"inv": next(views)}
