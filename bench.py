@@ -20,7 +20,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -31,7 +30,6 @@ METRIC = "optimizer step ms (103M GPT, 54 mats) + S8 GEMM MFMA %peak, 1 GPU"
 HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
 BF16_PEAK = 2.5e15         # dense BF16 MFMA, FLOP/s
 FP32_PEAK = 157.3e12       # FP32 MFMA, FLOP/s
-TILE = 256
 
 
 def parse():
@@ -87,60 +85,43 @@ def run_hooks(opt, sets, micro):
             opt._accumulate_b(p, d)
 
 
-def s8_flops(opt, mode):
-    """Logical S8 FLOPs 5(4 r^2 c + 2 r^3) and MFMA FLOPs the kernels issue."""
-    logical = issued = 0
+def summarize_s8(launches, steps):
+    """Per-step S8 GEMM time and issued MFMA FLOPs from the recorded launches
+    (Gram, square, apply; the elementwise stage-1 polynomial pass is listed
+    separately)."""
+    per = {}
+    for ms, phase, flops in launches:
+        d = per.setdefault(phase, [0, 0.0, 0.0])
+        d[0] += 1
+        d[1] += ms
+        d[2] += flops
+    gemm = [p for p in ("gram", "square", "apply") if p in per]
+    ms = sum(per[p][1] for p in gemm) / steps
+    flops = sum(per[p][2] for p in gemm) / steps
+    phases = {p: {"launches_per_step": per[p][0] / steps, "avg_us": round(per[p][1] / per[p][0] * 1e3, 1),
+                  "tflops": round(per[p][2] / (per[p][1] * 1e-3) / 1e12, 1) if per[p][2] else None}
+              for p in per}
+    return ms, flops, phases
+
+
+def logical_s8_flops(opt):
+    """Logical S8 FLOPs per step: 5 (4 r^2 c + 2 r^3) per oriented r x c matrix."""
+    total = 0
     for p in opt.named_matrices.values():
         r, c = sorted(p.shape)
-        logical += 5 * (4 * r * r * c + 2 * r ** 3)
-        tm, tn = math.ceil(r / TILE), math.ceil(c / TILE)
-        rp, cp = tm * TILE, tn * TILE
-        sym = tm * (tm + 1) // 2
-        per_stage = 2 * TILE * TILE * (sym * cp + sym * rp + tm * tn * rp)
-        issued += 5 * per_stage * (3 if mode == "comp_bf16" else 1)
-    return logical, issued
+        total += 5 * (4 * r * r * c + 2 * r ** 3)
+    return total
 
 
-def time_events(fn, reps=1):
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(reps):
-        fn()
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / reps
-
-
-def s8_only_time(opt, mode, device):
-    """One S8 pass over the step's matrices (same shape classes and
-    orientation), timed on the current stream."""
-    from sandmuon_amd import _native
-    from sandmuon_amd.optimizer import _s8_fp32
-    groups = {}
-    for p in opt.named_matrices.values():
-        groups.setdefault(tuple(p.shape), 0)
-        groups[tuple(p.shape)] += 1
-    xs = [torch.randn(n, *shape, device=device) for shape, n in groups.items()]
-    run = lambda: [_s8_fp32(x, mode=mode) for x in xs]
-    run()
-    torch.cuda.synchronize()
-    return time_events(run, reps=3)
-
-
-def stats_kernel_time(opt, sets):
-    """Sum of per-launch durations (events around each hook launch) for one
-    microbatch, and its bytes."""
-    a, b = sets[0]
-    evs = []
-    for p, x in a:
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record(); opt._accumulate_a(p, x); e.record(); evs.append((s, e, x.numel() * x.element_size()))
-    for p, d in b:
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record(); opt._accumulate_b(p, d); e.record(); evs.append((s, e, d.numel() * d.element_size()))
-    torch.cuda.synchronize()
-    ms = sum(s.elapsed_time(e) for s, e, _ in evs)
-    return ms, sum(n for *_, n in evs), len(evs)
+def committed_traffic():
+    """HBM bytes per launch of the dominant kernels, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None if absent)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_cfg4.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 # -------------------------------------------------------- CPU baseline ---
@@ -204,52 +185,68 @@ def main():
                           "n_gpus_requested": args.gpus}))
         sys.exit(2)
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from sandmuon_amd import _native
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
     log(f"building {args.config} ({args.s8_mode})")
     model, opt, sets, micro, stat_bytes = build(args.config, args.s8_mode, device)
     log(f"built: {len(opt.named_matrices)} matrices, {stat_bytes / 1e9:.2f} GB of hook input per step")
 
-    def one_step():
+    def one_step(ev=None):
+        if ev:
+            ev[0].record()
         run_hooks(opt, sets, micro)
+        if ev:
+            ev[1].record()
         opt.step()
+        if ev:
+            ev[2].record()
 
     for _ in range(args.warmup):
         one_step()
     torch.cuda.synchronize()
     log("warmup done")
+    # Timed region: K steps between two events; inside it, event pairs around
+    # the hook phase and step() of every step, and the library records an
+    # event pair around every S8 GEMM launch on the stream it uses.
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _native.s8_timing(True)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record()
-    for _ in range(args.steps):
-        one_step()
+    for k in range(args.steps):
+        one_step(evs[k])
     end.record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    _native.s8_timing(False)
+    launches = _native.s8_timing_read()
     ms = start.elapsed_time(end) / args.steps
-    log(f"timed {args.steps} steps: {ms:.3f} ms/step")
+    hooks_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    step_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    s8_ms, s8_issued, s8_phases = summarize_s8(launches, args.steps)
+    s8_logical = logical_s8_flops(opt)
+    log(f"timed {args.steps} steps: {ms:.3f} ms/step (hooks {hooks_ms:.3f}, step {step_ms:.3f}, "
+        f"S8 GEMM launches {s8_ms:.3f})")
 
-    # Phase breakdown (untimed above): hooks of one step, step() alone.
-    hooks_ms = time_events(lambda: run_hooks(opt, sets, micro))
-    step_ms = time_events(opt.step)
-    stats_ms_1, stats_bytes_1, stats_launches = stats_kernel_time(opt, sets)
-    s8_ms = s8_only_time(opt, args.s8_mode, device)
-    logical, issued = s8_flops(opt, args.s8_mode)
     peak_mfma = BF16_PEAK if args.s8_mode == "comp_bf16" else FP32_PEAK
-
-    stats_gbs = stats_bytes_1 / (stats_ms_1 * 1e-3) / 1e9
-    s8_issued_tfs = issued / (s8_ms * 1e-3) / 1e12
-    s8_logical_tfs = logical / (s8_ms * 1e-3) / 1e12
+    stats_gbs = stat_bytes / (hooks_ms * 1e-3) / 1e9
+    s8_tfs = s8_issued / (s8_ms * 1e-3) / 1e12
+    traffic = committed_traffic() or {}
     roof_stats = {"bound": "hbm", "achieved": round(stats_gbs, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                  "frac": round(stats_gbs / (HBM_PEAK / 1e9), 4), "traffic": None,
-                  "kernel": "stats_accumulate_kernel", "launches_timed": stats_launches,
-                  "bytes_per_step": stat_bytes, "ms_per_step_kernels": round(stats_ms_1 * micro, 3)}
-    roof_s8 = {"bound": "mfma", "achieved": round(s8_issued_tfs, 1), "peak": peak_mfma / 1e12, "unit": "TFLOP/s",
-               "frac": round(s8_issued_tfs / (peak_mfma / 1e12), 4), "traffic": None,
-               "kernel": "s8_stage_kernel (gram/square/apply)", "issued_flops_per_step": issued,
-               "logical_flops_per_step": logical, "logical_tflops": round(s8_logical_tfs, 1),
-               "ms_per_step": round(s8_ms, 3)}
-    dominant = roof_stats if stats_ms_1 * micro >= s8_ms else roof_s8
+                  "frac": round(stats_gbs / (HBM_PEAK / 1e9), 4),
+                  "traffic": traffic.get("stats_accumulate_kernel", {}).get("hbm_bytes_per_step"),
+                  "kernel": "stats_accumulate_kernel (every hook launch of the step, back to back)",
+                  "bytes_per_step": stat_bytes, "ms_per_step": round(hooks_ms, 3)}
+    roof_s8 = {"bound": "mfma", "achieved": round(s8_tfs, 1), "peak": peak_mfma / 1e12, "unit": "TFLOP/s",
+               "frac": round(s8_tfs / (peak_mfma / 1e12), 4),
+               "traffic": traffic.get("s8_stage_kernel", {}).get("hbm_bytes_per_step"),
+               "kernel": "s8_stage_kernel (Gram/square/apply launches of step())",
+               "issued_flops_per_step": s8_issued, "logical_flops_per_step": s8_logical,
+               "logical_tflops": round(s8_logical / (s8_ms * 1e-3) / 1e12, 1), "ms_per_step": round(s8_ms, 3),
+               "phases": s8_phases}
+    dominant = roof_stats if hooks_ms >= s8_ms else roof_s8
     out = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
@@ -263,7 +260,6 @@ def main():
         "roofline_s8": roof_s8,
         "phases_ms": {"hooks": round(hooks_ms, 3), "step": round(step_ms, 3), "host_wall_per_step": round(wall, 3)},
     }
-    log(f"breakdown: hooks {hooks_ms:.3f} ms, step {step_ms:.3f} ms, s8 {s8_ms:.3f} ms")
     if not args.no_cpu_baseline:
         log("cpu baseline")
         threads = args.cpu_threads or len(os.sched_getaffinity(0))

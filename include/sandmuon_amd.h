@@ -186,6 +186,22 @@ int smx_s8(const float *x, float *out, int64_t batch, int64_t rows,
            size_t workspace_bytes, void *stream);
 
 /* ------------------------------------------------------------------ *
+ * Launch timing of the S8 kernels (no counterpart in the reference; a
+ * measurement aid for benchmarks).  smx_s8_timing(1) discards earlier
+ * records and starts recording a HIP event pair around every S8 phase
+ * launch (by smx_matrix_step and smx_s8) on its stream; smx_s8_timing(0)
+ * stops recording.  smx_s8_timing_read waits for the recorded launches
+ * and writes up to `capacity` records: duration (ms), phase (0 Gram,
+ * 1 square, 2 apply, 3 stage-1 polynomial) and the MFMA FLOPs the launch
+ * issues (tiles computed x 2*256*256*K, x3 in SMX_S8_COMP_BF16 mode, plus
+ * the square phase's one-hot MFMAs).  It returns the number of records
+ * or a negative status.  The recorder is process-wide, not thread-safe.
+ * ------------------------------------------------------------------ */
+int smx_s8_timing(int32_t enable);
+int32_t smx_s8_timing_read(float *ms, int32_t *phase, double *flops,
+                           int32_t capacity);
+
+/* ------------------------------------------------------------------ *
  * Module-level helpers.
  * smx_rank1_apply: rank1_whiten (sandmuon/optimizer.py:38-45, order 0) and
  * rank1_mapback (:48-60, order 1) on a contiguous fp32 batch

@@ -74,6 +74,9 @@ SIGNATURES = {
     "smx_rank1_apply": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                 c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "smx_graft": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p]),
+    "smx_s8_timing": (c_int, [c_int32]),
+    "smx_s8_timing_read": (c_int32, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(c_int32),
+                                     ctypes.POINTER(c_double), c_int32]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -175,6 +178,24 @@ def matrix_step(descs: Sequence[MatrixDesc], mode: int, workspace: torch.Tensor)
     arr = (MatrixDesc * len(descs))(*descs)
     _check(lib().smx_matrix_step(arr, len(descs), mode, workspace.data_ptr(), workspace.numel(),
                                  stream_of(workspace.device)), "smx_matrix_step")
+
+
+S8_PHASES = {0: "gram", 1: "square", 2: "apply", 3: "poly1"}
+
+
+def s8_timing(enable: bool) -> None:
+    """Start (discarding earlier records) or stop the S8 launch recorder."""
+    _check(lib().smx_s8_timing(1 if enable else 0), "smx_s8_timing")
+
+
+def s8_timing_read(capacity: int = 4096):
+    """Recorded S8 launches as (ms, phase name, issued MFMA FLOPs); waits for them."""
+    ms = (ctypes.c_float * capacity)()
+    ph = (c_int32 * capacity)()
+    fl = (c_double * capacity)()
+    n = lib().smx_s8_timing_read(ms, ph, fl, capacity)
+    _check(min(n, 0), "smx_s8_timing_read")
+    return [(ms[i], S8_PHASES[ph[i]], fl[i]) for i in range(n)]
 
 
 def s8(x: torch.Tensor, out: torch.Tensor, mode: int) -> None:

@@ -622,6 +622,61 @@ __global__ void __launch_bounds__(256) s8_poly1_kernel(StageArgs args) {
 }
 
 // ------------------------------------------------------------- host ---
+// Optional per-launch event timing (smx_s8_timing).
+struct LaunchTiming {
+  bool on = false;
+  std::vector<hipEvent_t> start, stop;
+  std::vector<int32_t> phase;
+  std::vector<double> flops;
+  size_t used = 0;
+};
+static LaunchTiming g_timing;
+
+static int timing_begin(hipStream_t st) {
+  if (!g_timing.on) return SMX_OK;
+  if (g_timing.used == g_timing.start.size()) {
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)
+      return fail(SMX_ELAUNCH, "s8 timing: hipEventCreate failed");
+    g_timing.start.push_back(a);
+    g_timing.stop.push_back(b);
+    g_timing.phase.push_back(0);
+    g_timing.flops.push_back(0.0);
+  }
+  if (hipEventRecord(g_timing.start[g_timing.used], st) != hipSuccess)
+    return fail(SMX_ELAUNCH, "s8 timing: hipEventRecord failed");
+  return SMX_OK;
+}
+
+static int timing_end(hipStream_t st, int phase, double flops) {
+  if (!g_timing.on) return SMX_OK;
+  if (hipEventRecord(g_timing.stop[g_timing.used], st) != hipSuccess)
+    return fail(SMX_ELAUNCH, "s8 timing: hipEventRecord failed");
+  g_timing.phase[g_timing.used] = phase;
+  g_timing.flops[g_timing.used] = flops;
+  ++g_timing.used;
+  return SMX_OK;
+}
+
+// MFMA FLOPs of one launch: computed tiles x 2 * 256 * 256 * K (x3 in
+// compensated mode), plus the square phase's one-hot MFMAs (8 stages of
+// kSubN 32x32x16 products per wave).
+template <int PHASE>
+static double launch_flops(const S8Layout &Lay, int stage) {
+  if (PHASE == kPoly1) return 0.0;
+  const double prod = Lay.mode == SMX_S8_COMP_BF16 ? 3.0 : 1.0;
+  double f = 0.0;
+  for (int i = 0; i < Lay.n_classes; ++i) {
+    const S8Class &k = Lay.cls[i];
+    const double tiles = PHASE == kApply ? static_cast<double>(k.tiles_m) * k.tiles_n
+                                         : static_cast<double>(sym_tiles(k.tiles_m));
+    const double K = PHASE == kGram ? static_cast<double>(k.cp) : static_cast<double>(k.rp);
+    f += k.count * tiles * 2.0 * kTile * kTile * K * prod;
+    if (PHASE == kSquare && stage != 1) f += k.count * tiles * kWaves * 8.0 * kSubN * 2.0 * 32 * 32 * kBK * prod;
+  }
+  return f;
+}
+
 template <int PHASE>
 static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
   StageArgs a{};
@@ -657,19 +712,23 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
   a.seg_off[a.n_seg] = off;
   if (off == 0) return SMX_OK;
   const bool comp = Lay.mode == SMX_S8_COMP_BF16;
+  int rc = timing_begin(st);
+  if (rc) return rc;
   if constexpr (PHASE == kPoly1) {
     if (comp)
       hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_COMP_BF16>, dim3(off), dim3(256), 0, st, a);
     else
       hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_FP32>, dim3(off), dim3(256), 0, st, a);
-    return check_launch("s8 stage-1 polynomial");
+    rc = check_launch("s8 stage-1 polynomial");
   } else {
     if (comp)
       hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_COMP_BF16, PHASE>), dim3(off), dim3(kThreads), 0, st, a);
     else
       hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_FP32, PHASE>), dim3(off), dim3(kThreads), 0, st, a);
-    return check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : "s8 apply");
+    rc = check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : "s8 apply");
   }
+  if (rc) return rc;
+  return timing_end(st, PHASE, launch_flops<PHASE>(Lay, stage));
 }
 
 int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
@@ -747,3 +806,27 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
 }
 
 }  // namespace smx
+
+using smx::g_timing;
+
+extern "C" int smx_s8_timing(int32_t enable) {
+  g_timing.on = enable != 0;
+  if (g_timing.on) g_timing.used = 0;
+  return SMX_OK;
+}
+
+extern "C" int32_t smx_s8_timing_read(float *ms, int32_t *phase, double *flops, int32_t capacity) {
+  SMX_REQUIRE(capacity >= 0, SMX_EINVAL, "s8 timing: negative capacity");
+  const int32_t n = static_cast<int32_t>(std::min<size_t>(g_timing.used, static_cast<size_t>(capacity)));
+  for (int32_t i = 0; i < n; ++i) {
+    if (hipEventSynchronize(g_timing.stop[i]) != hipSuccess)
+      return smx::fail(SMX_ELAUNCH, "s8 timing: hipEventSynchronize failed");
+    float t = 0.f;
+    if (hipEventElapsedTime(&t, g_timing.start[i], g_timing.stop[i]) != hipSuccess)
+      return smx::fail(SMX_ELAUNCH, "s8 timing: hipEventElapsedTime failed");
+    if (ms) ms[i] = t;
+    if (phase) phase[i] = g_timing.phase[i];
+    if (flops) flops[i] = g_timing.flops[i];
+  }
+  return n;
+}

@@ -102,3 +102,11 @@ def test_workspace_sizes_are_consistent():
         dense = 4 * (36 * 768 * 768 + 18 * 768 * 3072) * 4 + 2 * 54 * 768 * 768 * 4
         assert dense <= ws <= dense * 1.01
     assert _native.lib().smx_s8_workspace_bytes(2, 7, 3, 0) > 0
+
+
+def test_s8_timing_recorder_without_launches():
+    lib = _native.lib()
+    assert lib.smx_s8_timing(1) == 0
+    assert _native.s8_timing_read(16) == []
+    assert lib.smx_s8_timing(0) == 0
+    assert lib.smx_s8_timing_read(None, None, None, -1) == -1

@@ -65,3 +65,27 @@ def test_s8_orientation_transpose_equivariance(device):
     a = _s8_fp32(x)
     b = _s8_fp32(x.transpose(-2, -1).contiguous())
     assert max(per_matrix_rel(b.transpose(-2, -1), a)) <= 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+def test_s8_launch_timing_records_every_phase(device, mode):
+    from sandmuon_amd import _native
+    x = torch.randn(3, 300, 520, device=device)
+    _native.s8_timing(True)
+    try:
+        _s8_fp32(x, mode=mode)
+    finally:
+        _native.s8_timing(False)
+    rec = _native.s8_timing_read()
+    phases = [p for _, p, _ in rec]
+    assert phases == ["gram", "square", "poly1", "apply"] + ["gram", "square", "apply"] * 4
+    assert all(ms > 0 for ms, _, _ in rec)
+    # oriented 300 x 520 padded to 512 x 768: 2 x 3 tiles, 3 symmetric tiles
+    prod = 3 if mode == "comp_bf16" else 1
+    gram, apply = 3 * 3 * 2 * 256 * 256 * 768 * prod, 3 * 6 * 2 * 256 * 256 * 512 * prod
+    square1 = 3 * 3 * 2 * 256 * 256 * 512 * prod
+    one_hot = 3 * 3 * 4 * 8 * 4 * 2 * 32 * 32 * 16 * prod
+    fl = [f for _, _, f in rec]
+    assert fl[:4] == [gram, square1, 0.0, apply]
+    assert fl[4:7] == [gram, square1 + one_hot, apply]
