@@ -5,7 +5,8 @@
  * Every entry point is extern "C", takes plain pointers and sizes, and
  * enqueues work on the explicit `stream` (a hipStream_t passed as void*).
  * No entry point allocates or frees device memory, synchronises the device
- * or copies device data to the host.  Device buffers (including workspaces)
+ * or copies device data to the host (smx_s8_timing_read, a benchmark aid,
+ * waits for the events it reports).  Device buffers (including workspaces)
  * belong to the caller.  Descriptor tables (smx_*_desc) are HOST arrays:
  * the library copies them into kernel arguments by value at launch, so the
  * caller may reuse or free them as soon as the call returns.
@@ -46,9 +47,10 @@ enum smx_dtype { SMX_F32 = 0, SMX_BF16 = 1, SMX_F16 = 2 };
  * SMX_S8_FP32: every product on FP32 MFMA (v_mfma_f32_32x32x2_f32), FP32
  *   intermediates.  Restates sandmuon/optimizer.py:69-93.
  * SMX_S8_COMP_BF16: every product as three BF16 MFMAs on hi/lo splits
- *   (hi*lo + lo*hi + hi*hi, FP32 accumulation), FP32 intermediates.  The
- *   compensated-product scheme of reproduction/odl/ops/
- *   bf16_compensated_mm_fast.py:18-68, applied to all five stages. */
+ *   (hi*lo + lo*hi + hi*hi, FP32 accumulation); intermediates are stored as
+ *   the BF16 hi/lo pair.  The compensated-product scheme of
+ *   reproduction/odl/ops/bf16_compensated_mm_fast.py:18-68, applied to all
+ *   five stages. */
 enum smx_s8_mode { SMX_S8_FP32 = 0, SMX_S8_COMP_BF16 = 1 };
 
 int smx_abi_version(void);
@@ -191,11 +193,13 @@ int smx_s8(const float *x, float *out, int64_t batch, int64_t rows,
  * records and starts recording a HIP event pair around every S8 phase
  * launch (by smx_matrix_step and smx_s8) on its stream; smx_s8_timing(0)
  * stops recording.  smx_s8_timing_read waits for the recorded launches
- * and writes up to `capacity` records: duration (ms), phase (0 Gram,
- * 1 square, 2 apply, 3 stage-1 polynomial) and the MFMA FLOPs the launch
- * issues (tiles computed x 2*256*256*K, x3 in SMX_S8_COMP_BF16 mode, plus
- * the square phase's one-hot MFMAs).  It returns the number of records
- * or a negative status.  The recorder is process-wide, not thread-safe.
+ * and writes up to `capacity` records in the order they were opened:
+ * duration (ms), phase (0 Gram, 1 square, 2 apply, 3 stage-1 polynomial,
+ * 4 a whole S8 run, first launch to last)
+ * and the MFMA FLOPs the launch (or run) issues (tiles computed x
+ * 2*256*256*K, x3 in SMX_S8_COMP_BF16 mode, plus the square phase's
+ * one-hot MFMAs).  It returns the number of records or a negative status.
+ * The recorder is process-wide, not thread-safe.
  * ------------------------------------------------------------------ */
 int smx_s8_timing(int32_t enable);
 int32_t smx_s8_timing_read(float *ms, int32_t *phase, double *flops,

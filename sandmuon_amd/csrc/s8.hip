@@ -54,7 +54,7 @@ constexpr int kStageBytes = 2 * kOpTile;           // A + B
 constexpr int kRingBytes = kStages * kStageBytes;
 constexpr int kLoadsPerStage = 2 * (kOpTile / 1024) / kWaves;  // 1 KB loads per wave and stage
 
-enum Phase { kGram = 0, kSquare = 1, kApply = 2, kPoly1 = 3 };
+enum Phase { kGram = 0, kSquare = 1, kApply = 2, kPoly1 = 3, kSpan = 4 };  // kSpan: timing record of a whole S8 run
 
 struct StageArgs {
   S8Layout L;
@@ -632,7 +632,10 @@ struct LaunchTiming {
 };
 static LaunchTiming g_timing;
 
-static int timing_begin(hipStream_t st) {
+// Opens a record (start event on `st`) and returns its index in `slot`
+// (-1 when the recorder is off); timing_end closes it.  Records nest.
+static int timing_begin(hipStream_t st, int &slot) {
+  slot = -1;
   if (!g_timing.on) return SMX_OK;
   if (g_timing.used == g_timing.start.size()) {
     hipEvent_t a, b;
@@ -643,18 +646,19 @@ static int timing_begin(hipStream_t st) {
     g_timing.phase.push_back(0);
     g_timing.flops.push_back(0.0);
   }
-  if (hipEventRecord(g_timing.start[g_timing.used], st) != hipSuccess)
+  slot = static_cast<int>(g_timing.used++);
+  g_timing.phase[slot] = -1;  // open
+  if (hipEventRecord(g_timing.start[slot], st) != hipSuccess)
     return fail(SMX_ELAUNCH, "s8 timing: hipEventRecord failed");
   return SMX_OK;
 }
 
-static int timing_end(hipStream_t st, int phase, double flops) {
-  if (!g_timing.on) return SMX_OK;
-  if (hipEventRecord(g_timing.stop[g_timing.used], st) != hipSuccess)
+static int timing_end(int slot, hipStream_t st, int phase, double flops) {
+  if (slot < 0) return SMX_OK;
+  if (hipEventRecord(g_timing.stop[slot], st) != hipSuccess)
     return fail(SMX_ELAUNCH, "s8 timing: hipEventRecord failed");
-  g_timing.phase[g_timing.used] = phase;
-  g_timing.flops[g_timing.used] = flops;
-  ++g_timing.used;
+  g_timing.phase[slot] = phase;
+  g_timing.flops[slot] = flops;
   return SMX_OK;
 }
 
@@ -712,7 +716,8 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
   a.seg_off[a.n_seg] = off;
   if (off == 0) return SMX_OK;
   const bool comp = Lay.mode == SMX_S8_COMP_BF16;
-  int rc = timing_begin(st);
+  int slot = -1;
+  int rc = timing_begin(st, slot);
   if (rc) return rc;
   if constexpr (PHASE == kPoly1) {
     if (comp)
@@ -728,18 +733,26 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
     rc = check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : "s8 apply");
   }
   if (rc) return rc;
-  return timing_end(st, PHASE, launch_flops<PHASE>(Lay, stage));
+  return timing_end(slot, st, PHASE, launch_flops<PHASE>(Lay, stage));
 }
 
+// The whole S8 run: per stage one launch per phase over every class (class
+// segments ordered by K cost, so long-K tiles start first and short tiles
+// fill the remaining CUs).  The launch recorder gets one record for the run.
 int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
+  int slot = -1;
+  int rc = timing_begin(st, slot);
+  if (rc) return rc;
+  double flops = 0.0;
   for (int stage = 1; stage <= 5; ++stage) {
-    int rc = launch_phase<kGram>(Lay, stage, st);
+    rc = launch_phase<kGram>(Lay, stage, st);
     if (!rc) rc = launch_phase<kSquare>(Lay, stage, st);
     if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, stage, st);
     if (!rc) rc = launch_phase<kApply>(Lay, stage, st);
     if (rc) return rc;
+    flops += launch_flops<kGram>(Lay, stage) + launch_flops<kSquare>(Lay, stage) + launch_flops<kApply>(Lay, stage);
   }
-  return SMX_OK;
+  return timing_end(slot, st, kSpan, flops);
 }
 
 bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, int mode, char *base,
@@ -819,6 +832,7 @@ extern "C" int32_t smx_s8_timing_read(float *ms, int32_t *phase, double *flops, 
   SMX_REQUIRE(capacity >= 0, SMX_EINVAL, "s8 timing: negative capacity");
   const int32_t n = static_cast<int32_t>(std::min<size_t>(g_timing.used, static_cast<size_t>(capacity)));
   for (int32_t i = 0; i < n; ++i) {
+    SMX_REQUIRE(g_timing.phase[i] >= 0, SMX_EINVAL, "s8 timing: a record is still open");
     if (hipEventSynchronize(g_timing.stop[i]) != hipSuccess)
       return smx::fail(SMX_ELAUNCH, "s8 timing: hipEventSynchronize failed");
     float t = 0.f;

@@ -79,8 +79,11 @@ def test_s8_launch_timing_records_every_phase(device, mode):
         _native.s8_timing(False)
     rec = _native.s8_timing_read()
     phases = [p for _, p, _ in rec]
-    assert phases == ["gram", "square", "poly1", "apply"] + ["gram", "square", "apply"] * 4
+    assert phases == ["run", "gram", "square", "poly1", "apply"] + ["gram", "square", "apply"] * 4
     assert all(ms > 0 for ms, _, _ in rec)
+    run, rec = rec[0], rec[1:]
+    assert run[2] == sum(f for _, _, f in rec)
+    assert run[0] >= max(ms for ms, _, _ in rec)
     # oriented 300 x 520 padded to 512 x 768: 2 x 3 tiles, 3 symmetric tiles
     prod = 3 if mode == "comp_bf16" else 1
     gram, apply = 3 * 3 * 2 * 256 * 256 * 768 * prod, 3 * 6 * 2 * 256 * 256 * 512 * prod
