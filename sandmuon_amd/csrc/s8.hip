@@ -82,30 +82,41 @@ struct Opnd {
 __device__ __forceinline__ int swz4(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 __device__ __forceinline__ int f32_off(int r, int kc) { return (r * 4 + (kc ^ swz4(r))) << 4; }
 
-// One 16-byte direct-to-LDS load per lane: lane l writes LDS[m0 + 16 l].
-// Issued from asm so the compiler does not treat later LDS reads as
-// aliasing the in-flight load (it would wait for every outstanding load);
-// the ring's waits are explicit (wait_vm).  M0 is an input operand.
-__device__ __forceinline__ void dma16(const void *src, char *lds_wave_base) {
-  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_wave_base));
-  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+// One 16-byte direct-to-LDS load per lane from sbase + voff (scalar base,
+// per-lane 32-bit byte offset): lane l writes LDS[m0 + 16 l].  Issued from
+// asm so the compiler does not treat later LDS reads as aliasing the
+// in-flight load (it would wait for every outstanding load); the ring's
+// waits are explicit (wait_vm).  M0 is an input operand; the s_nop is the
+// wait state an LDS DMA needs after a scalar write of M0, which the
+// compiler cannot see through the asm.
+__device__ __forceinline__ void dma16(uint32_t voff, const void *sbase, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
 }
 
-// This wave's share of an operand tile (rows row0.., K k0..k0+15; `ld` and
-// k0 in 4-byte elements): LDS chunk p = (wave*N+i)*64 + lane is stored slot
-// p&3 of row p>>2.
-__device__ __forceinline__ void dma_tile(const void *__restrict__ src, int64_t ld, int64_t row0, int64_t k0,
-                                         char *tile) {
-  const float *M = static_cast<const float *>(src);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  constexpr int N = (kOpTile / 1024) / kWaves;
+// This wave's share of an operand tile (rows row0.., 16 K columns): LDS
+// chunk p = (wave*N+i)*64 + lane is stored slot p&3 of row p>>2.  The
+// per-lane byte offsets at K = 0 are computed once per tile; a stage at K
+// offset k0 only moves the scalar base by 4*k0 bytes.
+constexpr int kChunksPerWave = (kOpTile / 1024) / kWaves;
+struct TileOffsets {
+  uint32_t v[kChunksPerWave];
+};
+__device__ __forceinline__ TileOffsets tile_offsets(int64_t ld, int64_t row0, int wave) {
+  const int lane = threadIdx.x & 63;
+  TileOffsets t;
 #pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const int p = (wave * N + i) * 64 + lane;
+  for (int i = 0; i < kChunksPerWave; ++i) {
+    const int p = (wave * kChunksPerWave + i) * 64 + lane;
     const int row = p >> 2;
     const int kc = (p & 3) ^ swz4(row);
-    dma16(M + (row0 + row) * ld + k0 + kc * 4, tile + (wave * N + i) * 1024);
+    t.v[i] = static_cast<uint32_t>(((row0 + row) * ld + kc * 4) * 4);
   }
+  return t;
+}
+
+__device__ __forceinline__ void dma_tile(const TileOffsets &t, const char *sbase, uint32_t lds) {
+#pragma unroll
+  for (int i = 0; i < kChunksPerWave; ++i) dma16(t.v[i], sbase, lds + i * 1024);
 }
 
 template <int N>
@@ -241,11 +252,12 @@ __device__ __forceinline__ AFrag<MODE> one_hot(float s, int r0) {
   return f;
 }
 
-// Issues one stage (A and B tiles) into a ring slot.
-__device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, int64_t arow0, int64_t brow0,
-                                            int64_t k0, char *st) {
-  dma_tile(A.p, A.ld, arow0, k0, st);
-  dma_tile(B.p, B.ld, brow0, k0, st + kOpTile);
+// Issues one stage (A and B tiles) into a ring slot.  `lds` is the slot's
+// LDS byte address plus this wave's first chunk (wave-uniform).
+__device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const TileOffsets &oa,
+                                            const TileOffsets &ob, int64_t k0, uint32_t lds) {
+  dma_tile(oa, static_cast<const char *>(A.p) + 4 * k0, lds);
+  dma_tile(ob, static_cast<const char *>(B.p) + 4 * k0, lds + kOpTile);
 }
 
 // Waits until at most `pending` stages of this wave's loads are in flight
@@ -258,7 +270,11 @@ __device__ __forceinline__ void wait_stages(int pending) {
   else wait_vm<0>();
 }
 
-__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// lgkmcnt(0) (vmcnt and expcnt left at their maxima) as a builtin, so the
+// compiler's own wait-count tracking sees the LDS reads complete; an asm
+// wait would leave them pending in its model and it would then insert
+// lgkmcnt waits before later MFMAs that stall on unrelated newer reads.
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // C[256 x 256] = A[arow0.., :K] * B[brow0.., :K]^T.
 //
@@ -276,15 +292,16 @@ __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)"
 // SEL >= 0: this stage is stage SEL of the wave's 8-stage one_hot window
 // (rows 16 SEL .. 16 SEL + 15 of the wave, accumulator block SEL / 2).
 template <int MODE, int SEL, int PAR>
-__device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, int64_t arow0, int64_t brow0, float sel_s,
-                                          char *smem, int kt, int nk, int wm, int wn, AFrag<MODE> (&af)[kSubM],
-                                          BFrags<MODE> (&bf)[2], f32x16 (&acc)[kSubM][kSubN]) {
+__device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const TileOffsets &oa, const TileOffsets &ob,
+                                          uint32_t lds0, float sel_s, char *smem, int kt, int nk, int wm, int wn,
+                                          AFrag<MODE> (&af)[kSubM], BFrags<MODE> (&bf)[2],
+                                          f32x16 (&acc)[kSubM][kSubN]) {
   constexpr int S = kStages;
   const bool more = kt + 1 < nk;
   if (more) wait_stages(min(S - 2, nk - 2 - kt));
   wait_lds();
   block_barrier();
-  if (kt + S < nk) issue_stage(A, B, arow0, brow0, static_cast<int64_t>(kt + S) * kBK, smem + (kt % S) * kStageBytes);
+  if (kt + S < nk) issue_stage(A, B, oa, ob, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * kStageBytes);
   const char *nxt = smem + ((kt + 1) % S) * kStageBytes;
   if (more) load_b<MODE>(nxt, wn, bf[PAR ^ 1]);
 #pragma unroll
@@ -310,9 +327,12 @@ __device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &B, int64_t K
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
   const int nk = static_cast<int>(K / kBK);
+  const TileOffsets oa = tile_offsets(A.ld, arow0, wave), ob = tile_offsets(B.ld, brow0, wave);
+  // LDS byte address of the ring plus this wave's first chunk.
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * kChunksPerWave * 1024;
 #pragma unroll
   for (int s = 0; s < kStages; ++s)
-    if (s < nk) issue_stage(A, B, arow0, brow0, static_cast<int64_t>(s) * kBK, smem + s * kStageBytes);
+    if (s < nk) issue_stage(A, B, oa, ob, static_cast<int64_t>(s) * kBK, lds0 + s * kStageBytes);
   wait_stages(min(kStages - 1, nk - 1));
   block_barrier();
   AFrag<MODE> af[kSubM];
@@ -321,7 +341,7 @@ __device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &B, int64_t K
 #pragma unroll
   for (int i = 0; i < kSubM; ++i) load_a<MODE>(smem, wm, i, af[i]);
 #define SMX_PIPE(SEL, PAR, KT) \
-  pipe_iter<MODE, SEL, PAR>(A, B, arow0, brow0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
+  pipe_iter<MODE, SEL, PAR>(A, B, oa, ob, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
   int kt = 0;
   if constexpr (ACCG) {
     // The wave's rows are K stages kt0 .. kt0 + 7 (kt0 = first row / 16, a
