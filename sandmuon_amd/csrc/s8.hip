@@ -291,17 +291,24 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 // interleaved with the reads of stage kt+1.
 // SEL >= 0: this stage is stage SEL of the wave's 8-stage one_hot window
 // (rows 16 SEL .. 16 SEL + 15 of the wave, accumulator block SEL / 2).
-template <int MODE, int SEL, int PAR>
+// STEADY: kt + kStages < nk, so a next stage exists, the refill is due and
+// kStages - 2 stages may stay in flight (no run-time conditions).
+template <int MODE, int SEL, int PAR, bool STEADY>
 __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const TileOffsets &oa, const TileOffsets &ob,
                                           uint32_t lds0, float sel_s, char *smem, int kt, int nk, int wm, int wn,
                                           AFrag<MODE> (&af)[kSubM], BFrags<MODE> (&bf)[2],
                                           f32x16 (&acc)[kSubM][kSubN]) {
   constexpr int S = kStages;
-  const bool more = kt + 1 < nk;
-  if (more) wait_stages(min(S - 2, nk - 2 - kt));
+  const bool more = STEADY || kt + 1 < nk;
+  if constexpr (STEADY) {
+    wait_vm<(S - 2) * kLoadsPerStage>();
+  } else {
+    if (more) wait_stages(min(S - 2, nk - 2 - kt));
+  }
   wait_lds();
   block_barrier();
-  if (kt + S < nk) issue_stage(A, B, oa, ob, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * kStageBytes);
+  if (STEADY || kt + S < nk)
+    issue_stage(A, B, oa, ob, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * kStageBytes);
   const char *nxt = smem + ((kt + 1) % S) * kStageBytes;
   if (more) load_b<MODE>(nxt, wn, bf[PAR ^ 1]);
 #pragma unroll
@@ -318,6 +325,7 @@ template <int MODE, bool ACCG>
 __device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &B, int64_t K, int64_t arow0, int64_t brow0,
                                          float sel_s, char *smem, f32x16 (&acc)[kSubM][kSubN]) {
   static_assert(kSubM == 4 && kBK == 16, "the one_hot window is 8 stages of 16 rows");
+  static_assert(kStages % 2 == 0, "pairs of stages keep the fragment parity");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int wm = wave >> 1, wn = wave & 1;
 #pragma unroll
@@ -340,32 +348,38 @@ __device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &B, int64_t K
   load_b<MODE>(smem, wn, bf[0]);
 #pragma unroll
   for (int i = 0; i < kSubM; ++i) load_a<MODE>(smem, wm, i, af[i]);
-#define SMX_PIPE(SEL, PAR, KT) \
-  pipe_iter<MODE, SEL, PAR>(A, B, oa, ob, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
+#define SMX_PIPE(SEL, PAR, KT, STEADY) \
+  pipe_iter<MODE, SEL, PAR, STEADY>(A, B, oa, ob, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
+  // Stages [kt, to) in pairs (kt and `to` even): branch-free while a refill
+  // is due, then the general form.
+  const int steady_end = nk - kStages;
+  auto run = [&](int &kt, int to) {
+    for (; kt + 1 < min(to, steady_end); kt += 2) {
+      SMX_PIPE(-1, 0, kt, true);
+      SMX_PIPE(-1, 1, kt + 1, true);
+    }
+    for (; kt + 1 < to; kt += 2) {
+      SMX_PIPE(-1, 0, kt, false);
+      SMX_PIPE(-1, 1, kt + 1, false);
+    }
+  };
   int kt = 0;
   if constexpr (ACCG) {
     // The wave's rows are K stages kt0 .. kt0 + 7 (kt0 = first row / 16, a
     // multiple of 8, so the stage parity matches the unrolled pairs).
     const int kt0 = static_cast<int>((arow0 + wm * (32 * kSubM)) / kBK);
-    for (; kt < kt0; kt += 2) {
-      SMX_PIPE(-1, 0, kt);
-      SMX_PIPE(-1, 1, kt + 1);
-    }
-    SMX_PIPE(0, 0, kt0);
-    SMX_PIPE(1, 1, kt0 + 1);
-    SMX_PIPE(2, 0, kt0 + 2);
-    SMX_PIPE(3, 1, kt0 + 3);
-    SMX_PIPE(4, 0, kt0 + 4);
-    SMX_PIPE(5, 1, kt0 + 5);
-    SMX_PIPE(6, 0, kt0 + 6);
-    SMX_PIPE(7, 1, kt0 + 7);
+    run(kt, kt0);
+    SMX_PIPE(0, 0, kt0, false);
+    SMX_PIPE(1, 1, kt0 + 1, false);
+    SMX_PIPE(2, 0, kt0 + 2, false);
+    SMX_PIPE(3, 1, kt0 + 3, false);
+    SMX_PIPE(4, 0, kt0 + 4, false);
+    SMX_PIPE(5, 1, kt0 + 5, false);
+    SMX_PIPE(6, 0, kt0 + 6, false);
+    SMX_PIPE(7, 1, kt0 + 7, false);
     kt = kt0 + 8;
   }
-  for (; kt + 1 < nk; kt += 2) {
-    SMX_PIPE(-1, 0, kt);
-    SMX_PIPE(-1, 1, kt + 1);
-  }
-  if (kt < nk) SMX_PIPE(-1, 0, kt);
+  run(kt, nk);
 #undef SMX_PIPE
   block_barrier();
 }
