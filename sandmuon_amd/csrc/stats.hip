@@ -158,10 +158,12 @@ static void launch_acc(const void *x, int64_t rows, int64_t cols, int64_t row_st
 template <int DT, int VEC>
 static void dispatch_ct(const void *x, int64_t rows, int64_t cols, int64_t row_stride,
                         float *slots_sq, float *slots_first, int32_t n_slots, hipStream_t st) {
+  // The widest column tile that still gives >= 6 tiles, so that a hook call
+  // of 16K rows puts >= 768 blocks (24 waves per CU) in flight.
   const int64_t vcols = ceil_div(cols, VEC);
-  if (vcols % 64 == 0 || vcols > 256)
+  if (vcols >= 6 * 64)
     launch_acc<DT, VEC, 64>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
-  else if (vcols % 32 == 0 || vcols > 16)
+  else if (vcols >= 6 * 32)
     launch_acc<DT, VEC, 32>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
   else
     launch_acc<DT, VEC, 16>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
