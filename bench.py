@@ -41,7 +41,22 @@ def parse():
     ap.add_argument("--s8-mode", default="comp_bf16", choices=["comp_bf16", "fp32"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: all cores in the affinity mask")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
+                    help="only run 3 plain device copies of MB megabytes (the known-size reference for "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     return ap.parse_args()
+
+
+def copy_calibration(mb):
+    """Three plain copies of `mb` MB (reads and writes mb*2^20 bytes each)."""
+    n = mb * (1 << 20) // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 3}), flush=True)
 
 
 # ------------------------------------------------------------ workload ---
@@ -177,6 +192,9 @@ def log(msg):
 # ---------------------------------------------------------------- main ---
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "bench.py measures one GPU only: the optimizer step is run and reported "
