@@ -100,20 +100,20 @@ def run_hooks(opt, sets, micro):
             opt._accumulate_b(p, d)
 
 
-def summarize_s8(launches, steps):
-    """Per-step S8 time and issued MFMA FLOPs from the recorded launches.
-    The time is the span of each whole S8 run (first launch to last, so it
-    includes the stage-1 polynomial pass and the gaps between launches);
-    per-phase launch averages are listed alongside."""
+def summarize_s8(runs, launches, steps):
+    """Per-step S8 time and issued MFMA FLOPs from the whole-run records of
+    the timed steps (first launch to last, so the time includes the stage-1
+    polynomial pass and the gaps between launches), and per-phase launch
+    averages from the per-launch records of one further, untimed step."""
+    assert [p for _, p, _ in runs] == ["run"] * len(runs) and len(runs) % steps == 0
+    ms = sum(r[0] for r in runs) / steps
+    flops = sum(r[2] for r in runs) / steps
     per = {}
-    for ms, phase, flops in launches:
-        d = per.setdefault(phase, [0, 0.0, 0.0])
+    for t, phase, fl in launches:
+        d = per.setdefault(phase, [0, 0.0])
         d[0] += 1
-        d[1] += ms
-        d[2] += flops
-    ms = per["run"][1] / steps
-    flops = per["run"][2] / steps
-    phases = {p: {"launches_per_step": per[p][0] / steps, "avg_us": round(per[p][1] / per[p][0] * 1e3, 1)}
+        d[1] += t
+    phases = {p: {"launches_per_step": per[p][0], "avg_us": round(per[p][1] / per[p][0] * 1e3, 1)}
               for p in per if p != "run"}
     return ms, flops, phases
 
@@ -225,10 +225,10 @@ def main():
     log("warmup done")
     # Timed region: K steps between two events; inside it, event pairs around
     # the hook phase and step() of every step, and the library records an
-    # event pair around every S8 GEMM launch on the stream it uses.
+    # event pair around each step's whole S8 run on the stream it uses.
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    _native.s8_timing(True)
+    _native.s8_timing(True, runs_only=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record()
@@ -238,11 +238,17 @@ def main():
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / args.steps
     _native.s8_timing(False)
+    runs = _native.s8_timing_read()
+    # One more step, untimed, with an event pair around every S8 launch for
+    # the per-phase breakdown.
+    _native.s8_timing(True)
+    one_step()
+    _native.s8_timing(False)
     launches = _native.s8_timing_read()
     ms = start.elapsed_time(end) / args.steps
     hooks_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
     step_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
-    s8_ms, s8_issued, s8_phases = summarize_s8(launches, args.steps)
+    s8_ms, s8_issued, s8_phases = summarize_s8(runs, launches, args.steps)
     s8_logical = logical_s8_flops(opt)
     log(f"timed {args.steps} steps: {ms:.3f} ms/step (hooks {hooks_ms:.3f}, step {step_ms:.3f}, "
         f"S8 GEMM launches {s8_ms:.3f})")

@@ -191,7 +191,9 @@ int smx_s8(const float *x, float *out, int64_t batch, int64_t rows,
  * Launch timing of the S8 kernels (no counterpart in the reference; a
  * measurement aid for benchmarks).  smx_s8_timing(1) discards earlier
  * records and starts recording a HIP event pair around every S8 phase
- * launch (by smx_matrix_step and smx_s8) on its stream; smx_s8_timing(0)
+ * launch (by smx_matrix_step and smx_s8) and around every whole S8 run,
+ * on its stream; smx_s8_timing(2) records whole runs only (two events per
+ * run, so the launches inside it run back to back); smx_s8_timing(0)
  * stops recording.  smx_s8_timing_read waits for the recorded launches
  * and writes up to `capacity` records in the order they were opened:
  * duration (ms), phase (0 Gram, 1 square, 2 apply, 3 stage-1 polynomial,

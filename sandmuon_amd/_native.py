@@ -191,9 +191,11 @@ def matrix_step(descs: Sequence[MatrixDesc], mode: int, workspace: torch.Tensor)
 S8_PHASES = {0: "gram", 1: "square", 2: "apply", 3: "poly1", 4: "run"}
 
 
-def s8_timing(enable: bool) -> None:
-    """Start (discarding earlier records) or stop the S8 launch recorder."""
-    _check(lib().smx_s8_timing(1 if enable else 0), "smx_s8_timing")
+def s8_timing(enable, runs_only: bool = False) -> None:
+    """Start (discarding earlier records) or stop the S8 launch recorder.
+    With runs_only, only whole S8 runs are recorded (two events per run)."""
+    level = 0 if not enable else (2 if runs_only else 1)
+    _check(lib().smx_s8_timing(level), "smx_s8_timing")
 
 
 def s8_timing_read(capacity: int = 4096):

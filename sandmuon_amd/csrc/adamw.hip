@@ -6,42 +6,65 @@
 #include "common.h"
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 
 namespace smx {
 
-constexpr int kAdamBatch = 32;
-constexpr int kAdamChunk = 2048;  // elements per block
+constexpr int kAdamBatch = 56;
+constexpr int kAdamMaxChunk = 2048;  // elements per block (large launches)
+constexpr int kAdamUnroll = 4;
 
 struct AdamPack {
+  int32_t first_blk[kAdamBatch];  // ceil(offset / chunk); INT32_MAX past the last
   smx_adamw_desc d[kAdamBatch];
   int32_t n;
   int64_t total;
+  int64_t chunk;
   float neg_lr, decay, b1, omb1, b2, omb2, eps;
 };
+static_assert(sizeof(AdamPack) <= 4000, "AdamPack is passed by value in the kernel arguments");
 
 __global__ void __launch_bounds__(256) adamw_kernel(AdamPack pk) {
-  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kAdamChunk;
-  const int64_t e1 = min(pk.total, e0 + kAdamChunk);
-  // Tensor holding e0 (offsets are ascending).
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * pk.chunk;
+  const int64_t e1 = min(pk.total, e0 + pk.chunk);
+  // Tensor holding e0, the last with offset <= e0 (offsets are ascending):
+  // independent compares, no chain of dependent descriptor loads.
   int k = 0;
-  while (k + 1 < pk.n && pk.d[k + 1].offset <= e0) ++k;
+#pragma unroll
+  for (int t = 1; t < kAdamBatch; ++t) k += static_cast<int>(blockIdx.x) >= pk.first_blk[t] ? 1 : 0;
   for (; k < pk.n && pk.d[k].offset < e1; ++k) {
     const smx_adamw_desc &d = pk.d[k];
     const int64_t lo = max(e0, d.offset) - d.offset;
     const int64_t hi = min(e1, d.offset + d.n) - d.offset;
-    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
-      float g;
-      if (d.grad_dtype == SMX_F32) g = static_cast<const float *>(d.grad)[i];
-      else if (d.grad_dtype == SMX_BF16) g = load_elem<SMX_BF16>(d.grad, i);
-      else g = load_elem<SMX_F16>(d.grad, i);
-      const float m = d.exp_avg[i] * pk.b1 + g * pk.omb1;
-      const float v = d.exp_avg_sq[i] * pk.b2 + (g * g) * pk.omb2;
-      d.exp_avg[i] = m;
-      d.exp_avg_sq[i] = v;
-      const float u = (m / d.bias1) / (sqrtf(v / d.bias2) + pk.eps);
-      const float p = d.param[i] * pk.decay;
-      d.param[i] = p + pk.neg_lr * u;
+    // kAdamUnroll elements per thread per pass, all loaded before any is
+    // updated, so a block over small tensors is not one latency per element.
+    for (int64_t i0 = lo + threadIdx.x; i0 < hi; i0 += 256 * kAdamUnroll) {
+      float g[kAdamUnroll], m[kAdamUnroll], v[kAdamUnroll], p[kAdamUnroll];
+#pragma unroll
+      for (int u = 0; u < kAdamUnroll; ++u) {
+        const int64_t i = i0 + u * 256;
+        if (i < hi) {
+          if (d.grad_dtype == SMX_F32) g[u] = static_cast<const float *>(d.grad)[i];
+          else if (d.grad_dtype == SMX_BF16) g[u] = load_elem<SMX_BF16>(d.grad, i);
+          else g[u] = load_elem<SMX_F16>(d.grad, i);
+          m[u] = d.exp_avg[i];
+          v[u] = d.exp_avg_sq[i];
+          p[u] = d.param[i];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kAdamUnroll; ++u) {
+        const int64_t i = i0 + u * 256;
+        if (i < hi) {
+          const float mu = m[u] * pk.b1 + g[u] * pk.omb1;
+          const float vu = v[u] * pk.b2 + (g[u] * g[u]) * pk.omb2;
+          d.exp_avg[i] = mu;
+          d.exp_avg_sq[i] = vu;
+          const float step = (mu / d.bias1) / (sqrtf(vu / d.bias2) + pk.eps);
+          d.param[i] = p[u] * pk.decay + pk.neg_lr * step;
+        }
+      }
     }
   }
 }
@@ -84,8 +107,15 @@ extern "C" int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t to
     pk.omb2 = static_cast<float>(1.0 - beta2);
     pk.eps = static_cast<float>(eps);
     if (pk.total == 0) continue;
-    hipLaunchKernelGGL(adamw_kernel, dim3(static_cast<unsigned>(ceil_div(pk.total, kAdamChunk))), dim3(256),
-                       0, st, pk);
+    // Small launches (the biases and norms left after the embeddings) use
+    // short chunks, so they spread over more CUs instead of queueing behind
+    // each other in a few blocks.
+    pk.chunk = std::min<int64_t>(kAdamMaxChunk, std::max<int64_t>(256, ceil_div(ceil_div(pk.total, 2048), 256) * 256));
+    const int64_t blocks = ceil_div(pk.total, pk.chunk);
+    SMX_REQUIRE(blocks < INT32_MAX, SMX_ESHAPE, "adamw: too many elements for one launch");
+    for (int i = 0; i < kAdamBatch; ++i)
+      pk.first_blk[i] = i < pk.n ? static_cast<int32_t>(ceil_div(pk.d[i].offset, pk.chunk)) : INT32_MAX;
+    hipLaunchKernelGGL(adamw_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, pk);
     const int rc = check_launch("adamw");
     if (rc) return rc;
   }

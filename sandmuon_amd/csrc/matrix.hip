@@ -21,6 +21,7 @@
 #include "s8.h"
 
 #include <algorithm>
+#include <climits>
 #include <cfloat>
 #include <cmath>
 #include <memory>
@@ -42,15 +43,19 @@ struct MatJob {
 
 constexpr int kMatBatch = 24;
 struct MatPack {
+  int32_t start[kMatBatch];  // first block of each job; INT32_MAX past the last
   MatJob j[kMatBatch];
   int32_t n;
   int32_t total_blocks;
 };
 static_assert(sizeof(MatPack) <= 4000, "MatPack is passed by value in the kernel arguments");
 
+// The job of block b: independent compares against the compact start
+// table (a few batched scalar loads, no chain of dependent lookups).
 __device__ __forceinline__ int find_job(const MatPack &p, int b) {
   int k = 0;
-  while (k + 1 < p.n && b >= p.j[k + 1].blk0) ++k;
+#pragma unroll
+  for (int t = 1; t < kMatBatch; ++t) k += b >= p.start[t] ? 1 : 0;
   return k;
 }
 
@@ -86,13 +91,27 @@ __global__ void __launch_bounds__(256) matrix_consts_kernel(MatPack pack) {
 }
 
 // Per-row reductions use FP32 lane partials and an FP32 wave sum; rows are
-// accumulated in FP64.  kRowsPerPart rows per block, one wave per row.
+// accumulated in FP64.  kRowsPerPart rows per block, one wave per row, so
+// every row's loads are in flight at once.
+constexpr int kRowThreads = 64 * kRowsPerPart;
+
+// FP64 sum of the per-wave row partials, in wave order; the result is valid
+// in thread 0.
+__device__ __forceinline__ double sum_wave_parts(double part, double *wave_part) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) wave_part[wave] = part;
+  __syncthreads();
+  double t = 0.0;
+  if (threadIdx.x == 0)
+    for (int w = 0; w < kRowsPerPart; ++w) t += wave_part[w];
+  return t;
+}
 
 // ------------------------------------------------------------- whiten ---
 // Momentum update m' = b m + (1-b) g (in place), u_i = b_i sum_j S_ij a_j z_j
 // and the row's ||V_i||^2 (closed form), for S = b m' + (1-b) g.
-__global__ void __launch_bounds__(256) whiten_rows_kernel(MatPack pack) {
-  __shared__ double wave_part[4];
+__global__ void __launch_bounds__(kRowThreads) whiten_rows_kernel(MatPack pack) {
+  __shared__ double wave_part[kRowsPerPart];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
   const int blk = blockIdx.x - J.blk0;
@@ -105,9 +124,8 @@ __global__ void __launch_bounds__(256) whiten_rows_kernel(MatPack pack) {
   const bool vec = d.grad_dtype == SMX_F32 && d.cols % 4 == 0 && aligned16(d.grad) && aligned16(d.momentum) &&
                    aligned16(d.inv_col) && (!r1 || aligned16(d.z));
   double part = 0.0;
-  for (int rr = wave; rr < kRowsPerPart; rr += 4) {
-    const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + rr;
-    if (i >= d.rows) break;
+  const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + wave;
+  if (i < d.rows) {
     float y2 = 0.f, yz = 0.f;
     float *mrow = d.momentum + i * d.cols;
     if (vec) {
@@ -145,12 +163,11 @@ __global__ void __launch_bounds__(256) whiten_rows_kernel(MatPack pack) {
     const double u = b * YZ;
     if (lane == 0) {
       J.u[i] = static_cast<float>(u);
-      part += b * b * Y2 + corr * u * u;
+      part = b * b * Y2 + corr * u * u;
     }
   }
-  if (lane == 0) wave_part[wave] = part;
-  __syncthreads();
-  if (threadIdx.x == 0) J.part[blk] = (wave_part[0] + wave_part[1]) + (wave_part[2] + wave_part[3]);
+  const double t = sum_wave_parts(part, wave_part);
+  if (threadIdx.x == 0) J.part[blk] = t;
 }
 
 // block = 256 threads, one 64x64 tile of the padded parameter layout:
@@ -222,8 +239,8 @@ __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
 // ------------------------------------------------------------ mapback ---
 // u_i = sum_j Q_ij z_j and ||U_i||^2 in closed form:
 // b_i^2 (sum (a Q)^2 + 2 kappa u_i sum (a Q)(a z) + kappa^2 u_i^2 sum (a z)^2).
-__global__ void __launch_bounds__(256) mapback_rows_kernel(MatPack pack) {
-  __shared__ double wave_part[4];
+__global__ void __launch_bounds__(kRowThreads) mapback_rows_kernel(MatPack pack) {
+  __shared__ double wave_part[kRowsPerPart];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
   const int blk = blockIdx.x - J.blk0;
@@ -233,9 +250,8 @@ __global__ void __launch_bounds__(256) mapback_rows_kernel(MatPack pack) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bool vec = d.cols % 4 == 0 && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
   double part = 0.0;
-  for (int rr = wave; rr < kRowsPerPart; rr += 4) {
-    const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + rr;
-    if (i >= d.rows) break;
+  const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + wave;
+  if (i < d.rows) {
     const float *q = J.pl + i * J.pcol_pad;
     float su = 0.f, sa = 0.f, sb = 0.f;
     if (vec) {
@@ -268,17 +284,16 @@ __global__ void __launch_bounds__(256) mapback_rows_kernel(MatPack pack) {
     if (lane == 0) {
       const double b = d.inv_row[i];
       J.u[i] = static_cast<float>(U);
-      part += b * b * (A + 2.0 * kappa * U * B + kappa * kappa * U * U * cz);
+      part = b * b * (A + 2.0 * kappa * U * B + kappa * kappa * U * U * cz);
     }
   }
-  if (lane == 0) wave_part[wave] = part;
-  __syncthreads();
-  if (threadIdx.x == 0) J.part[blk] = (wave_part[0] + wave_part[1]) + (wave_part[2] + wave_part[3]);
+  const double t = sum_wave_parts(part, wave_part);
+  if (threadIdx.x == 0) J.part[blk] = t;
 }
 
 // W -= lr * sqrt(rows) / max(||U||_F, FLT_MIN) * U over kRowsPerPart rows
 // (one wave per row).
-__global__ void __launch_bounds__(256) mapback_apply_kernel(MatPack pack) {
+__global__ void __launch_bounds__(kRowThreads) mapback_apply_kernel(MatPack pack) {
   __shared__ double bcast;
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
@@ -301,9 +316,8 @@ __global__ void __launch_bounds__(256) mapback_apply_kernel(MatPack pack) {
   const float kappa = r1 ? d.kappa[0] : 0.f;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bool vec = d.cols % 4 == 0 && aligned16(d.param) && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
-  for (int rr = wave; rr < kRowsPerPart; rr += 4) {
-    const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + rr;
-    if (i >= d.rows) break;
+  const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + wave;
+  if (i < d.rows) {
     const float *q = J.pl + i * J.pcol_pad;
     float *w = d.param + i * d.cols;
     const float b = d.inv_row[i];
@@ -384,19 +398,21 @@ static size_t group_bytes(const int64_t *rows, const int64_t *cols, const std::v
 
 template <typename KernelFn>
 static int launch_jobs(std::vector<MatJob> &jobs, int64_t (*blocks_of)(const MatJob &), KernelFn kernel,
-                       const char *what, hipStream_t st) {
+                       int threads, const char *what, hipStream_t st) {
   for (size_t b = 0; b < jobs.size(); b += kMatBatch) {
     MatPack pack{};
     pack.n = static_cast<int32_t>(std::min<size_t>(kMatBatch, jobs.size() - b));
     int64_t total = 0;
+    for (int k = 0; k < kMatBatch; ++k) pack.start[k] = INT32_MAX;
     for (int k = 0; k < pack.n; ++k) {
       pack.j[k] = jobs[b + k];
       pack.j[k].blk0 = static_cast<int32_t>(total);
+      pack.start[k] = static_cast<int32_t>(total);
       total += blocks_of(pack.j[k]);
     }
     pack.total_blocks = static_cast<int32_t>(total);
     if (total == 0) continue;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(total)), dim3(256), 0, st, pack);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(total)), dim3(threads), 0, st, pack);
     const int rc = check_launch(what);
     if (rc) return rc;
   }
@@ -477,12 +493,12 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
       j.planes = 0;
       fin[k] = j;
     }
-    int rc = launch_jobs(ping, one_block, matrix_consts_kernel, "matrix_consts", st);
-    if (!rc) rc = launch_jobs(ping, row_blocks, whiten_rows_kernel, "whiten_rows", st);
-    if (!rc) rc = launch_jobs(ping, tile_blocks, whiten_tiles_kernel, "whiten_tiles", st);
+    int rc = launch_jobs(ping, one_block, matrix_consts_kernel, 256, "matrix_consts", st);
+    if (!rc) rc = launch_jobs(ping, row_blocks, whiten_rows_kernel, kRowThreads, "whiten_rows", st);
+    if (!rc) rc = launch_jobs(ping, tile_blocks, whiten_tiles_kernel, 256, "whiten_tiles", st);
     if (!rc) rc = run_s8_stages(plan.layout, st);
-    if (!rc) rc = launch_jobs(fin, row_blocks, mapback_rows_kernel, "mapback_rows", st);
-    if (!rc) rc = launch_jobs(fin, row_blocks, mapback_apply_kernel, "mapback_apply", st);
+    if (!rc) rc = launch_jobs(fin, row_blocks, mapback_rows_kernel, kRowThreads, "mapback_rows", st);
+    if (!rc) rc = launch_jobs(fin, row_blocks, mapback_apply_kernel, kRowThreads, "mapback_apply", st);
     if (rc) return rc;
   }
   return SMX_OK;

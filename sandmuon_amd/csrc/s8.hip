@@ -658,7 +658,7 @@ __global__ void __launch_bounds__(256) s8_poly1_kernel(StageArgs args) {
 // ------------------------------------------------------------- host ---
 // Optional per-launch event timing (smx_s8_timing).
 struct LaunchTiming {
-  bool on = false;
+  int level = 0;  // 0 off, 1 every launch and every run, 2 runs only
   std::vector<hipEvent_t> start, stop;
   std::vector<int32_t> phase;
   std::vector<double> flops;
@@ -667,10 +667,11 @@ struct LaunchTiming {
 static LaunchTiming g_timing;
 
 // Opens a record (start event on `st`) and returns its index in `slot`
-// (-1 when the recorder is off); timing_end closes it.  Records nest.
-static int timing_begin(hipStream_t st, int &slot) {
+// (-1 when the recorder does not record this kind); timing_end closes it.
+// Records nest.
+static int timing_begin(hipStream_t st, int &slot, bool whole_run) {
   slot = -1;
-  if (!g_timing.on) return SMX_OK;
+  if (g_timing.level == 0 || (g_timing.level == 2 && !whole_run)) return SMX_OK;
   if (g_timing.used == g_timing.start.size()) {
     hipEvent_t a, b;
     if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)
@@ -751,7 +752,7 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
   if (off == 0) return SMX_OK;
   const bool comp = Lay.mode == SMX_S8_COMP_BF16;
   int slot = -1;
-  int rc = timing_begin(st, slot);
+  int rc = timing_begin(st, slot, false);
   if (rc) return rc;
   if constexpr (PHASE == kPoly1) {
     if (comp)
@@ -775,7 +776,7 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
 // fill the remaining CUs).  The launch recorder gets one record for the run.
 int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
   int slot = -1;
-  int rc = timing_begin(st, slot);
+  int rc = timing_begin(st, slot, true);
   if (rc) return rc;
   double flops = 0.0;
   for (int stage = 1; stage <= 5; ++stage) {
@@ -857,8 +858,9 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
 using smx::g_timing;
 
 extern "C" int smx_s8_timing(int32_t enable) {
-  g_timing.on = enable != 0;
-  if (g_timing.on) g_timing.used = 0;
+  SMX_REQUIRE(enable >= 0 && enable <= 2, SMX_EINVAL, "s8 timing: enable must be 0, 1 or 2");
+  g_timing.level = enable;
+  if (enable) g_timing.used = 0;
   return SMX_OK;
 }
 

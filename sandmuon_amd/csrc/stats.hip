@@ -93,7 +93,9 @@ stats_accumulate_kernel(const void *__restrict__ x, int64_t rows, int64_t cols,
   for (int k = 0; k < VEC; ++k) { acc_sq[k] = 0.f; acc_first[k] = 0.f; }
 
   if (active) {
-    constexpr int U = 4;
+    // Loads in flight per thread: 2 for the narrow tiles (measured 8% faster
+    // on 768-wide bf16 inputs), 4 otherwise.
+    constexpr int U = CT == 16 ? 2 : 4;
     int64_t r = r_begin + group;
     for (; r + (U - 1) * GROUPS < r_end; r += U * GROUPS) {
       float v[U][VEC];

@@ -108,5 +108,8 @@ def test_s8_timing_recorder_without_launches():
     lib = _native.lib()
     assert lib.smx_s8_timing(1) == 0
     assert _native.s8_timing_read(16) == []
+    assert lib.smx_s8_timing(2) == 0
+    assert _native.s8_timing_read(16) == []
     assert lib.smx_s8_timing(0) == 0
+    assert lib.smx_s8_timing(3) == -1
     assert lib.smx_s8_timing_read(None, None, None, -1) == -1

@@ -92,3 +92,23 @@ def test_s8_launch_timing_records_every_phase(device, mode):
     fl = [f for _, _, f in rec]
     assert fl[:4] == [gram, square1, 0.0, apply]
     assert fl[4:7] == [gram, square1 + one_hot, apply]
+
+
+@pytest.mark.gpu
+def test_s8_timing_runs_only_records_one_span_per_run(device):
+    from sandmuon_amd import _native
+    x = torch.randn(2, 200, 260, device=device)
+    _native.s8_timing(True)
+    _s8_fp32(x, mode="comp_bf16")
+    _native.s8_timing(False)
+    full = _native.s8_timing_read()
+    _native.s8_timing(True, runs_only=True)
+    try:
+        _s8_fp32(x, mode="comp_bf16")
+        _s8_fp32(x, mode="comp_bf16")
+    finally:
+        _native.s8_timing(False)
+    rec = _native.s8_timing_read()
+    assert [p for _, p, _ in rec] == ["run", "run"]
+    assert all(ms > 0 for ms, _, _ in rec)
+    assert rec[0][2] == rec[1][2] == full[0][2]
