@@ -8,14 +8,14 @@
 //            W -= lr * sqrt(rows) * U / max(||U||_F, FLT_MIN)
 //
 // In parameter layout the A factor always acts on columns (input channels)
-// and B on rows, whichever orientation the S8 map uses; the oriented copies
-// X (r x c, r <= c) and X^T are written by the whiten tile pass.
+// and B on rows, whichever orientation the S8 map uses; the whiten tile
+// pass writes the oriented iterate X (r x c, r <= c).
 //
 // whiten_rows  one pass per row: momentum update, u_i = b_i sum_j S_ij a_j z_j
 //              and the row's ||V_i||^2 in closed form
 //              (||V_i||^2 = b_i^2 sum_j (S_ij a_j)^2 + (2 kappa + kappa^2 |z|^2) u_i^2).
-// whiten_tiles 64x64 tiles: V from (g, m', u), stored to the parameter-layout
-//              buffer and, transposed through LDS, to the other buffer.
+// whiten_tiles 64x64 tiles: V from (g, m', u), stored to X directly, or
+//              transposed through LDS for a transposed parameter.
 // mapback_rows u_i = sum_j Q_ij z_j and ||U_i||^2 in closed form.
 // mapback_apply W -= lr * scale * U.
 #include "s8.h"
@@ -32,7 +32,7 @@ namespace smx {
 struct MatJob {
   smx_matrix_desc d;
   float *pl;         // parameter-layout buffer [prow_pad][pcol_pad]
-  float *tl;         // transposed buffer [pcol_pad][prow_pad] (whiten)
+  float *tl;         // transposed buffer [pcol_pad][prow_pad] (whiten of a transposed parameter)
   float *u;          // [rows] rank-one row coefficients
   double *part;      // [ceil(rows/kRowsPerPart)] partial sums
   double *cst;       // [2]: sum z^2, sum (a z)^2 (matrix_consts_kernel)
@@ -171,8 +171,9 @@ __global__ void __launch_bounds__(kRowThreads) whiten_rows_kernel(MatPack pack) 
 }
 
 // block = 256 threads, one 64x64 tile of the padded parameter layout:
-// V = b_i S_ij a_j + kappa u_i z_j, stored to the parameter-layout buffer and,
-// transposed through LDS, to the other buffer (operand form).
+// V = b_i S_ij a_j + kappa u_i z_j, stored in operand form to the oriented
+// iterate: directly (pl), or transposed through LDS for a transposed
+// parameter (tl).
 __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
   __shared__ float tile[64][65];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
@@ -225,8 +226,9 @@ __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) tile[lr][lc + e] = v[e];
-    put_operand4(J.pl, i * J.pcol_pad + j, v, J.planes != 0);
+    if (J.pl) put_operand4(J.pl, i * J.pcol_pad + j, v, J.planes != 0);
   }
+  if (!J.tl) return;  // uniform per block
   __syncthreads();
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -481,13 +483,14 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
       j.u = M.u();
       j.prow_pad = M.prow_pad();
       j.pcol_pad = M.pcol_pad();
-      j.pl = M.flip() ? M.xt0() : M.x0();
-      j.tl = M.flip() ? M.x0() : M.xt0();
+      // The oriented iterate x0 is the parameter layout, or its transpose.
+      j.pl = M.flip() ? nullptr : M.x0();
+      j.tl = M.flip() ? M.x0() : nullptr;
       j.part = M.fro();
       j.cst = M.cst();
       j.planes = mode == SMX_S8_COMP_BF16;
       ping[k] = j;
-      j.pl = M.flip() ? M.xt1() : M.x1();
+      j.pl = M.result();
       j.tl = nullptr;
       j.part = M.mb();
       j.planes = 0;

@@ -31,11 +31,12 @@ struct S8Class {
   int32_t tiles_n;     // cp / kTile
   int32_t parts;       // partial slots per matrix: ceil(cp / kRowsPerPart)
   int32_t pad_;
-  // Iterate buffers (4 bytes per element).  In SMX_S8_FP32 mode they hold
-  // FP32; in SMX_S8_COMP_BF16 mode interleaved BF16 hi/lo (put_operand),
-  // except the stage-5 result, which is FP32.
-  float *x0, *xt0;     // [count][rp][cp], [count][cp][rp]  (ping)
-  float *x1, *xt1;     // pong; after stage 5 the result is in x1/xt1
+  // Iterate buffers (4 bytes per element), oriented layout only.  In
+  // SMX_S8_FP32 mode they hold FP32; in SMX_S8_COMP_BF16 mode interleaved
+  // BF16 hi/lo (put_operand), except the stage-5 result, which is FP32.
+  float *x0, *x1;      // [count][rp][cp] ping, pong
+  float *xf;           // [n_flip][cp][rp] stage-5 result of transposed parameters
+                       // (parameter layout); the others end in x1
   float *g;            // [count][rp][rp] Gram (FP32, or planes in comp mode)
   float *p;            // [count][rp][rp] stage 1: FP32 G2; later: P (planes in comp mode)
   float *u;            // [count][cp] per param-row rank-one coefficient
@@ -60,9 +61,11 @@ struct S8Mat {
   __host__ __device__ const S8Class *kp() const { return &k_; }
   __host__ __device__ bool flip() const { return slot < kp()->n_flip; }
   __host__ __device__ float *x0() const { return kp()->x0 + slot * kp()->rp * kp()->cp; }
-  __host__ __device__ float *xt0() const { return kp()->xt0 + slot * kp()->rp * kp()->cp; }
   __host__ __device__ float *x1() const { return kp()->x1 + slot * kp()->rp * kp()->cp; }
-  __host__ __device__ float *xt1() const { return kp()->xt1 + slot * kp()->rp * kp()->cp; }
+  // Valid for flip() only.
+  __host__ __device__ float *xf() const { return kp()->xf + slot * kp()->rp * kp()->cp; }
+  // The stage-5 result in parameter layout [prow_pad][pcol_pad].
+  __host__ __device__ float *result() const { return flip() ? xf() : x1(); }
   __host__ __device__ float *g() const { return kp()->g + slot * kp()->rp * kp()->rp; }
   __host__ __device__ float *p() const { return kp()->p + slot * kp()->rp * kp()->rp; }
   __host__ __device__ float *u() const { return kp()->u + slot * kp()->cp; }
@@ -70,8 +73,8 @@ struct S8Mat {
   __host__ __device__ double *mb() const { return kp()->mb + static_cast<int64_t>(slot) * kp()->parts; }
   __host__ __device__ double *sch() const { return kp()->sch + slot * sym_tiles(kp()->tiles_m); }
   __host__ __device__ double *cst() const { return kp()->cst + 2 * static_cast<int64_t>(slot); }
-  // Parameter layout: rows x cols; the parameter-layout buffer of the
-  // ping side is xt0 for transposed parameters and x0 otherwise.
+  // Parameter layout: rows x cols (the transpose of the oriented layout
+  // for transposed parameters).
   __host__ __device__ int64_t prow() const { return flip() ? kp()->c : kp()->r; }
   __host__ __device__ int64_t pcol() const { return flip() ? kp()->r : kp()->c; }
   __host__ __device__ int64_t prow_pad() const { return flip() ? kp()->cp : kp()->rp; }
@@ -146,8 +149,8 @@ struct S8Plan {
 bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, int mode,
              char *base, S8Plan &plan, int32_t *cls_of, int32_t *slot_of);
 
-// Run the five S8 stages on a planned layout whose x0/xt0 (and fro
-// partials) are filled.  The result is in x1/xt1.
+// Run the five S8 stages on a planned layout whose x0 (and fro partials)
+// are filled.  The result of each matrix is in S8Mat::result().
 int run_s8_stages(const S8Layout &layout, hipStream_t st);
 
 }  // namespace smx

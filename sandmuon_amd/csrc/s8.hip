@@ -1,7 +1,7 @@
 // S8 polar map on gfx950 MFMA: sandmuon/optimizer.py:69-93 with the
 // constants of sandmuon/coefficients.py:3-11.
 //
-// Per matrix (oriented r <= c, unnormalised whitened input V in x0/xt0 and
+// Per matrix (oriented r <= c, unnormalised whitened input V in x0 and
 // its squared Frobenius norm as partials in `fro`) and stage k = 1..5:
 //   GRAM    G  = X X^T                 (stage 1: times 1/||V||^2)
 //   SQUARE  stage 1: G2 = G G  -> p buffer, plus Schatten-8 partials
@@ -9,13 +9,15 @@
 //   POLY1   stage 1 only: P1 = a I + b G/s^2 + c G2/s^4 -> p buffer,
 //           s = max(1.35 ||G2||_F^(1/4), 1e-30) (elementwise kernel)
 //   APPLY   stage 1: X' = P1 V / (||V|| s);  stage k: X' = P X
-// Every product is C = A B^T with A, B row-major and K contiguous: the
-// Gram uses X twice, the square uses the symmetric G twice, the apply uses
-// P and X^T.  The apply epilogue therefore writes the new iterate in both
-// layouts (X and X^T).  Gram and square only compute upper-triangle tiles
-// and store each off-diagonal tile twice (tile and mirror).  The (b/c) G
-// term of the square is accumulated by extra MFMAs from the B fragments
-// (one_hot), so no epilogue reads G.
+// The Gram (C = X X^T) and the square (C = G G, G symmetric) read both
+// operands as row-major K-contiguous rows.  The apply (C = P X) reads P the
+// same way and X itself as a K-major operand: its LDS tile holds 16 rows of
+// X and the MFMA fragments are gathered with the 16-bit transposed LDS read
+// (ds_read_b64_tr_b16), so the iterate is only ever stored in one layout.
+// Gram and square only compute upper-triangle tiles and store each
+// off-diagonal tile twice (tile and mirror).  The (b/c) G term of the square
+// is accumulated by extra MFMAs from the B fragments (one_hot), so no
+// epilogue reads G.
 //
 // Arithmetic modes:
 //   SMX_S8_FP32       v_mfma_f32_32x32x2_f32 on FP32 operands.
@@ -28,10 +30,11 @@
 //
 // Block: 256x256 output tile, 4 waves (2 x 2, one per SIMD), each wave
 // 128x128 (4 x 4 MFMA 32x32 tiles, 256 AGPR accumulators).  Operands stream
-// into a 4-stage LDS ring (K = 16 per stage, 32 KB; 64 contiguous bytes
-// per row and operand in both modes) with direct-to-LDS 16-byte loads
-// issued three stages ahead.  The epilogue stages each 32x32 accumulator
-// block through LDS in both orientations and writes row vectors.
+// into a 4-stage LDS ring (K = 16 per stage, 32 KB) with direct-to-LDS
+// 16-byte loads issued three stages ahead.  The epilogue stages each 32x32
+// accumulator block through LDS and writes row vectors (the transposed
+// orientation too for Gram/square mirror tiles and for the stage-5 result
+// of a transposed parameter).
 #include "s8.h"
 
 #include <algorithm>
@@ -81,6 +84,9 @@ struct Opnd {
 // 64-bank LDS.
 __device__ __forceinline__ int swz4(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 __device__ __forceinline__ int f32_off(int r, int kc) { return (r * 4 + (kc ^ swz4(r))) << 4; }
+// Chunk swizzle of the K-major operand tile (apply's B): an even value
+// 0..14 from bits 0, 1 and 3 of the K row.
+__device__ __forceinline__ int swzk(int k) { return ((k & 3) | ((k >> 1) & 4)) << 1; }
 
 // One 16-byte direct-to-LDS load per lane from sbase + voff (scalar base,
 // per-lane 32-bit byte offset): lane l writes LDS[m0 + 16 l].  Issued from
@@ -114,6 +120,21 @@ __device__ __forceinline__ TileOffsets tile_offsets(int64_t ld, int64_t row0, in
   return t;
 }
 
+// K-major tile (rows k = 4 wave + i, N columns n0 .. n0 + 255 of a
+// row-major operand with rows of `ld` elements): lane l of load i fills
+// slot l of row k with logical chunk l ^ swzk(k).  A stage at K offset k0
+// moves the scalar base by 4*k0*ld bytes.
+__device__ __forceinline__ TileOffsets tile_offsets_km(int64_t ld, int64_t n0, int wave) {
+  const int lane = threadIdx.x & 63;
+  TileOffsets t;
+#pragma unroll
+  for (int i = 0; i < kChunksPerWave; ++i) {
+    const int k = wave * kChunksPerWave + i;
+    t.v[i] = static_cast<uint32_t>((k * ld + n0) * 4 + ((lane ^ swzk(k)) << 4));
+  }
+  return t;
+}
+
 __device__ __forceinline__ void dma_tile(const TileOffsets &t, const char *sbase, uint32_t lds) {
 #pragma unroll
   for (int i = 0; i < kChunksPerWave; ++i) dma16(t.v[i], sbase, lds + i * 1024);
@@ -141,6 +162,26 @@ __device__ __forceinline__ void read8(const char *tile, int r, int h, float (&v)
 // Chunk kc of row r as 8 BF16 values.
 __device__ __forceinline__ bf16x8 read_b16(const char *tile, int r, int kc) {
   return *reinterpret_cast<const bf16x8 *>(tile + f32_off(r, kc));
+}
+
+// ------------------------------------------- K-major operand tile (apply) ---
+// [16 K rows][256 N columns] of a row-major operand (the iterate X), one
+// 1 KB row per K: 64 chunks of 16 bytes, logical chunk c at slot c ^ swzk(k).
+// Logical chunks follow the global bytes: interleaved BF16 4 G + 2 plane +
+// half (16-column group G, plane 0 hi / 1 lo, columns 8 half .. 8 half + 7
+// of the group); FP32 n / 4.  The swizzle spreads the 8 K rows one
+// transposed read touches over distinct bank groups (swzk, defined with the
+// row-major swizzle).
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane 4a + b receives
+// element b of the 4-element (8-byte) reads addressed by lanes a, a + 4,
+// a + 8 and a + 12, in that order.
+__device__ __forceinline__ i16x4 read_tr16(const char *p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(const_cast<char *>(p)));
 }
 
 // ----------------------------------------------------------- compute ---
@@ -203,6 +244,53 @@ __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) 
   }
 }
 
+// The four B column blocks of one stage from a K-major tile (apply).  Lane
+// (n, h) needs B[k = 8h .. 8h+7][n].  Interleaved BF16: per plane, two
+// transposed reads of 4 K rows each; lane s of a 16-lane group g addresses
+// row 8 (g >> 1) + 4 r + (s >> 2), columns 16 (g & 1) + 4 (s & 3) .. + 3 of
+// the 32-column block, so lane 16 (g & 1) + s of the block receives its
+// column at the 4 rows.  FP32: eight 4-byte reads.
+template <int MODE>
+__device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &f) {
+  const int lane = threadIdx.x & 63;
+  const char *bt = st + kOpTile;
+  if constexpr (MODE == SMX_S8_COMP_BF16) {
+    const int g = lane >> 4, s = lane & 15;
+    const int k = 8 * (g >> 1) + (s >> 2);
+    const int sw = swzk(k);  // the same for rows k and k + 4
+    const char *row = bt + k * 1024 + 8 * (s & 1);
+#pragma unroll
+    for (int j = 0; j < kSubN; ++j) {
+      const int grp = 8 * wn + 2 * j + (g & 1);
+#pragma unroll
+      for (int pl = 0; pl < 2; ++pl) {
+        const char *p = row + (((4 * grp + 2 * pl + ((s >> 1) & 1)) ^ sw) << 4);
+        const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * 1024);
+        const bf16x8 v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        if (pl == 0) f.h[j] = v;
+        else f.l[j] = v;
+      }
+    }
+  } else {
+    const int h = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < kSubN; ++j) {
+      const int n = wn * (32 * kSubN) + j * 32 + (lane & 31);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int k = 8 * h + q;
+        f.v[j][q] = *reinterpret_cast<const float *>(bt + k * 1024 + (((n >> 2) ^ swzk(k)) << 4) + (n & 3) * 4);
+      }
+    }
+  }
+}
+
+template <int MODE, bool BKM>
+__device__ __forceinline__ void load_b_any(const char *st, int wn, BFrags<MODE> &f) {
+  if constexpr (BKM) load_b_km<MODE>(st, wn, f);
+  else load_b<MODE>(st, wn, f);
+}
+
 // MFMAs of row block i: acc[i][j] += A_i B_j^T over the stage's 16 K.
 template <int MODE>
 __device__ __forceinline__ void mma_row(const AFrag<MODE> &a, const BFrags<MODE> &b, f32x16 (&acc)[kSubN]) {
@@ -253,11 +341,13 @@ __device__ __forceinline__ AFrag<MODE> one_hot(float s, int r0) {
 }
 
 // Issues one stage (A and B tiles) into a ring slot.  `lds` is the slot's
-// LDS byte address plus this wave's first chunk (wave-uniform).
+// LDS byte address plus this wave's first chunk (wave-uniform).  BKM: B is
+// K-major (its stage is 16 rows further down).
+template <bool BKM>
 __device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const TileOffsets &oa,
                                             const TileOffsets &ob, int64_t k0, uint32_t lds) {
   dma_tile(oa, static_cast<const char *>(A.p) + 4 * k0, lds);
-  dma_tile(ob, static_cast<const char *>(B.p) + 4 * k0, lds + kOpTile);
+  dma_tile(ob, static_cast<const char *>(B.p) + 4 * k0 * (BKM ? B.ld : 1), lds + kOpTile);
 }
 
 // Waits until at most `pending` stages of this wave's loads are in flight
@@ -293,7 +383,7 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 // (rows 16 SEL .. 16 SEL + 15 of the wave, accumulator block SEL / 2).
 // STEADY: kt + kStages < nk, so a next stage exists, the refill is due and
 // kStages - 2 stages may stay in flight (no run-time conditions).
-template <int MODE, int SEL, int PAR, bool STEADY>
+template <int MODE, int SEL, int PAR, bool STEADY, bool BKM>
 __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const TileOffsets &oa, const TileOffsets &ob,
                                           uint32_t lds0, float sel_s, char *smem, int kt, int nk, int wm, int wn,
                                           AFrag<MODE> (&af)[kSubM], BFrags<MODE> (&bf)[2],
@@ -308,9 +398,9 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Ti
   wait_lds();
   block_barrier();
   if (STEADY || kt + S < nk)
-    issue_stage(A, B, oa, ob, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * kStageBytes);
+    issue_stage<BKM>(A, B, oa, ob, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * kStageBytes);
   const char *nxt = smem + ((kt + 1) % S) * kStageBytes;
-  if (more) load_b<MODE>(nxt, wn, bf[PAR ^ 1]);
+  if (more) load_b_any<MODE, BKM>(nxt, wn, bf[PAR ^ 1]);
 #pragma unroll
   for (int i = 0; i < kSubM; ++i) {
     mma_row<MODE>(af[i], bf[PAR], acc[i]);
@@ -320,8 +410,9 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Ti
 }
 
 // ACCG: also accumulate sel_s * G over the wave's rows (square phase; A and
-// B are the same symmetric G, K = rows of G).
-template <int MODE, bool ACCG>
+// B are the same symmetric G, K = rows of G).  BKM: B is a K-major
+// row-major operand (C = A B, apply), brow0 its first column.
+template <int MODE, bool ACCG, bool BKM>
 __device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &B, int64_t K, int64_t arow0, int64_t brow0,
                                          float sel_s, char *smem, f32x16 (&acc)[kSubM][kSubN]) {
   static_assert(kSubM == 4 && kBK == 16, "the one_hot window is 8 stages of 16 rows");
@@ -335,21 +426,22 @@ __device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &B, int64_t K
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
   const int nk = static_cast<int>(K / kBK);
-  const TileOffsets oa = tile_offsets(A.ld, arow0, wave), ob = tile_offsets(B.ld, brow0, wave);
+  const TileOffsets oa = tile_offsets(A.ld, arow0, wave);
+  const TileOffsets ob = BKM ? tile_offsets_km(B.ld, brow0, wave) : tile_offsets(B.ld, brow0, wave);
   // LDS byte address of the ring plus this wave's first chunk.
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * kChunksPerWave * 1024;
 #pragma unroll
   for (int s = 0; s < kStages; ++s)
-    if (s < nk) issue_stage(A, B, oa, ob, static_cast<int64_t>(s) * kBK, lds0 + s * kStageBytes);
+    if (s < nk) issue_stage<BKM>(A, B, oa, ob, static_cast<int64_t>(s) * kBK, lds0 + s * kStageBytes);
   wait_stages(min(kStages - 1, nk - 1));
   block_barrier();
   AFrag<MODE> af[kSubM];
   BFrags<MODE> bf[2];
-  load_b<MODE>(smem, wn, bf[0]);
+  load_b_any<MODE, BKM>(smem, wn, bf[0]);
 #pragma unroll
   for (int i = 0; i < kSubM; ++i) load_a<MODE>(smem, wm, i, af[i]);
 #define SMX_PIPE(SEL, PAR, KT, STEADY) \
-  pipe_iter<MODE, SEL, PAR, STEADY>(A, B, oa, ob, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
+  pipe_iter<MODE, SEL, PAR, STEADY, BKM>(A, B, oa, ob, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
   // Stages [kt, to) in pairs (kt and `to` even): branch-free while a refill
   // is due, then the general form.
   const int steady_end = nk - kStages;
@@ -478,9 +570,7 @@ s8_stage_kernel(StageArgs args) {
   const int stage = args.stage;
   const bool odd = (stage & 1) != 0;
   float *x_in = odd ? M.x0() : M.x1();
-  float *xt_in = odd ? M.xt0() : M.xt1();
   float *x_out = odd ? M.x1() : M.x0();
-  float *xt_out = odd ? M.xt1() : M.xt0();
 
   f32x16 acc[kSubM][kSubN];
   float scale = 1.f;
@@ -490,15 +580,15 @@ s8_stage_kernel(StageArgs args) {
       scale = f > 0.0 ? static_cast<float>(1.0 / f) : 0.f;
     }
     const Opnd X{x_in, K.cp};
-    gemm_256<MODE, false>(X, X, K.cp, tm * kTile, tn * kTile, 0.f, smem, acc);
+    gemm_256<MODE, false, false>(X, X, K.cp, tm * kTile, tn * kTile, 0.f, smem, acc);
   } else if constexpr (PHASE == kSquare) {
     const Opnd G{M.g(), K.rp};
     if (stage == 1) {
-      gemm_256<MODE, false>(G, G, K.rp, tm * kTile, tn * kTile, 0.f, smem, acc);
+      gemm_256<MODE, false, false>(G, G, K.rp, tm * kTile, tn * kTile, 0.f, smem, acc);
     } else {
       // acc = G G + (b/c) G; the epilogue forms P = c acc + a I.
       scale = args.c;
-      gemm_256<MODE, true>(G, G, K.rp, tm * kTile, tn * kTile, args.b_over_c, smem, acc);
+      gemm_256<MODE, true, false>(G, G, K.rp, tm * kTile, tn * kTile, args.b_over_c, smem, acc);
     }
   } else {
     if (stage == 1) {
@@ -506,7 +596,8 @@ s8_stage_kernel(StageArgs args) {
       const Stage1Scalars sc = stage1_scalars(M, &bcast);
       scale = sc.ok ? static_cast<float>(1.0 / (sqrt(sc.fro2) * static_cast<double>(sc.s))) : 0.f;
     }
-    gemm_256<MODE, false>(Opnd{M.p(), K.rp}, Opnd{xt_in, K.rp}, K.rp, tm * kTile, tn * kTile, 0.f, smem, acc);
+    // X' = P X: B = X rows k (K-major), columns of the tile.
+    gemm_256<MODE, false, true>(Opnd{M.p(), K.rp}, Opnd{x_in, K.cp}, K.rp, tm * kTile, tn * kTile, 0.f, smem, acc);
   }
 
   // ------------------------------------------------------- epilogue ---
@@ -515,7 +606,7 @@ s8_stage_kernel(StageArgs args) {
   // transpose are written as row vectors of 8 elements per lane.
   //   GRAM    tile -> G, transpose -> G (off-diagonal tiles)
   //   SQUARE  stage 1: G2 (FP32) -> p; stage k: P = c acc + a I -> p
-  //   APPLY   tile -> X', transpose -> X'^T (stage 5: parameter layout only)
+  //   APPLY   tile -> X' (stage 5, transposed parameter: transpose -> xf)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
@@ -526,11 +617,13 @@ s8_stage_kernel(StageArgs args) {
   int64_t ld_t, ld_m;
   bool pl_t, pl_m, do_t, do_m;
   if constexpr (PHASE == kApply) {
+    const bool xf = last && M.flip();
     dst_t = x_out; ld_t = K.cp;
-    dst_m = xt_out; ld_m = K.rp;
-    pl_t = pl_m = PL && !last;
-    do_t = !last || !M.flip();
-    do_m = !last || M.flip();
+    dst_m = xf ? M.xf() : nullptr; ld_m = K.rp;
+    pl_t = PL && !last;
+    pl_m = false;
+    do_t = !xf;
+    do_m = xf;
   } else {
     dst_t = dst_m = PHASE == kGram ? M.g() : M.p();
     ld_t = ld_m = K.rp;
@@ -559,7 +652,7 @@ s8_stage_kernel(StageArgs args) {
         if constexpr (PHASE == kSquare) sq_local = fmaf(v[q], v[q], sq_local);  // used in stage 1
         T[(8 * k + 4 * lh + q) * kEpStride + lr] = v[q];
       }
-      *reinterpret_cast<f32x4 *>(U + lr * kEpStride + 8 * k + 4 * lh) = v;
+      if (do_m) *reinterpret_cast<f32x4 *>(U + lr * kEpStride + 8 * k + 4 * lh) = v;
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -838,9 +931,8 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     const size_t xs = static_cast<size_t>(C.count) * C.rp * C.cp * sizeof(float);
     const size_t gs = static_cast<size_t>(C.count) * C.rp * C.rp * sizeof(float);
     C.x0 = reinterpret_cast<float *>(take(xs));
-    C.xt0 = reinterpret_cast<float *>(take(xs));
     C.x1 = reinterpret_cast<float *>(take(xs));
-    C.xt1 = reinterpret_cast<float *>(take(xs));
+    C.xf = reinterpret_cast<float *>(take(static_cast<size_t>(C.n_flip) * C.rp * C.cp * sizeof(float)));
     C.g = reinterpret_cast<float *>(take(gs));
     C.p = reinterpret_cast<float *>(take(gs));
     C.u = reinterpret_cast<float *>(take(static_cast<size_t>(C.count) * C.cp * sizeof(float)));

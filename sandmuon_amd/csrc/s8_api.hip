@@ -37,14 +37,14 @@ __global__ void __launch_bounds__(256) s8_load_rows_kernel(S8IoArgs a) {
 }
 
 // Tile pass: 64x64 tiles of the padded parameter layout (input layout)
-// into the parameter-layout buffer and, transposed, the other buffer.
-// grid = (tiles, batch), block 256.
+// into the oriented iterate x0: directly, or transposed through LDS for
+// transposed parameters.  grid = (tiles, batch), block 256.
 __global__ void __launch_bounds__(256) s8_load_tiles_kernel(S8IoArgs a) {
   __shared__ float tile[64][65];
   const S8Mat M{a.k, static_cast<int32_t>(blockIdx.y)};
   const float *x = a.x + static_cast<int64_t>(blockIdx.y) * a.sb;
-  float *pl = M.flip() ? M.xt0() : M.x0();
-  float *tl = M.flip() ? M.x0() : M.xt0();
+  float *pl = M.flip() ? nullptr : M.x0();
+  float *tl = M.flip() ? M.x0() : nullptr;
   const int64_t ppad = M.pcol_pad(), rpad = M.prow_pad();
   const int64_t tiles_c = ppad / 64;
   const int64_t i0 = (blockIdx.x / tiles_c) * 64, j0 = (blockIdx.x % tiles_c) * 64;
@@ -60,8 +60,9 @@ __global__ void __launch_bounds__(256) s8_load_tiles_kernel(S8IoArgs a) {
       v[e] = (i < a.rows && j < a.cols) ? x[i * a.sr + j * a.sc] : 0.f;
       tile[lr][lc + e] = v[e];
     }
-    put_operand4(pl, i * ppad + j0 + lc, v, a.planes != 0);
+    if (pl) put_operand4(pl, i * ppad + j0 + lc, v, a.planes != 0);
   }
+  if (!tl) return;  // uniform per block
   __syncthreads();
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -71,11 +72,11 @@ __global__ void __launch_bounds__(256) s8_load_tiles_kernel(S8IoArgs a) {
   }
 }
 
-// Store: final iterate (parameter-layout side of x1/xt1) -> out (strided).
+// Store: final iterate (parameter layout) -> out (strided).
 // grid = (ceil(rows*cols / 256), batch).
 __global__ void __launch_bounds__(256) s8_store_kernel(S8IoArgs a) {
   const S8Mat M{a.k, static_cast<int32_t>(blockIdx.y)};
-  const float *q = M.flip() ? M.xt1() : M.x1();
+  const float *q = M.result();
   const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (e >= a.rows * a.cols) return;
   const int64_t i = e / a.cols, j = e % a.cols;
