@@ -42,7 +42,7 @@ struct S8Class {
   float *u;            // [count][cp] per param-row rank-one coefficient
   double *fro;         // [count][parts] whiten: partial sum of V^2
   double *mb;          // [count][parts] mapback: partial sum of U^2
-  double *sch;         // [count][tiles_m*(tiles_m+1)/2] Schatten partials
+  double *sch;         // [count][tiles_m*(tiles_m+1)] Schatten partials (two per upper block)
   double *cst;         // [count][2] matrix-step constants: sum z^2, sum (a z)^2
 };
 
@@ -71,7 +71,7 @@ struct S8Mat {
   __host__ __device__ float *u() const { return kp()->u + slot * kp()->cp; }
   __host__ __device__ double *fro() const { return kp()->fro + static_cast<int64_t>(slot) * kp()->parts; }
   __host__ __device__ double *mb() const { return kp()->mb + static_cast<int64_t>(slot) * kp()->parts; }
-  __host__ __device__ double *sch() const { return kp()->sch + slot * sym_tiles(kp()->tiles_m); }
+  __host__ __device__ double *sch() const { return kp()->sch + slot * 2 * sym_tiles(kp()->tiles_m); }
   __host__ __device__ double *cst() const { return kp()->cst + 2 * static_cast<int64_t>(slot); }
   // Parameter layout: rows x cols (the transpose of the oriented layout
   // for transposed parameters).

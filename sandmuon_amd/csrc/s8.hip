@@ -28,13 +28,14 @@
 //                     60-66, applied in all five stages with FP32
 //                     accumulation of every intermediate).
 //
-// Block: 256x256 output tile, 4 waves (2 x 2, one per SIMD), each wave
-// 128x128 (4 x 4 MFMA 32x32 tiles, 256 AGPR accumulators).  Operands stream
-// into a 4-stage LDS ring (K = 16 per stage, 32 KB) with direct-to-LDS
-// 16-byte loads issued three stages ahead.  The epilogue stages each 32x32
-// accumulator block through LDS and writes row vectors (the transposed
-// orientation too for Gram/square mirror tiles and for the stage-5 result
-// of a transposed parameter).
+// Block: 256x128 output tile, 4 waves stacked along M (one per SIMD), each
+// wave 64x128 (2 x 4 MFMA 32x32 tiles, 128 accumulator registers), and two
+// blocks per CU, so one block's epilogue and prologue overlap the other's
+// MFMAs.  Operands stream into a 3-stage LDS ring (K = 16 per stage, 24 KB)
+// with direct-to-LDS 16-byte loads issued two stages ahead.  The epilogue
+// stages each 32x32 accumulator block through LDS and writes row vectors
+// (the transposed orientation too for Gram/square mirror tiles and for the
+// stage-5 result of a transposed parameter).
 #include "s8.h"
 
 #include <algorithm>
@@ -47,15 +48,19 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;     // 4 waves, one per SIMD
+constexpr int kThreads = 256;      // 4 waves, one per SIMD; two blocks per CU
 constexpr int kWaves = kThreads / 64;
-constexpr int kSubM = 4, kSubN = 4; // 32x32 MFMA tiles per wave (128 x 128)
-constexpr int kBK = 16;            // K per pipeline stage
-constexpr int kOpTile = 16384;     // 256 x 16 operand tile (4 bytes per element)
-constexpr int kStages = 4;         // LDS ring depth (3 stages in flight)
-constexpr int kStageBytes = 2 * kOpTile;           // A + B
+constexpr int kTileM = kTile, kTileN = kTile / 2;  // block output tile 256 x 128
+constexpr int kSubM = 2, kSubN = 4; // 32x32 MFMA tiles per wave (64 x 128)
+constexpr int kBK = 16;             // K per pipeline stage
+constexpr int kOpA = kTileM * kBK * 4;  // A operand tile 256 x 16 (4 bytes per element)
+constexpr int kOpB = kTileN * kBK * 4;  // B operand tile 128 x 16
+constexpr int kStages = 3;          // LDS ring depth (2 stages in flight)
+constexpr int kStageBytes = kOpA + kOpB;
 constexpr int kRingBytes = kStages * kStageBytes;
-constexpr int kLoadsPerStage = 2 * (kOpTile / 1024) / kWaves;  // 1 KB loads per wave and stage
+constexpr int kLoadsA = kOpA / 1024 / kWaves, kLoadsB = kOpB / 1024 / kWaves;  // 1 KB loads per wave
+constexpr int kLoadsPerStage = kLoadsA + kLoadsB;
+constexpr int kKmRow = kTileN * 4;  // bytes per K row of the K-major B tile
 
 enum Phase { kGram = 0, kSquare = 1, kApply = 2, kPoly1 = 3, kSpan = 4 };  // kSpan: timing record of a whole S8 run
 
@@ -84,9 +89,13 @@ struct Opnd {
 // 64-bank LDS.
 __device__ __forceinline__ int swz4(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 __device__ __forceinline__ int f32_off(int r, int kc) { return (r * 4 + (kc ^ swz4(r))) << 4; }
-// Chunk swizzle of the K-major operand tile (apply's B): an even value
-// 0..14 from bits 0, 1 and 3 of the K row.
-__device__ __forceinline__ int swzk(int k) { return ((k & 3) | ((k >> 1) & 4)) << 1; }
+// Chunk swizzle of the K-major operand tile (apply's B): 0, 2, 12 or 14
+// from bits 0 and 1 of the K row.  A transposed read takes 4 consecutive K
+// rows per 16 lanes, two chunks of each; the swizzle puts the 16 chunks that
+// 32 consecutive lanes read at distinct positions modulo 16 (and the 8 of
+// 16 lanes at distinct positions modulo 8), so each read is conflict-free
+// for 64 banks serving 32 lanes per cycle and for 32 banks serving 16.
+__device__ __forceinline__ int swzk(int k) { return 2 * (k & 1) + 12 * ((k >> 1) & 1); }
 
 // One 16-byte direct-to-LDS load per lane from sbase + voff (scalar base,
 // per-lane 32-bit byte offset): lane l writes LDS[m0 + 16 l].  Issued from
@@ -99,20 +108,23 @@ __device__ __forceinline__ void dma16(uint32_t voff, const void *sbase, uint32_t
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
 }
 
-// This wave's share of an operand tile (rows row0.., 16 K columns): LDS
-// chunk p = (wave*N+i)*64 + lane is stored slot p&3 of row p>>2.  The
-// per-lane byte offsets at K = 0 are computed once per tile; a stage at K
-// offset k0 only moves the scalar base by 4*k0 bytes.
-constexpr int kChunksPerWave = (kOpTile / 1024) / kWaves;
+// Per-lane byte offsets of this wave's N loads of one operand tile; a
+// stage at K offset k0 only moves the scalar base.
+template <int N>
 struct TileOffsets {
-  uint32_t v[kChunksPerWave];
+  uint32_t v[N];
 };
-__device__ __forceinline__ TileOffsets tile_offsets(int64_t ld, int64_t row0, int wave) {
+
+// Row-major operand tile (rows row0.., 16 K columns): LDS chunk
+// p = (wave*N+i)*64 + lane is stored slot p&3 of row p>>2; the scalar base
+// of a stage at K offset k0 moves by 4*k0 bytes.
+template <int N>
+__device__ __forceinline__ TileOffsets<N> tile_offsets(int64_t ld, int64_t row0, int wave) {
   const int lane = threadIdx.x & 63;
-  TileOffsets t;
+  TileOffsets<N> t;
 #pragma unroll
-  for (int i = 0; i < kChunksPerWave; ++i) {
-    const int p = (wave * kChunksPerWave + i) * 64 + lane;
+  for (int i = 0; i < N; ++i) {
+    const int p = (wave * N + i) * 64 + lane;
     const int row = p >> 2;
     const int kc = (p & 3) ^ swz4(row);
     t.v[i] = static_cast<uint32_t>(((row0 + row) * ld + kc * 4) * 4);
@@ -120,32 +132,35 @@ __device__ __forceinline__ TileOffsets tile_offsets(int64_t ld, int64_t row0, in
   return t;
 }
 
-// K-major tile (rows k = 4 wave + i, N columns n0 .. n0 + 255 of a
-// row-major operand with rows of `ld` elements): lane l of load i fills
-// slot l of row k with logical chunk l ^ swzk(k).  A stage at K offset k0
-// moves the scalar base by 4*k0*ld bytes.
-__device__ __forceinline__ TileOffsets tile_offsets_km(int64_t ld, int64_t n0, int wave) {
+// K-major tile (16 K rows, N columns n0 .. n0 + kTileN - 1 of a row-major
+// operand with rows of `ld` elements; kKmRow bytes per K row): load i
+// covers K rows 2 (wave*N+i) and 2 (wave*N+i) + 1, lane l filling slot
+// l & 31 of its row k with logical chunk (l & 31) ^ swzk(k).  The scalar
+// base of a stage at K offset k0 moves by 4*k0*ld bytes.
+template <int N>
+__device__ __forceinline__ TileOffsets<N> tile_offsets_km(int64_t ld, int64_t n0, int wave) {
+  static_assert(kKmRow == 512, "two K rows per 1 KB load");
   const int lane = threadIdx.x & 63;
-  TileOffsets t;
+  TileOffsets<N> t;
 #pragma unroll
-  for (int i = 0; i < kChunksPerWave; ++i) {
-    const int k = wave * kChunksPerWave + i;
-    t.v[i] = static_cast<uint32_t>((k * ld + n0) * 4 + ((lane ^ swzk(k)) << 4));
+  for (int i = 0; i < N; ++i) {
+    const int k = 2 * (wave * N + i) + (lane >> 5);
+    t.v[i] = static_cast<uint32_t>((k * ld + n0) * 4 + (((lane & 31) ^ swzk(k)) << 4));
   }
   return t;
 }
 
-__device__ __forceinline__ void dma_tile(const TileOffsets &t, const char *sbase, uint32_t lds) {
+template <int N>
+__device__ __forceinline__ void dma_tile(const TileOffsets<N> &t, const char *sbase, uint32_t lds) {
 #pragma unroll
-  for (int i = 0; i < kChunksPerWave; ++i) dma16(t.v[i], sbase, lds + i * 1024);
+  for (int i = 0; i < N; ++i) dma16(t.v[i], sbase, lds + i * 1024);
 }
 
 template <int N>
 __device__ __forceinline__ void wait_vm() {
   if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  else if constexpr (N == 24) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  else if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
   else static_assert(N == 0, "unsupported vmcnt");
 }
 
@@ -165,23 +180,26 @@ __device__ __forceinline__ bf16x8 read_b16(const char *tile, int r, int kc) {
 }
 
 // ------------------------------------------- K-major operand tile (apply) ---
-// [16 K rows][256 N columns] of a row-major operand (the iterate X), one
-// 1 KB row per K: 64 chunks of 16 bytes, logical chunk c at slot c ^ swzk(k).
+// [16 K rows][kTileN N columns] of a row-major operand (the iterate X), one
+// row per K, in chunks of 16 bytes, logical chunk c at slot c ^ swzk(k).
 // Logical chunks follow the global bytes: interleaved BF16 4 G + 2 plane +
 // half (16-column group G, plane 0 hi / 1 lo, columns 8 half .. 8 half + 7
-// of the group); FP32 n / 4.  The swizzle spreads the 8 K rows one
-// transposed read touches over distinct bank groups (swzk, defined with the
-// row-major swizzle).
+// of the group); FP32 n / 4.  (swzk is defined with the row-major swizzle.)
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) char lds_char;
+
+// An LDS pointer of a generic pointer into __shared__ memory; arithmetic on
+// it lets constant offsets fold into the LDS instructions' offset field.
+__device__ __forceinline__ lds_char *to_lds(const char *p) { return (lds_char *)(const_cast<char *>(p)); }
 
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane 4a + b receives
 // element b of the 4-element (8-byte) reads addressed by lanes a, a + 4,
 // a + 8 and a + 12, in that order.
-__device__ __forceinline__ i16x4 read_tr16(const char *p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(const_cast<char *>(p)));
+__device__ __forceinline__ i16x4 read_tr16(lds_char *p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)p);
 }
 
 // ----------------------------------------------------------- compute ---
@@ -231,7 +249,7 @@ template <int MODE>
 __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
-  const char *bt = st + kOpTile;
+  const char *bt = st + kOpA;
 #pragma unroll
   for (int j = 0; j < kSubN; ++j) {
     const int r = wn * (32 * kSubN) + j * 32 + lr;
@@ -250,22 +268,41 @@ __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) 
 // row 8 (g >> 1) + 4 r + (s >> 2), columns 16 (g & 1) + 4 (s & 3) .. + 3 of
 // the 32-column block, so lane 16 (g & 1) + s of the block receives its
 // column at the 4 rows.  FP32: eight 4-byte reads.
-template <int MODE>
-__device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &f) {
+// The per-lane part of those addresses, fixed for a tile: the logical chunk
+// 32 wn + 8 j + 4 (g & 1) + 2 plane + ((s >> 1) & 1) is XORed with
+// swzk(k) < 16, which only touches bits 1..3, so bits 4 and up (16 (j >> 1)
+// and 32 wn) add to the chunk index; the rest takes one offset per
+// (j & 1, plane).
+struct BkmLane {
+  uint32_t o[2][2];
+};
+__device__ __forceinline__ BkmLane bkm_lane() {
   const int lane = threadIdx.x & 63;
-  const char *bt = st + kOpTile;
+  const int g = lane >> 4, s = lane & 15;
+  const int k = 8 * (g >> 1) + (s >> 2);
+  const int sw = swzk(k);  // the same for rows k and k + 4
+  BkmLane L;
+#pragma unroll
+  for (int jl = 0; jl < 2; ++jl)
+#pragma unroll
+    for (int pl = 0; pl < 2; ++pl)
+      L.o[jl][pl] = static_cast<uint32_t>(k * kKmRow + 8 * (s & 1) +
+                                          (((8 * jl + 4 * (g & 1) + 2 * pl + ((s >> 1) & 1)) ^ sw) << 4));
+  return L;
+}
+
+template <int MODE>
+__device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &f, const BkmLane &L) {
+  const int lane = threadIdx.x & 63;
+  const char *bt = st + kOpA;
   if constexpr (MODE == SMX_S8_COMP_BF16) {
-    const int g = lane >> 4, s = lane & 15;
-    const int k = 8 * (g >> 1) + (s >> 2);
-    const int sw = swzk(k);  // the same for rows k and k + 4
-    const char *row = bt + k * 1024 + 8 * (s & 1);
+    lds_char *lt = to_lds(st);
 #pragma unroll
     for (int j = 0; j < kSubN; ++j) {
-      const int grp = 8 * wn + 2 * j + (g & 1);
 #pragma unroll
       for (int pl = 0; pl < 2; ++pl) {
-        const char *p = row + (((4 * grp + 2 * pl + ((s >> 1) & 1)) ^ sw) << 4);
-        const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * 1024);
+        lds_char *p = lt + L.o[j & 1][pl] + (kOpA + ((32 * wn + 16 * (j >> 1)) << 4));
+        const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * kKmRow);
         const bf16x8 v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         if (pl == 0) f.h[j] = v;
         else f.l[j] = v;
@@ -279,15 +316,15 @@ __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         const int k = 8 * h + q;
-        f.v[j][q] = *reinterpret_cast<const float *>(bt + k * 1024 + (((n >> 2) ^ swzk(k)) << 4) + (n & 3) * 4);
+        f.v[j][q] = *reinterpret_cast<const float *>(bt + k * kKmRow + (((n >> 2) ^ swzk(k)) << 4) + (n & 3) * 4);
       }
     }
   }
 }
 
 template <int MODE, bool BKM>
-__device__ __forceinline__ void load_b_any(const char *st, int wn, BFrags<MODE> &f) {
-  if constexpr (BKM) load_b_km<MODE>(st, wn, f);
+__device__ __forceinline__ void load_b_any(const char *st, int wn, BFrags<MODE> &f, const BkmLane &L) {
+  if constexpr (BKM) load_b_km<MODE>(st, wn, f, L);
   else load_b<MODE>(st, wn, f);
 }
 
@@ -341,21 +378,28 @@ __device__ __forceinline__ AFrag<MODE> one_hot(float s, int r0) {
 }
 
 // Issues one stage (A and B tiles) into a ring slot.  `lds` is the slot's
-// LDS byte address plus this wave's first chunk (wave-uniform).  BKM: B is
-// K-major (its stage is 16 rows further down).
+// LDS byte address plus this wave's first A chunk (wave-uniform); the
+// wave's B chunks start kOpA bytes later, less the difference of the
+// wave's A and B shares.  BKM: B is K-major (its stage is 16 rows further
+// down).
+struct WaveOffsets {
+  TileOffsets<kLoadsA> a;
+  TileOffsets<kLoadsB> b;
+  uint32_t b_lds;  // LDS byte offset of the wave's B chunks from its A chunks
+};
 template <bool BKM>
-__device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const TileOffsets &oa,
-                                            const TileOffsets &ob, int64_t k0, uint32_t lds) {
-  dma_tile(oa, static_cast<const char *>(A.p) + 4 * k0, lds);
-  dma_tile(ob, static_cast<const char *>(B.p) + 4 * k0 * (BKM ? B.ld : 1), lds + kOpTile);
+__device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const WaveOffsets &o, int64_t k0,
+                                            uint32_t lds) {
+  dma_tile(o.a, static_cast<const char *>(A.p) + 4 * k0, lds);
+  dma_tile(o.b, static_cast<const char *>(B.p) + 4 * k0 * (BKM ? B.ld : 1), lds + o.b_lds);
 }
 
 // Waits until at most `pending` stages of this wave's loads are in flight
 // (loads complete in issue order).
 __device__ __forceinline__ void wait_stages(int pending) {
   constexpr int L = kLoadsPerStage;
-  if (pending >= 3) wait_vm<3 * L>();
-  else if (pending == 2) wait_vm<2 * L>();
+  static_assert(kStages == 3, "at most two stages in flight");
+  if (pending >= 2) wait_vm<2 * L>();
   else if (pending == 1) wait_vm<L>();
   else wait_vm<0>();
 }
@@ -366,7 +410,8 @@ __device__ __forceinline__ void wait_stages(int pending) {
 // lgkmcnt waits before later MFMAs that stall on unrelated newer reads.
 __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// C[256 x 256] = A[arow0.., :K] * B[brow0.., :K]^T.
+// C[256 x 128] = A[arow0.., :K] * B[brow0.., :K]^T (BKM: A[arow0.., :K] *
+// B[:K, brow0..]).
 //
 // Two pipelines overlap the MFMAs:
 //  * a ring of kStages LDS slots filled by direct-to-LDS loads, kStages
@@ -379,12 +424,12 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 // barrier makes every wave's loads of kt+1 visible and every wave's reads
 // of kt finished; refill slot kt with stage kt+kStages; MFMAs of stage kt
 // interleaved with the reads of stage kt+1.
-// SEL >= 0: this stage is stage SEL of the wave's 8-stage one_hot window
+// SEL >= 0: this stage is stage SEL of the wave's 4-stage one_hot window
 // (rows 16 SEL .. 16 SEL + 15 of the wave, accumulator block SEL / 2).
 // STEADY: kt + kStages < nk, so a next stage exists, the refill is due and
 // kStages - 2 stages may stay in flight (no run-time conditions).
 template <int MODE, int SEL, int PAR, bool STEADY, bool BKM>
-__device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const TileOffsets &oa, const TileOffsets &ob,
+__device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const WaveOffsets &o, const BkmLane &bl,
                                           uint32_t lds0, float sel_s, char *smem, int kt, int nk, int wm, int wn,
                                           AFrag<MODE> (&af)[kSubM], BFrags<MODE> (&bf)[2],
                                           f32x16 (&acc)[kSubM][kSubN]) {
@@ -398,9 +443,9 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Ti
   wait_lds();
   block_barrier();
   if (STEADY || kt + S < nk)
-    issue_stage<BKM>(A, B, oa, ob, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * kStageBytes);
+    issue_stage<BKM>(A, B, o, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * kStageBytes);
   const char *nxt = smem + ((kt + 1) % S) * kStageBytes;
-  if (more) load_b_any<MODE, BKM>(nxt, wn, bf[PAR ^ 1]);
+  if (more) load_b_any<MODE, BKM>(nxt, wn, bf[PAR ^ 1], bl);
 #pragma unroll
   for (int i = 0; i < kSubM; ++i) {
     mma_row<MODE>(af[i], bf[PAR], acc[i]);
@@ -413,12 +458,11 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Ti
 // B are the same symmetric G, K = rows of G).  BKM: B is a K-major
 // row-major operand (C = A B, apply), brow0 its first column.
 template <int MODE, bool ACCG, bool BKM>
-__device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &B, int64_t K, int64_t arow0, int64_t brow0,
-                                         float sel_s, char *smem, f32x16 (&acc)[kSubM][kSubN]) {
-  static_assert(kSubM == 4 && kBK == 16, "the one_hot window is 8 stages of 16 rows");
-  static_assert(kStages % 2 == 0, "pairs of stages keep the fragment parity");
+__device__ __forceinline__ void gemm_tile(const Opnd &A, const Opnd &B, int64_t K, int64_t arow0, int64_t brow0,
+                                          float sel_s, char *smem, f32x16 (&acc)[kSubM][kSubN]) {
+  static_assert(kSubM == 2 && kBK == 16, "the one_hot window is 4 stages of 16 rows");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave, wn = 0;  // waves stacked along M, each 64 x 128
 #pragma unroll
   for (int i = 0; i < kSubM; ++i)
 #pragma unroll
@@ -426,22 +470,25 @@ __device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &B, int64_t K
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
   const int nk = static_cast<int>(K / kBK);
-  const TileOffsets oa = tile_offsets(A.ld, arow0, wave);
-  const TileOffsets ob = BKM ? tile_offsets_km(B.ld, brow0, wave) : tile_offsets(B.ld, brow0, wave);
-  // LDS byte address of the ring plus this wave's first chunk.
-  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * kChunksPerWave * 1024;
+  WaveOffsets o;
+  o.a = tile_offsets<kLoadsA>(A.ld, arow0, wave);
+  o.b = BKM ? tile_offsets_km<kLoadsB>(B.ld, brow0, wave) : tile_offsets<kLoadsB>(B.ld, brow0, wave);
+  o.b_lds = static_cast<uint32_t>(kOpA + wave * (kLoadsB - kLoadsA) * 1024);
+  const BkmLane bl = bkm_lane();  // used by the K-major B path only
+  // LDS byte address of the ring plus this wave's first A chunk.
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * kLoadsA * 1024;
 #pragma unroll
   for (int s = 0; s < kStages; ++s)
-    if (s < nk) issue_stage<BKM>(A, B, oa, ob, static_cast<int64_t>(s) * kBK, lds0 + s * kStageBytes);
+    if (s < nk) issue_stage<BKM>(A, B, o, static_cast<int64_t>(s) * kBK, lds0 + s * kStageBytes);
   wait_stages(min(kStages - 1, nk - 1));
   block_barrier();
   AFrag<MODE> af[kSubM];
   BFrags<MODE> bf[2];
-  load_b_any<MODE, BKM>(smem, wn, bf[0]);
+  load_b_any<MODE, BKM>(smem, wn, bf[0], bl);
 #pragma unroll
   for (int i = 0; i < kSubM; ++i) load_a<MODE>(smem, wm, i, af[i]);
 #define SMX_PIPE(SEL, PAR, KT, STEADY) \
-  pipe_iter<MODE, SEL, PAR, STEADY, BKM>(A, B, oa, ob, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
+  pipe_iter<MODE, SEL, PAR, STEADY, BKM>(A, B, o, bl, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
   // Stages [kt, to) in pairs (kt and `to` even): branch-free while a refill
   // is due, then the general form.
   const int steady_end = nk - kStages;
@@ -457,19 +504,15 @@ __device__ __forceinline__ void gemm_256(const Opnd &A, const Opnd &B, int64_t K
   };
   int kt = 0;
   if constexpr (ACCG) {
-    // The wave's rows are K stages kt0 .. kt0 + 7 (kt0 = first row / 16, a
-    // multiple of 8, so the stage parity matches the unrolled pairs).
+    // The wave's rows are K stages kt0 .. kt0 + 3 (kt0 = first row / 16, a
+    // multiple of 4, so the stage parity matches the unrolled pairs).
     const int kt0 = static_cast<int>((arow0 + wm * (32 * kSubM)) / kBK);
     run(kt, kt0);
     SMX_PIPE(0, 0, kt0, false);
     SMX_PIPE(1, 1, kt0 + 1, false);
     SMX_PIPE(2, 0, kt0 + 2, false);
     SMX_PIPE(3, 1, kt0 + 3, false);
-    SMX_PIPE(4, 0, kt0 + 4, false);
-    SMX_PIPE(5, 1, kt0 + 5, false);
-    SMX_PIPE(6, 0, kt0 + 6, false);
-    SMX_PIPE(7, 1, kt0 + 7, false);
-    kt = kt0 + 8;
+    kt = kt0 + 4;
   }
   run(kt, nk);
 #undef SMX_PIPE
@@ -506,7 +549,7 @@ struct Stage1Scalars {
 __device__ Stage1Scalars stage1_scalars(const S8Mat &M, double *bcast) {
   Stage1Scalars r;
   r.fro2 = sum_parts(M.fro(), fro_parts_used(M), bcast);
-  const double sq = sum_parts(M.sch(), static_cast<int>(sym_tiles(M.kp()->tiles_m)), bcast);
+  const double sq = sum_parts(M.sch(), static_cast<int>(2 * sym_tiles(M.kp()->tiles_m)), bcast);
   r.ok = r.fro2 > 0.0 && sq > 0.0;
   r.s = r.ok ? fmaxf(static_cast<float>(kS8Margin * pow(sq, 0.125)), 1e-30f) : 1.f;
   return r;
@@ -542,8 +585,17 @@ __device__ __forceinline__ void ep_read8(const float *s, int row, int col, float
 }
 
 // ------------------------------------------------------------ kernel ---
+// Output tiles are 256 x 128: tm counts 256-row blocks, tn 128-column
+// blocks.  The Gram and the square compute the upper-triangle 256 x 256
+// blocks of their symmetric result, each as two 128-column halves
+// (tix = 2 * block index + half); a diagonal block's halves together cover
+// it, an off-diagonal half also writes its mirror.
+__host__ __device__ inline int64_t phase_tiles(const S8Class &k, int phase) {
+  return phase == kApply ? static_cast<int64_t>(k.tiles_m) * (k.cp / kTileN) : 2 * sym_tiles(k.tiles_m);
+}
+
 template <int MODE, int PHASE>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 s8_stage_kernel(StageArgs args) {
   __shared__ __attribute__((aligned(16))) char smem[kRingBytes];
   __shared__ double dscratch[16];
@@ -552,19 +604,23 @@ s8_stage_kernel(StageArgs args) {
 
   const TileRef ref = tile_of(args);
   const S8Class &K = *ref.k;
-  const int64_t tpm = PHASE == kApply ? static_cast<int64_t>(K.tiles_m) * K.tiles_n : sym_tiles(K.tiles_m);
+  const int64_t tpm = phase_tiles(K, PHASE);
   if (ref.L >= tpm * K.count) return;
   const int slot = static_cast<int>(ref.L / tpm);
   const int64_t tix = ref.L % tpm;
   int64_t tm, tn;
+  bool diag = false;  // Gram / square: a half of a diagonal 256 x 256 block
   if constexpr (PHASE == kApply) {
-    tm = tix / K.tiles_n;
-    tn = tix % K.tiles_n;
+    const int64_t tn2 = K.cp / kTileN;
+    tm = tix / tn2;
+    tn = tix % tn2;
   } else {
-    int64_t rem = tix;
+    int64_t rem = tix >> 1;
     tm = 0;
     while (rem >= K.tiles_m - tm) { rem -= K.tiles_m - tm; ++tm; }
-    tn = tm + rem;
+    const int64_t tb = tm + rem;
+    tn = 2 * tb + (tix & 1);
+    diag = tb == tm;
   }
   const S8Mat M{K, slot};
   const int stage = args.stage;
@@ -580,15 +636,15 @@ s8_stage_kernel(StageArgs args) {
       scale = f > 0.0 ? static_cast<float>(1.0 / f) : 0.f;
     }
     const Opnd X{x_in, K.cp};
-    gemm_256<MODE, false, false>(X, X, K.cp, tm * kTile, tn * kTile, 0.f, smem, acc);
+    gemm_tile<MODE, false, false>(X, X, K.cp, tm * kTileM, tn * kTileN, 0.f, smem, acc);
   } else if constexpr (PHASE == kSquare) {
     const Opnd G{M.g(), K.rp};
     if (stage == 1) {
-      gemm_256<MODE, false, false>(G, G, K.rp, tm * kTile, tn * kTile, 0.f, smem, acc);
+      gemm_tile<MODE, false, false>(G, G, K.rp, tm * kTileM, tn * kTileN, 0.f, smem, acc);
     } else {
       // acc = G G + (b/c) G; the epilogue forms P = c acc + a I.
       scale = args.c;
-      gemm_256<MODE, true, false>(G, G, K.rp, tm * kTile, tn * kTile, args.b_over_c, smem, acc);
+      gemm_tile<MODE, true, false>(G, G, K.rp, tm * kTileM, tn * kTileN, args.b_over_c, smem, acc);
     }
   } else {
     if (stage == 1) {
@@ -597,21 +653,22 @@ s8_stage_kernel(StageArgs args) {
       scale = sc.ok ? static_cast<float>(1.0 / (sqrt(sc.fro2) * static_cast<double>(sc.s))) : 0.f;
     }
     // X' = P X: B = X rows k (K-major), columns of the tile.
-    gemm_256<MODE, false, true>(Opnd{M.p(), K.rp}, Opnd{x_in, K.cp}, K.rp, tm * kTile, tn * kTile, 0.f, smem, acc);
+    gemm_tile<MODE, false, true>(Opnd{M.p(), K.rp}, Opnd{x_in, K.cp}, K.rp, tm * kTileM, tn * kTileN, 0.f, smem,
+                                 acc);
   }
 
   // ------------------------------------------------------- epilogue ---
   // Each 32x32 accumulator block goes through wave-private LDS in both
   // orientations (T row-major, U column-major), so that the tile and its
   // transpose are written as row vectors of 8 elements per lane.
-  //   GRAM    tile -> G, transpose -> G (off-diagonal tiles)
+  //   GRAM    tile -> G, transpose -> G (halves of off-diagonal blocks)
   //   SQUARE  stage 1: G2 (FP32) -> p; stage k: P = c acc + a I -> p
   //   APPLY   tile -> X' (stage 5, transposed parameter: transpose -> xf)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave, wn = 0;
   const int lr = lane & 31, lh = lane >> 5;
   const int rr = lane >> 2, cc = (lane & 3) * 8;  // read-back: rows rr, rr + 16; cols cc..cc+7
-  const int64_t R0 = tm * kTile + wm * (32 * kSubM), C0 = tn * kTile + wn * (32 * kSubN);
+  const int64_t R0 = tm * kTileM + wm * (32 * kSubM), C0 = tn * kTileN + wn * (32 * kSubN);
   const bool last = stage == 5;
   float *dst_t, *dst_m;
   int64_t ld_t, ld_m;
@@ -629,7 +686,7 @@ s8_stage_kernel(StageArgs args) {
     ld_t = ld_m = K.rp;
     pl_t = pl_m = PL && (PHASE == kGram || stage != 1);
     do_t = true;
-    do_m = tm != tn;
+    do_m = !diag;
   }
   const bool eye = PHASE == kSquare && stage != 1;  // add a I on the diagonal
   float *const T = reinterpret_cast<float *>(smem) + wave * 2 * kEpBlock;
@@ -673,13 +730,13 @@ s8_stage_kernel(StageArgs args) {
       }
     }
     // Keep the scheduler from hoisting every accumulator read to the top
-    // of the epilogue (256 values would not fit in the VGPRs).
+    // of the epilogue (the values would not fit in the VGPRs).
     __builtin_amdgcn_sched_barrier(0);
   }
   if constexpr (PHASE == kSquare) {
     if (stage == 1) {
       const double s = block_sum(static_cast<double>(sq_local), dscratch);
-      if (threadIdx.x == 0) M.sch()[tix] = (tm == tn ? 1.0 : 2.0) * s;
+      if (threadIdx.x == 0) M.sch()[tix] = (diag ? 1.0 : 2.0) * s;
     }
   }
 }
@@ -800,11 +857,12 @@ static double launch_flops(const S8Layout &Lay, int stage) {
   double f = 0.0;
   for (int i = 0; i < Lay.n_classes; ++i) {
     const S8Class &k = Lay.cls[i];
-    const double tiles = PHASE == kApply ? static_cast<double>(k.tiles_m) * k.tiles_n
-                                         : static_cast<double>(sym_tiles(k.tiles_m));
+    const double tiles = static_cast<double>(phase_tiles(k, PHASE));
     const double K = PHASE == kGram ? static_cast<double>(k.cp) : static_cast<double>(k.rp);
-    f += k.count * tiles * 2.0 * kTile * kTile * K * prod;
-    if (PHASE == kSquare && stage != 1) f += k.count * tiles * kWaves * 8.0 * kSubN * 2.0 * 32 * 32 * kBK * prod;
+    f += k.count * tiles * 2.0 * kTileM * kTileN * K * prod;
+    // one-hot: per wave 2 kSubM stages of kSubN MFMA tiles
+    if (PHASE == kSquare && stage != 1)
+      f += k.count * tiles * kWaves * (2.0 * kSubM) * kSubN * 2.0 * 32 * 32 * kBK * prod;
   }
   return f;
 }
@@ -832,9 +890,7 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
   for (int ci : order) {
     const S8Class &k = Lay.cls[ci];
     if (k.count == 0) continue;
-    const int64_t tpm = PHASE == kApply   ? static_cast<int64_t>(k.tiles_m) * k.tiles_n
-                        : PHASE == kPoly1 ? static_cast<int64_t>(k.tiles_m) * k.tiles_m
-                                          : sym_tiles(k.tiles_m);
+    const int64_t tpm = PHASE == kPoly1 ? static_cast<int64_t>(k.tiles_m) * k.tiles_m : phase_tiles(k, PHASE);
     const int64_t nt = round_up(tpm * k.count, 8);
     a.seg_off[a.n_seg] = off;
     a.seg_cls[a.n_seg] = ci;
@@ -938,7 +994,7 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.u = reinterpret_cast<float *>(take(static_cast<size_t>(C.count) * C.cp * sizeof(float)));
     C.fro = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));
     C.mb = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));
-    C.sch = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * sym_tiles(C.tiles_m) * sizeof(double)));
+    C.sch = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * 2 * sym_tiles(C.tiles_m) * sizeof(double)));
     C.cst = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * 2 * sizeof(double)));
   }
   plan.bytes = off;
