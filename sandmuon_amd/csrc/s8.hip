@@ -296,12 +296,23 @@ __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &
   const int lane = threadIdx.x & 63;
   const char *bt = st + kOpA;
   if constexpr (MODE == SMX_S8_COMP_BF16) {
-    lds_char *lt = to_lds(st);
+    // Four base addresses per stage; the empty asm keeps the compiler from
+    // pre-adding every read's constant offset into a register of its own
+    // (sixteen live registers and two VALU ops per read) instead of using
+    // the instructions' offset field.
+    lds_char *q[2][2];
+#pragma unroll
+    for (int jl = 0; jl < 2; ++jl)
+#pragma unroll
+      for (int pl = 0; pl < 2; ++pl) {
+        q[jl][pl] = to_lds(st) + L.o[jl][pl];
+        asm volatile("" : "+v"(q[jl][pl]));
+      }
 #pragma unroll
     for (int j = 0; j < kSubN; ++j) {
 #pragma unroll
       for (int pl = 0; pl < 2; ++pl) {
-        lds_char *p = lt + L.o[j & 1][pl] + (kOpA + ((32 * wn + 16 * (j >> 1)) << 4));
+        lds_char *p = q[j & 1][pl] + (kOpA + ((32 * wn + 16 * (j >> 1)) << 4));
         const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * kKmRow);
         const bf16x8 v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         if (pl == 0) f.h[j] = v;
