@@ -28,8 +28,8 @@
 //                     60-66, applied in all five stages with FP32
 //                     accumulation of every intermediate).
 //
-// Block: 256x128 output tile, 4 waves stacked along M (one per SIMD), each
-// wave 64x128 (2 x 4 MFMA 32x32 tiles, 128 accumulator registers), and two
+// Block: 256x128 output tile, 4 waves (2 x 2, one per SIMD), each wave
+// 128x64 (4 x 2 MFMA 32x32 tiles, 128 accumulator registers), and two
 // blocks per CU, so one block's epilogue and prologue overlap the other's
 // MFMAs.  Operands stream into a 3-stage LDS ring (K = 16 per stage, 24 KB)
 // with direct-to-LDS 16-byte loads issued two stages ahead.  The epilogue
@@ -51,7 +51,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;      // 4 waves, one per SIMD; two blocks per CU
 constexpr int kWaves = kThreads / 64;
 constexpr int kTileM = kTile, kTileN = kTile / 2;  // block output tile 256 x 128
-constexpr int kSubM = 2, kSubN = 4; // 32x32 MFMA tiles per wave (64 x 128)
+constexpr int kSubM = 4, kSubN = 2; // 32x32 MFMA tiles per wave (128 x 64; waves 2 x 2)
 constexpr int kBK = 16;             // K per pipeline stage
 constexpr int kOpA = kTileM * kBK * 4;  // A operand tile 256 x 16 (4 bytes per element)
 constexpr int kOpB = kTileN * kBK * 4;  // B operand tile 128 x 16
@@ -269,9 +269,9 @@ __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) 
 // the 32-column block, so lane 16 (g & 1) + s of the block receives its
 // column at the 4 rows.  FP32: eight 4-byte reads.
 // The per-lane part of those addresses, fixed for a tile: the logical chunk
-// 32 wn + 8 j + 4 (g & 1) + 2 plane + ((s >> 1) & 1) is XORed with
+// 8 kSubN wn + 8 j + 4 (g & 1) + 2 plane + ((s >> 1) & 1) is XORed with
 // swzk(k) < 16, which only touches bits 1..3, so bits 4 and up (16 (j >> 1)
-// and 32 wn) add to the chunk index; the rest takes one offset per
+// and 8 kSubN wn) add to the chunk index; the rest takes one offset per
 // (j & 1, plane).
 struct BkmLane {
   uint32_t o[2][2];
@@ -312,7 +312,7 @@ __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &
     for (int j = 0; j < kSubN; ++j) {
 #pragma unroll
       for (int pl = 0; pl < 2; ++pl) {
-        lds_char *p = q[j & 1][pl] + (kOpA + ((32 * wn + 16 * (j >> 1)) << 4));
+        lds_char *p = q[j & 1][pl] + (kOpA + ((8 * kSubN * wn + 16 * (j >> 1)) << 4));
         const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * kKmRow);
         const bf16x8 v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         if (pl == 0) f.h[j] = v;
@@ -435,7 +435,7 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 // barrier makes every wave's loads of kt+1 visible and every wave's reads
 // of kt finished; refill slot kt with stage kt+kStages; MFMAs of stage kt
 // interleaved with the reads of stage kt+1.
-// SEL >= 0: this stage is stage SEL of the wave's 4-stage one_hot window
+// SEL >= 0: this stage is stage SEL of the wave's 8-stage one_hot window
 // (rows 16 SEL .. 16 SEL + 15 of the wave, accumulator block SEL / 2).
 // STEADY: kt + kStages < nk, so a next stage exists, the refill is due and
 // kStages - 2 stages may stay in flight (no run-time conditions).
@@ -471,9 +471,10 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Wa
 template <int MODE, bool ACCG, bool BKM>
 __device__ __forceinline__ void gemm_tile(const Opnd &A, const Opnd &B, int64_t K, int64_t arow0, int64_t brow0,
                                           float sel_s, char *smem, f32x16 (&acc)[kSubM][kSubN]) {
-  static_assert(kSubM == 2 && kBK == 16, "the one_hot window is 4 stages of 16 rows");
+  static_assert(kSubM == 4 && kBK == 16, "the one_hot window is 8 stages of 16 rows");
+  static_assert((8 * kSubN) % 16 == 0, "the wave's K-major column offset must be whole chunk groups");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  const int wm = wave, wn = 0;  // waves stacked along M, each 64 x 128
+  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves, each 128 x 64
 #pragma unroll
   for (int i = 0; i < kSubM; ++i)
 #pragma unroll
@@ -515,15 +516,19 @@ __device__ __forceinline__ void gemm_tile(const Opnd &A, const Opnd &B, int64_t 
   };
   int kt = 0;
   if constexpr (ACCG) {
-    // The wave's rows are K stages kt0 .. kt0 + 3 (kt0 = first row / 16, a
-    // multiple of 4, so the stage parity matches the unrolled pairs).
+    // The wave's rows are K stages kt0 .. kt0 + 7 (kt0 = first row / 16, a
+    // multiple of 8, so the stage parity matches the unrolled pairs).
     const int kt0 = static_cast<int>((arow0 + wm * (32 * kSubM)) / kBK);
     run(kt, kt0);
     SMX_PIPE(0, 0, kt0, false);
     SMX_PIPE(1, 1, kt0 + 1, false);
     SMX_PIPE(2, 0, kt0 + 2, false);
     SMX_PIPE(3, 1, kt0 + 3, false);
-    kt = kt0 + 4;
+    SMX_PIPE(4, 0, kt0 + 4, false);
+    SMX_PIPE(5, 1, kt0 + 5, false);
+    SMX_PIPE(6, 0, kt0 + 6, false);
+    SMX_PIPE(7, 1, kt0 + 7, false);
+    kt = kt0 + 8;
   }
   run(kt, nk);
 #undef SMX_PIPE
@@ -676,7 +681,7 @@ s8_stage_kernel(StageArgs args) {
   //   SQUARE  stage 1: G2 (FP32) -> p; stage k: P = c acc + a I -> p
   //   APPLY   tile -> X' (stage 5, transposed parameter: transpose -> xf)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int wm = wave, wn = 0;
+  const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
   const int rr = lane >> 2, cc = (lane & 3) * 8;  // read-back: rows rr, rr + 16; cols cc..cc+7
   const int64_t R0 = tm * kTileM + wm * (32 * kSubM), C0 = tn * kTileN + wn * (32 * kSubN);
