@@ -340,13 +340,20 @@ class DiagonalWeightedPE(Optimizer):
             d.z, d.kappa = out["z"].data_ptr(), out["kappa"].data_ptr()
         return d
 
+    def _run_closure(self, closure):
+        """sandmuon/optimizer.py:226-230: the closure runs with gradients enabled."""
+        if closure is None:
+            return None
+        with torch.enable_grad():
+            return closure()
+
+    def _momentum(self, group) -> float:
+        """Matrix momentum of a group (sandmuon/optimizer.py:246-248)."""
+        return float(group["momentum"])
+
     @torch.no_grad()
     def step(self, closure=None):
-        if closure is None:
-            loss = None
-        else:
-            with torch.enable_grad():
-                loss = closure()
+        loss = self._run_closure(closure)
         matrix_items, auxiliary_items = [], []
         a_counts: Dict[int, int] = {}
         for group in self.param_groups:
@@ -416,7 +423,7 @@ class DiagonalWeightedPE(Optimizer):
                                     momentum=state["momentum_buffer"].data_ptr(),
                                     inv_row=b_out[id(parameter)]["inv"].data_ptr(), inv_col=a["inv"].data_ptr(),
                                     rows=parameter.shape[0], cols=parameter.shape[1], lr=float(group["lr"]),
-                                    momentum_beta=float(group["momentum"]),
+                                    momentum_beta=self._momentum(group),
                                     grad_dtype=_native.dtype_code(grad.dtype))
             if self.rank_one_a:
                 md.z, md.kappa = a["z"].data_ptr(), a["kappa"].data_ptr()
