@@ -486,6 +486,48 @@ class OracleOptimizer:
             for d, (p, *_rest) in zip(dirs, entries):
                 p.add_(d.to(p.dtype), alpha=-self.lr)
 
+    # ------------------------------------------------------ checkpoints ---
+    def _params(self):
+        return list(self.matrices.values()) + list(self.aux)
+
+    def state_dict(self) -> dict:
+        """The torch.optim.Optimizer.state_dict() layout of the reference
+        (sandmuon/optimizer.py:137-144 groups; state keyed by the index of
+        the parameter in group order: matrices, then auxiliaries)."""
+        base = dict(lr=self.lr, use_muon=True, momentum=self.momentum, weight_decay=0.,
+                    adamw_lr_ratio=.1, adamw_betas=(.9, .999), adamw_eps=1e-8)
+        n = len(self.matrices)
+        groups = [dict(base, params=list(range(n)))]
+        if self.aux:
+            groups.append(dict(base, use_muon=False, weight_decay=.01, params=list(range(n, n + len(self.aux)))))
+        state = {}
+        for i, p in enumerate(self._params()):
+            entry = self.state.get(id(p))
+            if entry:
+                state[i] = {k: (v.clone() if torch.is_tensor(v) else v) for k, v in entry.items()}
+        return {"state": state, "param_groups": groups}
+
+    def load_state_dict(self, sd: dict) -> None:
+        """Loads a state_dict() of this layout (from this class or from the
+        GPU build); tensors move to the CPU, a tensor AdamW step becomes an
+        int."""
+        params = self._params()
+        total = sum(len(g["params"]) for g in sd["param_groups"])
+        if total != len(params):
+            raise ValueError(f"checkpoint has {total} parameters, this optimizer {len(params)}")
+        self.state = {}
+        for i, entry in sd["state"].items():
+            p = params[int(i)]
+            out = {}
+            for k, v in entry.items():
+                if torch.is_tensor(v):
+                    v = v.detach().cpu().clone()
+                    if k == "step":
+                        v = int(v.item())
+                out[k] = v
+            self.state[id(p)] = out
+        self.lr = float(sd["param_groups"][0]["lr"])
+
     def close(self):
         for h in self.handles:
             h.remove()

@@ -1,6 +1,8 @@
 """The CPU oracle against golden vectors written by the reference itself
 (tests/golden/make_golden.py runs sandmuon/optimizer.py in the build
 container; the fixtures hold inputs and outputs)."""
+import copy
+import json
 from pathlib import Path
 
 import numpy as np
@@ -90,4 +92,43 @@ def test_oracle_step_matches_reference(tag, rank_one, steps):
             assert int(st[field]) == int(ref), key
         else:
             assert rel(st[field], torch.from_numpy(ref)) <= 1e-5, key
+    if tag == "rank1":
+        # The oracle's checkpoint layout is the reference's (state_dict.json
+        # was written by the reference after this run), so checkpoints cross
+        # between the oracle and the GPU build.
+        assert structure(opt.state_dict()) == json.loads((Path(__file__).parent / "golden" / "state_dict.json").read_text())
     opt.close()
+
+
+def structure(sd):
+    """Keys, types, dtypes and shapes of a state_dict (the fixture's form)."""
+    groups = [{k: (len(v) if k == "params" else (list(v) if isinstance(v, tuple) else v)) for k, v in g.items()}
+              for g in sd["param_groups"]]
+    state = {str(i): {k: ({"tensor": list(v.shape), "dtype": str(v.dtype)} if torch.is_tensor(v)
+                          else {"type": type(v).__name__}) for k, v in st.items()}
+             for i, st in sd["state"].items()}
+    return {"param_groups": groups, "state": state}
+
+
+def test_oracle_checkpoint_round_trip_is_exact():
+    z = load("step_rank1.npz")
+    runs = []
+    for resume in (False, True):
+        model = model_from(z)
+        batches = batches_from(z)
+        opt = O.OracleOptimizer(model, 3e-3, rank_one_a=True, module_filter=transformer_filter)
+        for s in range(2):
+            if resume and s == 1:
+                saved = copy.deepcopy(opt.state_dict())
+                opt.close()
+                opt = O.OracleOptimizer(model, 3e-3, rank_one_a=True, module_filter=transformer_filter)
+                opt.load_state_dict(saved)
+            for p in model.parameters():
+                p.grad = None
+            for idx, tgt in batches:
+                (model(idx, tgt) / len(batches)).backward()
+            opt.step()
+        runs.append({n: p.detach().clone() for n, p in model.named_parameters()})
+        opt.close()
+    for n in runs[0]:
+        assert torch.equal(runs[0][n], runs[1][n]), n

@@ -59,22 +59,28 @@ class Capture:
             h.remove()
 
 
-def run_pair(device, model, batches, loss_fn, opt_cls, mode, lr, steps, module_filter=None):
-    gpu_model = model.to(device)
-    cpu_model = copy.deepcopy(model).cpu()
-    opt = opt_cls(gpu_model, lr, module_filter=module_filter, s8_mode=mode)
-    ora = O.OracleOptimizer(cpu_model, lr, rank_one_a=opt.rank_one_a, module_filter=module_filter, hooks=False)
-    assert list(opt.named_matrices) == list(ora.matrices)
-    cap = Capture(gpu_model, opt.named_matrices)
-    gparams = dict(gpu_model.named_parameters())
-    cparams = dict(cpu_model.named_parameters())
-    name_of = {id(p): n for n, p in gparams.items()}
-    history = []
-    for _ in range(steps):
+class Pair:
+    """A GPU model + optimizer and a CPU copy + oracle stepped in lockstep:
+    the oracle is fed the GPU side's captured hook inputs and gradients."""
+
+    def __init__(self, device, model, opt_cls, mode, lr, module_filter=None):
+        self.device, self.lr = device, lr
+        self.gpu_model = model.to(device)
+        self.cpu_model = copy.deepcopy(model).cpu()
+        self.opt = opt_cls(self.gpu_model, lr, module_filter=module_filter, s8_mode=mode)
+        self.ora = O.OracleOptimizer(self.cpu_model, lr, rank_one_a=self.opt.rank_one_a,
+                                     module_filter=module_filter, hooks=False)
+        assert list(self.opt.named_matrices) == list(self.ora.matrices)
+        self.cap = Capture(self.gpu_model, self.opt.named_matrices)
+
+    def step(self, batches, loss_fn):
+        opt, ora, device = self.opt, self.ora, self.device
+        gparams = dict(self.gpu_model.named_parameters())
+        cparams = dict(self.cpu_model.named_parameters())
         opt.zero_grad(set_to_none=True)
         for x, y in batches:
-            loss_fn(gpu_model, x.to(device), y.to(device)).backward()
-        for name, kind, t in cap.drain():
+            loss_fn(self.gpu_model, x.to(device), y.to(device)).backward()
+        for name, kind, t in self.cap.drain():
             ora.feed(name, x=t if kind == "a" else None, delta=t if kind == "b" else None)
         with torch.no_grad():
             for n, p in gparams.items():
@@ -84,8 +90,8 @@ def run_pair(device, model, batches, loss_fn, opt_cls, mode, lr, steps, module_f
         opt.step()
         ora.step()
         torch.cuda.synchronize()
-        history.append((before, {n: p.detach().clone() for n, p in gparams.items()},
-                        {n: p.detach().clone() for n, p in cparams.items()}))
+        entry = (before, {n: p.detach().clone() for n, p in gparams.items()},
+                 {n: p.detach().clone() for n, p in cparams.items()})
         # state comparisons
         for n, p in opt.named_matrices.items():
             gs, cs = opt.state[p], ora.st(ora.matrices[n])
@@ -97,9 +103,18 @@ def run_pair(device, model, batches, loss_fn, opt_cls, mode, lr, steps, module_f
                 if key in cs:
                     assert gs[key] == cs[key] == 0
             assert rel(gs["momentum_buffer"], cs["momentum_buffer"]) <= 1e-6
-    cap.close()
-    opt.close()
-    return history, opt, ora
+        return entry
+
+    def close(self):
+        self.cap.close()
+        self.opt.close()
+
+
+def run_pair(device, model, batches, loss_fn, opt_cls, mode, lr, steps, module_filter=None):
+    pair = Pair(device, model, opt_cls, mode, lr, module_filter)
+    history = [pair.step(batches, loss_fn) for _ in range(steps)]
+    pair.close()
+    return history, pair.opt, pair.ora
 
 
 def check_directions(history, opt, lr, mode):
@@ -191,3 +206,46 @@ def test_tiny_gpt_two_steps(device, opt_cls, mode):
     worst = check_directions(hist, opt, 3e-3, mode)
     print(f"tiny gpt {opt_cls.__name__} {mode}: worst direction rel err {worst:.3e}")
     check_aux(hist, opt, ora)
+
+
+def _tiny_gpt_batches(seed, n=3):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for mb in range(n):
+        idx = torch.randint(0, GPT_TINY.vocab, (2 + mb, GPT_TINY.ctx), generator=g)
+        tgt = torch.randint(0, GPT_TINY.vocab, (2 + mb, GPT_TINY.ctx), generator=g)
+        out.append((idx, tgt))
+    return out
+
+
+@pytest.mark.parametrize("source", ["gpu", "oracle"])
+def test_checkpoint_crossloads_between_the_gpu_build_and_the_oracle(device, source):
+    """Checkpoint interop: a state_dict() saved by one side after a step is
+    loaded by a fresh instance of the other, and the next step matches the
+    uninterrupted side to the parity gates (fp32 mode)."""
+    mode, lr = "fp32", 3e-3
+    torch.manual_seed(31)
+    model = GPT(GPT_TINY)
+    model.init_weights(31)
+    loss = lambda m, x, y: m(x, y) / 3
+    pair = Pair(device, model, RankOneAWeightedPE, mode, lr, transformer_filter)
+    pair.step(_tiny_gpt_batches(32), loss)
+    if source == "gpu":
+        saved = pair.opt.state_dict()
+        saved = {"state": {k: {n: (v.detach().cpu().clone() if torch.is_tensor(v) else v) for n, v in e.items()}
+                           for k, e in saved["state"].items()},
+                 "param_groups": copy.deepcopy(saved["param_groups"])}
+        cpu_model = copy.deepcopy(pair.cpu_model)
+        ora = O.OracleOptimizer(cpu_model, lr, rank_one_a=True, module_filter=transformer_filter, hooks=False)
+        ora.load_state_dict(saved)
+        pair.cpu_model, pair.ora = cpu_model, ora
+    else:
+        saved = pair.ora.state_dict()
+        pair.opt.close()
+        pair.opt = RankOneAWeightedPE(pair.gpu_model, lr, module_filter=transformer_filter, s8_mode=mode)
+        pair.opt.load_state_dict(copy.deepcopy(saved))
+        assert all(isinstance(s["step"], int) for s in pair.ora.state.values() if "step" in s)
+    entry = pair.step(_tiny_gpt_batches(33), loss)
+    check_directions([entry], pair.opt, lr, mode)
+    check_aux([entry], pair.opt, pair.ora)
+    pair.close()
