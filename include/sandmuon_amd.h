@@ -167,7 +167,9 @@ size_t smx_matrix_step_workspace_bytes(const int64_t *rows,
                                        int mode);
 
 /* Runs the whole matrix update for the n matrices of the host table
- * `descs`.  The workspace (256-byte aligned, at least
+ * `descs`.  Either every matrix of a call has a rank-one term (z, kappa
+ * set) or none has (SMX_EINVAL otherwise); an optimizer is one or the
+ * other.  The workspace (256-byte aligned, at least
  * smx_matrix_step_workspace_bytes) holds the S8 iterates; its contents on
  * entry are irrelevant. */
 int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode,

@@ -53,11 +53,45 @@ __device__ __forceinline__ float load_elem(const void *p, int64_t i) {
 }
 
 // ---------------------------------------------------- wave reductions ---
+// Sum over the 64 lanes of a fully active wave, the same value in every
+// lane.  Within each row of 16 lanes four DPP moves (quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror, row_mirror) pair every lane with
+// its partner, so every lane of a row ends with the row sum; the four row
+// sums are then read from lanes 0, 16, 32 and 48 and added in a fixed
+// order.  No LDS round trips.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, dpp_mov<CTRL>(__builtin_bit_cast(uint32_t, v)));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = dpp_mov<CTRL>(static_cast<uint32_t>(b)), hi = dpp_mov<CTRL>(static_cast<uint32_t>(b >> 32));
+  return __builtin_bit_cast(double, lo | (hi << 32));
+}
+template <typename T>
+__device__ __forceinline__ T read_lane(T v, int lane) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+  } else {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b)), lane));
+    const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b >> 32)), lane));
+    return __builtin_bit_cast(T, lo | (hi << 32));
+  }
+}
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "float or double");
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  return (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
 }
 
 // Block-wide sum; every thread receives the result.  `scratch` must hold

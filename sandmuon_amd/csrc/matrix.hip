@@ -94,6 +94,7 @@ __global__ void __launch_bounds__(256) matrix_consts_kernel(MatPack pack) {
 // accumulated in FP64.  kRowsPerPart rows per block, one wave per row, so
 // every row's loads are in flight at once.
 constexpr int kRowThreads = 64 * kRowsPerPart;
+constexpr int kRowUnroll = 4;  // float4 columns per lane whose loads are in flight together
 
 // FP64 sum of the per-wave row partials, in wave order; the result is valid
 // in thread 0.
@@ -110,12 +111,13 @@ __device__ __forceinline__ double sum_wave_parts(double part, double *wave_part)
 // ------------------------------------------------------------- whiten ---
 // Momentum update m' = b m + (1-b) g (in place), u_i = b_i sum_j S_ij a_j z_j
 // and the row's ||V_i||^2 (closed form), for S = b m' + (1-b) g.
+template <bool R1>
 __global__ void __launch_bounds__(kRowThreads) whiten_rows_kernel(MatPack pack) {
   __shared__ double wave_part[kRowsPerPart];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
   const int blk = blockIdx.x - J.blk0;
-  const bool r1 = d.z != nullptr;
+  constexpr bool r1 = R1;
   const double zz = r1 ? J.cst[0] : 0.0;
   const float kappa = r1 ? d.kappa[0] : 0.f;
   const double corr = r1 ? 2.0 * kappa + static_cast<double>(kappa) * kappa * zz : 0.0;
@@ -131,20 +133,36 @@ __global__ void __launch_bounds__(kRowThreads) whiten_rows_kernel(MatPack pack) 
     if (vec) {
       const float *grow = static_cast<const float *>(d.grad) + i * d.cols;
       const int64_t n4 = d.cols / 4;
-#pragma unroll 4
-      for (int64_t q = lane; q < n4; q += 64) {
-        const float4 g = ld4(grow, q);
-        float4 m = ld4(mrow, q);
-        const float4 a = ld4(d.inv_col, q);
-        m.x = fmaf(m.x, beta, g.x * omb); m.y = fmaf(m.y, beta, g.y * omb);
-        m.z = fmaf(m.z, beta, g.z * omb); m.w = fmaf(m.w, beta, g.w * omb);
-        st4(mrow, q, m);
-        const float y0 = fmaf(m.x, beta, g.x * omb) * a.x, y1 = fmaf(m.y, beta, g.y * omb) * a.y;
-        const float y2_ = fmaf(m.z, beta, g.z * omb) * a.z, y3 = fmaf(m.w, beta, g.w * omb) * a.w;
-        y2 = fmaf(y0, y0, fmaf(y1, y1, fmaf(y2_, y2_, fmaf(y3, y3, y2))));
-        if (r1) {
-          const float4 z = ld4(d.z, q);
-          yz = fmaf(y0, z.x, fmaf(y1, z.y, fmaf(y2_, z.z, fmaf(y3, z.w, yz))));
+      for (int64_t q0 = lane; q0 < n4; q0 += 64 * kRowUnroll) {
+        // Every load of the chunk is issued before the first store.
+        float4 g[kRowUnroll], m[kRowUnroll], a[kRowUnroll], z[kRowUnroll];
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+          const int64_t q = q0 + 64 * u;
+          if (q < n4) {
+            g[u] = ld4(grow, q);
+            m[u] = ld4(mrow, q);
+            a[u] = ld4(d.inv_col, q);
+            if constexpr (R1) z[u] = ld4(d.z, q);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+          const int64_t q = q0 + 64 * u;
+          if (q < n4) {
+            float4 mm = m[u];
+            const float4 gg = g[u], aa = a[u];
+            mm.x = fmaf(mm.x, beta, gg.x * omb); mm.y = fmaf(mm.y, beta, gg.y * omb);
+            mm.z = fmaf(mm.z, beta, gg.z * omb); mm.w = fmaf(mm.w, beta, gg.w * omb);
+            st4(mrow, q, mm);
+            const float y0 = fmaf(mm.x, beta, gg.x * omb) * aa.x, y1 = fmaf(mm.y, beta, gg.y * omb) * aa.y;
+            const float y2_ = fmaf(mm.z, beta, gg.z * omb) * aa.z, y3 = fmaf(mm.w, beta, gg.w * omb) * aa.w;
+            y2 = fmaf(y0, y0, fmaf(y1, y1, fmaf(y2_, y2_, fmaf(y3, y3, y2))));
+            if constexpr (R1) {
+              const float4 zz4 = z[u];
+              yz = fmaf(y0, zz4.x, fmaf(y1, zz4.y, fmaf(y2_, zz4.z, fmaf(y3, zz4.w, yz))));
+            }
+          }
         }
       }
     } else {
@@ -174,6 +192,7 @@ __global__ void __launch_bounds__(kRowThreads) whiten_rows_kernel(MatPack pack) 
 // V = b_i S_ij a_j + kappa u_i z_j, stored in operand form to the oriented
 // iterate: directly (pl), or transposed through LDS for a transposed
 // parameter (tl).
+template <bool R1>
 __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
   __shared__ float tile[64][65];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
@@ -181,52 +200,73 @@ __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
   const int64_t tiles_c = J.pcol_pad / 64;
   const int64_t tb = blockIdx.x - J.blk0;
   const int64_t i0 = (tb / tiles_c) * 64, j0 = (tb % tiles_c) * 64;
-  const bool r1 = d.z != nullptr;
+  constexpr bool r1 = R1;
   const float kappa = r1 ? d.kappa[0] : 0.f;
   const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
   const bool vec = d.grad_dtype == SMX_F32 && d.cols % 4 == 0 && aligned16(d.grad) && aligned16(d.momentum) &&
                    aligned16(d.inv_col) && (!r1 || aligned16(d.z));
   const int t = threadIdx.x;
   const int lc = (t & 15) * 4;
+  const int64_t j = j0 + lc;
+  // The thread's four rows: every load first, then the arithmetic and the
+  // stores (a store between them would serialise the rows' loads).
+  float v[4][4];
+  if (vec && j + 3 < d.cols) {
+    float4 g[4], m[4];
+    float b[4], ku[4];
+    const float4 a = ld4(d.inv_col, j / 4);
+    float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (R1) z = ld4(d.z, j / 4);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int lr = (t >> 4) + 16 * q;
-    const int64_t i = i0 + lr, j = j0 + lc;
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (i < d.rows) {
-      const float b = d.inv_row[i];
-      const float ku = r1 ? kappa * J.u[i] : 0.f;
-      if (vec && j + 3 < d.cols) {
+    for (int q = 0; q < 4; ++q) {
+      const int64_t i = i0 + (t >> 4) + 16 * q;
+      if (i < d.rows) {
         const int64_t e4 = (i * d.cols + j) / 4;
-        const float4 g = ld4(static_cast<const float *>(d.grad), e4), m = ld4(d.momentum, e4);
-        const float4 a = ld4(d.inv_col, j / 4);
-        const float gs[4] = {g.x, g.y, g.z, g.w}, ms[4] = {m.x, m.y, m.z, m.w}, as[4] = {a.x, a.y, a.z, a.w};
-        float zs[4] = {0.f, 0.f, 0.f, 0.f};
-        if (r1) {
-          const float4 z = ld4(d.z, j / 4);
-          zs[0] = z.x; zs[1] = z.y; zs[2] = z.z; zs[3] = z.w;
-        }
+        g[q] = ld4(static_cast<const float *>(d.grad), e4);
+        m[q] = ld4(d.momentum, e4);
+        b[q] = d.inv_row[i];
+        ku[q] = r1 ? kappa * J.u[i] : 0.f;
+      }
+    }
+    const float as[4] = {a.x, a.y, a.z, a.w}, zs[4] = {z.x, z.y, z.z, z.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+    for (int q = 0; q < 4; ++q) {
+      const int64_t i = i0 + (t >> 4) + 16 * q;
+      const float gs[4] = {g[q].x, g[q].y, g[q].z, g[q].w}, ms[4] = {m[q].x, m[q].y, m[q].z, m[q].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[q][e] = 0.f;
+        if (i < d.rows) {
           const float s = fmaf(ms[e], beta, gs[e] * omb);
-          v[e] = (s * b) * as[e];
-          if (r1) v[e] = fmaf(ku, zs[e], v[e]);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (j + e < d.cols) {
-            const float g = load_grad(d.grad, d.grad_dtype, i * d.cols + j + e);
-            const float s = fmaf(d.momentum[i * d.cols + j + e], beta, g * omb);
-            v[e] = (s * b) * d.inv_col[j + e];
-            if (r1) v[e] = fmaf(ku, d.z[j + e], v[e]);
-          }
+          v[q][e] = (s * b[q]) * as[e];
+          if constexpr (R1) v[q][e] = fmaf(ku[q], zs[e], v[q][e]);
         }
       }
     }
+  } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) tile[lr][lc + e] = v[e];
-    if (J.pl) put_operand4(J.pl, i * J.pcol_pad + j, v, J.planes != 0);
+    for (int q = 0; q < 4; ++q) {
+      const int64_t i = i0 + (t >> 4) + 16 * q;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[q][e] = 0.f;
+        if (i < d.rows && j + e < d.cols) {
+          const float b = d.inv_row[i];
+          const float g = load_grad(d.grad, d.grad_dtype, i * d.cols + j + e);
+          const float s = fmaf(d.momentum[i * d.cols + j + e], beta, g * omb);
+          v[q][e] = (s * b) * d.inv_col[j + e];
+          if constexpr (R1) v[q][e] = fmaf(kappa * J.u[i], d.z[j + e], v[q][e]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int lr = (t >> 4) + 16 * q;
+    const int64_t i = i0 + lr;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[lr][lc + e] = v[q][e];
+    if (J.pl) put_operand4(J.pl, i * J.pcol_pad + j, v[q], J.planes != 0);
   }
   if (!J.tl) return;  // uniform per block
   __syncthreads();
@@ -241,12 +281,13 @@ __global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
 // ------------------------------------------------------------ mapback ---
 // u_i = sum_j Q_ij z_j and ||U_i||^2 in closed form:
 // b_i^2 (sum (a Q)^2 + 2 kappa u_i sum (a Q)(a z) + kappa^2 u_i^2 sum (a z)^2).
+template <bool R1>
 __global__ void __launch_bounds__(kRowThreads) mapback_rows_kernel(MatPack pack) {
   __shared__ double wave_part[kRowsPerPart];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
   const int blk = blockIdx.x - J.blk0;
-  const bool r1 = d.z != nullptr;
+  constexpr bool r1 = R1;
   const double cz = r1 ? J.cst[1] : 0.0;
   const double kappa = r1 ? d.kappa[0] : 0.0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -258,15 +299,29 @@ __global__ void __launch_bounds__(kRowThreads) mapback_rows_kernel(MatPack pack)
     float su = 0.f, sa = 0.f, sb = 0.f;
     if (vec) {
       const int64_t n4 = d.cols / 4;
-#pragma unroll 4
-      for (int64_t k = lane; k < n4; k += 64) {
-        const float4 qv = ld4(q, k), a = ld4(d.inv_col, k);
-        const float aq0 = a.x * qv.x, aq1 = a.y * qv.y, aq2 = a.z * qv.z, aq3 = a.w * qv.w;
-        sa = fmaf(aq0, aq0, fmaf(aq1, aq1, fmaf(aq2, aq2, fmaf(aq3, aq3, sa))));
-        if (r1) {
-          const float4 z = ld4(d.z, k);
-          su = fmaf(qv.x, z.x, fmaf(qv.y, z.y, fmaf(qv.z, z.z, fmaf(qv.w, z.w, su))));
-          sb = fmaf(aq0, a.x * z.x, fmaf(aq1, a.y * z.y, fmaf(aq2, a.z * z.z, fmaf(aq3, a.w * z.w, sb))));
+      for (int64_t k0 = lane; k0 < n4; k0 += 64 * kRowUnroll) {
+        float4 qv[kRowUnroll], av[kRowUnroll], zv[kRowUnroll];
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+          const int64_t k = k0 + 64 * u;
+          if (k < n4) {
+            qv[u] = ld4(q, k);
+            av[u] = ld4(d.inv_col, k);
+            if constexpr (R1) zv[u] = ld4(d.z, k);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+          if (k0 + 64 * u < n4) {
+            const float4 qq = qv[u], a = av[u];
+            const float aq0 = a.x * qq.x, aq1 = a.y * qq.y, aq2 = a.z * qq.z, aq3 = a.w * qq.w;
+            sa = fmaf(aq0, aq0, fmaf(aq1, aq1, fmaf(aq2, aq2, fmaf(aq3, aq3, sa))));
+            if constexpr (R1) {
+              const float4 z = zv[u];
+              su = fmaf(qq.x, z.x, fmaf(qq.y, z.y, fmaf(qq.z, z.z, fmaf(qq.w, z.w, su))));
+              sb = fmaf(aq0, a.x * z.x, fmaf(aq1, a.y * z.y, fmaf(aq2, a.z * z.z, fmaf(aq3, a.w * z.w, sb))));
+            }
+          }
         }
       }
     } else {
@@ -295,6 +350,7 @@ __global__ void __launch_bounds__(kRowThreads) mapback_rows_kernel(MatPack pack)
 
 // W -= lr * sqrt(rows) / max(||U||_F, FLT_MIN) * U over kRowsPerPart rows
 // (one wave per row).
+template <bool R1>
 __global__ void __launch_bounds__(kRowThreads) mapback_apply_kernel(MatPack pack) {
   __shared__ double bcast;
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
@@ -314,7 +370,7 @@ __global__ void __launch_bounds__(kRowThreads) mapback_apply_kernel(MatPack pack
   // gives a zero update.
   const float scale = n2 > 0.0 ? static_cast<float>(sqrt(static_cast<double>(d.rows))) / fmaxf(norm, FLT_MIN) : 0.f;
   const float nlr = static_cast<float>(-d.lr);
-  const bool r1 = d.z != nullptr;
+  constexpr bool r1 = R1;
   const float kappa = r1 ? d.kappa[0] : 0.f;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bool vec = d.cols % 4 == 0 && aligned16(d.param) && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
@@ -326,20 +382,36 @@ __global__ void __launch_bounds__(kRowThreads) mapback_apply_kernel(MatPack pack
     const float ku = r1 ? kappa * J.u[i] : 0.f;
     if (vec) {
       const int64_t n4 = d.cols / 4;
-#pragma unroll 4
-      for (int64_t k = lane; k < n4; k += 64) {
-        float4 v = ld4(q, k);
-        const float4 a = ld4(d.inv_col, k);
-        float4 wv = ld4(w, k);
-        if (r1) {
-          const float4 z = ld4(d.z, k);
-          v.x = fmaf(ku, z.x, v.x); v.y = fmaf(ku, z.y, v.y); v.z = fmaf(ku, z.z, v.z); v.w = fmaf(ku, z.w, v.w);
+      for (int64_t k0 = lane; k0 < n4; k0 += 64 * kRowUnroll) {
+        // Every load of the chunk is issued before the first store.
+        float4 qv[kRowUnroll], av[kRowUnroll], wv[kRowUnroll], zv[kRowUnroll];
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+          const int64_t k = k0 + 64 * u;
+          if (k < n4) {
+            qv[u] = ld4(q, k);
+            av[u] = ld4(d.inv_col, k);
+            wv[u] = ld4(w, k);
+            if constexpr (R1) zv[u] = ld4(d.z, k);
+          }
         }
-        wv.x = fmaf(nlr, ((v.x * b) * a.x) * scale, wv.x);
-        wv.y = fmaf(nlr, ((v.y * b) * a.y) * scale, wv.y);
-        wv.z = fmaf(nlr, ((v.z * b) * a.z) * scale, wv.z);
-        wv.w = fmaf(nlr, ((v.w * b) * a.w) * scale, wv.w);
-        st4(w, k, wv);
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+          const int64_t k = k0 + 64 * u;
+          if (k < n4) {
+            float4 v = qv[u], ww = wv[u];
+            const float4 a = av[u];
+            if constexpr (R1) {
+              const float4 z = zv[u];
+              v.x = fmaf(ku, z.x, v.x); v.y = fmaf(ku, z.y, v.y); v.z = fmaf(ku, z.z, v.z); v.w = fmaf(ku, z.w, v.w);
+            }
+            ww.x = fmaf(nlr, ((v.x * b) * a.x) * scale, ww.x);
+            ww.y = fmaf(nlr, ((v.y * b) * a.y) * scale, ww.y);
+            ww.z = fmaf(nlr, ((v.z * b) * a.z) * scale, ww.z);
+            ww.w = fmaf(nlr, ((v.w * b) * a.w) * scale, ww.w);
+            st4(w, k, ww);
+          }
+        }
       }
     } else {
       for (int64_t j = lane; j < d.cols; j += 64) {
@@ -450,6 +522,8 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
                 "matrix_step: param, grad, momentum, inv_row and inv_col are required");
     SMX_REQUIRE((d.z == nullptr) == (d.kappa == nullptr), SMX_EINVAL,
                 "matrix_step: z and kappa must both be set or both NULL");
+    SMX_REQUIRE((d.z == nullptr) == (descs[0].z == nullptr), SMX_EINVAL,
+                "matrix_step: either every matrix of a call has a rank-one term or none has");
     SMX_REQUIRE(d.rows >= 1 && d.cols >= 1, SMX_ESHAPE, "matrix_step: rows and cols must be >= 1");
     SMX_REQUIRE(d.grad_dtype == SMX_F32 || d.grad_dtype == SMX_BF16 || d.grad_dtype == SMX_F16, SMX_EDTYPE,
                 "matrix_step: grad dtype must be f32, bf16 or f16");
@@ -496,12 +570,19 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
       j.planes = 0;
       fin[k] = j;
     }
+    // The kernels are specialised on whether the matrices carry a rank-one
+    // term (all of a call or none, checked above).
+    const bool r1 = descs[0].z != nullptr;
     int rc = launch_jobs(ping, one_block, matrix_consts_kernel, 256, "matrix_consts", st);
-    if (!rc) rc = launch_jobs(ping, row_blocks, whiten_rows_kernel, kRowThreads, "whiten_rows", st);
-    if (!rc) rc = launch_jobs(ping, tile_blocks, whiten_tiles_kernel, 256, "whiten_tiles", st);
+    if (!rc) rc = r1 ? launch_jobs(ping, row_blocks, whiten_rows_kernel<true>, kRowThreads, "whiten_rows", st)
+                     : launch_jobs(ping, row_blocks, whiten_rows_kernel<false>, kRowThreads, "whiten_rows", st);
+    if (!rc) rc = r1 ? launch_jobs(ping, tile_blocks, whiten_tiles_kernel<true>, 256, "whiten_tiles", st)
+                     : launch_jobs(ping, tile_blocks, whiten_tiles_kernel<false>, 256, "whiten_tiles", st);
     if (!rc) rc = run_s8_stages(plan.layout, st);
-    if (!rc) rc = launch_jobs(fin, row_blocks, mapback_rows_kernel, kRowThreads, "mapback_rows", st);
-    if (!rc) rc = launch_jobs(fin, row_blocks, mapback_apply_kernel, kRowThreads, "mapback_apply", st);
+    if (!rc) rc = r1 ? launch_jobs(fin, row_blocks, mapback_rows_kernel<true>, kRowThreads, "mapback_rows", st)
+                     : launch_jobs(fin, row_blocks, mapback_rows_kernel<false>, kRowThreads, "mapback_rows", st);
+    if (!rc) rc = r1 ? launch_jobs(fin, row_blocks, mapback_apply_kernel<true>, kRowThreads, "mapback_apply", st)
+                     : launch_jobs(fin, row_blocks, mapback_apply_kernel<false>, kRowThreads, "mapback_apply", st);
     if (rc) return rc;
   }
   return SMX_OK;
