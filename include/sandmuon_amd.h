@@ -74,6 +74,34 @@ int smx_stats_accumulate(const void *x, int dtype, int64_t rows, int64_t cols,
                          int64_t row_stride, float *slots_sq,
                          float *slots_first, int32_t n_slots, void *stream);
 
+/* The statistics fused into passes a mixed-precision Linear makes anyway
+ * (the hook bodies above, moved; no counterpart entry point in the
+ * reference).  Both add sum(x^2) to slots_sq exactly as
+ * smx_stats_accumulate does, bit for bit.
+ *
+ * smx_stats_cast: the forward's fp32 -> bf16/f16 input cast (what autocast
+ * does before the GEMM) with the A statistic of sandmuon/optimizer.py:
+ * 156-168 taken from the same read.  x must be f32; out (out_dtype
+ * SMX_BF16 or SMX_F16, row stride out_stride) receives x rounded to nearest
+ * even.  slots_first may be NULL. */
+int smx_stats_cast(const void *x, int dtype, int64_t rows, int64_t cols,
+                   int64_t row_stride, float *slots_sq, float *slots_first,
+                   int32_t n_slots, void *out, int out_dtype,
+                   int64_t out_stride, void *stream);
+
+/* smx_stats_colsum: the backward's bias gradient, colsum[c] = sum over the
+ * rows of x (FP32 chunk partials folded in a fixed order in FP64), with
+ * the B statistic of sandmuon/optimizer.py:171-177 taken from the same
+ * read.  rows may be 0 (colsum becomes zero).  `workspace` holds
+ * smx_stats_colsum_workspace_bytes(cols, n_slots) bytes, 256-byte aligned,
+ * zero-filled before its first use; each call leaves it reusable.  Calls
+ * sharing a workspace must be ordered on one stream. */
+int64_t smx_stats_colsum_workspace_bytes(int64_t cols, int32_t n_slots);
+int smx_stats_colsum(const void *x, int dtype, int64_t rows, int64_t cols,
+                     int64_t row_stride, float *slots_sq, int32_t n_slots,
+                     float *colsum, void *workspace, int64_t workspace_bytes,
+                     void *stream);
+
 /* Fold: sum[c] += sum_p slots[p*n + c] (in FP64), then zero the slots.
  * Used when the running sums must be materialised outside a step (for
  * example before state_dict()).  first_* may be NULL. */

@@ -61,6 +61,11 @@ SIGNATURES = {
     "smx_last_error": (ctypes.c_char_p, []),
     "smx_stats_accumulate": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                      c_int32, c_void_p]),
+    "smx_stats_cast": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int32,
+                               c_void_p, c_int, c_int64, c_void_p]),
+    "smx_stats_colsum_workspace_bytes": (c_int64, [c_int64, c_int32]),
+    "smx_stats_colsum": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_int32, c_void_p,
+                                 c_void_p, c_int64, c_void_p]),
     "smx_stats_fold": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
     "smx_stats_finish": (c_int, [ctypes.POINTER(FinishDesc), c_int32, c_double, c_void_p]),
     "smx_adamw": (c_int, [ctypes.POINTER(AdamwDesc), c_int32, c_int64, c_double, c_double, c_double, c_double,
@@ -149,6 +154,32 @@ def stats_accumulate(rows2d: torch.Tensor, slots_sq: torch.Tensor, slots_first: 
                                     rows2d.shape[1], rows2d.stride(0), slots_sq.data_ptr(),
                                     ptr(slots_first), slots_sq.shape[0], stream_of(rows2d.device))
     _check(rc, "smx_stats_accumulate")
+
+
+def stats_cast(rows2d: torch.Tensor, slots_sq: torch.Tensor, slots_first: Optional[torch.Tensor],
+               out2d: torch.Tensor) -> None:
+    """A statistic of an fp32 [rows, cols] view plus its bf16/f16 copy in out2d."""
+    rc = lib().smx_stats_cast(rows2d.data_ptr(), dtype_code(rows2d.dtype), rows2d.shape[0], rows2d.shape[1],
+                              rows2d.stride(0), slots_sq.data_ptr(), ptr(slots_first), slots_sq.shape[0],
+                              out2d.data_ptr(), dtype_code(out2d.dtype), out2d.stride(0),
+                              stream_of(rows2d.device))
+    _check(rc, "smx_stats_cast")
+
+
+def stats_colsum_workspace_bytes(cols: int, n_slots: int) -> int:
+    n = lib().smx_stats_colsum_workspace_bytes(cols, n_slots)
+    _check(min(n, 0), "smx_stats_colsum_workspace_bytes")
+    return n
+
+
+def stats_colsum(rows2d: torch.Tensor, slots_sq: torch.Tensor, colsum: torch.Tensor,
+                 workspace: torch.Tensor) -> None:
+    """B statistic of a [rows, cols] view plus colsum = its column sums."""
+    rc = lib().smx_stats_colsum(rows2d.data_ptr(), dtype_code(rows2d.dtype), rows2d.shape[0], rows2d.shape[1],
+                                rows2d.stride(0), slots_sq.data_ptr(), slots_sq.shape[0], colsum.data_ptr(),
+                                workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                                stream_of(rows2d.device))
+    _check(rc, "smx_stats_colsum")
 
 
 def stats_fold(sum_sq, slots_sq, sum_first, slots_first) -> None:

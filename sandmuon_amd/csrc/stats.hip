@@ -65,14 +65,55 @@ struct VecLoad<SMX_BF16, 1> : VecLoad1<SMX_BF16> {};
 template <>
 struct VecLoad<SMX_F16, 1> : VecLoad1<SMX_F16> {};
 
+// What a launch produces besides sum(x^2) into the slot rows.
+enum StatsMode : int {
+  kSqOnly = 0,    // B side, diagonal A
+  kSqFirst = 1,   // rank-one A: sum(x) into its own slot rows
+  kSqColsum = 2,  // sum(x) of this call's rows into colsum (a bias gradient)
+};
+
+struct StatsArgs {
+  const void *x;
+  int64_t rows, cols, row_stride, rows_per_chunk;
+  float *slots_sq;
+  float *first;        // kSqFirst: slot rows of sum(x); kSqColsum: per-chunk partials
+  void *cast_out;      // CAST: low-precision copy of x
+  int64_t out_stride;
+  float *colsum;       // kSqColsum: [cols] sum of x over this call's rows
+  uint32_t *counters;  // kSqColsum: one arrival counter per column tile, 0 between calls
+};
+
+template <int CAST, int VEC>
+__device__ __forceinline__ void store_cast(void *out, int64_t i, const float *v) {
+  uint16_t h[VEC];
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    if constexpr (CAST == SMX_BF16) {
+      h[k] = f32_to_bf16_bits(v[k]);
+    } else {
+      const _Float16 f = static_cast<_Float16>(v[k]);
+      __builtin_memcpy(&h[k], &f, sizeof(f));
+    }
+  }
+  uint16_t *o = static_cast<uint16_t *>(out) + i;
+  if constexpr (VEC == 4) {
+    *reinterpret_cast<uint2 *>(o) = make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16),
+                                               h[2] | (static_cast<uint32_t>(h[3]) << 16));
+  } else {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = h[k];
+  }
+}
+
 // grid = (column tiles, row chunks); block = kStatsThreads.
 // A column tile is CT lanes x VEC channels; a wave covers 64/CT rows per
-// step, the block kStatsWaves*64/CT rows per step.
-template <int DT, int VEC, int CT, bool FIRST>
-__global__ void __launch_bounds__(kStatsThreads)
-stats_accumulate_kernel(const void *__restrict__ x, int64_t rows, int64_t cols,
-                        int64_t row_stride, int64_t rows_per_chunk,
-                        float *__restrict__ slots_sq, float *__restrict__ slots_first) {
+// step, the block kStatsWaves*64/CT rows per step.  CAST (SMX_BF16 or
+// SMX_F16, fp32 input only) also writes x converted, as the mixed-precision
+// cast in front of a Linear would.  MODE and CAST change nothing in how
+// sum(x^2) is formed, so every variant adds the same bits to the slots.
+template <int DT, int VEC, int CT, int MODE, int CAST>
+__global__ void __launch_bounds__(kStatsThreads) stats_accumulate_kernel(StatsArgs a) {
+  constexpr bool FIRST = MODE != kSqOnly;
   constexpr int RPW = 64 / CT;                 // rows per wave step
   constexpr int GROUPS = kStatsWaves * RPW;    // row groups per block
   constexpr int TW = CT * VEC;                 // channels per tile
@@ -83,10 +124,13 @@ stats_accumulate_kernel(const void *__restrict__ x, int64_t rows, int64_t cols,
   const int group = wave * RPW + lane / CT;
   const int64_t vcol = static_cast<int64_t>(blockIdx.x) * CT + (lane % CT);
   const int64_t col0 = vcol * VEC;
-  const int64_t r_begin = static_cast<int64_t>(blockIdx.y) * rows_per_chunk;
-  const int64_t r_end = min(rows, r_begin + rows_per_chunk);
-  if (r_begin >= r_end) return;  // whole block: nothing to add
-  const bool active = col0 < cols;
+  const int64_t r_begin = static_cast<int64_t>(blockIdx.y) * a.rows_per_chunk;
+  const int64_t r_end = min(a.rows, r_begin + a.rows_per_chunk);
+  const bool empty = r_begin >= r_end;
+  // An empty chunk adds nothing; with kSqColsum it still writes its zero
+  // partial and arrives at the counter.
+  if (MODE != kSqColsum && empty) return;
+  const bool active = col0 < a.cols;
 
   float acc_sq[VEC], acc_first[VEC];
 #pragma unroll
@@ -101,7 +145,7 @@ stats_accumulate_kernel(const void *__restrict__ x, int64_t rows, int64_t cols,
       float v[U][VEC];
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        VecLoad<DT, VEC>::load(x, (r + u * GROUPS) * row_stride + col0, v[u]);
+        VecLoad<DT, VEC>::load(a.x, (r + u * GROUPS) * a.row_stride + col0, v[u]);
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -109,15 +153,20 @@ stats_accumulate_kernel(const void *__restrict__ x, int64_t rows, int64_t cols,
           acc_sq[k] = fmaf(v[u][k], v[u][k], acc_sq[k]);
           if constexpr (FIRST) acc_first[k] += v[u][k];
         }
+      if constexpr (CAST != 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) store_cast<CAST, VEC>(a.cast_out, (r + u * GROUPS) * a.out_stride + col0, v[u]);
+      }
     }
     for (; r < r_end; r += GROUPS) {
       float v[VEC];
-      VecLoad<DT, VEC>::load(x, r * row_stride + col0, v);
+      VecLoad<DT, VEC>::load(a.x, r * a.row_stride + col0, v);
 #pragma unroll
       for (int k = 0; k < VEC; ++k) {
         acc_sq[k] = fmaf(v[k], v[k], acc_sq[k]);
         if constexpr (FIRST) acc_first[k] += v[k];
       }
+      if constexpr (CAST != 0) store_cast<CAST, VEC>(a.cast_out, r * a.out_stride + col0, v);
     }
   }
   const int cl = (lane % CT) * VEC;
@@ -128,47 +177,88 @@ stats_accumulate_kernel(const void *__restrict__ x, int64_t rows, int64_t cols,
   }
   __syncthreads();
   const int64_t tile_col0 = static_cast<int64_t>(blockIdx.x) * TW;
-  float *slot_sq = slots_sq + static_cast<int64_t>(blockIdx.y) * cols + tile_col0;
-  float *slot_first = FIRST ? slots_first + static_cast<int64_t>(blockIdx.y) * cols + tile_col0 : nullptr;
+  const int64_t row_off = static_cast<int64_t>(blockIdx.y) * a.cols + tile_col0;
+  float *slot_sq = a.slots_sq + row_off;
+  float *first = FIRST ? a.first + row_off : nullptr;
   for (int c = threadIdx.x; c < TW; c += kStatsThreads) {
-    if (tile_col0 + c >= cols) break;
+    if (tile_col0 + c >= a.cols) break;
     float s = 0.f, f = 0.f;
 #pragma unroll
     for (int g = 0; g < GROUPS; ++g) {
       s += red_sq[g][c];
       if constexpr (FIRST) f += red_first[g][c];
     }
-    slot_sq[c] += s;
-    if constexpr (FIRST) slot_first[c] += f;
+    if (!empty) slot_sq[c] += s;
+    if constexpr (MODE == kSqFirst) first[c] += f;
+    if constexpr (MODE == kSqColsum) first[c] = f;
+  }
+  if constexpr (MODE == kSqColsum) {
+    // The last block of this column tile to arrive folds the per-chunk
+    // partials in chunk order (FP64), so the sum does not depend on which
+    // block that is.  Release: every writer's fence before the barrier and
+    // the arrival; acquire: the fence after it.
+    __shared__ bool last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) last = atomicAdd(a.counters + blockIdx.x, 1u) == gridDim.y - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    for (int c = threadIdx.x; c < TW; c += kStatsThreads) {
+      const int64_t col = tile_col0 + c;
+      if (col >= a.cols) break;
+      double t = 0.0;
+      for (unsigned p = 0; p < gridDim.y; ++p) t += static_cast<double>(a.first[p * a.cols + col]);
+      a.colsum[col] = static_cast<float>(t);
+    }
+    if (threadIdx.x == 0) a.counters[blockIdx.x] = 0u;
   }
 }
 
-template <int DT, int VEC, int CT>
-static void launch_acc(const void *x, int64_t rows, int64_t cols, int64_t row_stride,
-                       float *slots_sq, float *slots_first, int32_t n_slots, hipStream_t st) {
-  const int64_t vcols = ceil_div(cols, VEC);
+template <int DT, int VEC, int CT, int MODE, int CAST>
+static void launch_acc(StatsArgs a, int32_t n_slots, hipStream_t st) {
+  const int64_t vcols = ceil_div(a.cols, VEC);
   dim3 grid(static_cast<unsigned>(ceil_div(vcols, CT)), static_cast<unsigned>(n_slots));
-  const int64_t rpc = ceil_div(rows, n_slots);
-  if (slots_first)
-    hipLaunchKernelGGL((stats_accumulate_kernel<DT, VEC, CT, true>), grid, dim3(kStatsThreads), 0, st,
-                       x, rows, cols, row_stride, rpc, slots_sq, slots_first);
-  else
-    hipLaunchKernelGGL((stats_accumulate_kernel<DT, VEC, CT, false>), grid, dim3(kStatsThreads), 0, st,
-                       x, rows, cols, row_stride, rpc, slots_sq, slots_first);
+  a.rows_per_chunk = ceil_div(a.rows, n_slots);
+  hipLaunchKernelGGL((stats_accumulate_kernel<DT, VEC, CT, MODE, CAST>), grid, dim3(kStatsThreads), 0, st, a);
 }
 
-template <int DT, int VEC>
-static void dispatch_ct(const void *x, int64_t rows, int64_t cols, int64_t row_stride,
-                        float *slots_sq, float *slots_first, int32_t n_slots, hipStream_t st) {
+// Column tiles of every width a launch may use have >= 16 channels.
+constexpr int kMinTileCols = 16;
+
+template <int DT, int VEC, int MODE, int CAST>
+static void dispatch_ct(const StatsArgs &a, int32_t n_slots, hipStream_t st) {
   // The widest column tile that still gives >= 6 tiles, so that a hook call
   // of 16K rows puts >= 768 blocks (24 waves per CU) in flight.
-  const int64_t vcols = ceil_div(cols, VEC);
+  const int64_t vcols = ceil_div(a.cols, VEC);
   if (vcols >= 6 * 64)
-    launch_acc<DT, VEC, 64>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+    launch_acc<DT, VEC, 64, MODE, CAST>(a, n_slots, st);
   else if (vcols >= 6 * 32)
-    launch_acc<DT, VEC, 32>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+    launch_acc<DT, VEC, 32, MODE, CAST>(a, n_slots, st);
   else
-    launch_acc<DT, VEC, 16>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
+    launch_acc<DT, VEC, 16, MODE, CAST>(a, n_slots, st);
+}
+
+template <int MODE, int CAST>
+static void dispatch_dtype(const StatsArgs &a, int dtype, int32_t n_slots, hipStream_t st) {
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(a.x);
+  if (dtype == SMX_F32) {
+    bool v4 = a.cols % 4 == 0 && a.row_stride % 4 == 0 && addr % 16 == 0;
+    if (CAST != 0) v4 = v4 && a.out_stride % 4 == 0 && reinterpret_cast<uintptr_t>(a.cast_out) % 8 == 0;
+    if (v4) dispatch_ct<SMX_F32, 4, MODE, CAST>(a, n_slots, st);
+    else dispatch_ct<SMX_F32, 1, MODE, CAST>(a, n_slots, st);
+    return;
+  }
+  if constexpr (CAST == 0) {
+    const bool v8 = a.cols % 8 == 0 && a.row_stride % 8 == 0 && addr % 16 == 0;
+    if (dtype == SMX_BF16) {
+      if (v8) dispatch_ct<SMX_BF16, 8, MODE, 0>(a, n_slots, st);
+      else dispatch_ct<SMX_BF16, 1, MODE, 0>(a, n_slots, st);
+    } else {
+      if (v8) dispatch_ct<SMX_F16, 8, MODE, 0>(a, n_slots, st);
+      else dispatch_ct<SMX_F16, 1, MODE, 0>(a, n_slots, st);
+    }
+  }
 }
 
 // ------------------------------------------------------------- fold ---
@@ -319,34 +409,80 @@ __global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta
 
 using namespace smx;
 
+static int check_rows(const char *who, const void *x, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
+                      const float *slots_sq, int32_t n_slots) {
+  const std::string w(who);
+  SMX_REQUIRE(rows >= 0 && cols >= 1, SMX_ESHAPE, w + ": need rows >= 0 and cols >= 1");
+  SMX_REQUIRE(rows == 0 || x, SMX_EINVAL, w + ": null input");
+  SMX_REQUIRE(rows == 0 || slots_sq, SMX_EINVAL, w + ": null slots_sq");
+  SMX_REQUIRE(row_stride >= cols || rows <= 1, SMX_ESHAPE, w + ": row_stride must be >= cols");
+  SMX_REQUIRE(n_slots >= 1 && n_slots <= 65535, SMX_EINVAL, w + ": n_slots in [1, 65535]");
+  SMX_REQUIRE(dtype == SMX_F32 || dtype == SMX_BF16 || dtype == SMX_F16, SMX_EDTYPE,
+              w + ": dtype must be f32, bf16 or f16");
+  return SMX_OK;
+}
+
 extern "C" int smx_stats_accumulate(const void *x, int dtype, int64_t rows, int64_t cols,
                                     int64_t row_stride, float *slots_sq, float *slots_first,
                                     int32_t n_slots, void *stream) {
-  SMX_REQUIRE(rows >= 0 && cols >= 1, SMX_ESHAPE, "stats_accumulate: need rows >= 0 and cols >= 1");
+  int rc = check_rows("stats_accumulate", x, dtype, rows, cols, row_stride, slots_sq, n_slots);
+  if (rc) return rc;
   if (rows == 0) return SMX_OK;  // empty microbatch: nothing to add
-  SMX_REQUIRE(x && slots_sq, SMX_EINVAL, "stats_accumulate: null pointer");
-  SMX_REQUIRE(row_stride >= cols || rows == 1, SMX_ESHAPE, "stats_accumulate: row_stride must be >= cols");
-  SMX_REQUIRE(n_slots >= 1 && n_slots <= 65535, SMX_EINVAL, "stats_accumulate: n_slots in [1, 65535]");
-  SMX_REQUIRE(dtype == SMX_F32 || dtype == SMX_BF16 || dtype == SMX_F16, SMX_EDTYPE,
-              "stats_accumulate: dtype must be f32, bf16 or f16");
+  const StatsArgs a{x, rows, cols, row_stride, 0, slots_sq, slots_first, nullptr, 0, nullptr, nullptr};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const uintptr_t addr = reinterpret_cast<uintptr_t>(x);
-  if (dtype == SMX_F32) {
-    if (cols % 4 == 0 && row_stride % 4 == 0 && addr % 16 == 0)
-      dispatch_ct<SMX_F32, 4>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
-    else
-      dispatch_ct<SMX_F32, 1>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
-  } else {
-    const bool v8 = cols % 8 == 0 && row_stride % 8 == 0 && addr % 16 == 0;
-    if (dtype == SMX_BF16) {
-      if (v8) dispatch_ct<SMX_BF16, 8>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
-      else dispatch_ct<SMX_BF16, 1>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
-    } else {
-      if (v8) dispatch_ct<SMX_F16, 8>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
-      else dispatch_ct<SMX_F16, 1>(x, rows, cols, row_stride, slots_sq, slots_first, n_slots, st);
-    }
-  }
+  if (slots_first) dispatch_dtype<kSqFirst, 0>(a, dtype, n_slots, st);
+  else dispatch_dtype<kSqOnly, 0>(a, dtype, n_slots, st);
   return check_launch("stats_accumulate");
+}
+
+extern "C" int smx_stats_cast(const void *x, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
+                              float *slots_sq, float *slots_first, int32_t n_slots, void *out,
+                              int out_dtype, int64_t out_stride, void *stream) {
+  int rc = check_rows("stats_cast", x, dtype, rows, cols, row_stride, slots_sq, n_slots);
+  if (rc) return rc;
+  SMX_REQUIRE(dtype == SMX_F32, SMX_EDTYPE, "stats_cast: the input must be f32");
+  SMX_REQUIRE(out_dtype == SMX_BF16 || out_dtype == SMX_F16, SMX_EDTYPE, "stats_cast: out_dtype must be bf16 or f16");
+  SMX_REQUIRE(rows == 0 || out, SMX_EINVAL, "stats_cast: null output");
+  SMX_REQUIRE(out_stride >= cols || rows <= 1, SMX_ESHAPE, "stats_cast: out_stride must be >= cols");
+  if (rows == 0) return SMX_OK;
+  const StatsArgs a{x, rows, cols, row_stride, 0, slots_sq, slots_first, out, out_stride, nullptr, nullptr};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (out_dtype == SMX_BF16) {
+    if (slots_first) dispatch_dtype<kSqFirst, SMX_BF16>(a, dtype, n_slots, st);
+    else dispatch_dtype<kSqOnly, SMX_BF16>(a, dtype, n_slots, st);
+  } else {
+    if (slots_first) dispatch_dtype<kSqFirst, SMX_F16>(a, dtype, n_slots, st);
+    else dispatch_dtype<kSqOnly, SMX_F16>(a, dtype, n_slots, st);
+  }
+  return check_launch("stats_cast");
+}
+
+static int64_t colsum_partial_bytes(int64_t cols, int32_t n_slots) {
+  return round_up(static_cast<int64_t>(n_slots) * cols * 4, 256);
+}
+
+extern "C" int64_t smx_stats_colsum_workspace_bytes(int64_t cols, int32_t n_slots) {
+  if (cols < 1 || n_slots < 1) return -1;
+  return colsum_partial_bytes(cols, n_slots) + round_up(ceil_div(cols, kMinTileCols) * 4, 256);
+}
+
+extern "C" int smx_stats_colsum(const void *x, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
+                                float *slots_sq, int32_t n_slots, float *colsum, void *workspace,
+                                int64_t workspace_bytes, void *stream) {
+  int rc = check_rows("stats_colsum", x, dtype, rows, cols, row_stride, slots_sq, n_slots);
+  if (rc) return rc;
+  SMX_REQUIRE(slots_sq && colsum && workspace, SMX_EINVAL, "stats_colsum: null slots_sq, colsum or workspace");
+  const int64_t need = smx_stats_colsum_workspace_bytes(cols, n_slots);
+  SMX_REQUIRE(workspace_bytes >= need, SMX_EWORKSPACE,
+              "stats_colsum: workspace of " + std::to_string(workspace_bytes) + " bytes, need " + std::to_string(need));
+  SMX_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, SMX_EALIGN, "stats_colsum: workspace must be 256-byte aligned");
+  char *ws = static_cast<char *>(workspace);
+  float *partial = reinterpret_cast<float *>(ws);
+  uint32_t *counters = reinterpret_cast<uint32_t *>(ws + colsum_partial_bytes(cols, n_slots));
+  // rows == 0 still launches: every chunk is empty and colsum becomes zero.
+  const StatsArgs a{x, rows, cols, rows ? row_stride : cols, 0, slots_sq, partial, nullptr, 0, colsum, counters};
+  dispatch_dtype<kSqColsum, 0>(a, dtype, n_slots, static_cast<hipStream_t>(stream));
+  return check_launch("stats_colsum");
 }
 
 extern "C" int smx_stats_fold(float *sum_sq, float *slots_sq, float *sum_first, float *slots_first,

@@ -233,10 +233,17 @@ class DiagonalWeightedPE(Optimizer):
         self.register_state_dict_pre_hook(DiagonalWeightedPE._flush_slots)
         self.register_load_state_dict_post_hook(DiagonalWeightedPE._drop_slots)
         self.handles = []
+        self._matrix_modules = modules
+        self._hook_handles = {}
+        self._fused = None
         for name, module in modules.items():
-            parameter = matrices[name]
-            self.handles.append(module.register_forward_hook(
-                self._capture(parameter, capture_a=self.a_sources[id(parameter)] is parameter)))
+            self._hook_handles[name] = self._install_hook(name)
+            self.handles.append(self._hook_handles[name])
+
+    def _install_hook(self, name: str):
+        parameter = self.named_matrices[name]
+        return self._matrix_modules[name].register_forward_hook(
+            self._capture(parameter, capture_a=self.a_sources[id(parameter)] is parameter))
 
     # ------------------------------------------------------------ hooks ---
     def _slot_pair(self, parameter, side: str, n: int, device, first: bool):
@@ -249,17 +256,27 @@ class DiagonalWeightedPE(Optimizer):
             self._slots[key] = entry
         return entry[1], entry[2]
 
+    def _a_slots(self, parameter, n: int, device, state: dict):
+        """State entries and slot rows the A statistic of `parameter` adds into."""
+        if "a_sum" not in state:
+            state["a_sum"] = torch.zeros(n, device=device, dtype=torch.float32)
+            state["a_count"] = 0
+            if self.rank_one_a:
+                state["a_first_sum"] = torch.zeros_like(state["a_sum"])
+        return self._slot_pair(parameter, "a", n, device, self.rank_one_a)
+
+    def _b_slots(self, parameter, n: int, device, state: dict) -> torch.Tensor:
+        if "b_sum" not in state:
+            state["b_sum"] = torch.zeros(n, device=device, dtype=torch.float32)
+            state["b_count"] = 0
+        return self._slot_pair(parameter, "b", n, device, False)[0]
+
     def _accumulate_a(self, parameter, x: torch.Tensor, state: Optional[dict] = None) -> None:
         """Forward-hook body (sandmuon/optimizer.py:156-168): a_sum += sum x^2,
         a_first_sum += sum x (rank-one), a_count += rows."""
         state = self.state[parameter] if state is None else state
         rows = _rows2d(x)
-        if "a_sum" not in state:
-            state["a_sum"] = torch.zeros(rows.shape[-1], device=rows.device, dtype=torch.float32)
-            state["a_count"] = 0
-            if self.rank_one_a:
-                state["a_first_sum"] = torch.zeros_like(state["a_sum"])
-        sq, fs = self._slot_pair(parameter, "a", rows.shape[-1], rows.device, self.rank_one_a)
+        sq, fs = self._a_slots(parameter, rows.shape[-1], rows.device, state)
         _native.stats_accumulate(rows, sq, fs)
         state["a_count"] += rows.shape[0]
 
@@ -267,10 +284,7 @@ class DiagonalWeightedPE(Optimizer):
         """Cotangent-hook body (sandmuon/optimizer.py:171-177): b_sum += sum delta^2."""
         state = self.state[parameter] if state is None else state
         rows = _rows2d(delta)
-        if "b_sum" not in state:
-            state["b_sum"] = torch.zeros(rows.shape[-1], device=rows.device, dtype=torch.float32)
-            state["b_count"] = 0
-        sq, _ = self._slot_pair(parameter, "b", rows.shape[-1], rows.device, False)
+        sq = self._b_slots(parameter, rows.shape[-1], rows.device, state)
         _native.stats_accumulate(rows, sq, None)
         state["b_count"] += rows.shape[0]
 
@@ -467,6 +481,8 @@ class DiagonalWeightedPE(Optimizer):
             _native.adamw(descs, offset, lr, b1, b2, group["adamw_eps"], group["weight_decay"], device)
 
     def close(self):
+        if self._fused is not None:
+            self._fused.close()
         for handle in self.handles:
             handle.remove()
         self.handles.clear()

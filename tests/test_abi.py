@@ -87,6 +87,19 @@ def test_validation_errors_return_before_gpu_work():
     # finish: bad kind
     f = _native.FinishDesc(sum_sq=16, slots_sq=16, ema=16, inv=16, n=4, count=1, n_slots=1, kind=5)
     assert lib.smx_stats_finish((_native.FinishDesc * 1)(f), 1, .97, None) == -1
+    # fused statistics: the cast takes f32 input and a bf16/f16 output only
+    assert lib.smx_stats_cast(ctypes.c_void_p(16), 1, 4, 4, 4, ctypes.c_void_p(16), None, 1, ctypes.c_void_p(16), 1,
+                              4, None) == -3
+    assert lib.smx_stats_cast(ctypes.c_void_p(16), 0, 4, 4, 4, ctypes.c_void_p(16), None, 1, ctypes.c_void_p(16), 0,
+                              4, None) == -3
+    assert lib.smx_stats_cast(None, 0, 0, 4, 4, ctypes.c_void_p(16), None, 1, None, 1, 4, None) == 0
+    need = lib.smx_stats_colsum_workspace_bytes(768, 128)
+    assert need >= 128 * 768 * 4 + 768 // 16 * 4 and need % 256 == 0
+    assert lib.smx_stats_colsum_workspace_bytes(0, 128) == -1
+    assert lib.smx_stats_colsum(ctypes.c_void_p(16), 1, 4, 768, 768, ctypes.c_void_p(16), 128, ctypes.c_void_p(16),
+                                ctypes.c_void_p(256), need - 1, None) == -5
+    assert lib.smx_stats_colsum(ctypes.c_void_p(16), 1, 4, 768, 768, ctypes.c_void_p(16), 128, ctypes.c_void_p(16),
+                                ctypes.c_void_p(16), need, None) == -4
     # adamw: offsets must be prefix sums
     a = _native.AdamwDesc(param=16, grad=16, exp_avg=16, exp_avg_sq=16, n=4, offset=3, bias1=.1, bias2=.1)
     assert lib.smx_adamw((_native.AdamwDesc * 1)(a), 1, 4, 1e-3, .9, .999, 1e-8, .01, None) == -2

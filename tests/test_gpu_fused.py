@@ -1,0 +1,212 @@
+"""Statistics fused into the Linear's input cast and bias-gradient passes
+(sandmuon_amd.fused) against the hook path and torch's own layer.
+
+* smx_stats_cast: the low-precision copy equals torch's cast bit for bit and
+  the slot rows equal smx_stats_accumulate's bit for bit;
+* smx_stats_colsum: the slot rows equal smx_stats_accumulate's bit for bit;
+  the column sums match an FP64 reference (rel. <= 1e-6);
+* a fused nn.Linear under bf16 autocast gives torch's output, input gradient
+  and weight gradient bit for bit, and the bias gradient within the bf16
+  rounding torch's own bias gradient carries;
+* a GPT step with fused statistics gives the hook path's statistics and
+  matrix updates bit for bit.
+"""
+import copy
+
+import pytest
+import torch
+from torch import nn
+
+from sandmuon_amd import RankOneAWeightedPE, _native
+from sandmuon_amd.fused import fuse_statistics
+from sandmuon_amd.workloads import GPT, GPTConfig, transformer_filter
+
+pytestmark = pytest.mark.gpu
+
+SLOTS = 128
+
+
+def fp64_colsum(x2d):
+    return x2d.double().sum(0)
+
+
+def rel(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-300)).item()
+
+
+@pytest.mark.parametrize("rows,cols", [(16384, 768), (16384, 3072), (7, 5), (1000, 96), (33, 100)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("first", [True, False])
+def test_stats_cast_matches_torch_cast_and_hook_slots(device, rows, cols, out_dtype, first):
+    g = torch.Generator(device=device).manual_seed(rows + cols)
+    x = torch.randn(rows, cols, generator=g, device=device) * 3 + 0.5
+    ref_sq = torch.zeros(SLOTS, cols, device=device)
+    ref_fs = torch.zeros(SLOTS, cols, device=device) if first else None
+    _native.stats_accumulate(x, ref_sq, ref_fs)
+    sq = torch.zeros(SLOTS, cols, device=device)
+    fs = torch.zeros(SLOTS, cols, device=device) if first else None
+    out = torch.empty(rows, cols, dtype=out_dtype, device=device)
+    _native.stats_cast(x, sq, fs, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), x.to(out_dtype).view(torch.int16))
+    assert torch.equal(sq, ref_sq)
+    if first:
+        assert torch.equal(fs, ref_fs)
+
+
+def test_stats_cast_strided_rows(device):
+    base = torch.randn(300, 130, device=device)
+    x = base[:, :128]  # row stride 130
+    out_base = torch.empty(300, 136, dtype=torch.bfloat16, device=device)
+    out = out_base[:, :128]
+    sq, ref = torch.zeros(SLOTS, 128, device=device), torch.zeros(SLOTS, 128, device=device)
+    _native.stats_cast(x, sq, None, out)
+    _native.stats_accumulate(x, ref, None)
+    torch.cuda.synchronize()
+    assert torch.equal(out, x.to(torch.bfloat16)) and torch.equal(sq, ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("rows,cols", [(16384, 768), (16384, 3072), (0, 64), (1, 16), (130, 100), (33, 7)])
+def test_stats_colsum_matches_fp64_and_hook_slots(device, dtype, rows, cols):
+    g = torch.Generator(device=device).manual_seed(7 * rows + cols)
+    x = (torch.randn(rows, cols, generator=g, device=device) * 1e-3 + 2e-4).to(dtype)
+    ws = torch.zeros(_native.stats_colsum_workspace_bytes(cols, SLOTS), dtype=torch.uint8, device=device)
+    sq, ref = torch.zeros(SLOTS, cols, device=device), torch.zeros(SLOTS, cols, device=device)
+    colsum = torch.full((cols,), float("nan"), device=device)
+    for rep in range(2):  # the workspace is reused: its counters must come back to zero
+        _native.stats_colsum(x, sq, colsum, ws)
+        if rows:
+            _native.stats_accumulate(x, ref, None)
+        torch.cuda.synchronize()
+        assert torch.equal(sq, ref), rep
+        want = fp64_colsum(x)
+        if rows == 0:
+            assert torch.equal(colsum, torch.zeros(cols, device=device))
+        else:
+            assert rel(colsum, want) <= 1e-6, rep
+            # elementwise: within FP32 rounding of the magnitudes summed
+            bound = 1e-6 * x.double().abs().sum(0) + 1e-30
+            assert ((colsum.double() - want).abs() <= bound).all()
+
+
+def _native_linear(lin, x, dy):
+    lin = copy.deepcopy(lin)
+    x = x.detach().clone().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = lin(x)
+    y.backward(dy)
+    return y.detach(), x.grad, lin.weight.grad, None if lin.bias is None else lin.bias.grad
+
+
+@pytest.mark.parametrize("bias", [True, False])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16])
+def test_fused_linear_matches_autocast_linear(device, bias, in_dtype):
+    torch.manual_seed(5)
+
+    class Net(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.fc = nn.Linear(768, 3072, bias=bias)
+
+    net = Net().to(device)
+    ref_fc = copy.deepcopy(net.fc)
+    opt = RankOneAWeightedPE(net, 1e-2)
+    handle = fuse_statistics(opt)
+    assert handle.fused_names == ["fc.weight"] and opt.handles == []
+    x = (torch.randn(4, 1024, 768, device=device) + 0.3).to(in_dtype)
+    dy = (torch.randn(4, 1024, 3072, device=device) * 1e-3).bfloat16()
+    ry, rdx, rdw, rdb = _native_linear(ref_fc, x, dy)
+    xx = x.detach().clone().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = net.fc(xx)
+    y.backward(dy)
+    torch.cuda.synchronize()
+    assert y.dtype == ry.dtype and torch.equal(y, ry)
+    assert xx.grad.dtype == rdx.dtype and torch.equal(xx.grad, rdx)
+    assert torch.equal(net.fc.weight.grad, rdw)
+    if bias:
+        want = fp64_colsum(dy.reshape(-1, 3072).float())
+        assert net.fc.bias.grad.dtype == torch.float32
+        assert rel(net.fc.bias.grad, want) <= 1e-6
+        # torch's bias gradient is the bf16-rounded sum
+        assert ((net.fc.bias.grad - rdb).abs() <= rdb.abs() * 2 ** -8 + 1e-6).all()
+    # the statistics are the hooks' own
+    st = opt.state[net.fc.weight]
+    assert st["a_count"] == st["b_count"] == 4096
+    handle.close()
+    assert len(opt.handles) == 1 and "forward" not in net.fc.__dict__
+    opt.close()
+
+
+def _gpt_pair(device, cfg, seed):
+    model = GPT(cfg)
+    model.init_weights(seed)
+    model = model.to(device)
+    twin = copy.deepcopy(model)
+    a = RankOneAWeightedPE(model, 1e-2, module_filter=transformer_filter)
+    b = RankOneAWeightedPE(twin, 1e-2, module_filter=transformer_filter)
+    return model, twin, a, b
+
+
+def test_fused_gpt_step_equals_hook_step(device):
+    cfg = GPTConfig(vocab=257, ctx=128, layers=2, width=256, heads=4, mlp=1024)
+    model, twin, hooked, fused_opt = _gpt_pair(device, cfg, 11)
+    handle = fuse_statistics(fused_opt)
+    assert len(handle.fused_names) == 12 and fused_opt.handles == []
+    g = torch.Generator().manual_seed(12)
+    gm, gt = dict(model.named_parameters()), dict(twin.named_parameters())
+    # Test-only tensor hooks on the fused layers' outputs record the
+    # cotangents (the fused layers themselves use no hooks).
+    captured = {}
+    for name in handle.fused_names:
+        module = dict(twin.named_modules())[name[: -len(".weight")]]
+        store = captured.setdefault(name[: -len("weight")] + "bias", [])
+
+        def fwd_hook(mod, inputs, output, store=store):
+            output.register_hook(lambda grad: store.append(grad.detach().clone()))
+        module.register_forward_hook(fwd_hook)
+    for step in range(2):
+        # The biases take slightly different AdamW steps (their gradients
+        # differ in rounding); start every step from the same parameters.
+        with torch.no_grad():
+            for n, p in gm.items():
+                gt[n].copy_(p)
+        for opt in (hooked, fused_opt):
+            opt.zero_grad(set_to_none=True)
+        for mb in range(3):
+            idx = torch.randint(0, cfg.vocab, (4, cfg.ctx), generator=g).to(device)
+            tgt = torch.randint(0, cfg.vocab, (4, cfg.ctx), generator=g).to(device)
+            for m in (model, twin):
+                with torch.autocast("cuda", dtype=torch.bfloat16):
+                    loss = m(idx, tgt) / 3
+                loss.backward()
+        for n in hooked.named_matrices:
+            assert torch.equal(gm[n].grad, gt[n].grad), n
+        # Linear biases: the fused gradient is the FP32 column sum of the
+        # captured cotangents, torch's the bf16-rounded one.  Both are held
+        # against the FP64 sum: the fused one within FP32 rounding of the
+        # magnitudes summed, and never further from it than torch's.
+        for name, deltas in captured.items():
+            d = torch.cat([t.reshape(-1, t.shape[-1]) for t in deltas]).double()
+            want, mag = d.sum(0), d.abs().sum(0)
+            err_fused = (gt[name].grad.double() - want).abs()
+            err_torch = (gm[name].grad.double() - want).abs()
+            assert (err_fused <= 1e-6 * mag + 1e-30).all(), name
+            assert err_fused.max() <= err_torch.max(), name
+            deltas.clear()
+        hooked.step()
+        fused_opt.step()
+        torch.cuda.synchronize()
+        for n, p in hooked.named_matrices.items():
+            q = fused_opt.named_matrices[n]
+            sa, sb = hooked.state[p], fused_opt.state[q]
+            for key in ("a_ema", "a_mean_ema", "b_ema"):
+                if key in sa:
+                    assert torch.equal(sa[key], sb[key]), (step, n, key)
+            assert torch.equal(p, q), (step, n)
+    handle.close()
+    assert len(fused_opt.handles) == 12
+    hooked.close()
+    fused_opt.close()
