@@ -41,6 +41,10 @@ def parse():
     ap.add_argument("--s8-mode", default="comp_bf16", choices=["comp_bf16", "fp32"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: all cores in the affinity mask")
+    ap.add_argument("--train", action="store_true",
+                    help="time whole training steps instead (model forward/backward of 8 microbatches under bf16 "
+                         "autocast + step()), with the hook statistics, with the fused statistics, and with "
+                         "no statistics; prints its own JSON line")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run 3 plain device copies of MB megabytes (the known-size reference for "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -189,6 +193,80 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def train_bench(args, device):
+    """Whole training steps of the cfg4 GPT: 8 microbatches of 16 x 1024
+    random tokens, forward and backward under bf16 autocast, then step().
+    Three variants on the same model and optimizer: the statistics in the
+    hooks (the reference's design), fused into the Linear's input cast and
+    bias-gradient passes (sandmuon_amd.fused), and none at all (hooks
+    removed, forward/backward only) as the floor both are measured against."""
+    from sandmuon_amd import RankOneAWeightedPE
+    from sandmuon_amd.fused import fuse_statistics
+    from sandmuon_amd.workloads import GPT, GPT_103M, transformer_filter
+    model = GPT(GPT_103M).to(device)
+    model.init_weights(1337)
+    opt = RankOneAWeightedPE(model, lr=1e-4, module_filter=transformer_filter, s8_mode=args.s8_mode)
+    g = torch.Generator(device=device).manual_seed(1337)
+    micro = [(torch.randint(0, GPT_103M.vocab, (16, 1024), generator=g, device=device),
+              torch.randint(0, GPT_103M.vocab, (16, 1024), generator=g, device=device)) for _ in range(8)]
+
+    def fwd_bwd():
+        for idx, tgt in micro:
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss = model(idx, tgt) / len(micro)
+            loss.backward()
+
+    def timed(with_step):
+        def once(ev=None):
+            opt.zero_grad(set_to_none=True)
+            if ev:
+                ev[0].record()
+            fwd_bwd()
+            if ev:
+                ev[1].record()
+            if with_step:
+                opt.step()
+            if ev:
+                ev[2].record()
+        for _ in range(args.warmup):
+            once()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        for k in range(args.steps):
+            once(evs[k])
+        torch.cuda.synchronize()
+        fb = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+        st = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+        return round(fb + st, 3), round(fb, 3), round(st, 3)
+
+    log("train: hook statistics")
+    hooks = timed(True)
+    log(f"train: hooks {hooks}")
+    handle = fuse_statistics(opt)
+    log(f"train: fused statistics ({len(handle.fused_names)} layers)")
+    fused = timed(True)
+    log(f"train: fused {fused}")
+    handle.close()
+    opt.close()
+    log("train: no statistics (forward/backward only)")
+    floor = timed(False)
+    log(f"train: floor {floor}")
+    out = {
+        "metric": "training step ms (103M GPT: 8 x 16x1024-token microbatches fwd+bwd under bf16 autocast + "
+                  "SandMuon step), 1 GPU",
+        "value": fused[0], "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": fused[0], "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "cfg4 training step with fused statistics", "s8_mode": args.s8_mode,
+                   "matrices": len(opt.named_matrices), "microbatches": len(micro)},
+        "variants_ms": {"hooks": {"total": hooks[0], "fwd_bwd": hooks[1], "step": hooks[2]},
+                        "fused": {"total": fused[0], "fwd_bwd": fused[1], "step": fused[2]},
+                        "no_statistics_fwd_bwd": floor[1]},
+        "statistics_cost_ms": {"hooks": round(hooks[1] - floor[1], 3), "fused": round(fused[1] - floor[1], 3)},
+    }
+    print(json.dumps(out), flush=True)
+
+
 # ---------------------------------------------------------------- main ---
 def main():
     args = parse()
@@ -205,6 +283,11 @@ def main():
     from sandmuon_amd import _native
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    if args.train:
+        if args.config != "gpt103m":
+            sys.exit("--train runs the cfg4 (gpt103m) model only")
+        train_bench(args, device)
+        return
     log(f"building {args.config} ({args.s8_mode})")
     model, opt, sets, micro, stat_bytes = build(args.config, args.s8_mode, device)
     log(f"built: {len(opt.named_matrices)} matrices, {stat_bytes / 1e9:.2f} GB of hook input per step")

@@ -90,12 +90,12 @@ int smx_stats_cast(const void *x, int dtype, int64_t rows, int64_t cols,
                    int64_t out_stride, void *stream);
 
 /* smx_stats_colsum: the backward's bias gradient, colsum[c] = sum over the
- * rows of x (FP32 chunk partials folded in a fixed order in FP64), with
- * the B statistic of sandmuon/optimizer.py:171-177 taken from the same
- * read.  rows may be 0 (colsum becomes zero).  `workspace` holds
- * smx_stats_colsum_workspace_bytes(cols, n_slots) bytes, 256-byte aligned,
- * zero-filled before its first use; each call leaves it reusable.  Calls
- * sharing a workspace must be ordered on one stream. */
+ * rows of x, with the B statistic of sandmuon/optimizer.py:171-177 taken
+ * from the same read.  The read writes one FP32 partial per row chunk into
+ * `workspace` (smx_stats_colsum_workspace_bytes(cols, n_slots) bytes,
+ * 256-byte aligned); a second, small launch folds them in a fixed order in
+ * FP64.  rows may be 0 (colsum becomes zero).  Calls sharing a workspace
+ * must be ordered on one stream. */
 int64_t smx_stats_colsum_workspace_bytes(int64_t cols, int32_t n_slots);
 int smx_stats_colsum(const void *x, int dtype, int64_t rows, int64_t cols,
                      int64_t row_stride, float *slots_sq, int32_t n_slots,

@@ -69,18 +69,16 @@ struct VecLoad<SMX_F16, 1> : VecLoad1<SMX_F16> {};
 enum StatsMode : int {
   kSqOnly = 0,    // B side, diagonal A
   kSqFirst = 1,   // rank-one A: sum(x) into its own slot rows
-  kSqColsum = 2,  // sum(x) of this call's rows into colsum (a bias gradient)
+  kSqColsum = 2,  // sum(x) of this call's rows into per-chunk partials (a bias gradient)
 };
 
 struct StatsArgs {
   const void *x;
   int64_t rows, cols, row_stride, rows_per_chunk;
   float *slots_sq;
-  float *first;        // kSqFirst: slot rows of sum(x); kSqColsum: per-chunk partials
+  float *first;        // kSqFirst: slot rows of sum(x); kSqColsum: per-chunk partials, plain stores
   void *cast_out;      // CAST: low-precision copy of x
   int64_t out_stride;
-  float *colsum;       // kSqColsum: [cols] sum of x over this call's rows
-  uint32_t *counters;  // kSqColsum: one arrival counter per column tile, 0 between calls
 };
 
 template <int CAST, int VEC>
@@ -128,7 +126,7 @@ __global__ void __launch_bounds__(kStatsThreads) stats_accumulate_kernel(StatsAr
   const int64_t r_end = min(a.rows, r_begin + a.rows_per_chunk);
   const bool empty = r_begin >= r_end;
   // An empty chunk adds nothing; with kSqColsum it still writes its zero
-  // partial and arrives at the counter.
+  // partial.
   if (MODE != kSqColsum && empty) return;
   const bool active = col0 < a.cols;
 
@@ -192,27 +190,6 @@ __global__ void __launch_bounds__(kStatsThreads) stats_accumulate_kernel(StatsAr
     if constexpr (MODE == kSqFirst) first[c] += f;
     if constexpr (MODE == kSqColsum) first[c] = f;
   }
-  if constexpr (MODE == kSqColsum) {
-    // The last block of this column tile to arrive folds the per-chunk
-    // partials in chunk order (FP64), so the sum does not depend on which
-    // block that is.  Release: every writer's fence before the barrier and
-    // the arrival; acquire: the fence after it.
-    __shared__ bool last;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(a.counters + blockIdx.x, 1u) == gridDim.y - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    for (int c = threadIdx.x; c < TW; c += kStatsThreads) {
-      const int64_t col = tile_col0 + c;
-      if (col >= a.cols) break;
-      double t = 0.0;
-      for (unsigned p = 0; p < gridDim.y; ++p) t += static_cast<double>(a.first[p * a.cols + col]);
-      a.colsum[col] = static_cast<float>(t);
-    }
-    if (threadIdx.x == 0) a.counters[blockIdx.x] = 0u;
-  }
 }
 
 template <int DT, int VEC, int CT, int MODE, int CAST>
@@ -222,9 +199,6 @@ static void launch_acc(StatsArgs a, int32_t n_slots, hipStream_t st) {
   a.rows_per_chunk = ceil_div(a.rows, n_slots);
   hipLaunchKernelGGL((stats_accumulate_kernel<DT, VEC, CT, MODE, CAST>), grid, dim3(kStatsThreads), 0, st, a);
 }
-
-// Column tiles of every width a launch may use have >= 16 channels.
-constexpr int kMinTileCols = 16;
 
 template <int DT, int VEC, int MODE, int CAST>
 static void dispatch_ct(const StatsArgs &a, int32_t n_slots, hipStream_t st) {
@@ -259,6 +233,34 @@ static void dispatch_dtype(const StatsArgs &a, int dtype, int32_t n_slots, hipSt
       else dispatch_ct<SMX_F16, 1, MODE, 0>(a, n_slots, st);
     }
   }
+}
+
+// colsum[c] = sum over the n_parts partial rows (stride cols) in FP64.
+// grid = ceil(cols / 64) blocks of 256: wave w sums rows w, w+4, ... of 64
+// columns (one 256-byte row segment per load, 8 loads in flight); the four
+// wave sums are added in wave order, so the result is deterministic.
+__global__ void __launch_bounds__(256)
+colsum_fold_kernel(const float *__restrict__ partial, int64_t cols, int32_t n_parts, float *__restrict__ colsum) {
+  constexpr int kFold = 8;
+  __shared__ double part[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  double t = 0.0;
+  if (c < cols) {
+    int p = wave;
+    for (; p + 4 * (kFold - 1) < n_parts; p += 4 * kFold) {
+      float v[kFold];
+#pragma unroll
+      for (int u = 0; u < kFold; ++u) v[u] = partial[static_cast<int64_t>(p + 4 * u) * cols + c];
+#pragma unroll
+      for (int u = 0; u < kFold; ++u) t += static_cast<double>(v[u]);
+    }
+    for (; p < n_parts; p += 4) t += static_cast<double>(partial[static_cast<int64_t>(p) * cols + c]);
+  }
+  part[wave][lane] = t;
+  __syncthreads();
+  if (wave == 0 && c < cols)
+    colsum[c] = static_cast<float>((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
 }
 
 // ------------------------------------------------------------- fold ---
@@ -428,7 +430,7 @@ extern "C" int smx_stats_accumulate(const void *x, int dtype, int64_t rows, int6
   int rc = check_rows("stats_accumulate", x, dtype, rows, cols, row_stride, slots_sq, n_slots);
   if (rc) return rc;
   if (rows == 0) return SMX_OK;  // empty microbatch: nothing to add
-  const StatsArgs a{x, rows, cols, row_stride, 0, slots_sq, slots_first, nullptr, 0, nullptr, nullptr};
+  const StatsArgs a{x, rows, cols, row_stride, 0, slots_sq, slots_first, nullptr, 0};
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (slots_first) dispatch_dtype<kSqFirst, 0>(a, dtype, n_slots, st);
   else dispatch_dtype<kSqOnly, 0>(a, dtype, n_slots, st);
@@ -445,7 +447,7 @@ extern "C" int smx_stats_cast(const void *x, int dtype, int64_t rows, int64_t co
   SMX_REQUIRE(rows == 0 || out, SMX_EINVAL, "stats_cast: null output");
   SMX_REQUIRE(out_stride >= cols || rows <= 1, SMX_ESHAPE, "stats_cast: out_stride must be >= cols");
   if (rows == 0) return SMX_OK;
-  const StatsArgs a{x, rows, cols, row_stride, 0, slots_sq, slots_first, out, out_stride, nullptr, nullptr};
+  const StatsArgs a{x, rows, cols, row_stride, 0, slots_sq, slots_first, out, out_stride};
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (out_dtype == SMX_BF16) {
     if (slots_first) dispatch_dtype<kSqFirst, SMX_BF16>(a, dtype, n_slots, st);
@@ -457,13 +459,9 @@ extern "C" int smx_stats_cast(const void *x, int dtype, int64_t rows, int64_t co
   return check_launch("stats_cast");
 }
 
-static int64_t colsum_partial_bytes(int64_t cols, int32_t n_slots) {
-  return round_up(static_cast<int64_t>(n_slots) * cols * 4, 256);
-}
-
 extern "C" int64_t smx_stats_colsum_workspace_bytes(int64_t cols, int32_t n_slots) {
   if (cols < 1 || n_slots < 1) return -1;
-  return colsum_partial_bytes(cols, n_slots) + round_up(ceil_div(cols, kMinTileCols) * 4, 256);
+  return round_up(static_cast<int64_t>(n_slots) * cols * 4, 256);
 }
 
 extern "C" int smx_stats_colsum(const void *x, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
@@ -476,13 +474,16 @@ extern "C" int smx_stats_colsum(const void *x, int dtype, int64_t rows, int64_t 
   SMX_REQUIRE(workspace_bytes >= need, SMX_EWORKSPACE,
               "stats_colsum: workspace of " + std::to_string(workspace_bytes) + " bytes, need " + std::to_string(need));
   SMX_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, SMX_EALIGN, "stats_colsum: workspace must be 256-byte aligned");
-  char *ws = static_cast<char *>(workspace);
-  float *partial = reinterpret_cast<float *>(ws);
-  uint32_t *counters = reinterpret_cast<uint32_t *>(ws + colsum_partial_bytes(cols, n_slots));
-  // rows == 0 still launches: every chunk is empty and colsum becomes zero.
-  const StatsArgs a{x, rows, cols, rows ? row_stride : cols, 0, slots_sq, partial, nullptr, 0, colsum, counters};
-  dispatch_dtype<kSqColsum, 0>(a, dtype, n_slots, static_cast<hipStream_t>(stream));
-  return check_launch("stats_colsum");
+  float *partial = static_cast<float *>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // rows == 0 still launches: every chunk is empty, its partial zero.
+  const StatsArgs a{x, rows, cols, rows ? row_stride : cols, 0, slots_sq, partial, nullptr, 0};
+  dispatch_dtype<kSqColsum, 0>(a, dtype, n_slots, st);
+  rc = check_launch("stats_colsum");
+  if (rc) return rc;
+  hipLaunchKernelGGL(colsum_fold_kernel, dim3(static_cast<unsigned>(ceil_div(cols, 64))), dim3(256), 0, st,
+                     partial, cols, n_slots, colsum);
+  return check_launch("stats_colsum(fold)");
 }
 
 extern "C" int smx_stats_fold(float *sum_sq, float *slots_sq, float *sum_first, float *slots_first,

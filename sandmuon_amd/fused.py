@@ -66,8 +66,7 @@ class _Site:
         need = _native.stats_colsum_workspace_bytes(cols, self.optimizer.STAT_SLOTS)
         ws = self.workspace
         if ws is None or ws.numel() < need or ws.device != device:
-            # Zero-filled once; every colsum call leaves it reusable.
-            ws = self.workspace = torch.zeros(need, dtype=torch.uint8, device=device)
+            ws = self.workspace = torch.empty(need, dtype=torch.uint8, device=device)
         return ws
 
 

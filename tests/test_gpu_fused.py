@@ -72,10 +72,10 @@ def test_stats_cast_strided_rows(device):
 def test_stats_colsum_matches_fp64_and_hook_slots(device, dtype, rows, cols):
     g = torch.Generator(device=device).manual_seed(7 * rows + cols)
     x = (torch.randn(rows, cols, generator=g, device=device) * 1e-3 + 2e-4).to(dtype)
-    ws = torch.zeros(_native.stats_colsum_workspace_bytes(cols, SLOTS), dtype=torch.uint8, device=device)
+    ws = torch.full((_native.stats_colsum_workspace_bytes(cols, SLOTS),), 255, dtype=torch.uint8, device=device)
     sq, ref = torch.zeros(SLOTS, cols, device=device), torch.zeros(SLOTS, cols, device=device)
     colsum = torch.full((cols,), float("nan"), device=device)
-    for rep in range(2):  # the workspace is reused: its counters must come back to zero
+    for rep in range(2):  # the workspace starts as garbage (NaN bytes) and is reused
         _native.stats_colsum(x, sq, colsum, ws)
         if rows:
             _native.stats_accumulate(x, ref, None)
