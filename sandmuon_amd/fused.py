@@ -13,6 +13,9 @@ backward reduces the output cotangent over its rows for the bias gradient.
   x, writes the copy autocast would make and adds the A statistic.  The GEMM
   is torch's ``F.linear`` on the operands autocast would give it, so the
   output is unchanged bit for bit;
+  Layers that share the A statistic of another (k and v of a q projection)
+  reuse its cast when they are handed the same, unmodified input, where
+  autocast would cast it once per layer;
 * backward, with a bias: one kernel (``smx_stats_colsum``) reads delta, adds
   the B statistic and writes the bias gradient.  dX = delta W and
   dW = delta^T x are the matrix products torch's own backward of the layer
@@ -30,6 +33,7 @@ the B statistic of a layer without a bias.  Modules other than plain
 from __future__ import annotations
 
 import types
+import weakref
 from typing import Dict, Optional
 
 import torch
@@ -61,6 +65,24 @@ class _Site:
         self.parameter = optimizer.named_matrices[name]
         self.capture_a = optimizer.a_sources[id(self.parameter)] is self.parameter
         self.workspace: Optional[torch.Tensor] = None
+        # The A-source layer's cast of its fp32 input, kept for the layers
+        # sharing its statistic (k/v of a q projection), which are handed the
+        # same tensor: (weak reference to x, x's version, the cast, uses left).
+        self.source: Optional["_Site"] = None
+        self.n_sharers = 0
+        self.cast_cache = None
+
+    def shared_cast(self, x: torch.Tensor, lp: torch.dtype) -> Optional[torch.Tensor]:
+        """The A-source layer's cast of this very input, if it made one."""
+        src = self.source
+        cache = None if src is None else src.cast_cache
+        if cache is None or cache[0]() is not x or cache[1] != x._version or cache[2].dtype != lp:
+            return None
+        if cache[3] <= 1:
+            src.cast_cache = None
+        else:
+            src.cast_cache = (cache[0], cache[1], cache[2], cache[3] - 1)
+        return cache[2]
 
     def colsum_workspace(self, cols: int, device) -> torch.Tensor:
         need = _native.stats_colsum_workspace_bytes(cols, self.optimizer.STAT_SLOTS)
@@ -77,15 +99,19 @@ class _FusedLinear(torch.autograd.Function):
         state = opt.state[p]
         lp = _autocast_dtype(x.device.type)
         if lp is not None and x.dtype == torch.float32 and lp in (torch.bfloat16, torch.float16):
-            rows = _rows2d(x)
-            x_lp = torch.empty(rows.shape, dtype=lp, device=x.device)
-            if site.capture_a:
-                sq, fs = opt._a_slots(p, rows.shape[1], rows.device, state)
-                _native.stats_cast(rows, sq, fs, x_lp)
-                state["a_count"] += rows.shape[0]
-            else:
-                x_lp.copy_(rows)
-            x_lp = x_lp.view(x.shape)
+            x_lp = None if site.capture_a else site.shared_cast(x, lp)
+            if x_lp is None:
+                rows = _rows2d(x)
+                x_lp = torch.empty(rows.shape, dtype=lp, device=x.device)
+                if site.capture_a:
+                    sq, fs = opt._a_slots(p, rows.shape[1], rows.device, state)
+                    _native.stats_cast(rows, sq, fs, x_lp)
+                    state["a_count"] += rows.shape[0]
+                else:
+                    x_lp.copy_(rows)
+                x_lp = x_lp.view(x.shape)
+                if site.capture_a and site.n_sharers:
+                    site.cast_cache = (weakref.ref(x), x._version, x_lp, site.n_sharers)
         else:
             if site.capture_a:
                 opt._accumulate_a(p, x, state)
@@ -157,6 +183,12 @@ class FusedStatistics:
             optimizer.handles.remove(handle)
             module.forward = types.MethodType(_fused_forward(site), module)
             self.sites[name] = site
+        by_param = {id(site.parameter): site for site in self.sites.values()}
+        for site in self.sites.values():
+            if not site.capture_a:
+                site.source = by_param.get(id(optimizer.a_sources[id(site.parameter)]))
+                if site.source is not None:
+                    site.source.n_sharers += 1
         optimizer._fused = self
 
     @property
@@ -166,6 +198,7 @@ class FusedStatistics:
     def close(self) -> None:
         opt = self.optimizer
         for name, site in self.sites.items():
+            site.cast_cache = None
             site.module.__dict__.pop("forward", None)
             handle = opt._install_hook(name)
             opt._hook_handles[name] = handle

@@ -140,6 +140,41 @@ def test_fused_linear_matches_autocast_linear(device, bias, in_dtype):
     opt.close()
 
 
+def test_qkv_share_the_source_cast_of_an_unmodified_input(device):
+    class Attn(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.q_proj, self.k_proj, self.v_proj = nn.Linear(64, 64), nn.Linear(64, 64), nn.Linear(64, 64)
+
+    class Net(nn.Module):  # the q/k/v sharing applies to transformer.h.N.attn.*
+        def __init__(self):
+            super().__init__()
+            self.transformer = nn.Module()
+            blk = nn.Module()
+            blk.attn = Attn()
+            self.transformer.h = nn.ModuleList([blk])
+
+    net = Net().to(device)
+    opt = RankOneAWeightedPE(net, 1e-2)
+    fuse_statistics(opt)
+    x = torch.randn(2, 16, 64, device=device, requires_grad=True)
+    a = net.transformer.h[0].attn
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        yq, yk, yv = a.q_proj(x), a.k_proj(x), a.v_proj(x)
+    saved = [y.grad_fn.saved_tensors[0] for y in (yq, yk, yv)]
+    assert saved[0].data_ptr() == saved[1].data_ptr() == saved[2].data_ptr()
+    assert torch.equal(saved[0], x.detach().to(torch.bfloat16))
+    # an input modified in place after the source's cast is cast again
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        x2 = x.detach().clone()
+        yq = a.q_proj(x2)
+        x2.mul_(2)
+        yk = a.k_proj(x2)
+    assert yk.grad_fn.saved_tensors[0].data_ptr() != yq.grad_fn.saved_tensors[0].data_ptr()
+    assert torch.equal(yk.grad_fn.saved_tensors[0], x2.to(torch.bfloat16))
+    opt.close()
+
+
 def _gpt_pair(device, cfg, seed):
     model = GPT(cfg)
     model.init_weights(seed)
