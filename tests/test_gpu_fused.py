@@ -17,7 +17,7 @@ import pytest
 import torch
 from torch import nn
 
-from sandmuon_amd import RankOneAWeightedPE, _native
+from sandmuon_amd import DiagonalWeightedPE, RankOneAWeightedPE, _native
 from sandmuon_amd.fused import fuse_statistics
 from sandmuon_amd.workloads import GPT, GPTConfig, transformer_filter
 
@@ -175,19 +175,21 @@ def test_qkv_share_the_source_cast_of_an_unmodified_input(device):
     opt.close()
 
 
-def _gpt_pair(device, cfg, seed):
+def _gpt_pair(device, cfg, seed, opt_cls):
     model = GPT(cfg)
     model.init_weights(seed)
     model = model.to(device)
     twin = copy.deepcopy(model)
-    a = RankOneAWeightedPE(model, 1e-2, module_filter=transformer_filter)
-    b = RankOneAWeightedPE(twin, 1e-2, module_filter=transformer_filter)
+    a = opt_cls(model, 1e-2, module_filter=transformer_filter)
+    b = opt_cls(twin, 1e-2, module_filter=transformer_filter)
     return model, twin, a, b
 
 
-def test_fused_gpt_step_equals_hook_step(device):
+@pytest.mark.parametrize("opt_cls,amp", [(RankOneAWeightedPE, torch.bfloat16), (DiagonalWeightedPE, torch.bfloat16),
+                                         (RankOneAWeightedPE, torch.float16)])
+def test_fused_gpt_step_equals_hook_step(device, opt_cls, amp):
     cfg = GPTConfig(vocab=257, ctx=128, layers=2, width=256, heads=4, mlp=1024)
-    model, twin, hooked, fused_opt = _gpt_pair(device, cfg, 11)
+    model, twin, hooked, fused_opt = _gpt_pair(device, cfg, 11, opt_cls)
     handle = fuse_statistics(fused_opt)
     assert len(handle.fused_names) == 12 and fused_opt.handles == []
     g = torch.Generator().manual_seed(12)
@@ -214,7 +216,7 @@ def test_fused_gpt_step_equals_hook_step(device):
             idx = torch.randint(0, cfg.vocab, (4, cfg.ctx), generator=g).to(device)
             tgt = torch.randint(0, cfg.vocab, (4, cfg.ctx), generator=g).to(device)
             for m in (model, twin):
-                with torch.autocast("cuda", dtype=torch.bfloat16):
+                with torch.autocast("cuda", dtype=amp):
                     loss = m(idx, tgt) / 3
                 loss.backward()
         for n in hooked.named_matrices:
