@@ -1,0 +1,130 @@
+"""The matrix step and AdamW through the C ABI as a non-torch host calls
+them, and the optimizer on shapes that take the kernels' scalar paths.
+
+* bf16/f16 gradients (smx_matrix_desc.grad_dtype, smx_adamw_desc.grad_dtype):
+  torch keeps fp32 gradients for fp32 parameters, so only another host
+  reaches these paths.  The momentum and AdamW are elementwise and must equal
+  the fp32-gradient run on the same (exactly widened) values bit for bit;
+  the update direction, whose row sums run in another order on the scalar
+  path, to 1e-5 (fp32 mode) and 1e-4 (comp_bf16 mode).
+* odd shapes (columns not a multiple of 4, transposed parameters, sizes far
+  from the 256 padding) through the whole optimizer against the CPU oracle,
+  at the north-star gates.
+"""
+import math
+
+import pytest
+import torch
+from torch import nn
+
+from sandmuon_amd import RankOneAWeightedPE, _native
+
+from test_gpu_optimizer import check_aux, check_directions, rel, run_pair
+
+pytestmark = pytest.mark.gpu
+
+
+def _factors(rows, cols, seed, device):
+    g = torch.Generator().manual_seed(seed)
+    inv_row = torch.rand(rows, generator=g) + 0.5
+    inv_col = torch.rand(cols, generator=g) + 0.5
+    z = torch.randn(cols, generator=g) * 0.3
+    rho = math.sqrt(1.0 + float((z.double() ** 2).sum()))
+    kappa = torch.tensor([-1.0 / (rho * (rho + 1.0))])
+    return [t.float().to(device) for t in (inv_row, inv_col, z, kappa)]
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("gdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(96, 64), (64, 96), (37, 53), (130, 7)])
+def test_matrix_step_low_precision_gradients(device, mode, gdt, shape):
+    rows, cols = shape
+    inv_row, inv_col, z, kappa = _factors(rows, cols, rows * cols, device)
+    g = torch.Generator().manual_seed(rows + cols)
+    grad_lp = (torch.randn(rows, cols, generator=g) * 1e-2).to(gdt).to(device)
+    mom0 = torch.randn(rows, cols, generator=g) * 1e-2
+    w0 = torch.randn(rows, cols, generator=g) * 0.02
+    lr = 1e-2
+
+    def run(grad):
+        w, m = w0.clone().to(device), mom0.clone().to(device)
+        d = _native.MatrixDesc(param=w.data_ptr(), grad=grad.data_ptr(), momentum=m.data_ptr(),
+                               inv_row=inv_row.data_ptr(), inv_col=inv_col.data_ptr(), z=z.data_ptr(),
+                               kappa=kappa.data_ptr(), rows=rows, cols=cols, lr=lr, momentum_beta=.8,
+                               grad_dtype=_native.dtype_code(grad.dtype))
+        ws = torch.empty(_native.matrix_step_workspace_bytes([shape], mode), dtype=torch.uint8, device=device)
+        _native.matrix_step([d], mode, ws)
+        torch.cuda.synchronize()
+        return w, m
+
+    w_lp, m_lp = run(grad_lp)
+    w_32, m_32 = run(grad_lp.float().contiguous())
+    assert torch.equal(m_lp, m_32)
+    d_lp = (w0.to(device) - w_lp) / lr
+    d_32 = (w0.to(device) - w_32) / lr
+    # comp_bf16 rounds the iterate to 16-17 bits in every stage, so a
+    # last-bit difference in the whitening row sums moves it by a few 1e-5
+    assert rel(d_lp, d_32) <= (1e-5 if mode == 0 else 1e-4)
+    # the graft: ||direction|| = sqrt(rows)
+    assert abs(d_lp.double().norm().item() - math.sqrt(rows)) <= 1e-4 * math.sqrt(rows)
+
+
+@pytest.mark.parametrize("gdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("sizes", [[1000, 4096, 3], [50257 * 3, 768, 1]])
+def test_adamw_low_precision_gradients(device, gdt, sizes):
+    g = torch.Generator().manual_seed(sum(sizes))
+    params = [torch.randn(n, generator=g).to(device) for n in sizes]
+    grads = [(torch.randn(n, generator=g) * 1e-3).to(gdt).to(device) for n in sizes]
+
+    def run(gs):
+        ps = [p.clone() for p in params]
+        m = [torch.zeros_like(p) for p in params]
+        v = [torch.zeros_like(p) for p in params]
+        for step in (1, 2):
+            descs, off = [], 0
+            for p, gr, ea, es in zip(ps, gs, m, v):
+                descs.append(_native.AdamwDesc(param=p.data_ptr(), grad=gr.data_ptr(), exp_avg=ea.data_ptr(),
+                                               exp_avg_sq=es.data_ptr(), n=p.numel(), offset=off,
+                                               bias1=1 - .9 ** step, bias2=1 - .999 ** step,
+                                               grad_dtype=_native.dtype_code(gr.dtype)))
+                off += p.numel()
+            _native.adamw(descs, off, 1e-3, .9, .999, 1e-8, .01, device)
+        torch.cuda.synchronize()
+        return ps, m, v
+
+    a = run(grads)
+    b = run([gr.float() for gr in grads])
+    for xs, ys in zip(a, b):
+        for x, y in zip(xs, ys):
+            assert torch.equal(x, y)
+
+
+class Chain(nn.Module):
+    """Linears of odd widths: 53 -> 37 -> 130 -> 7 -> 300 -> 5 (two of them
+    transposed in the S8 map, every column count but one off a multiple of 4)."""
+
+    def __init__(self):
+        super().__init__()
+        dims = [53, 37, 130, 7, 300, 5]
+        self.layers = nn.ModuleList([nn.Linear(a, b) for a, b in zip(dims, dims[1:])])
+
+    def forward(self, x):
+        for k, layer in enumerate(self.layers):
+            x = layer(x)
+            if k + 1 < len(self.layers):
+                x = torch.tanh(x)
+        return x
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+def test_odd_shapes_through_the_optimizer(device, mode):
+    torch.manual_seed(41)
+    model = Chain()
+    g = torch.Generator().manual_seed(42)
+    batches = [(torch.randn(4, 64, 53, generator=g) + 0.2, torch.randn(4, 64, 5, generator=g)) for _ in range(2)]
+    loss = lambda m, x, y: (m(x) - y).square().mean() / 2
+    hist, opt, ora = run_pair(device, model, batches, loss, RankOneAWeightedPE, mode, 1e-2, steps=2)
+    assert len(opt.named_matrices) == 5
+    worst = check_directions(hist, opt, 1e-2, mode)
+    print(f"odd shapes {mode}: worst direction rel err {worst:.3e}")
+    check_aux(hist, opt, ora)
