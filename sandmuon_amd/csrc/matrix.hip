@@ -11,11 +11,11 @@
 // and B on rows, whichever orientation the S8 map uses; the whiten tile
 // pass writes the oriented iterate X (r x c, r <= c).
 //
-// whiten_rows  one pass per row: momentum update, u_i = b_i sum_j S_ij a_j z_j
-//              and the row's ||V_i||^2 in closed form
-//              (||V_i||^2 = b_i^2 sum_j (S_ij a_j)^2 + (2 kappa + kappa^2 |z|^2) u_i^2).
-// whiten_tiles 64x64 tiles: V from (g, m', u), stored to X directly, or
-//              transposed through LDS for a transposed parameter.
+// whiten       two passes per row in one launch: momentum update,
+//              u_i = b_i sum_j S_ij a_j z_j and the row's ||V_i||^2 in closed
+//              form (||V_i||^2 = b_i^2 sum_j (S_ij a_j)^2 + (2 kappa + kappa^2 |z|^2) u_i^2);
+//              then V from (g, m', u) stored to X directly, or transposed
+//              through LDS for a transposed parameter.
 // mapback_rows u_i = sum_j Q_ij z_j and ||U_i||^2 in closed form.
 // mapback_apply W -= lr * scale * U.
 #include "s8.h"
@@ -109,11 +109,23 @@ __device__ __forceinline__ double sum_wave_parts(double part, double *wave_part)
 }
 
 // ------------------------------------------------------------- whiten ---
-// Momentum update m' = b m + (1-b) g (in place), u_i = b_i sum_j S_ij a_j z_j
-// and the row's ||V_i||^2 (closed form), for S = b m' + (1-b) g.
-template <bool R1>
-__global__ void __launch_bounds__(kRowThreads) whiten_rows_kernel(MatPack pack) {
+// One block of kRowsPerPart waves per 16 rows of the padded parameter
+// layout, one wave per row, two passes over the row:
+//  1. momentum m' = b m + (1-b) g (in place), u_i = b_i sum_j S_ij a_j z_j
+//     and the row's ||V_i||^2 (closed form) for S = b m' + (1-b) g;
+//  2. V_ij = b_i S_ij a_j + kappa u_i z_j from g and m' again (the row was
+//     just read, so this comes from cache) stored in operand form to the
+//     oriented iterate: row i of X directly (pl), or, for a transposed
+//     parameter (tl), through LDS in chunks of kWhitenChunk columns, where
+//     the block's 16 rows are one 16-element K group of each X row.
+// Rows and columns of the padding are written as zeros.
+constexpr int kWhitenChunk = 1024;  // = 4 * 64 * kRowUnroll
+
+template <bool R1, bool FLIP>
+__global__ void __launch_bounds__(kRowThreads) whiten_kernel(MatPack pack) {
+  static_assert(kRowsPerPart == 16 && kRowThreads == 1024, "one 16-row K group per block, 4 lanes per X row");
   __shared__ double wave_part[kRowsPerPart];
+  __shared__ float tile[FLIP ? kRowsPerPart : 1][FLIP ? kWhitenChunk + 4 : 1];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
   const int blk = blockIdx.x - J.blk0;
@@ -125,13 +137,19 @@ __global__ void __launch_bounds__(kRowThreads) whiten_rows_kernel(MatPack pack) 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bool vec = d.grad_dtype == SMX_F32 && d.cols % 4 == 0 && aligned16(d.grad) && aligned16(d.momentum) &&
                    aligned16(d.inv_col) && (!r1 || aligned16(d.z));
+  const bool planes = J.planes != 0;
+  const int64_t i0 = static_cast<int64_t>(blk) * kRowsPerPart;
+  const int64_t i = i0 + wave;
+  const bool live = i < d.rows;
+  float *mrow = live ? d.momentum + i * d.cols : nullptr;
+  const float *grow = live && vec ? static_cast<const float *>(d.grad) + i * d.cols : nullptr;
+
+  // ---- pass 1
   double part = 0.0;
-  const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + wave;
-  if (i < d.rows) {
+  float b = 0.f, ku = 0.f;
+  if (live) {
     float y2 = 0.f, yz = 0.f;
-    float *mrow = d.momentum + i * d.cols;
     if (vec) {
-      const float *grow = static_cast<const float *>(d.grad) + i * d.cols;
       const int64_t n4 = d.cols / 4;
       for (int64_t q0 = lane; q0 < n4; q0 += 64 * kRowUnroll) {
         // Every load of the chunk is issued before the first store.
@@ -177,105 +195,99 @@ __global__ void __launch_bounds__(kRowThreads) whiten_rows_kernel(MatPack pack) 
     }
     const double Y2 = wave_sum(y2);
     const double YZ = wave_sum(yz);
-    const double b = d.inv_row[i];
-    const double u = b * YZ;
+    const double bd = d.inv_row[i];
+    const double u = bd * YZ;
+    b = d.inv_row[i];
+    ku = r1 ? kappa * static_cast<float>(u) : 0.f;
     if (lane == 0) {
       J.u[i] = static_cast<float>(u);
-      part = b * b * Y2 + corr * u * u;
+      part = bd * bd * Y2 + corr * u * u;
     }
   }
-  const double t = sum_wave_parts(part, wave_part);
-  if (threadIdx.x == 0) J.part[blk] = t;
-}
-
-// block = 256 threads, one 64x64 tile of the padded parameter layout:
-// V = b_i S_ij a_j + kappa u_i z_j, stored in operand form to the oriented
-// iterate: directly (pl), or transposed through LDS for a transposed
-// parameter (tl).
-template <bool R1>
-__global__ void __launch_bounds__(256) whiten_tiles_kernel(MatPack pack) {
-  __shared__ float tile[64][65];
-  const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
-  const smx_matrix_desc &d = J.d;
-  const int64_t tiles_c = J.pcol_pad / 64;
-  const int64_t tb = blockIdx.x - J.blk0;
-  const int64_t i0 = (tb / tiles_c) * 64, j0 = (tb % tiles_c) * 64;
-  constexpr bool r1 = R1;
-  const float kappa = r1 ? d.kappa[0] : 0.f;
-  const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
-  const bool vec = d.grad_dtype == SMX_F32 && d.cols % 4 == 0 && aligned16(d.grad) && aligned16(d.momentum) &&
-                   aligned16(d.inv_col) && (!r1 || aligned16(d.z));
-  const int t = threadIdx.x;
-  const int lc = (t & 15) * 4;
-  const int64_t j = j0 + lc;
-  // The thread's four rows: every load first, then the arithmetic and the
-  // stores (a store between them would serialise the rows' loads).
-  float v[4][4];
-  if (vec && j + 3 < d.cols) {
-    float4 g[4], m[4];
-    float b[4], ku[4];
-    const float4 a = ld4(d.inv_col, j / 4);
-    float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    if constexpr (R1) z = ld4(d.z, j / 4);
+  // ---- pass 2: V of the row, kRowUnroll groups of four consecutive
+  // columns at a time, every load of a batch issued before the arithmetic.
+  auto batch = [&](int64_t j0, int64_t stride, float (&v)[kRowUnroll][4]) {
+    if (live && vec) {
+      float4 g[kRowUnroll], m[kRowUnroll], a[kRowUnroll], z[kRowUnroll];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t i = i0 + (t >> 4) + 16 * q;
-      if (i < d.rows) {
-        const int64_t e4 = (i * d.cols + j) / 4;
-        g[q] = ld4(static_cast<const float *>(d.grad), e4);
-        m[q] = ld4(d.momentum, e4);
-        b[q] = d.inv_row[i];
-        ku[q] = r1 ? kappa * J.u[i] : 0.f;
+      for (int u = 0; u < kRowUnroll; ++u) {
+        const int64_t j = j0 + stride * u;
+        if (j < d.cols) {
+          g[u] = ld4(grow, j / 4);
+          m[u] = ld4(mrow, j / 4);
+          a[u] = ld4(d.inv_col, j / 4);
+          if constexpr (R1) z[u] = ld4(d.z, j / 4);
+        }
       }
-    }
-    const float as[4] = {a.x, a.y, a.z, a.w}, zs[4] = {z.x, z.y, z.z, z.w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t i = i0 + (t >> 4) + 16 * q;
-      const float gs[4] = {g[q].x, g[q].y, g[q].z, g[q].w}, ms[4] = {m[q].x, m[q].y, m[q].z, m[q].w};
+      for (int u = 0; u < kRowUnroll; ++u) {
+        const int64_t j = j0 + stride * u;
+        const float gs[4] = {g[u].x, g[u].y, g[u].z, g[u].w}, ms[4] = {m[u].x, m[u].y, m[u].z, m[u].w};
+        const float as[4] = {a[u].x, a[u].y, a[u].z, a[u].w};
+        float zs[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (R1) {
+          zs[0] = z[u].x; zs[1] = z[u].y; zs[2] = z[u].z; zs[3] = z[u].w;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float s = fmaf(ms[e], beta, gs[e] * omb);
+          float x = (s * b) * as[e];
+          if constexpr (R1) x = fmaf(ku, zs[e], x);
+          v[u][e] = j < d.cols ? x : 0.f;
+        }
+      }
+      return;
+    }
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t j = j0 + stride * u;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[q][e] = 0.f;
-        if (i < d.rows) {
-          const float s = fmaf(ms[e], beta, gs[e] * omb);
-          v[q][e] = (s * b[q]) * as[e];
-          if constexpr (R1) v[q][e] = fmaf(ku[q], zs[e], v[q][e]);
+        v[u][e] = 0.f;
+        if (live && j + e < d.cols) {
+          const float g = load_grad(d.grad, d.grad_dtype, i * d.cols + j + e);
+          const float s = fmaf(mrow[j + e], beta, g * omb);
+          v[u][e] = (s * b) * d.inv_col[j + e];
+          if constexpr (R1) v[u][e] = fmaf(ku, d.z[j + e], v[u][e]);
         }
+      }
+    }
+  };
+  if constexpr (!FLIP) {
+    for (int64_t j0 = 4 * lane; j0 < J.pcol_pad; j0 += 4 * 64 * kRowUnroll) {
+      float v[kRowUnroll][4];
+      batch(j0, 4 * 64, v);
+#pragma unroll
+      for (int u = 0; u < kRowUnroll; ++u) {
+        const int64_t j = j0 + 4 * 64 * u;
+        if (j < J.pcol_pad) put_operand4(J.pl, i * J.pcol_pad + j, v[u], planes);
       }
     }
   } else {
+    static_assert(kWhitenChunk == 4 * 64 * kRowUnroll, "one batch per lane fills a chunk row");
+    const int qq = threadIdx.x & 3;  // 4-row quarter of the K group
+    for (int64_t c0 = 0; c0 < J.pcol_pad; c0 += kWhitenChunk) {
+      float v[kRowUnroll][4];
+      batch(c0 + 4 * lane, 4 * 64, v);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t i = i0 + (t >> 4) + 16 * q;
+      for (int u = 0; u < kRowUnroll; ++u)
+        *reinterpret_cast<float4 *>(&tile[wave][4 * (lane + 64 * u)]) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+      __syncthreads();
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[q][e] = 0.f;
-        if (i < d.rows && j + e < d.cols) {
-          const float b = d.inv_row[i];
-          const float g = load_grad(d.grad, d.grad_dtype, i * d.cols + j + e);
-          const float s = fmaf(d.momentum[i * d.cols + j + e], beta, g * omb);
-          v[q][e] = (s * b) * d.inv_col[j + e];
-          if constexpr (R1) v[q][e] = fmaf(kappa * J.u[i], d.z[j + e], v[q][e]);
+      for (int r = 0; r < kWhitenChunk / 256; ++r) {
+        const int jj = (threadIdx.x >> 2) + 256 * r;  // X row in the chunk
+        if (c0 + jj < J.pcol_pad) {
+          const float w[4] = {tile[4 * qq][jj], tile[4 * qq + 1][jj], tile[4 * qq + 2][jj], tile[4 * qq + 3][jj]};
+          put_operand4(J.tl, (c0 + jj) * J.prow_pad + i0 + 4 * qq, w, planes);
         }
       }
+      __syncthreads();
     }
   }
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int lr = (t >> 4) + 16 * q;
-    const int64_t i = i0 + lr;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) tile[lr][lc + e] = v[q][e];
-    if (J.pl) put_operand4(J.pl, i * J.pcol_pad + j, v[q], J.planes != 0);
-  }
-  if (!J.tl) return;  // uniform per block
-  __syncthreads();
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int lr = (t >> 4) + 16 * q;  // transposed row = parameter column
-    const float v[4] = {tile[lc][lr], tile[lc + 1][lr], tile[lc + 2][lr], tile[lc + 3][lr]};
-    put_operand4(J.tl, (j0 + lr) * J.prow_pad + i0 + lc, v, J.planes != 0);
-  }
+  // The block's partial of ||V||^2, after pass 2 so that no barrier
+  // separates the passes.
+  const double t = sum_wave_parts(part, wave_part);
+  if (threadIdx.x == 0 && i0 < d.rows) J.part[blk] = t;
 }
 
 // ------------------------------------------------------------ mapback ---
@@ -495,7 +507,7 @@ static int launch_jobs(std::vector<MatJob> &jobs, int64_t (*blocks_of)(const Mat
 
 static int64_t one_block(const MatJob &) { return 1; }
 static int64_t row_blocks(const MatJob &j) { return ceil_div(j.d.rows, kRowsPerPart); }
-static int64_t tile_blocks(const MatJob &j) { return (j.prow_pad / 64) * (j.pcol_pad / 64); }
+static int64_t padded_row_blocks(const MatJob &j) { return j.prow_pad / kRowsPerPart; }
 
 }  // namespace smx
 
@@ -574,10 +586,14 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
     // term (all of a call or none, checked above).
     const bool r1 = descs[0].z != nullptr;
     int rc = launch_jobs(ping, one_block, matrix_consts_kernel, 256, "matrix_consts", st);
-    if (!rc) rc = r1 ? launch_jobs(ping, row_blocks, whiten_rows_kernel<true>, kRowThreads, "whiten_rows", st)
-                     : launch_jobs(ping, row_blocks, whiten_rows_kernel<false>, kRowThreads, "whiten_rows", st);
-    if (!rc) rc = r1 ? launch_jobs(ping, tile_blocks, whiten_tiles_kernel<true>, 256, "whiten_tiles", st)
-                     : launch_jobs(ping, tile_blocks, whiten_tiles_kernel<false>, 256, "whiten_tiles", st);
+    // The whiten kernel is specialised on the orientation too: the jobs go
+    // to two launches, parameters kept as they are and transposed ones.
+    std::vector<MatJob> keep, flip;
+    for (const MatJob &j : ping) (j.tl ? flip : keep).push_back(j);
+    if (!rc) rc = r1 ? launch_jobs(keep, padded_row_blocks, whiten_kernel<true, false>, kRowThreads, "whiten", st)
+                     : launch_jobs(keep, padded_row_blocks, whiten_kernel<false, false>, kRowThreads, "whiten", st);
+    if (!rc) rc = r1 ? launch_jobs(flip, padded_row_blocks, whiten_kernel<true, true>, kRowThreads, "whiten", st)
+                     : launch_jobs(flip, padded_row_blocks, whiten_kernel<false, true>, kRowThreads, "whiten", st);
     if (!rc) rc = run_s8_stages(plan.layout, st);
     if (!rc) rc = r1 ? launch_jobs(fin, row_blocks, mapback_rows_kernel<true>, kRowThreads, "mapback_rows", st)
                      : launch_jobs(fin, row_blocks, mapback_rows_kernel<false>, kRowThreads, "mapback_rows", st);
