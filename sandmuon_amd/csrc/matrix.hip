@@ -361,13 +361,37 @@ __global__ void __launch_bounds__(kRowThreads) mapback_rows_kernel(MatPack pack)
 }
 
 // W -= lr * sqrt(rows) / max(||U||_F, FLT_MIN) * U over kRowsPerPart rows
-// (one wave per row).
+// (one wave per row).  The first chunk of the row is loaded before the
+// norm is summed, so the block does not wait on two memory round trips in
+// a row.
 template <bool R1>
 __global__ void __launch_bounds__(kRowThreads) mapback_apply_kernel(MatPack pack) {
   __shared__ double bcast;
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
   const int blk = blockIdx.x - J.blk0;
+  constexpr bool r1 = R1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool vec = d.cols % 4 == 0 && aligned16(d.param) && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
+  const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + wave;
+  const bool live = i < d.rows;
+  const float *q = live ? J.pl + i * J.pcol_pad : nullptr;
+  float *w = live ? d.param + i * d.cols : nullptr;
+  const int64_t n4 = d.cols / 4;
+  float4 qv[kRowUnroll], av[kRowUnroll], wv[kRowUnroll], zv[kRowUnroll];
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t k = k0 + 64 * u;
+      if (k < n4) {
+        qv[u] = ld4(q, k);
+        av[u] = ld4(d.inv_col, k);
+        wv[u] = ld4(w, k);
+        if constexpr (R1) zv[u] = ld4(d.z, k);
+      }
+    }
+  };
+  if (live && vec) load(lane);
   if (threadIdx.x < 64) {
     double s = 0.0;
     const int np = static_cast<int>(ceil_div(d.rows, kRowsPerPart));
@@ -382,56 +406,37 @@ __global__ void __launch_bounds__(kRowThreads) mapback_apply_kernel(MatPack pack
   // gives a zero update.
   const float scale = n2 > 0.0 ? static_cast<float>(sqrt(static_cast<double>(d.rows))) / fmaxf(norm, FLT_MIN) : 0.f;
   const float nlr = static_cast<float>(-d.lr);
-  constexpr bool r1 = R1;
   const float kappa = r1 ? d.kappa[0] : 0.f;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool vec = d.cols % 4 == 0 && aligned16(d.param) && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
-  const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + wave;
-  if (i < d.rows) {
-    const float *q = J.pl + i * J.pcol_pad;
-    float *w = d.param + i * d.cols;
-    const float b = d.inv_row[i];
-    const float ku = r1 ? kappa * J.u[i] : 0.f;
-    if (vec) {
-      const int64_t n4 = d.cols / 4;
-      for (int64_t k0 = lane; k0 < n4; k0 += 64 * kRowUnroll) {
-        // Every load of the chunk is issued before the first store.
-        float4 qv[kRowUnroll], av[kRowUnroll], wv[kRowUnroll], zv[kRowUnroll];
+  if (!live) return;
+  const float b = d.inv_row[i];
+  const float ku = r1 ? kappa * J.u[i] : 0.f;
+  if (vec) {
+    for (int64_t k0 = lane; k0 < n4; k0 += 64 * kRowUnroll) {
+      if (k0 != lane) load(k0);  // the first chunk was loaded above
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u) {
-          const int64_t k = k0 + 64 * u;
-          if (k < n4) {
-            qv[u] = ld4(q, k);
-            av[u] = ld4(d.inv_col, k);
-            wv[u] = ld4(w, k);
-            if constexpr (R1) zv[u] = ld4(d.z, k);
+      for (int u = 0; u < kRowUnroll; ++u) {
+        const int64_t k = k0 + 64 * u;
+        if (k < n4) {
+          float4 v = qv[u], ww = wv[u];
+          const float4 a = av[u];
+          if constexpr (R1) {
+            const float4 z = zv[u];
+            v.x = fmaf(ku, z.x, v.x); v.y = fmaf(ku, z.y, v.y); v.z = fmaf(ku, z.z, v.z); v.w = fmaf(ku, z.w, v.w);
           }
-        }
-#pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u) {
-          const int64_t k = k0 + 64 * u;
-          if (k < n4) {
-            float4 v = qv[u], ww = wv[u];
-            const float4 a = av[u];
-            if constexpr (R1) {
-              const float4 z = zv[u];
-              v.x = fmaf(ku, z.x, v.x); v.y = fmaf(ku, z.y, v.y); v.z = fmaf(ku, z.z, v.z); v.w = fmaf(ku, z.w, v.w);
-            }
-            ww.x = fmaf(nlr, ((v.x * b) * a.x) * scale, ww.x);
-            ww.y = fmaf(nlr, ((v.y * b) * a.y) * scale, ww.y);
-            ww.z = fmaf(nlr, ((v.z * b) * a.z) * scale, ww.z);
-            ww.w = fmaf(nlr, ((v.w * b) * a.w) * scale, ww.w);
-            st4(w, k, ww);
-          }
+          ww.x = fmaf(nlr, ((v.x * b) * a.x) * scale, ww.x);
+          ww.y = fmaf(nlr, ((v.y * b) * a.y) * scale, ww.y);
+          ww.z = fmaf(nlr, ((v.z * b) * a.z) * scale, ww.z);
+          ww.w = fmaf(nlr, ((v.w * b) * a.w) * scale, ww.w);
+          st4(w, k, ww);
         }
       }
-    } else {
-      for (int64_t j = lane; j < d.cols; j += 64) {
-        float v = q[j];
-        if (r1) v = fmaf(ku, d.z[j], v);
-        const float U = (v * b) * d.inv_col[j];
-        w[j] = fmaf(nlr, U * scale, w[j]);
-      }
+    }
+  } else {
+    for (int64_t j = lane; j < d.cols; j += 64) {
+      float v = q[j];
+      if (r1) v = fmaf(ku, d.z[j], v);
+      const float U = (v * b) * d.inv_col[j];
+      w[j] = fmaf(nlr, U * scale, w[j]);
     }
   }
 }
