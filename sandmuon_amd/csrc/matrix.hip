@@ -34,7 +34,7 @@ struct MatJob {
   float *pl;         // parameter-layout buffer [prow_pad][pcol_pad]
   float *tl;         // transposed buffer [pcol_pad][prow_pad] (whiten of a transposed parameter)
   float *u;          // [rows] rank-one row coefficients
-  double *part;      // [ceil(rows/kRowsPerPart)] partial sums
+  double *part;      // [ceil(rows/kPartRows)] partial sums
   double *cst;       // [2]: sum z^2, sum (a z)^2 (matrix_consts_kernel)
   int64_t prow_pad, pcol_pad;
   int32_t blk0;      // first block of this job in the launch
@@ -96,15 +96,18 @@ __global__ void __launch_bounds__(256) matrix_consts_kernel(MatPack pack) {
 constexpr int kRowThreads = 64 * kRowsPerPart;
 constexpr int kRowUnroll = 4;  // float4 columns per lane whose loads are in flight together
 
-// FP64 sum of the per-wave row partials, in wave order; the result is valid
-// in thread 0.
+constexpr int kMapThreads = 64 * kPartRows;
+
+// FP64 sum of the NW per-wave row partials, in wave order; the result is
+// valid in thread 0.
+template <int NW = kRowsPerPart>
 __device__ __forceinline__ double sum_wave_parts(double part, double *wave_part) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) wave_part[wave] = part;
   __syncthreads();
   double t = 0.0;
   if (threadIdx.x == 0)
-    for (int w = 0; w < kRowsPerPart; ++w) t += wave_part[w];
+    for (int w = 0; w < NW; ++w) t += wave_part[w];
   return t;
 }
 
@@ -121,10 +124,17 @@ __device__ __forceinline__ double sum_wave_parts(double part, double *wave_part)
 // Rows and columns of the padding are written as zeros.
 constexpr int kWhitenChunk = 1024;  // = 4 * 64 * kRowUnroll
 
+// Rows per block: a transposed parameter needs 16 (one K group of every X
+// row); the others take kPartRows, so that more, shorter blocks share a CU.
+template <bool FLIP>
+constexpr int whiten_rows_per_block() { return FLIP ? kRowsPerPart : kPartRows; }
+
 template <bool R1, bool FLIP>
 __global__ void __launch_bounds__(kRowThreads) whiten_kernel(MatPack pack) {
-  static_assert(kRowsPerPart == 16 && kRowThreads == 1024, "one 16-row K group per block, 4 lanes per X row");
-  __shared__ double wave_part[kRowsPerPart];
+  constexpr int RB = whiten_rows_per_block<FLIP>();
+  static_assert(kRowsPerPart == 16 && kRowThreads == 1024, "one 16-row K group per transposed block, 4 lanes per X row");
+  static_assert(RB % kPartRows == 0, "whole partials per block");
+  __shared__ double wave_part[RB];
   __shared__ float tile[FLIP ? kRowsPerPart : 1][FLIP ? kWhitenChunk + 4 : 1];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
@@ -138,7 +148,7 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(MatPack pack) {
   const bool vec = d.grad_dtype == SMX_F32 && d.cols % 4 == 0 && aligned16(d.grad) && aligned16(d.momentum) &&
                    aligned16(d.inv_col) && (!r1 || aligned16(d.z));
   const bool planes = J.planes != 0;
-  const int64_t i0 = static_cast<int64_t>(blk) * kRowsPerPart;
+  const int64_t i0 = static_cast<int64_t>(blk) * RB;
   const int64_t i = i0 + wave;
   const bool live = i < d.rows;
   float *mrow = live ? d.momentum + i * d.cols : nullptr;
@@ -284,18 +294,27 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(MatPack pack) {
       __syncthreads();
     }
   }
-  // The block's partial of ||V||^2, after pass 2 so that no barrier
-  // separates the passes.
-  const double t = sum_wave_parts(part, wave_part);
-  if (threadIdx.x == 0 && i0 < d.rows) J.part[blk] = t;
+  // The partials of ||V||^2 (one per kPartRows rows, waves in order), after
+  // pass 2 so that no barrier separates the passes.
+  if (lane == 0) wave_part[wave] = part;
+  __syncthreads();
+  if (threadIdx.x < RB / kPartRows) {
+    const int p = threadIdx.x;
+    const int64_t r0 = i0 + p * kPartRows;
+    if (r0 < d.rows) {
+      double t = 0.0;
+      for (int w = 0; w < kPartRows; ++w) t += wave_part[p * kPartRows + w];
+      J.part[r0 / kPartRows] = t;
+    }
+  }
 }
 
 // ------------------------------------------------------------ mapback ---
 // u_i = sum_j Q_ij z_j and ||U_i||^2 in closed form:
 // b_i^2 (sum (a Q)^2 + 2 kappa u_i sum (a Q)(a z) + kappa^2 u_i^2 sum (a z)^2).
 template <bool R1>
-__global__ void __launch_bounds__(kRowThreads) mapback_rows_kernel(MatPack pack) {
-  __shared__ double wave_part[kRowsPerPart];
+__global__ void __launch_bounds__(kMapThreads) mapback_rows_kernel(MatPack pack) {
+  __shared__ double wave_part[kPartRows];
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
   const int blk = blockIdx.x - J.blk0;
@@ -305,7 +324,7 @@ __global__ void __launch_bounds__(kRowThreads) mapback_rows_kernel(MatPack pack)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bool vec = d.cols % 4 == 0 && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
   double part = 0.0;
-  const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + wave;
+  const int64_t i = static_cast<int64_t>(blk) * kPartRows + wave;
   if (i < d.rows) {
     const float *q = J.pl + i * J.pcol_pad;
     float su = 0.f, sa = 0.f, sb = 0.f;
@@ -356,16 +375,16 @@ __global__ void __launch_bounds__(kRowThreads) mapback_rows_kernel(MatPack pack)
       part = b * b * (A + 2.0 * kappa * U * B + kappa * kappa * U * U * cz);
     }
   }
-  const double t = sum_wave_parts(part, wave_part);
+  const double t = sum_wave_parts<kPartRows>(part, wave_part);
   if (threadIdx.x == 0) J.part[blk] = t;
 }
 
-// W -= lr * sqrt(rows) / max(||U||_F, FLT_MIN) * U over kRowsPerPart rows
+// W -= lr * sqrt(rows) / max(||U||_F, FLT_MIN) * U over kPartRows rows
 // (one wave per row).  The first chunk of the row is loaded before the
 // norm is summed, so the block does not wait on two memory round trips in
 // a row.
 template <bool R1>
-__global__ void __launch_bounds__(kRowThreads) mapback_apply_kernel(MatPack pack) {
+__global__ void __launch_bounds__(kMapThreads) mapback_apply_kernel(MatPack pack) {
   __shared__ double bcast;
   const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
   const smx_matrix_desc &d = J.d;
@@ -373,7 +392,7 @@ __global__ void __launch_bounds__(kRowThreads) mapback_apply_kernel(MatPack pack
   constexpr bool r1 = R1;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bool vec = d.cols % 4 == 0 && aligned16(d.param) && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
-  const int64_t i = static_cast<int64_t>(blk) * kRowsPerPart + wave;
+  const int64_t i = static_cast<int64_t>(blk) * kPartRows + wave;
   const bool live = i < d.rows;
   const float *q = live ? J.pl + i * J.pcol_pad : nullptr;
   float *w = live ? d.param + i * d.cols : nullptr;
@@ -394,7 +413,7 @@ __global__ void __launch_bounds__(kRowThreads) mapback_apply_kernel(MatPack pack
   if (live && vec) load(lane);
   if (threadIdx.x < 64) {
     double s = 0.0;
-    const int np = static_cast<int>(ceil_div(d.rows, kRowsPerPart));
+    const int np = static_cast<int>(ceil_div(d.rows, kPartRows));
     for (int k = threadIdx.x; k < np; k += 64) s += J.part[k];
     s = wave_sum(s);
     if (threadIdx.x == 0) bcast = s;
@@ -511,8 +530,9 @@ static int launch_jobs(std::vector<MatJob> &jobs, int64_t (*blocks_of)(const Mat
 }
 
 static int64_t one_block(const MatJob &) { return 1; }
-static int64_t row_blocks(const MatJob &j) { return ceil_div(j.d.rows, kRowsPerPart); }
-static int64_t padded_row_blocks(const MatJob &j) { return j.prow_pad / kRowsPerPart; }
+static int64_t map_blocks(const MatJob &j) { return ceil_div(j.d.rows, kPartRows); }
+template <bool FLIP>
+static int64_t whiten_blocks(const MatJob &j) { return j.prow_pad / whiten_rows_per_block<FLIP>(); }
 
 }  // namespace smx
 
@@ -595,15 +615,16 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
     // to two launches, parameters kept as they are and transposed ones.
     std::vector<MatJob> keep, flip;
     for (const MatJob &j : ping) (j.tl ? flip : keep).push_back(j);
-    if (!rc) rc = r1 ? launch_jobs(keep, padded_row_blocks, whiten_kernel<true, false>, kRowThreads, "whiten", st)
-                     : launch_jobs(keep, padded_row_blocks, whiten_kernel<false, false>, kRowThreads, "whiten", st);
-    if (!rc) rc = r1 ? launch_jobs(flip, padded_row_blocks, whiten_kernel<true, true>, kRowThreads, "whiten", st)
-                     : launch_jobs(flip, padded_row_blocks, whiten_kernel<false, true>, kRowThreads, "whiten", st);
+    constexpr int kKeepThreads = 64 * whiten_rows_per_block<false>();
+    if (!rc) rc = r1 ? launch_jobs(keep, whiten_blocks<false>, whiten_kernel<true, false>, kKeepThreads, "whiten", st)
+                     : launch_jobs(keep, whiten_blocks<false>, whiten_kernel<false, false>, kKeepThreads, "whiten", st);
+    if (!rc) rc = r1 ? launch_jobs(flip, whiten_blocks<true>, whiten_kernel<true, true>, kRowThreads, "whiten", st)
+                     : launch_jobs(flip, whiten_blocks<true>, whiten_kernel<false, true>, kRowThreads, "whiten", st);
     if (!rc) rc = run_s8_stages(plan.layout, st);
-    if (!rc) rc = r1 ? launch_jobs(fin, row_blocks, mapback_rows_kernel<true>, kRowThreads, "mapback_rows", st)
-                     : launch_jobs(fin, row_blocks, mapback_rows_kernel<false>, kRowThreads, "mapback_rows", st);
-    if (!rc) rc = r1 ? launch_jobs(fin, row_blocks, mapback_apply_kernel<true>, kRowThreads, "mapback_apply", st)
-                     : launch_jobs(fin, row_blocks, mapback_apply_kernel<false>, kRowThreads, "mapback_apply", st);
+    if (!rc) rc = r1 ? launch_jobs(fin, map_blocks, mapback_rows_kernel<true>, kMapThreads, "mapback_rows", st)
+                     : launch_jobs(fin, map_blocks, mapback_rows_kernel<false>, kMapThreads, "mapback_rows", st);
+    if (!rc) rc = r1 ? launch_jobs(fin, map_blocks, mapback_apply_kernel<true>, kMapThreads, "mapback_apply", st)
+                     : launch_jobs(fin, map_blocks, mapback_apply_kernel<false>, kMapThreads, "mapback_apply", st);
     if (rc) return rc;
   }
   return SMX_OK;

@@ -10,7 +10,8 @@ namespace smx {
 
 constexpr int kTile = 256;        // GEMM macro tile (M and N) and padding
 constexpr int kMaxClasses = 8;    // shape classes per GEMM launch
-constexpr int kRowsPerPart = 16;  // param rows per whiten/mapback partial (one block)
+constexpr int kRowsPerPart = 16;  // param rows per whiten block of a transposed parameter (one K group)
+constexpr int kPartRows = 4;      // param rows per whiten / mapback partial
 
 // Fixed S8 recipe: sandmuon/coefficients.py:3-11.
 constexpr double kS8Margin = 1.35;
@@ -29,7 +30,7 @@ struct S8Class {
   int32_t n_flip;      // slots [0, n_flip) hold transposed parameters
   int32_t tiles_m;     // rp / kTile
   int32_t tiles_n;     // cp / kTile
-  int32_t parts;       // partial slots per matrix: ceil(cp / kRowsPerPart)
+  int32_t parts;       // partial slots per matrix: ceil(cp / kPartRows)
   int32_t pad_;
   // Iterate buffers (4 bytes per element), oriented layout only.  In
   // SMX_S8_FP32 mode they hold FP32; in SMX_S8_COMP_BF16 mode interleaved

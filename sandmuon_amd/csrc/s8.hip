@@ -551,7 +551,7 @@ __device__ double sum_parts(const double *p, int n, double *bcast) {
 }
 
 __device__ __forceinline__ int fro_parts_used(const S8Mat &m) {
-  return static_cast<int>(ceil_div(m.prow(), kRowsPerPart));
+  return static_cast<int>(ceil_div(m.prow(), kPartRows));
 }
 
 // Stage-1 scalars of a matrix: ||V||^2 (sum of the whiten partials) and the
@@ -999,7 +999,7 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.cp = round_up(C.c, kTile);
     C.tiles_m = static_cast<int32_t>(C.rp / kTile);
     C.tiles_n = static_cast<int32_t>(C.cp / kTile);
-    C.parts = static_cast<int32_t>(ceil_div(C.cp, kRowsPerPart));
+    C.parts = static_cast<int32_t>(ceil_div(C.cp, kPartRows));
     const size_t xs = static_cast<size_t>(C.count) * C.rp * C.cp * sizeof(float);
     const size_t gs = static_cast<size_t>(C.count) * C.rp * C.rp * sizeof(float);
     C.x0 = reinterpret_cast<float *>(take(xs));
