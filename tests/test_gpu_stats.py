@@ -36,7 +36,8 @@ def accumulate(x, n_slots=128, first=True):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows,cols", [(0, 8), (1, 4), (9, 4), (7, 5), (33, 100), (1000, 768), (16384, 768),
-                                       (4096, 3072), (300, 24)])
+                                       (4096, 3072), (300, 24),
+                                       (8192, 2048), (8192, 8192)])  # cfg5 hook shapes (8 x 1024 tokens)
 def test_accumulate_matches_fp64_brute_force(device, dtype, rows, cols):
     x = stats_cfg3_tensor(rows * 7 + cols, rows, cols, dtype=dtype)
     sq, fs = accumulate(x.to(device))
