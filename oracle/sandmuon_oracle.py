@@ -19,7 +19,7 @@ from __future__ import annotations
 
 import math
 import re
-from typing import Callable, Dict, List, Optional, Tuple
+from typing import Callable, Dict, Optional
 
 import torch
 from torch import nn

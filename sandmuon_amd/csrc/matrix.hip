@@ -8,8 +8,8 @@
 //            W -= lr * sqrt(rows) * U / max(||U||_F, FLT_MIN)
 //
 // In parameter layout the A factor always acts on columns (input channels)
-// and B on rows, whichever orientation the S8 map uses; the whiten tile
-// pass writes the oriented iterate X (r x c, r <= c).
+// and B on rows, whichever orientation the S8 map uses; the whiten kernel
+// writes the oriented iterate X (r x c, r <= c).
 //
 // whiten       two passes per row in one launch: momentum update,
 //              u_i = b_i sum_j S_ij a_j z_j and the row's ||V_i||^2 in closed
@@ -90,17 +90,16 @@ __global__ void __launch_bounds__(256) matrix_consts_kernel(MatPack pack) {
   }
 }
 
-// Per-row reductions use FP32 lane partials and an FP32 wave sum; rows are
-// accumulated in FP64.  kRowsPerPart rows per block, one wave per row, so
-// every row's loads are in flight at once.
-constexpr int kRowThreads = 64 * kRowsPerPart;
+// The row kernels run one wave per row.  Per-row reductions use FP32 lane
+// partials and an FP32 wave sum; rows are accumulated in FP64, one partial
+// per kPartRows rows.
+constexpr int kRowThreads = 64 * kRowsPerPart;  // the largest block (16 rows)
+constexpr int kMapThreads = 64 * kPartRows;     // mapback blocks (4 rows)
 constexpr int kRowUnroll = 4;  // float4 columns per lane whose loads are in flight together
-
-constexpr int kMapThreads = 64 * kPartRows;
 
 // FP64 sum of the NW per-wave row partials, in wave order; the result is
 // valid in thread 0.
-template <int NW = kRowsPerPart>
+template <int NW>
 __device__ __forceinline__ double sum_wave_parts(double part, double *wave_part) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) wave_part[wave] = part;

@@ -7,7 +7,7 @@ from torch import nn
 
 from sandmuon_amd import DiagonalWeightedPE, RankOneAWeightedPE, S8_COEFFICIENTS, S8_MARGIN, S8_MULTIPLIER
 from sandmuon_amd.optimizer import select_matrices, shared_source
-from sandmuon_amd.workloads import GPT, GPT_103M, GPT_TINY, transformer_filter
+from sandmuon_amd.workloads import GPT, GPT_103M, transformer_filter
 
 
 class Attention(nn.Module):

@@ -3,7 +3,6 @@
 (diagonal_weighted_pe.py:551-561), the historical matrix selection and its
 errors (:178-220)."""
 import pytest
-import torch
 from torch import nn
 
 from sandmuon_amd import odl
