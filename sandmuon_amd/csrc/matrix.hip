@@ -111,8 +111,8 @@ __device__ __forceinline__ double sum_wave_parts(double part, double *wave_part)
 }
 
 // ------------------------------------------------------------- whiten ---
-// One block of kRowsPerPart waves per 16 rows of the padded parameter
-// layout, one wave per row, two passes over the row:
+// One wave per row of the padded parameter layout (blocks of 4 rows, or 16
+// for a transposed parameter), two passes over the row:
 //  1. momentum m' = b m + (1-b) g (in place), u_i = b_i sum_j S_ij a_j z_j
 //     and the row's ||V_i||^2 (closed form) for S = b m' + (1-b) g;
 //  2. V_ij = b_i S_ij a_j + kappa u_i z_j from g and m' again (the row was
