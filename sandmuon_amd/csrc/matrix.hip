@@ -609,7 +609,8 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
     // The kernels are specialised on whether the matrices carry a rank-one
     // term (all of a call or none, checked above).
     const bool r1 = descs[0].z != nullptr;
-    int rc = launch_jobs(ping, one_block, matrix_consts_kernel, 256, "matrix_consts", st);
+    // The rank-one constants (sum z^2, sum (a z)^2) exist only with a rank-one term.
+    int rc = r1 ? launch_jobs(ping, one_block, matrix_consts_kernel, 256, "matrix_consts", st) : SMX_OK;
     // The whiten kernel is specialised on the orientation too: the jobs go
     // to two launches, parameters kept as they are and transposed ones.
     std::vector<MatJob> keep, flip;

@@ -294,11 +294,14 @@ struct FinishPack {
 static_assert(sizeof(FinishPack) <= 4000, "FinishPack is passed by value in the kernel arguments");
 
 // Fold pass over a batch of descriptors: grid.x enumerates 64-channel
-// chunks of every vector, grid.y = descriptor.  Wave w sums slots w, w+4, ...
-// of the chunk (coalesced 256-byte rows, several loads in flight) and zeroes
-// them; the four wave partials are combined in a fixed order (FP64).
-__global__ void __launch_bounds__(256) finish_fold_kernel(FinishPack pack) {
-  __shared__ double part[2][4][64];
+// chunks of every vector, grid.y = descriptor.  Wave w of kFoldWaves sums
+// slots w, w + kFoldWaves, ... of the chunk (coalesced 256-byte rows, all
+// loads of the wave in flight together) and zeroes them; the wave partials
+// are combined in a fixed order (FP64).
+constexpr int kFoldWaves = 8;
+
+__global__ void __launch_bounds__(64 * kFoldWaves) finish_fold_kernel(FinishPack pack) {
+  __shared__ double part[2][kFoldWaves][64];
   const smx_finish_desc &d = pack.d[blockIdx.y];
   if (static_cast<int64_t>(blockIdx.x) * 64 >= d.n) return;  // uniform per block
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -309,8 +312,8 @@ __global__ void __launch_bounds__(256) finish_fold_kernel(FinishPack pack) {
     float *slots = v ? d.slots_first : d.slots_sq;
     double t = 0.0;
     if (ok) {
-#pragma unroll 8
-      for (int p = wave; p < d.n_slots; p += 4) {
+#pragma unroll 16
+      for (int p = wave; p < d.n_slots; p += kFoldWaves) {
         float *s = slots + static_cast<int64_t>(p) * d.n + c;
         t += static_cast<double>(*s);
         *s = 0.f;
@@ -322,7 +325,9 @@ __global__ void __launch_bounds__(256) finish_fold_kernel(FinishPack pack) {
   if (wave == 0 && ok) {
     for (int v = 0; v < nv; ++v) {
       float *sum = v ? d.sum_first : d.sum_sq;
-      const double t = (part[v][0][lane] + part[v][1][lane]) + (part[v][2][lane] + part[v][3][lane]);
+      double t = 0.0;
+#pragma unroll
+      for (int w = 0; w < kFoldWaves; ++w) t += part[v][w][lane];
       sum[c] = static_cast<float>(static_cast<double>(sum[c]) + t);
     }
   }
@@ -333,8 +338,10 @@ __device__ __forceinline__ float ema_update(float e, float x, float beta, float 
   return e * beta + x * omb;
 }
 
-// One block per descriptor.
-__global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta, float omb) {
+// One block of kFinishThreads per descriptor.
+constexpr int kFinishThreads = 1024;
+
+__global__ void __launch_bounds__(kFinishThreads) finish_kernel(FinishPack pack, float beta, float omb) {
   __shared__ double scratch[16];
   const smx_finish_desc &d = pack.d[blockIdx.x];
   const int64_t n = d.n;
@@ -343,11 +350,11 @@ __global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta
   if (d.kind == 2) {
     // b = sum/count; b /= max(mean(b), tiny); EMA; diagonal inverse sqrt.
     double part = 0.0;
-    for (int64_t c = t; c < n; c += 256) part += static_cast<double>(d.sum_sq[c] / cnt);
+    for (int64_t c = t; c < n; c += kFinishThreads) part += static_cast<double>(d.sum_sq[c] / cnt);
     const float bmean = static_cast<float>(block_sum(part, scratch) / static_cast<double>(n));
     const float den = fmaxf(bmean, FLT_MIN);
     double epart = 0.0;
-    for (int64_t c = t; c < n; c += 256) {
+    for (int64_t c = t; c < n; c += kFinishThreads) {
       const float b = (d.sum_sq[c] / cnt) / den;
       const float e = d.first ? b : ema_update(d.ema[c], b, beta, omb);
       d.ema[c] = e;
@@ -355,7 +362,7 @@ __global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta
     }
     const float em = static_cast<float>(block_sum(epart, scratch) / static_cast<double>(n));
     const float emc = fmaxf(em, FLT_MIN);
-    for (int64_t c = t; c < n; c += 256) {
+    for (int64_t c = t; c < n; c += kFinishThreads) {
       const float r = fmaxf(d.ema[c], em * 1e-6f) / emc;
       d.inv[c] = rsqrtf(fmaxf(r, 1e-6f));
       d.sum_sq[c] = 0.f;
@@ -364,7 +371,7 @@ __global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta
   }
   // A side: second = sum/count; EMA (first copies); factor.
   double epart = 0.0;
-  for (int64_t c = t; c < n; c += 256) {
+  for (int64_t c = t; c < n; c += kFinishThreads) {
     const float second = d.sum_sq[c] / cnt;
     const float e = d.first ? second : ema_update(d.ema[c], second, beta, omb);
     d.ema[c] = e;
@@ -379,7 +386,7 @@ __global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta
   const float em = static_cast<float>(block_sum(epart, scratch) / static_cast<double>(n));
   if (d.kind == 0) {
     const float emc = fmaxf(em, FLT_MIN);
-    for (int64_t c = t; c < n; c += 256) {
+    for (int64_t c = t; c < n; c += kFinishThreads) {
       const float r = fmaxf(d.ema[c], em * 1e-6f) / emc;
       d.inv[c] = rsqrtf(fmaxf(r, 1e-6f));
     }
@@ -391,7 +398,7 @@ __global__ void __launch_bounds__(256) finish_kernel(FinishPack pack, float beta
   const float q = fmaxf(em, FLT_MIN);
   const float sq = sqrtf(q);
   double zpart = 0.0;
-  for (int64_t c = t; c < n; c += 256) {
+  for (int64_t c = t; c < n; c += kFinishThreads) {
     const float m = d.mean_ema[c];
     const float var = fmaxf(d.ema[c] - m * m, 0.f);
     const float inv = rsqrtf(fmaxf(var / q, 1e-6f));
@@ -523,10 +530,10 @@ extern "C" int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc, do
       nmax = std::max<int64_t>(nmax, pack.d[i].n);
     }
     hipLaunchKernelGGL(finish_fold_kernel, dim3(static_cast<unsigned>(ceil_div(nmax, 64)), pack.n),
-                       dim3(256), 0, st, pack);
+                       dim3(64 * kFoldWaves), 0, st, pack);
     int rc = check_launch("stats_finish(fold)");
     if (rc) return rc;
-    hipLaunchKernelGGL(finish_kernel, dim3(pack.n), dim3(256), 0, st, pack, static_cast<float>(beta),
+    hipLaunchKernelGGL(finish_kernel, dim3(pack.n), dim3(kFinishThreads), 0, st, pack, static_cast<float>(beta),
                        static_cast<float>(1.0 - beta));
     rc = check_launch("stats_finish");
     if (rc) return rc;
