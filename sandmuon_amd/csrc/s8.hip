@@ -757,67 +757,87 @@ s8_stage_kernel(StageArgs args) {
   }
 }
 
-// Stage-1 polynomial operand (sandmuon/optimizer.py:84-86), one 256x256
-// tile of one matrix per block: P1 = a I + (b G)/s^2 + (c G2)/s^4 from the
+// Stage-1 polynomial operand (sandmuon/optimizer.py:84-86) over the r x r
+// matrices of a class: P1 = a I + (b G)/s^2 + (c G2)/s^4 from the
 // normalised G and the FP32 G2 of the square phase, written over G2 in the
-// p buffer in operand form.  Each thread handles whole 16-element groups,
-// whose FP32 and interleaved BF16 forms occupy the same 64 bytes.
+// p buffer in operand form.  A block takes kPolyChunk consecutive
+// 16-element groups of one matrix (64 KB of each buffer, contiguous), a
+// thread kPolyGroups of them; whole groups keep the FP32 and interleaved
+// BF16 forms in the same 64 bytes.  The loads are issued before the block
+// sums the stage-1 scalars, which they do not depend on.
+constexpr int kPolyGroups = 4;
+constexpr int kPolyChunk = 256 * kPolyGroups;  // groups per block
+
+__host__ __device__ inline int64_t poly_blocks_per_matrix(const S8Class &k) {
+  return k.rp * k.rp / 16 / kPolyChunk;  // rp is a multiple of 256
+}
+
 template <int MODE>
 __global__ void __launch_bounds__(256) s8_poly1_kernel(StageArgs args) {
   __shared__ double bcast;
   constexpr bool PL = MODE == SMX_S8_COMP_BF16;
   const TileRef ref = tile_of(args);
   const S8Class &K = *ref.k;
-  const int64_t tpm = static_cast<int64_t>(K.tiles_m) * K.tiles_m;
+  const int64_t tpm = poly_blocks_per_matrix(K);
   if (ref.L >= tpm * K.count) return;
   const S8Mat M{K, static_cast<int>(ref.L / tpm)};
-  const int64_t tix = ref.L % tpm;
-  const int64_t r0 = (tix / K.tiles_m) * kTile, c0 = (tix % K.tiles_m) * kTile;
+  const int64_t g0 = (ref.L % tpm) * kPolyChunk;  // first group of the block
+  const int64_t gpr = K.rp / 16;                   // groups per row
+  const float *G = M.g();
+  float *P = M.p();
+  int64_t row[kPolyGroups], col[kPolyGroups], idx[kPolyGroups];
+  float4 w4[kPolyGroups][4];
+  uint4 g4[kPolyGroups][4];  // FP32 G, or its 16 hi then 16 lo BF16 values
+#pragma unroll
+  for (int k = 0; k < kPolyGroups; ++k) {
+    const int64_t q = g0 + threadIdx.x + 256 * k;
+    row[k] = q / gpr;
+    col[k] = (q % gpr) * 16;
+    idx[k] = q * 16;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w4[k][e] = reinterpret_cast<const float4 *>(P + idx[k])[e];
+      g4[k][e] = reinterpret_cast<const uint4 *>(G + idx[k])[e];
+    }
+  }
   const Stage1Scalars sc = stage1_scalars(M, &bcast);
   const float s2 = sc.s * sc.s;
   const float is2 = sc.ok ? 1.0f / s2 : 0.f, is4 = sc.ok ? 1.0f / (s2 * s2) : 0.f;
-  const float *G = M.g();
-  float *P = M.p();
-  constexpr int kGroups = kTile * kTile / 16;
-  for (int q = threadIdx.x; q < kGroups; q += 256) {
-    const int64_t row = r0 + q / (kTile / 16), col = c0 + (q % (kTile / 16)) * 16;
-    const int64_t idx = row * K.rp + col;
+#pragma unroll
+  for (int k = 0; k < kPolyGroups; ++k) {
     float g[16], w[16];
-    const float4 *w4 = reinterpret_cast<const float4 *>(P + idx);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float4 t = w4[e];
-      w[4 * e] = t.x; w[4 * e + 1] = t.y; w[4 * e + 2] = t.z; w[4 * e + 3] = t.w;
+      w[4 * e] = w4[k][e].x; w[4 * e + 1] = w4[k][e].y; w[4 * e + 2] = w4[k][e].z; w[4 * e + 3] = w4[k][e].w;
     }
     if constexpr (PL) {
-      const uint4 *g4 = reinterpret_cast<const uint4 *>(G + idx);  // 16 hi, then 16 lo
-      const uint4 h0 = g4[0], h1 = g4[1], l0 = g4[2], l1 = g4[3];
-      const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-      const uint32_t lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+      const uint32_t hw[8] = {g4[k][0].x, g4[k][0].y, g4[k][0].z, g4[k][0].w,
+                              g4[k][1].x, g4[k][1].y, g4[k][1].z, g4[k][1].w};
+      const uint32_t lw[8] = {g4[k][2].x, g4[k][2].y, g4[k][2].z, g4[k][2].w,
+                              g4[k][3].x, g4[k][3].y, g4[k][3].z, g4[k][3].w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         g[2 * e] = __uint_as_float(hw[e] << 16) + __uint_as_float(lw[e] << 16);
         g[2 * e + 1] = __uint_as_float(hw[e] & 0xffff0000u) + __uint_as_float(lw[e] & 0xffff0000u);
       }
     } else {
-      const float4 *g4 = reinterpret_cast<const float4 *>(G + idx);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float4 t = g4[e];
-        g[4 * e] = t.x; g[4 * e + 1] = t.y; g[4 * e + 2] = t.z; g[4 * e + 3] = t.w;
+        g[4 * e] = __uint_as_float(g4[k][e].x); g[4 * e + 1] = __uint_as_float(g4[k][e].y);
+        g[4 * e + 2] = __uint_as_float(g4[k][e].z); g[4 * e + 3] = __uint_as_float(g4[k][e].w);
       }
     }
     float v[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const float eye = (row == col + e && row < K.r) ? args.a : 0.f;
+      const float eye = (row[k] == col[k] + e && row[k] < K.r) ? args.a : 0.f;
       v[e] = (eye + (args.b * g[e]) * is2) + (args.c * w[e]) * is4;
     }
     float lo8[8], hi8[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) { lo8[e] = v[e]; hi8[e] = v[8 + e]; }
-    put_operand8(P, idx, lo8, PL);
-    put_operand8(P, idx + 8, hi8, PL);
+    put_operand8(P, idx[k], lo8, PL);
+    put_operand8(P, idx[k] + 8, hi8, PL);
   }
 }
 
@@ -906,7 +926,7 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
   for (int ci : order) {
     const S8Class &k = Lay.cls[ci];
     if (k.count == 0) continue;
-    const int64_t tpm = PHASE == kPoly1 ? static_cast<int64_t>(k.tiles_m) * k.tiles_m : phase_tiles(k, PHASE);
+    const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE);
     const int64_t nt = round_up(tpm * k.count, 8);
     a.seg_off[a.n_seg] = off;
     a.seg_cls[a.n_seg] = ci;
