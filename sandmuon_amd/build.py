@@ -2,7 +2,9 @@
 
 Usage: python -m sandmuon_amd.build   (or sandmuon_amd.build.build())
 Each .hip file under csrc/ is compiled to an object in parallel, then the
-objects are linked into sandmuon_amd/libsandmuon_amd.so.
+objects are linked into sandmuon_amd/libsandmuon_amd.so; the C-ABI example
+program examples/abi_example.cpp is linked against it as
+sandmuon_amd/abi_example.
 """
 from __future__ import annotations
 
@@ -17,6 +19,10 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libsandmuon_amd.so"
+# A host program that uses the library through the C ABI only (HIP memory
+# and streams, no Python); tests/test_gpu_abi_example.py runs it.
+EXAMPLE_SRC = HERE / "examples" / "abi_example.cpp"
+EXAMPLE = HERE / "abi_example"
 ARCH = os.environ.get("SANDMUON_AMD_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep the compiler from emitting packed FP32 VALU ops.
@@ -65,6 +71,13 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         if res.returncode != 0:
             raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
         shutil.move(str(tmp_lib), str(LIB))
+        tmp_exe = Path(tmp) / EXAMPLE.name
+        cmd = [hipcc, "-O2", "-std=c++17", str(EXAMPLE_SRC), "-o", str(tmp_exe), f"-L{HERE}", "-lsandmuon_amd",
+               "-Wl,-rpath,$ORIGIN", "-Wno-unused-command-line-argument"]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"example build failed:\n{res.stdout}{res.stderr}")
+        shutil.move(str(tmp_exe), str(EXAMPLE))
     return LIB
 
 
