@@ -74,6 +74,24 @@ int smx_stats_accumulate(const void *x, int dtype, int64_t rows, int64_t cols,
                          int64_t row_stride, float *slots_sq,
                          float *slots_first, int32_t n_slots, void *stream);
 
+/* smx_stats_accumulate_batch: several hook calls of the bodies above in
+ * one launch (the same sandmuon/optimizer.py:156-168 / :171-177 bodies,
+ * applied to n_desc inputs at once).  Each descriptor adds exactly what
+ * smx_stats_accumulate with the same arguments adds, bit for bit.  The
+ * descriptors run concurrently, so no two may share slot rows (SMX_EINVAL
+ * if their slot ranges overlap); the inputs must stay unmodified until the
+ * launch has run on `stream`. */
+typedef struct smx_stats_desc {
+  const void *x;
+  float *slots_sq;
+  float *slots_first;   /* NULL: B side or diagonal A */
+  int64_t rows, cols, row_stride;
+  int32_t dtype, n_slots;
+} smx_stats_desc;
+
+int smx_stats_accumulate_batch(const smx_stats_desc *descs, int32_t n_desc,
+                               void *stream);
+
 /* The statistics fused into passes a mixed-precision Linear makes anyway
  * (the hook bodies above, moved; no counterpart entry point in the
  * reference).  Both add sum(x^2) to slots_sq exactly as

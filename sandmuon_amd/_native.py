@@ -42,6 +42,12 @@ class FinishDesc(ctypes.Structure):
                 ("first", c_int32), ("pad_", c_int32)]
 
 
+class StatsDesc(ctypes.Structure):
+    _fields_ = [("x", c_void_p), ("slots_sq", c_void_p), ("slots_first", c_void_p),
+                ("rows", c_int64), ("cols", c_int64), ("row_stride", c_int64),
+                ("dtype", c_int32), ("n_slots", c_int32)]
+
+
 class AdamwDesc(ctypes.Structure):
     _fields_ = [("param", c_void_p), ("grad", c_void_p), ("exp_avg", c_void_p),
                 ("exp_avg_sq", c_void_p), ("n", c_int64), ("offset", c_int64),
@@ -61,6 +67,7 @@ SIGNATURES = {
     "smx_last_error": (ctypes.c_char_p, []),
     "smx_stats_accumulate": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                      c_int32, c_void_p]),
+    "smx_stats_accumulate_batch": (c_int, [ctypes.POINTER(StatsDesc), c_int32, c_void_p]),
     "smx_stats_cast": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int32,
                                c_void_p, c_int, c_int64, c_void_p]),
     "smx_stats_colsum_workspace_bytes": (c_int64, [c_int64, c_int32]),
@@ -154,6 +161,18 @@ def stats_accumulate(rows2d: torch.Tensor, slots_sq: torch.Tensor, slots_first: 
                                     rows2d.shape[1], rows2d.stride(0), slots_sq.data_ptr(),
                                     ptr(slots_first), slots_sq.shape[0], stream_of(rows2d.device))
     _check(rc, "smx_stats_accumulate")
+
+
+def stats_accumulate_batch(entries, stream: int) -> None:
+    """One launch over several hook inputs: entries of (rows2d, slots_sq,
+    slots_first) whose slot rows are pairwise distinct."""
+    descs = (StatsDesc * len(entries))()
+    for d, (rows2d, sq, fs) in zip(descs, entries):
+        d.x, d.slots_sq, d.slots_first = rows2d.data_ptr(), sq.data_ptr(), ptr(fs)
+        d.rows, d.cols, d.row_stride = rows2d.shape[0], rows2d.shape[1], rows2d.stride(0)
+        d.dtype, d.n_slots = dtype_code(rows2d.dtype), sq.shape[0]
+    rc = lib().smx_stats_accumulate_batch(descs, len(entries), stream)
+    _check(rc, "smx_stats_accumulate_batch")
 
 
 def stats_cast(rows2d: torch.Tensor, slots_sq: torch.Tensor, slots_first: Optional[torch.Tensor],

@@ -12,73 +12,65 @@
 
 #include <algorithm>
 #include <cfloat>
+#include <climits>
+#include <type_traits>
 #include <vector>
 
 namespace smx {
 
 constexpr int kStatsThreads = 512;
 constexpr int kStatsWaves = kStatsThreads / 64;
+constexpr int kStatsMaxTW = 256; // widest column tile (channels)
 
-template <int DT, int VEC>
-struct VecLoad;
-
-template <>
-struct VecLoad<SMX_F32, 4> {
-  __device__ __forceinline__ static void load(const void *p, int64_t i, float *v) {
-    float4 q = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
-    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
-  }
-};
-
-template <int DT>
-struct VecLoad2B8 {
-  __device__ __forceinline__ static void load(const void *p, int64_t i, float *v) {
-    uint4 q = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
-    uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      if constexpr (DT == SMX_BF16) {
-        v[2 * k] = __uint_as_float(w[k] << 16);
-        v[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
-      } else {
-        v[2 * k] = f16_bits_to_f32(static_cast<uint16_t>(w[k] & 0xffffu));
-        v[2 * k + 1] = f16_bits_to_f32(static_cast<uint16_t>(w[k] >> 16));
-      }
-    }
-  }
-};
-template <>
-struct VecLoad<SMX_BF16, 8> : VecLoad2B8<SMX_BF16> {};
-template <>
-struct VecLoad<SMX_F16, 8> : VecLoad2B8<SMX_F16> {};
-
-template <int DT>
-struct VecLoad1 {
-  __device__ __forceinline__ static void load(const void *p, int64_t i, float *v) {
-    v[0] = load_elem<DT>(p, i);
-  }
-};
-template <>
-struct VecLoad<SMX_F32, 1> : VecLoad1<SMX_F32> {};
-template <>
-struct VecLoad<SMX_BF16, 1> : VecLoad1<SMX_BF16> {};
-template <>
-struct VecLoad<SMX_F16, 1> : VecLoad1<SMX_F16> {};
-
-// What a launch produces besides sum(x^2) into the slot rows.
+// What a job produces besides sum(x^2) into the slot rows.
 enum StatsMode : int {
   kSqOnly = 0,    // B side, diagonal A
   kSqFirst = 1,   // rank-one A: sum(x) into its own slot rows
   kSqColsum = 2,  // sum(x) of this call's rows into per-chunk partials (a bias gradient)
 };
 
-struct StatsArgs {
-  const void *x;
-  int64_t rows, cols, row_stride, rows_per_chunk;
-  float *slots_sq;
-  float *first;        // kSqFirst: slot rows of sum(x); kSqColsum: per-chunk partials, plain stores
-  void *cast_out;      // CAST: low-precision copy of x
-  int64_t out_stride;
+// Element access of one lane's VEC consecutive channels: `raw` loads their
+// bits (16 bytes for the vector forms, one element otherwise) and `cvt`
+// widens them to FP32.  Keeping the raw bits in registers until they are
+// consumed lets the next batch of loads be issued first.
+template <int DT, int VEC>
+struct Elems {
+  using Raw = std::conditional_t<VEC == 1, uint32_t, uint4>;
+  static constexpr int kSize = DT == SMX_F32 ? 4 : 2;
+  static_assert(VEC == 1 || VEC * kSize == 16, "vector forms load 16 bytes");
+  __device__ __forceinline__ static Raw raw(const void *p, int64_t i) {
+    const char *b = static_cast<const char *>(p) + i * kSize;
+    if constexpr (VEC > 1) return *reinterpret_cast<const uint4 *>(b);
+    else if constexpr (kSize == 4) return *reinterpret_cast<const uint32_t *>(b);
+    else return *reinterpret_cast<const uint16_t *>(b);
+  }
+  __device__ __forceinline__ static float one(uint32_t w) {
+    if constexpr (DT == SMX_F32) return __uint_as_float(w);
+    else if constexpr (DT == SMX_BF16) return __uint_as_float(w << 16);
+    else return f16_bits_to_f32(static_cast<uint16_t>(w));
+  }
+  __device__ __forceinline__ static void cvt(const Raw &q, float *v) {
+    if constexpr (VEC == 1) {
+      v[0] = one(q);
+    } else {
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if constexpr (DT == SMX_F32) {
+          v[k] = __uint_as_float(w[k]);
+        } else if constexpr (DT == SMX_BF16) {
+          v[2 * k] = __uint_as_float(w[k] << 16);
+          v[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+        } else {
+          typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+          typedef float float2_t __attribute__((ext_vector_type(2)));
+          const float2_t f = __builtin_convertvector(__builtin_bit_cast(half2_t, w[k]), float2_t);
+          v[2 * k] = f.x;
+          v[2 * k + 1] = f.y;
+        }
+      }
+    }
+  }
 };
 
 template <int CAST, int VEC>
@@ -103,136 +95,263 @@ __device__ __forceinline__ void store_cast(void *out, int64_t i, const float *v)
   }
 }
 
-// grid = (column tiles, row chunks); block = kStatsThreads.
-// A column tile is CT lanes x VEC channels; a wave covers 64/CT rows per
-// step, the block kStatsWaves*64/CT rows per step.  CAST (SMX_BF16 or
-// SMX_F16, fp32 input only) also writes x converted, as the mixed-precision
-// cast in front of a Linear would.  MODE and CAST change nothing in how
-// sum(x^2) is formed, so every variant adds the same bits to the slots.
-template <int DT, int VEC, int CT, int MODE, int CAST>
-__global__ void __launch_bounds__(kStatsThreads) stats_accumulate_kernel(StatsArgs a) {
+// One statistics job: a [rows, cols] input split into n_chunks row chunks
+// (chunk p adds into slot row p) and column tiles of CT lanes x VEC
+// channels; it occupies blocks [block_begin, block_begin + tiles*n_chunks)
+// of a launch.
+struct StatsJob {
+  const void *x;
+  float *sq;
+  float *first;     // kSqFirst: slot rows of sum(x); kSqColsum: per-chunk partials, plain stores
+  void *cast_out;   // CAST: low-precision copy of x
+  int64_t rows, cols, row_stride, out_stride, rows_per_chunk;
+  int32_t block_begin, tiles, code, pad_;
+};
+constexpr int kStatsJobs = 24;  // jobs per launch, passed by value
+struct StatsPack {
+  StatsJob job[kStatsJobs];
+  int32_t n;
+};
+static_assert(sizeof(StatsPack) <= 4000, "StatsPack is passed by value in the kernel arguments");
+
+// The block (tile, chunk) of a job.  A wave covers 64/CT rows per step, the
+// block kStatsWaves*64/CT rows.  Each lane sums its rows in order, with
+// U loads in flight and the next batch issued before the current one
+// is consumed; lanes holding the same channels are then added by xor
+// shuffles, the waves in wave order, and the sum is added to the slot row,
+// whose old value was loaded at the start of the block.  CAST (fp32 input
+// only) also writes x converted to bf16/f16, as the mixed-precision cast in
+// front of a Linear would.  MODE and CAST change nothing in how sum(x^2) is
+// formed, so every variant adds the same bits to the slots.
+template <int DT, int VEC, int CT, int U, int MODE, int CAST>
+__device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int64_t chunk, float *red) {
+  using E = Elems<DT, VEC>;
+  using Raw = typename E::Raw;
   constexpr bool FIRST = MODE != kSqOnly;
-  constexpr int RPW = 64 / CT;                 // rows per wave step
-  constexpr int GROUPS = kStatsWaves * RPW;    // row groups per block
-  constexpr int TW = CT * VEC;                 // channels per tile
-  __shared__ float red_sq[GROUPS][TW];
-  __shared__ float red_first[FIRST ? GROUPS : 1][FIRST ? TW : 1];
+  constexpr int RPW = 64 / CT;
+  constexpr int GROUPS = kStatsWaves * RPW;
+  constexpr int TW = CT * VEC;
+  static_assert(TW <= kStatsMaxTW && TW <= kStatsThreads, "one owner thread per channel");
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int group = wave * RPW + lane / CT;
-  const int64_t vcol = static_cast<int64_t>(blockIdx.x) * CT + (lane % CT);
-  const int64_t col0 = vcol * VEC;
-  const int64_t r_begin = static_cast<int64_t>(blockIdx.y) * a.rows_per_chunk;
-  const int64_t r_end = min(a.rows, r_begin + a.rows_per_chunk);
+  const int64_t col0 = (tile * CT + lane % CT) * VEC;
+  const int64_t r_begin = chunk * J.rows_per_chunk;
+  const int64_t r_end = min(J.rows, r_begin + J.rows_per_chunk);
   const bool empty = r_begin >= r_end;
   // An empty chunk adds nothing; with kSqColsum it still writes its zero
-  // partial.
+  // partial.  Uniform per block.
   if (MODE != kSqColsum && empty) return;
-  const bool active = col0 < a.cols;
+  const int64_t tile_col0 = tile * TW;
+  const int64_t row_off = chunk * J.cols + tile_col0;
+  const int c = threadIdx.x;
+  const bool own = c < TW && tile_col0 + c < J.cols;
+  float old_sq = 0.f, old_first = 0.f;
+  if (own && !empty) old_sq = J.sq[row_off + c];
+  if constexpr (MODE == kSqFirst)
+    if (own) old_first = J.first[row_off + c];
 
   float acc_sq[VEC], acc_first[VEC];
 #pragma unroll
   for (int k = 0; k < VEC; ++k) { acc_sq[k] = 0.f; acc_first[k] = 0.f; }
 
-  if (active) {
-    // Loads in flight per thread: 2 for the narrow tiles (measured 8% faster
-    // on 768-wide bf16 inputs), 4 otherwise.
-    constexpr int U = CT == 16 ? 2 : 4;
+  if (!empty && col0 < J.cols) {
     int64_t r = r_begin + group;
-    for (; r + (U - 1) * GROUPS < r_end; r += U * GROUPS) {
-      float v[U][VEC];
+    auto issue = [&](Raw (&q)[U], int64_t &rq) {
+      rq = r;
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        VecLoad<DT, VEC>::load(a.x, (r + u * GROUPS) * a.row_stride + col0, v[u]);
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) {
-          acc_sq[k] = fmaf(v[u][k], v[u][k], acc_sq[k]);
-          if constexpr (FIRST) acc_first[k] += v[u][k];
-        }
-      if constexpr (CAST != 0) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) store_cast<CAST, VEC>(a.cast_out, (r + u * GROUPS) * a.out_stride + col0, v[u]);
-      }
-    }
-    for (; r < r_end; r += GROUPS) {
+      for (int u = 0; u < U; ++u) q[u] = E::raw(J.x, (r + u * GROUPS) * J.row_stride + col0);
+      r += U * GROUPS;
+    };
+    auto eat1 = [&](const Raw &q, int64_t row) {
       float v[VEC];
-      VecLoad<DT, VEC>::load(a.x, r * a.row_stride + col0, v);
+      E::cvt(q, v);
 #pragma unroll
       for (int k = 0; k < VEC; ++k) {
         acc_sq[k] = fmaf(v[k], v[k], acc_sq[k]);
         if constexpr (FIRST) acc_first[k] += v[k];
       }
-      if constexpr (CAST != 0) store_cast<CAST, VEC>(a.cast_out, r * a.out_stride + col0, v);
-    }
-  }
-  const int cl = (lane % CT) * VEC;
+      if constexpr (CAST != 0) store_cast<CAST, VEC>(J.cast_out, row * J.out_stride + col0, v);
+    };
+    auto eat = [&](const Raw (&q)[U], int64_t rq) {
 #pragma unroll
-  for (int k = 0; k < VEC; ++k) {
-    red_sq[group][cl + k] = acc_sq[k];
-    if constexpr (FIRST) red_first[group][cl + k] = acc_first[k];
+      for (int u = 0; u < U; ++u) eat1(q[u], rq + u * GROUPS);
+    };
+    const int64_t n_rows = r < r_end ? (r_end - r + GROUPS - 1) / GROUPS : 0;
+    const int64_t nb = n_rows / U;
+    Raw A[U], B[U];
+    int64_t ra = 0, rb = 0;
+    if (nb > 0) {
+      issue(A, ra);
+      int64_t k = 1;
+      for (; k + 1 < nb; k += 2) {
+        issue(B, rb);
+        eat(A, ra);
+        issue(A, ra);
+        eat(B, rb);
+      }
+      if (k < nb) {
+        issue(B, rb);
+        eat(A, ra);
+        eat(B, rb);
+      } else {
+        eat(A, ra);
+      }
+    }
+    for (; r < r_end; r += GROUPS) eat1(E::raw(J.x, r * J.row_stride + col0), r);
+  }
+  // Lanes l, l + CT, ... of a wave hold the same channels.
+#pragma unroll
+  for (int off = CT; off < 64; off <<= 1)
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      acc_sq[k] += __shfl_xor(acc_sq[k], off);
+      if constexpr (FIRST) acc_first[k] += __shfl_xor(acc_first[k], off);
+    }
+  float *red_sq = red, *red_first = red + kStatsWaves * kStatsMaxTW;
+  if (lane < CT) {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      red_sq[wave * TW + lane * VEC + k] = acc_sq[k];
+      if constexpr (FIRST) red_first[wave * TW + lane * VEC + k] = acc_first[k];
+    }
   }
   __syncthreads();
-  const int64_t tile_col0 = static_cast<int64_t>(blockIdx.x) * TW;
-  const int64_t row_off = static_cast<int64_t>(blockIdx.y) * a.cols + tile_col0;
-  float *slot_sq = a.slots_sq + row_off;
-  float *first = FIRST ? a.first + row_off : nullptr;
-  for (int c = threadIdx.x; c < TW; c += kStatsThreads) {
-    if (tile_col0 + c >= a.cols) break;
+  if (own) {
     float s = 0.f, f = 0.f;
 #pragma unroll
-    for (int g = 0; g < GROUPS; ++g) {
-      s += red_sq[g][c];
-      if constexpr (FIRST) f += red_first[g][c];
+    for (int w = 0; w < kStatsWaves; ++w) {
+      s += red_sq[w * TW + c];
+      if constexpr (FIRST) f += red_first[w * TW + c];
     }
-    if (!empty) slot_sq[c] += s;
-    if constexpr (MODE == kSqFirst) first[c] += f;
-    if constexpr (MODE == kSqColsum) first[c] = f;
+    if (!empty) J.sq[row_off + c] = old_sq + s;
+    if constexpr (MODE == kSqFirst) J.first[row_off + c] = old_first + f;
+    if constexpr (MODE == kSqColsum) J.first[row_off + c] = f;
   }
 }
 
-template <int DT, int VEC, int CT, int MODE, int CAST>
-static void launch_acc(StatsArgs a, int32_t n_slots, hipStream_t st) {
-  const int64_t vcols = ceil_div(a.cols, VEC);
-  dim3 grid(static_cast<unsigned>(ceil_div(vcols, CT)), static_cast<unsigned>(n_slots));
-  a.rows_per_chunk = ceil_div(a.rows, n_slots);
-  hipLaunchKernelGGL((stats_accumulate_kernel<DT, VEC, CT, MODE, CAST>), grid, dim3(kStatsThreads), 0, st, a);
+// Element forms of a job: the vector forms load 16 bytes per lane (32-lane
+// column tiles), the scalar forms one element (64-lane tiles) for inputs
+// whose width, row stride or address is not 16-byte aligned.
+enum StatsForm : int { kF32V4 = 0, kBf16V8, kF16V8, kF32V1, kBf16V1, kF16V1, kNumForms };
+__host__ __device__ constexpr int stats_code(int form, int mode, int cast) { return (form * 3 + mode) * 3 + cast; }
+
+template <int FORM>
+struct FormTraits;
+// U: loads per lane per register batch (the f16 form widens its batch
+// early, so it keeps two loads per batch to stay within the register
+// budget the other forms set).
+template <> struct FormTraits<kF32V4> { static constexpr int DT = SMX_F32, VEC = 4, CT = 32, U = 4; };
+template <> struct FormTraits<kBf16V8> { static constexpr int DT = SMX_BF16, VEC = 8, CT = 32, U = 4; };
+template <> struct FormTraits<kF16V8> { static constexpr int DT = SMX_F16, VEC = 8, CT = 32, U = 2; };
+template <> struct FormTraits<kF32V1> { static constexpr int DT = SMX_F32, VEC = 1, CT = 64, U = 4; };
+template <> struct FormTraits<kBf16V1> { static constexpr int DT = SMX_BF16, VEC = 1, CT = 64, U = 4; };
+template <> struct FormTraits<kF16V1> { static constexpr int DT = SMX_F16, VEC = 1, CT = 64, U = 4; };
+
+template <int FORM, int MODE, int CAST>
+__device__ __forceinline__ void run_tile(const StatsJob &J, int64_t tile, int64_t chunk, float *red) {
+  using F = FormTraits<FORM>;
+  stats_tile<F::DT, F::VEC, F::CT, F::U, MODE, CAST>(J, tile, chunk, red);
 }
 
-template <int DT, int VEC, int MODE, int CAST>
-static void dispatch_ct(const StatsArgs &a, int32_t n_slots, hipStream_t st) {
-  // The widest column tile that still gives >= 6 tiles, so that a hook call
-  // of 16K rows puts >= 768 blocks (24 waves per CU) in flight.
-  const int64_t vcols = ceil_div(a.cols, VEC);
-  if (vcols >= 6 * 64)
-    launch_acc<DT, VEC, 64, MODE, CAST>(a, n_slots, st);
-  else if (vcols >= 6 * 32)
-    launch_acc<DT, VEC, 32, MODE, CAST>(a, n_slots, st);
-  else
-    launch_acc<DT, VEC, 16, MODE, CAST>(a, n_slots, st);
-}
-
-template <int MODE, int CAST>
-static void dispatch_dtype(const StatsArgs &a, int dtype, int32_t n_slots, hipStream_t st) {
-  const uintptr_t addr = reinterpret_cast<uintptr_t>(a.x);
-  if (dtype == SMX_F32) {
-    bool v4 = a.cols % 4 == 0 && a.row_stride % 4 == 0 && addr % 16 == 0;
-    if (CAST != 0) v4 = v4 && a.out_stride % 4 == 0 && reinterpret_cast<uintptr_t>(a.cast_out) % 8 == 0;
-    if (v4) dispatch_ct<SMX_F32, 4, MODE, CAST>(a, n_slots, st);
-    else dispatch_ct<SMX_F32, 1, MODE, CAST>(a, n_slots, st);
-    return;
+// grid.x = sum over the jobs of tiles * n_chunks; block = kStatsThreads.
+__global__ void __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(6))) stats_accumulate_kernel(StatsPack pack) {
+  __shared__ float red[2 * kStatsWaves * kStatsMaxTW];
+  const int b = static_cast<int>(blockIdx.x);
+  int j = 0;
+  while (j + 1 < pack.n && b >= pack.job[j + 1].block_begin) ++j;
+  const StatsJob &J = pack.job[j];
+  const int64_t local = b - J.block_begin;
+  const int64_t tile = local % J.tiles, chunk = local / J.tiles;
+#define SMX_STATS_CASE(FORM, MODE, CAST) \
+  case stats_code(FORM, MODE, CAST): run_tile<FORM, MODE, CAST>(J, tile, chunk, red); break;
+#define SMX_STATS_MODES(FORM)          \
+  SMX_STATS_CASE(FORM, kSqOnly, 0)     \
+  SMX_STATS_CASE(FORM, kSqFirst, 0)    \
+  SMX_STATS_CASE(FORM, kSqColsum, 0)
+#define SMX_STATS_CASTS(FORM)                 \
+  SMX_STATS_CASE(FORM, kSqOnly, SMX_BF16)     \
+  SMX_STATS_CASE(FORM, kSqFirst, SMX_BF16)    \
+  SMX_STATS_CASE(FORM, kSqOnly, SMX_F16)      \
+  SMX_STATS_CASE(FORM, kSqFirst, SMX_F16)
+  switch (J.code) {
+    SMX_STATS_MODES(kF32V4)
+    SMX_STATS_MODES(kBf16V8)
+    SMX_STATS_MODES(kF16V8)
+    SMX_STATS_MODES(kF32V1)
+    SMX_STATS_MODES(kBf16V1)
+    SMX_STATS_MODES(kF16V1)
+    SMX_STATS_CASTS(kF32V4)
+    SMX_STATS_CASTS(kF32V1)
+    default: break;
   }
-  if constexpr (CAST == 0) {
-    const bool v8 = a.cols % 8 == 0 && a.row_stride % 8 == 0 && addr % 16 == 0;
-    if (dtype == SMX_BF16) {
-      if (v8) dispatch_ct<SMX_BF16, 8, MODE, 0>(a, n_slots, st);
-      else dispatch_ct<SMX_BF16, 1, MODE, 0>(a, n_slots, st);
-    } else {
-      if (v8) dispatch_ct<SMX_F16, 8, MODE, 0>(a, n_slots, st);
-      else dispatch_ct<SMX_F16, 1, MODE, 0>(a, n_slots, st);
+#undef SMX_STATS_CASTS
+#undef SMX_STATS_MODES
+#undef SMX_STATS_CASE
+}
+
+// Host side: one job per input, launched in packs of kStatsJobs.
+struct StatsInput {
+  const void *x;
+  int dtype;
+  int64_t rows, cols, row_stride;
+  float *sq, *first;
+  int32_t n_slots;
+  int mode, cast;
+  void *cast_out;
+  int64_t out_stride;
+};
+
+static int stats_form(const StatsInput &in) {
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(in.x);
+  if (in.dtype == SMX_F32) {
+    bool v4 = in.cols % 4 == 0 && in.row_stride % 4 == 0 && addr % 16 == 0;
+    if (in.cast) v4 = v4 && in.out_stride % 4 == 0 && reinterpret_cast<uintptr_t>(in.cast_out) % 8 == 0;
+    return v4 ? kF32V4 : kF32V1;
+  }
+  const bool v8 = in.cols % 8 == 0 && in.row_stride % 8 == 0 && addr % 16 == 0;
+  if (in.dtype == SMX_BF16) return v8 ? kBf16V8 : kBf16V1;
+  return v8 ? kF16V8 : kF16V1;
+}
+
+static int stats_launch(const StatsInput *in, int n, hipStream_t st, const char *who) {
+  StatsPack pack{};
+  int64_t blocks = 0;
+  auto flush = [&]() -> int {
+    if (pack.n == 0) return SMX_OK;
+    hipLaunchKernelGGL(stats_accumulate_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kStatsThreads), 0, st,
+                       pack);
+    pack.n = 0;
+    blocks = 0;
+    return check_launch(who);
+  };
+  for (int i = 0; i < n; ++i) {
+    const StatsInput &s = in[i];
+    const int form = stats_form(s);
+    const int vec = form == kF32V4 ? 4 : (form == kBf16V8 || form == kF16V8) ? 8 : 1;
+    const int ct = vec == 1 ? 64 : 32;
+    const int64_t tiles = ceil_div(ceil_div(s.cols, vec), ct);
+    const int64_t nb = tiles * s.n_slots;
+    if (pack.n == kStatsJobs || blocks + nb > INT32_MAX) {
+      int rc = flush();
+      if (rc) return rc;
     }
+    StatsJob &J = pack.job[pack.n++];
+    J.x = s.x;
+    J.sq = s.sq;
+    J.first = s.first;
+    J.cast_out = s.cast_out;
+    J.rows = s.rows;
+    J.cols = s.cols;
+    J.row_stride = s.row_stride;
+    J.out_stride = s.out_stride;
+    J.rows_per_chunk = ceil_div(s.rows, s.n_slots);
+    J.block_begin = static_cast<int32_t>(blocks);
+    J.tiles = static_cast<int32_t>(tiles);
+    J.code = stats_code(form, s.mode, s.cast);
+    blocks += nb;
   }
+  return flush();
 }
 
 // colsum[c] = sum over the n_parts partial rows (stride cols) in FP64.
@@ -437,11 +556,45 @@ extern "C" int smx_stats_accumulate(const void *x, int dtype, int64_t rows, int6
   int rc = check_rows("stats_accumulate", x, dtype, rows, cols, row_stride, slots_sq, n_slots);
   if (rc) return rc;
   if (rows == 0) return SMX_OK;  // empty microbatch: nothing to add
-  const StatsArgs a{x, rows, cols, row_stride, 0, slots_sq, slots_first, nullptr, 0};
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (slots_first) dispatch_dtype<kSqFirst, 0>(a, dtype, n_slots, st);
-  else dispatch_dtype<kSqOnly, 0>(a, dtype, n_slots, st);
-  return check_launch("stats_accumulate");
+  const StatsInput in{x, dtype, rows, cols, row_stride, slots_sq, slots_first, n_slots,
+                      slots_first ? kSqFirst : kSqOnly, 0, nullptr, 0};
+  return stats_launch(&in, 1, static_cast<hipStream_t>(stream), "stats_accumulate");
+}
+
+extern "C" int smx_stats_accumulate_batch(const smx_stats_desc *descs, int32_t n_desc, void *stream) {
+  SMX_REQUIRE(n_desc >= 0 && (n_desc == 0 || descs), SMX_EINVAL, "stats_accumulate_batch: bad descriptor table");
+  std::vector<StatsInput> in;
+  in.reserve(n_desc);
+  for (int32_t i = 0; i < n_desc; ++i) {
+    const smx_stats_desc &d = descs[i];
+    const std::string who = "stats_accumulate_batch[" + std::to_string(i) + "]";
+    int rc = check_rows(who.c_str(), d.x, d.dtype, d.rows, d.cols, d.row_stride, d.slots_sq, d.n_slots);
+    if (rc) return rc;
+    // Jobs of one launch run concurrently: no two may add into the same
+    // slot rows.
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(d.slots_sq);
+    const uintptr_t hi = lo + static_cast<uintptr_t>(d.n_slots) * d.cols * 4;
+    for (int32_t k = 0; k < i; ++k) {
+      const smx_stats_desc &e = descs[k];
+      for (const float *p : {e.slots_sq, e.slots_first}) {
+        if (!p) continue;
+        const uintptr_t elo = reinterpret_cast<uintptr_t>(p);
+        const uintptr_t ehi = elo + static_cast<uintptr_t>(e.n_slots) * e.cols * 4;
+        for (const float *q : {d.slots_sq, d.slots_first}) {
+          if (!q) continue;
+          const uintptr_t qlo = reinterpret_cast<uintptr_t>(q);
+          const uintptr_t qhi = qlo + (hi - lo);
+          SMX_REQUIRE(qhi <= elo || ehi <= qlo, SMX_EINVAL,
+                      who + ": slot rows overlap those of descriptor " + std::to_string(k));
+        }
+      }
+    }
+    if (d.rows == 0) continue;  // empty microbatch: nothing to add
+    in.push_back(StatsInput{d.x, d.dtype, d.rows, d.cols, d.row_stride, d.slots_sq, d.slots_first, d.n_slots,
+                            d.slots_first ? kSqFirst : kSqOnly, 0, nullptr, 0});
+  }
+  return stats_launch(in.data(), static_cast<int>(in.size()), static_cast<hipStream_t>(stream),
+                      "stats_accumulate_batch");
 }
 
 extern "C" int smx_stats_cast(const void *x, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
@@ -454,16 +607,9 @@ extern "C" int smx_stats_cast(const void *x, int dtype, int64_t rows, int64_t co
   SMX_REQUIRE(rows == 0 || out, SMX_EINVAL, "stats_cast: null output");
   SMX_REQUIRE(out_stride >= cols || rows <= 1, SMX_ESHAPE, "stats_cast: out_stride must be >= cols");
   if (rows == 0) return SMX_OK;
-  const StatsArgs a{x, rows, cols, row_stride, 0, slots_sq, slots_first, out, out_stride};
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (out_dtype == SMX_BF16) {
-    if (slots_first) dispatch_dtype<kSqFirst, SMX_BF16>(a, dtype, n_slots, st);
-    else dispatch_dtype<kSqOnly, SMX_BF16>(a, dtype, n_slots, st);
-  } else {
-    if (slots_first) dispatch_dtype<kSqFirst, SMX_F16>(a, dtype, n_slots, st);
-    else dispatch_dtype<kSqOnly, SMX_F16>(a, dtype, n_slots, st);
-  }
-  return check_launch("stats_cast");
+  const StatsInput in{x, dtype, rows, cols, row_stride, slots_sq, slots_first, n_slots,
+                      slots_first ? kSqFirst : kSqOnly, out_dtype, out, out_stride};
+  return stats_launch(&in, 1, static_cast<hipStream_t>(stream), "stats_cast");
 }
 
 extern "C" int64_t smx_stats_colsum_workspace_bytes(int64_t cols, int32_t n_slots) {
@@ -484,9 +630,9 @@ extern "C" int smx_stats_colsum(const void *x, int dtype, int64_t rows, int64_t 
   float *partial = static_cast<float *>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
   // rows == 0 still launches: every chunk is empty, its partial zero.
-  const StatsArgs a{x, rows, cols, rows ? row_stride : cols, 0, slots_sq, partial, nullptr, 0};
-  dispatch_dtype<kSqColsum, 0>(a, dtype, n_slots, st);
-  rc = check_launch("stats_colsum");
+  const StatsInput in{x, dtype, rows, cols, rows ? row_stride : cols, slots_sq, partial, n_slots,
+                      kSqColsum, 0, nullptr, 0};
+  rc = stats_launch(&in, 1, st, "stats_colsum");
   if (rc) return rc;
   hipLaunchKernelGGL(colsum_fold_kernel, dim3(static_cast<unsigned>(ceil_div(cols, 64))), dim3(256), 0, st,
                      partial, cols, n_slots, colsum);

@@ -105,6 +105,7 @@ class _FusedLinear(torch.autograd.Function):
                 x_lp = torch.empty(rows.shape, dtype=lp, device=x.device)
                 if site.capture_a:
                     sq, fs = opt._a_slots(p, rows.shape[1], rows.device, state)
+                    opt._stats_barrier(sq)
                     _native.stats_cast(rows, sq, fs, x_lp)
                     state["a_count"] += rows.shape[0]
                 else:
@@ -138,10 +139,11 @@ class _FusedLinear(torch.autograd.Function):
         grad_b = None
         if ctx.b_dtype is not None and ctx.needs_input_grad[2]:
             colsum = torch.empty(g.shape[1], dtype=torch.float32, device=g.device)
+            opt._stats_barrier(sq)
             _native.stats_colsum(g, sq, colsum, site.colsum_workspace(g.shape[1], g.device))
             grad_b = colsum if ctx.b_dtype == torch.float32 else colsum.to(ctx.b_dtype)
         else:
-            _native.stats_accumulate(g, sq, None)
+            opt._enqueue_stats(g, sq, None)
         state["b_count"] += g.shape[0]
         g2 = grad_y.reshape(-1, grad_y.shape[-1])
         grad_x = grad_w = None

@@ -9,9 +9,16 @@ close().  The module-level helpers imported by the reference tests
 (_s8_fp32, diagonal_inverse_sqrt, _graft_direction, rank1_inverse_sqrt,
 rank1_mapback, rank1_whiten) are GPU-backed here as well.
 
-Added keyword (default keeps the production recipe): ``s8_mode`` selects the
-arithmetic of the S8 products, "comp_bf16" (compensated BF16 MFMA, FP32
-intermediates) or "fp32" (FP32 MFMA).
+Added keywords (defaults keep the production recipe and the reference's
+results):
+* ``s8_mode`` selects the arithmetic of the S8 products, "comp_bf16"
+  (compensated BF16 MFMA, FP32 intermediates) or "fp32" (FP32 MFMA);
+* ``hook_batch_bytes``: the hooks queue their inputs and take the
+  statistics of the queue in one launch once it holds this many bytes (and
+  at step(), state_dict() and close()); 0 launches in every hook call.  The
+  statistics are bit-identical either way.  A queued input must not be
+  modified in place before its launch: the launch checks the tensor's
+  version counter and raises RuntimeError if it moved.
 """
 from __future__ import annotations
 
@@ -179,6 +186,33 @@ def _rows2d(t: torch.Tensor) -> torch.Tensor:
     return rows
 
 
+class _StatsQueue:
+    """Hook inputs whose statistics are still to be taken, in hook order.
+
+    Every entry adds into its own slot rows (an entry whose slot rows are
+    already queued flushes the queue first), so one launch over the whole
+    queue adds exactly what one launch per hook call would, in the same
+    order per slot row.  The queue keeps its tensors alive until the launch
+    is enqueued on the stream current at the first hook call.
+    """
+
+    __slots__ = ("limit", "entries", "slot_ptrs", "nbytes", "stream", "device")
+
+    def __init__(self, limit: int):
+        self.limit = int(limit)
+        self.entries: List[Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor], int]] = []
+        self.slot_ptrs = set()
+        self.nbytes = 0
+        self.stream = None
+        self.device = None
+
+    def clear(self) -> None:
+        self.entries = []
+        self.slot_ptrs = set()
+        self.nbytes = 0
+        self.stream = self.device = None
+
+
 # ------------------------------------------------------------- optimizer ---
 class DiagonalWeightedPE(Optimizer):
     """S8 directions weighted by activation and output-cotangent diagonals.
@@ -192,10 +226,14 @@ class DiagonalWeightedPE(Optimizer):
     # Slot rows per statistics vector: each hook launch spreads its rows over
     # this many row chunks, each chunk owning one slot row.
     STAT_SLOTS = 128
+    # Queued hook bytes that trigger a statistics launch.  One launch per
+    # hook call pays a fixed start/drain cost that is large against the
+    # 25-100 MB of one call; a launch over 256 MB runs near the streaming rate.
+    HOOK_BATCH_BYTES = 256 << 20
 
     def __init__(self, model: nn.Module, lr: float, *, rank_one_a: bool = False,
                  module_filter: Optional[Callable[[str, nn.Module], bool]] = None,
-                 s8_mode: str = "comp_bf16"):
+                 s8_mode: str = "comp_bf16", hook_batch_bytes: Optional[int] = None):
         matrices, modules = select_matrices(model, module_filter)
         if s8_mode not in _native.S8_MODES:
             raise ValueError(f"s8_mode must be one of {sorted(_native.S8_MODES)}")
@@ -229,6 +267,10 @@ class DiagonalWeightedPE(Optimizer):
         # Pending per-chunk partial sums of the hooks, folded into a_sum /
         # b_sum by step() (or before state_dict()).  Not optimizer state.
         self._slots: Dict[Tuple[int, str], Tuple[nn.Parameter, torch.Tensor, Optional[torch.Tensor]]] = {}
+        limit = self.HOOK_BATCH_BYTES if hook_batch_bytes is None else int(hook_batch_bytes)
+        if limit < 0:
+            raise ValueError("hook_batch_bytes must be >= 0")
+        self._queue = _StatsQueue(limit)
         self._workspace: Optional[torch.Tensor] = None
         self.register_state_dict_pre_hook(DiagonalWeightedPE._flush_slots)
         self.register_load_state_dict_post_hook(DiagonalWeightedPE._drop_slots)
@@ -277,7 +319,7 @@ class DiagonalWeightedPE(Optimizer):
         state = self.state[parameter] if state is None else state
         rows = _rows2d(x)
         sq, fs = self._a_slots(parameter, rows.shape[-1], rows.device, state)
-        _native.stats_accumulate(rows, sq, fs)
+        self._enqueue_stats(rows, sq, fs)
         state["a_count"] += rows.shape[0]
 
     def _accumulate_b(self, parameter, delta: torch.Tensor, state: Optional[dict] = None) -> None:
@@ -285,8 +327,54 @@ class DiagonalWeightedPE(Optimizer):
         state = self.state[parameter] if state is None else state
         rows = _rows2d(delta)
         sq = self._b_slots(parameter, rows.shape[-1], rows.device, state)
-        _native.stats_accumulate(rows, sq, None)
+        self._enqueue_stats(rows, sq, None)
         state["b_count"] += rows.shape[0]
+
+    def _enqueue_stats(self, rows: torch.Tensor, sq: torch.Tensor, fs: Optional[torch.Tensor]) -> None:
+        """Queues one hook input (or launches at once when batching is off)."""
+        q = self._queue
+        if q.limit == 0:
+            _native.stats_accumulate(rows, sq, fs)
+            return
+        if rows.shape[0] == 0:
+            return  # an empty microbatch adds nothing
+        stream = _native.stream_of(rows.device)
+        if q.entries and (stream != q.stream or rows.device != q.device or sq.data_ptr() in q.slot_ptrs):
+            self._flush_stats()
+        if not q.entries:
+            q.stream, q.device = stream, rows.device
+        q.entries.append((rows, sq, fs, rows._version))
+        q.slot_ptrs.add(sq.data_ptr())
+        q.nbytes += rows.numel() * rows.element_size()
+        if q.nbytes >= q.limit:
+            self._flush_stats()
+
+    def _stats_barrier(self, sq: torch.Tensor) -> None:
+        """Launches the queue if it adds into `sq`, so that an immediate launch
+        into the same slot rows comes after it."""
+        if sq.data_ptr() in self._queue.slot_ptrs:
+            self._flush_stats()
+
+    def _flush_stats(self) -> None:
+        """Takes the statistics of every queued hook input in one launch, on
+        the stream of the queued hook calls (the current stream waits for it
+        when it is another one)."""
+        q = self._queue
+        if not q.entries:
+            return
+        entries, stream, device = q.entries, q.stream, q.device
+        q.clear()
+        for rows, _, _, version in entries:
+            if rows._version != version:
+                raise RuntimeError(
+                    "a hook input was modified in place before its statistics were taken; construct the "
+                    "optimizer with hook_batch_bytes=0 to take them inside the hook")
+        _native.stats_accumulate_batch([(rows, sq, fs) for rows, sq, fs, _ in entries], stream)
+        current = _native.stream_of(device)
+        if current != stream:
+            done = torch.cuda.Event()
+            done.record(torch.cuda.ExternalStream(stream, device=device))
+            torch.cuda.ExternalStream(current, device=device).wait_event(done)
 
     def _capture(self, parameter, *, capture_a):
         def hook(module, inputs, output):
@@ -306,6 +394,7 @@ class DiagonalWeightedPE(Optimizer):
     @staticmethod
     def _flush_slots(self) -> None:
         """Folds pending hook partials into a_sum / b_sum (before state_dict())."""
+        self._flush_stats()
         for (pid, side), (parameter, sq, fs) in self._slots.items():
             state = self.state.get(parameter, {})
             total = state.get(f"{side}_sum")
@@ -317,6 +406,7 @@ class DiagonalWeightedPE(Optimizer):
     @staticmethod
     def _drop_slots(self) -> None:
         """Loaded sums are authoritative: pending partials are discarded."""
+        self._queue.clear()
         self._slots.clear()
 
     # ------------------------------------------------------------- step ---
@@ -368,6 +458,7 @@ class DiagonalWeightedPE(Optimizer):
     @torch.no_grad()
     def step(self, closure=None):
         loss = self._run_closure(closure)
+        self._flush_stats()
         matrix_items, auxiliary_items = [], []
         a_counts: Dict[int, int] = {}
         for group in self.param_groups:
@@ -481,6 +572,7 @@ class DiagonalWeightedPE(Optimizer):
             _native.adamw(descs, offset, lr, b1, b2, group["adamw_eps"], group["weight_decay"], device)
 
     def close(self):
+        self._flush_stats()
         if self._fused is not None:
             self._fused.close()
         for handle in self.handles:
@@ -494,5 +586,6 @@ class RankOneAWeightedPE(DiagonalWeightedPE):
 
     def __init__(self, model: nn.Module, lr: float, *,
                  module_filter: Optional[Callable[[str, nn.Module], bool]] = None,
-                 s8_mode: str = "comp_bf16"):
-        super().__init__(model, lr, rank_one_a=True, module_filter=module_filter, s8_mode=s8_mode)
+                 s8_mode: str = "comp_bf16", hook_batch_bytes: Optional[int] = None):
+        super().__init__(model, lr, rank_one_a=True, module_filter=module_filter, s8_mode=s8_mode,
+                         hook_batch_bytes=hook_batch_bytes)

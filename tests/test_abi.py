@@ -45,6 +45,7 @@ def test_struct_layouts_match_header(tmp_path):
     src = tmp_path / "layout.c"
     fields = {
         "smx_finish_desc": _native.FinishDesc,
+        "smx_stats_desc": _native.StatsDesc,
         "smx_adamw_desc": _native.AdamwDesc,
         "smx_matrix_desc": _native.MatrixDesc,
     }
@@ -72,6 +73,18 @@ def test_validation_errors_return_before_gpu_work():
     assert b"dtype" in lib.smx_last_error()
     # empty input is a no-op even with null pointers
     assert lib.smx_stats_accumulate(None, 0, 0, 4, 4, None, None, 1, None) == 0
+    # batched statistics: two descriptors adding into overlapping slot rows
+    # are rejected before any launch, and an empty table is a no-op
+    S = _native.StatsDesc
+    d0 = S(x=16, slots_sq=4096, slots_first=None, rows=4, cols=8, row_stride=8, dtype=0, n_slots=2)
+    d1 = S(x=16, slots_sq=4096 + 32, slots_first=None, rows=4, cols=8, row_stride=8, dtype=1, n_slots=2)
+    assert lib.smx_stats_accumulate_batch((S * 2)(d0, d1), 2, None) == -1
+    assert b"overlap" in lib.smx_last_error()
+    d1.slots_sq, d1.slots_first = 1 << 20, 4096 + 60  # first-moment rows overlapping d0's sums
+    assert lib.smx_stats_accumulate_batch((S * 2)(d0, d1), 2, None) == -1
+    d1.dtype = 7
+    assert lib.smx_stats_accumulate_batch((S * 2)(d0, d1), 2, None) == -3
+    assert lib.smx_stats_accumulate_batch(None, 0, None) == 0
     # matrix step: workspace too small
     d = _native.MatrixDesc(param=16, grad=16, momentum=16, inv_row=16, inv_col=16, rows=64, cols=32,
                            lr=1e-3, momentum_beta=.8, grad_dtype=0)
