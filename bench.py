@@ -19,6 +19,7 @@ Prints one JSON line (driver contract) with `roofline` (dominant kernel) and
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -192,6 +193,16 @@ def cpu_model_name():
     return "unknown"
 
 
+def quiet_gc():
+    """Collect once and freeze the surviving objects before a timed region,
+    as long training loops do: a full collection of the ~270K objects torch
+    and the harness hold takes ~70 ms of host time, and when one falls inside
+    the timed steps the GPU idles behind it.  Objects created later are
+    still collected."""
+    gc.collect()
+    gc.freeze()
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -235,6 +246,7 @@ def train_bench(args, device):
             once()
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
         torch.cuda.synchronize()
+        quiet_gc()
         for k in range(args.steps):
             once(evs[k])
         torch.cuda.synchronize()
@@ -308,6 +320,7 @@ def main():
     for _ in range(args.warmup):
         one_step()
     torch.cuda.synchronize()
+    quiet_gc()
     log("warmup done")
     # Timed region: K steps between two events; inside it, event pairs around
     # the hook phase and step() of every step, and the library records an

@@ -230,23 +230,37 @@ __device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int6
   }
 }
 
-// Element forms of a job: the vector forms load 16 bytes per lane (32-lane
-// column tiles), the scalar forms one element (64-lane tiles) for inputs
-// whose width, row stride or address is not 16-byte aligned.
+// Element forms of a job: the vector forms load 16 bytes per lane, the
+// scalar forms one element (64-lane tiles) for inputs whose width, row
+// stride or address is not 16-byte aligned.
 enum StatsForm : int { kF32V4 = 0, kBf16V8, kF16V8, kF32V1, kBf16V1, kF16V1, kNumForms };
 __host__ __device__ constexpr int stats_code(int form, int mode, int cast) { return (form * 3 + mode) * 3 + cast; }
 
+// CT: lanes across a column tile (32 for the vector forms: 128 f32 or 256
+// 16-bit channels; 16 lanes measured 2% slower on the cfg4 hook inputs).
+// U: loads per lane per register batch
+// (the f16 form widens its batch early, so it keeps two loads per batch to
+// stay within the register budget the other forms set).
 template <int FORM>
 struct FormTraits;
-// U: loads per lane per register batch (the f16 form widens its batch
-// early, so it keeps two loads per batch to stay within the register
-// budget the other forms set).
 template <> struct FormTraits<kF32V4> { static constexpr int DT = SMX_F32, VEC = 4, CT = 32, U = 4; };
 template <> struct FormTraits<kBf16V8> { static constexpr int DT = SMX_BF16, VEC = 8, CT = 32, U = 4; };
 template <> struct FormTraits<kF16V8> { static constexpr int DT = SMX_F16, VEC = 8, CT = 32, U = 2; };
 template <> struct FormTraits<kF32V1> { static constexpr int DT = SMX_F32, VEC = 1, CT = 64, U = 4; };
 template <> struct FormTraits<kBf16V1> { static constexpr int DT = SMX_BF16, VEC = 1, CT = 64, U = 4; };
 template <> struct FormTraits<kF16V1> { static constexpr int DT = SMX_F16, VEC = 1, CT = 64, U = 4; };
+
+template <int FORM>
+constexpr int64_t tile_channels() { return FormTraits<FORM>::VEC * FormTraits<FORM>::CT; }
+constexpr int64_t kTileChannels[kNumForms] = {tile_channels<kF32V4>(),  tile_channels<kBf16V8>(),
+                                              tile_channels<kF16V8>(),  tile_channels<kF32V1>(),
+                                              tile_channels<kBf16V1>(), tile_channels<kF16V1>()};
+
+// Row chunks hold at least this many rows (fewer slot rows are then used):
+// a block then streams 256 KB, so its start and its reduction weigh less
+// (measured against 128 and 256 rows on the cfg4 hook inputs).  The chunking depends on the job alone, so a job adds the same
+// bits whether it is launched alone or with others.
+constexpr int64_t kStatsMinChunkRows = 512;
 
 template <int FORM, int MODE, int CAST>
 __device__ __forceinline__ void run_tile(const StatsJob &J, int64_t tile, int64_t chunk, float *red) {
@@ -257,9 +271,13 @@ __device__ __forceinline__ void run_tile(const StatsJob &J, int64_t tile, int64_
 // grid.x = sum over the jobs of tiles * n_chunks; block = kStatsThreads.
 __global__ void __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(6))) stats_accumulate_kernel(StatsPack pack) {
   __shared__ float red[2 * kStatsWaves * kStatsMaxTW];
+  // The job of this block: block_begin grows with the job index, so the
+  // index is the count of later jobs that begin at or before the block
+  // (unrolled, so the scalar loads of every begin are issued together).
   const int b = static_cast<int>(blockIdx.x);
   int j = 0;
-  while (j + 1 < pack.n && b >= pack.job[j + 1].block_begin) ++j;
+#pragma unroll
+  for (int i = 1; i < kStatsJobs; ++i) j += (i < pack.n && b >= pack.job[i].block_begin) ? 1 : 0;
   const StatsJob &J = pack.job[j];
   const int64_t local = b - J.block_begin;
   const int64_t tile = local % J.tiles, chunk = local / J.tiles;
@@ -328,10 +346,12 @@ static int stats_launch(const StatsInput *in, int n, hipStream_t st, const char 
   for (int i = 0; i < n; ++i) {
     const StatsInput &s = in[i];
     const int form = stats_form(s);
-    const int vec = form == kF32V4 ? 4 : (form == kBf16V8 || form == kF16V8) ? 8 : 1;
-    const int ct = vec == 1 ? 64 : 32;
-    const int64_t tiles = ceil_div(ceil_div(s.cols, vec), ct);
-    const int64_t nb = tiles * s.n_slots;
+    const int64_t tiles = ceil_div(s.cols, kTileChannels[form]);
+    const int64_t rows_per_chunk = std::max<int64_t>(ceil_div(s.rows, s.n_slots), kStatsMinChunkRows);
+    // Chunks that hold rows; colsum writes a zero partial into every slot
+    // row, so it keeps one block per slot row.
+    const int64_t chunks = s.mode == kSqColsum ? s.n_slots : std::max<int64_t>(ceil_div(s.rows, rows_per_chunk), 1);
+    const int64_t nb = tiles * chunks;
     if (pack.n == kStatsJobs || blocks + nb > INT32_MAX) {
       int rc = flush();
       if (rc) return rc;
@@ -345,7 +365,7 @@ static int stats_launch(const StatsInput *in, int n, hipStream_t st, const char 
     J.cols = s.cols;
     J.row_stride = s.row_stride;
     J.out_stride = s.out_stride;
-    J.rows_per_chunk = ceil_div(s.rows, s.n_slots);
+    J.rows_per_chunk = rows_per_chunk;
     J.block_begin = static_cast<int32_t>(blocks);
     J.tiles = static_cast<int32_t>(tiles);
     J.code = stats_code(form, s.mode, s.cast);

@@ -228,8 +228,8 @@ class DiagonalWeightedPE(Optimizer):
     STAT_SLOTS = 128
     # Queued hook bytes that trigger a statistics launch.  One launch per
     # hook call pays a fixed start/drain cost that is large against the
-    # 25-100 MB of one call; a launch over 256 MB runs near the streaming rate.
-    HOOK_BATCH_BYTES = 256 << 20
+    # 25-100 MB of one call; launches over 1 GB run near the streaming rate.
+    HOOK_BATCH_BYTES = 1 << 30
 
     def __init__(self, model: nn.Module, lr: float, *, rank_one_a: bool = False,
                  module_filter: Optional[Callable[[str, nn.Module], bool]] = None,
