@@ -8,7 +8,8 @@
 
 namespace smx {
 
-constexpr int kTile = 256;        // GEMM macro tile (M and N) and padding
+constexpr int kTile = 256;        // apply tile rows and buffer padding
+constexpr int kSymTile = 128;     // Gram / square output tile edge
 constexpr int kMaxClasses = 8;    // shape classes per GEMM launch
 constexpr int kRowsPerPart = 16;  // param rows per whiten block of a transposed parameter (one K group)
 constexpr int kPartRows = 4;      // param rows per whiten / mapback partial
@@ -31,7 +32,7 @@ struct S8Class {
   int32_t tiles_m;     // rp / kTile
   int32_t tiles_n;     // cp / kTile
   int32_t parts;       // partial slots per matrix: ceil(cp / kPartRows)
-  int32_t pad_;
+  int32_t tiles_s;     // rp / kSymTile
   // Iterate buffers (4 bytes per element), oriented layout only.  In
   // SMX_S8_FP32 mode they hold FP32; in SMX_S8_COMP_BF16 mode interleaved
   // BF16 hi/lo (put_operand), except the stage-5 result, which is FP32.
@@ -43,7 +44,7 @@ struct S8Class {
   float *u;            // [count][cp] per param-row rank-one coefficient
   double *fro;         // [count][parts] whiten: partial sum of V^2
   double *mb;          // [count][parts] mapback: partial sum of U^2
-  double *sch;         // [count][tiles_m*(tiles_m+1)] Schatten partials (two per upper block)
+  double *sch;         // [count][sym_tiles(tiles_s)] Schatten partials (one per upper-triangle Gram tile)
   double *cst;         // [count][2] matrix-step constants: sum z^2, sum (a z)^2
 };
 
@@ -72,7 +73,7 @@ struct S8Mat {
   __host__ __device__ float *u() const { return kp()->u + slot * kp()->cp; }
   __host__ __device__ double *fro() const { return kp()->fro + static_cast<int64_t>(slot) * kp()->parts; }
   __host__ __device__ double *mb() const { return kp()->mb + static_cast<int64_t>(slot) * kp()->parts; }
-  __host__ __device__ double *sch() const { return kp()->sch + slot * 2 * sym_tiles(kp()->tiles_m); }
+  __host__ __device__ double *sch() const { return kp()->sch + slot * sym_tiles(kp()->tiles_s); }
   __host__ __device__ double *cst() const { return kp()->cst + 2 * static_cast<int64_t>(slot); }
   // Parameter layout: rows x cols (the transpose of the oriented layout
   // for transposed parameters).

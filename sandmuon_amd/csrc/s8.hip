@@ -48,21 +48,39 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;      // 4 waves, one per SIMD; two blocks per CU
+enum Phase { kGram = 0, kSquare = 1, kApply = 2, kPoly1 = 3, kSpan = 4 };  // kSpan: timing record of a whole S8 run
+
+constexpr int kThreads = 256;      // 4 waves, one per SIMD
 constexpr int kWaves = kThreads / 64;
-constexpr int kTileM = kTile, kTileN = kTile / 2;  // block output tile 256 x 128
-constexpr int kSubM = 4, kSubN = 2; // 32x32 MFMA tiles per wave (128 x 64; waves 2 x 2)
+constexpr int kTileN = 128;         // block output tile columns
+constexpr int kSubN = 2;            // 32x32 MFMA column tiles per wave (waves 2 x 2)
 constexpr int kBK = 16;             // K per pipeline stage
-constexpr int kOpA = kTileM * kBK * 4;  // A operand tile 256 x 16 (4 bytes per element)
-constexpr int kOpB = kTileN * kBK * 4;  // B operand tile 128 x 16
+constexpr int kOpB = kTileN * kBK * 4;  // B operand tile 128 x 16 (4 bytes per element)
 constexpr int kStages = 3;          // LDS ring depth (2 stages in flight)
-constexpr int kStageBytes = kOpA + kOpB;
-constexpr int kRingBytes = kStages * kStageBytes;
-constexpr int kLoadsA = kOpA / 1024 / kWaves, kLoadsB = kOpB / 1024 / kWaves;  // 1 KB loads per wave
-constexpr int kLoadsPerStage = kLoadsA + kLoadsB;
+constexpr int kLoadsB = kOpB / 1024 / kWaves;  // 1 KB loads per wave
 constexpr int kKmRow = kTileN * 4;  // bytes per K row of the K-major B tile
 
-enum Phase { kGram = 0, kSquare = 1, kApply = 2, kPoly1 = 3, kSpan = 4 };  // kSpan: timing record of a whole S8 run
+// Block tile geometry, by output rows TM: 256 x 128 (each wave 128 x 64,
+// two blocks per CU) or 128 x 128 (each wave 64 x 64, three blocks per CU).
+// The Gram and the apply use 256 x 128 tiles.  The square uses 128 x 128
+// tiles when they take fewer rounds of the CUs' block slots, allowing for
+// their lower rate (square_small): the smaller tile moves a third more
+// operand bytes per MFMA, and a round of it takes 0.9 of a round of the
+// larger one.  At 768 x 768 the square's 12 half-tiles per matrix need two
+// rounds of 512 slots, its 21 small tiles 1.5 rounds of 768 (cfg4: 104
+// against 117 us per launch); at 2048 x 2048 the larger tile wins.
+// (128 x 128 Gram tiles measured no faster at 768 x 3072.)
+template <int TM>
+struct Geo {
+  static constexpr int kTileM = TM;
+  static constexpr int kSubM = TM / 64;           // 32x32 MFMA row tiles per wave
+  static constexpr int kOpA = TM * kBK * 4;       // A operand tile TM x 16
+  static constexpr int kStageBytes = kOpA + kOpB;
+  static constexpr int kRingBytes = kStages * kStageBytes;
+  static constexpr int kLoadsA = kOpA / 1024 / kWaves;
+  static constexpr int kLoadsPerStage = kLoadsA + kLoadsB;
+  static constexpr int kWavesPerEU = TM == 256 ? 2 : 3;
+};
 
 struct StageArgs {
   S8Layout L;
@@ -70,6 +88,7 @@ struct StageArgs {
   int32_t seg_cls[kMaxClasses];
   int32_t n_seg;
   int32_t stage;  // 1..5
+  int32_t sq_small;  // this run's square uses 128 x 128 tiles (else 256 x 128)
   float a, b, c;
   float b_over_c;
 };
@@ -159,7 +178,9 @@ __device__ __forceinline__ void dma_tile(const TileOffsets<N> &t, const char *sb
 template <int N>
 __device__ __forceinline__ void wait_vm() {
   if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
   else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
   else if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
   else static_assert(N == 0, "unsupported vmcnt");
 }
@@ -232,11 +253,11 @@ struct BFrags<SMX_S8_FP32> {
 // LDS -> registers: A row block i, and the four B column blocks, of one
 // stage.  Lane (r, h) takes K = 8h .. 8h+7 of its row: chunks h (hi) and
 // 2 + h (lo) of the interleaved form, chunks 2h and 2h + 1 of FP32.
-template <int MODE>
+template <int MODE, int TM>
 __device__ __forceinline__ void load_a(const char *st, int wm, int i, AFrag<MODE> &f) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
-  const int r = wm * (32 * kSubM) + i * 32 + lr;
+  const int r = wm * (32 * Geo<TM>::kSubM) + i * 32 + lr;
   if constexpr (MODE == SMX_S8_COMP_BF16) {
     f.h = read_b16(st, r, lh);
     f.l = read_b16(st, r, 2 + lh);
@@ -245,11 +266,11 @@ __device__ __forceinline__ void load_a(const char *st, int wm, int i, AFrag<MODE
   }
 }
 
-template <int MODE>
+template <int MODE, int TM>
 __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
-  const char *bt = st + kOpA;
+  const char *bt = st + Geo<TM>::kOpA;
 #pragma unroll
   for (int j = 0; j < kSubN; ++j) {
     const int r = wn * (32 * kSubN) + j * 32 + lr;
@@ -291,8 +312,9 @@ __device__ __forceinline__ BkmLane bkm_lane() {
   return L;
 }
 
-template <int MODE>
+template <int MODE, int TM>
 __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &f, const BkmLane &L) {
+  constexpr int kOpA = Geo<TM>::kOpA;
   const int lane = threadIdx.x & 63;
   const char *bt = st + kOpA;
   if constexpr (MODE == SMX_S8_COMP_BF16) {
@@ -333,10 +355,10 @@ __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &
   }
 }
 
-template <int MODE, bool BKM>
+template <int MODE, int TM, bool BKM>
 __device__ __forceinline__ void load_b_any(const char *st, int wn, BFrags<MODE> &f, const BkmLane &L) {
-  if constexpr (BKM) load_b_km<MODE>(st, wn, f, L);
-  else load_b<MODE>(st, wn, f);
+  if constexpr (BKM) load_b_km<MODE, TM>(st, wn, f, L);
+  else load_b<MODE, TM>(st, wn, f);
 }
 
 // MFMAs of row block i: acc[i][j] += A_i B_j^T over the stage's 16 K.
@@ -393,13 +415,14 @@ __device__ __forceinline__ AFrag<MODE> one_hot(float s, int r0) {
 // wave's B chunks start kOpA bytes later, less the difference of the
 // wave's A and B shares.  BKM: B is K-major (its stage is 16 rows further
 // down).
+template <int TM>
 struct WaveOffsets {
-  TileOffsets<kLoadsA> a;
+  TileOffsets<Geo<TM>::kLoadsA> a;
   TileOffsets<kLoadsB> b;
   uint32_t b_lds;  // LDS byte offset of the wave's B chunks from its A chunks
 };
-template <bool BKM>
-__device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const WaveOffsets &o, int64_t k0,
+template <int TM, bool BKM>
+__device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const WaveOffsets<TM> &o, int64_t k0,
                                             uint32_t lds) {
   dma_tile(o.a, static_cast<const char *>(A.p) + 4 * k0, lds);
   dma_tile(o.b, static_cast<const char *>(B.p) + 4 * k0 * (BKM ? B.ld : 1), lds + o.b_lds);
@@ -407,8 +430,9 @@ __device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const 
 
 // Waits until at most `pending` stages of this wave's loads are in flight
 // (loads complete in issue order).
+template <int TM>
 __device__ __forceinline__ void wait_stages(int pending) {
-  constexpr int L = kLoadsPerStage;
+  constexpr int L = Geo<TM>::kLoadsPerStage;
   static_assert(kStages == 3, "at most two stages in flight");
   if (pending >= 2) wait_vm<2 * L>();
   else if (pending == 1) wait_vm<L>();
@@ -439,32 +463,33 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 // (rows 16 SEL .. 16 SEL + 15 of the wave, accumulator block SEL / 2).
 // STEADY: kt + kStages < nk, so a next stage exists, the refill is due and
 // kStages - 2 stages may stay in flight (no run-time conditions).
-template <int MODE, int SEL, int PAR, bool STEADY, bool BKM>
-__device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const WaveOffsets &o, const BkmLane &bl,
+template <int MODE, int TM, int SEL, int PAR, bool STEADY, bool BKM>
+__device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const WaveOffsets<TM> &o, const BkmLane &bl,
                                           uint32_t lds0, float sel_s, char *smem, int kt, int nk, int wm, int wn,
-                                          AFrag<MODE> (&af)[kSubM], BFrags<MODE> (&bf)[2],
-                                          f32x16 (&acc)[kSubM][kSubN]) {
+                                          AFrag<MODE> (&af)[Geo<TM>::kSubM], BFrags<MODE> (&bf)[2],
+                                          f32x16 (&acc)[Geo<TM>::kSubM][kSubN]) {
+  using G = Geo<TM>;
   constexpr int S = kStages;
   const bool more = STEADY || kt + 1 < nk;
   if constexpr (STEADY) {
-    wait_vm<(S - 2) * kLoadsPerStage>();
+    wait_vm<(S - 2) * G::kLoadsPerStage>();
   } else {
-    if (more) wait_stages(min(S - 2, nk - 2 - kt));
+    if (more) wait_stages<TM>(min(S - 2, nk - 2 - kt));
   }
   wait_lds();
   block_barrier();
   if (STEADY || kt + S < nk)
-    issue_stage<BKM>(A, B, o, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * kStageBytes);
-  const char *nxt = smem + ((kt + 1) % S) * kStageBytes;
-  if (more) load_b_any<MODE, BKM>(nxt, wn, bf[PAR ^ 1], bl);
+    issue_stage<TM, BKM>(A, B, o, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * G::kStageBytes);
+  const char *nxt = smem + ((kt + 1) % S) * G::kStageBytes;
+  if (more) load_b_any<MODE, TM, BKM>(nxt, wn, bf[PAR ^ 1], bl);
   // Raised wave priority while this wave issues its MFMAs, so the
   // arbiter favours it over the other block's wave on the SIMD that is
   // issuing LDS reads and loads (Gram launches 5% faster).
   __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-  for (int i = 0; i < kSubM; ++i) {
+  for (int i = 0; i < G::kSubM; ++i) {
     mma_row<MODE>(af[i], bf[PAR], acc[i]);
-    if (more) load_a<MODE>(nxt, wm, i, af[i]);
+    if (more) load_a<MODE, TM>(nxt, wm, i, af[i]);
   }
   if constexpr (SEL >= 0) mma_row<MODE>(one_hot<MODE>(sel_s, (SEL & 1) * 16), bf[PAR], acc[SEL >> 1]);
   __builtin_amdgcn_s_setprio(0);
@@ -473,10 +498,12 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Wa
 // ACCG: also accumulate sel_s * G over the wave's rows (square phase; A and
 // B are the same symmetric G, K = rows of G).  BKM: B is a K-major
 // row-major operand (C = A B, apply), brow0 its first column.
-template <int MODE, bool ACCG, bool BKM>
+template <int MODE, int TM, bool ACCG, bool BKM>
 __device__ __forceinline__ void gemm_tile(const Opnd &A, const Opnd &B, int64_t K, int64_t arow0, int64_t brow0,
-                                          float sel_s, char *smem, f32x16 (&acc)[kSubM][kSubN]) {
-  static_assert(kSubM == 4 && kBK == 16, "the one_hot window is 8 stages of 16 rows");
+                                          float sel_s, char *smem, f32x16 (&acc)[Geo<TM>::kSubM][kSubN]) {
+  using G = Geo<TM>;
+  constexpr int kSubM = G::kSubM;
+  static_assert((kSubM == 4 || kSubM == 2) && kBK == 16, "the one_hot window is 2 kSubM stages of 16 rows");
   static_assert((8 * kSubN) % 16 == 0, "the wave's K-major column offset must be whole chunk groups");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves, each 128 x 64
@@ -487,25 +514,25 @@ __device__ __forceinline__ void gemm_tile(const Opnd &A, const Opnd &B, int64_t 
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
   const int nk = static_cast<int>(K / kBK);
-  WaveOffsets o;
-  o.a = tile_offsets<kLoadsA>(A.ld, arow0, wave);
+  WaveOffsets<TM> o;
+  o.a = tile_offsets<G::kLoadsA>(A.ld, arow0, wave);
   o.b = BKM ? tile_offsets_km<kLoadsB>(B.ld, brow0, wave) : tile_offsets<kLoadsB>(B.ld, brow0, wave);
-  o.b_lds = static_cast<uint32_t>(kOpA + wave * (kLoadsB - kLoadsA) * 1024);
+  o.b_lds = static_cast<uint32_t>(G::kOpA + wave * (kLoadsB - G::kLoadsA) * 1024);
   const BkmLane bl = bkm_lane();  // used by the K-major B path only
   // LDS byte address of the ring plus this wave's first A chunk.
-  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * kLoadsA * 1024;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * G::kLoadsA * 1024;
 #pragma unroll
   for (int s = 0; s < kStages; ++s)
-    if (s < nk) issue_stage<BKM>(A, B, o, static_cast<int64_t>(s) * kBK, lds0 + s * kStageBytes);
-  wait_stages(min(kStages - 1, nk - 1));
+    if (s < nk) issue_stage<TM, BKM>(A, B, o, static_cast<int64_t>(s) * kBK, lds0 + s * G::kStageBytes);
+  wait_stages<TM>(min(kStages - 1, nk - 1));
   block_barrier();
   AFrag<MODE> af[kSubM];
   BFrags<MODE> bf[2];
-  load_b_any<MODE, BKM>(smem, wn, bf[0], bl);
+  load_b_any<MODE, TM, BKM>(smem, wn, bf[0], bl);
 #pragma unroll
-  for (int i = 0; i < kSubM; ++i) load_a<MODE>(smem, wm, i, af[i]);
+  for (int i = 0; i < kSubM; ++i) load_a<MODE, TM>(smem, wm, i, af[i]);
 #define SMX_PIPE(SEL, PAR, KT, STEADY) \
-  pipe_iter<MODE, SEL, PAR, STEADY, BKM>(A, B, o, bl, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
+  pipe_iter<MODE, TM, SEL, PAR, STEADY, BKM>(A, B, o, bl, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
   // Stages [kt, to) in pairs (kt and `to` even): branch-free while a refill
   // is due, then the general form.
   const int steady_end = nk - kStages;
@@ -521,19 +548,22 @@ __device__ __forceinline__ void gemm_tile(const Opnd &A, const Opnd &B, int64_t 
   };
   int kt = 0;
   if constexpr (ACCG) {
-    // The wave's rows are K stages kt0 .. kt0 + 7 (kt0 = first row / 16, a
-    // multiple of 8, so the stage parity matches the unrolled pairs).
+    // The wave's rows are K stages kt0 .. kt0 + 2 kSubM - 1 (kt0 = first
+    // row / 16, a multiple of 4, so the stage parity matches the unrolled
+    // pairs).
     const int kt0 = static_cast<int>((arow0 + wm * (32 * kSubM)) / kBK);
     run(kt, kt0);
     SMX_PIPE(0, 0, kt0, false);
     SMX_PIPE(1, 1, kt0 + 1, false);
     SMX_PIPE(2, 0, kt0 + 2, false);
     SMX_PIPE(3, 1, kt0 + 3, false);
-    SMX_PIPE(4, 0, kt0 + 4, false);
-    SMX_PIPE(5, 1, kt0 + 5, false);
-    SMX_PIPE(6, 0, kt0 + 6, false);
-    SMX_PIPE(7, 1, kt0 + 7, false);
-    kt = kt0 + 8;
+    if constexpr (kSubM == 4) {
+      SMX_PIPE(4, 0, kt0 + 4, false);
+      SMX_PIPE(5, 1, kt0 + 5, false);
+      SMX_PIPE(6, 0, kt0 + 6, false);
+      SMX_PIPE(7, 1, kt0 + 7, false);
+    }
+    kt = kt0 + 2 * kSubM;
   }
   run(kt, nk);
 #undef SMX_PIPE
@@ -567,10 +597,14 @@ struct Stage1Scalars {
   float s;
   bool ok;
 };
-__device__ Stage1Scalars stage1_scalars(const S8Mat &M, double *bcast) {
+__host__ __device__ inline int64_t square_tiles(const S8Class &k, bool small) {
+  return small ? sym_tiles(k.tiles_s) : 2 * sym_tiles(k.tiles_m);
+}
+
+__device__ Stage1Scalars stage1_scalars(const S8Mat &M, bool sq_small, double *bcast) {
   Stage1Scalars r;
   r.fro2 = sum_parts(M.fro(), fro_parts_used(M), bcast);
-  const double sq = sum_parts(M.sch(), static_cast<int>(2 * sym_tiles(M.kp()->tiles_m)), bcast);
+  const double sq = sum_parts(M.sch(), static_cast<int>(square_tiles(*M.kp(), sq_small)), bcast);
   r.ok = r.fro2 > 0.0 && sq > 0.0;
   r.s = r.ok ? fmaxf(static_cast<float>(kS8Margin * pow(sq, 0.125)), 1e-30f) : 1.f;
   return r;
@@ -596,7 +630,7 @@ __device__ __forceinline__ TileRef tile_of(const StageArgs &args) {
 // padded to 36 floats (16-byte aligned row vectors).
 constexpr int kEpStride = 36;
 constexpr int kEpBlock = 32 * kEpStride;
-static_assert(kWaves * 2 * kEpBlock * 4 <= kRingBytes, "epilogue staging must fit in the operand ring");
+static_assert(kWaves * 2 * kEpBlock * 4 <= Geo<kSymTile>::kRingBytes, "epilogue staging must fit in the operand ring");
 
 __device__ __forceinline__ void ep_read8(const float *s, int row, int col, float (&w)[8]) {
   const f32x4 a = *reinterpret_cast<const f32x4 *>(s + row * kEpStride + col);
@@ -606,26 +640,32 @@ __device__ __forceinline__ void ep_read8(const float *s, int row, int col, float
 }
 
 // ------------------------------------------------------------ kernel ---
-// Output tiles are 256 x 128: tm counts 256-row blocks, tn 128-column
-// blocks.  The Gram and the square compute the upper-triangle 256 x 256
-// blocks of their symmetric result, each as two 128-column halves
-// (tix = 2 * block index + half); a diagonal block's halves together cover
-// it, an off-diagonal half also writes its mirror.
-__host__ __device__ inline int64_t phase_tiles(const S8Class &k, int phase) {
-  return phase == kApply ? static_cast<int64_t>(k.tiles_m) * (k.cp / kTileN) : 2 * sym_tiles(k.tiles_m);
+// Output tiles are TM x 128: tm counts TM-row blocks, tn 128-column blocks.
+// The Gram and the square compute the upper triangle of their symmetric
+// result: with 256 x 128 tiles as the upper-triangle 256 x 256 blocks,
+// each as two 128-column halves (tix = 2 * block index + half); with
+// 128 x 128 tiles as the upper-triangle tiles (tn >= tm, row by row).  A
+// diagonal block or tile is computed whole; an off-diagonal one also
+// writes its mirror.
+__host__ __device__ inline int64_t phase_tiles(const S8Class &k, int phase, bool sq_small) {
+  if (phase == kApply) return static_cast<int64_t>(k.tiles_m) * (k.cp / kTileN);
+  return phase == kSquare ? square_tiles(k, sq_small) : 2 * sym_tiles(k.tiles_m);
 }
 
-template <int MODE, int PHASE>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int MODE, int PHASE, int TM>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(Geo<TM>::kWavesPerEU, Geo<TM>::kWavesPerEU)))
 s8_stage_kernel(StageArgs args) {
-  __shared__ __attribute__((aligned(16))) char smem[kRingBytes];
+  static_assert(TM == kTile || PHASE == kSquare, "128 x 128 tiles for the square only");
+  using Gm = Geo<TM>;
+  constexpr int kSubM = Gm::kSubM;
+  __shared__ __attribute__((aligned(16))) char smem[Gm::kRingBytes];
   __shared__ double dscratch[16];
   __shared__ double bcast;
   constexpr bool PL = MODE == SMX_S8_COMP_BF16;  // operands stored as interleaved BF16
 
   const TileRef ref = tile_of(args);
   const S8Class &K = *ref.k;
-  const int64_t tpm = phase_tiles(K, PHASE);
+  const int64_t tpm = phase_tiles(K, PHASE, TM == kSymTile);
   if (ref.L >= tpm * K.count) return;
   const int slot = static_cast<int>(ref.L / tpm);
   const int64_t tix = ref.L % tpm;
@@ -635,13 +675,19 @@ s8_stage_kernel(StageArgs args) {
     const int64_t tn2 = K.cp / kTileN;
     tm = tix / tn2;
     tn = tix % tn2;
-  } else {
+  } else if constexpr (TM == kTile) {
     int64_t rem = tix >> 1;
     tm = 0;
     while (rem >= K.tiles_m - tm) { rem -= K.tiles_m - tm; ++tm; }
     const int64_t tb = tm + rem;
     tn = 2 * tb + (tix & 1);
     diag = tb == tm;
+  } else {
+    int64_t rem = tix;
+    tm = 0;
+    while (rem >= K.tiles_s - tm) { rem -= K.tiles_s - tm; ++tm; }
+    tn = tm + rem;
+    diag = tn == tm;
   }
   const S8Mat M{K, slot};
   const int stage = args.stage;
@@ -657,25 +703,25 @@ s8_stage_kernel(StageArgs args) {
       scale = f > 0.0 ? static_cast<float>(1.0 / f) : 0.f;
     }
     const Opnd X{x_in, K.cp};
-    gemm_tile<MODE, false, false>(X, X, K.cp, tm * kTileM, tn * kTileN, 0.f, smem, acc);
+    gemm_tile<MODE, TM, false, false>(X, X, K.cp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
   } else if constexpr (PHASE == kSquare) {
     const Opnd G{M.g(), K.rp};
     if (stage == 1) {
-      gemm_tile<MODE, false, false>(G, G, K.rp, tm * kTileM, tn * kTileN, 0.f, smem, acc);
+      gemm_tile<MODE, TM, false, false>(G, G, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
     } else {
       // acc = G G + (b/c) G; the epilogue forms P = c acc + a I.
       scale = args.c;
-      gemm_tile<MODE, true, false>(G, G, K.rp, tm * kTileM, tn * kTileN, args.b_over_c, smem, acc);
+      gemm_tile<MODE, TM, true, false>(G, G, K.rp, tm * Gm::kTileM, tn * kTileN, args.b_over_c, smem, acc);
     }
   } else {
     if (stage == 1) {
       // X' = P1 V / (||V|| s)
-      const Stage1Scalars sc = stage1_scalars(M, &bcast);
+      const Stage1Scalars sc = stage1_scalars(M, args.sq_small != 0, &bcast);
       scale = sc.ok ? static_cast<float>(1.0 / (sqrt(sc.fro2) * static_cast<double>(sc.s))) : 0.f;
     }
     // X' = P X: B = X rows k (K-major), columns of the tile.
-    gemm_tile<MODE, false, true>(Opnd{M.p(), K.rp}, Opnd{x_in, K.cp}, K.rp, tm * kTileM, tn * kTileN, 0.f, smem,
-                                 acc);
+    gemm_tile<MODE, TM, false, true>(Opnd{M.p(), K.rp}, Opnd{x_in, K.cp}, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f,
+                                     smem, acc);
   }
 
   // ------------------------------------------------------- epilogue ---
@@ -689,7 +735,7 @@ s8_stage_kernel(StageArgs args) {
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
   const int rr = lane >> 2, cc = (lane & 3) * 8;  // read-back: rows rr, rr + 16; cols cc..cc+7
-  const int64_t R0 = tm * kTileM + wm * (32 * kSubM), C0 = tn * kTileN + wn * (32 * kSubN);
+  const int64_t R0 = tm * Gm::kTileM + wm * (32 * kSubM), C0 = tn * kTileN + wn * (32 * kSubN);
   const bool last = stage == 5;
   float *dst_t, *dst_m;
   int64_t ld_t, ld_m;
@@ -805,7 +851,7 @@ __global__ void __launch_bounds__(256) s8_poly1_kernel(StageArgs args) {
       g4[k][e] = reinterpret_cast<const uint4 *>(G + idx[k])[e];
     }
   }
-  const Stage1Scalars sc = stage1_scalars(M, &bcast);
+  const Stage1Scalars sc = stage1_scalars(M, args.sq_small != 0, &bcast);
   const float s2 = sc.s * sc.s;
   const float is2 = sc.ok ? 1.0f / s2 : 0.f, is4 = sc.ok ? 1.0f / (s2 * s2) : 0.f;
 #pragma unroll
@@ -888,31 +934,54 @@ static int timing_end(int slot, hipStream_t st, int phase, double flops) {
   return SMX_OK;
 }
 
-// MFMA FLOPs of one launch: computed tiles x 2 * 256 * 256 * K (x3 in
-// compensated mode), plus the square phase's one-hot MFMAs (8 stages of
-// kSubN 32x32x16 products per wave).
+// MFMA FLOPs of one launch: computed tiles x 2 * TM * 128 * K (x3 in
+// compensated mode), plus the square phase's one-hot MFMAs (2 kSubM stages
+// of kSubN 32x32x16 products per wave).
 template <int PHASE>
-static double launch_flops(const S8Layout &Lay, int stage) {
+static double launch_flops(const S8Layout &Lay, int stage, bool sq_small) {
   if (PHASE == kPoly1) return 0.0;
   const double prod = Lay.mode == SMX_S8_COMP_BF16 ? 3.0 : 1.0;
+  const int tm = PHASE == kSquare && sq_small ? kSymTile : kTile;
+  const int sub_m = tm / 64;
   double f = 0.0;
   for (int i = 0; i < Lay.n_classes; ++i) {
     const S8Class &k = Lay.cls[i];
-    const double tiles = static_cast<double>(phase_tiles(k, PHASE));
+    const double tiles = static_cast<double>(phase_tiles(k, PHASE, sq_small));
     const double K = PHASE == kGram ? static_cast<double>(k.cp) : static_cast<double>(k.rp);
-    f += k.count * tiles * 2.0 * kTileM * kTileN * K * prod;
+    f += k.count * tiles * 2.0 * tm * kTileN * K * prod;
     // one-hot: per wave 2 kSubM stages of kSubN MFMA tiles
     if (PHASE == kSquare && stage != 1)
-      f += k.count * tiles * kWaves * (2.0 * kSubM) * kSubN * 2.0 * 32 * 32 * kBK * prod;
+      f += k.count * tiles * kWaves * (2.0 * sub_m) * kSubN * 2.0 * 32 * 32 * kBK * prod;
   }
   return f;
 }
 
+// Whether the square phase of a layout takes 128 x 128 tiles: rounds of the
+// device's block slots (two 256 x 128 or three 128 x 128 blocks per CU),
+// a round of the smaller tile counted as 0.9 of one of the larger.
+static bool square_small(const S8Layout &Lay, hipStream_t st) {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  if (cus[dev] == 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return false;
+  (void)st;
+  int64_t big = 0, small = 0;
+  for (int i = 0; i < Lay.n_classes; ++i) {
+    big += Lay.cls[i].count * square_tiles(Lay.cls[i], false);
+    small += Lay.cls[i].count * square_tiles(Lay.cls[i], true);
+  }
+  const double r_big = static_cast<double>(ceil_div(big, 2 * static_cast<int64_t>(cus[dev])));
+  const double r_small = static_cast<double>(ceil_div(small, 3 * static_cast<int64_t>(cus[dev])));
+  return 0.9 * r_small < r_big;
+}
+
 template <int PHASE>
-static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
+static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, hipStream_t st) {
   StageArgs a{};
   a.L = Lay;
   a.stage = stage;
+  a.sq_small = sq_small ? 1 : 0;
   const auto &co = kS8Coefficients[stage - 1];
   a.a = static_cast<float>(co[0]);
   a.b = static_cast<float>(co[1]);
@@ -931,7 +1000,7 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
   for (int ci : order) {
     const S8Class &k = Lay.cls[ci];
     if (k.count == 0) continue;
-    const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE);
+    const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE, sq_small);
     const int64_t nt = round_up(tpm * k.count, 8);
     a.seg_off[a.n_seg] = off;
     a.seg_cls[a.n_seg] = ci;
@@ -951,14 +1020,24 @@ static int launch_phase(const S8Layout &Lay, int stage, hipStream_t st) {
       hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_FP32>, dim3(off), dim3(256), 0, st, a);
     rc = check_launch("s8 stage-1 polynomial");
   } else {
-    if (comp)
-      hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_COMP_BF16, PHASE>), dim3(off), dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_FP32, PHASE>), dim3(off), dim3(kThreads), 0, st, a);
+    if constexpr (PHASE == kSquare) {
+      if (sq_small) {
+        if (comp)
+          hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_COMP_BF16, PHASE, kSymTile>), dim3(off), dim3(kThreads), 0, st, a);
+        else
+          hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_FP32, PHASE, kSymTile>), dim3(off), dim3(kThreads), 0, st, a);
+      }
+    }
+    if (PHASE != kSquare || !sq_small) {
+      if (comp)
+        hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_COMP_BF16, PHASE, kTile>), dim3(off), dim3(kThreads), 0, st, a);
+      else
+        hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_FP32, PHASE, kTile>), dim3(off), dim3(kThreads), 0, st, a);
+    }
     rc = check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : "s8 apply");
   }
   if (rc) return rc;
-  return timing_end(slot, st, PHASE, launch_flops<PHASE>(Lay, stage));
+  return timing_end(slot, st, PHASE, launch_flops<PHASE>(Lay, stage, sq_small));
 }
 
 // The whole S8 run: per stage one launch per phase over every class (class
@@ -968,14 +1047,16 @@ int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
   int slot = -1;
   int rc = timing_begin(st, slot, true);
   if (rc) return rc;
+  const bool sq_small = square_small(Lay, st);
   double flops = 0.0;
   for (int stage = 1; stage <= 5; ++stage) {
-    rc = launch_phase<kGram>(Lay, stage, st);
-    if (!rc) rc = launch_phase<kSquare>(Lay, stage, st);
-    if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, stage, st);
-    if (!rc) rc = launch_phase<kApply>(Lay, stage, st);
+    rc = launch_phase<kGram>(Lay, stage, sq_small, st);
+    if (!rc) rc = launch_phase<kSquare>(Lay, stage, sq_small, st);
+    if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, stage, sq_small, st);
+    if (!rc) rc = launch_phase<kApply>(Lay, stage, sq_small, st);
     if (rc) return rc;
-    flops += launch_flops<kGram>(Lay, stage) + launch_flops<kSquare>(Lay, stage) + launch_flops<kApply>(Lay, stage);
+    flops += launch_flops<kGram>(Lay, stage, sq_small) + launch_flops<kSquare>(Lay, stage, sq_small) +
+             launch_flops<kApply>(Lay, stage, sq_small);
   }
   return timing_end(slot, st, kSpan, flops);
 }
@@ -1024,6 +1105,7 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.cp = round_up(C.c, kTile);
     C.tiles_m = static_cast<int32_t>(C.rp / kTile);
     C.tiles_n = static_cast<int32_t>(C.cp / kTile);
+    C.tiles_s = static_cast<int32_t>(C.rp / kSymTile);
     C.parts = static_cast<int32_t>(ceil_div(C.cp, kPartRows));
     const size_t xs = static_cast<size_t>(C.count) * C.rp * C.cp * sizeof(float);
     const size_t gs = static_cast<size_t>(C.count) * C.rp * C.rp * sizeof(float);
@@ -1035,7 +1117,7 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.u = reinterpret_cast<float *>(take(static_cast<size_t>(C.count) * C.cp * sizeof(float)));
     C.fro = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));
     C.mb = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));
-    C.sch = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * 2 * sym_tiles(C.tiles_m) * sizeof(double)));
+    C.sch = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * sym_tiles(C.tiles_s) * sizeof(double)));
     C.cst = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * 2 * sizeof(double)));
   }
   plan.bytes = off;

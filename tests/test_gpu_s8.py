@@ -84,11 +84,15 @@ def test_s8_launch_timing_records_every_phase(device, mode):
     run, rec = rec[0], rec[1:]
     assert run[2] == sum(f for _, _, f in rec)
     assert run[0] >= max(ms for ms, _, _ in rec)
-    # oriented 300 x 520 padded to 512 x 768: 2 x 3 tiles, 3 symmetric tiles
+    # oriented 300 x 520 padded to 512 x 768: the apply computes 2 x 6 tiles
+    # of 256 x 128, the Gram the 3 upper-triangle 256 x 256 blocks of its
+    # 512 x 512 result and the square its 10 upper-triangle 128 x 128 tiles;
+    # the one-hot term adds, per square tile and wave, 4 K stages of 2 MFMA
+    # tiles 32 x 32 x 16.
     prod = 3 if mode == "comp_bf16" else 1
-    gram, apply = 3 * 3 * 2 * 256 * 256 * 768 * prod, 3 * 6 * 2 * 256 * 256 * 512 * prod
-    square1 = 3 * 3 * 2 * 256 * 256 * 512 * prod
-    one_hot = 3 * 3 * 4 * 8 * 4 * 2 * 32 * 32 * 16 * prod
+    gram, apply = 3 * 3 * 2 * 256 * 256 * 768 * prod, 3 * 12 * 2 * 256 * 128 * 512 * prod
+    square1 = 3 * 10 * 2 * 128 * 128 * 512 * prod
+    one_hot = 3 * 10 * 4 * 4 * 2 * 2 * 32 * 32 * 16 * prod
     fl = [f for _, _, f in rec]
     assert fl[:4] == [gram, square1, 0.0, apply]
     assert fl[4:7] == [gram, square1 + one_hot, apply]
@@ -112,3 +116,33 @@ def test_s8_timing_runs_only_records_one_span_per_run(device):
     assert [p for _, p, _ in rec] == ["run", "run"]
     assert all(ms > 0 for ms, _, _ in rec)
     assert rec[0][2] == rec[1][2] == full[0][2]
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("batch,small", [(8, True), (160, False)])
+def test_s8_square_tile_geometries(device, mode, batch, small):
+    """The square phase takes 128 x 128 tiles when they need fewer rounds of
+    the CUs' block slots (8 matrices of 512 x 512 on 256 CUs: 80 small tiles
+    against 48 large ones, one round each) and 256 x 128 tiles otherwise
+    (160 matrices: 960 large tiles fit two rounds of two blocks per CU, the
+    1600 small ones need three rounds of three, counted 0.9 each).  Both geometries meet the gates;
+    the recorded square FLOPs show which one ran."""
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    big_rounds = -(-batch * 6 // (2 * cus))
+    small_rounds = -(-batch * 10 // (3 * cus))
+    assert (0.9 * small_rounds < big_rounds) == small, "the case no longer selects the geometry it names"
+    torch.manual_seed(batch)
+    x = torch.randn(batch, 512, 512)
+    from sandmuon_amd import _native
+    _native.s8_timing(True)
+    try:
+        out = _s8_fp32(x.to(device), mode=mode)
+    finally:
+        _native.s8_timing(False)
+    rec = _native.s8_timing_read()
+    prod = 3 if mode == "comp_bf16" else 1
+    square1 = [f for _, p, f in rec if p == "square"][0]
+    tiles, tm = (10, 128) if small else (6, 256)
+    assert square1 == batch * tiles * 2 * tm * 128 * 512 * prod
+    errs = per_matrix_rel(out, O.s8(x))
+    assert max(errs) <= TOL[mode]
