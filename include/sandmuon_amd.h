@@ -92,6 +92,12 @@ typedef struct smx_stats_desc {
 int smx_stats_accumulate_batch(const smx_stats_desc *descs, int32_t n_desc,
                                void *stream);
 
+/* smx_stats_slot_rows: how many leading slot rows (of n_slots) a call with
+ * `rows` input rows adds into (the row chunks hold at least 512 rows), so
+ * that the fold and finish can skip rows no call touched; -1 for invalid
+ * arguments.  No counterpart in the reference (its sums have no slots). */
+int32_t smx_stats_slot_rows(int64_t rows, int32_t n_slots);
+
 /* The statistics fused into passes a mixed-precision Linear makes anyway
  * (the hook bodies above, moved; no counterpart entry point in the
  * reference).  Both add sum(x^2) to slots_sq exactly as

@@ -8,6 +8,7 @@ current HIP stream of the tensor's device.
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 from ctypes import c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
 from pathlib import Path
@@ -68,6 +69,7 @@ SIGNATURES = {
     "smx_stats_accumulate": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                      c_int32, c_void_p]),
     "smx_stats_accumulate_batch": (c_int, [ctypes.POINTER(StatsDesc), c_int32, c_void_p]),
+    "smx_stats_slot_rows": (c_int32, [c_int64, c_int32]),
     "smx_stats_cast": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int32,
                                c_void_p, c_int, c_int64, c_void_p]),
     "smx_stats_colsum_workspace_bytes": (c_int64, [c_int64, c_int32]),
@@ -161,6 +163,14 @@ def stats_accumulate(rows2d: torch.Tensor, slots_sq: torch.Tensor, slots_first: 
                                     rows2d.shape[1], rows2d.stride(0), slots_sq.data_ptr(),
                                     ptr(slots_first), slots_sq.shape[0], stream_of(rows2d.device))
     _check(rc, "smx_stats_accumulate")
+
+
+@functools.lru_cache(maxsize=256)
+def stats_slot_rows(rows: int, n_slots: int) -> int:
+    """Leading slot rows (of n_slots) a statistics call over `rows` rows adds into."""
+    n = lib().smx_stats_slot_rows(rows, n_slots)
+    _check(min(n, 0), "smx_stats_slot_rows")
+    return n
 
 
 def stats_accumulate_batch(entries, stream: int) -> None:

@@ -581,6 +581,13 @@ extern "C" int smx_stats_accumulate(const void *x, int dtype, int64_t rows, int6
   return stats_launch(&in, 1, static_cast<hipStream_t>(stream), "stats_accumulate");
 }
 
+extern "C" int32_t smx_stats_slot_rows(int64_t rows, int32_t n_slots) {
+  if (rows < 0 || n_slots < 1) return -1;
+  if (rows == 0) return 0;
+  const int64_t rows_per_chunk = std::max<int64_t>(ceil_div(rows, n_slots), kStatsMinChunkRows);
+  return static_cast<int32_t>(ceil_div(rows, rows_per_chunk));
+}
+
 extern "C" int smx_stats_accumulate_batch(const smx_stats_desc *descs, int32_t n_desc, void *stream) {
   SMX_REQUIRE(n_desc >= 0 && (n_desc == 0 || descs), SMX_EINVAL, "stats_accumulate_batch: bad descriptor table");
   std::vector<StatsInput> in;

@@ -107,6 +107,7 @@ class _FusedLinear(torch.autograd.Function):
                     sq, fs = opt._a_slots(p, rows.shape[1], rows.device, state)
                     opt._stats_barrier(sq)
                     _native.stats_cast(rows, sq, fs, x_lp)
+                    opt._note_slots(sq, rows.shape[0])
                     state["a_count"] += rows.shape[0]
                 else:
                     x_lp.copy_(rows)
@@ -141,6 +142,7 @@ class _FusedLinear(torch.autograd.Function):
             colsum = torch.empty(g.shape[1], dtype=torch.float32, device=g.device)
             opt._stats_barrier(sq)
             _native.stats_colsum(g, sq, colsum, site.colsum_workspace(g.shape[1], g.device))
+            opt._note_slots(sq, g.shape[0])
             grad_b = colsum if ctx.b_dtype == torch.float32 else colsum.to(ctx.b_dtype)
         else:
             opt._enqueue_stats(g, sq, None)

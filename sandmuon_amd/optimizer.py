@@ -271,6 +271,9 @@ class DiagonalWeightedPE(Optimizer):
         if limit < 0:
             raise ValueError("hook_batch_bytes must be >= 0")
         self._queue = _StatsQueue(limit)
+        # Leading slot rows any call has added into since the last fold, per
+        # slot buffer (data pointer): the fold and finish read only those.
+        self._slot_rows: Dict[int, int] = {}
         self._workspace: Optional[torch.Tensor] = None
         self.register_state_dict_pre_hook(DiagonalWeightedPE._flush_slots)
         self.register_load_state_dict_post_hook(DiagonalWeightedPE._drop_slots)
@@ -330,9 +333,22 @@ class DiagonalWeightedPE(Optimizer):
         self._enqueue_stats(rows, sq, None)
         state["b_count"] += rows.shape[0]
 
+    def _note_slots(self, sq: torch.Tensor, rows: int) -> None:
+        """Records the slot rows a statistics call over `rows` rows adds into."""
+        n = _native.stats_slot_rows(rows, sq.shape[0])
+        key = sq.data_ptr()
+        if n > self._slot_rows.get(key, 0):
+            self._slot_rows[key] = n
+
+    def _take_slot_rows(self, sq: torch.Tensor) -> int:
+        """Slot rows the next fold of `sq` must read (at least one); the count
+        restarts, since the fold zeroes them."""
+        return max(self._slot_rows.pop(sq.data_ptr(), 0), 1)
+
     def _enqueue_stats(self, rows: torch.Tensor, sq: torch.Tensor, fs: Optional[torch.Tensor]) -> None:
         """Queues one hook input (or launches at once when batching is off)."""
         q = self._queue
+        self._note_slots(sq, rows.shape[0])
         if q.limit == 0:
             _native.stats_accumulate(rows, sq, fs)
             return
@@ -401,13 +417,15 @@ class DiagonalWeightedPE(Optimizer):
             if total is None:
                 continue
             first = state.get("a_first_sum") if side == "a" and fs is not None else None
-            _native.stats_fold(total, sq, first, fs if first is not None else None)
+            n = self._take_slot_rows(sq)
+            _native.stats_fold(total, sq[:n], first, fs[:n] if first is not None else None)
 
     @staticmethod
     def _drop_slots(self) -> None:
         """Loaded sums are authoritative: pending partials are discarded."""
         self._queue.clear()
         self._slots.clear()
+        self._slot_rows.clear()
 
     # ------------------------------------------------------------- step ---
     def _finish_a_check(self, parameter) -> int:
@@ -436,7 +454,7 @@ class DiagonalWeightedPE(Optimizer):
                 state["a_mean_ema"] = torch.empty(n, dtype=torch.float32, device=total.device)
         kind = _KIND_B if side == "b" else (_KIND_RANK1_A if rank1 else _KIND_DIAG_A)
         d = _native.FinishDesc(sum_sq=total.data_ptr(), slots_sq=sq.data_ptr(), ema=state[ema_key].data_ptr(),
-                               inv=out["inv"].data_ptr(), n=n, count=int(count), n_slots=sq.shape[0],
+                               inv=out["inv"].data_ptr(), n=n, count=int(count), n_slots=self._take_slot_rows(sq),
                                kind=kind, first=int(first))
         if rank1:
             d.sum_first, d.slots_first = state["a_first_sum"].data_ptr(), fs.data_ptr()

@@ -118,6 +118,16 @@ def test_validation_errors_return_before_gpu_work():
     assert lib.smx_adamw((_native.AdamwDesc * 1)(a), 1, 4, 1e-3, .9, .999, 1e-8, .01, None) == -2
 
 
+def test_stats_slot_rows():
+    # Row chunks hold at least 512 rows and at most n_slots chunks are used.
+    lib = _native.lib()
+    cases = {0: 0, 1: 1, 512: 1, 513: 2, 16384: 32, 8192: 16, 65536: 128, 70000: 128, 10**7: 128}
+    for rows, want in cases.items():
+        assert lib.smx_stats_slot_rows(rows, 128) == want, rows
+    assert lib.smx_stats_slot_rows(5000, 4) == 4
+    assert lib.smx_stats_slot_rows(-1, 128) == -1 and lib.smx_stats_slot_rows(10, 0) == -1
+
+
 def test_workspace_sizes_are_consistent():
     # 103M GPT matrices: 36 of 768x768 and 18 of 768x3072 (9 of them transposed).
     shapes = [(768, 768)] * 36 + [(3072, 768)] * 9 + [(768, 3072)] * 9
