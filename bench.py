@@ -135,6 +135,42 @@ def logical_s8_flops(opt):
     return total
 
 
+def vendor_gemm_rate(opt, device, reps=20):
+    """Plain BF16 batched GEMMs of one S8 stage's shapes through torch.bmm
+    (hipBLASLt), FP32 accumulation, one product each: per shape class of
+    oriented r x c, the Gram X X^T, the square G G and the apply P X.  Dense
+    FLOPs (the Gram and square in full) / time: the vendor library's rate on
+    the S8's shapes on this box, a reference for the S8 kernel's own rate.
+    Every operand is contiguous (no transposed views into bmm)."""
+    classes = {}
+    for p in opt.named_matrices.values():
+        r, c = sorted(p.shape)
+        classes[(r, c)] = classes.get((r, c), 0) + 1
+    g = torch.Generator(device=device).manual_seed(7)
+    work = []
+    for (r, c), n in classes.items():
+        x = torch.randn(n, r, c, generator=g, device=device).bfloat16()
+        xt = x.transpose(1, 2).contiguous()
+        gm = torch.randn(n, r, r, generator=g, device=device).bfloat16()
+        work += [(x, xt, 2 * n * r * r * c), (gm, gm, 2 * n * r * r * r), (gm, x, 2 * n * r * r * c)]
+    flops = sum(f for _, _, f in work)
+    for a, b, _ in work:
+        torch.bmm(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for a, b, _ in work:
+            torch.bmm(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    return {"tflops": round(flops / (ms * 1e-3) / 1e12, 1), "frac": round(flops / (ms * 1e-3) / BF16_PEAK, 4),
+            "ms_per_stage": round(ms, 3), "flops_per_stage": flops,
+            "what": "torch.bmm bf16 (hipBLASLt) on one S8 stage's shapes: Gram X X^T, square G G, apply P X, "
+                    "one product each, dense"}
+
+
 def committed_traffic():
     """HBM bytes per launch of the dominant kernels, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None if absent)."""
@@ -369,6 +405,7 @@ def main():
                "issued_flops_per_step": s8_issued, "logical_flops_per_step": s8_logical,
                "logical_tflops": round(s8_logical / (s8_ms * 1e-3) / 1e12, 1), "ms_per_step": round(s8_ms, 3),
                "phases": s8_phases}
+    roof_s8["vendor_bf16_gemm"] = vendor_gemm_rate(opt, device)
     dominant = roof_stats if hooks_ms >= s8_ms else roof_s8
     out = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
