@@ -6,7 +6,10 @@
 //      calls, folded into the running sum (smx_stats_accumulate,
 //      smx_stats_fold), against FP64 host sums;
 //   2. the fused bias-gradient column sum with the same statistic
-//      (smx_stats_colsum);
+//      (smx_stats_colsum), and one batched launch over two inputs
+//      (smx_stats_accumulate_batch), which must add exactly what one call
+//      per input adds, folded over the slot rows it touched
+//      (smx_stats_slot_rows);
 //   3. one matrix step of a 256 x 384 parameter with diagonal factors in
 //      FP32-MFMA mode (smx_matrix_step): the momentum is exactly
 //      (1 - beta) g from a zero start, and the update has ||dW|| / lr =
@@ -119,6 +122,45 @@ int main() {
   ok &= report("stats_accumulate x2 + fold: rel. error of sum x^2", std::sqrt(num / den), 1e-6);
   ok &= report("stats_colsum: max |colsum - sum x| / sum |x|", worst, 1e-6);
 
+  // Batched: the whole tensor and its first 5000 rows (an odd microbatch)
+  // into two slot buffers in one launch, against one call each.
+  const int64_t part_rows = 5000;
+  float *sb_d[4];
+  for (auto &p : sb_d) {
+    HIP_OK(hipMalloc(reinterpret_cast<void **>(&p), slots * cols * 4));
+    HIP_OK(hipMemset(p, 0, slots * cols * 4));
+  }
+  smx_stats_desc descs[2] = {{xd, sb_d[0], nullptr, rows, cols, cols, SMX_BF16, slots},
+                             {xd, sb_d[1], nullptr, part_rows, cols, cols, SMX_BF16, slots}};
+  SMX_OK_(smx_stats_accumulate_batch(descs, 2, st));
+  SMX_OK_(smx_stats_accumulate(xd, SMX_BF16, rows, cols, cols, sb_d[2], nullptr, slots, st));
+  SMX_OK_(smx_stats_accumulate(xd, SMX_BF16, part_rows, cols, cols, sb_d[3], nullptr, slots, st));
+  HIP_OK(hipStreamSynchronize(st));
+  std::vector<float> sb[4];
+  for (int k = 0; k < 4; ++k) {
+    sb[k].resize(slots * cols);
+    HIP_OK(hipMemcpy(sb[k].data(), sb_d[k], slots * cols * 4, hipMemcpyDeviceToHost));
+  }
+  const bool same = sb[0] == sb[2] && sb[1] == sb[3];
+  std::printf("%-58s %s\n", "stats_accumulate_batch: bit-identical to one call each", same ? "ok" : "FAIL");
+  ok &= same;
+  // Only the leading slot rows a call touched hold partials.
+  const int32_t used = smx_stats_slot_rows(rows, slots);
+  bool rest_zero = used >= 1 && used <= slots;
+  for (int64_t i = static_cast<int64_t>(used) * cols; i < slots * cols; ++i) rest_zero &= sb[0][i] == 0.f;
+  HIP_OK(hipMemset(sum_d, 0, cols * 4));
+  SMX_OK_(smx_stats_fold(sum_d, sb_d[0], nullptr, nullptr, cols, used, st));
+  HIP_OK(hipMemcpy(sum.data(), sum_d, cols * 4, hipMemcpyDeviceToHost));
+  num = den = 0;
+  for (int64_t j = 0; j < cols; ++j) {
+    num += (sum[j] - want_sq[j]) * (sum[j] - want_sq[j]);
+    den += want_sq[j] * want_sq[j];
+  }
+  std::printf("%-58s %d of %d %s\n", "smx_stats_slot_rows: rows touched, the rest zero", used, slots,
+              rest_zero ? "ok" : "FAIL");
+  ok &= rest_zero;
+  ok &= report("batched stats, fold of the touched rows: rel. error", std::sqrt(num / den), 1e-6);
+
   // ---- 3: one matrix step, diagonal factors, FP32-MFMA mode
   const int64_t r = 256, c = 384;
   const double lr = 1e-2, beta = 0.8;
@@ -171,6 +213,7 @@ int main() {
                1e-4);
 
   hipFree(xd); hipFree(slot_d); hipFree(sum_d); hipFree(colsum_d); hipFree(ws); hipFree(slot2_d);
+  for (auto p : sb_d) hipFree(p);
   hipFree(w_d); hipFree(g_d); hipFree(m_d); hipFree(ir_d); hipFree(ic_d); hipFree(mws);
   hipStreamDestroy(st);
   std::printf("%s\n", ok ? "all checks passed" : "FAILED");
