@@ -115,21 +115,29 @@ __device__ __forceinline__ double sum_wave_parts(double part, double *wave_part)
 // for a transposed parameter), two passes over the row:
 //  1. momentum m' = b m + (1-b) g (in place), u_i = b_i sum_j S_ij a_j z_j
 //     and the row's ||V_i||^2 (closed form) for S = b m' + (1-b) g;
-//  2. V_ij = b_i S_ij a_j + kappa u_i z_j from g and m' again (the row was
-//     just read, so this comes from cache) stored in operand form to the
+//  2. V_ij = b_i S_ij a_j + kappa u_i z_j stored in operand form to the
 //     oriented iterate: row i of X directly (pl), or, for a transposed
 //     parameter (tl), through LDS in chunks of kWhitenChunk columns, where
 //     the block's 16 rows are one 16-element K group of each X row.
+// KEEP > 0 (rows of at most KEEP * kWhitenChunk columns, FP32 gradients,
+// 16-byte aligned): pass 1 keeps S of the lane's columns in registers and
+// pass 2 reads it from there; KEEP = 0: pass 2 reads g and m' again (the
+// row was just read, so mostly from cache).  Both give the same bits.
 // Rows and columns of the padding are written as zeros.
 constexpr int kWhitenChunk = 1024;  // = 4 * 64 * kRowUnroll
+// Most column chunks a row keeps in registers: 4 for parameters kept as
+// they are (256-thread blocks, up to ~170 VGPRs), 1 for transposed ones
+// (1024-thread blocks hold at most 128 VGPRs per lane).
+constexpr int kWhitenKeep = 4;
+constexpr int kWhitenKeepFlip = 1;
 
 // Rows per block: a transposed parameter needs 16 (one K group of every X
 // row); the others take kPartRows, so that more, shorter blocks share a CU.
 template <bool FLIP>
 constexpr int whiten_rows_per_block() { return FLIP ? kRowsPerPart : kPartRows; }
 
-template <bool R1, bool FLIP>
-__global__ void __launch_bounds__(kRowThreads) whiten_kernel(MatPack pack) {
+template <bool R1, bool FLIP, int KEEP>
+__global__ void __launch_bounds__(64 * whiten_rows_per_block<FLIP>()) whiten_kernel(MatPack pack) {
   constexpr int RB = whiten_rows_per_block<FLIP>();
   static_assert(kRowsPerPart == 16 && kRowThreads == 1024, "one 16-row K group per transposed block, 4 lanes per X row");
   static_assert(RB % kPartRows == 0, "whole partials per block");
@@ -152,6 +160,10 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(MatPack pack) {
   const bool live = i < d.rows;
   float *mrow = live ? d.momentum + i * d.cols : nullptr;
   const float *grow = live && vec ? static_cast<const float *>(d.grad) + i * d.cols : nullptr;
+  // S of this lane's columns: chunk k, float4 u covers columns
+  // 4 lane + 4 * 64 u + kWhitenChunk k (pass 1's and pass 2's mapping).
+  const bool kept = KEEP > 0 && vec && d.cols <= static_cast<int64_t>(KEEP) * kWhitenChunk;
+  float4 sk[KEEP > 0 ? KEEP : 1][kRowUnroll];
 
   // ---- pass 1
   double part = 0.0;
@@ -160,7 +172,8 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(MatPack pack) {
     float y2 = 0.f, yz = 0.f;
     if (vec) {
       const int64_t n4 = d.cols / 4;
-      for (int64_t q0 = lane; q0 < n4; q0 += 64 * kRowUnroll) {
+      // One chunk of kRowUnroll float4 per lane; S goes to keep_s.
+      auto chunk = [&](int64_t q0, float4 (&keep_s)[kRowUnroll]) {
         // Every load of the chunk is issued before the first store.
         float4 g[kRowUnroll], m[kRowUnroll], a[kRowUnroll], z[kRowUnroll];
 #pragma unroll
@@ -182,15 +195,26 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(MatPack pack) {
             mm.x = fmaf(mm.x, beta, gg.x * omb); mm.y = fmaf(mm.y, beta, gg.y * omb);
             mm.z = fmaf(mm.z, beta, gg.z * omb); mm.w = fmaf(mm.w, beta, gg.w * omb);
             st4(mrow, q, mm);
-            const float y0 = fmaf(mm.x, beta, gg.x * omb) * aa.x, y1 = fmaf(mm.y, beta, gg.y * omb) * aa.y;
-            const float y2_ = fmaf(mm.z, beta, gg.z * omb) * aa.z, y3 = fmaf(mm.w, beta, gg.w * omb) * aa.w;
+            const float s0 = fmaf(mm.x, beta, gg.x * omb), s1 = fmaf(mm.y, beta, gg.y * omb);
+            const float s2 = fmaf(mm.z, beta, gg.z * omb), s3 = fmaf(mm.w, beta, gg.w * omb);
+            keep_s[u] = make_float4(s0, s1, s2, s3);
+            const float y0 = s0 * aa.x, y1 = s1 * aa.y;
+            const float y2_ = s2 * aa.z, y3 = s3 * aa.w;
             y2 = fmaf(y0, y0, fmaf(y1, y1, fmaf(y2_, y2_, fmaf(y3, y3, y2))));
             if constexpr (R1) {
               const float4 zz4 = z[u];
               yz = fmaf(y0, zz4.x, fmaf(y1, zz4.y, fmaf(y2_, zz4.z, fmaf(y3, zz4.w, yz))));
             }
+          } else {
+            keep_s[u] = make_float4(0.f, 0.f, 0.f, 0.f);
           }
         }
+      };
+      if (kept) {
+#pragma unroll
+        for (int k = 0; k < (KEEP > 0 ? KEEP : 1); ++k) chunk(lane + 64 * kRowUnroll * k, sk[k]);
+      } else {
+        for (int64_t q0 = lane; q0 < n4; q0 += 64 * kRowUnroll) chunk(q0, sk[0]);
       }
     } else {
       for (int64_t j = lane; j < d.cols; j += 64) {
@@ -262,22 +286,77 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(MatPack pack) {
       }
     }
   };
+  // The same with S from the registers of pass 1 (chunk k of the lane).
+  auto batch_kept = [&](int k, int64_t j0, float (&v)[kRowUnroll][4]) {
+    float4 a[kRowUnroll], z[kRowUnroll];
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t j = j0 + 4 * 64 * u;
+      if (j < d.cols) {
+        a[u] = ld4(d.inv_col, j / 4);
+        if constexpr (R1) z[u] = ld4(d.z, j / 4);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t j = j0 + 4 * 64 * u;
+      const float4 sv = sk[KEEP > 0 ? k : 0][u];
+      const float ss[4] = {sv.x, sv.y, sv.z, sv.w};
+      float as[4] = {0.f, 0.f, 0.f, 0.f}, zs[4] = {0.f, 0.f, 0.f, 0.f};
+      if (j < d.cols) {
+        as[0] = a[u].x; as[1] = a[u].y; as[2] = a[u].z; as[3] = a[u].w;
+        if constexpr (R1) {
+          zs[0] = z[u].x; zs[1] = z[u].y; zs[2] = z[u].z; zs[3] = z[u].w;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float x = (ss[e] * b) * as[e];
+        if constexpr (R1) x = fmaf(ku, zs[e], x);
+        v[u][e] = live && j < d.cols ? x : 0.f;
+      }
+    }
+  };
   if constexpr (!FLIP) {
-    for (int64_t j0 = 4 * lane; j0 < J.pcol_pad; j0 += 4 * 64 * kRowUnroll) {
-      float v[kRowUnroll][4];
-      batch(j0, 4 * 64, v);
+    auto store = [&](int64_t j0, const float (&v)[kRowUnroll][4]) {
 #pragma unroll
       for (int u = 0; u < kRowUnroll; ++u) {
         const int64_t j = j0 + 4 * 64 * u;
         if (j < J.pcol_pad) put_operand4(J.pl, i * J.pcol_pad + j, v[u], planes);
       }
+    };
+    if (kept) {
+#pragma unroll
+      for (int k = 0; k < (KEEP > 0 ? KEEP : 1); ++k) {
+        const int64_t j0 = 4 * lane + static_cast<int64_t>(kWhitenChunk) * k;
+        if (j0 < J.pcol_pad) {
+          float v[kRowUnroll][4];
+          batch_kept(k, j0, v);
+          store(j0, v);
+        }
+      }
+    } else {
+      for (int64_t j0 = 4 * lane; j0 < J.pcol_pad; j0 += 4 * 64 * kRowUnroll) {
+        float v[kRowUnroll][4];
+        batch(j0, 4 * 64, v);
+        store(j0, v);
+      }
     }
   } else {
     static_assert(kWhitenChunk == 4 * 64 * kRowUnroll, "one batch per lane fills a chunk row");
     const int qq = threadIdx.x & 3;  // 4-row quarter of the K group
+    // `kept` is uniform per block (one job per block), so the chunk loop and
+    // its barriers are too.
     for (int64_t c0 = 0; c0 < J.pcol_pad; c0 += kWhitenChunk) {
       float v[kRowUnroll][4];
-      batch(c0 + 4 * lane, 4 * 64, v);
+      if (kept) {
+        const int k = static_cast<int>(c0 / kWhitenChunk);
+#pragma unroll
+        for (int kk = 0; kk < (KEEP > 0 ? KEEP : 1); ++kk)
+          if (kk == k) batch_kept(kk, c0 + 4 * lane, v);
+      } else {
+        batch(c0 + 4 * lane, 4 * 64, v);
+      }
 #pragma unroll
       for (int u = 0; u < kRowUnroll; ++u)
         *reinterpret_cast<float4 *>(&tile[wave][4 * (lane + 64 * u)]) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
@@ -533,6 +612,29 @@ static int64_t map_blocks(const MatJob &j) { return ceil_div(j.d.rows, kPartRows
 template <bool FLIP>
 static int64_t whiten_blocks(const MatJob &j) { return j.prow_pad / whiten_rows_per_block<FLIP>(); }
 
+// Whiten launches for the job lists bucketed by kept chunks (index KEEP).
+template <int KEEP>
+static int launch_whiten_keep(std::vector<MatJob> *keep, std::vector<MatJob> *flip, bool r1, hipStream_t st) {
+  constexpr int kKeepThreads = 64 * whiten_rows_per_block<false>();
+  int rc = SMX_OK;
+  if (!keep[KEEP].empty())
+    rc = r1 ? launch_jobs(keep[KEEP], whiten_blocks<false>, whiten_kernel<true, false, KEEP>, kKeepThreads, "whiten", st)
+            : launch_jobs(keep[KEEP], whiten_blocks<false>, whiten_kernel<false, false, KEEP>, kKeepThreads, "whiten", st);
+  if constexpr (KEEP <= kWhitenKeepFlip) {
+    if (!rc && !flip[KEEP].empty())
+      rc = r1 ? launch_jobs(flip[KEEP], whiten_blocks<true>, whiten_kernel<true, true, KEEP>, kRowThreads, "whiten", st)
+              : launch_jobs(flip[KEEP], whiten_blocks<true>, whiten_kernel<false, true, KEEP>, kRowThreads, "whiten", st);
+  }
+  if constexpr (KEEP < kWhitenKeep) {
+    if (!rc) rc = launch_whiten_keep<KEEP + 1>(keep, flip, r1, st);
+  }
+  return rc;
+}
+
+static int launch_whiten(std::vector<MatJob> *keep, std::vector<MatJob> *flip, bool r1, hipStream_t st) {
+  return launch_whiten_keep<0>(keep, flip, r1, st);
+}
+
 }  // namespace smx
 
 using namespace smx;
@@ -613,13 +715,15 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
     int rc = r1 ? launch_jobs(ping, one_block, matrix_consts_kernel, 256, "matrix_consts", st) : SMX_OK;
     // The whiten kernel is specialised on the orientation too: the jobs go
     // to two launches, parameters kept as they are and transposed ones.
-    std::vector<MatJob> keep, flip;
-    for (const MatJob &j : ping) (j.tl ? flip : keep).push_back(j);
-    constexpr int kKeepThreads = 64 * whiten_rows_per_block<false>();
-    if (!rc) rc = r1 ? launch_jobs(keep, whiten_blocks<false>, whiten_kernel<true, false>, kKeepThreads, "whiten", st)
-                     : launch_jobs(keep, whiten_blocks<false>, whiten_kernel<false, false>, kKeepThreads, "whiten", st);
-    if (!rc) rc = r1 ? launch_jobs(flip, whiten_blocks<true>, whiten_kernel<true, true>, kRowThreads, "whiten", st)
-                     : launch_jobs(flip, whiten_blocks<true>, whiten_kernel<false, true>, kRowThreads, "whiten", st);
+    // and on how many kWhitenChunk column chunks of a row pass 1 keeps in
+    // registers (rows of at most kWhitenKeep chunks; wider ones re-read).
+    std::vector<MatJob> keep[kWhitenKeep + 1], flip[kWhitenKeep + 1];
+    for (const MatJob &j : ping) {
+      const int64_t chunks = ceil_div(j.d.cols, kWhitenChunk);
+      const int64_t most = j.tl ? kWhitenKeepFlip : kWhitenKeep;
+      (j.tl ? flip : keep)[chunks <= most ? chunks : 0].push_back(j);
+    }
+    if (!rc) rc = launch_whiten(keep, flip, r1, st);
     if (!rc) rc = run_s8_stages(plan.layout, st);
     if (!rc) rc = r1 ? launch_jobs(fin, map_blocks, mapback_rows_kernel<true>, kMapThreads, "mapback_rows", st)
                      : launch_jobs(fin, map_blocks, mapback_rows_kernel<false>, kMapThreads, "mapback_rows", st);
