@@ -153,6 +153,14 @@ def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def stream_wait(waiter: int, signaler: int, device: torch.device) -> None:
+    """Makes stream `waiter` wait for the work enqueued so far on stream
+    `signaler` (raw hipStream_t values of `device`)."""
+    done = torch.cuda.Event()
+    done.record(torch.cuda.ExternalStream(signaler, device=device))
+    torch.cuda.ExternalStream(waiter, device=device).wait_event(done)
+
+
 def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 

@@ -237,6 +237,9 @@ class DiagonalWeightedPE(Optimizer):
         matrices, modules = select_matrices(model, module_filter)
         if s8_mode not in _native.S8_MODES:
             raise ValueError(f"s8_mode must be one of {sorted(_native.S8_MODES)}")
+        limit = self.HOOK_BATCH_BYTES if hook_batch_bytes is None else int(hook_batch_bytes)
+        if limit < 0:
+            raise ValueError("hook_batch_bytes must be >= 0")
         _native.lib()  # fails loudly without the HIP library
 
         self.named_matrices = matrices
@@ -267,9 +270,6 @@ class DiagonalWeightedPE(Optimizer):
         # Pending per-chunk partial sums of the hooks, folded into a_sum /
         # b_sum by step() (or before state_dict()).  Not optimizer state.
         self._slots: Dict[Tuple[int, str], Tuple[nn.Parameter, torch.Tensor, Optional[torch.Tensor]]] = {}
-        limit = self.HOOK_BATCH_BYTES if hook_batch_bytes is None else int(hook_batch_bytes)
-        if limit < 0:
-            raise ValueError("hook_batch_bytes must be >= 0")
         self._queue = _StatsQueue(limit)
         # Leading slot rows any call has added into since the last fold, per
         # slot buffer (data pointer): the fold and finish read only those.
@@ -388,9 +388,7 @@ class DiagonalWeightedPE(Optimizer):
         _native.stats_accumulate_batch([(rows, sq, fs) for rows, sq, fs, _ in entries], stream)
         current = _native.stream_of(device)
         if current != stream:
-            done = torch.cuda.Event()
-            done.record(torch.cuda.ExternalStream(stream, device=device))
-            torch.cuda.ExternalStream(current, device=device).wait_event(done)
+            _native.stream_wait(current, stream, device)
 
     def _capture(self, parameter, *, capture_a):
         def hook(module, inputs, output):
