@@ -2,9 +2,14 @@
 //
 //  * stats_accumulate: the hook bodies of sandmuon/optimizer.py:156-168 and
 //    :171-177 (sum of x^2, and sum of x for the rank-one A variant), as one
-//    HBM pass.  Each block owns a (row chunk, column tile) and adds its FP32
-//    partial into slot row `chunk`, so the result is deterministic and no
-//    atomics or tail combine are needed in the hook.
+//    HBM pass, for one input or for a batch of queued hook inputs in one
+//    launch (one job per input).  An input is cut into row chunks of at
+//    least kStatsMinChunkRows rows; each block owns a (job, row chunk,
+//    column tile) and adds its FP32 partial into slot row `chunk` of the
+//    job, so the result is deterministic, depends on the job alone (not on
+//    the other jobs of the launch), and no atomics or tail combine are
+//    needed.  The same kernel takes the statistic inside a Linear's input
+//    cast (CAST) and bias-gradient column sum (kSqColsum).
 //  * stats_fold: sum += sum over slot rows (FP64), slots zeroed.
 //  * stats_finish: _finish_a/_finish_b (sandmuon/optimizer.py:182-222) with
 //    rank1_inverse_sqrt (:27-35) and diagonal_inverse_sqrt (:19-24).
