@@ -714,9 +714,10 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
     // The rank-one constants (sum z^2, sum (a z)^2) exist only with a rank-one term.
     int rc = r1 ? launch_jobs(ping, one_block, matrix_consts_kernel, 256, "matrix_consts", st) : SMX_OK;
     // The whiten kernel is specialised on the orientation too: the jobs go
-    // to two launches, parameters kept as they are and transposed ones.
+    // to two launches, parameters kept as they are and transposed ones,
     // and on how many kWhitenChunk column chunks of a row pass 1 keeps in
-    // registers (rows of at most kWhitenKeep chunks; wider ones re-read).
+    // registers (rows of at most kWhitenKeep chunks, kWhitenKeepFlip for
+    // transposed parameters; wider rows re-read).
     std::vector<MatJob> keep[kWhitenKeep + 1], flip[kWhitenKeep + 1];
     for (const MatJob &j : ping) {
       const int64_t chunks = ceil_div(j.d.cols, kWhitenChunk);

@@ -128,3 +128,42 @@ def test_odd_shapes_through_the_optimizer(device, mode):
     worst = check_directions(hist, opt, 1e-2, mode)
     print(f"odd shapes {mode}: worst direction rel err {worst:.3e}")
     check_aux(hist, opt, ora)
+
+
+class WideBranches(nn.Module):
+    """Linears whose parameter rows take each path of the whiten kernel:
+    in-widths 2048 and 4096 keep 2 and 4 column chunks of S in registers,
+    4100 is wider than 4096 and re-reads g and m'; 64 -> 700 is a transposed
+    parameter with one kept chunk, 1100 -> 1300 a transposed one whose 1100
+    columns re-read.  The batches hold more samples (4096) than the widest
+    parameter has rows or columns: with fewer, the gradients of the 1100 x
+    1300 parameter are rank-deficient, and the polar map of a rank-deficient
+    matrix amplifies the rounding in its null space (two FP32 evaluations of
+    such a matrix already differ by about 1.2e-4), which no FP32 gate can
+    hold to 1e-4."""
+
+    WIDTHS = [(2048, 48), (4096, 40), (4100, 36), (64, 700), (1100, 1300)]
+
+    def __init__(self):
+        super().__init__()
+        self.layers = nn.ModuleList([nn.Linear(a, b) for a, b in self.WIDTHS])
+
+    def forward(self, x):
+        parts = torch.split(x, [a for a, _ in self.WIDTHS], dim=-1)
+        return torch.cat([torch.tanh(layer(p)) for layer, p in zip(self.layers, parts)], dim=-1)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+def test_wide_rows_through_the_optimizer(device, mode):
+    torch.manual_seed(43)
+    model = WideBranches()
+    g = torch.Generator().manual_seed(44)
+    d_in, d_out = sum(a for a, _ in WideBranches.WIDTHS), sum(b for _, b in WideBranches.WIDTHS)
+    batches = [(torch.randn(4, 512, d_in, generator=g) * 0.5 + 0.1, torch.randn(4, 512, d_out, generator=g) * 0.5)
+               for _ in range(2)]
+    loss = lambda m, x, y: (m(x) - y).square().mean() / 2
+    hist, opt, ora = run_pair(device, model, batches, loss, RankOneAWeightedPE, mode, 1e-2, steps=2)
+    assert len(opt.named_matrices) == 5
+    worst = check_directions(hist, opt, 1e-2, mode)
+    print(f"wide rows {mode}: worst direction rel err {worst:.3e}")
+    check_aux(hist, opt, ora)
