@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 1
+#define SMX_ABI_VERSION 2
 
 enum smx_status {
   SMX_OK = 0,
@@ -41,7 +41,9 @@ enum smx_status {
   SMX_ELAUNCH = -6      /* kernel launch failed (see smx_last_error) */
 };
 
-enum smx_dtype { SMX_F32 = 0, SMX_BF16 = 1, SMX_F16 = 2 };
+/* SMX_F64 is accepted by the module-level helpers only (smx_inverse_sqrt,
+ * smx_rank1_apply), which the reference also runs in float64. */
+enum smx_dtype { SMX_F32 = 0, SMX_BF16 = 1, SMX_F16 = 2, SMX_F64 = 3 };
 
 /* Arithmetic of the S8 polar map.
  * SMX_S8_FP32: every product on FP32 MFMA (v_mfma_f32_32x32x2_f32), FP32
@@ -166,7 +168,7 @@ int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc,
  * AdamW on the auxiliary parameters: sandmuon/optimizer.py:268-281.
  * ------------------------------------------------------------------ */
 typedef struct smx_adamw_desc {
-  float *param;        /* [n] fp32                                  */
+  void *param;         /* [n] of param_dtype                        */
   const void *grad;    /* [n] of grad_dtype                         */
   float *exp_avg;      /* [n]                                       */
   float *exp_avg_sq;   /* [n]                                       */
@@ -175,8 +177,13 @@ typedef struct smx_adamw_desc {
   float bias1;         /* 1 - beta1^step (this tensor's step)        */
   float bias2;         /* 1 - beta2^step                             */
   int32_t grad_dtype;
-  int32_t pad_;
+  int32_t param_dtype; /* SMX_F32, SMX_BF16 or SMX_F16                */
 } smx_adamw_desc;
+
+/* The state (exp_avg, exp_avg_sq) is FP32 for every parameter dtype.  A
+ * 16-bit parameter is updated as the reference updates it
+ * (sandmuon/optimizer.py:280-281): p = round(p * (1 - lr*wd)), then
+ * p = round(p - lr * round(update)), each round to the parameter dtype. */
 
 int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t total,
               double lr, double beta1, double beta2, double eps,
@@ -195,10 +202,13 @@ int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t total,
  *   Q = S8(V)    (computed on the r<=c orientation of V)
  *   U = D_b Q (I + kappa z z^T) D_a             (mapback)
  *   W -= lr * sqrt(rows) * U / max(||U||_F, FLT_MIN)
- * The diagonal variant has z = NULL (kappa ignored).
+ * The diagonal variant has z = NULL (kappa ignored).  The momentum is FP32
+ * for every parameter dtype; a 16-bit parameter receives
+ * W = round(W - lr * round(direction)) (sandmuon/optimizer.py:315, where
+ * direction.to(parameter.dtype) is added with alpha -lr).
  * ------------------------------------------------------------------ */
 typedef struct smx_matrix_desc {
-  float *param;          /* [rows, cols] fp32                         */
+  void *param;           /* [rows, cols] of param_dtype, row-major    */
   const void *grad;      /* [rows, cols] of grad_dtype                */
   float *momentum;       /* [rows, cols] fp32, updated in place       */
   const float *inv_row;  /* [rows] B factor                           */
@@ -209,7 +219,7 @@ typedef struct smx_matrix_desc {
   double lr;
   double momentum_beta;
   int32_t grad_dtype;
-  int32_t pad_;
+  int32_t param_dtype;   /* SMX_F32, SMX_BF16 or SMX_F16              */
 } smx_matrix_desc;
 
 /* Device workspace needed for one smx_matrix_step call over the given
@@ -262,24 +272,53 @@ int32_t smx_s8_timing_read(float *ms, int32_t *phase, double *flops,
                            int32_t capacity);
 
 /* ------------------------------------------------------------------ *
- * Module-level helpers.
- * smx_rank1_apply: rank1_whiten (sandmuon/optimizer.py:38-45, order 0) and
- * rank1_mapback (:48-60, order 1) on a contiguous fp32 batch
- * [batch, rows, cols]; both sides may carry a rank-one term.  li/lz are
- * [batch, rows], ri/rz [batch, cols], lc/rc [batch] (device).  `work`
- * holds batch*(rows+cols) floats.  out must not alias x.
- * smx_graft: _graft_direction (:63-66) on n contiguous fp32 values:
- * out = x*sqrt(output_rows)/max(||x||_F, FLT_MIN); a zero input gives a
- * zero output (the reference returns NaN for a zero input once
- * sqrt(rows)/FLT_MIN overflows).  `work` holds work_len doubles (>= 1).
+ * Module-level helpers (sandmuon/optimizer.py:19-66), in the dtype of their
+ * inputs as the reference computes them: SMX_F32 or SMX_F64.
+ *
+ * smx_inverse_sqrt: the factor of one statistics vector of n channels.
+ *   kind 0, diagonal_inverse_sqrt (:19-24): inv = rsqrt(max(max(v, m*1e-6) /
+ *     max(m, tiny), 1e-6)) with m = mean(v) (`second` is v; mean, z and
+ *     kappa are unused and may be NULL).
+ *   kind 1, rank1_inverse_sqrt (:27-35): q = max(mean(second), tiny),
+ *     inv = rsqrt(max(max(second - mean^2, 0) / q, 1e-6)),
+ *     z = inv * (mean / sqrt(q)), rho = sqrt(1 + |z|^2),
+ *     kappa = -1 / (rho (rho + 1)) (kappa: one element).
+ *   Every pointer is a device pointer of `dtype`; n >= 1.
+ * smx_rank1_apply: rank1_whiten (:38-45, order 0) and rank1_mapback
+ *   (:48-60, order 1) on a contiguous batch [batch, rows, cols] of `dtype`;
+ *   both sides may carry a rank-one term.  li/lz are [batch, rows], ri/rz
+ *   [batch, cols], lc/rc [batch] (device, `dtype`).  `work` holds
+ *   batch*(rows+cols) doubles.  out must not alias x.
+ * smx_graft: _graft_direction (:63-66) on n contiguous fp32 values (the
+ *   reference grafts in float32 whatever the input dtype):
+ *   out = x*sqrt(output_rows)/max(||x||_F, FLT_MIN); a zero input gives a
+ *   zero output (the reference returns NaN for a zero input once
+ *   sqrt(rows)/FLT_MIN overflows).  `work` holds work_len doubles (>= 1).
  * ------------------------------------------------------------------ */
-int smx_rank1_apply(const float *x, float *out, int64_t batch, int64_t rows,
-                    int64_t cols, const float *li, const float *lz,
-                    const float *lc, const float *ri, const float *rz,
-                    const float *rc, int order, float *work, void *stream);
+int smx_inverse_sqrt(int kind, int dtype, const void *second,
+                     const void *mean, int64_t n, void *inv, void *z,
+                     void *kappa, void *stream);
+
+int smx_rank1_apply(int dtype, const void *x, void *out, int64_t batch,
+                    int64_t rows, int64_t cols, const void *li,
+                    const void *lz, const void *lc, const void *ri,
+                    const void *rz, const void *rc, int order, double *work,
+                    void *stream);
 
 int smx_graft(const float *x, float *out, int64_t n, int64_t output_rows,
               double *work, int32_t work_len, void *stream);
+
+/* ------------------------------------------------------------------ *
+ * Compensated stages of SMX_S8_COMP_BF16 (no counterpart in the
+ * reference; a measurement aid for choosing the recipe).  Stages 1..k use
+ * the compensated product hi*lo + lo*hi + hi*hi, stages k+1..5 the plain
+ * BF16 product hi*hi of the same stored operands.  The default, 5, is the
+ * production recipe; 1 is the historical one
+ * (reproduction/odl/ops/dense_s8_compensated_fast.py:53-85).  Process-wide,
+ * read at each S8 launch; returns the previous value, or SMX_EINVAL for k
+ * outside [0, 5] (then nothing changes).
+ * ------------------------------------------------------------------ */
+int smx_s8_comp_stages(int32_t k);
 
 #ifdef __cplusplus
 }

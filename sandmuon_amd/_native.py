@@ -17,9 +17,9 @@ from typing import Optional, Sequence
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsandmuon_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
-SMX_F32, SMX_BF16, SMX_F16 = 0, 1, 2
+SMX_F32, SMX_BF16, SMX_F16, SMX_F64 = 0, 1, 2, 3
 S8_FP32, S8_COMP_BF16 = 0, 1
 S8_MODES = {"fp32": S8_FP32, "comp_bf16": S8_COMP_BF16}
 
@@ -52,14 +52,14 @@ class StatsDesc(ctypes.Structure):
 class AdamwDesc(ctypes.Structure):
     _fields_ = [("param", c_void_p), ("grad", c_void_p), ("exp_avg", c_void_p),
                 ("exp_avg_sq", c_void_p), ("n", c_int64), ("offset", c_int64),
-                ("bias1", c_float), ("bias2", c_float), ("grad_dtype", c_int32), ("pad_", c_int32)]
+                ("bias1", c_float), ("bias2", c_float), ("grad_dtype", c_int32), ("param_dtype", c_int32)]
 
 
 class MatrixDesc(ctypes.Structure):
     _fields_ = [("param", c_void_p), ("grad", c_void_p), ("momentum", c_void_p),
                 ("inv_row", c_void_p), ("inv_col", c_void_p), ("z", c_void_p), ("kappa", c_void_p),
                 ("rows", c_int64), ("cols", c_int64), ("lr", c_double), ("momentum_beta", c_double),
-                ("grad_dtype", c_int32), ("pad_", c_int32)]
+                ("grad_dtype", c_int32), ("param_dtype", c_int32)]
 
 
 # name -> (restype, argtypes); every symbol include/sandmuon_amd.h declares.
@@ -85,9 +85,12 @@ SIGNATURES = {
     "smx_s8_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int]),
     "smx_s8": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int,
                        c_void_p, c_size_t, c_void_p]),
-    "smx_rank1_apply": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+    "smx_inverse_sqrt": (c_int, [c_int, c_int, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
+                                 c_void_p]),
+    "smx_rank1_apply": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                 c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "smx_graft": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p]),
+    "smx_s8_comp_stages": (c_int, [c_int32]),
     "smx_s8_timing": (c_int, [c_int32]),
     "smx_s8_timing_read": (c_int32, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(c_int32),
                                      ctypes.POINTER(c_double), c_int32]),
@@ -153,12 +156,29 @@ def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_streams = {}  # (raw stream, device index) -> torch stream object
+
+
+def torch_stream(stream: int, device: torch.device) -> torch.cuda.Stream:
+    """The torch stream object of a raw hipStream_t of `device`.  The null
+    handle is the default stream: torch.cuda.ExternalStream(0) would hand
+    out a new pool stream instead."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (stream, index)
+    s = _streams.get(key)
+    if s is None:
+        dev = torch.device("cuda", index)
+        s = torch.cuda.default_stream(dev) if stream == 0 else torch.cuda.ExternalStream(stream, device=dev)
+        _streams[key] = s
+    return s
+
+
 def stream_wait(waiter: int, signaler: int, device: torch.device) -> None:
     """Makes stream `waiter` wait for the work enqueued so far on stream
     `signaler` (raw hipStream_t values of `device`)."""
     done = torch.cuda.Event()
-    done.record(torch.cuda.ExternalStream(signaler, device=device))
-    torch.cuda.ExternalStream(waiter, device=device).wait_event(done)
+    done.record(torch_stream(signaler, device))
+    torch_stream(waiter, device).wait_event(done)
 
 
 def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -171,6 +191,15 @@ def stats_accumulate(rows2d: torch.Tensor, slots_sq: torch.Tensor, slots_first: 
                                     rows2d.shape[1], rows2d.stride(0), slots_sq.data_ptr(),
                                     ptr(slots_first), slots_sq.shape[0], stream_of(rows2d.device))
     _check(rc, "smx_stats_accumulate")
+    _record_use(rows2d, stream_of(rows2d.device))
+
+
+def _record_use(t: torch.Tensor, stream: int) -> None:
+    """Tells the caching allocator that `t` is read by work enqueued on
+    `stream` (a raw hipStream_t of t's device), which need not be the stream
+    t was allocated on: its memory is then not handed to another allocation
+    before that work has run."""
+    t.record_stream(torch_stream(stream, t.device))
 
 
 @functools.lru_cache(maxsize=256)
@@ -191,6 +220,8 @@ def stats_accumulate_batch(entries, stream: int) -> None:
         d.dtype, d.n_slots = dtype_code(rows2d.dtype), sq.shape[0]
     rc = lib().smx_stats_accumulate_batch(descs, len(entries), stream)
     _check(rc, "smx_stats_accumulate_batch")
+    for rows2d, _, _ in entries:
+        _record_use(rows2d, stream)
 
 
 def stats_cast(rows2d: torch.Tensor, slots_sq: torch.Tensor, slots_first: Optional[torch.Tensor],
@@ -288,13 +319,35 @@ def s8(x: torch.Tensor, out: torch.Tensor, mode: int) -> None:
     _check(rc, "smx_s8")
 
 
+_HELPER_DTYPES = {torch.float32: SMX_F32, torch.float64: SMX_F64}
+
+
+def helper_dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _HELPER_DTYPES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported helper dtype {dtype}; expected float32 or float64") from None
+
+
+def inverse_sqrt(kind: int, second: torch.Tensor, mean: Optional[torch.Tensor], inv: torch.Tensor,
+                 z: Optional[torch.Tensor], kappa: Optional[torch.Tensor]) -> None:
+    """kind 0: diagonal_inverse_sqrt of `second`; kind 1: rank1_inverse_sqrt
+    of (second, mean) into inv, z, kappa.  Contiguous 1-D tensors of one
+    dtype (float32 or float64) on the GPU."""
+    rc = lib().smx_inverse_sqrt(kind, helper_dtype_code(second.dtype), second.data_ptr(), ptr(mean),
+                                second.numel(), inv.data_ptr(), ptr(z), ptr(kappa), stream_of(second.device))
+    _check(rc, "smx_inverse_sqrt")
+
+
 def rank1_apply(x: torch.Tensor, out: torch.Tensor, left, right, order: int) -> None:
+    """x, out: contiguous [batch, rows, cols]; left/right: (inv, z, coef) of
+    shapes [batch, n], [batch, n], [batch], all of x's dtype."""
     b, r, c = x.shape
     li, lz, lc = left
     ri, rz, rc_ = right
-    work = torch.empty(max(b * (r + c), 1), dtype=torch.float32, device=x.device)
-    rc = lib().smx_rank1_apply(x.data_ptr(), out.data_ptr(), b, r, c, li.data_ptr(), lz.data_ptr(),
-                               lc.data_ptr(), ri.data_ptr(), rz.data_ptr(), rc_.data_ptr(), order,
+    work = torch.empty(max(b * (r + c), 1), dtype=torch.float64, device=x.device)
+    rc = lib().smx_rank1_apply(helper_dtype_code(x.dtype), x.data_ptr(), out.data_ptr(), b, r, c, li.data_ptr(),
+                               lz.data_ptr(), lc.data_ptr(), ri.data_ptr(), rz.data_ptr(), rc_.data_ptr(), order,
                                work.data_ptr(), stream_of(x.device))
     _check(rc, "smx_rank1_apply")
 
@@ -304,3 +357,11 @@ def graft(x: torch.Tensor, out: torch.Tensor, output_rows: int) -> None:
     rc = lib().smx_graft(x.data_ptr(), out.data_ptr(), x.numel(), output_rows, work.data_ptr(), 1024,
                          stream_of(x.device))
     _check(rc, "smx_graft")
+
+
+def s8_comp_stages(k: int) -> int:
+    """Sets how many S8 stages of the compensated-BF16 mode are compensated
+    (a measurement aid; 5 is the production recipe); returns the old value."""
+    prev = lib().smx_s8_comp_stages(int(k))
+    _check(min(prev, 0), "smx_s8_comp_stages")
+    return prev

@@ -3,6 +3,9 @@
 //   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2
 //   u = (m / bias1) / (sqrt(v / bias2) + eps)
 //   p = p (1 - lr wd);  p = p - lr u
+// A 16-bit parameter is rounded to its dtype after each of the two
+// parameter updates and u before the second, as the reference's in-place
+// mul_ and add_(u.to(p.dtype)) on that dtype do (:280-281).
 #include "common.h"
 
 #include <algorithm>
@@ -50,7 +53,7 @@ __global__ void __launch_bounds__(256) adamw_kernel(AdamPack pk) {
           else g[u] = load_elem<SMX_F16>(d.grad, i);
           m[u] = d.exp_avg[i];
           v[u] = d.exp_avg_sq[i];
-          p[u] = d.param[i];
+          p[u] = d.param_dtype == SMX_F32 ? static_cast<const float *>(d.param)[i] : load_any(d.param, d.param_dtype, i);
         }
       }
 #pragma unroll
@@ -62,7 +65,13 @@ __global__ void __launch_bounds__(256) adamw_kernel(AdamPack pk) {
           d.exp_avg[i] = mu;
           d.exp_avg_sq[i] = vu;
           const float step = (mu / d.bias1) / (sqrtf(vu / d.bias2) + pk.eps);
-          d.param[i] = p[u] * pk.decay + pk.neg_lr * step;
+          if (d.param_dtype == SMX_F32) {
+            static_cast<float *>(d.param)[i] = fmaf(pk.neg_lr, step, p[u] * pk.decay);
+          } else {
+            const int dt = d.param_dtype;
+            const float p1 = round_to(dt, p[u] * pk.decay);
+            store_any(d.param, dt, i, round_to(dt, fmaf(pk.neg_lr, round_to(dt, step), p1)));
+          }
         }
       }
     }
@@ -83,6 +92,8 @@ extern "C" int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t to
     SMX_REQUIRE(d.n >= 0 && d.offset == sum, SMX_ESHAPE, "adamw: offsets must be the prefix sums of n");
     SMX_REQUIRE(d.grad_dtype == SMX_F32 || d.grad_dtype == SMX_BF16 || d.grad_dtype == SMX_F16, SMX_EDTYPE,
                 "adamw: grad dtype must be f32, bf16 or f16");
+    SMX_REQUIRE(d.param_dtype == SMX_F32 || d.param_dtype == SMX_BF16 || d.param_dtype == SMX_F16, SMX_EDTYPE,
+                "adamw: param dtype must be f32, bf16 or f16");
     SMX_REQUIRE(d.bias1 > 0.f && d.bias2 > 0.f, SMX_EINVAL, "adamw: bias corrections must be positive");
     sum += d.n;
   }

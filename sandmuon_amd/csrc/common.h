@@ -52,6 +52,32 @@ __device__ __forceinline__ float load_elem(const void *p, int64_t i) {
   }
 }
 
+// A parameter element of dtype `dt` (SMX_F32, SMX_BF16 or SMX_F16).
+__device__ __forceinline__ float load_any(const void *p, int dt, int64_t i) {
+  if (dt == SMX_F32) return load_elem<SMX_F32>(p, i);
+  if (dt == SMX_BF16) return load_elem<SMX_BF16>(p, i);
+  return load_elem<SMX_F16>(p, i);
+}
+
+// v rounded to nearest even in dtype `dt` and widened back to FP32.
+__device__ __forceinline__ float round_to(int dt, float v) {
+  if (dt == SMX_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  if (dt == SMX_F16) return static_cast<float>(static_cast<_Float16>(v));
+  return v;
+}
+
+// Stores v (already representable in `dt`, see round_to) as dtype `dt`.
+__device__ __forceinline__ void store_any(void *p, int dt, int64_t i, float v) {
+  if (dt == SMX_F32) {
+    static_cast<float *>(p)[i] = v;
+  } else if (dt == SMX_BF16) {
+    static_cast<uint16_t *>(p)[i] = f32_to_bf16_bits(v);
+  } else {
+    const _Float16 h = static_cast<_Float16>(v);
+    static_cast<_Float16 *>(p)[i] = h;
+  }
+}
+
 // ---------------------------------------------------- wave reductions ---
 // Sum over the 64 lanes of a fully active wave, the same value in every
 // lane.  Within each row of 16 lanes four DPP moves (quad_perm [1,0,3,2],

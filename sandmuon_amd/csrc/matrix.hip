@@ -460,7 +460,8 @@ __global__ void __launch_bounds__(kMapThreads) mapback_rows_kernel(MatPack pack)
 // W -= lr * sqrt(rows) / max(||U||_F, FLT_MIN) * U over kPartRows rows
 // (one wave per row).  The first chunk of the row is loaded before the
 // norm is summed, so the block does not wait on two memory round trips in
-// a row.
+// a row.  A 16-bit parameter takes W = round(W - lr * round(direction))
+// (sandmuon/optimizer.py:315) on the per-element path.
 template <bool R1>
 __global__ void __launch_bounds__(kMapThreads) mapback_apply_kernel(MatPack pack) {
   __shared__ double bcast;
@@ -469,11 +470,13 @@ __global__ void __launch_bounds__(kMapThreads) mapback_apply_kernel(MatPack pack
   const int blk = blockIdx.x - J.blk0;
   constexpr bool r1 = R1;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool vec = d.cols % 4 == 0 && aligned16(d.param) && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
+  const int pdt = d.param_dtype;
+  const bool vec = pdt == SMX_F32 && d.cols % 4 == 0 && aligned16(d.param) && aligned16(d.inv_col) &&
+                   (!r1 || aligned16(d.z));
   const int64_t i = static_cast<int64_t>(blk) * kPartRows + wave;
   const bool live = i < d.rows;
   const float *q = live ? J.pl + i * J.pcol_pad : nullptr;
-  float *w = live ? d.param + i * d.cols : nullptr;
+  float *w = live && pdt == SMX_F32 ? static_cast<float *>(d.param) + i * d.cols : nullptr;
   const int64_t n4 = d.cols / 4;
   float4 qv[kRowUnroll], av[kRowUnroll], wv[kRowUnroll], zv[kRowUnroll];
   auto load = [&](int64_t k0) {
@@ -529,11 +532,12 @@ __global__ void __launch_bounds__(kMapThreads) mapback_apply_kernel(MatPack pack
       }
     }
   } else {
+    const int64_t row = i * d.cols;
     for (int64_t j = lane; j < d.cols; j += 64) {
       float v = q[j];
       if (r1) v = fmaf(ku, d.z[j], v);
-      const float U = (v * b) * d.inv_col[j];
-      w[j] = fmaf(nlr, U * scale, w[j]);
+      const float dir = round_to(pdt, ((v * b) * d.inv_col[j]) * scale);
+      store_any(d.param, pdt, row + j, round_to(pdt, fmaf(nlr, dir, load_any(d.param, pdt, row + j))));
     }
   }
 }
@@ -665,6 +669,8 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
     SMX_REQUIRE(d.rows >= 1 && d.cols >= 1, SMX_ESHAPE, "matrix_step: rows and cols must be >= 1");
     SMX_REQUIRE(d.grad_dtype == SMX_F32 || d.grad_dtype == SMX_BF16 || d.grad_dtype == SMX_F16, SMX_EDTYPE,
                 "matrix_step: grad dtype must be f32, bf16 or f16");
+    SMX_REQUIRE(d.param_dtype == SMX_F32 || d.param_dtype == SMX_BF16 || d.param_dtype == SMX_F16, SMX_EDTYPE,
+                "matrix_step: param dtype must be f32, bf16 or f16");
     rows[i] = d.rows;
     cols[i] = d.cols;
   }

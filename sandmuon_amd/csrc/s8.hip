@@ -26,7 +26,9 @@
 //                     v_mfma_f32_32x32x16_bf16 (the compensated product of
 //                     reproduction/odl/ops/bf16_compensated_mm_fast.py:
 //                     60-66, applied in all five stages with FP32
-//                     accumulation of every intermediate).
+//                     accumulation of every intermediate).  Stages past
+//                     smx_s8_comp_stages(k) (default 5, i.e. none) run as
+//                     kS8HiOnly: the same stored operands, acc += hi*hi.
 //
 // Block: 256x128 output tile, 4 waves (2 x 2, one per SIMD), each wave
 // 128x64 (4 x 2 MFMA 32x32 tiles, 128 accumulator registers), and two
@@ -49,6 +51,12 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum Phase { kGram = 0, kSquare = 1, kApply = 2, kPoly1 = 3, kSpan = 4 };  // kSpan: timing record of a whole S8 run
+
+// Internal MFMA mode of a plain BF16 stage of the compensated recipe: the
+// operands in their stored hi/lo form, only the hi*hi product issued.
+constexpr int kS8HiOnly = 2;
+// Stages 1..g_comp_stages of SMX_S8_COMP_BF16 are compensated.
+static int g_comp_stages = 5;
 
 constexpr int kThreads = 256;      // 4 waves, one per SIMD
 constexpr int kWaves = kThreads / 64;
@@ -239,6 +247,8 @@ template <>
 struct AFrag<SMX_S8_FP32> {
   float v[8];
 };
+template <>
+struct AFrag<kS8HiOnly> : AFrag<SMX_S8_COMP_BF16> {};
 template <int MODE>
 struct BFrags;
 template <>
@@ -249,6 +259,8 @@ template <>
 struct BFrags<SMX_S8_FP32> {
   float v[kSubN][8];
 };
+template <>
+struct BFrags<kS8HiOnly> : BFrags<SMX_S8_COMP_BF16> {};
 
 // LDS -> registers: A row block i, and the four B column blocks, of one
 // stage.  Lane (r, h) takes K = 8h .. 8h+7 of its row: chunks h (hi) and
@@ -258,9 +270,9 @@ __device__ __forceinline__ void load_a(const char *st, int wm, int i, AFrag<MODE
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
   const int r = wm * (32 * Geo<TM>::kSubM) + i * 32 + lr;
-  if constexpr (MODE == SMX_S8_COMP_BF16) {
+  if constexpr (MODE != SMX_S8_FP32) {
     f.h = read_b16(st, r, lh);
-    f.l = read_b16(st, r, 2 + lh);
+    if constexpr (MODE == SMX_S8_COMP_BF16) f.l = read_b16(st, r, 2 + lh);
   } else {
     read8(st, r, lh, f.v);
   }
@@ -274,9 +286,9 @@ __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) 
 #pragma unroll
   for (int j = 0; j < kSubN; ++j) {
     const int r = wn * (32 * kSubN) + j * 32 + lr;
-    if constexpr (MODE == SMX_S8_COMP_BF16) {
+    if constexpr (MODE != SMX_S8_FP32) {
       f.h[j] = read_b16(bt, r, lh);
-      f.l[j] = read_b16(bt, r, 2 + lh);
+      if constexpr (MODE == SMX_S8_COMP_BF16) f.l[j] = read_b16(bt, r, 2 + lh);
     } else {
       read8(bt, r, lh, f.v[j]);
     }
@@ -317,7 +329,7 @@ __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &
   constexpr int kOpA = Geo<TM>::kOpA;
   const int lane = threadIdx.x & 63;
   const char *bt = st + kOpA;
-  if constexpr (MODE == SMX_S8_COMP_BF16) {
+  if constexpr (MODE != SMX_S8_FP32) {
     // Four base addresses per stage; the empty asm keeps the compiler from
     // pre-adding every read's constant offset into a register of its own
     // (sixteen live registers and two VALU ops per read) instead of using
@@ -333,7 +345,7 @@ __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &
 #pragma unroll
     for (int j = 0; j < kSubN; ++j) {
 #pragma unroll
-      for (int pl = 0; pl < 2; ++pl) {
+      for (int pl = 0; pl < (MODE == SMX_S8_COMP_BF16 ? 2 : 1); ++pl) {
         lds_char *p = q[j & 1][pl] + (kOpA + ((8 * kSubN * wn + 16 * (j >> 1)) << 4));
         const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * kKmRow);
         const bf16x8 v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -372,6 +384,9 @@ __device__ __forceinline__ void mma_row(const AFrag<MODE> &a, const BFrags<MODE>
     for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.l, b.h[j], acc[j], 0, 0, 0);
 #pragma unroll
     for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.h[j], acc[j], 0, 0, 0);
+  } else if constexpr (MODE == kS8HiOnly) {
+#pragma unroll
+    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.h[j], acc[j], 0, 0, 0);
   } else {
     // Lane half h supplies k = 8h + q to MFMA q (the same permutation for
     // both operands, so every k is paired exactly once).
@@ -394,7 +409,7 @@ __device__ __forceinline__ AFrag<MODE> one_hot(float s, int r0) {
   const int lane = threadIdx.x & 63;
   const int e = (lane & 31) - r0 - 8 * (lane >> 5);  // position of k = row - R in this lane's 8
   AFrag<MODE> f;
-  if constexpr (MODE == SMX_S8_COMP_BF16) {
+  if constexpr (MODE != SMX_S8_FP32) {
     const __bf16 sh = static_cast<__bf16>(s);
     const __bf16 sl = static_cast<__bf16>(s - static_cast<float>(sh));
     const __bf16 z = static_cast<__bf16>(0.f);
@@ -661,7 +676,7 @@ s8_stage_kernel(StageArgs args) {
   __shared__ __attribute__((aligned(16))) char smem[Gm::kRingBytes];
   __shared__ double dscratch[16];
   __shared__ double bcast;
-  constexpr bool PL = MODE == SMX_S8_COMP_BF16;  // operands stored as interleaved BF16
+  constexpr bool PL = MODE != SMX_S8_FP32;  // operands stored as interleaved BF16
 
   const TileRef ref = tile_of(args);
   const S8Class &K = *ref.k;
@@ -937,13 +952,20 @@ static int timing_end(int slot, hipStream_t st, int phase, double flops) {
   return SMX_OK;
 }
 
-// MFMA FLOPs of one launch: computed tiles x 2 * TM * 128 * K (x3 in
-// compensated mode), plus the square phase's one-hot MFMAs (2 kSubM stages
+// The MFMA mode of a stage: FP32, compensated, or (compensated recipe,
+// stages past g_comp_stages) hi*hi only.
+static int stage_mode(const S8Layout &Lay, int stage) {
+  if (Lay.mode != SMX_S8_COMP_BF16) return SMX_S8_FP32;
+  return stage <= g_comp_stages ? SMX_S8_COMP_BF16 : kS8HiOnly;
+}
+
+// MFMA FLOPs of one launch: computed tiles x 2 * TM * 128 * K (x3 for a
+// compensated stage), plus the square phase's one-hot MFMAs (2 kSubM stages
 // of kSubN 32x32x16 products per wave).
 template <int PHASE>
 static double launch_flops(const S8Layout &Lay, int stage, bool sq_small) {
   if (PHASE == kPoly1) return 0.0;
-  const double prod = Lay.mode == SMX_S8_COMP_BF16 ? 3.0 : 1.0;
+  const double prod = stage_mode(Lay, stage) == SMX_S8_COMP_BF16 ? 3.0 : 1.0;
   const int tm = PHASE == kSquare && sq_small ? kSymTile : kTile;
   const int sub_m = tm / 64;
   double f = 0.0;
@@ -979,6 +1001,19 @@ static bool square_small(const S8Layout &Lay, hipStream_t st) {
   return 0.9 * r_small < r_big;
 }
 
+// One phase launch of a stage kernel (the square on 128 x 128 tiles when
+// sq_small).
+template <int MODE, int PHASE>
+static void launch_stage(bool sq_small, int32_t blocks, const StageArgs &a, hipStream_t st) {
+  if constexpr (PHASE == kSquare) {
+    if (sq_small) {
+      hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, kSymTile>), dim3(blocks), dim3(kThreads), 0, st, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, kTile>), dim3(blocks), dim3(kThreads), 0, st, a);
+}
+
 template <int PHASE>
 static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, hipStream_t st) {
   StageArgs a{};
@@ -1012,31 +1047,20 @@ static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, hipStream
   }
   a.seg_off[a.n_seg] = off;
   if (off == 0) return SMX_OK;
-  const bool comp = Lay.mode == SMX_S8_COMP_BF16;
+  const int mode = stage_mode(Lay, stage);
   int slot = -1;
   int rc = timing_begin(st, slot, false);
   if (rc) return rc;
   if constexpr (PHASE == kPoly1) {
-    if (comp)
+    if (mode != SMX_S8_FP32)
       hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_COMP_BF16>, dim3(off), dim3(256), 0, st, a);
     else
       hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_FP32>, dim3(off), dim3(256), 0, st, a);
     rc = check_launch("s8 stage-1 polynomial");
   } else {
-    if constexpr (PHASE == kSquare) {
-      if (sq_small) {
-        if (comp)
-          hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_COMP_BF16, PHASE, kSymTile>), dim3(off), dim3(kThreads), 0, st, a);
-        else
-          hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_FP32, PHASE, kSymTile>), dim3(off), dim3(kThreads), 0, st, a);
-      }
-    }
-    if (PHASE != kSquare || !sq_small) {
-      if (comp)
-        hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_COMP_BF16, PHASE, kTile>), dim3(off), dim3(kThreads), 0, st, a);
-      else
-        hipLaunchKernelGGL((s8_stage_kernel<SMX_S8_FP32, PHASE, kTile>), dim3(off), dim3(kThreads), 0, st, a);
-    }
+    if (mode == SMX_S8_COMP_BF16) launch_stage<SMX_S8_COMP_BF16, PHASE>(sq_small, off, a, st);
+    else if (mode == kS8HiOnly) launch_stage<kS8HiOnly, PHASE>(sq_small, off, a, st);
+    else launch_stage<SMX_S8_FP32, PHASE>(sq_small, off, a, st);
     rc = check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : "s8 apply");
   }
   if (rc) return rc;
@@ -1130,6 +1154,13 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
 }  // namespace smx
 
 using smx::g_timing;
+
+extern "C" int smx_s8_comp_stages(int32_t k) {
+  SMX_REQUIRE(k >= 0 && k <= 5, SMX_EINVAL, "s8 compensated stages: k must be in [0, 5]");
+  const int prev = smx::g_comp_stages;
+  smx::g_comp_stages = k;
+  return prev;
+}
 
 extern "C" int smx_s8_timing(int32_t enable) {
   SMX_REQUIRE(enable >= 0 && enable <= 2, SMX_EINVAL, "s8 timing: enable must be 0, 1 or 2");

@@ -45,73 +45,70 @@ _KIND_DIAG_A, _KIND_RANK1_A, _KIND_B = 0, 1, 2
 
 
 # --------------------------------------------------------------- helpers ---
-def _to_gpu_f32(t: torch.Tensor) -> torch.Tensor:
+# The module-level helpers run in float64 when their input is float64 and
+# in float32 otherwise, as the reference computes them in the input dtype;
+# _graft_direction and _s8_fp32 work in float32, as the reference's do.
+def _to_gpu(t, dtype: torch.dtype) -> torch.Tensor:
+    t = torch.as_tensor(t)
     if t.device.type != "cuda":
         if not torch.cuda.is_available():
             raise RuntimeError("sandmuon_amd needs a ROCm GPU; none is available")
         t = t.to(torch.device("cuda", torch.cuda.current_device()))
-    return t.to(torch.float32).contiguous()
+    return t.to(dtype).contiguous()
 
 
-def _finish_vector(kind: int, second: torch.Tensor, first: Optional[torch.Tensor]):
-    """Runs the batched finish kernel on one vector with count 1 (EMA copy)."""
-    dev = second.device
-    n = second.numel()
-    sum_sq = second.clone()
-    slots_sq = torch.zeros(1, n, dtype=torch.float32, device=dev)
-    ema = torch.empty(n, dtype=torch.float32, device=dev)
-    inv = torch.empty(n, dtype=torch.float32, device=dev)
-    d = _native.FinishDesc(sum_sq=sum_sq.data_ptr(), slots_sq=slots_sq.data_ptr(), ema=ema.data_ptr(),
-                           inv=inv.data_ptr(), n=n, count=1, n_slots=1, kind=kind, first=1)
-    z = kappa = None
-    if kind == _KIND_RANK1_A:
-        sum_first = first.clone()
-        slots_first = torch.zeros(1, n, dtype=torch.float32, device=dev)
-        mean_ema = torch.empty(n, dtype=torch.float32, device=dev)
-        z = torch.empty(n, dtype=torch.float32, device=dev)
-        kappa = torch.empty(1, dtype=torch.float32, device=dev)
-        d.sum_first, d.slots_first = sum_first.data_ptr(), slots_first.data_ptr()
-        d.mean_ema, d.z, d.kappa = mean_ema.data_ptr(), z.data_ptr(), kappa.data_ptr()
-    _native.stats_finish([d], 1.0, dev)
-    return inv, z, kappa
+def _to_gpu_f32(t) -> torch.Tensor:
+    return _to_gpu(t, torch.float32)
+
+
+def _work_dtype(*tensors) -> torch.dtype:
+    """float64 if any input is float64, else float32."""
+    return torch.float64 if any(torch.as_tensor(t).dtype == torch.float64 for t in tensors) else torch.float32
 
 
 def diagonal_inverse_sqrt(value: torch.Tensor) -> torch.Tensor:
     """Mean-normalised diagonal inverse square root (sandmuon/optimizer.py:19-24)."""
-    v = _to_gpu_f32(value).reshape(-1)
+    dt = _work_dtype(value)
+    v = _to_gpu(value, dt).reshape(-1)
     if v.numel() == 0:
         return value.new_empty(value.shape)
-    inv, _, _ = _finish_vector(_KIND_DIAG_A, v, None)
+    inv = torch.empty_like(v)
+    _native.inverse_sqrt(0, v, None, inv, None, None)
     return inv.reshape(value.shape).to(value.device, value.dtype)
 
 
 def rank1_inverse_sqrt(second: torch.Tensor, mean: torch.Tensor):
     """D^-1/2 and the Sherman-Morrison rank-one (z, kappa) (sandmuon/optimizer.py:27-35)."""
-    s = _to_gpu_f32(second).reshape(-1)
-    m = _to_gpu_f32(mean).reshape(-1)
-    inv, z, kappa = _finish_vector(_KIND_RANK1_A, s, m)
-    out = lambda t: t.to(second.device, second.dtype)
-    return out(inv), out(z), out(kappa.reshape(()))
+    dt = _work_dtype(second, mean)
+    s = _to_gpu(second, dt).reshape(-1)
+    m = _to_gpu(mean, dt).reshape(-1)
+    inv, z = torch.empty_like(s), torch.empty_like(s)
+    kappa = torch.empty((), dtype=dt, device=s.device)
+    _native.inverse_sqrt(1, s, m, inv, z, kappa)
+    out_dtype = torch.promote_types(second.dtype, mean.dtype)
+    out = lambda t: t.to(second.device, out_dtype)
+    return out(inv), out(z), out(kappa)
 
 
-def _batched_factor(f, batch_shape, n, device):
-    vec = _to_gpu_f32(f[0]).expand(*batch_shape, n).reshape(-1, n).contiguous()
-    z = _to_gpu_f32(f[1]).expand(*batch_shape, n).reshape(-1, n).contiguous()
-    c = _to_gpu_f32(torch.as_tensor(f[2])).expand(*batch_shape).reshape(-1).contiguous()
-    return vec.to(device), z.to(device), c.to(device)
+def _batched_factor(f, batch_shape, n, dt):
+    vec = _to_gpu(f[0], dt).expand(*batch_shape, n).reshape(-1, n).contiguous()
+    z = _to_gpu(f[1], dt).expand(*batch_shape, n).reshape(-1, n).contiguous()
+    c = _to_gpu(f[2], dt).expand(torch.Size(batch_shape)).reshape(-1).contiguous()
+    return vec, z, c
 
 
 def _rank1(matrix: torch.Tensor, left, right, order: int) -> torch.Tensor:
-    x = _to_gpu_f32(matrix)
+    dt = _work_dtype(matrix, *left, *right)
+    x = _to_gpu(matrix, dt)
     r, c = x.shape[-2], x.shape[-1]
     batch_shape = x.shape[:-2]
     xb = x.reshape(-1, r, c)
     out = torch.empty_like(xb)
-    lf = _batched_factor(left, batch_shape, r, x.device)
-    rf = _batched_factor(right, batch_shape, c, x.device)
+    lf = _batched_factor(left, batch_shape, r, dt)
+    rf = _batched_factor(right, batch_shape, c, dt)
     _native.rank1_apply(xb, out, lf, rf, order)
     res = out.reshape(x.shape)
-    return res.to(matrix.device, torch.promote_types(matrix.dtype, torch.float32))
+    return res.to(matrix.device, torch.promote_types(matrix.dtype, dt))
 
 
 def rank1_whiten(matrix: torch.Tensor, left, right) -> torch.Tensor:
@@ -125,7 +122,7 @@ def rank1_mapback(value: torch.Tensor, left, right) -> torch.Tensor:
 
 
 def _graft_direction(value: torch.Tensor, output_rows: int) -> torch.Tensor:
-    """Frobenius graft to sqrt(output_rows) (sandmuon/optimizer.py:63-66)."""
+    """Frobenius graft to sqrt(output_rows) in float32 (sandmuon/optimizer.py:63-66)."""
     v = _to_gpu_f32(value)
     out = torch.empty_like(v)
     _native.graft(v, out, int(output_rows))
@@ -140,6 +137,42 @@ def _s8_fp32(x: torch.Tensor, mode: str = "fp32") -> torch.Tensor:
     out = torch.empty_like(vb)
     _native.s8(vb, out, _native.S8_MODES[mode])
     return (out.reshape(v.shape) * S8_MULTIPLIER).to(x.device)
+
+
+_PARAM_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _dense(t: torch.Tensor) -> bool:
+    """Whether t's elements fill its storage span without gaps or overlap
+    (any dimension order), so that an elementwise kernel can walk it flat."""
+    if t.is_contiguous():
+        return True
+    dims = sorted((st, n) for st, n in zip(t.stride(), t.shape) if n != 1)
+    expect = 1
+    for st, n in dims:
+        if st != expect:
+            return False
+        expect *= n
+    return True
+
+
+def _check_layout(parameter: torch.Tensor, name: str, matrix: bool) -> None:
+    """Matrix kernels read parameters as row-major [rows, cols]; the
+    elementwise AdamW kernel walks any gap-free layout."""
+    if matrix and not parameter.is_contiguous():
+        raise ValueError(f"sandmuon_amd needs row-major contiguous matrix parameters; {name} has strides "
+                         f"{tuple(parameter.stride())} (call .contiguous() on it before building the optimizer)")
+    if not matrix and not _dense(parameter):
+        raise ValueError(f"sandmuon_amd needs parameters without gaps or overlap; {name} has strides "
+                         f"{tuple(parameter.stride())}")
+
+
+def _like(t: torch.Tensor, parameter: torch.Tensor, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """t (same shape as `parameter`) with the parameter's strides: as it is
+    when they already match, else copied into the parameter's layout."""
+    if t.stride() == parameter.stride() and (dtype is None or t.dtype == dtype):
+        return t
+    return torch.empty_like(parameter, dtype=dtype or t.dtype).copy_(t)
 
 
 def select_matrices(model: nn.Module, module_filter=None):
@@ -255,12 +288,14 @@ class DiagonalWeightedPE(Optimizer):
 
         matrix_ids = {id(p) for p in matrices.values()}
         auxiliary = [p for p in model.parameters() if p.requires_grad and id(p) not in matrix_ids]
+        matrix_names = {id(p): name for name, p in matrices.items()}
         for p in list(matrices.values()) + auxiliary:
             if p.device.type != "cuda":
                 raise RuntimeError("sandmuon_amd runs on ROCm GPU parameters only; move the model to the GPU "
                                    f"before constructing the optimizer (got {p.device})")
-            if p.dtype != torch.float32:
-                raise TypeError(f"sandmuon_amd expects float32 parameters (got {p.dtype})")
+            if p.dtype not in _PARAM_DTYPES:
+                raise TypeError(f"sandmuon_amd expects float32, bfloat16 or float16 parameters (got {p.dtype})")
+            _check_layout(p, matrix_names.get(id(p), "an auxiliary parameter"), id(p) in matrix_names)
         defaults = dict(lr=float(lr), use_muon=True, momentum=.8, weight_decay=0.,
                         adamw_lr_ratio=.1, adamw_betas=(.9, .999), adamw_eps=1e-8)
         groups = [dict(params=list(matrices.values()), use_muon=True)]
@@ -530,22 +565,30 @@ class DiagonalWeightedPE(Optimizer):
         for parameter, _, _ in items:
             self.state[parameter]["b_count"] = 0
 
-        mdescs, shapes = [], []
+        # Converted or re-laid-out gradients are temporaries: they must stay
+        # alive until the launch that reads them is enqueued (the allocator
+        # would hand a freed one to the next temporary of this loop).
+        mdescs, shapes, keep = [], [], []
         for parameter, source, group in items:
             state = self.state[parameter]
+            _check_layout(parameter, self.parameter_names[id(parameter)], True)
             if "momentum_buffer" not in state:
                 state["momentum_buffer"] = torch.zeros_like(parameter, dtype=torch.float32)
+            elif not state["momentum_buffer"].is_contiguous() or state["momentum_buffer"].dtype != torch.float32:
+                state["momentum_buffer"] = state["momentum_buffer"].to(torch.float32).contiguous()
             grad = parameter.grad
-            if grad.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            if grad.dtype not in _PARAM_DTYPES:
                 grad = grad.float()
             grad = grad.contiguous()
+            keep.append(grad)
             a = a_out[id(source)]
             md = _native.MatrixDesc(param=parameter.data_ptr(), grad=grad.data_ptr(),
                                     momentum=state["momentum_buffer"].data_ptr(),
                                     inv_row=b_out[id(parameter)]["inv"].data_ptr(), inv_col=a["inv"].data_ptr(),
                                     rows=parameter.shape[0], cols=parameter.shape[1], lr=float(group["lr"]),
                                     momentum_beta=self._momentum(group),
-                                    grad_dtype=_native.dtype_code(grad.dtype))
+                                    grad_dtype=_native.dtype_code(grad.dtype),
+                                    param_dtype=_native.dtype_code(parameter.dtype))
             if self.rank_one_a:
                 md.z, md.kappa = a["z"].data_ptr(), a["kappa"].data_ptr()
             mdescs.append(md)
@@ -556,6 +599,7 @@ class DiagonalWeightedPE(Optimizer):
             self._workspace = None
             self._workspace = torch.empty(need, dtype=torch.uint8, device=device)
         _native.matrix_step(mdescs, mode, self._workspace)
+        del keep
 
     def _auxiliary_update(self, items) -> None:
         by_group: Dict[int, list] = {}
@@ -564,28 +608,35 @@ class DiagonalWeightedPE(Optimizer):
         for entries in by_group.values():
             group = entries[0][1]
             b1, b2 = group["adamw_betas"]
-            descs, offset = [], 0
+            descs, offset, keep = [], 0, []
             device = entries[0][0].device
             for parameter, _ in entries:
                 state = self.state[parameter]
+                # The kernel walks parameter, gradient and state flat, so all
+                # of them take the parameter's layout.
+                _check_layout(parameter, "an auxiliary parameter", False)
                 if "exp_avg" not in state:
                     state["exp_avg"] = torch.zeros_like(parameter, dtype=torch.float32)
                     state["exp_avg_sq"] = torch.zeros_like(parameter, dtype=torch.float32)
                     state["step"] = 0
+                for key in ("exp_avg", "exp_avg_sq"):
+                    state[key] = _like(state[key], parameter, torch.float32)
                 state["step"] = int(state["step"]) + 1
                 grad = parameter.grad
-                if grad.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                if grad.dtype not in _PARAM_DTYPES:
                     grad = grad.float()
-                grad = grad.contiguous()
+                grad = _like(grad, parameter)
+                keep.append(grad)  # alive until the launch below is enqueued
                 n = parameter.numel()
                 descs.append(_native.AdamwDesc(
                     param=parameter.data_ptr(), grad=grad.data_ptr(), exp_avg=state["exp_avg"].data_ptr(),
                     exp_avg_sq=state["exp_avg_sq"].data_ptr(), n=n, offset=offset,
                     bias1=1 - b1 ** state["step"], bias2=1 - b2 ** state["step"],
-                    grad_dtype=_native.dtype_code(grad.dtype)))
+                    grad_dtype=_native.dtype_code(grad.dtype), param_dtype=_native.dtype_code(parameter.dtype)))
                 offset += n
             lr = group["lr"] * group["adamw_lr_ratio"]
             _native.adamw(descs, offset, lr, b1, b2, group["adamw_eps"], group["weight_decay"], device)
+            del keep
 
     def close(self):
         self._flush_stats()

@@ -113,9 +113,35 @@ def test_validation_errors_return_before_gpu_work():
                                 ctypes.c_void_p(256), need - 1, None) == -5
     assert lib.smx_stats_colsum(ctypes.c_void_p(16), 1, 4, 768, 768, ctypes.c_void_p(16), 128, ctypes.c_void_p(16),
                                 ctypes.c_void_p(16), need, None) == -4
-    # adamw: offsets must be prefix sums
+    # adamw: offsets must be prefix sums; the parameter dtype must be known
     a = _native.AdamwDesc(param=16, grad=16, exp_avg=16, exp_avg_sq=16, n=4, offset=3, bias1=.1, bias2=.1)
     assert lib.smx_adamw((_native.AdamwDesc * 1)(a), 1, 4, 1e-3, .9, .999, 1e-8, .01, None) == -2
+    a.offset, a.param_dtype = 0, 3
+    assert lib.smx_adamw((_native.AdamwDesc * 1)(a), 1, 4, 1e-3, .9, .999, 1e-8, .01, None) == -3
+    # matrix step: f64 parameters are not a step dtype
+    d = _native.MatrixDesc(param=16, grad=16, momentum=16, inv_row=16, inv_col=16, rows=64, cols=32,
+                           lr=1e-3, momentum_beta=.8, grad_dtype=0, param_dtype=3)
+    assert lib.smx_matrix_step((_native.MatrixDesc * 1)(d), 1, 1, ctypes.c_void_p(256), 1 << 40, None) == -3
+    assert b"param dtype" in lib.smx_last_error()
+    # helpers: kind, dtype and the rank-one pointers are checked
+    v = ctypes.c_void_p(16)
+    assert lib.smx_inverse_sqrt(2, 0, v, v, 4, v, v, v, None) == -1
+    assert lib.smx_inverse_sqrt(0, 1, v, None, 4, v, None, None, None) == -3
+    assert lib.smx_inverse_sqrt(1, 3, v, None, 4, v, None, None, None) == -1
+    assert lib.smx_inverse_sqrt(0, 0, v, None, 0, v, None, None, None) == -2
+    assert lib.smx_rank1_apply(2, v, ctypes.c_void_p(32), 1, 4, 4, v, v, v, v, v, v, 0, v, None) == -3
+    assert lib.smx_rank1_apply(3, v, v, 1, 4, 4, v, v, v, v, v, v, 0, v, None) == -1  # out aliases x
+    assert lib.smx_rank1_apply(0, v, ctypes.c_void_p(32), 0, 4, 4, v, v, v, v, v, v, 1, v, None) == 0
+
+
+def test_compensated_stage_count_setting():
+    lib = _native.lib()
+    assert lib.smx_s8_comp_stages(7) == -1 and lib.smx_s8_comp_stages(-1) == -1
+    assert lib.smx_s8_comp_stages(3) == 5   # the production default is unchanged by the rejected calls
+    assert _native.s8_comp_stages(5) == 3
+    with pytest.raises(ValueError):
+        _native.s8_comp_stages(6)
+    assert lib.smx_s8_comp_stages(5) == 5
 
 
 def test_stats_slot_rows():

@@ -73,13 +73,17 @@ class Pair:
         assert list(self.opt.named_matrices) == list(self.ora.matrices)
         self.cap = Capture(self.gpu_model, self.opt.named_matrices)
 
-    def step(self, batches, loss_fn):
+    def step(self, batches, loss_fn, prepare=None):
+        """One step on both sides; `prepare(gpu_model)` may rewrite the GPU
+        gradients (same values) after the backward passes."""
         opt, ora, device = self.opt, self.ora, self.device
         gparams = dict(self.gpu_model.named_parameters())
         cparams = dict(self.cpu_model.named_parameters())
         opt.zero_grad(set_to_none=True)
         for x, y in batches:
             loss_fn(self.gpu_model, x.to(device), y.to(device)).backward()
+        if prepare is not None:
+            prepare(self.gpu_model)
         for name, kind, t in self.cap.drain():
             ora.feed(name, x=t if kind == "a" else None, delta=t if kind == "b" else None)
         with torch.no_grad():

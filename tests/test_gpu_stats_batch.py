@@ -158,3 +158,58 @@ def test_in_place_change_of_a_queued_input_raises(device):
     with pytest.raises(RuntimeError, match="modified in place"):
         opt.step()
     assert not opt._queue.entries
+
+
+def test_hook_input_from_another_stream_is_kept_until_its_launch(device):
+    """A hook input allocated on another stream and dropped right after its
+    hook.  The queued launch runs later, on the hook's stream (kept busy
+    here by a bounded sleep kernel); the allocator must not hand the input's
+    memory to a new allocation on its own stream before then, so the launch
+    records its use of every input on its stream."""
+    torch.manual_seed(5)
+    model = nn.Sequential(nn.Linear(256, 64)).to(device)
+    opt = DiagonalWeightedPE(model, 1e-2)
+    p = model[0].weight
+    side = torch.cuda.Stream(device)  # default priority
+    cur = torch.cuda.current_stream(device)
+    rows, cols = 8192, 256
+    with torch.cuda.stream(side):
+        x = torch.randn(rows, cols, device=device)
+    cur.wait_stream(side)
+    want = x.double().square().sum(0)
+    torch.cuda._sleep(50_000_000)
+    opt._accumulate_a(p, x)
+    opt._flush_stats()
+    del x
+    with torch.cuda.stream(side):
+        junk = torch.full((rows, cols), 1e3, device=device)
+    torch.cuda.synchronize()
+    _, sq, _ = opt._slots[(id(p), "a")]
+    got = sq.double().sum(0)
+    assert ((got - want).norm() / want.norm()).item() <= 1e-6
+    del junk
+    opt.close()
+
+
+def test_queue_launched_on_the_hook_stream_orders_the_current_stream(device):
+    """Hooks run on a side stream (kept busy by a bounded sleep kernel); the
+    queue is launched from the default stream, on the hooks' stream, and the
+    default stream must wait for that launch before it reads the slot rows."""
+    torch.manual_seed(6)
+    model = nn.Sequential(nn.Linear(256, 64)).to(device)
+    opt = DiagonalWeightedPE(model, 1e-2)
+    p = model[0].weight
+    x = torch.randn(8192, 256, device=device)
+    want = x.double().square().sum(0)
+    side = torch.cuda.Stream(device)  # default priority
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        torch.cuda._sleep(50_000_000)
+        opt._accumulate_a(p, x)
+    x.record_stream(side)
+    opt._flush_stats()  # from the default stream
+    _, sq, _ = opt._slots[(id(p), "a")]
+    got = sq.double().sum(0)  # enqueued on the default stream
+    torch.cuda.synchronize()
+    assert ((got - want).norm() / want.norm()).item() <= 1e-6
+    opt.close()

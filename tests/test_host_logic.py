@@ -88,3 +88,21 @@ def test_constructor_errors():
 
 def test_public_exports():
     assert S8_MARGIN == 1.35 and S8_MULTIPLIER == 1.0 and len(S8_COEFFICIENTS) == 5
+
+
+def test_helper_factor_batching(monkeypatch):
+    # The module-level rank-one helpers take factors with or without batch
+    # dimensions and a 0-dim or batched coefficient (rank1_mapback is called
+    # on 2-D values, tests/test_optimizer.py:46-54).
+    from sandmuon_amd import optimizer as M
+    monkeypatch.setattr(M, "_to_gpu", lambda t, dtype: torch.as_tensor(t).to(dtype).contiguous())
+    vec, z, c = torch.rand(5), torch.rand(5), torch.tensor(-.4)
+    for batch_shape in (torch.Size([]), torch.Size([3]), torch.Size([2, 3])):
+        bv, bz, bc = M._batched_factor((vec, z, c), batch_shape, 5, torch.float64)
+        n = max(1, batch_shape.numel())
+        assert bv.shape == bz.shape == (n, 5) and bc.shape == (n,) and bc.dtype == torch.float64
+    batched = (vec.expand(3, 5), z.expand(3, 5), c.expand(3))
+    bv, _, bc = M._batched_factor(batched, torch.Size([3]), 5, torch.float32)
+    assert bv.shape == (3, 5) and bc.shape == (3,)
+    assert M._work_dtype(torch.zeros(2), torch.zeros(2, dtype=torch.float64)) == torch.float64
+    assert M._work_dtype(torch.zeros(2, dtype=torch.bfloat16)) == torch.float32
