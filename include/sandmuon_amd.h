@@ -237,6 +237,19 @@ size_t smx_matrix_step_workspace_bytes(const int64_t *rows,
 int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode,
                     void *workspace, size_t workspace_bytes, void *stream);
 
+/* smx_matrix_step_static: smx_matrix_step with its workspace in a static
+ * device array of SMX_MATRIX_STEP_STATIC_BYTES instead of a caller buffer.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  It allocates nothing; the array is
+ * placed on a GPU by the first call there and held until the process ends.
+ * Matrices whose workspace (smx_matrix_step_workspace_bytes) exceeds the
+ * array are refused with SMX_EWORKSPACE before any launch.  Every call on
+ * one GPU uses that GPU's one array: calls that overlap on one GPU race. */
+#define SMX_MATRIX_STEP_STATIC_BYTES ((size_t)1 << 30)
+int smx_matrix_step_static(const smx_matrix_desc *descs, int32_t n, int mode,
+                           void *stream);
+
 /* ------------------------------------------------------------------ *
  * Stand-alone S8 polar map on a batch: _s8_fp32, sandmuon/optimizer.py:
  * 69-93.  x and out are [batch, rows, cols] fp32 with the given strides

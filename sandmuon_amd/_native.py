@@ -82,6 +82,7 @@ SIGNATURES = {
     "smx_matrix_step_workspace_bytes": (c_size_t, [ctypes.POINTER(c_int64), ctypes.POINTER(c_int64),
                                                    c_int32, c_int]),
     "smx_matrix_step": (c_int, [ctypes.POINTER(MatrixDesc), c_int32, c_int, c_void_p, c_size_t, c_void_p]),
+    "smx_matrix_step_static": (c_int, [ctypes.POINTER(MatrixDesc), c_int32, c_int, c_void_p]),
     "smx_s8_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int]),
     "smx_s8": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int,
                        c_void_p, c_size_t, c_void_p]),
