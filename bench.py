@@ -183,40 +183,77 @@ def committed_traffic():
 
 
 # -------------------------------------------------------- CPU baseline ---
+def _median_of_3(fn):
+    """One warm-up call, then three timed calls: (median, min, max) seconds."""
+    fn()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[1], times[0], times[2]
+
+
 def cpu_baseline(cfg_name, threads):
-    """The CPU oracle (eager FP32 restatement of the reference) on a bounded
-    sample of the same workload, scaled to one step."""
+    """The CPU oracle (the eager FP32 restatement of the reference) timed on
+    this host's cores: step() on a deep copy of a pre-filled state (one
+    microbatch of statistics and synthetic gradients for every matrix), and
+    the hook bodies on one full microbatch of every hooked class (shape,
+    dtype, side), each with one warm-up and the median of three, scaled by
+    the number of such calls per step."""
+    import copy
     from oracle import sandmuon_oracle as O
     from sandmuon_amd.workloads import GPT, GPT_103M, GPT_2048, transformer_filter
     torch.set_num_threads(threads)
     cfg = GPT_103M if cfg_name == "gpt103m" else GPT_2048
-    micro, mb_rows = (8, 16 * 1024) if cfg_name == "gpt103m" else (4, 8 * 1024)
-    sample_rows = 2048
+    micro, rows = (8, 16 * 1024) if cfg_name == "gpt103m" else (4, 8 * 1024)
     model = GPT(cfg)
     model.init_weights(1337)
     ora = O.OracleOptimizer(model, 1e-2, rank_one_a=True, module_filter=transformer_filter, hooks=False)
     g = torch.Generator().manual_seed(7)
     for p in model.parameters():
         p.grad = torch.randn(p.shape, generator=g) * 1e-3
-    # Hooks: one microbatch sample of `sample_rows` rows per hooked tensor.
-    t_hooks = 0.0
+    w, m = cfg.width, cfg.mlp
+    # Hook classes of one transformer block under bf16 autocast: A (sum x^2
+    # and sum x) of the LayerNorm-fed q and c_fc inputs in fp32 and of the
+    # attention and GELU outputs in bf16; B (sum d^2) of the six cotangents.
+    classes = {("a", w, torch.float32): 2, ("a", w, torch.bfloat16): 1, ("a", m, torch.bfloat16): 1,
+               ("b", w, torch.bfloat16): 5, ("b", m, torch.bfloat16): 1}
+    per_step = {"median": 0.0, "min": 0.0, "max": 0.0}
+    for (side, width, dtype), calls in classes.items():
+        x = torch.randn(rows, width, generator=g).to(dtype)
+        sq = torch.zeros(width)
+        first = torch.zeros(width) if side == "a" else None
+        med, lo, hi = _median_of_3(lambda: O.accumulate_rows(x, sq, first))
+        n = calls * cfg.layers * micro
+        per_step["median"] += med * n
+        per_step["min"] += lo * n
+        per_step["max"] += hi * n
+    # step(): statistics of one microbatch per matrix so that every factor
+    # is defined; the state is deep-copied before each timed call.
     for name, p in ora.matrices.items():
         own = ora.a_source[id(p)] is p
-        x = torch.randn(sample_rows, p.shape[1], generator=g)
-        if "c_proj" in name:
-            x = x.bfloat16()
-        d = torch.randn(sample_rows, p.shape[0], generator=g).bfloat16()
-        t0 = time.perf_counter()
-        ora.feed(name, x=x if own else None, delta=d)
-        t_hooks += time.perf_counter() - t0
-    hooks_per_step = t_hooks * (mb_rows / sample_rows) * micro
-    t0 = time.perf_counter()
-    ora.step()
-    t_step = time.perf_counter() - t0
-    sample = (f"hook statistics on {sample_rows} rows of every hooked tensor (scaled x{mb_rows // sample_rows * micro} "
-              f"to {micro} microbatches of {mb_rows} rows) + one full oracle step() on all {len(ora.matrices)} "
-              f"matrices and the AdamW parameters")
-    return (hooks_per_step + t_step) * 1e3, hooks_per_step * 1e3, t_step * 1e3, sample
+        ora.feed(name, x=torch.randn(256, p.shape[1], generator=g) if own else None,
+                 delta=torch.randn(256, p.shape[0], generator=g))
+    filled = copy.deepcopy(ora.state)
+    params = {id(p): p.detach().clone() for p in model.parameters()}
+
+    def step_once():
+        ora.state = copy.deepcopy(filled)
+        with torch.no_grad():
+            for p in model.parameters():
+                p.copy_(params[id(p)])
+        ora.step()
+
+    step_med, step_lo, step_hi = _median_of_3(step_once)
+    sample = (f"oracle step() on all {len(ora.matrices)} matrices and the AdamW parameters (1 warm-up, median of 3, "
+              f"state deep-copied per call) + the hook bodies on one {rows}-row microbatch of each of the "
+              f"{len(classes)} hooked classes (1 warm-up, median of 3), scaled x{cfg.layers * micro} per class "
+              f"count ({micro} microbatches of {cfg.layers} blocks)")
+    spread = {"step_ms": [round(step_lo * 1e3, 1), round(step_hi * 1e3, 1)],
+              "hooks_ms": [round(per_step["min"] * 1e3, 1), round(per_step["max"] * 1e3, 1)]}
+    return (per_step["median"] + step_med) * 1e3, per_step["median"] * 1e3, step_med * 1e3, sample, spread
 
 
 def cpu_model_name():
@@ -423,10 +460,10 @@ def main():
     if not args.no_cpu_baseline:
         log("cpu baseline")
         threads = args.cpu_threads or len(os.sched_getaffinity(0))
-        total, hooks, step, sample = cpu_baseline(args.config, threads)
+        total, hooks, step, sample, spread = cpu_baseline(args.config, threads)
         out["cpu_baseline"] = {"value": round(total, 1), "unit": "ms", "cores": threads, "kind": "port",
                                "sample": sample, "hooks_ms": round(hooks, 1), "step_ms": round(step, 1),
-                               "cpu": cpu_model_name()}
+                               "spread_min_max": spread, "cpu": cpu_model_name()}
     print(json.dumps(out), flush=True)
 
 
