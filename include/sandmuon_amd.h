@@ -274,7 +274,9 @@ int smx_s8(const float *x, float *out, int64_t batch, int64_t rows,
  * stops recording.  smx_s8_timing_read waits for the recorded launches
  * and writes up to `capacity` records in the order they were opened:
  * duration (ms), phase (0 Gram, 1 square, 2 apply, 3 stage-1 polynomial,
- * 4 a whole S8 run, first launch to last)
+ * 4 a whole S8 run, first launch to last, 5 the symmetric r x r products
+ * of Gram-space classes, which are iterated on r x r matrices when their
+ * padded columns exceed their padded rows)
  * and the MFMA FLOPs the launch (or run) issues (tiles computed x
  * 2*256*256*K, x3 in SMX_S8_COMP_BF16 mode, plus the square phase's
  * one-hot MFMAs).  It returns the number of records or a negative status.

@@ -288,7 +288,7 @@ def matrix_step(descs: Sequence[MatrixDesc], mode: int, workspace: torch.Tensor)
                                  stream_of(workspace.device)), "smx_matrix_step")
 
 
-S8_PHASES = {0: "gram", 1: "square", 2: "apply", 3: "poly1", 4: "run"}
+S8_PHASES = {0: "gram", 1: "square", 2: "apply", 3: "poly1", 4: "run", 5: "sym"}
 
 
 def s8_timing(enable, runs_only: bool = False) -> None:

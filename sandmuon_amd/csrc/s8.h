@@ -2,6 +2,18 @@
 // mapback).  Matrices are grouped in classes of equal oriented shape
 // (r <= c); every class buffer is padded to multiples of kTile so that the
 // GEMM tiles never need bounds checks.  Padding holds zeros.
+//
+// Two iteration forms.  Each stage's P_k is a polynomial in the stage's
+// Gram G_k = X_k X_k^T, so every P_k and G_k commute.  A class with
+// cp == rp runs the stages on the iterate (X-space): G = X X^T, P from G,
+// X <- P X.  A wider class (cp > rp, Gram space) runs them on r x r
+// matrices, G_{k+1} = P_k G_k P_k and Q_k = P_k Q_{k-1}, in two segments:
+// stages 1-2 from X0 (then X2 = Q2 X0), stages 3-5 from a fresh Gram of
+// X2 (then X5 = Q X2).  A Gram carried forward keeps the absolute rounding
+// of the Gram it started from, which the small eigenvalues of a
+// long-tailed spectrum cannot afford over more than two or three stages;
+// the fresh Gram of X2 restores their relative precision.  For r x c with
+// c = 4r this takes a third fewer MFMA FLOPs than X-space.
 #pragma once
 
 #include "common.h"
@@ -33,14 +45,20 @@ struct S8Class {
   int32_t tiles_n;     // cp / kTile
   int32_t parts;       // partial slots per matrix: ceil(cp / kPartRows)
   int32_t tiles_s;     // rp / kSymTile
+  int32_t gs;          // Gram-space iteration (cp > rp): the stages run on r x r
+                       // products and X0 is applied once, at stage 5
   // Iterate buffers (4 bytes per element), oriented layout only.  In
   // SMX_S8_FP32 mode they hold FP32; in SMX_S8_COMP_BF16 mode interleaved
   // BF16 hi/lo (put_operand), except the stage-5 result, which is FP32.
-  float *x0, *x1;      // [count][rp][cp] ping, pong
+  float *x0, *x1;      // [count][rp][cp] ping, pong (Gram space: X0, then X2)
   float *xf;           // [n_flip][cp][rp] stage-5 result of transposed parameters
-                       // (parameter layout); the others end in x1
+                       // (parameter layout); the others end in x1 (X-space)
+                       // or x0 (Gram space)
   float *g;            // [count][rp][rp] Gram (FP32, or planes in comp mode)
   float *p;            // [count][rp][rp] stage 1: FP32 G2; later: P (planes in comp mode)
+  float *t, *qa, *qb;  // Gram-space classes only, [count][rp][rp] each (operand
+                       // form): T = P G, and the accumulated product Q of a
+                       // segment's stage polynomials (qa, qb: ping-pong)
   float *u;            // [count][cp] per param-row rank-one coefficient
   double *fro;         // [count][parts] whiten: partial sum of V^2
   double *mb;          // [count][parts] mapback: partial sum of U^2
@@ -67,9 +85,12 @@ struct S8Mat {
   // Valid for flip() only.
   __host__ __device__ float *xf() const { return kp()->xf + slot * kp()->rp * kp()->cp; }
   // The stage-5 result in parameter layout [prow_pad][pcol_pad].
-  __host__ __device__ float *result() const { return flip() ? xf() : x1(); }
+  __host__ __device__ float *result() const { return flip() ? xf() : kp()->gs ? x0() : x1(); }
   __host__ __device__ float *g() const { return kp()->g + slot * kp()->rp * kp()->rp; }
   __host__ __device__ float *p() const { return kp()->p + slot * kp()->rp * kp()->rp; }
+  __host__ __device__ float *t() const { return kp()->t + slot * kp()->rp * kp()->rp; }
+  __host__ __device__ float *qa() const { return kp()->qa + slot * kp()->rp * kp()->rp; }
+  __host__ __device__ float *qb() const { return kp()->qb + slot * kp()->rp * kp()->rp; }
   __host__ __device__ float *u() const { return kp()->u + slot * kp()->cp; }
   __host__ __device__ double *fro() const { return kp()->fro + static_cast<int64_t>(slot) * kp()->parts; }
   __host__ __device__ double *mb() const { return kp()->mb + static_cast<int64_t>(slot) * kp()->parts; }

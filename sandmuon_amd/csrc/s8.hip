@@ -9,6 +9,22 @@
 //   POLY1   stage 1 only: P1 = a I + b G/s^2 + c G2/s^4 -> p buffer,
 //           s = max(1.35 ||G2||_F^(1/4), 1e-30) (elementwise kernel)
 //   APPLY   stage 1: X' = P1 V / (||V|| s);  stage k: X' = P X
+// A Gram-space class (cp > rp, see s8.h) replaces most per-stage Grams and
+// applies by products of r x r matrices, in two segments:
+//   stage 1: GRAM (X0), SQUARE, POLY1 (P1 -> qa = Q1), SYM T = P1 G,
+//            SYM G = T P1 / s^2
+//   stage 2: SQUARE (P2), APPLY Q2 = P2 Q1 (-> qb), APPLY X2 = Q2 X0 /
+//            (||V|| s) (-> x1)
+//   stage 3: GRAM (X2), SQUARE (P3 -> qa = Q3), SYM T = P3 G, SYM G = T P3
+//   stage 4: SQUARE (P4), SYM T = P4 G, SYM G = T P4, APPLY Q4 = P4 Q3 (-> qb)
+//   stage 5: SQUARE (P5), APPLY Q5 = P5 Q4 (-> qa), APPLY X5 = Q5 X2 (-> x0,
+//            or xf for a transposed parameter)
+// T = P G and T P are symmetric (P is a polynomial in G, computed from the
+// same G) and are computed as C = A B^T on upper-triangle tiles like the
+// Gram.  Q' = P Q is not mirrored: Q spans a wide range of eigenvalues (1
+// to ~1300), and the rounding of P makes P and Q commute only to that
+// range's precision, so Q' is the full product with Q as the K-major
+// operand of an apply tile (a mirrored Q' costs ~6x in accuracy).
 // The Gram (C = X X^T) and the square (C = G G, G symmetric) read both
 // operands as row-major K-contiguous rows.  The apply (C = P X) reads P the
 // same way and X itself as a K-major operand: its LDS tile holds 16 rows of
@@ -50,7 +66,21 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-enum Phase { kGram = 0, kSquare = 1, kApply = 2, kPoly1 = 3, kSpan = 4 };  // kSpan: timing record of a whole S8 run
+enum Phase { kGram = 0, kSquare = 1, kApply = 2, kPoly1 = 3, kSpan = 4, kSym = 5 };  // kSpan: timing record of a whole S8 run
+// SYM products of a Gram-space class (per segment of a SYM launch).
+// The product of a segment of a SYM or APPLY launch: PG / TP of a
+// Gram-space class (SYM); X' = P X of an X-space class, Q' = P Q and the
+// final X5 = Q X0 of a Gram-space class (APPLY).
+enum SegOp { kOpPG = 0, kOpTP = 1, kOpApplyX = 2, kOpApplyQ = 3, kOpApplyMid = 4, kOpApplyFinal = 5 };
+
+// The Gram-space schedule (see the header): Gram at stages 1 and 3, SYM
+// products at stages 1, 3 and 4, Q' = P Q at stages 2, 4 and 5, X2 = Q2 X0
+// after stage 2, X5 = Q5 X2 after stage 5.  A segment's first stage (1, 3)
+// keeps its P in qa: it is the segment's first Q.
+__host__ __device__ constexpr bool gs_gram(int stage) { return stage == 1 || stage == 3; }
+__host__ __device__ constexpr bool gs_sym(int stage) { return stage == 1 || stage == 3 || stage == 4; }
+__host__ __device__ constexpr bool gs_apply_q(int stage) { return stage == 2 || stage == 4 || stage == 5; }
+constexpr int kMaxSeg = 2 * kMaxClasses;
 
 // Internal MFMA mode of a plain BF16 stage of the compensated recipe: the
 // operands in their stored hi/lo form, only the hi*hi product issued.
@@ -92,8 +122,9 @@ struct Geo {
 
 struct StageArgs {
   S8Layout L;
-  int32_t seg_off[kMaxClasses + 1];  // block offsets (multiples of 8)
-  int32_t seg_cls[kMaxClasses];
+  int32_t seg_off[kMaxSeg + 1];  // block offsets (multiples of 8)
+  int32_t seg_cls[kMaxSeg];
+  int32_t seg_op[kMaxSeg];       // SYM / APPLY launches: the product of the segment (SegOp)
   int32_t n_seg;
   int32_t stage;  // 1..5
   int32_t sq_small;  // this run's square uses 128 x 128 tiles (else 256 x 128)
@@ -631,6 +662,7 @@ __device__ Stage1Scalars stage1_scalars(const S8Mat &M, bool sq_small, double *b
 struct TileRef {
   const S8Class *k;
   int64_t L;
+  int op;  // SegOp of the segment (SYM and APPLY launches)
 };
 __device__ __forceinline__ TileRef tile_of(const StageArgs &args) {
   const int b = blockIdx.x;
@@ -638,7 +670,7 @@ __device__ __forceinline__ TileRef tile_of(const StageArgs &args) {
   while (seg + 1 < args.n_seg && b >= args.seg_off[seg + 1]) ++seg;
   const int jb = b - args.seg_off[seg];
   const int per = (args.seg_off[seg + 1] - args.seg_off[seg]) / 8;
-  return TileRef{&args.L.cls[args.seg_cls[seg]], static_cast<int64_t>(jb % 8) * per + jb / 8};
+  return TileRef{&args.L.cls[args.seg_cls[seg]], static_cast<int64_t>(jb % 8) * per + jb / 8, args.seg_op[seg]};
 }
 
 // Epilogue staging: a 32 x 32 FP32 block per orientation per wave, rows
@@ -662,9 +694,9 @@ __device__ __forceinline__ void ep_read8(const float *s, int row, int col, float
 // 128 x 128 tiles as the upper-triangle tiles (tn >= tm, row by row).  A
 // diagonal block or tile is computed whole; an off-diagonal one also
 // writes its mirror.
-__host__ __device__ inline int64_t phase_tiles(const S8Class &k, int phase, bool sq_small) {
-  if (phase == kApply) return static_cast<int64_t>(k.tiles_m) * (k.cp / kTileN);
-  return phase == kSquare ? square_tiles(k, sq_small) : 2 * sym_tiles(k.tiles_m);
+__host__ __device__ inline int64_t phase_tiles(const S8Class &k, int phase, bool sq_small, int op = -1) {
+  if (phase == kApply) return static_cast<int64_t>(k.tiles_m) * ((op == kOpApplyQ ? k.rp : k.cp) / kTileN);
+  return phase == kSquare ? square_tiles(k, sq_small) : 2 * sym_tiles(k.tiles_m);  // Gram, SYM
 }
 
 template <int MODE, int PHASE, int TM>
@@ -680,7 +712,7 @@ s8_stage_kernel(StageArgs args) {
 
   const TileRef ref = tile_of(args);
   const S8Class &K = *ref.k;
-  const int64_t tpm = phase_tiles(K, PHASE, TM == kSymTile);
+  const int64_t tpm = phase_tiles(K, PHASE, TM == kSymTile, ref.op);
   if (ref.L >= tpm * K.count) return;
   const int slot = static_cast<int>(ref.L / tpm);
   const int64_t tix = ref.L % tpm;
@@ -715,12 +747,33 @@ s8_stage_kernel(StageArgs args) {
 
   f32x16 acc[kSubM][kSubN];
   float scale = 1.f;
-  if constexpr (PHASE == kGram) {
+  float *sym_out = nullptr;  // SYM: the product's destination
+  // Gram space (see the header): a segment's first Q sits in qa; Q' = P Q
+  // goes qa -> qb at stages 2 and 4 and qb -> qa at stage 5.
+  float *q_in = stage == 5 ? M.qb() : M.qa();
+  float *q_out = stage == 5 ? M.qa() : M.qb();
+  if constexpr (PHASE == kSym) {
+    float *pk = stage == 1 || stage == 3 ? M.qa() : M.p();
+    const float *A, *B;
+    if (ref.op == kOpPG) {
+      A = pk; B = M.g(); sym_out = M.t();
+    } else {
+      A = M.t(); B = pk; sym_out = M.g();
+      if (stage == 1) {
+        // G1 = P1 G0 P1 / s^2
+        const Stage1Scalars sc = stage1_scalars(M, args.sq_small != 0, &bcast);
+        scale = sc.ok ? 1.0f / (sc.s * sc.s) : 0.f;
+      }
+    }
+    gemm_tile<MODE, TM, false, false>(Opnd{A, K.rp}, Opnd{B, K.rp}, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem,
+                                      acc);
+  } else if constexpr (PHASE == kGram) {
     if (stage == 1) {
       const double f = sum_parts(M.fro(), fro_parts_used(M), &bcast);
       scale = f > 0.0 ? static_cast<float>(1.0 / f) : 0.f;
     }
-    const Opnd X{x_in, K.cp};
+    // A Gram-space class takes its stage-3 Gram of X2 from x1.
+    const Opnd X{K.gs && stage == 3 ? M.x1() : x_in, K.cp};
     gemm_tile<MODE, TM, false, false>(X, X, K.cp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
   } else if constexpr (PHASE == kSquare) {
     const Opnd G{M.g(), K.rp};
@@ -732,14 +785,18 @@ s8_stage_kernel(StageArgs args) {
       gemm_tile<MODE, TM, true, false>(G, G, K.rp, tm * Gm::kTileM, tn * kTileN, args.b_over_c, smem, acc);
     }
   } else {
-    if (stage == 1) {
-      // X' = P1 V / (||V|| s)
+    // X-space: X' = P X (stage 1: X' = P1 V / (||V|| s)).  Gram space:
+    // Q' = P Q; X2 = Q2 V / (||V|| s), V in x0; X5 = Q5 X2, X2 in x1.
+    const int op = ref.op;
+    const bool gq = op == kOpApplyQ, mid = op == kOpApplyMid, fin = op == kOpApplyFinal;
+    if (stage == 1 || mid) {
       const Stage1Scalars sc = stage1_scalars(M, args.sq_small != 0, &bcast);
       scale = sc.ok ? static_cast<float>(1.0 / (sqrt(sc.fro2) * static_cast<double>(sc.s))) : 0.f;
     }
-    // X' = P X: B = X rows k (K-major), columns of the tile.
-    gemm_tile<MODE, TM, false, true>(Opnd{M.p(), K.rp}, Opnd{x_in, K.cp}, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f,
-                                     smem, acc);
+    const float *A = mid ? M.qb() : fin ? M.qa() : M.p();
+    const Opnd B = gq ? Opnd{q_in, K.rp} : Opnd{mid ? M.x0() : fin ? M.x1() : x_in, K.cp};
+    // B = X (or Q) rows k (K-major), columns of the tile.
+    gemm_tile<MODE, TM, false, true>(Opnd{A, K.rp}, B, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
   }
 
   // ------------------------------------------------------- epilogue ---
@@ -759,17 +816,35 @@ s8_stage_kernel(StageArgs args) {
   int64_t ld_t, ld_m;
   bool pl_t, pl_m, do_t, do_m;
   if constexpr (PHASE == kApply) {
-    const bool xf = last && M.flip();
-    dst_t = x_out; ld_t = K.cp;
-    dst_m = xf ? M.xf() : nullptr; ld_m = K.rp;
-    pl_t = PL && !last;
-    pl_m = false;
-    do_t = !xf;
-    do_m = xf;
+    if (ref.op == kOpApplyQ) {
+      dst_t = q_out; ld_t = K.rp;
+      dst_m = nullptr; ld_m = K.rp;
+      pl_t = PL;
+      pl_m = false;
+      do_t = true;
+      do_m = false;
+    } else if (ref.op == kOpApplyMid) {
+      dst_t = M.x1(); ld_t = K.cp;  // X2, an operand of the stage-3 Gram and the final apply
+      dst_m = nullptr; ld_m = K.rp;
+      pl_t = PL;
+      pl_m = false;
+      do_t = true;
+      do_m = false;
+    } else {
+      const bool xf = last && M.flip();
+      dst_t = ref.op == kOpApplyFinal ? M.x0() : x_out; ld_t = K.cp;
+      dst_m = xf ? M.xf() : nullptr; ld_m = K.rp;
+      pl_t = PL && !last;
+      pl_m = false;
+      do_t = !xf;
+      do_m = xf;
+    }
   } else {
-    dst_t = dst_m = PHASE == kGram ? M.g() : M.p();
+    // A Gram-space square at stage 3 writes P3 to qa: it is Q3.
+    float *sq_out = K.gs && stage == 3 ? M.qa() : M.p();
+    dst_t = dst_m = PHASE == kSym ? sym_out : PHASE == kGram ? M.g() : sq_out;
     ld_t = ld_m = K.rp;
-    pl_t = pl_m = PL && (PHASE == kGram || stage != 1);
+    pl_t = pl_m = PL && (PHASE != kSquare || stage != 1);
     do_t = true;
     do_m = !diag;
   }
@@ -829,7 +904,8 @@ s8_stage_kernel(StageArgs args) {
 // Stage-1 polynomial operand (sandmuon/optimizer.py:84-86) over the r x r
 // matrices of a class: P1 = a I + (b G)/s^2 + (c G2)/s^4 from the
 // normalised G and the FP32 G2 of the square phase, written over G2 in the
-// p buffer in operand form.  A block takes kPolyChunk consecutive
+// p buffer in operand form (into qa, as Q1, for a Gram-space class).  A
+// block takes kPolyChunk consecutive
 // 16-element groups of one matrix (64 KB of each buffer, contiguous), a
 // thread kPolyGroups of them; whole groups keep the FP32 and interleaved
 // BF16 forms in the same 64 bytes.  The loads are issued before the block
@@ -853,7 +929,8 @@ __global__ void __launch_bounds__(256) s8_poly1_kernel(StageArgs args) {
   const int64_t g0 = (ref.L % tpm) * kPolyChunk;  // first group of the block
   const int64_t gpr = K.rp / 16;                   // groups per row
   const float *G = M.g();
-  float *P = M.p();
+  float *P = M.p();                       // FP32 G2 in, and P1 out for an X-space class
+  float *Pout = K.gs ? M.qa() : M.p();    // Gram space: P1 is Q1
   int64_t row[kPolyGroups], col[kPolyGroups], idx[kPolyGroups];
   float4 w4[kPolyGroups][4];
   uint4 g4[kPolyGroups][4];  // FP32 G, or its 16 hi then 16 lo BF16 values
@@ -905,8 +982,8 @@ __global__ void __launch_bounds__(256) s8_poly1_kernel(StageArgs args) {
     float lo8[8], hi8[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) { lo8[e] = v[e]; hi8[e] = v[8 + e]; }
-    put_operand8(P, idx[k], lo8, PL);
-    put_operand8(P, idx[k] + 8, hi8, PL);
+    put_operand8(Pout, idx[k], lo8, PL);
+    put_operand8(Pout, idx[k] + 8, hi8, PL);
   }
 }
 
@@ -959,23 +1036,61 @@ static int stage_mode(const S8Layout &Lay, int stage) {
   return stage <= g_comp_stages ? SMX_S8_COMP_BF16 : kS8HiOnly;
 }
 
+// The segments of one launch, in class order by per-tile cost (K length,
+// most expensive first, so long-K tiles start first and short tiles fill
+// the remaining CUs).  A Gram-space class takes the Gram at stages 1 and 3
+// only; SYM and APPLY launches take one segment per class and product in
+// `ops` that applies to it at this stage (the Gram-space schedule above;
+// APPLY: X' = P X for an X-space class).
+struct Seg {
+  int cls;
+  int op;
+};
+static std::vector<Seg> launch_segments(const S8Layout &Lay, int phase, int stage, const std::vector<int> &ops) {
+  std::vector<int> order(Lay.n_classes);
+  for (int i = 0; i < Lay.n_classes; ++i) order[i] = i;
+  std::stable_sort(order.begin(), order.end(), [&](int x, int y) {
+    const int64_t kx = phase == kGram ? Lay.cls[x].cp : Lay.cls[x].rp;
+    const int64_t ky = phase == kGram ? Lay.cls[y].cp : Lay.cls[y].rp;
+    return kx > ky;
+  });
+  std::vector<Seg> segs;
+  for (int ci : order) {
+    const S8Class &k = Lay.cls[ci];
+    if (k.count == 0) continue;
+    if (phase == kSym || phase == kApply) {
+      for (int op : ops) {
+        const bool takes = phase == kSym ? k.gs != 0 && gs_sym(stage)
+                           : op == kOpApplyX ? k.gs == 0
+                           : op == kOpApplyQ ? k.gs != 0 && gs_apply_q(stage)
+                           : op == kOpApplyMid ? k.gs != 0 && stage == 2
+                                               : k.gs != 0 && stage == 5;
+        if (takes) segs.push_back(Seg{ci, op});
+      }
+      continue;
+    }
+    if (k.gs && phase == kGram && !gs_gram(stage)) continue;
+    segs.push_back(Seg{ci, -1});
+  }
+  return segs;
+}
+
 // MFMA FLOPs of one launch: computed tiles x 2 * TM * 128 * K (x3 for a
 // compensated stage), plus the square phase's one-hot MFMAs (2 kSubM stages
 // of kSubN 32x32x16 products per wave).
-template <int PHASE>
-static double launch_flops(const S8Layout &Lay, int stage, bool sq_small) {
-  if (PHASE == kPoly1) return 0.0;
+static double launch_flops(const S8Layout &Lay, int phase, int stage, bool sq_small, const std::vector<Seg> &segs) {
+  if (phase == kPoly1) return 0.0;
   const double prod = stage_mode(Lay, stage) == SMX_S8_COMP_BF16 ? 3.0 : 1.0;
-  const int tm = PHASE == kSquare && sq_small ? kSymTile : kTile;
+  const int tm = phase == kSquare && sq_small ? kSymTile : kTile;
   const int sub_m = tm / 64;
   double f = 0.0;
-  for (int i = 0; i < Lay.n_classes; ++i) {
-    const S8Class &k = Lay.cls[i];
-    const double tiles = static_cast<double>(phase_tiles(k, PHASE, sq_small));
-    const double K = PHASE == kGram ? static_cast<double>(k.cp) : static_cast<double>(k.rp);
+  for (const Seg &sg : segs) {
+    const S8Class &k = Lay.cls[sg.cls];
+    const double tiles = static_cast<double>(phase_tiles(k, phase, sq_small, sg.op));
+    const double K = phase == kGram ? static_cast<double>(k.cp) : static_cast<double>(k.rp);
     f += k.count * tiles * 2.0 * tm * kTileN * K * prod;
     // one-hot: per wave 2 kSubM stages of kSubN MFMA tiles
-    if (PHASE == kSquare && stage != 1)
+    if (phase == kSquare && stage != 1)
       f += k.count * tiles * kWaves * (2.0 * sub_m) * kSubN * 2.0 * 32 * 32 * kBK * prod;
   }
   return f;
@@ -1015,7 +1130,8 @@ static void launch_stage(bool sq_small, int32_t blocks, const StageArgs &a, hipS
 }
 
 template <int PHASE>
-static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, hipStream_t st) {
+static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, hipStream_t st, double &flops,
+                        const std::vector<int> &ops = {}) {
   StageArgs a{};
   a.L = Lay;
   a.stage = stage;
@@ -1025,23 +1141,17 @@ static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, hipStream
   a.b = static_cast<float>(co[1]);
   a.c = static_cast<float>(co[2]);
   a.b_over_c = static_cast<float>(co[1] / co[2]);
-  // Order classes by per-tile cost (K length), most expensive first.
-  std::vector<int> order(Lay.n_classes);
-  for (int i = 0; i < Lay.n_classes; ++i) order[i] = i;
-  std::stable_sort(order.begin(), order.end(), [&](int x, int y) {
-    const int64_t kx = PHASE == kGram ? Lay.cls[x].cp : Lay.cls[x].rp;
-    const int64_t ky = PHASE == kGram ? Lay.cls[y].cp : Lay.cls[y].rp;
-    return kx > ky;
-  });
+  const std::vector<Seg> segs = launch_segments(Lay, PHASE, stage, ops);
+  if (static_cast<int>(segs.size()) > kMaxSeg) return fail(SMX_EINVAL, "s8: too many launch segments");
   int32_t off = 0;
   a.n_seg = 0;
-  for (int ci : order) {
-    const S8Class &k = Lay.cls[ci];
-    if (k.count == 0) continue;
-    const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE, sq_small);
+  for (const Seg &sg : segs) {
+    const S8Class &k = Lay.cls[sg.cls];
+    const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE, sq_small, sg.op);
     const int64_t nt = round_up(tpm * k.count, 8);
     a.seg_off[a.n_seg] = off;
-    a.seg_cls[a.n_seg] = ci;
+    a.seg_cls[a.n_seg] = sg.cls;
+    a.seg_op[a.n_seg] = sg.op;
     ++a.n_seg;
     off += static_cast<int32_t>(nt);
   }
@@ -1061,30 +1171,41 @@ static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, hipStream
     if (mode == SMX_S8_COMP_BF16) launch_stage<SMX_S8_COMP_BF16, PHASE>(sq_small, off, a, st);
     else if (mode == kS8HiOnly) launch_stage<kS8HiOnly, PHASE>(sq_small, off, a, st);
     else launch_stage<SMX_S8_FP32, PHASE>(sq_small, off, a, st);
-    rc = check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : "s8 apply");
+    rc = check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : PHASE == kSym ? "s8 sym"
+                                                                                                : "s8 apply");
   }
   if (rc) return rc;
-  return timing_end(slot, st, PHASE, launch_flops<PHASE>(Lay, stage, sq_small));
+  const double f = launch_flops(Lay, PHASE, stage, sq_small, segs);
+  flops += f;
+  return timing_end(slot, st, PHASE, f);
 }
 
-// The whole S8 run: per stage one launch per phase over every class (class
-// segments ordered by K cost, so long-K tiles start first and short tiles
-// fill the remaining CUs).  The launch recorder gets one record for the run.
+// The whole S8 run: per stage one launch per phase over every class it
+// applies to; Gram-space classes add their two SYM products before the
+// apply launch at stages 1, 3 and 4, and an apply of their own after it at
+// stages 2 (X2) and 5 (X5).
+// The launch recorder gets one record for the run.
 int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
   int slot = -1;
   int rc = timing_begin(st, slot, true);
   if (rc) return rc;
   const bool sq_small = square_small(Lay, st);
+  bool any_gs = false;
+  for (int i = 0; i < Lay.n_classes; ++i) any_gs = any_gs || (Lay.cls[i].gs && Lay.cls[i].count);
   double flops = 0.0;
-  for (int stage = 1; stage <= 5; ++stage) {
-    rc = launch_phase<kGram>(Lay, stage, sq_small, st);
-    if (!rc) rc = launch_phase<kSquare>(Lay, stage, sq_small, st);
-    if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, stage, sq_small, st);
-    if (!rc) rc = launch_phase<kApply>(Lay, stage, sq_small, st);
-    if (rc) return rc;
-    flops += launch_flops<kGram>(Lay, stage, sq_small) + launch_flops<kSquare>(Lay, stage, sq_small) +
-             launch_flops<kApply>(Lay, stage, sq_small);
+  for (int stage = 1; stage <= 5 && !rc; ++stage) {
+    rc = launch_phase<kGram>(Lay, stage, sq_small, st, flops);
+    if (!rc) rc = launch_phase<kSquare>(Lay, stage, sq_small, st, flops);
+    if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, stage, sq_small, st, flops);
+    if (!rc && any_gs && gs_sym(stage)) {
+      rc = launch_phase<kSym>(Lay, stage, sq_small, st, flops, {kOpPG});
+      if (!rc) rc = launch_phase<kSym>(Lay, stage, sq_small, st, flops, {kOpTP});
+    }
+    if (!rc) rc = launch_phase<kApply>(Lay, stage, sq_small, st, flops, {kOpApplyX, kOpApplyQ});
+    if (!rc && any_gs && (stage == 2 || stage == 5))
+      rc = launch_phase<kApply>(Lay, stage, sq_small, st, flops, {stage == 2 ? kOpApplyMid : kOpApplyFinal});
   }
+  if (rc) return rc;
   return timing_end(slot, st, kSpan, flops);
 }
 
@@ -1134,6 +1255,7 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.tiles_n = static_cast<int32_t>(C.cp / kTile);
     C.tiles_s = static_cast<int32_t>(C.rp / kSymTile);
     C.parts = static_cast<int32_t>(ceil_div(C.cp, kPartRows));
+    C.gs = C.cp > C.rp ? 1 : 0;
     const size_t xs = static_cast<size_t>(C.count) * C.rp * C.cp * sizeof(float);
     const size_t gs = static_cast<size_t>(C.count) * C.rp * C.rp * sizeof(float);
     C.x0 = reinterpret_cast<float *>(take(xs));
@@ -1141,6 +1263,9 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.xf = reinterpret_cast<float *>(take(static_cast<size_t>(C.n_flip) * C.rp * C.cp * sizeof(float)));
     C.g = reinterpret_cast<float *>(take(gs));
     C.p = reinterpret_cast<float *>(take(gs));
+    C.t = C.gs ? reinterpret_cast<float *>(take(gs)) : nullptr;
+    C.qa = C.gs ? reinterpret_cast<float *>(take(gs)) : nullptr;
+    C.qb = C.gs ? reinterpret_cast<float *>(take(gs)) : nullptr;
     C.u = reinterpret_cast<float *>(take(static_cast<size_t>(C.count) * C.cp * sizeof(float)));
     C.fro = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));
     C.mb = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));

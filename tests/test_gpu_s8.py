@@ -47,12 +47,13 @@ def test_s8_cfg2_inputs(device, mode, shape):
     assert max(errs) <= TOL[mode]
 
 
-def test_s8_zero_matrix_is_zero_and_batch_neighbours_unaffected(device):
+@pytest.mark.parametrize("cols", [24, 300])  # 40 x 24: X-space; 40 x 300: Gram space
+def test_s8_zero_matrix_is_zero_and_batch_neighbours_unaffected(device, cols):
     torch.manual_seed(3)
-    x = torch.randn(3, 40, 24)
+    x = torch.randn(3, 40, cols)
     x[1] = 0
     out = _s8_fp32(x.to(device))
-    assert torch.equal(out[1].cpu(), torch.zeros(40, 24))
+    assert torch.equal(out[1].cpu(), torch.zeros(40, cols))
     ref = O.s8(x[[0, 2]])
     assert max(per_matrix_rel(out[[0, 2]], ref)) <= 1e-4
     zero = _s8_fp32(torch.zeros(1, 4, 3, device=device))
@@ -67,35 +68,63 @@ def test_s8_orientation_transpose_equivariance(device):
     assert max(per_matrix_rel(b.transpose(-2, -1), a)) <= 1e-5
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
-def test_s8_launch_timing_records_every_phase(device, mode):
+def _timed_s8(x, mode):
     from sandmuon_amd import _native
-    x = torch.randn(3, 300, 520, device=device)
     _native.s8_timing(True)
     try:
-        _s8_fp32(x, mode=mode)
+        out = _s8_fp32(x, mode=mode)
     finally:
         _native.s8_timing(False)
     rec = _native.s8_timing_read()
-    phases = [p for _, p, _ in rec]
-    assert phases == ["run", "gram", "square", "poly1", "apply"] + ["gram", "square", "apply"] * 4
     assert all(ms > 0 for ms, _, _ in rec)
     run, rec = rec[0], rec[1:]
-    assert run[2] == sum(f for _, _, f in rec)
+    assert run[1] == "run" and run[2] == sum(f for _, _, f in rec)
     assert run[0] >= max(ms for ms, _, _ in rec)
-    # oriented 300 x 520 padded to 512 x 768: the apply computes 2 x 6 tiles
-    # of 256 x 128, the Gram the 3 upper-triangle 256 x 256 blocks of its
-    # 512 x 512 result and the square its 10 upper-triangle 128 x 128 tiles;
-    # the one-hot term adds, per square tile and wave, 4 K stages of 2 MFMA
-    # tiles 32 x 32 x 16.
+    return out, [p for _, p, _ in rec], [f for _, _, f in rec]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+def test_s8_launch_timing_records_every_phase_x_space(device, mode):
+    # oriented 300 x 500 padded to 512 x 512 (cp == rp): the stages run on
+    # the iterate.  The apply computes 2 x 4 tiles of 256 x 128, the Gram the
+    # 3 upper-triangle 256 x 256 blocks of its 512 x 512 result and the
+    # square its 10 upper-triangle 128 x 128 tiles; the one-hot term adds,
+    # per square tile and wave, 4 K stages of 2 MFMA tiles 32 x 32 x 16.
+    x = torch.randn(3, 300, 500, device=device)
+    _, phases, fl = _timed_s8(x, mode)
+    assert phases == ["gram", "square", "poly1", "apply"] + ["gram", "square", "apply"] * 4
     prod = 3 if mode == "comp_bf16" else 1
-    gram, apply = 3 * 3 * 2 * 256 * 256 * 768 * prod, 3 * 12 * 2 * 256 * 128 * 512 * prod
+    gram, apply = 3 * 3 * 2 * 256 * 256 * 512 * prod, 3 * 8 * 2 * 256 * 128 * 512 * prod
     square1 = 3 * 10 * 2 * 128 * 128 * 512 * prod
     one_hot = 3 * 10 * 4 * 4 * 2 * 2 * 32 * 32 * 16 * prod
-    fl = [f for _, _, f in rec]
     assert fl[:4] == [gram, square1, 0.0, apply]
     assert fl[4:7] == [gram, square1 + one_hot, apply]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+def test_s8_launch_timing_records_every_phase_gram_space(device, mode):
+    # oriented 300 x 520 padded to 512 x 768 (cp > rp): Gram space, in two
+    # segments.  Grams of X0 (stage 1) and X2 (stage 3), K = 768; applies of
+    # Q2 to X0 and of Q5 to X2 over 2 x 6 tiles; symmetric r x r products
+    # T = P G and G = T P (stages 1, 3, 4) on the Gram's 3 upper-triangle
+    # blocks and full products Q' = P Q (stages 2, 4, 5) over 2 x 4 apply
+    # tiles, all with K = 512.
+    x = torch.randn(3, 300, 520, device=device)
+    out, phases, fl = _timed_s8(x, mode)
+    assert phases == (["gram", "square", "poly1", "sym", "sym"] + ["square", "apply", "apply"]
+                      + ["gram", "square", "sym", "sym"] + ["square", "sym", "sym", "apply"]
+                      + ["square", "apply", "apply"])
+    prod = 3 if mode == "comp_bf16" else 1
+    gram, x_apply = 3 * 3 * 2 * 256 * 256 * 768 * prod, 3 * 12 * 2 * 256 * 128 * 512 * prod
+    sym, apply_q = 3 * 3 * 2 * 256 * 256 * 512 * prod, 3 * 8 * 2 * 256 * 128 * 512 * prod
+    square1 = 3 * 10 * 2 * 128 * 128 * 512 * prod
+    square = square1 + 3 * 10 * 4 * 4 * 2 * 2 * 32 * 32 * 16 * prod
+    assert fl == ([gram, square1, 0.0, sym, sym] + [square, apply_q, x_apply] + [gram, square, sym, sym]
+                  + [square, sym, sym, apply_q] + [square, apply_q, x_apply])
+    ref = O.s8(x.cpu())
+    assert max(per_matrix_rel(out, ref)) <= TOL[mode]
 
 
 @pytest.mark.gpu
