@@ -694,15 +694,16 @@ __device__ __forceinline__ void ep_read8(const float *s, int row, int col, float
 // 128 x 128 tiles as the upper-triangle tiles (tn >= tm, row by row).  A
 // diagonal block or tile is computed whole; an off-diagonal one also
 // writes its mirror.
-__host__ __device__ inline int64_t phase_tiles(const S8Class &k, int phase, bool sq_small, int op = -1) {
+// `small`: the launch's tiles are 128 x 128 (square and SYM launches).
+__host__ __device__ inline int64_t phase_tiles(const S8Class &k, int phase, bool small, int op = -1) {
   if (phase == kApply) return static_cast<int64_t>(k.tiles_m) * ((op == kOpApplyQ ? k.rp : k.cp) / kTileN);
-  return phase == kSquare ? square_tiles(k, sq_small) : 2 * sym_tiles(k.tiles_m);  // Gram, SYM
+  return phase == kSquare || phase == kSym ? square_tiles(k, small) : 2 * sym_tiles(k.tiles_m);
 }
 
 template <int MODE, int PHASE, int TM>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(Geo<TM>::kWavesPerEU, Geo<TM>::kWavesPerEU)))
 s8_stage_kernel(StageArgs args) {
-  static_assert(TM == kTile || PHASE == kSquare, "128 x 128 tiles for the square only");
+  static_assert(TM == kTile || PHASE == kSquare || PHASE == kSym, "128 x 128 tiles for the square and SYM only");
   using Gm = Geo<TM>;
   constexpr int kSubM = Gm::kSubM;
   __shared__ __attribute__((aligned(16))) char smem[Gm::kRingBytes];
@@ -1078,15 +1079,15 @@ static std::vector<Seg> launch_segments(const S8Layout &Lay, int phase, int stag
 // MFMA FLOPs of one launch: computed tiles x 2 * TM * 128 * K (x3 for a
 // compensated stage), plus the square phase's one-hot MFMAs (2 kSubM stages
 // of kSubN 32x32x16 products per wave).
-static double launch_flops(const S8Layout &Lay, int phase, int stage, bool sq_small, const std::vector<Seg> &segs) {
+static double launch_flops(const S8Layout &Lay, int phase, int stage, bool small, const std::vector<Seg> &segs) {
   if (phase == kPoly1) return 0.0;
   const double prod = stage_mode(Lay, stage) == SMX_S8_COMP_BF16 ? 3.0 : 1.0;
-  const int tm = phase == kSquare && sq_small ? kSymTile : kTile;
+  const int tm = (phase == kSquare || phase == kSym) && small ? kSymTile : kTile;
   const int sub_m = tm / 64;
   double f = 0.0;
   for (const Seg &sg : segs) {
     const S8Class &k = Lay.cls[sg.cls];
-    const double tiles = static_cast<double>(phase_tiles(k, phase, sq_small, sg.op));
+    const double tiles = static_cast<double>(phase_tiles(k, phase, small, sg.op));
     const double K = phase == kGram ? static_cast<double>(k.cp) : static_cast<double>(k.rp);
     f += k.count * tiles * 2.0 * tm * kTileN * K * prod;
     // one-hot: per wave 2 kSubM stages of kSubN MFMA tiles
@@ -1096,18 +1097,20 @@ static double launch_flops(const S8Layout &Lay, int phase, int stage, bool sq_sm
   return f;
 }
 
-// Whether the square phase of a layout takes 128 x 128 tiles: rounds of the
-// device's block slots (two 256 x 128 or three 128 x 128 blocks per CU),
-// a round of the smaller tile counted as 0.9 of one of the larger.
-static bool square_small(const S8Layout &Lay, hipStream_t st) {
+// Whether a symmetric-output launch (square, SYM) over the classes `use`
+// selects takes 128 x 128 tiles: rounds of the device's block slots (two
+// 256 x 128 or three 128 x 128 blocks per CU), a round of the smaller tile
+// counted as 0.9 of one of the larger.
+template <typename Use>
+static bool small_tiles(const S8Layout &Lay, Use use) {
   static int cus[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
   if (cus[dev] == 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return false;
-  (void)st;
   int64_t big = 0, small = 0;
   for (int i = 0; i < Lay.n_classes; ++i) {
+    if (!use(Lay.cls[i])) continue;
     big += Lay.cls[i].count * square_tiles(Lay.cls[i], false);
     small += Lay.cls[i].count * square_tiles(Lay.cls[i], true);
   }
@@ -1116,12 +1119,12 @@ static bool square_small(const S8Layout &Lay, hipStream_t st) {
   return 0.9 * r_small < r_big;
 }
 
-// One phase launch of a stage kernel (the square on 128 x 128 tiles when
-// sq_small).
+// One phase launch of a stage kernel (a square or SYM launch on 128 x 128
+// tiles when `small`).
 template <int MODE, int PHASE>
-static void launch_stage(bool sq_small, int32_t blocks, const StageArgs &a, hipStream_t st) {
-  if constexpr (PHASE == kSquare) {
-    if (sq_small) {
+static void launch_stage(bool small, int32_t blocks, const StageArgs &a, hipStream_t st) {
+  if constexpr (PHASE == kSquare || PHASE == kSym) {
+    if (small) {
       hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, kSymTile>), dim3(blocks), dim3(kThreads), 0, st, a);
       return;
     }
@@ -1129,9 +1132,12 @@ static void launch_stage(bool sq_small, int32_t blocks, const StageArgs &a, hipS
   hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, kTile>), dim3(blocks), dim3(kThreads), 0, st, a);
 }
 
+// sq_small: the run's square takes 128 x 128 tiles (the stage-1 Schatten
+// partials are per square tile); sym_small: its SYM launches do.
 template <int PHASE>
-static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, hipStream_t st, double &flops,
-                        const std::vector<int> &ops = {}) {
+static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, bool sym_small, hipStream_t st,
+                        double &flops, const std::vector<int> &ops = {}) {
+  const bool small = PHASE == kSquare ? sq_small : PHASE == kSym ? sym_small : false;
   StageArgs a{};
   a.L = Lay;
   a.stage = stage;
@@ -1147,7 +1153,7 @@ static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, hipStream
   a.n_seg = 0;
   for (const Seg &sg : segs) {
     const S8Class &k = Lay.cls[sg.cls];
-    const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE, sq_small, sg.op);
+    const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE, small, sg.op);
     const int64_t nt = round_up(tpm * k.count, 8);
     a.seg_off[a.n_seg] = off;
     a.seg_cls[a.n_seg] = sg.cls;
@@ -1168,14 +1174,14 @@ static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, hipStream
       hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_FP32>, dim3(off), dim3(256), 0, st, a);
     rc = check_launch("s8 stage-1 polynomial");
   } else {
-    if (mode == SMX_S8_COMP_BF16) launch_stage<SMX_S8_COMP_BF16, PHASE>(sq_small, off, a, st);
-    else if (mode == kS8HiOnly) launch_stage<kS8HiOnly, PHASE>(sq_small, off, a, st);
-    else launch_stage<SMX_S8_FP32, PHASE>(sq_small, off, a, st);
+    if (mode == SMX_S8_COMP_BF16) launch_stage<SMX_S8_COMP_BF16, PHASE>(small, off, a, st);
+    else if (mode == kS8HiOnly) launch_stage<kS8HiOnly, PHASE>(small, off, a, st);
+    else launch_stage<SMX_S8_FP32, PHASE>(small, off, a, st);
     rc = check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : PHASE == kSym ? "s8 sym"
                                                                                                 : "s8 apply");
   }
   if (rc) return rc;
-  const double f = launch_flops(Lay, PHASE, stage, sq_small, segs);
+  const double f = launch_flops(Lay, PHASE, stage, small, segs);
   flops += f;
   return timing_end(slot, st, PHASE, f);
 }
@@ -1189,21 +1195,22 @@ int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
   int slot = -1;
   int rc = timing_begin(st, slot, true);
   if (rc) return rc;
-  const bool sq_small = square_small(Lay, st);
+  const bool sq_small = small_tiles(Lay, [](const S8Class &) { return true; });
+  const bool sym_small = small_tiles(Lay, [](const S8Class &k) { return k.gs != 0; });
   bool any_gs = false;
   for (int i = 0; i < Lay.n_classes; ++i) any_gs = any_gs || (Lay.cls[i].gs && Lay.cls[i].count);
   double flops = 0.0;
   for (int stage = 1; stage <= 5 && !rc; ++stage) {
-    rc = launch_phase<kGram>(Lay, stage, sq_small, st, flops);
-    if (!rc) rc = launch_phase<kSquare>(Lay, stage, sq_small, st, flops);
-    if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, stage, sq_small, st, flops);
+    rc = launch_phase<kGram>(Lay, stage, sq_small, sym_small, st, flops);
+    if (!rc) rc = launch_phase<kSquare>(Lay, stage, sq_small, sym_small, st, flops);
+    if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, stage, sq_small, sym_small, st, flops);
     if (!rc && any_gs && gs_sym(stage)) {
-      rc = launch_phase<kSym>(Lay, stage, sq_small, st, flops, {kOpPG});
-      if (!rc) rc = launch_phase<kSym>(Lay, stage, sq_small, st, flops, {kOpTP});
+      rc = launch_phase<kSym>(Lay, stage, sq_small, sym_small, st, flops, {kOpPG});
+      if (!rc) rc = launch_phase<kSym>(Lay, stage, sq_small, sym_small, st, flops, {kOpTP});
     }
-    if (!rc) rc = launch_phase<kApply>(Lay, stage, sq_small, st, flops, {kOpApplyX, kOpApplyQ});
+    if (!rc) rc = launch_phase<kApply>(Lay, stage, sq_small, sym_small, st, flops, {kOpApplyX, kOpApplyQ});
     if (!rc && any_gs && (stage == 2 || stage == 5))
-      rc = launch_phase<kApply>(Lay, stage, sq_small, st, flops, {stage == 2 ? kOpApplyMid : kOpApplyFinal});
+      rc = launch_phase<kApply>(Lay, stage, sq_small, sym_small, st, flops, {stage == 2 ? kOpApplyMid : kOpApplyFinal});
   }
   if (rc) return rc;
   return timing_end(slot, st, kSpan, flops);

@@ -108,9 +108,10 @@ def test_s8_launch_timing_records_every_phase_gram_space(device, mode):
     # oriented 300 x 520 padded to 512 x 768 (cp > rp): Gram space, in two
     # segments.  Grams of X0 (stage 1) and X2 (stage 3), K = 768; applies of
     # Q2 to X0 and of Q5 to X2 over 2 x 6 tiles; symmetric r x r products
-    # T = P G and G = T P (stages 1, 3, 4) on the Gram's 3 upper-triangle
-    # blocks and full products Q' = P Q (stages 2, 4, 5) over 2 x 4 apply
-    # tiles, all with K = 512.
+    # T = P G and G = T P (stages 1, 3, 4) on the 10 upper-triangle
+    # 128 x 128 tiles (three matrices take fewer rounds of the CUs' block
+    # slots in the smaller geometry) and full products Q' = P Q (stages 2,
+    # 4, 5) over 2 x 4 apply tiles, all with K = 512.
     x = torch.randn(3, 300, 520, device=device)
     out, phases, fl = _timed_s8(x, mode)
     assert phases == (["gram", "square", "poly1", "sym", "sym"] + ["square", "apply", "apply"]
@@ -118,7 +119,7 @@ def test_s8_launch_timing_records_every_phase_gram_space(device, mode):
                       + ["square", "apply", "apply"])
     prod = 3 if mode == "comp_bf16" else 1
     gram, x_apply = 3 * 3 * 2 * 256 * 256 * 768 * prod, 3 * 12 * 2 * 256 * 128 * 512 * prod
-    sym, apply_q = 3 * 3 * 2 * 256 * 256 * 512 * prod, 3 * 8 * 2 * 256 * 128 * 512 * prod
+    sym, apply_q = 3 * 10 * 2 * 128 * 128 * 512 * prod, 3 * 8 * 2 * 256 * 128 * 512 * prod
     square1 = 3 * 10 * 2 * 128 * 128 * 512 * prod
     square = square1 + 3 * 10 * 4 * 4 * 2 * 2 * 32 * 32 * 16 * prod
     assert fl == ([gram, square1, 0.0, sym, sym] + [square, apply_q, x_apply] + [gram, square, sym, sym]
