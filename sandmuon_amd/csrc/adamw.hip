@@ -17,6 +17,7 @@ namespace smx {
 constexpr int kAdamBatch = 56;
 constexpr int kAdamMaxChunk = 2048;  // elements per block (large launches)
 constexpr int kAdamUnroll = 4;
+constexpr int kAdamVec = 2;  // float4 per thread per pass (FP32 tensors)
 
 struct AdamPack {
   int32_t first_blk[kAdamBatch];  // ceil(offset / chunk); INT32_MAX past the last
@@ -28,6 +29,23 @@ struct AdamPack {
 };
 static_assert(sizeof(AdamPack) <= 4000, "AdamPack is passed by value in the kernel arguments");
 
+__device__ __forceinline__ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// The moments and the step of one element, with explicit fused
+// multiply-adds so that every code path rounds the same way.
+__device__ __forceinline__ float adam_step(const AdamPack &pk, const smx_adamw_desc &d, float g, float &m, float &v) {
+  m = fmaf(m, pk.b1, g * pk.omb1);
+  v = fmaf(v, pk.b2, (g * g) * pk.omb2);
+  return (m / d.bias1) / (sqrtf(v / d.bias2) + pk.eps);
+}
+
+// One element of the FP32 update.
+__device__ __forceinline__ void adam_f32(const AdamPack &pk, const smx_adamw_desc &d, float g, float &m, float &v,
+                                         float &p) {
+  const float step = adam_step(pk, d, g, m, v);
+  p = fmaf(pk.neg_lr, step, p * pk.decay);
+}
+
 __global__ void __launch_bounds__(256) adamw_kernel(AdamPack pk) {
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * pk.chunk;
   const int64_t e1 = min(pk.total, e0 + pk.chunk);
@@ -38,8 +56,46 @@ __global__ void __launch_bounds__(256) adamw_kernel(AdamPack pk) {
   for (int t = 1; t < kAdamBatch; ++t) k += static_cast<int>(blockIdx.x) >= pk.first_blk[t] ? 1 : 0;
   for (; k < pk.n && pk.d[k].offset < e1; ++k) {
     const smx_adamw_desc &d = pk.d[k];
-    const int64_t lo = max(e0, d.offset) - d.offset;
+    int64_t lo = max(e0, d.offset) - d.offset;
     const int64_t hi = min(e1, d.offset + d.n) - d.offset;
+    // FP32 tensors whose block range starts on a 16-byte boundary: float4
+    // loads and stores, kAdamVec per thread in flight; the scalar loop
+    // below takes the tail.
+    if (d.param_dtype == SMX_F32 && d.grad_dtype == SMX_F32 && (lo & 3) == 0 && aligned16(d.param) &&
+        aligned16(d.grad) && aligned16(d.exp_avg) && aligned16(d.exp_avg_sq)) {
+      const int64_t lo4 = lo / 4, hi4 = hi / 4;
+      const float4 *G = static_cast<const float4 *>(d.grad);
+      float4 *P = static_cast<float4 *>(d.param);
+      float4 *M = reinterpret_cast<float4 *>(d.exp_avg);
+      float4 *V = reinterpret_cast<float4 *>(d.exp_avg_sq);
+      for (int64_t q0 = lo4 + threadIdx.x; q0 < hi4; q0 += 256 * kAdamVec) {
+        float4 g[kAdamVec], m[kAdamVec], v[kAdamVec], p[kAdamVec];
+#pragma unroll
+        for (int u = 0; u < kAdamVec; ++u) {
+          const int64_t q = q0 + 256 * u;
+          if (q < hi4) {
+            g[u] = G[q];
+            m[u] = M[q];
+            v[u] = V[q];
+            p[u] = P[q];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kAdamVec; ++u) {
+          const int64_t q = q0 + 256 * u;
+          if (q < hi4) {
+            adam_f32(pk, d, g[u].x, m[u].x, v[u].x, p[u].x);
+            adam_f32(pk, d, g[u].y, m[u].y, v[u].y, p[u].y);
+            adam_f32(pk, d, g[u].z, m[u].z, v[u].z, p[u].z);
+            adam_f32(pk, d, g[u].w, m[u].w, v[u].w, p[u].w);
+            M[q] = m[u];
+            V[q] = v[u];
+            P[q] = p[u];
+          }
+        }
+      }
+      lo = hi4 * 4;
+    }
     // kAdamUnroll elements per thread per pass, all loaded before any is
     // updated, so a block over small tensors is not one latency per element.
     for (int64_t i0 = lo + threadIdx.x; i0 < hi; i0 += 256 * kAdamUnroll) {
@@ -60,14 +116,17 @@ __global__ void __launch_bounds__(256) adamw_kernel(AdamPack pk) {
       for (int u = 0; u < kAdamUnroll; ++u) {
         const int64_t i = i0 + u * 256;
         if (i < hi) {
-          const float mu = m[u] * pk.b1 + g[u] * pk.omb1;
-          const float vu = v[u] * pk.b2 + (g[u] * g[u]) * pk.omb2;
-          d.exp_avg[i] = mu;
-          d.exp_avg_sq[i] = vu;
-          const float step = (mu / d.bias1) / (sqrtf(vu / d.bias2) + pk.eps);
           if (d.param_dtype == SMX_F32) {
-            static_cast<float *>(d.param)[i] = fmaf(pk.neg_lr, step, p[u] * pk.decay);
-          } else {
+            adam_f32(pk, d, g[u], m[u], v[u], p[u]);
+            d.exp_avg[i] = m[u];
+            d.exp_avg_sq[i] = v[u];
+            static_cast<float *>(d.param)[i] = p[u];
+            continue;
+          }
+          const float step = adam_step(pk, d, g[u], m[u], v[u]);
+          d.exp_avg[i] = m[u];
+          d.exp_avg_sq[i] = v[u];
+          {
             const int dt = d.param_dtype;
             const float p1 = round_to(dt, p[u] * pk.decay);
             store_any(d.param, dt, i, round_to(dt, fmaf(pk.neg_lr, round_to(dt, step), p1)));

@@ -8,15 +8,31 @@
 //            W -= lr * sqrt(rows) * U / max(||U||_F, FLT_MIN)
 //
 // In parameter layout the A factor always acts on columns (input channels)
-// and B on rows, whichever orientation the S8 map uses; the whiten kernel
-// writes the oriented iterate X (r x c, r <= c).
+// and B on rows, whichever orientation the S8 map uses; the whiten kernels
+// write the oriented iterate X (r x c, r <= c).
 //
-// whiten       two passes per row in one launch: momentum update,
-//              u_i = b_i sum_j S_ij a_j z_j and the row's ||V_i||^2 in closed
-//              form (||V_i||^2 = b_i^2 sum_j (S_ij a_j)^2 + (2 kappa + kappa^2 |z|^2) u_i^2);
-//              then V from (g, m', u) stored to X directly, or transposed
-//              through LDS for a transposed parameter.
-// mapback_rows u_i = sum_j Q_ij z_j and ||U_i||^2 in closed form.
+// Launch structure.  A small prep launch copies the host's per-matrix job
+// records into a table in the workspace; every row kernel then covers all
+// matrices of the call in one launch (up to kLaunchJobs), finding its job
+// from a table of first blocks in its kernel arguments.  A row is handled
+// by `wpr` waves (1, 2 or 4, so that a lane holds at most kMaxSlices float4
+// of it), a 256-thread block by 4 / wpr rows.  Sums over a matrix (||V||^2
+// for the S8 normalisation, ||U||^2 for the graft) are per-block FP64
+// partials, added in a fixed order by a one-block-per-matrix launch after
+// the row kernel.  (Adding them in the matrix's last block instead needs a
+// device-scope release per block, which on this part writes back the L2:
+// that made the whiten launch six times slower.)
+//
+// whiten        two passes per row: momentum update, u_i = b_i sum_j S_ij a_j z_j
+//               and the row's ||V_i||^2 in closed form
+//               (||V_i||^2 = b_i^2 sum_j (S_ij a_j)^2 + (2 kappa + kappa^2 |z|^2) u_i^2);
+//               then V stored to X (S a and z of the pass kept in registers).
+// whiten_flip   the same for a transposed parameter, 16 rows per block (one
+//               16-element K group of the oriented iterate), V written
+//               transposed through LDS.
+// mapback_norm  u_i = sum_j Q_ij z_j and ||U_i||^2 in closed form, from the
+//               row-sum partials that the S8 map's stage-5 apply leaves
+//               beside its result (Q itself is read once, by the apply).
 // mapback_apply W -= lr * scale * U.
 #include "s8.h"
 
@@ -29,35 +45,125 @@
 
 namespace smx {
 
+constexpr int kRowThreads = 256;   // row kernels: 4 waves
+constexpr int kMaxSlices = 3;      // float4 per lane per row kept in registers
+constexpr int kFlipRows = 16;      // transposed whiten: rows per block (one K group)
+constexpr int kFlipThreads = 64 * kFlipRows;
+constexpr int kFlipChunk = 256 * kMaxSlices;  // transposed whiten: columns per LDS chunk
+
 struct MatJob {
   smx_matrix_desc d;
-  float *pl;         // parameter-layout buffer [prow_pad][pcol_pad]
-  float *tl;         // transposed buffer [pcol_pad][prow_pad] (whiten of a transposed parameter)
-  float *u;          // [rows] rank-one row coefficients
-  double *part;      // [ceil(rows/kPartRows)] partial sums
-  double *cst;       // [2]: sum z^2, sum (a z)^2 (matrix_consts_kernel)
-  int64_t prow_pad, pcol_pad;
-  int32_t blk0;      // first block of this job in the launch
-  int32_t planes;    // whiten: write X, X^T as BF16 hi/lo planes (comp mode)
+  float *x;          // whiten: the oriented iterate ([prow_pad][pcol_pad], or for a transposed
+                     // parameter [pcol_pad][prow_pad])
+  const float *q;    // mapback: the S8 result in parameter layout ([prow_pad][pcol_pad])
+  float *u;          // [prow_pad] rank-one row coefficients
+  double *fro;       // whiten per-block partials of ||V||^2
+  double *mb;        // mapback per-block partials of ||U||^2
+  double *cst;       // kCst per-matrix scalars
+  const float **colv;  // the S8 class's slot entry for (inv_col, z)
+  const float *mrp;  // stage-5 row-sum partials (3 arrays of mrp_size) [strips][prow_pad]
+  int64_t mrp_size;
+  int32_t prow_pad, pcol_pad;
+  int32_t planes;    // whiten: X as interleaved BF16 hi/lo (comp mode)
+  int32_t wpr;       // waves per row
+  int32_t slices;    // float4 per lane over a row: ceil(cols / 4 / (64 wpr))
+  int32_t cvec;      // float4 column vectors: cols % 4 == 0, inv_col and z 16-byte aligned
+  int32_t wvec;      // whiten float4 path: cvec, F32 gradient, gradient and momentum aligned
+  int32_t mvec;      // mapback_apply float4 path: cvec, F32 parameter, aligned
+  int32_t strips;    // row-sum partials per parameter row
+  int32_t flip;      // a transposed parameter
 };
 
-constexpr int kMatBatch = 24;
-struct MatPack {
-  int32_t start[kMatBatch];  // first block of each job; INT32_MAX past the last
-  MatJob j[kMatBatch];
+constexpr int kLaunchJobs = 128;
+struct JobRange {
+  const MatJob *jobs;          // the launch's first job in the table
+  int32_t start[kLaunchJobs];  // first block of each job; INT32_MAX past the last
   int32_t n;
-  int32_t total_blocks;
 };
-static_assert(sizeof(MatPack) <= 4000, "MatPack is passed by value in the kernel arguments");
+static_assert(sizeof(JobRange) <= 4000, "JobRange is passed by value in the kernel arguments");
 
-// The job of block b: independent compares against the compact start
-// table (a few batched scalar loads, no chain of dependent lookups).
-__device__ __forceinline__ int find_job(const MatPack &p, int b) {
+// The job of block b: the number of jobs after the first whose first block
+// is <= b (start[] ascends), 16 independent compares at a time.
+__device__ __forceinline__ int find_job(const JobRange &r, int b) {
   int k = 0;
+  for (int c = 0; c < kLaunchJobs; c += 16) {
+    if (r.start[c] > b) break;
 #pragma unroll
-  for (int t = 1; t < kMatBatch; ++t) k += b >= p.start[t] ? 1 : 0;
+    for (int t = 0; t < 16; ++t) k += (c + t > 0 && b >= r.start[c + t]) ? 1 : 0;
+  }
   return k;
 }
+
+// The job as the row kernels hold it, with every pointer in the global
+// address space: a pointer read from memory (the job table) is a generic
+// pointer to the compiler, and accesses through it would be FLAT
+// instructions, which also count against the LDS / scalar wait counter and
+// address with a 64-bit VGPR pair per access.
+#define SMX_GLOBAL __attribute__((address_space(1)))
+struct DevDesc {
+  SMX_GLOBAL void *param;
+  const SMX_GLOBAL void *grad;
+  SMX_GLOBAL float *momentum;
+  const SMX_GLOBAL float *inv_row, *inv_col, *z, *kappa;
+  int64_t rows, cols;
+  double lr, momentum_beta;
+  int32_t grad_dtype, param_dtype;
+};
+struct DevJob {
+  DevDesc d;
+  SMX_GLOBAL float *x;
+  const SMX_GLOBAL float *q;
+  SMX_GLOBAL float *u;
+  SMX_GLOBAL double *fro, *mb, *cst;
+  const SMX_GLOBAL float *mrp;
+  int64_t mrp_size;
+  int64_t prow_pad, pcol_pad;
+  int32_t planes, wpr, slices, cvec, wvec, mvec, strips, flip;
+};
+
+// Copied from the table once, before any store of the kernel, so that its
+// fields stay in registers.
+__device__ __forceinline__ DevJob load_job(const MatJob *table, int jid) {
+  const MatJob J = table[jid];
+  DevJob D;
+  D.d.param = (SMX_GLOBAL void *)J.d.param;
+  D.d.grad = (const SMX_GLOBAL void *)J.d.grad;
+  D.d.momentum = (SMX_GLOBAL float *)J.d.momentum;
+  D.d.inv_row = (const SMX_GLOBAL float *)J.d.inv_row;
+  D.d.inv_col = (const SMX_GLOBAL float *)J.d.inv_col;
+  D.d.z = (const SMX_GLOBAL float *)J.d.z;
+  D.d.kappa = (const SMX_GLOBAL float *)J.d.kappa;
+  D.d.rows = J.d.rows;
+  D.d.cols = J.d.cols;
+  D.d.lr = J.d.lr;
+  D.d.momentum_beta = J.d.momentum_beta;
+  D.d.grad_dtype = J.d.grad_dtype;
+  D.d.param_dtype = J.d.param_dtype;
+  D.x = (SMX_GLOBAL float *)J.x;
+  D.q = (const SMX_GLOBAL float *)J.q;
+  D.u = (SMX_GLOBAL float *)J.u;
+  D.fro = (SMX_GLOBAL double *)J.fro;
+  D.mb = (SMX_GLOBAL double *)J.mb;
+  D.cst = (SMX_GLOBAL double *)J.cst;
+  D.mrp = (const SMX_GLOBAL float *)J.mrp;
+  D.mrp_size = J.mrp_size;
+  D.strips = J.strips;
+  D.prow_pad = J.prow_pad;
+  D.pcol_pad = J.pcol_pad;
+  D.planes = J.planes;
+  D.wpr = J.wpr;
+  D.slices = J.slices;
+  D.cvec = J.cvec;
+  D.wvec = J.wvec;
+  D.mvec = J.mvec;
+  D.flip = J.flip;
+  return D;
+}
+
+template <typename P>
+__device__ __forceinline__ float4 ld4(P p, int q) { return ((const float4 *)p)[q]; }
+template <typename P>
+__device__ __forceinline__ void st4(P p, int q, float4 v) { ((float4 *)p)[q] = v; }
 
 __device__ __forceinline__ float load_grad(const void *g, int dt, int64_t i) {
   if (dt == SMX_F32) return static_cast<const float *>(g)[i];
@@ -65,462 +171,603 @@ __device__ __forceinline__ float load_grad(const void *g, int dt, int64_t i) {
   return load_elem<SMX_F16>(g, i);
 }
 
-__device__ __forceinline__ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
-__device__ __forceinline__ float4 ld4(const float *p, int64_t q) { return reinterpret_cast<const float4 *>(p)[q]; }
-__device__ __forceinline__ void st4(float *p, int64_t q, float4 v) { reinterpret_cast<float4 *>(p)[q] = v; }
+// --------------------------------------------------------------- prep ---
+constexpr int kPrepBatch = 19;
+struct PrepPack {
+  MatJob j[kPrepBatch];
+  MatJob *table;  // destination of j[0]
+  int32_t n;
+};
+static_assert(sizeof(PrepPack) <= 4000, "PrepPack is passed by value in the kernel arguments");
+static_assert(sizeof(MatJob) % 4 == 0, "the prep kernel copies jobs as 32-bit words");
 
-// One block per job: the rank-one constants of the matrix,
-// cst = {sum_j z_j^2, sum_j (a_j z_j)^2} (FP64), used by the row kernels.
-__global__ void __launch_bounds__(256) matrix_consts_kernel(MatPack pack) {
+constexpr int kPrepThreads = 256;
+constexpr int kPrepUnroll = 12;  // loads in flight per thread (one pass over 3072 columns)
+
+// One block per job: the record into the table, and (rank-one term) the
+// constants sum z^2 and sum (a z)^2 of the matrix (FP64; each thread's
+// loads issued together).
+__global__ void __launch_bounds__(kPrepThreads) matrix_prep_kernel(PrepPack pack) {
   __shared__ double scratch[16];
   const MatJob &J = pack.j[blockIdx.x];
-  const smx_matrix_desc &d = J.d;
-  if (d.z == nullptr) return;
+  const uint32_t *src = reinterpret_cast<const uint32_t *>(&J);
+  uint32_t *dst = reinterpret_cast<uint32_t *>(pack.table + blockIdx.x);
+  for (int k = threadIdx.x; k < static_cast<int>(sizeof(MatJob) / 4); k += kPrepThreads) dst[k] = src[k];
+  if (threadIdx.x == 0) {
+    // the column vectors of the slot, for the stage-5 row sums of the S8 map
+    J.colv[0] = J.d.inv_col;
+    J.colv[1] = J.d.z;
+  }
+  if (J.d.z == nullptr) return;  // uniform per block
+  const SMX_GLOBAL float *zp = (const SMX_GLOBAL float *)J.d.z, *ap = (const SMX_GLOBAL float *)J.d.inv_col;
   double zz = 0.0, az = 0.0;
-  for (int64_t j = threadIdx.x; j < d.cols; j += blockDim.x) {
-    const double z = d.z[j], a = d.inv_col[j];
-    zz += z * z;
-    az += (a * z) * (a * z);
+  for (int64_t j0 = threadIdx.x; j0 < J.d.cols; j0 += kPrepThreads * kPrepUnroll) {
+    float z[kPrepUnroll], a[kPrepUnroll];
+#pragma unroll
+    for (int u = 0; u < kPrepUnroll; ++u) {
+      const int64_t j = j0 + kPrepThreads * u;
+      z[u] = j < J.d.cols ? zp[j] : 0.f;
+      a[u] = j < J.d.cols ? ap[j] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kPrepUnroll; ++u) {
+      const double zd = z[u], t = static_cast<double>(a[u]) * zd;
+      zz += zd * zd;
+      az += t * t;
+    }
   }
   zz = block_sum(zz, scratch);
   az = block_sum(az, scratch);
   if (threadIdx.x == 0) {
-    J.cst[0] = zz;
-    J.cst[1] = az;
+    SMX_GLOBAL double *cst = (SMX_GLOBAL double *)J.cst;
+    cst[kCstZZ] = zz;
+    cst[kCstAZ] = az;
   }
 }
 
-// The row kernels run one wave per row.  Per-row reductions use FP32 lane
-// partials and an FP32 wave sum; rows are accumulated in FP64, one partial
-// per kPartRows rows.
-constexpr int kRowThreads = 64 * kRowsPerPart;  // the largest block (16 rows)
-constexpr int kMapThreads = 64 * kPartRows;     // mapback blocks (4 rows)
-constexpr int kRowUnroll = 4;  // float4 columns per lane whose loads are in flight together
+// Blocks per matrix of the row kernels (host MatJob or device DevJob).
+template <typename Job>
+__host__ __device__ inline int64_t whiten_blocks(const Job &j) {
+  return j.flip ? j.prow_pad / kFlipRows : j.prow_pad / (4 / j.wpr);
+}
+template <typename Job>
+__host__ __device__ inline int64_t mapback_blocks(const Job &j) { return ceil_div(j.d.rows, 4 / j.wpr); }
+template <typename Job>
+__host__ __device__ inline int64_t norm_blocks(const Job &j) { return ceil_div(j.d.rows, kRowThreads / 4); }
 
-// FP64 sum of the NW per-wave row partials, in wave order; the result is
-// valid in thread 0.
-template <int NW>
-__device__ __forceinline__ double sum_wave_parts(double part, double *wave_part) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) wave_part[wave] = part;
-  __syncthreads();
-  double t = 0.0;
-  if (threadIdx.x == 0)
-    for (int w = 0; w < NW; ++w) t += wave_part[w];
-  return t;
+// One 64-thread block per job: the FP64 sum of the job's per-block
+// partials (lane l takes partials l, l + 64, ..., then a fixed-order wave
+// sum) -> ||V||^2 (which = kCstFro, after the whiten) or ||U||^2 (kCstU,
+// after mapback_norm).
+__global__ void __launch_bounds__(64) matrix_total_kernel(const MatJob *jobs, int which) {
+  const DevJob J = load_job(jobs, blockIdx.x);
+  const bool fro = which == kCstFro;
+  const SMX_GLOBAL double *parts = fro ? J.fro : J.mb;
+  const int64_t nblk = fro ? whiten_blocks(J) : norm_blocks(J);
+  constexpr int kU = 8;  // loads in flight per lane
+  double s = 0.0;
+  for (int64_t k0 = threadIdx.x; k0 < nblk; k0 += 64 * kU) {
+    double v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) v[u] = k0 + 64 * u < nblk ? parts[k0 + 64 * u] : 0.0;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) s += v[u];
+  }
+  s = wave_sum(s);
+  if (threadIdx.x == 0) J.cst[which] = s;
 }
 
 // ------------------------------------------------------------- whiten ---
-// One wave per row of the padded parameter layout (blocks of 4 rows, or 16
-// for a transposed parameter), two passes over the row:
-//  1. momentum m' = b m + (1-b) g (in place), u_i = b_i sum_j S_ij a_j z_j
-//     and the row's ||V_i||^2 (closed form) for S = b m' + (1-b) g;
-//  2. V_ij = b_i S_ij a_j + kappa u_i z_j stored in operand form to the
-//     oriented iterate: row i of X directly (pl), or, for a transposed
-//     parameter (tl), through LDS in chunks of kWhitenChunk columns, where
-//     the block's 16 rows are one 16-element K group of each X row.
-// KEEP > 0 (rows of at most KEEP * kWhitenChunk columns, FP32 gradients,
-// 16-byte aligned): pass 1 keeps S of the lane's columns in registers and
-// pass 2 reads it from there; KEEP = 0: pass 2 reads g and m' again (the
-// row was just read, so mostly from cache).  Both give the same bits.
-// Rows and columns of the padding are written as zeros.
-constexpr int kWhitenChunk = 1024;  // = 4 * 64 * kRowUnroll
-// Most column chunks a row keeps in registers: 4 for parameters kept as
-// they are (256-thread blocks, up to ~170 VGPRs), 1 for transposed ones
-// (1024-thread blocks hold at most 128 VGPRs per lane).
-constexpr int kWhitenKeep = 4;
-constexpr int kWhitenKeepFlip = 1;
+// Row geometry of a block: 4 / wpr rows, wave w on row w / wpr, covering
+// float4 wr * 64 + lane + 64 wpr t (wr = w % wpr, slice t) of it.
+// The row and the wave's place in it are wave-uniform (scalar registers,
+// so row base addresses are too); offsets within a row are 32-bit.
+struct RowPos {
+  int64_t i;    // parameter row
+  int q0;       // this lane's first float4 of the row
+  int span;     // float4 between a lane's slices
+  int wr, rib;  // wave within the row, row within the block
+};
+__device__ __forceinline__ RowPos row_pos(const DevJob &J, int blk) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = J.wpr;
+  RowPos p;
+  p.rib = wave / W;
+  p.wr = wave % W;
+  p.i = static_cast<int64_t>(blk) * (4 / W) + p.rib;
+  p.q0 = p.wr * 64 + lane;
+  p.span = 64 * W;
+  return p;
+}
 
-// Rows per block: a transposed parameter needs 16 (one K group of every X
-// row); the others take kPartRows, so that more, shorter blocks share a CU.
-template <bool FLIP>
-constexpr int whiten_rows_per_block() { return FLIP ? kRowsPerPart : kPartRows; }
-
-template <bool R1, bool FLIP, int KEEP>
-__global__ void __launch_bounds__(64 * whiten_rows_per_block<FLIP>()) whiten_kernel(MatPack pack) {
-  constexpr int RB = whiten_rows_per_block<FLIP>();
-  static_assert(kRowsPerPart == 16 && kRowThreads == 1024, "one 16-row K group per transposed block, 4 lanes per X row");
-  static_assert(RB % kPartRows == 0, "whole partials per block");
-  __shared__ double wave_part[RB];
-  __shared__ float tile[FLIP ? kRowsPerPart : 1][FLIP ? kWhitenChunk + 4 : 1];
-  const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
-  const smx_matrix_desc &d = J.d;
-  const int blk = blockIdx.x - J.blk0;
-  constexpr bool r1 = R1;
-  const double zz = r1 ? J.cst[0] : 0.0;
-  const float kappa = r1 ? d.kappa[0] : 0.f;
-  const double corr = r1 ? 2.0 * kappa + static_cast<double>(kappa) * kappa * zz : 0.0;
-  const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool vec = d.grad_dtype == SMX_F32 && d.cols % 4 == 0 && aligned16(d.grad) && aligned16(d.momentum) &&
-                   aligned16(d.inv_col) && (!r1 || aligned16(d.z));
-  const bool planes = J.planes != 0;
-  const int64_t i0 = static_cast<int64_t>(blk) * RB;
-  const int64_t i = i0 + wave;
-  const bool live = i < d.rows;
-  float *mrow = live ? d.momentum + i * d.cols : nullptr;
-  const float *grow = live && vec ? static_cast<const float *>(d.grad) + i * d.cols : nullptr;
-  // S of this lane's columns: chunk k, float4 u covers columns
-  // 4 lane + 4 * 64 u + kWhitenChunk k (pass 1's and pass 2's mapping).
-  const bool kept = KEEP > 0 && vec && d.cols <= static_cast<int64_t>(KEEP) * kWhitenChunk;
-  float4 sk[KEEP > 0 ? KEEP : 1][kRowUnroll];
-
-  // ---- pass 1
-  double part = 0.0;
-  float b = 0.f, ku = 0.f;
-  if (live) {
-    float y2 = 0.f, yz = 0.f;
-    if (vec) {
-      const int64_t n4 = d.cols / 4;
-      // One chunk of kRowUnroll float4 per lane; S goes to keep_s.
-      auto chunk = [&](int64_t q0, float4 (&keep_s)[kRowUnroll]) {
-        // Every load of the chunk is issued before the first store.
-        float4 g[kRowUnroll], m[kRowUnroll], a[kRowUnroll], z[kRowUnroll];
+// Sums of a row over its waves (the same value in every wave of the row):
+// red[wave][k] holds each wave's partials; fixed order over the waves.
+template <int N>
+__device__ __forceinline__ void row_sums(double (&v)[N], double (*red)[4], const RowPos &p, int W) {
+  if (W == 1) return;  // uniform per block
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0)
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u) {
-          const int64_t q = q0 + 64 * u;
-          if (q < n4) {
-            g[u] = ld4(grow, q);
-            m[u] = ld4(mrow, q);
-            a[u] = ld4(d.inv_col, q);
-            if constexpr (R1) z[u] = ld4(d.z, q);
+    for (int k = 0; k < N; ++k) red[wave][k] = v[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    double s = 0.0;
+    for (int w = 0; w < W; ++w) s += red[p.rib * W + w][k];
+    v[k] = s;
+  }
+}
+
+// The block's partial (its rows in order) -> parts[blk].
+__device__ __forceinline__ void block_part(const DevJob &J, double row_part, const RowPos &p, int blk,
+                                           SMX_GLOBAL double *parts, double *rp) {
+  if ((threadIdx.x & 63) == 0 && p.wr == 0) rp[p.rib] = row_part;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int r = 0; r < 4 / J.wpr; ++r) t += rp[r];
+    parts[blk] = t;
+  }
+}
+
+template <bool R1>
+__global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
+  __shared__ double red[4][4];  // row_sums
+  __shared__ double rp[4];
+  const int jid = find_job(range, blockIdx.x);
+  const DevJob J = load_job(range.jobs, jid);
+  const DevDesc &d = J.d;
+  const int blk = blockIdx.x - range.start[jid];
+  const RowPos p = row_pos(J, blk);
+  const int lane = threadIdx.x & 63;
+  const bool live = p.i < d.rows;
+  const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
+  const float kappa = R1 ? d.kappa[0] : 0.f;
+  const bool planes = J.planes != 0;
+  SMX_GLOBAL float *mrow = live ? d.momentum + p.i * d.cols : nullptr;
+  SMX_GLOBAL float *xrow = J.x + p.i * J.pcol_pad;
+  const int pc4 = static_cast<int>(J.pcol_pad / 4);
+
+  // sum z^2 of the rank-one term (the prep launch)
+  const double zz = R1 ? J.cst[kCstZZ] : 0.0;
+
+  // ---- pass 1: m' (stored), y = S a of the lane's columns, and the row's
+  // sum y^2 and y.z.
+  float y2 = 0.f, yz = 0.f;
+  float4 yk[kMaxSlices];
+  const bool kept = J.wvec && J.slices <= kMaxSlices;  // uniform per block
+  if (J.wvec) {
+    const int n4 = static_cast<int>(d.cols / 4);
+    const SMX_GLOBAL float *grow = live ? (const SMX_GLOBAL float *)d.grad + p.i * d.cols : nullptr;
+    // Slices [t0, t0 + kMaxSlices) of the row; y goes to yk.
+    auto pass1 = [&](int t0) {
+      float4 g[kMaxSlices], m[kMaxSlices], a[kMaxSlices], z[kMaxSlices];
+#pragma unroll
+      for (int t = 0; t < kMaxSlices; ++t) {
+        const int q = p.q0 + p.span * (t0 + t);
+        if (q < n4) {
+          a[t] = ld4(d.inv_col, q);
+          if constexpr (R1) z[t] = ld4(d.z, q);
+          if (live) {
+            g[t] = ld4(grow, q);
+            m[t] = ld4(mrow, q);
           }
         }
+      }
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u) {
-          const int64_t q = q0 + 64 * u;
-          if (q < n4) {
-            float4 mm = m[u];
-            const float4 gg = g[u], aa = a[u];
+      for (int t = 0; t < kMaxSlices; ++t) {
+        const int q = p.q0 + p.span * (t0 + t);
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f), zz4 = y;
+        if (q < n4) {
+          const float4 aa = a[t];
+          if constexpr (R1) zz4 = z[t];
+          if (live) {
+            float4 mm = m[t];
+            const float4 gg = g[t];
             mm.x = fmaf(mm.x, beta, gg.x * omb); mm.y = fmaf(mm.y, beta, gg.y * omb);
             mm.z = fmaf(mm.z, beta, gg.z * omb); mm.w = fmaf(mm.w, beta, gg.w * omb);
             st4(mrow, q, mm);
-            const float s0 = fmaf(mm.x, beta, gg.x * omb), s1 = fmaf(mm.y, beta, gg.y * omb);
-            const float s2 = fmaf(mm.z, beta, gg.z * omb), s3 = fmaf(mm.w, beta, gg.w * omb);
-            keep_s[u] = make_float4(s0, s1, s2, s3);
-            const float y0 = s0 * aa.x, y1 = s1 * aa.y;
-            const float y2_ = s2 * aa.z, y3 = s3 * aa.w;
-            y2 = fmaf(y0, y0, fmaf(y1, y1, fmaf(y2_, y2_, fmaf(y3, y3, y2))));
-            if constexpr (R1) {
-              const float4 zz4 = z[u];
-              yz = fmaf(y0, zz4.x, fmaf(y1, zz4.y, fmaf(y2_, zz4.z, fmaf(y3, zz4.w, yz))));
-            }
-          } else {
-            keep_s[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            y.x = fmaf(mm.x, beta, gg.x * omb) * aa.x; y.y = fmaf(mm.y, beta, gg.y * omb) * aa.y;
+            y.z = fmaf(mm.z, beta, gg.z * omb) * aa.z; y.w = fmaf(mm.w, beta, gg.w * omb) * aa.w;
+            y2 = fmaf(y.x, y.x, fmaf(y.y, y.y, fmaf(y.z, y.z, fmaf(y.w, y.w, y2))));
+            if constexpr (R1) yz = fmaf(y.x, zz4.x, fmaf(y.y, zz4.y, fmaf(y.z, zz4.z, fmaf(y.w, zz4.w, yz))));
           }
         }
-      };
-      if (kept) {
-#pragma unroll
-        for (int k = 0; k < (KEEP > 0 ? KEEP : 1); ++k) chunk(lane + 64 * kRowUnroll * k, sk[k]);
-      } else {
-        for (int64_t q0 = lane; q0 < n4; q0 += 64 * kRowUnroll) chunk(q0, sk[0]);
-      }
-    } else {
-      for (int64_t j = lane; j < d.cols; j += 64) {
-        const float g = load_grad(d.grad, d.grad_dtype, i * d.cols + j);
-        const float m = fmaf(mrow[j], beta, g * omb);
-        mrow[j] = m;
-        const float y = fmaf(m, beta, g * omb) * d.inv_col[j];
-        y2 = fmaf(y, y, y2);
-        if (r1) yz = fmaf(y, d.z[j], yz);
-      }
-    }
-    const double Y2 = wave_sum(y2);
-    const double YZ = wave_sum(yz);
-    const double bd = d.inv_row[i];
-    const double u = bd * YZ;
-    b = d.inv_row[i];
-    ku = r1 ? kappa * static_cast<float>(u) : 0.f;
-    if (lane == 0) {
-      J.u[i] = static_cast<float>(u);
-      part = bd * bd * Y2 + corr * u * u;
-    }
-  }
-  // ---- pass 2: V of the row, kRowUnroll groups of four consecutive
-  // columns at a time, every load of a batch issued before the arithmetic.
-  auto batch = [&](int64_t j0, int64_t stride, float (&v)[kRowUnroll][4]) {
-    if (live && vec) {
-      float4 g[kRowUnroll], m[kRowUnroll], a[kRowUnroll], z[kRowUnroll];
-#pragma unroll
-      for (int u = 0; u < kRowUnroll; ++u) {
-        const int64_t j = j0 + stride * u;
-        if (j < d.cols) {
-          g[u] = ld4(grow, j / 4);
-          m[u] = ld4(mrow, j / 4);
-          a[u] = ld4(d.inv_col, j / 4);
-          if constexpr (R1) z[u] = ld4(d.z, j / 4);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kRowUnroll; ++u) {
-        const int64_t j = j0 + stride * u;
-        const float gs[4] = {g[u].x, g[u].y, g[u].z, g[u].w}, ms[4] = {m[u].x, m[u].y, m[u].z, m[u].w};
-        const float as[4] = {a[u].x, a[u].y, a[u].z, a[u].w};
-        float zs[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (R1) {
-          zs[0] = z[u].x; zs[1] = z[u].y; zs[2] = z[u].z; zs[3] = z[u].w;
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float s = fmaf(ms[e], beta, gs[e] * omb);
-          float x = (s * b) * as[e];
-          if constexpr (R1) x = fmaf(ku, zs[e], x);
-          v[u][e] = j < d.cols ? x : 0.f;
-        }
-      }
-      return;
-    }
-#pragma unroll
-    for (int u = 0; u < kRowUnroll; ++u) {
-      const int64_t j = j0 + stride * u;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[u][e] = 0.f;
-        if (live && j + e < d.cols) {
-          const float g = load_grad(d.grad, d.grad_dtype, i * d.cols + j + e);
-          const float s = fmaf(mrow[j + e], beta, g * omb);
-          v[u][e] = (s * b) * d.inv_col[j + e];
-          if constexpr (R1) v[u][e] = fmaf(ku, d.z[j + e], v[u][e]);
-        }
-      }
-    }
-  };
-  // The same with S from the registers of pass 1 (chunk k of the lane).
-  auto batch_kept = [&](int k, int64_t j0, float (&v)[kRowUnroll][4]) {
-    float4 a[kRowUnroll], z[kRowUnroll];
-#pragma unroll
-    for (int u = 0; u < kRowUnroll; ++u) {
-      const int64_t j = j0 + 4 * 64 * u;
-      if (j < d.cols) {
-        a[u] = ld4(d.inv_col, j / 4);
-        if constexpr (R1) z[u] = ld4(d.z, j / 4);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kRowUnroll; ++u) {
-      const int64_t j = j0 + 4 * 64 * u;
-      const float4 sv = sk[KEEP > 0 ? k : 0][u];
-      const float ss[4] = {sv.x, sv.y, sv.z, sv.w};
-      float as[4] = {0.f, 0.f, 0.f, 0.f}, zs[4] = {0.f, 0.f, 0.f, 0.f};
-      if (j < d.cols) {
-        as[0] = a[u].x; as[1] = a[u].y; as[2] = a[u].z; as[3] = a[u].w;
-        if constexpr (R1) {
-          zs[0] = z[u].x; zs[1] = z[u].y; zs[2] = z[u].z; zs[3] = z[u].w;
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float x = (ss[e] * b) * as[e];
-        if constexpr (R1) x = fmaf(ku, zs[e], x);
-        v[u][e] = live && j < d.cols ? x : 0.f;
-      }
-    }
-  };
-  if constexpr (!FLIP) {
-    auto store = [&](int64_t j0, const float (&v)[kRowUnroll][4]) {
-#pragma unroll
-      for (int u = 0; u < kRowUnroll; ++u) {
-        const int64_t j = j0 + 4 * 64 * u;
-        if (j < J.pcol_pad) put_operand4(J.pl, i * J.pcol_pad + j, v[u], planes);
+        yk[t] = y;
       }
     };
-    if (kept) {
+    for (int t0 = 0; t0 < J.slices; t0 += kMaxSlices) pass1(t0);
+  } else {
+    for (int j = p.q0; j < d.cols; j += p.span) {
+      const float a = d.inv_col[j];
+      float zj = 0.f;
+      if constexpr (R1) zj = d.z[j];
+      if (live) {
+        const float g = load_grad((const void *)d.grad, d.grad_dtype, p.i * d.cols + j);
+        const float m = fmaf(mrow[j], beta, g * omb);
+        mrow[j] = m;
+        const float y = fmaf(m, beta, g * omb) * a;
+        y2 = fmaf(y, y, y2);
+        if constexpr (R1) yz = fmaf(y, zj, yz);
+      }
+    }
+  }
+  double v[2] = {static_cast<double>(wave_sum(y2)), static_cast<double>(wave_sum(yz))};
+  row_sums<2>(v, red, p, J.wpr);
+  const double corr = R1 ? 2.0 * kappa + static_cast<double>(kappa) * kappa * zz : 0.0;
+  double row_part = 0.0;
+  float b = 0.f, ku = 0.f;
+  if (live) {
+    const double bd = d.inv_row[p.i];
+    const double u = bd * v[1];
+    b = d.inv_row[p.i];
+    ku = R1 ? kappa * static_cast<float>(u) : 0.f;
+    row_part = bd * bd * v[0] + corr * u * u;
+    if (lane == 0 && p.wr == 0) J.u[p.i] = static_cast<float>(u);
+  }
+
+  // ---- pass 2: V_ij = b_i y_j + kappa u_i z_j (zeros in padding rows and
+  // columns) in operand form.
+  if (kept) {
+    // z again (a cached vector) rather than held through the row sums
+    const int n4 = static_cast<int>(d.cols / 4);
+    float4 zk[kMaxSlices];
 #pragma unroll
-      for (int k = 0; k < (KEEP > 0 ? KEEP : 1); ++k) {
-        const int64_t j0 = 4 * lane + static_cast<int64_t>(kWhitenChunk) * k;
-        if (j0 < J.pcol_pad) {
-          float v[kRowUnroll][4];
-          batch_kept(k, j0, v);
-          store(j0, v);
+    for (int t = 0; t < kMaxSlices; ++t) {
+      const int q = p.q0 + p.span * t;
+      zk[t] = R1 && live && t < J.slices && q < n4 ? ld4(d.z, q) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int t = 0; t < kMaxSlices; ++t) {
+      const int q = p.q0 + p.span * t;
+      if (t < J.slices && q < pc4) {
+        float w[4] = {0.f, 0.f, 0.f, 0.f};
+        if (live && q < n4) {
+          const float4 y = yk[t], z = zk[t];
+          w[0] = fmaf(ku, z.x, b * y.x); w[1] = fmaf(ku, z.y, b * y.y);
+          w[2] = fmaf(ku, z.z, b * y.z); w[3] = fmaf(ku, z.w, b * y.w);
+        }
+        put_operand4((float *)xrow, 4 * q, w, planes);
+      }
+    }
+  } else if (J.wvec) {
+    // Wide rows: m' and g again (the row was just read and written).
+    const int n4 = static_cast<int>(d.cols / 4);
+    const SMX_GLOBAL float *grow = live ? (const SMX_GLOBAL float *)d.grad + p.i * d.cols : nullptr;
+    for (int q0 = p.q0; q0 < pc4; q0 += p.span * kMaxSlices) {
+      float4 g[kMaxSlices], m[kMaxSlices], a[kMaxSlices], z[kMaxSlices];
+#pragma unroll
+      for (int t = 0; t < kMaxSlices; ++t) {
+        const int q = q0 + p.span * t;
+        if (live && q < n4) {
+          g[t] = ld4(grow, q);
+          m[t] = ld4(mrow, q);
+          a[t] = ld4(d.inv_col, q);
+          if constexpr (R1) z[t] = ld4(d.z, q);
         }
       }
-    } else {
-      for (int64_t j0 = 4 * lane; j0 < J.pcol_pad; j0 += 4 * 64 * kRowUnroll) {
-        float v[kRowUnroll][4];
-        batch(j0, 4 * 64, v);
-        store(j0, v);
+#pragma unroll
+      for (int t = 0; t < kMaxSlices; ++t) {
+        const int q = q0 + p.span * t;
+        if (q >= pc4) continue;
+        float w[4] = {0.f, 0.f, 0.f, 0.f};
+        if (live && q < n4) {
+          const float gs[4] = {g[t].x, g[t].y, g[t].z, g[t].w}, ms[4] = {m[t].x, m[t].y, m[t].z, m[t].w};
+          const float as[4] = {a[t].x, a[t].y, a[t].z, a[t].w};
+          float zs[4] = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (R1) {
+            zs[0] = z[t].x; zs[1] = z[t].y; zs[2] = z[t].z; zs[3] = z[t].w;
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = fmaf(ku, zs[e], b * (fmaf(ms[e], beta, gs[e] * omb) * as[e]));
+        }
+        put_operand4((float *)xrow, 4 * q, w, planes);
       }
     }
   } else {
-    static_assert(kWhitenChunk == 4 * 64 * kRowUnroll, "one batch per lane fills a chunk row");
-    const int qq = threadIdx.x & 3;  // 4-row quarter of the K group
-    // `kept` is uniform per block (one job per block), so the chunk loop and
-    // its barriers are too.
-    for (int64_t c0 = 0; c0 < J.pcol_pad; c0 += kWhitenChunk) {
-      float v[kRowUnroll][4];
-      if (kept) {
-        const int k = static_cast<int>(c0 / kWhitenChunk);
-#pragma unroll
-        for (int kk = 0; kk < (KEEP > 0 ? KEEP : 1); ++kk)
-          if (kk == k) batch_kept(kk, c0 + 4 * lane, v);
-      } else {
-        batch(c0 + 4 * lane, 4 * 64, v);
+    for (int j = p.q0; j < J.pcol_pad; j += p.span) {
+      float x = 0.f;
+      if (live && j < d.cols) {
+        const float g = load_grad((const void *)d.grad, d.grad_dtype, p.i * d.cols + j);
+        const float y = fmaf(mrow[j], beta, g * omb) * d.inv_col[j];
+        x = b * y;
+        if constexpr (R1) x = fmaf(ku, d.z[j], x);
       }
-#pragma unroll
-      for (int u = 0; u < kRowUnroll; ++u)
-        *reinterpret_cast<float4 *>(&tile[wave][4 * (lane + 64 * u)]) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
-      __syncthreads();
-#pragma unroll
-      for (int r = 0; r < kWhitenChunk / 256; ++r) {
-        const int jj = (threadIdx.x >> 2) + 256 * r;  // X row in the chunk
-        if (c0 + jj < J.pcol_pad) {
-          const float w[4] = {tile[4 * qq][jj], tile[4 * qq + 1][jj], tile[4 * qq + 2][jj], tile[4 * qq + 3][jj]};
-          put_operand4(J.tl, (c0 + jj) * J.prow_pad + i0 + 4 * qq, w, planes);
-        }
-      }
-      __syncthreads();
+      put_operand((float *)xrow, j, x, planes);
     }
   }
-  // The partials of ||V||^2 (one per kPartRows rows, waves in order), after
-  // pass 2 so that no barrier separates the passes.
-  if (lane == 0) wave_part[wave] = part;
-  __syncthreads();
-  if (threadIdx.x < RB / kPartRows) {
-    const int p = threadIdx.x;
-    const int64_t r0 = i0 + p * kPartRows;
-    if (r0 < d.rows) {
-      double t = 0.0;
-      for (int w = 0; w < kPartRows; ++w) t += wave_part[p * kPartRows + w];
-      J.part[r0 / kPartRows] = t;
+  block_part(J, row_part, p, blk, J.fro, rp);
+}
+
+// Transposed parameters: one wave per row, kFlipRows rows per block, the
+// row in chunks of kFlipChunk columns (kMaxSlices float4 per lane); pass 1
+// keeps y = S a when the row is one chunk (KEPT, a launch of its own), else
+// pass 2 reads g and m' again.  Pass 2 stages each chunk of V in LDS: the block's 16 rows are
+// one 16-element K group of every X row of the chunk, written as 64-byte
+// runs (4 lanes per X row).
+template <bool R1, bool KEPT>
+__global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange range) {
+  __shared__ float tile[kFlipRows][kFlipChunk + 4];
+  __shared__ double rp[kFlipRows];
+  const int jid = find_job(range, blockIdx.x);
+  const DevJob J = load_job(range.jobs, jid);
+  const DevDesc &d = J.d;
+  const int blk = blockIdx.x - range.start[jid];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the row: wave-uniform
+  const int64_t i0 = static_cast<int64_t>(blk) * kFlipRows;
+  const int64_t i = i0 + wave;
+  const bool live = i < d.rows;
+  const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
+  const float kappa = R1 ? d.kappa[0] : 0.f;
+  const bool planes = J.planes != 0;
+  SMX_GLOBAL float *mrow = live ? d.momentum + i * d.cols : nullptr;
+  const bool vec = J.wvec != 0;
+  constexpr bool kept = KEPT;  // the host's bucket: vec && cols <= kFlipChunk
+  const int n4 = static_cast<int>(d.cols / 4);
+  const SMX_GLOBAL float *grow = live && vec ? (const SMX_GLOBAL float *)d.grad + i * d.cols : nullptr;
+  const double zz = R1 ? J.cst[kCstZZ] : 0.0;
+  const float b = live ? d.inv_row[i] : 0.f;
+  // Slice t of chunk c of this lane: float4 c * kFlipChunk / 4 + lane + 64 t.
+  // KEPT: pass 1 leaves b y = b S a of its row in the LDS tile, and pass 2
+  // adds kappa u z there.
+  float y2 = 0.f, yz = 0.f;
+  if (vec) {
+    // Two slices' loads in flight at a time: with kMaxSlices at once the
+    // 1024-thread block needs more than 64 VGPRs, and a CU then holds one
+    // block instead of two.
+    constexpr int kB = 2;
+    for (int c4 = 0; c4 < n4; c4 += kFlipChunk / 4) {
+#pragma unroll
+      for (int t0 = 0; t0 < kMaxSlices; t0 += kB) {
+      float4 g[kB], m[kB], a[kB], z[kB];
+#pragma unroll
+      for (int tb = 0; tb < kB; ++tb) {
+        const int q = c4 + lane + 64 * (t0 + tb);
+        if (t0 + tb < kMaxSlices && q < n4) {
+          a[tb] = ld4(d.inv_col, q);
+          if constexpr (R1) z[tb] = ld4(d.z, q);
+          if (live) {
+            g[tb] = ld4(grow, q);
+            m[tb] = ld4(mrow, q);
+          }
+        }
+      }
+#pragma unroll
+      for (int tb = 0; tb < kB; ++tb) {
+        const int t = t0 + tb;
+        if (t >= kMaxSlices) continue;
+        const int q = c4 + lane + 64 * t;
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (q < n4 && live) {
+          const float4 aa = a[tb], gg = g[tb];
+          float4 mm = m[tb];
+          mm.x = fmaf(mm.x, beta, gg.x * omb); mm.y = fmaf(mm.y, beta, gg.y * omb);
+          mm.z = fmaf(mm.z, beta, gg.z * omb); mm.w = fmaf(mm.w, beta, gg.w * omb);
+          st4(mrow, q, mm);
+          y.x = fmaf(mm.x, beta, gg.x * omb) * aa.x; y.y = fmaf(mm.y, beta, gg.y * omb) * aa.y;
+          y.z = fmaf(mm.z, beta, gg.z * omb) * aa.z; y.w = fmaf(mm.w, beta, gg.w * omb) * aa.w;
+          y2 = fmaf(y.x, y.x, fmaf(y.y, y.y, fmaf(y.z, y.z, fmaf(y.w, y.w, y2))));
+          if constexpr (R1) {
+            const float4 zz4 = z[tb];
+            yz = fmaf(y.x, zz4.x, fmaf(y.y, zz4.y, fmaf(y.z, zz4.z, fmaf(y.w, zz4.w, yz))));
+          }
+        }
+        if constexpr (KEPT)
+          *reinterpret_cast<float4 *>(&tile[wave][4 * (lane + 64 * t)]) =
+              make_float4(b * y.x, b * y.y, b * y.z, b * y.w);
+      }
+      }
     }
+  } else {
+    for (int j = lane; j < d.cols; j += 64) {
+      const float a = d.inv_col[j];
+      float zj = 0.f;
+      if constexpr (R1) zj = d.z[j];
+      if (live) {
+        const float g = load_grad((const void *)d.grad, d.grad_dtype, i * d.cols + j);
+        const float m = fmaf(mrow[j], beta, g * omb);
+        mrow[j] = m;
+        const float y = fmaf(m, beta, g * omb) * a;
+        y2 = fmaf(y, y, y2);
+        if constexpr (R1) yz = fmaf(y, zj, yz);
+      }
+    }
+  }
+  const double Y2 = wave_sum(y2), YZ = wave_sum(yz);
+  const double corr = R1 ? 2.0 * kappa + static_cast<double>(kappa) * kappa * zz : 0.0;
+  double row_part = 0.0;
+  float ku = 0.f;
+  if (live) {
+    const double bd = b;
+    const double u = bd * YZ;
+    ku = R1 ? kappa * static_cast<float>(u) : 0.f;
+    row_part = bd * bd * Y2 + corr * u * u;
+    if (lane == 0) J.u[i] = static_cast<float>(u);
+  }
+
+  // ---- pass 2, chunk by chunk through LDS.
+  const int qq = threadIdx.x & 3;  // 4-row quarter of the K group
+  for (int c0 = 0; c0 < J.pcol_pad; c0 += kFlipChunk) {
+    const int c4 = c0 / 4;
+    if constexpr (KEPT) {
+      // one chunk (pcol_pad <= kFlipChunk): the tile row holds b y
+      if constexpr (R1) {
+#pragma unroll
+        for (int t = 0; t < kMaxSlices; ++t) {
+          const int q = lane + 64 * t;
+          if (live && q < n4) {
+            float4 *v = reinterpret_cast<float4 *>(&tile[wave][4 * q]);
+            const float4 z = ld4(d.z, q);
+            float4 w = *v;
+            w.x = fmaf(ku, z.x, w.x); w.y = fmaf(ku, z.y, w.y); w.z = fmaf(ku, z.z, w.z); w.w = fmaf(ku, z.w, w.w);
+            *v = w;
+          }
+        }
+      }
+    } else {
+    float4 g[kMaxSlices], m[kMaxSlices], a[kMaxSlices], z[kMaxSlices];
+#pragma unroll
+    for (int t = 0; t < kMaxSlices; ++t) {
+      const int q = c4 + lane + 64 * t;
+      if (vec && live && q < n4) {
+        if constexpr (R1) z[t] = ld4(d.z, q);
+        g[t] = ld4(grow, q);
+        m[t] = ld4(mrow, q);
+        a[t] = ld4(d.inv_col, q);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kMaxSlices; ++t) {
+      const int q = c4 + lane + 64 * t;
+      const int j = 4 * q;
+      float w[4] = {0.f, 0.f, 0.f, 0.f};
+      if (live && j < d.cols) {
+        if (vec) {
+          float4 y;
+          y.x = fmaf(m[t].x, beta, g[t].x * omb) * a[t].x; y.y = fmaf(m[t].y, beta, g[t].y * omb) * a[t].y;
+          y.z = fmaf(m[t].z, beta, g[t].z * omb) * a[t].z; y.w = fmaf(m[t].w, beta, g[t].w * omb) * a[t].w;
+          float4 zz4 = make_float4(0.f, 0.f, 0.f, 0.f);
+          if constexpr (R1) zz4 = z[t];
+          w[0] = fmaf(ku, zz4.x, b * y.x); w[1] = fmaf(ku, zz4.y, b * y.y);
+          w[2] = fmaf(ku, zz4.z, b * y.z); w[3] = fmaf(ku, zz4.w, b * y.w);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (j + e < d.cols) {
+              const float gv = load_grad((const void *)d.grad, d.grad_dtype, i * d.cols + j + e);
+              float x = b * (fmaf(mrow[j + e], beta, gv * omb) * d.inv_col[j + e]);
+              if constexpr (R1) x = fmaf(ku, d.z[j + e], x);
+              w[e] = x;
+            }
+          }
+        }
+      }
+      *reinterpret_cast<float4 *>(&tile[wave][4 * (lane + 64 * t)]) = make_float4(w[0], w[1], w[2], w[3]);
+    }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kFlipChunk / 256; ++r) {
+      const int jj = (threadIdx.x >> 2) + 256 * r;  // X row in the chunk
+      if (c0 + jj < J.pcol_pad) {
+        const float w[4] = {tile[4 * qq][jj], tile[4 * qq + 1][jj], tile[4 * qq + 2][jj], tile[4 * qq + 3][jj]};
+        put_operand4((float *)J.x, (c0 + jj) * J.prow_pad + i0 + 4 * qq, w, planes);
+      }
+    }
+    __syncthreads();
+  }
+  if (lane == 0) rp[wave] = row_part;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int r = 0; r < kFlipRows; ++r) t += rp[r];
+    J.fro[blk] = t;
   }
 }
 
 // ------------------------------------------------------------ mapback ---
-// u_i = sum_j Q_ij z_j and ||U_i||^2 in closed form:
-// b_i^2 (sum (a Q)^2 + 2 kappa u_i sum (a Q)(a z) + kappa^2 u_i^2 sum (a z)^2).
+// From the stage-5 row-sum partials: u_i = sum_j Q_ij z_j and ||U_i||^2 in
+// closed form, b_i^2 (sum (a Q)^2 + 2 kappa u_i sum (a Q)(a z) + kappa^2
+// u_i^2 sum (a z)^2); per-block partials of ||U||^2.  kNormRows rows per
+// block, 4 lanes per row (strips p, p + 4, ... of lane p, all loads of a
+// lane in flight together for up to 4 kNormUnroll strips per row).
+constexpr int kNormRows = kRowThreads / 4;
+constexpr int kNormUnroll = 12;
+
 template <bool R1>
-__global__ void __launch_bounds__(kMapThreads) mapback_rows_kernel(MatPack pack) {
-  __shared__ double wave_part[kPartRows];
-  const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
-  const smx_matrix_desc &d = J.d;
-  const int blk = blockIdx.x - J.blk0;
-  constexpr bool r1 = R1;
-  const double cz = r1 ? J.cst[1] : 0.0;
-  const double kappa = r1 ? d.kappa[0] : 0.0;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool vec = d.cols % 4 == 0 && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
-  double part = 0.0;
-  const int64_t i = static_cast<int64_t>(blk) * kPartRows + wave;
-  if (i < d.rows) {
-    const float *q = J.pl + i * J.pcol_pad;
-    float su = 0.f, sa = 0.f, sb = 0.f;
-    if (vec) {
-      const int64_t n4 = d.cols / 4;
-      for (int64_t k0 = lane; k0 < n4; k0 += 64 * kRowUnroll) {
-        float4 qv[kRowUnroll], av[kRowUnroll], zv[kRowUnroll];
+__global__ void __launch_bounds__(kRowThreads) mapback_norm_kernel(JobRange range) {
+  __shared__ double scratch[16];
+  const int jid = find_job(range, blockIdx.x);
+  const DevJob J = load_job(range.jobs, jid);
+  const DevDesc &d = J.d;
+  const int blk = blockIdx.x - range.start[jid];
+  const int part = threadIdx.x & 3;
+  const int64_t i = static_cast<int64_t>(blk) * kNormRows + (threadIdx.x >> 2);
+  const bool live = i < d.rows;
+  double su = 0.0, sa = 0.0, sb = 0.0;
+  if (live) {
+    const SMX_GLOBAL float *p0 = J.mrp + i;
+    for (int k0 = part; k0 < J.strips; k0 += 4 * kNormUnroll) {
+      float v[kNormUnroll][3];
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u) {
-          const int64_t k = k0 + 64 * u;
-          if (k < n4) {
-            qv[u] = ld4(q, k);
-            av[u] = ld4(d.inv_col, k);
-            if constexpr (R1) zv[u] = ld4(d.z, k);
-          }
-        }
+      for (int u = 0; u < kNormUnroll; ++u) {
+        const int k = k0 + 4 * u;
+        const int64_t o = static_cast<int64_t>(k) * J.prow_pad;
+        const bool in = k < J.strips;
+        v[u][0] = in ? p0[o] : 0.f;
+        v[u][1] = in ? p0[J.mrp_size + o] : 0.f;
+        v[u][2] = in ? p0[2 * J.mrp_size + o] : 0.f;
+      }
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; ++u) {
-          if (k0 + 64 * u < n4) {
-            const float4 qq = qv[u], a = av[u];
-            const float aq0 = a.x * qq.x, aq1 = a.y * qq.y, aq2 = a.z * qq.z, aq3 = a.w * qq.w;
-            sa = fmaf(aq0, aq0, fmaf(aq1, aq1, fmaf(aq2, aq2, fmaf(aq3, aq3, sa))));
-            if constexpr (R1) {
-              const float4 z = zv[u];
-              su = fmaf(qq.x, z.x, fmaf(qq.y, z.y, fmaf(qq.z, z.z, fmaf(qq.w, z.w, su))));
-              sb = fmaf(aq0, a.x * z.x, fmaf(aq1, a.y * z.y, fmaf(aq2, a.z * z.z, fmaf(aq3, a.w * z.w, sb))));
-            }
-          }
-        }
+      for (int u = 0; u < kNormUnroll; ++u) {
+        su += v[u][0];
+        sa += v[u][1];
+        sb += v[u][2];
       }
-    } else {
-      for (int64_t j = lane; j < d.cols; j += 64) {
-        const float a = d.inv_col[j];
-        const float aq = a * q[j];
-        sa = fmaf(aq, aq, sa);
-        if (r1) {
-          su = fmaf(q[j], d.z[j], su);
-          sb = fmaf(aq, a * d.z[j], sb);
-        }
-      }
-    }
-    const double U = wave_sum(su);
-    const double A = wave_sum(sa);
-    const double B = wave_sum(sb);
-    if (lane == 0) {
-      const double b = d.inv_row[i];
-      J.u[i] = static_cast<float>(U);
-      part = b * b * (A + 2.0 * kappa * U * B + kappa * kappa * U * U * cz);
     }
   }
-  const double t = sum_wave_parts<kPartRows>(part, wave_part);
-  if (threadIdx.x == 0) J.part[blk] = t;
+  // the row's 4 lanes (a DPP quad), fixed order
+  su += dpp_mov<0xB1>(su); su += dpp_mov<0x4E>(su);
+  sa += dpp_mov<0xB1>(sa); sa += dpp_mov<0x4E>(sa);
+  sb += dpp_mov<0xB1>(sb); sb += dpp_mov<0x4E>(sb);
+  double row_part = 0.0;
+  if (live && part == 0) {
+    const double b = d.inv_row[i];
+    const double kappa = R1 ? d.kappa[0] : 0.0;
+    const double cz = R1 ? J.cst[kCstAZ] : 0.0;
+    J.u[i] = static_cast<float>(su);
+    row_part = b * b * (sa + 2.0 * kappa * su * sb + kappa * kappa * su * su * cz);
+  }
+  const double t = block_sum(row_part, scratch);
+  if (threadIdx.x == 0) J.mb[blk] = t;
 }
 
-// W -= lr * sqrt(rows) / max(||U||_F, FLT_MIN) * U over kPartRows rows
-// (one wave per row).  The first chunk of the row is loaded before the
-// norm is summed, so the block does not wait on two memory round trips in
-// a row.  A 16-bit parameter takes W = round(W - lr * round(direction))
+// W -= lr * sqrt(rows) / max(||U||_F, FLT_MIN) * U (wpr waves per row).  A
+// 16-bit parameter takes W = round(W - lr * round(direction))
 // (sandmuon/optimizer.py:315) on the per-element path.
 template <bool R1>
-__global__ void __launch_bounds__(kMapThreads) mapback_apply_kernel(MatPack pack) {
-  __shared__ double bcast;
-  const MatJob &J = pack.j[find_job(pack, blockIdx.x)];
-  const smx_matrix_desc &d = J.d;
-  const int blk = blockIdx.x - J.blk0;
-  constexpr bool r1 = R1;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__global__ void __launch_bounds__(kRowThreads) mapback_apply_kernel(JobRange range) {
+  const int jid = find_job(range, blockIdx.x);
+  const DevJob J = load_job(range.jobs, jid);
+  const DevDesc &d = J.d;
+  const int blk = blockIdx.x - range.start[jid];
+  const RowPos p = row_pos(J, blk);
+  if (p.i >= d.rows) return;
   const int pdt = d.param_dtype;
-  const bool vec = pdt == SMX_F32 && d.cols % 4 == 0 && aligned16(d.param) && aligned16(d.inv_col) &&
-                   (!r1 || aligned16(d.z));
-  const int64_t i = static_cast<int64_t>(blk) * kPartRows + wave;
-  const bool live = i < d.rows;
-  const float *q = live ? J.pl + i * J.pcol_pad : nullptr;
-  float *w = live && pdt == SMX_F32 ? static_cast<float *>(d.param) + i * d.cols : nullptr;
-  const int64_t n4 = d.cols / 4;
-  float4 qv[kRowUnroll], av[kRowUnroll], wv[kRowUnroll], zv[kRowUnroll];
-  auto load = [&](int64_t k0) {
-#pragma unroll
-    for (int u = 0; u < kRowUnroll; ++u) {
-      const int64_t k = k0 + 64 * u;
-      if (k < n4) {
-        qv[u] = ld4(q, k);
-        av[u] = ld4(d.inv_col, k);
-        wv[u] = ld4(w, k);
-        if constexpr (R1) zv[u] = ld4(d.z, k);
-      }
-    }
-  };
-  if (live && vec) load(lane);
-  if (threadIdx.x < 64) {
-    double s = 0.0;
-    const int np = static_cast<int>(ceil_div(d.rows, kPartRows));
-    for (int k = threadIdx.x; k < np; k += 64) s += J.part[k];
-    s = wave_sum(s);
-    if (threadIdx.x == 0) bcast = s;
-  }
-  __syncthreads();
-  const double n2 = bcast;
+  const SMX_GLOBAL float *q = J.q + p.i * J.pcol_pad;
+  const double n2 = J.cst[kCstU];
   const float norm = static_cast<float>(sqrt(n2));
   // _graft_direction: sqrt(rows) / max(||U||, FLT_MIN); a zero direction
   // gives a zero update.
   const float scale = n2 > 0.0 ? static_cast<float>(sqrt(static_cast<double>(d.rows))) / fmaxf(norm, FLT_MIN) : 0.f;
   const float nlr = static_cast<float>(-d.lr);
-  const float kappa = r1 ? d.kappa[0] : 0.f;
-  if (!live) return;
-  const float b = d.inv_row[i];
-  const float ku = r1 ? kappa * J.u[i] : 0.f;
-  if (vec) {
-    for (int64_t k0 = lane; k0 < n4; k0 += 64 * kRowUnroll) {
-      if (k0 != lane) load(k0);  // the first chunk was loaded above
+  const float b = d.inv_row[p.i];
+  const float ku = R1 ? d.kappa[0] * J.u[p.i] : 0.f;
+  if (J.mvec) {
+    SMX_GLOBAL float *w = (SMX_GLOBAL float *)d.param + p.i * d.cols;
+    const int n4 = static_cast<int>(d.cols / 4);
+    for (int q0 = p.q0; q0 < n4; q0 += p.span * kMaxSlices) {
+      float4 qv[kMaxSlices], av[kMaxSlices], wv[kMaxSlices], zv[kMaxSlices];
 #pragma unroll
-      for (int u = 0; u < kRowUnroll; ++u) {
-        const int64_t k = k0 + 64 * u;
+      for (int t = 0; t < kMaxSlices; ++t) {
+        const int k = q0 + p.span * t;
         if (k < n4) {
-          float4 v = qv[u], ww = wv[u];
-          const float4 a = av[u];
+          qv[t] = ld4(q, k);
+          wv[t] = ld4(w, k);
+          av[t] = ld4(d.inv_col, k);
+          if constexpr (R1) zv[t] = ld4(d.z, k);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kMaxSlices; ++t) {
+        const int k = q0 + p.span * t;
+        if (k < n4) {
+          float4 v = qv[t], ww = wv[t];
+          const float4 a = av[t];
           if constexpr (R1) {
-            const float4 z = zv[u];
+            const float4 z = zv[t];
             v.x = fmaf(ku, z.x, v.x); v.y = fmaf(ku, z.y, v.y); v.z = fmaf(ku, z.z, v.z); v.w = fmaf(ku, z.w, v.w);
           }
           ww.x = fmaf(nlr, ((v.x * b) * a.x) * scale, ww.x);
@@ -532,22 +779,17 @@ __global__ void __launch_bounds__(kMapThreads) mapback_apply_kernel(MatPack pack
       }
     }
   } else {
-    const int64_t row = i * d.cols;
-    for (int64_t j = lane; j < d.cols; j += 64) {
+    const int64_t row = p.i * d.cols;
+    for (int j = p.q0; j < d.cols; j += p.span) {
       float v = q[j];
-      if (r1) v = fmaf(ku, d.z[j], v);
+      if constexpr (R1) v = fmaf(ku, d.z[j], v);
       const float dir = round_to(pdt, ((v * b) * d.inv_col[j]) * scale);
-      store_any(d.param, pdt, row + j, round_to(pdt, fmaf(nlr, dir, load_any(d.param, pdt, row + j))));
+      store_any((void *)d.param, pdt, row + j, round_to(pdt, fmaf(nlr, dir, load_any((const void *)d.param, pdt, row + j))));
     }
   }
 }
 
 // --------------------------------------------------------------- host ---
-struct Planned {
-  S8Plan plan;
-  std::vector<int32_t> cls, slot;
-};
-
 static bool oriented(const smx_matrix_desc &d, int64_t &r, int64_t &c, bool &flip) {
   flip = d.rows > d.cols;
   r = flip ? d.cols : d.rows;
@@ -573,6 +815,9 @@ static std::vector<std::vector<int32_t>> shape_groups(const int64_t *rows, const
   return groups;
 }
 
+// The job table follows the S8 buffers of a group.
+static size_t table_bytes(size_t jobs) { return static_cast<size_t>(round_up(jobs * sizeof(MatJob), 256)); }
+
 static size_t group_bytes(const int64_t *rows, const int64_t *cols, const std::vector<int32_t> &g, int mode) {
   const int32_t m = static_cast<int32_t>(g.size());
   std::vector<int64_t> r(m), c(m);
@@ -585,58 +830,45 @@ static size_t group_bytes(const int64_t *rows, const int64_t *cols, const std::v
   S8Plan plan;
   std::vector<int32_t> cls(m), slot(m);
   plan_s8(r.data(), c.data(), fl.get(), m, mode, nullptr, plan, cls.data(), slot.data());
-  return plan.bytes;
+  return plan.bytes + table_bytes(m);
 }
 
+// Waves per row and float4 per lane for rows of `cols` columns.
+static void row_geometry(int64_t cols, int32_t &wpr, int32_t &slices) {
+  const int64_t n4 = ceil_div(cols, 4);
+  wpr = n4 <= 64 * kMaxSlices ? 1 : n4 <= 128 * kMaxSlices ? 2 : 4;
+  slices = static_cast<int32_t>(ceil_div(n4, 64 * wpr));
+}
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Launches `kernel` over table jobs [first, first + n), kLaunchJobs at a time.
 template <typename KernelFn>
-static int launch_jobs(std::vector<MatJob> &jobs, int64_t (*blocks_of)(const MatJob &), KernelFn kernel,
-                       int threads, const char *what, hipStream_t st) {
-  for (size_t b = 0; b < jobs.size(); b += kMatBatch) {
-    MatPack pack{};
-    pack.n = static_cast<int32_t>(std::min<size_t>(kMatBatch, jobs.size() - b));
+static int launch_range(const MatJob *host, MatJob *table, int32_t first, int32_t n,
+                        int64_t (*blocks_of)(const MatJob &), KernelFn kernel, int threads, const char *what,
+                        hipStream_t st) {
+  for (int32_t b = first; b < first + n; b += kLaunchJobs) {
+    JobRange r{};
+    r.jobs = table + b;
+    r.n = std::min<int32_t>(kLaunchJobs, first + n - b);
     int64_t total = 0;
-    for (int k = 0; k < kMatBatch; ++k) pack.start[k] = INT32_MAX;
-    for (int k = 0; k < pack.n; ++k) {
-      pack.j[k] = jobs[b + k];
-      pack.j[k].blk0 = static_cast<int32_t>(total);
-      pack.start[k] = static_cast<int32_t>(total);
-      total += blocks_of(pack.j[k]);
+    for (int k = 0; k < kLaunchJobs; ++k) r.start[k] = INT32_MAX;
+    for (int k = 0; k < r.n; ++k) {
+      r.start[k] = static_cast<int32_t>(total);
+      total += blocks_of(host[b + k]);
     }
-    pack.total_blocks = static_cast<int32_t>(total);
+    SMX_REQUIRE(total < INT32_MAX, SMX_ESHAPE, std::string(what) + ": too many blocks for one launch");
     if (total == 0) continue;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(total)), dim3(threads), 0, st, pack);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(total)), dim3(threads), 0, st, r);
     const int rc = check_launch(what);
     if (rc) return rc;
   }
   return SMX_OK;
 }
 
-static int64_t one_block(const MatJob &) { return 1; }
-static int64_t map_blocks(const MatJob &j) { return ceil_div(j.d.rows, kPartRows); }
-template <bool FLIP>
-static int64_t whiten_blocks(const MatJob &j) { return j.prow_pad / whiten_rows_per_block<FLIP>(); }
-
-// Whiten launches for the job lists bucketed by kept chunks (index KEEP).
-template <int KEEP>
-static int launch_whiten_keep(std::vector<MatJob> *keep, std::vector<MatJob> *flip, bool r1, hipStream_t st) {
-  constexpr int kKeepThreads = 64 * whiten_rows_per_block<false>();
-  int rc = SMX_OK;
-  if (!keep[KEEP].empty())
-    rc = r1 ? launch_jobs(keep[KEEP], whiten_blocks<false>, whiten_kernel<true, false, KEEP>, kKeepThreads, "whiten", st)
-            : launch_jobs(keep[KEEP], whiten_blocks<false>, whiten_kernel<false, false, KEEP>, kKeepThreads, "whiten", st);
-  if constexpr (KEEP <= kWhitenKeepFlip) {
-    if (!rc && !flip[KEEP].empty())
-      rc = r1 ? launch_jobs(flip[KEEP], whiten_blocks<true>, whiten_kernel<true, true, KEEP>, kRowThreads, "whiten", st)
-              : launch_jobs(flip[KEEP], whiten_blocks<true>, whiten_kernel<false, true, KEEP>, kRowThreads, "whiten", st);
-  }
-  if constexpr (KEEP < kWhitenKeep) {
-    if (!rc) rc = launch_whiten_keep<KEEP + 1>(keep, flip, r1, st);
-  }
-  return rc;
-}
-
-static int launch_whiten(std::vector<MatJob> *keep, std::vector<MatJob> *flip, bool r1, hipStream_t st) {
-  return launch_whiten_keep<0>(keep, flip, r1, st);
+static int matrix_totals(MatJob *table, int32_t m, int which, hipStream_t st) {
+  hipLaunchKernelGGL(matrix_total_kernel, dim3(static_cast<unsigned>(m)), dim3(64), 0, st, table, which);
+  return check_launch("matrix_total");
 }
 
 }  // namespace smx
@@ -679,6 +911,7 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
   SMX_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, SMX_EALIGN,
               "matrix_step: workspace must be 256-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool r1 = descs[0].z != nullptr;
   for (const auto &g : shape_groups(rows.data(), cols.data(), n)) {
     const int32_t m = static_cast<int32_t>(g.size());
     std::vector<int64_t> r(m), c(m);
@@ -693,49 +926,84 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
     if (!plan_s8(r.data(), c.data(), fl.get(), m, mode, static_cast<char *>(workspace), plan, cls.data(),
                  slot.data()))
       return fail(SMX_EINVAL, "matrix_step: internal shape grouping error");
-    std::vector<MatJob> ping(m), fin(m);
-    for (int32_t k = 0; k < m; ++k) {
-      const S8Mat M{plan.layout.cls[cls[k]], slot[k]};
-      MatJob j{};
-      j.d = descs[g[k]];
-      j.u = M.u();
-      j.prow_pad = M.prow_pad();
-      j.pcol_pad = M.pcol_pad();
-      // The oriented iterate x0 is the parameter layout, or its transpose.
-      j.pl = M.flip() ? nullptr : M.x0();
-      j.tl = M.flip() ? M.x0() : nullptr;
-      j.part = M.fro();
-      j.cst = M.cst();
-      j.planes = mode == SMX_S8_COMP_BF16;
-      ping[k] = j;
-      j.pl = M.result();
-      j.tl = nullptr;
-      j.part = M.mb();
-      j.planes = 0;
-      fin[k] = j;
+    MatJob *table = reinterpret_cast<MatJob *>(static_cast<char *>(workspace) + plan.bytes);
+    // Table order: parameters kept as they are, then transposed ones whose
+    // rows fit one LDS chunk with the float4 path, then the other transposed
+    // ones (one whiten launch each); both mapback launches take the whole
+    // table.
+    std::vector<MatJob> jobs;
+    jobs.reserve(m);
+    int32_t n_plain = 0, n_kept = 0;
+    auto flip_kept = [&](int32_t k) {
+      const smx_matrix_desc &d = descs[g[k]];
+      return d.cols % 4 == 0 && d.cols <= kFlipChunk && d.grad_dtype == SMX_F32 && aligned16(d.grad) &&
+             aligned16(d.momentum) && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
+    };
+    for (int pass = 0; pass < 3; ++pass) {
+      for (int32_t k = 0; k < m; ++k) {
+        if (pass != (!fl[k] ? 0 : flip_kept(k) ? 1 : 2)) continue;
+        const S8Mat M{plan.layout.cls[cls[k]], slot[k]};
+        MatJob j{};
+        j.d = descs[g[k]];
+        j.x = M.x0();
+        j.flip = M.flip();
+        j.q = M.result();
+        j.u = M.u();
+        j.fro = M.fro();
+        j.mb = M.mb();
+        j.cst = M.cst();
+        j.colv = M.colv();
+        j.mrp = M.mrp(0);
+        j.mrp_size = M.mrp_size();
+        j.strips = static_cast<int32_t>(M.strips());
+        j.prow_pad = static_cast<int32_t>(M.prow_pad());
+        j.pcol_pad = static_cast<int32_t>(M.pcol_pad());
+        j.planes = mode == SMX_S8_COMP_BF16;
+        row_geometry(j.d.cols, j.wpr, j.slices);
+        j.cvec = j.d.cols % 4 == 0 && aligned16(j.d.inv_col) && (!r1 || aligned16(j.d.z));
+        j.wvec = j.cvec && j.d.grad_dtype == SMX_F32 && aligned16(j.d.grad) && aligned16(j.d.momentum);
+        j.mvec = j.cvec && j.d.param_dtype == SMX_F32 && aligned16(j.d.param);
+        jobs.push_back(j);
+        n_plain += pass == 0;
+        n_kept += pass <= 1;
+      }
+    }
+    for (int32_t b = 0; b < m; b += kPrepBatch) {
+      PrepPack pk{};
+      pk.n = std::min<int32_t>(kPrepBatch, m - b);
+      for (int k = 0; k < pk.n; ++k) pk.j[k] = jobs[b + k];
+      pk.table = table + b;
+      hipLaunchKernelGGL(matrix_prep_kernel, dim3(pk.n), dim3(kPrepThreads), 0, st, pk);
+      const int rc = check_launch("matrix_prep");
+      if (rc) return rc;
     }
     // The kernels are specialised on whether the matrices carry a rank-one
     // term (all of a call or none, checked above).
-    const bool r1 = descs[0].z != nullptr;
-    // The rank-one constants (sum z^2, sum (a z)^2) exist only with a rank-one term.
-    int rc = r1 ? launch_jobs(ping, one_block, matrix_consts_kernel, 256, "matrix_consts", st) : SMX_OK;
-    // The whiten kernel is specialised on the orientation too: the jobs go
-    // to two launches, parameters kept as they are and transposed ones,
-    // and on how many kWhitenChunk column chunks of a row pass 1 keeps in
-    // registers (rows of at most kWhitenKeep chunks, kWhitenKeepFlip for
-    // transposed parameters; wider rows re-read).
-    std::vector<MatJob> keep[kWhitenKeep + 1], flip[kWhitenKeep + 1];
-    for (const MatJob &j : ping) {
-      const int64_t chunks = ceil_div(j.d.cols, kWhitenChunk);
-      const int64_t most = j.tl ? kWhitenKeepFlip : kWhitenKeep;
-      (j.tl ? flip : keep)[chunks <= most ? chunks : 0].push_back(j);
-    }
-    if (!rc) rc = launch_whiten(keep, flip, r1, st);
+    const MatJob *h = jobs.data();
+    int rc = r1 ? launch_range(h, table, 0, n_plain, whiten_blocks, whiten_kernel<true>, kRowThreads, "whiten", st)
+                : launch_range(h, table, 0, n_plain, whiten_blocks, whiten_kernel<false>, kRowThreads, "whiten", st);
+    if (!rc && n_kept > n_plain)
+      rc = r1 ? launch_range(h, table, n_plain, n_kept - n_plain, whiten_blocks, whiten_flip_kernel<true, true>,
+                             kFlipThreads, "whiten", st)
+              : launch_range(h, table, n_plain, n_kept - n_plain, whiten_blocks, whiten_flip_kernel<false, true>,
+                             kFlipThreads, "whiten", st);
+    if (!rc && m > n_kept)
+      rc = r1 ? launch_range(h, table, n_kept, m - n_kept, whiten_blocks, whiten_flip_kernel<true, false>,
+                             kFlipThreads, "whiten", st)
+              : launch_range(h, table, n_kept, m - n_kept, whiten_blocks, whiten_flip_kernel<false, false>,
+                             kFlipThreads, "whiten", st);
+    if (!rc) rc = matrix_totals(table, m, kCstFro, st);
+    plan.layout.rowsums = 1;
     if (!rc) rc = run_s8_stages(plan.layout, st);
-    if (!rc) rc = r1 ? launch_jobs(fin, map_blocks, mapback_rows_kernel<true>, kMapThreads, "mapback_rows", st)
-                     : launch_jobs(fin, map_blocks, mapback_rows_kernel<false>, kMapThreads, "mapback_rows", st);
-    if (!rc) rc = r1 ? launch_jobs(fin, map_blocks, mapback_apply_kernel<true>, kMapThreads, "mapback_apply", st)
-                     : launch_jobs(fin, map_blocks, mapback_apply_kernel<false>, kMapThreads, "mapback_apply", st);
+    if (!rc)
+      rc = r1 ? launch_range(h, table, 0, m, norm_blocks, mapback_norm_kernel<true>, kRowThreads, "mapback_norm", st)
+              : launch_range(h, table, 0, m, norm_blocks, mapback_norm_kernel<false>, kRowThreads, "mapback_norm", st);
+    if (!rc) rc = matrix_totals(table, m, kCstU, st);
+    if (!rc)
+      rc = r1 ? launch_range(h, table, 0, m, mapback_blocks, mapback_apply_kernel<true>, kRowThreads, "mapback_apply",
+                             st)
+              : launch_range(h, table, 0, m, mapback_blocks, mapback_apply_kernel<false>, kRowThreads,
+                             "mapback_apply", st);
     if (rc) return rc;
   }
   return SMX_OK;

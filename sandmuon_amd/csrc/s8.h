@@ -23,8 +23,9 @@ namespace smx {
 constexpr int kTile = 256;        // apply tile rows and buffer padding
 constexpr int kSymTile = 128;     // Gram / square output tile edge
 constexpr int kMaxClasses = 8;    // shape classes per GEMM launch
-constexpr int kRowsPerPart = 16;  // param rows per whiten block of a transposed parameter (one K group)
-constexpr int kPartRows = 4;      // param rows per whiten / mapback partial
+// Parameter columns per stage-5 row-sum partial: a wave's 64 output columns
+// of an apply tile, or (transposed parameter) its 128 output rows.
+constexpr int kStripT = 64, kStripM = 128;
 
 // Fixed S8 recipe: sandmuon/coefficients.py:3-11.
 constexpr double kS8Margin = 1.35;
@@ -36,6 +37,12 @@ constexpr double kS8Coefficients[5][3] = {
     {2.282741575232451, -1.6302296637355072, 0.40275720810675486},
 };
 
+// Per-matrix scalars (S8Class::cst): ||V||^2 of the whitened input (the
+// S8 normalisation; the total of the whiten partials, or of the input for
+// the stand-alone map), sum z^2 and sum (a z)^2 of the rank-one term, and
+// ||U||^2 of the mapped-back direction (the graft).
+constexpr int kCstFro = 0, kCstZZ = 1, kCstAZ = 2, kCstU = 3, kCst = 4;
+
 struct S8Class {
   int64_t r, c;        // oriented logical dims, r <= c
   int64_t rp, cp;      // padded dims
@@ -43,7 +50,8 @@ struct S8Class {
   int32_t n_flip;      // slots [0, n_flip) hold transposed parameters
   int32_t tiles_m;     // rp / kTile
   int32_t tiles_n;     // cp / kTile
-  int32_t parts;       // partial slots per matrix: ceil(cp / kPartRows)
+  int32_t parts;       // per-block partial slots per matrix (cp: the most blocks a
+                       // whiten or mapback launch gives one matrix)
   int32_t tiles_s;     // rp / kSymTile
   int32_t gs;          // Gram-space iteration (cp > rp): the stages run on r x r
                        // products and X0 is applied once, at stage 5
@@ -60,16 +68,24 @@ struct S8Class {
                        // form): T = P G, and the accumulated product Q of a
                        // segment's stage polynomials (qa, qb: ping-pong)
   float *u;            // [count][cp] per param-row rank-one coefficient
-  double *fro;         // [count][parts] whiten: partial sum of V^2
-  double *mb;          // [count][parts] mapback: partial sum of U^2
+  double *fro;         // [count][parts] whiten: per-block partial sums of V^2
+  double *mb;          // [count][parts] mapback: per-block partial sums of U^2
   double *sch;         // [count][sym_tiles(tiles_s)] Schatten partials (one per upper-triangle Gram tile)
-  double *cst;         // [count][2] matrix-step constants: sum z^2, sum (a z)^2
+  double *cst;         // [count][kCst] per-matrix scalars (see the kCst* indices)
+  // Matrix step only (S8Layout::rowsums): the A factor diagonal and the
+  // rank-one vector (NULL without one) of each slot's matrix, and the
+  // stage-5 row-sum partials of the mapback: per parameter row and strip
+  // of kStripT parameter columns (kStripM for a transposed parameter), the
+  // sums of Q z, (a Q)^2 and (a Q)(a z).
+  const float **colv;  // [count][2]: inv_col, z
+  float *mrp;          // [count][3][rp * cp / kStripT]
 };
 
 struct S8Layout {
   S8Class cls[kMaxClasses];
   int32_t n_classes;
   int32_t mode;
+  int32_t rowsums;  // the stage-5 apply writes the mapback row-sum partials (matrix step)
 };
 
 __host__ __device__ inline int64_t sym_tiles(int64_t t) { return t * (t + 1) / 2; }
@@ -95,7 +111,15 @@ struct S8Mat {
   __host__ __device__ double *fro() const { return kp()->fro + static_cast<int64_t>(slot) * kp()->parts; }
   __host__ __device__ double *mb() const { return kp()->mb + static_cast<int64_t>(slot) * kp()->parts; }
   __host__ __device__ double *sch() const { return kp()->sch + slot * sym_tiles(kp()->tiles_s); }
-  __host__ __device__ double *cst() const { return kp()->cst + 2 * static_cast<int64_t>(slot); }
+  __host__ __device__ double *cst() const { return kp()->cst + kCst * static_cast<int64_t>(slot); }
+  __host__ __device__ const float *acol() const { return kp()->colv[2 * slot]; }
+  __host__ __device__ const float *zcol() const { return kp()->colv[2 * slot + 1]; }
+  __host__ __device__ const float **colv() const { return kp()->colv + 2 * slot; }
+  // Row-sum partials: k = 0 (Q z), 1 ((a Q)^2), 2 ((a Q)(a z)), each
+  // [strips()][prow_pad] (a strip's rows contiguous).
+  __host__ __device__ int64_t mrp_size() const { return kp()->rp * kp()->cp / kStripT; }
+  __host__ __device__ float *mrp(int k) const { return kp()->mrp + (3 * static_cast<int64_t>(slot) + k) * mrp_size(); }
+  __host__ __device__ int64_t strips() const { return flip() ? kp()->rp / kStripM : kp()->cp / kStripT; }
   // Parameter layout: rows x cols (the transpose of the oriented layout
   // for transposed parameters).
   __host__ __device__ int64_t prow() const { return flip() ? kp()->c : kp()->r; }
@@ -172,8 +196,8 @@ struct S8Plan {
 bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, int mode,
              char *base, S8Plan &plan, int32_t *cls_of, int32_t *slot_of);
 
-// Run the five S8 stages on a planned layout whose x0 (and fro partials)
-// are filled.  The result of each matrix is in S8Mat::result().
+// Run the five S8 stages on a planned layout whose x0 and input norms
+// (cst()[kCstFro]) are filled.  The result of each matrix is in S8Mat::result().
 int run_s8_stages(const S8Layout &layout, hipStream_t st);
 
 }  // namespace smx

@@ -631,11 +631,7 @@ __device__ double sum_parts(const double *p, int n, double *bcast) {
   return v;
 }
 
-__device__ __forceinline__ int fro_parts_used(const S8Mat &m) {
-  return static_cast<int>(ceil_div(m.prow(), kPartRows));
-}
-
-// Stage-1 scalars of a matrix: ||V||^2 (sum of the whiten partials) and the
+// Stage-1 scalars of a matrix: ||V||^2 (the input's total, kCstFro) and the
 // Schatten scale s = max(1.35 ||G2||_F^(1/4), 1e-30) of the normalised G2
 // (sandmuon/optimizer.py:80-84).  ok = false for a zero matrix.
 struct Stage1Scalars {
@@ -649,7 +645,7 @@ __host__ __device__ inline int64_t square_tiles(const S8Class &k, bool small) {
 
 __device__ Stage1Scalars stage1_scalars(const S8Mat &M, bool sq_small, double *bcast) {
   Stage1Scalars r;
-  r.fro2 = sum_parts(M.fro(), fro_parts_used(M), bcast);
+  r.fro2 = M.cst()[kCstFro];
   const double sq = sum_parts(M.sch(), static_cast<int>(square_tiles(*M.kp(), sq_small)), bcast);
   r.ok = r.fro2 > 0.0 && sq > 0.0;
   r.s = r.ok ? fmaxf(static_cast<float>(kS8Margin * pow(sq, 0.125)), 1e-30f) : 1.f;
@@ -678,6 +674,8 @@ __device__ __forceinline__ TileRef tile_of(const StageArgs &args) {
 constexpr int kEpStride = 36;
 constexpr int kEpBlock = 32 * kEpStride;
 static_assert(kWaves * 2 * kEpBlock * 4 <= Geo<kSymTile>::kRingBytes, "epilogue staging must fit in the operand ring");
+static_assert((kWaves * 2 * kEpBlock + 2 * kTile) * 4 <= Geo<kTile>::kRingBytes,
+              "apply epilogue staging and the row-sum column vectors must fit in the operand ring");
 
 __device__ __forceinline__ void ep_read8(const float *s, int row, int col, float (&w)[8]) {
   const f32x4 a = *reinterpret_cast<const f32x4 *>(s + row * kEpStride + col);
@@ -743,6 +741,30 @@ s8_stage_kernel(StageArgs args) {
   const S8Mat M{K, slot};
   const int stage = args.stage;
   const bool odd = (stage & 1) != 0;
+  // The stage-5 result of the matrix step also leaves row sums for the
+  // mapback (see the epilogue); the A factor and rank-one entries of the
+  // tile's parameter columns are loaded two per thread, here in the
+  // compensated modes, so their latency hides under the K loop (the FP32
+  // kernel has no two registers to spare and loads them after it), and
+  // pass through LDS to the epilogue.
+  const bool rsum = PHASE == kApply && stage == 5 && args.L.rowsums != 0 &&
+                    (ref.op == kOpApplyX || ref.op == kOpApplyFinal);
+  const int64_t rs_c0 = M.flip() ? tm * Gm::kTileM : tn * kTileN;  // first parameter column of the tile
+  const int rs_w = M.flip() ? Gm::kTileM : kTileN;                 // parameter columns of the tile
+  float colv_pre[2] = {0.f, 0.f};
+  auto load_colv = [&]() {
+    const float *acol = M.acol(), *zcol = M.zcol();
+    const int64_t pcols = M.pcol();
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int idx = static_cast<int>(threadIdx.x) + kThreads * v;  // [vector][column]
+      const int64_t col = rs_c0 + idx % rs_w;
+      const float *src = idx < rs_w ? acol : zcol;
+      if (idx < 2 * rs_w && src && col < pcols) colv_pre[v] = src[col];
+    }
+  };
+  constexpr bool kColvEarly = MODE != SMX_S8_FP32;
+  if (kColvEarly && rsum) load_colv();
   float *x_in = odd ? M.x0() : M.x1();
   float *x_out = odd ? M.x1() : M.x0();
 
@@ -770,7 +792,7 @@ s8_stage_kernel(StageArgs args) {
                                       acc);
   } else if constexpr (PHASE == kGram) {
     if (stage == 1) {
-      const double f = sum_parts(M.fro(), fro_parts_used(M), &bcast);
+      const double f = M.cst()[kCstFro];
       scale = f > 0.0 ? static_cast<float>(1.0 / f) : 0.f;
     }
     // A Gram-space class takes its stage-3 Gram of X2 from x1.
@@ -853,6 +875,59 @@ s8_stage_kernel(StageArgs args) {
   float *const T = reinterpret_cast<float *>(smem) + wave * 2 * kEpBlock;
   float *const U = T + kEpBlock;
   float sq_local = 0.f;
+  // The stage-5 result of the matrix step: per parameter row, partial sums
+  // of Q z, (a Q)^2 and (a Q)(a z) over the wave's strip of parameter
+  // columns (its 64 output columns; its 128 output rows for a transposed
+  // parameter), reduced over the 4 lanes of the row and stored for the
+  // mapback (its row coefficients and graft norm), so no later pass reads Q
+  // for them.
+  static_assert(PHASE != kApply || (kStripT == 32 * kSubN && kStripM == 32 * kSubM),
+                "a row-sum strip is one wave's share of an apply tile");
+  const int64_t strips = M.strips(), prows = M.prow_pad();
+  // a and z of the tile's parameter columns in LDS past the staging blocks
+  // (the operand ring is free once the K loop is done).
+  float *const colv_lds = reinterpret_cast<float *>(smem) + kWaves * 2 * kEpBlock;
+  if (rsum) {
+    if (!kColvEarly) load_colv();
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int idx = static_cast<int>(threadIdx.x) + kThreads * v;
+      if (idx < 2 * rs_w) colv_lds[idx] = colv_pre[v];
+    }
+    __syncthreads();
+  }
+  float rs[kSubN][2][3];
+#pragma unroll
+  for (int j = 0; j < kSubN; ++j)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) rs[j][q][0] = rs[j][q][1] = rs[j][q][2] = 0.f;
+  // a and z of parameter columns gc .. gc + 7 (zeros past the last column)
+  auto colv8 = [&](int64_t gc, float (&a8)[8], float (&z8)[8]) {
+    const int o = static_cast<int>(gc - rs_c0);
+    ep_read8(colv_lds, 0, o, a8);
+    ep_read8(colv_lds, 0, rs_w + o, z8);
+  };
+  auto accum = [&](const float (&w)[8], const float (&a8)[8], const float (&z8)[8], float (&r)[3]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float aw = a8[e] * w[e];
+      r[0] = fmaf(w[e], z8[e], r[0]);
+      r[1] = fmaf(aw, aw, r[1]);
+      r[2] = fmaf(aw, a8[e] * z8[e], r[2]);
+    }
+  };
+  auto emit = [&](int64_t prow, int64_t strip, float (&r)[3]) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      r[k] += dpp_mov<0xB1>(r[k]);  // quad_perm [1,0,3,2]
+      r[k] += dpp_mov<0x4E>(r[k]);  // quad_perm [2,3,0,1]: the row's 4 lanes
+    }
+    if ((lane & 3) == 0)
+#pragma unroll
+      for (int k = 0; k < 3; ++k) M.mrp(k)[strip * prows + prow] = r[k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) r[k] = 0.f;
+  };
   auto add_eye = [&](int64_t row, int64_t col0, float(&w)[8]) {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -872,6 +947,8 @@ s8_stage_kernel(StageArgs args) {
       }
       if (do_m) *reinterpret_cast<f32x4 *>(U + lr * kEpStride + 8 * k + 4 * lh) = v;
     }
+    float a8[8], z8[8];
+    if (rsum) colv8(do_m ? R0 + i * 32 + cc : C0 + j * 32 + cc, a8, z8);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int row = rr + 16 * q;
@@ -881,6 +958,10 @@ s8_stage_kernel(StageArgs args) {
         const int64_t gr = R0 + i * 32 + row, gc = C0 + j * 32 + cc;
         if (eye) add_eye(gr, gc, w);
         put_operand8(dst_t, gr * ld_t + gc, w, pl_t);
+        if (rsum) {
+          accum(w, a8, z8, rs[0][q]);
+          if (j == kSubN - 1) emit(gr, C0 / kStripT, rs[0][q]);
+        }
       }
       if (do_m) {
         float w[8];
@@ -888,6 +969,10 @@ s8_stage_kernel(StageArgs args) {
         const int64_t gr = C0 + j * 32 + row, gc = R0 + i * 32 + cc;
         if (eye) add_eye(gr, gc, w);
         put_operand8(dst_m, gr * ld_m + gc, w, pl_m);
+        if (rsum) {
+          accum(w, a8, z8, rs[j][q]);
+          if (i == kSubM - 1) emit(gr, R0 / kStripM, rs[j][q]);
+        }
       }
     }
     // Keep the scheduler from hoisting every accumulator read to the top
@@ -1261,7 +1346,7 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.tiles_m = static_cast<int32_t>(C.rp / kTile);
     C.tiles_n = static_cast<int32_t>(C.cp / kTile);
     C.tiles_s = static_cast<int32_t>(C.rp / kSymTile);
-    C.parts = static_cast<int32_t>(ceil_div(C.cp, kPartRows));
+    C.parts = static_cast<int32_t>(C.cp);
     C.gs = C.cp > C.rp ? 1 : 0;
     const size_t xs = static_cast<size_t>(C.count) * C.rp * C.cp * sizeof(float);
     const size_t gs = static_cast<size_t>(C.count) * C.rp * C.rp * sizeof(float);
@@ -1277,7 +1362,9 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.fro = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));
     C.mb = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * C.parts * sizeof(double)));
     C.sch = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * sym_tiles(C.tiles_s) * sizeof(double)));
-    C.cst = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * 2 * sizeof(double)));
+    C.cst = reinterpret_cast<double *>(take(static_cast<size_t>(C.count) * kCst * sizeof(double)));
+    C.colv = reinterpret_cast<const float **>(take(static_cast<size_t>(C.count) * 2 * sizeof(float *)));
+    C.mrp = reinterpret_cast<float *>(take(static_cast<size_t>(C.count) * 3 * (C.rp * C.cp / kStripT) * sizeof(float)));
   }
   plan.bytes = off;
   return true;

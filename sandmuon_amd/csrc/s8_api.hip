@@ -16,24 +16,20 @@ struct S8IoArgs {
   int32_t planes;              // iterate stored as BF16 planes (comp mode)
 };
 
-// Row pass: per kPartRows input rows, the sum of squares -> fro partial.
-// grid = (ceil(rows / kPartRows), batch), block 256.
-__global__ void __launch_bounds__(256) s8_load_rows_kernel(S8IoArgs a) {
+// Norm pass: the input's sum of squares (FP64) -> the matrix's kCstFro.
+// grid = (1, batch), block 256.
+__global__ void __launch_bounds__(256) s8_load_norm_kernel(S8IoArgs a) {
   __shared__ double scratch[16];
   const S8Mat M{a.k, static_cast<int32_t>(blockIdx.y)};
   const float *x = a.x + static_cast<int64_t>(blockIdx.y) * a.sb;
-  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kPartRows;
   double s = 0.0;
-  for (int rr = 0; rr < kPartRows; ++rr) {
-    const int64_t i = i0 + rr;
-    if (i >= a.rows) break;
+  for (int64_t i = 0; i < a.rows; ++i)
     for (int64_t j = threadIdx.x; j < a.cols; j += 256) {
       const double v = x[i * a.sr + j * a.sc];
       s += v * v;
     }
-  }
   s = block_sum(s, scratch);
-  if (threadIdx.x == 0) M.fro()[blockIdx.x] = s;
+  if (threadIdx.x == 0) M.cst()[kCstFro] = s;
 }
 
 // Tile pass: 64x64 tiles of the padded parameter layout (input layout)
@@ -130,9 +126,8 @@ extern "C" int smx_s8(const float *x, float *out, int64_t batch, int64_t rows, i
   a.planes = mode == SMX_S8_COMP_BF16;
   const S8Mat M0{a.k, 0};
   const unsigned tiles = static_cast<unsigned>((M0.prow_pad() / 64) * (M0.pcol_pad() / 64));
-  hipLaunchKernelGGL(s8_load_rows_kernel, dim3(static_cast<unsigned>(ceil_div(rows, kPartRows)), batch),
-                     dim3(256), 0, st, a);
-  int rc = check_launch("s8 load rows");
+  hipLaunchKernelGGL(s8_load_norm_kernel, dim3(1, batch), dim3(256), 0, st, a);
+  int rc = check_launch("s8 load norm");
   if (rc) return rc;
   hipLaunchKernelGGL(s8_load_tiles_kernel, dim3(tiles, batch), dim3(256), 0, st, a);
   rc = check_launch("s8 load tiles");
