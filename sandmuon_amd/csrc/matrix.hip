@@ -181,47 +181,16 @@ struct PrepPack {
 static_assert(sizeof(PrepPack) <= 4000, "PrepPack is passed by value in the kernel arguments");
 static_assert(sizeof(MatJob) % 4 == 0, "the prep kernel copies jobs as 32-bit words");
 
-constexpr int kPrepThreads = 256;
-constexpr int kPrepUnroll = 12;  // loads in flight per thread (one pass over 3072 columns)
-
-// One block per job: the record into the table, and (rank-one term) the
-// constants sum z^2 and sum (a z)^2 of the matrix (FP64; each thread's
-// loads issued together).
-__global__ void __launch_bounds__(kPrepThreads) matrix_prep_kernel(PrepPack pack) {
-  __shared__ double scratch[16];
+// One 64-thread block per job: the record into the table, and the slot's
+// column vectors for the stage-5 row sums of the S8 map.
+__global__ void __launch_bounds__(64) matrix_prep_kernel(PrepPack pack) {
   const MatJob &J = pack.j[blockIdx.x];
   const uint32_t *src = reinterpret_cast<const uint32_t *>(&J);
   uint32_t *dst = reinterpret_cast<uint32_t *>(pack.table + blockIdx.x);
-  for (int k = threadIdx.x; k < static_cast<int>(sizeof(MatJob) / 4); k += kPrepThreads) dst[k] = src[k];
+  for (int k = threadIdx.x; k < static_cast<int>(sizeof(MatJob) / 4); k += 64) dst[k] = src[k];
   if (threadIdx.x == 0) {
-    // the column vectors of the slot, for the stage-5 row sums of the S8 map
     J.colv[0] = J.d.inv_col;
     J.colv[1] = J.d.z;
-  }
-  if (J.d.z == nullptr) return;  // uniform per block
-  const SMX_GLOBAL float *zp = (const SMX_GLOBAL float *)J.d.z, *ap = (const SMX_GLOBAL float *)J.d.inv_col;
-  double zz = 0.0, az = 0.0;
-  for (int64_t j0 = threadIdx.x; j0 < J.d.cols; j0 += kPrepThreads * kPrepUnroll) {
-    float z[kPrepUnroll], a[kPrepUnroll];
-#pragma unroll
-    for (int u = 0; u < kPrepUnroll; ++u) {
-      const int64_t j = j0 + kPrepThreads * u;
-      z[u] = j < J.d.cols ? zp[j] : 0.f;
-      a[u] = j < J.d.cols ? ap[j] : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < kPrepUnroll; ++u) {
-      const double zd = z[u], t = static_cast<double>(a[u]) * zd;
-      zz += zd * zd;
-      az += t * t;
-    }
-  }
-  zz = block_sum(zz, scratch);
-  az = block_sum(az, scratch);
-  if (threadIdx.x == 0) {
-    SMX_GLOBAL double *cst = (SMX_GLOBAL double *)J.cst;
-    cst[kCstZZ] = zz;
-    cst[kCstAZ] = az;
   }
 }
 
@@ -235,26 +204,87 @@ __host__ __device__ inline int64_t mapback_blocks(const Job &j) { return ceil_di
 template <typename Job>
 __host__ __device__ inline int64_t norm_blocks(const Job &j) { return ceil_div(j.d.rows, kRowThreads / 4); }
 
-// One 64-thread block per job: the FP64 sum of the job's per-block
-// partials (lane l takes partials l, l + 64, ..., then a fixed-order wave
-// sum) -> ||V||^2 (which = kCstFro, after the whiten) or ||U||^2 (kCstU,
-// after mapback_norm).
-__global__ void __launch_bounds__(64) matrix_total_kernel(const MatJob *jobs, int which) {
+// One block per job, after the whiten (which = kCstFro) or mapback_norm
+// (kCstU): the FP64 sums of the job's per-block partials (thread t takes
+// partials t, t + 256, ..., then a fixed-order block sum).  After the
+// whiten it also forms the rank-one constants sum z^2 and sum (a z)^2, and
+// ||V||^2 = sum b^2 |S a|^2 + (2 kappa + kappa^2 sum z^2) sum u^2 from the
+// whiten's two partials.
+constexpr int kTotalThreads = 256;
+constexpr int kTotalUnroll = 12;  // column loads in flight per thread (3072 columns in one pass)
+
+// Block-wide sums of N values at once (fixed order: wave sums, then the
+// waves in order); every thread receives them.
+template <int N>
+__device__ __forceinline__ void block_sums(double (&v)[N], double (*scratch)[kTotalThreads / 64]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = wave_sum(v[k]);
+  if (lane == 0)
+#pragma unroll
+    for (int k = 0; k < N; ++k) scratch[k][wave] = v[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < kTotalThreads / 64; ++w) t += scratch[k][w];
+    v[k] = t;
+  }
+}
+
+__global__ void __launch_bounds__(kTotalThreads) matrix_total_kernel(const MatJob *jobs, int which) {
+  __shared__ double scratch[4][kTotalThreads / 64];
   const DevJob J = load_job(jobs, blockIdx.x);
+  const DevDesc &d = J.d;
   const bool fro = which == kCstFro;
   const SMX_GLOBAL double *parts = fro ? J.fro : J.mb;
   const int64_t nblk = fro ? whiten_blocks(J) : norm_blocks(J);
-  constexpr int kU = 8;  // loads in flight per lane
-  double s = 0.0;
-  for (int64_t k0 = threadIdx.x; k0 < nblk; k0 += 64 * kU) {
-    double v[kU];
+  const bool r1 = fro && d.z != nullptr;  // uniform per block
+  // Every load of the thread first (partials, then z and a), then the sums.
+  double s[4] = {0.0, 0.0, 0.0, 0.0};  // partials (kind 0, kind 1), sum z^2, sum (a z)^2
+  for (int64_t k0 = threadIdx.x; k0 < nblk; k0 += kTotalThreads * 4) {
+    double v[2][4];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) v[u] = k0 + 64 * u < nblk ? parts[k0 + 64 * u] : 0.0;
+    for (int u = 0; u < 4; ++u) {
+      const int64_t k = k0 + kTotalThreads * u;
+      v[0][u] = k < nblk ? parts[k] : 0.0;
+      v[1][u] = fro && k < nblk ? parts[nblk + k] : 0.0;
+    }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) s += v[u];
+    for (int u = 0; u < 4; ++u) {
+      s[0] += v[0][u];
+      s[1] += v[1][u];
+    }
   }
-  s = wave_sum(s);
-  if (threadIdx.x == 0) J.cst[which] = s;
+  if (r1) {
+    for (int64_t j0 = threadIdx.x; j0 < d.cols; j0 += kTotalThreads * kTotalUnroll) {
+      float z[kTotalUnroll], a[kTotalUnroll];
+#pragma unroll
+      for (int u = 0; u < kTotalUnroll; ++u) {
+        const int64_t j = j0 + kTotalThreads * u;
+        z[u] = j < d.cols ? d.z[j] : 0.f;
+        a[u] = j < d.cols ? d.inv_col[j] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kTotalUnroll; ++u) {
+        const double zd = z[u], t = static_cast<double>(a[u]) * zd;
+        s[2] += zd * zd;
+        s[3] += t * t;
+      }
+    }
+  }
+  block_sums<4>(s, scratch);
+  if (threadIdx.x != 0) return;
+  if (!fro) {
+    J.cst[kCstU] = s[0];
+    return;
+  }
+  // s[0] = sum b^2 |S a|^2, s[1] = sum u^2
+  const double kappa = r1 ? d.kappa[0] : 0.0;
+  J.cst[kCstZZ] = s[2];
+  J.cst[kCstAZ] = s[3];
+  J.cst[kCstFro] = s[0] + (2.0 * kappa + kappa * kappa * s[2]) * s[1];
 }
 
 // ------------------------------------------------------------- whiten ---
@@ -299,22 +329,26 @@ __device__ __forceinline__ void row_sums(double (&v)[N], double (*red)[4], const
   }
 }
 
-// The block's partial (its rows in order) -> parts[blk].
-__device__ __forceinline__ void block_part(const DevJob &J, double row_part, const RowPos &p, int blk,
-                                           SMX_GLOBAL double *parts, double *rp) {
-  if ((threadIdx.x & 63) == 0 && p.wr == 0) rp[p.rib] = row_part;
+// The block's partials of the rows' b^2 |S a|^2 and u^2 (its rows in
+// order) -> parts[blk] and parts[nblk + blk].
+__device__ __forceinline__ void block_part(const DevJob &J, double vy, double vu, const RowPos &p, int blk, int nblk,
+                                           SMX_GLOBAL double *parts, double (*rp)[4]) {
+  if ((threadIdx.x & 63) == 0 && p.wr == 0) {
+    rp[0][p.rib] = vy;
+    rp[1][p.rib] = vu;
+  }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < 2) {
     double t = 0.0;
-    for (int r = 0; r < 4 / J.wpr; ++r) t += rp[r];
-    parts[blk] = t;
+    for (int r = 0; r < 4 / J.wpr; ++r) t += rp[threadIdx.x][r];
+    parts[threadIdx.x * nblk + blk] = t;
   }
 }
 
 template <bool R1>
 __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
   __shared__ double red[4][4];  // row_sums
-  __shared__ double rp[4];
+  __shared__ double rp[2][4];
   const int jid = find_job(range, blockIdx.x);
   const DevJob J = load_job(range.jobs, jid);
   const DevDesc &d = J.d;
@@ -328,9 +362,6 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
   SMX_GLOBAL float *mrow = live ? d.momentum + p.i * d.cols : nullptr;
   SMX_GLOBAL float *xrow = J.x + p.i * J.pcol_pad;
   const int pc4 = static_cast<int>(J.pcol_pad / 4);
-
-  // sum z^2 of the rank-one term (the prep launch)
-  const double zz = R1 ? J.cst[kCstZZ] : 0.0;
 
   // ---- pass 1: m' (stored), y = S a of the lane's columns, and the row's
   // sum y^2 and y.z.
@@ -395,15 +426,15 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
   }
   double v[2] = {static_cast<double>(wave_sum(y2)), static_cast<double>(wave_sum(yz))};
   row_sums<2>(v, red, p, J.wpr);
-  const double corr = R1 ? 2.0 * kappa + static_cast<double>(kappa) * kappa * zz : 0.0;
-  double row_part = 0.0;
+  double vy = 0.0, vu = 0.0;  // the row's b^2 |S a|^2 and u^2
   float b = 0.f, ku = 0.f;
   if (live) {
     const double bd = d.inv_row[p.i];
     const double u = bd * v[1];
     b = d.inv_row[p.i];
     ku = R1 ? kappa * static_cast<float>(u) : 0.f;
-    row_part = bd * bd * v[0] + corr * u * u;
+    vy = bd * bd * v[0];
+    vu = u * u;
     if (lane == 0 && p.wr == 0) J.u[p.i] = static_cast<float>(u);
   }
 
@@ -477,7 +508,7 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
       put_operand((float *)xrow, j, x, planes);
     }
   }
-  block_part(J, row_part, p, blk, J.fro, rp);
+  block_part(J, vy, vu, p, blk, static_cast<int>(whiten_blocks(J)), J.fro, rp);
 }
 
 // Transposed parameters: one wave per row, kFlipRows rows per block, the
@@ -489,11 +520,16 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
 template <bool R1, bool KEPT>
 __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange range) {
   __shared__ float tile[kFlipRows][kFlipChunk + 4];
-  __shared__ double rp[kFlipRows];
+  __shared__ double rp[2][kFlipRows];
   const int jid = find_job(range, blockIdx.x);
   const DevJob J = load_job(range.jobs, jid);
   const DevDesc &d = J.d;
-  const int blk = blockIdx.x - range.start[jid];
+  // Row group of the block: the hardware deals blocks to the 8 XCDs in
+  // turn, and the blocks of one XCD take consecutive groups, so the two
+  // 64-byte halves of a 128-byte line of X (adjacent K groups) meet in one
+  // L2.  (Every job's first block and block count are multiples of 8.)
+  const int jb = blockIdx.x - range.start[jid];
+  const int blk = (jb & 7) * static_cast<int>(J.prow_pad / kFlipRows / 8) + (jb >> 3);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the row: wave-uniform
   const int64_t i0 = static_cast<int64_t>(blk) * kFlipRows;
@@ -507,7 +543,6 @@ __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange rang
   constexpr bool kept = KEPT;  // the host's bucket: vec && cols <= kFlipChunk
   const int n4 = static_cast<int>(d.cols / 4);
   const SMX_GLOBAL float *grow = live && vec ? (const SMX_GLOBAL float *)d.grad + i * d.cols : nullptr;
-  const double zz = R1 ? J.cst[kCstZZ] : 0.0;
   const float b = live ? d.inv_row[i] : 0.f;
   // Slice t of chunk c of this lane: float4 c * kFlipChunk / 4 + lane + 64 t.
   // KEPT: pass 1 leaves b y = b S a of its row in the LDS tile, and pass 2
@@ -576,14 +611,14 @@ __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange rang
     }
   }
   const double Y2 = wave_sum(y2), YZ = wave_sum(yz);
-  const double corr = R1 ? 2.0 * kappa + static_cast<double>(kappa) * kappa * zz : 0.0;
-  double row_part = 0.0;
+  double vy = 0.0, vu = 0.0;  // the row's b^2 |S a|^2 and u^2
   float ku = 0.f;
   if (live) {
     const double bd = b;
     const double u = bd * YZ;
     ku = R1 ? kappa * static_cast<float>(u) : 0.f;
-    row_part = bd * bd * Y2 + corr * u * u;
+    vy = bd * bd * Y2;
+    vu = u * u;
     if (lane == 0) J.u[i] = static_cast<float>(u);
   }
 
@@ -658,12 +693,15 @@ __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange rang
     }
     __syncthreads();
   }
-  if (lane == 0) rp[wave] = row_part;
+  if (lane == 0) {
+    rp[0][wave] = vy;
+    rp[1][wave] = vu;
+  }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < 2) {
     double t = 0.0;
-    for (int r = 0; r < kFlipRows; ++r) t += rp[r];
-    J.fro[blk] = t;
+    for (int r = 0; r < kFlipRows; ++r) t += rp[threadIdx.x][r];
+    J.fro[threadIdx.x * whiten_blocks(J) + blk] = t;
   }
 }
 
@@ -867,7 +905,7 @@ static int launch_range(const MatJob *host, MatJob *table, int32_t first, int32_
 }
 
 static int matrix_totals(MatJob *table, int32_t m, int which, hipStream_t st) {
-  hipLaunchKernelGGL(matrix_total_kernel, dim3(static_cast<unsigned>(m)), dim3(64), 0, st, table, which);
+  hipLaunchKernelGGL(matrix_total_kernel, dim3(static_cast<unsigned>(m)), dim3(kTotalThreads), 0, st, table, which);
   return check_launch("matrix_total");
 }
 
@@ -973,7 +1011,7 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
       pk.n = std::min<int32_t>(kPrepBatch, m - b);
       for (int k = 0; k < pk.n; ++k) pk.j[k] = jobs[b + k];
       pk.table = table + b;
-      hipLaunchKernelGGL(matrix_prep_kernel, dim3(pk.n), dim3(kPrepThreads), 0, st, pk);
+      hipLaunchKernelGGL(matrix_prep_kernel, dim3(pk.n), dim3(64), 0, st, pk);
       const int rc = check_launch("matrix_prep");
       if (rc) return rc;
     }

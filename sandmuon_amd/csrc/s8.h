@@ -50,8 +50,8 @@ struct S8Class {
   int32_t n_flip;      // slots [0, n_flip) hold transposed parameters
   int32_t tiles_m;     // rp / kTile
   int32_t tiles_n;     // cp / kTile
-  int32_t parts;       // per-block partial slots per matrix (cp: the most blocks a
-                       // whiten or mapback launch gives one matrix)
+  int32_t parts;       // per-block partial slots per matrix (2 cp: two partials
+                       // for each of the at most cp blocks a whiten launch gives one matrix)
   int32_t tiles_s;     // rp / kSymTile
   int32_t gs;          // Gram-space iteration (cp > rp): the stages run on r x r
                        // products and X0 is applied once, at stage 5
@@ -68,7 +68,7 @@ struct S8Class {
                        // form): T = P G, and the accumulated product Q of a
                        // segment's stage polynomials (qa, qb: ping-pong)
   float *u;            // [count][cp] per param-row rank-one coefficient
-  double *fro;         // [count][parts] whiten: per-block partial sums of V^2
+  double *fro;         // [count][parts] whiten: per-block partial sums (two kinds)
   double *mb;          // [count][parts] mapback: per-block partial sums of U^2
   double *sch;         // [count][sym_tiles(tiles_s)] Schatten partials (one per upper-triangle Gram tile)
   double *cst;         // [count][kCst] per-matrix scalars (see the kCst* indices)

@@ -1346,7 +1346,7 @@ bool plan_s8(const int64_t *r, const int64_t *c, const bool *flips, int32_t n, i
     C.tiles_m = static_cast<int32_t>(C.rp / kTile);
     C.tiles_n = static_cast<int32_t>(C.cp / kTile);
     C.tiles_s = static_cast<int32_t>(C.rp / kSymTile);
-    C.parts = static_cast<int32_t>(C.cp);
+    C.parts = static_cast<int32_t>(2 * C.cp);
     C.gs = C.cp > C.rp ? 1 : 0;
     const size_t xs = static_cast<size_t>(C.count) * C.rp * C.cp * sizeof(float);
     const size_t gs = static_cast<size_t>(C.count) * C.rp * C.rp * sizeof(float);
