@@ -58,6 +58,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 namespace smx {
@@ -125,6 +126,8 @@ struct StageArgs {
   int32_t seg_off[kMaxSeg + 1];  // block offsets (multiples of 8)
   int32_t seg_cls[kMaxSeg];
   int32_t seg_op[kMaxSeg];       // SYM / APPLY launches: the product of the segment (SegOp)
+  int32_t seg_slot0[kMaxSeg];    // the segment's matrices: slots slot0 .. slot0 + cnt - 1 of its class
+  int32_t seg_cnt[kMaxSeg];
   int32_t n_seg;
   int32_t stage;  // 1..5
   int32_t sq_small;  // this run's square uses 128 x 128 tiles (else 256 x 128)
@@ -658,7 +661,9 @@ __device__ Stage1Scalars stage1_scalars(const S8Mat &M, bool sq_small, double *b
 struct TileRef {
   const S8Class *k;
   int64_t L;
-  int op;  // SegOp of the segment (SYM and APPLY launches)
+  int op;     // SegOp of the segment (SYM and APPLY launches)
+  int slot0;  // the segment's first slot and number of matrices
+  int cnt;
 };
 __device__ __forceinline__ TileRef tile_of(const StageArgs &args) {
   const int b = blockIdx.x;
@@ -666,7 +671,8 @@ __device__ __forceinline__ TileRef tile_of(const StageArgs &args) {
   while (seg + 1 < args.n_seg && b >= args.seg_off[seg + 1]) ++seg;
   const int jb = b - args.seg_off[seg];
   const int per = (args.seg_off[seg + 1] - args.seg_off[seg]) / 8;
-  return TileRef{&args.L.cls[args.seg_cls[seg]], static_cast<int64_t>(jb % 8) * per + jb / 8, args.seg_op[seg]};
+  return TileRef{&args.L.cls[args.seg_cls[seg]], static_cast<int64_t>(jb % 8) * per + jb / 8, args.seg_op[seg],
+                 args.seg_slot0[seg], args.seg_cnt[seg]};
 }
 
 // Epilogue staging: a 32 x 32 FP32 block per orientation per wave, rows
@@ -712,8 +718,8 @@ s8_stage_kernel(StageArgs args) {
   const TileRef ref = tile_of(args);
   const S8Class &K = *ref.k;
   const int64_t tpm = phase_tiles(K, PHASE, TM == kSymTile, ref.op);
-  if (ref.L >= tpm * K.count) return;
-  const int slot = static_cast<int>(ref.L / tpm);
+  if (ref.L >= tpm * ref.cnt) return;
+  const int slot = ref.slot0 + static_cast<int>(ref.L / tpm);
   const int64_t tix = ref.L % tpm;
   int64_t tm, tn;
   bool diag = false;  // Gram / square: a half of a diagonal 256 x 256 block
@@ -1010,8 +1016,8 @@ __global__ void __launch_bounds__(256) s8_poly1_kernel(StageArgs args) {
   const TileRef ref = tile_of(args);
   const S8Class &K = *ref.k;
   const int64_t tpm = poly_blocks_per_matrix(K);
-  if (ref.L >= tpm * K.count) return;
-  const S8Mat M{K, static_cast<int>(ref.L / tpm)};
+  if (ref.L >= tpm * ref.cnt) return;
+  const S8Mat M{K, ref.slot0 + static_cast<int>(ref.L / tpm)};
   const int64_t g0 = (ref.L % tpm) * kPolyChunk;  // first group of the block
   const int64_t gpr = K.rp / 16;                   // groups per row
   const float *G = M.g();
@@ -1131,8 +1137,19 @@ static int stage_mode(const S8Layout &Lay, int stage) {
 struct Seg {
   int cls;
   int op;
+  int lo, hi;  // slots
 };
-static std::vector<Seg> launch_segments(const S8Layout &Lay, int phase, int stage, const std::vector<int> &ops) {
+// The matrices of one launch chain: slots lo[c] .. hi[c] - 1 of class c.
+struct SlotSet {
+  int32_t lo[kMaxClasses] = {}, hi[kMaxClasses] = {};
+  bool empty() const {
+    for (int i = 0; i < kMaxClasses; ++i)
+      if (hi[i] > lo[i]) return false;
+    return true;
+  }
+};
+static std::vector<Seg> launch_segments(const S8Layout &Lay, const SlotSet &set, int phase, int stage,
+                                        const std::vector<int> &ops) {
   std::vector<int> order(Lay.n_classes);
   for (int i = 0; i < Lay.n_classes; ++i) order[i] = i;
   std::stable_sort(order.begin(), order.end(), [&](int x, int y) {
@@ -1143,7 +1160,8 @@ static std::vector<Seg> launch_segments(const S8Layout &Lay, int phase, int stag
   std::vector<Seg> segs;
   for (int ci : order) {
     const S8Class &k = Lay.cls[ci];
-    if (k.count == 0) continue;
+    const int lo = set.lo[ci], hi = set.hi[ci];
+    if (hi <= lo) continue;
     if (phase == kSym || phase == kApply) {
       for (int op : ops) {
         const bool takes = phase == kSym ? k.gs != 0 && gs_sym(stage)
@@ -1151,12 +1169,12 @@ static std::vector<Seg> launch_segments(const S8Layout &Lay, int phase, int stag
                            : op == kOpApplyQ ? k.gs != 0 && gs_apply_q(stage)
                            : op == kOpApplyMid ? k.gs != 0 && stage == 2
                                                : k.gs != 0 && stage == 5;
-        if (takes) segs.push_back(Seg{ci, op});
+        if (takes) segs.push_back(Seg{ci, op, lo, hi});
       }
       continue;
     }
     if (k.gs && phase == kGram && !gs_gram(stage)) continue;
-    segs.push_back(Seg{ci, -1});
+    segs.push_back(Seg{ci, -1, lo, hi});
   }
   return segs;
 }
@@ -1174,18 +1192,19 @@ static double launch_flops(const S8Layout &Lay, int phase, int stage, bool small
     const S8Class &k = Lay.cls[sg.cls];
     const double tiles = static_cast<double>(phase_tiles(k, phase, small, sg.op));
     const double K = phase == kGram ? static_cast<double>(k.cp) : static_cast<double>(k.rp);
-    f += k.count * tiles * 2.0 * tm * kTileN * K * prod;
+    const double cnt = sg.hi - sg.lo;
+    f += cnt * tiles * 2.0 * tm * kTileN * K * prod;
     // one-hot: per wave 2 kSubM stages of kSubN MFMA tiles
     if (phase == kSquare && stage != 1)
-      f += k.count * tiles * kWaves * (2.0 * sub_m) * kSubN * 2.0 * 32 * 32 * kBK * prod;
+      f += cnt * tiles * kWaves * (2.0 * sub_m) * kSubN * 2.0 * 32 * 32 * kBK * prod;
   }
   return f;
 }
 
-// Whether a symmetric-output launch (square, SYM) over the classes `use`
-// selects takes 128 x 128 tiles: rounds of the device's block slots (two
-// 256 x 128 or three 128 x 128 blocks per CU), a round of the smaller tile
-// counted as 0.9 of one of the larger.
+// Whether a symmetric-output launch (square, SYM) over use(i) matrices of
+// each class i takes 128 x 128 tiles: rounds of the device's block slots
+// (two 256 x 128 or three 128 x 128 blocks per CU), a round of the smaller
+// tile counted as 0.9 of one of the larger.
 template <typename Use>
 static bool small_tiles(const S8Layout &Lay, Use use) {
   static int cus[64] = {};
@@ -1195,9 +1214,9 @@ static bool small_tiles(const S8Layout &Lay, Use use) {
     return false;
   int64_t big = 0, small = 0;
   for (int i = 0; i < Lay.n_classes; ++i) {
-    if (!use(Lay.cls[i])) continue;
-    big += Lay.cls[i].count * square_tiles(Lay.cls[i], false);
-    small += Lay.cls[i].count * square_tiles(Lay.cls[i], true);
+    const int64_t cnt = use(i);  // matrices of class i in the launches
+    big += cnt * square_tiles(Lay.cls[i], false);
+    small += cnt * square_tiles(Lay.cls[i], true);
   }
   const double r_big = static_cast<double>(ceil_div(big, 2 * static_cast<int64_t>(cus[dev])));
   const double r_small = static_cast<double>(ceil_div(small, 3 * static_cast<int64_t>(cus[dev])));
@@ -1220,7 +1239,7 @@ static void launch_stage(bool small, int32_t blocks, const StageArgs &a, hipStre
 // sq_small: the run's square takes 128 x 128 tiles (the stage-1 Schatten
 // partials are per square tile); sym_small: its SYM launches do.
 template <int PHASE>
-static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, bool sym_small, hipStream_t st,
+static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, bool sq_small, bool sym_small, hipStream_t st,
                         double &flops, const std::vector<int> &ops = {}) {
   const bool small = PHASE == kSquare ? sq_small : PHASE == kSym ? sym_small : false;
   StageArgs a{};
@@ -1232,17 +1251,19 @@ static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, bool sym_
   a.b = static_cast<float>(co[1]);
   a.c = static_cast<float>(co[2]);
   a.b_over_c = static_cast<float>(co[1] / co[2]);
-  const std::vector<Seg> segs = launch_segments(Lay, PHASE, stage, ops);
+  const std::vector<Seg> segs = launch_segments(Lay, set, PHASE, stage, ops);
   if (static_cast<int>(segs.size()) > kMaxSeg) return fail(SMX_EINVAL, "s8: too many launch segments");
   int32_t off = 0;
   a.n_seg = 0;
   for (const Seg &sg : segs) {
     const S8Class &k = Lay.cls[sg.cls];
     const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE, small, sg.op);
-    const int64_t nt = round_up(tpm * k.count, 8);
+    const int64_t nt = round_up(tpm * (sg.hi - sg.lo), 8);
     a.seg_off[a.n_seg] = off;
     a.seg_cls[a.n_seg] = sg.cls;
     a.seg_op[a.n_seg] = sg.op;
+    a.seg_slot0[a.n_seg] = sg.lo;
+    a.seg_cnt[a.n_seg] = sg.hi - sg.lo;
     ++a.n_seg;
     off += static_cast<int32_t>(nt);
   }
@@ -1271,31 +1292,116 @@ static int launch_phase(const S8Layout &Lay, int stage, bool sq_small, bool sym_
   return timing_end(slot, st, PHASE, f);
 }
 
-// The whole S8 run: per stage one launch per phase over every class it
-// applies to; Gram-space classes add their two SYM products before the
-// apply launch at stages 1, 3 and 4, and an apply of their own after it at
-// stages 2 (X2) and 5 (X5).
-// The launch recorder gets one record for the run.
+// Stage `stage` of the S8 map over the matrices of `set`: one launch per
+// phase; Gram-space classes add their two SYM products before the apply
+// launch at stages 1, 3 and 4, and an apply of their own after it at stages
+// 2 (X2) and 5 (X5).
+static int run_s8_set_stage(const S8Layout &Lay, const SlotSet &set, int stage, hipStream_t st, double &flops) {
+  auto cnt = [&](int i) { return static_cast<int64_t>(set.hi[i] - set.lo[i]); };
+  const bool sq_small = small_tiles(Lay, [&](int i) { return cnt(i); });
+  const bool sym_small = small_tiles(Lay, [&](int i) { return Lay.cls[i].gs ? cnt(i) : int64_t{0}; });
+  bool any_gs = false;
+  for (int i = 0; i < Lay.n_classes; ++i) any_gs = any_gs || (Lay.cls[i].gs && cnt(i) > 0);
+  int rc = SMX_OK;
+  {
+    rc = launch_phase<kGram>(Lay, set, stage, sq_small, sym_small, st, flops);
+    if (!rc) rc = launch_phase<kSquare>(Lay, set, stage, sq_small, sym_small, st, flops);
+    if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, set, stage, sq_small, sym_small, st, flops);
+    if (!rc && any_gs && gs_sym(stage)) {
+      rc = launch_phase<kSym>(Lay, set, stage, sq_small, sym_small, st, flops, {kOpPG});
+      if (!rc) rc = launch_phase<kSym>(Lay, set, stage, sq_small, sym_small, st, flops, {kOpTP});
+    }
+    if (!rc) rc = launch_phase<kApply>(Lay, set, stage, sq_small, sym_small, st, flops, {kOpApplyX, kOpApplyQ});
+    if (!rc && any_gs && (stage == 2 || stage == 5))
+      rc = launch_phase<kApply>(Lay, set, stage, sq_small, sym_small, st, flops,
+                                {stage == 2 ? kOpApplyMid : kOpApplyFinal});
+  }
+  return rc;
+}
+
+// A second stream of the device (default priority) and the two events of a
+// fork and join, created once per device.
+struct ForkStream {
+  hipStream_t aux = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+static std::mutex g_fork_lock;
+static ForkStream g_fork[64];
+
+static int fork_stream(ForkStream *&out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(SMX_ELAUNCH, "s8: no current HIP device");
+  std::lock_guard<std::mutex> lock(g_fork_lock);
+  ForkStream &f = g_fork[dev];
+  if (!f.aux) {
+    if (hipStreamCreateWithFlags(&f.aux, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&f.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&f.join, hipEventDisableTiming) != hipSuccess)
+      return fail(SMX_ELAUNCH, "s8: cannot create the second stream and its events");
+  }
+  out = &f;
+  return SMX_OK;
+}
+
+// The whole S8 run.  The matrices are independent until the run ends, so
+// they go to two launch chains: a class of at least kSplitCount matrices is
+// split in halves, one to each chain, and a smaller class whole to the
+// chain with less work so far (r^2 c per matrix, largest classes first).
+// One chain runs on the caller's stream, the other on a second stream
+// forked from it and joined back before the run ends: the blocks of one
+// chain's launches fill the CUs that the other's leave idle (a launch's
+// tail, tiles that take longer than the rest).  The launch recorder gets
+// one record for the run, on the caller's stream.
+constexpr int kSplitCount = 4;
+
 int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
   int slot = -1;
   int rc = timing_begin(st, slot, true);
   if (rc) return rc;
-  const bool sq_small = small_tiles(Lay, [](const S8Class &) { return true; });
-  const bool sym_small = small_tiles(Lay, [](const S8Class &k) { return k.gs != 0; });
-  bool any_gs = false;
-  for (int i = 0; i < Lay.n_classes; ++i) any_gs = any_gs || (Lay.cls[i].gs && Lay.cls[i].count);
-  double flops = 0.0;
-  for (int stage = 1; stage <= 5 && !rc; ++stage) {
-    rc = launch_phase<kGram>(Lay, stage, sq_small, sym_small, st, flops);
-    if (!rc) rc = launch_phase<kSquare>(Lay, stage, sq_small, sym_small, st, flops);
-    if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, stage, sq_small, sym_small, st, flops);
-    if (!rc && any_gs && gs_sym(stage)) {
-      rc = launch_phase<kSym>(Lay, stage, sq_small, sym_small, st, flops, {kOpPG});
-      if (!rc) rc = launch_phase<kSym>(Lay, stage, sq_small, sym_small, st, flops, {kOpTP});
+  std::vector<int> order;
+  for (int i = 0; i < Lay.n_classes; ++i)
+    if (Lay.cls[i].count) order.push_back(i);
+  auto work = [&](int i, int n) {
+    const S8Class &k = Lay.cls[i];
+    return static_cast<double>(n) * k.rp * k.rp * k.cp;
+  };
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int x, int y) { return work(x, Lay.cls[x].count) > work(y, Lay.cls[y].count); });
+  SlotSet set[2];
+  double load[2] = {0.0, 0.0};
+  for (int i : order) {
+    const int c = Lay.cls[i].count;
+    if (c >= kSplitCount) {
+      set[0].lo[i] = 0;
+      set[0].hi[i] = set[1].lo[i] = c - c / 2;
+      set[1].hi[i] = c;
+      load[0] += work(i, c - c / 2);
+      load[1] += work(i, c / 2);
+    } else {
+      const int t = load[0] <= load[1] ? 0 : 1;
+      set[t].lo[i] = 0;
+      set[t].hi[i] = c;
+      load[t] += work(i, c);
     }
-    if (!rc) rc = launch_phase<kApply>(Lay, stage, sq_small, sym_small, st, flops, {kOpApplyX, kOpApplyQ});
-    if (!rc && any_gs && (stage == 2 || stage == 5))
-      rc = launch_phase<kApply>(Lay, stage, sq_small, sym_small, st, flops, {stage == 2 ? kOpApplyMid : kOpApplyFinal});
+  }
+  double flops = 0.0;
+  if (set[1].empty()) {
+    for (int stage = 1; stage <= 5 && !rc; ++stage) rc = run_s8_set_stage(Lay, set[0], stage, st, flops);
+  } else {
+    ForkStream *f = nullptr;
+    rc = fork_stream(f);
+    if (!rc && (hipEventRecord(f->fork, st) != hipSuccess || hipStreamWaitEvent(f->aux, f->fork, 0) != hipSuccess))
+      rc = fail(SMX_ELAUNCH, "s8: fork to the second stream failed");
+    // The two chains are enqueued a stage at a time each, so that the
+    // second starts while the host is still enqueuing the first.
+    for (int stage = 1; stage <= 5 && !rc; ++stage) {
+      rc = run_s8_set_stage(Lay, set[1], stage, f->aux, flops);
+      if (!rc) rc = run_s8_set_stage(Lay, set[0], stage, st, flops);
+    }
+    // Join even after a failed launch, so the caller's stream never runs
+    // ahead of work already on the second stream.
+    if (f && (hipEventRecord(f->join, f->aux) != hipSuccess || hipStreamWaitEvent(st, f->join, 0) != hipSuccess) && !rc)
+      rc = fail(SMX_ELAUNCH, "s8: join of the second stream failed");
   }
   if (rc) return rc;
   return timing_end(slot, st, kSpan, flops);

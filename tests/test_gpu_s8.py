@@ -152,15 +152,19 @@ def test_s8_timing_runs_only_records_one_span_per_run(device):
 @pytest.mark.parametrize("batch,small", [(8, True), (160, False)])
 def test_s8_square_tile_geometries(device, mode, batch, small):
     """The square phase takes 128 x 128 tiles when they need fewer rounds of
-    the CUs' block slots (8 matrices of 512 x 512 on 256 CUs: 80 small tiles
-    against 48 large ones, one round each) and 256 x 128 tiles otherwise
-    (160 matrices: 960 large tiles fit two rounds of two blocks per CU, the
-    1600 small ones need three rounds of three, counted 0.9 each).  Both geometries meet the gates;
-    the recorded square FLOPs show which one ran."""
+    the CUs' block slots and 256 x 128 tiles otherwise.  A class of 4 or
+    more matrices runs as two launch chains of halves, and each chain's
+    launches decide for themselves: 4 matrices of 512 x 512 on 256 CUs give
+    40 small tiles against 24 large ones, one round each; 80 matrices give
+    480 large tiles in one round of two blocks per CU, while their 800 small
+    ones need two rounds of three, counted 0.9 each.  Both geometries meet
+    the gates; the recorded square FLOPs show which one ran."""
     cus = torch.cuda.get_device_properties(device).multi_processor_count
-    big_rounds = -(-batch * 6 // (2 * cus))
-    small_rounds = -(-batch * 10 // (3 * cus))
-    assert (0.9 * small_rounds < big_rounds) == small, "the case no longer selects the geometry it names"
+    chains = [batch - batch // 2, batch // 2] if batch >= 4 else [batch]
+    for n in chains:
+        big_rounds = -(-n * 6 // (2 * cus))
+        small_rounds = -(-n * 10 // (3 * cus))
+        assert (0.9 * small_rounds < big_rounds) == small, "the case no longer selects the geometry it names"
     torch.manual_seed(batch)
     x = torch.randn(batch, 512, 512)
     from sandmuon_amd import _native
@@ -171,8 +175,12 @@ def test_s8_square_tile_geometries(device, mode, batch, small):
         _native.s8_timing(False)
     rec = _native.s8_timing_read()
     prod = 3 if mode == "comp_bf16" else 1
-    square1 = [f for _, p, f in rec if p == "square"][0]
     tiles, tm = (10, 128) if small else (6, 256)
-    assert square1 == batch * tiles * 2 * tm * 128 * 512 * prod
+    # per matrix: stage 1 (G G) and stages 2-5 (G G plus the one-hot (b/c) G
+    # MFMAs: per wave 2 tm/64 K stages of 2 32x32x16 products per tile)
+    f1 = tiles * 2 * tm * 128 * 512 * prod
+    f2 = f1 + tiles * 4 * (2 * tm // 64) * 2 * 2 * 32 * 32 * 16 * prod
+    want = sorted(f for n in chains for f in [n * f1] + [n * f2] * 4)
+    assert sorted(f for _, p, f in rec if p == "square") == want
     errs = per_matrix_rel(out, O.s8(x))
     assert max(errs) <= TOL[mode]
