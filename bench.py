@@ -53,7 +53,10 @@ def parse():
 
 
 def copy_calibration(mb):
-    """Three plain copies of `mb` MB (reads and writes mb*2^20 bytes each)."""
+    """Three plain copies of `mb` MB (reads and writes mb*2^20 bytes each),
+    the known-size reference for the rocprofv3 byte counters, then the rate
+    of 20 more: the device's read+write streaming ceiling, against which the
+    elementwise kernels of the step (read+write mixes) are judged."""
     n = mb * (1 << 20) // 4
     src = torch.randn(n, device="cuda")
     dst = torch.empty_like(src)
@@ -61,7 +64,15 @@ def copy_calibration(mb):
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 3}), flush=True)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(20):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) / 20 * 1e3
+    print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 3, "timed_copies": 20, "us_per_copy": round(us, 1),
+                      "read_write_tb_s": round(2 * n * 4 / us / 1e6, 3)}), flush=True)
 
 
 # ------------------------------------------------------------ workload ---
@@ -428,7 +439,9 @@ def main():
     peak_mfma = BF16_PEAK if args.s8_mode == "comp_bf16" else FP32_PEAK
     stats_gbs = stat_bytes / (hooks_ms * 1e-3) / 1e9
     s8_tfs = s8_issued / (s8_ms * 1e-3) / 1e12
-    traffic = committed_traffic() or {}
+    # The committed counter summary covers the cfg4 step in comp_bf16 mode;
+    # other workloads and modes carry no traffic figure.
+    traffic = (committed_traffic() or {}) if (args.config, args.s8_mode) == ("gpt103m", "comp_bf16") else {}
     roof_stats = {"bound": "hbm", "achieved": round(stats_gbs, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                   "frac": round(stats_gbs / (HBM_PEAK / 1e9), 4),
                   "traffic": traffic.get("stats_accumulate_kernel", {}).get("hbm_bytes_per_step"),

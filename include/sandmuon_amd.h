@@ -233,7 +233,11 @@ size_t smx_matrix_step_workspace_bytes(const int64_t *rows,
  * set) or none has (SMX_EINVAL otherwise); an optimizer is one or the
  * other.  The workspace (256-byte aligned, at least
  * smx_matrix_step_workspace_bytes) holds the S8 iterates; its contents on
- * entry are irrelevant. */
+ * entry are irrelevant.  Everything is ordered on `stream`: the S8 map
+ * runs part of its matrices on a second stream of the device (created by
+ * the library, default priority), which waits for `stream` at the start
+ * and which `stream` waits for before the call's later launches, so to
+ * the caller the call behaves as if every launch were on `stream`. */
 int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode,
                     void *workspace, size_t workspace_bytes, void *stream);
 
@@ -255,7 +259,9 @@ int smx_matrix_step_static(const smx_matrix_desc *descs, int32_t n, int mode,
  * 69-93.  x and out are [batch, rows, cols] fp32 with the given strides
  * (elements); out may alias x.  A matrix that is entirely zero maps to
  * zero.  (The reference returns zeros only when the whole batch is zero
- * and NaN for a zero matrix inside a non-zero batch.)
+ * and NaN for a zero matrix inside a non-zero batch.)  Ordered on
+ * `stream` as smx_matrix_step is (a batch of 4 or more matrices runs half
+ * of them on the library's second stream).
  * ------------------------------------------------------------------ */
 size_t smx_s8_workspace_bytes(int64_t batch, int64_t rows, int64_t cols,
                               int mode);
