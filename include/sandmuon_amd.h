@@ -341,6 +341,18 @@ int smx_graft(const float *x, float *out, int64_t n, int64_t output_rows,
  * ------------------------------------------------------------------ */
 int smx_s8_comp_stages(int32_t k);
 
+/* ------------------------------------------------------------------ *
+ * Tile geometry of the S8 GEMM launches (no counterpart in the reference;
+ * a test and measurement aid).  0 (the default): each launch picks its
+ * tiles from its size (256 x 256 blocks of 8 waves for launches that fill
+ * the device with a long K loop, else 256 x 128 or 128 x 128 blocks of 4
+ * waves); 1: 256 x 256 tiles for every launch; 2: never 256 x 256.  The
+ * results agree to rounding across geometries.  Process-wide, read at each
+ * S8 launch; returns the previous value, or SMX_EINVAL for a value outside
+ * [0, 2] (then nothing changes).
+ * ------------------------------------------------------------------ */
+int smx_s8_tile_geometry(int32_t policy);
+
 #ifdef __cplusplus
 }
 #endif

@@ -92,6 +92,7 @@ SIGNATURES = {
                                 c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "smx_graft": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p]),
     "smx_s8_comp_stages": (c_int, [c_int32]),
+    "smx_s8_tile_geometry": (c_int, [c_int32]),
     "smx_s8_timing": (c_int, [c_int32]),
     "smx_s8_timing_read": (c_int32, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(c_int32),
                                      ctypes.POINTER(c_double), c_int32]),
@@ -358,6 +359,14 @@ def graft(x: torch.Tensor, out: torch.Tensor, output_rows: int) -> None:
     rc = lib().smx_graft(x.data_ptr(), out.data_ptr(), x.numel(), output_rows, work.data_ptr(), 1024,
                          stream_of(x.device))
     _check(rc, "smx_graft")
+
+
+def s8_tile_geometry(policy: int) -> int:
+    """Sets the S8 GEMM tile geometry policy (0 automatic, 1 256 x 256 tiles
+    for every launch, 2 never 256 x 256; a test aid); returns the old value."""
+    prev = lib().smx_s8_tile_geometry(int(policy))
+    _check(min(prev, 0), "smx_s8_tile_geometry")
+    return prev
 
 
 def s8_comp_stages(k: int) -> int:

@@ -88,38 +88,56 @@ constexpr int kMaxSeg = 2 * kMaxClasses;
 constexpr int kS8HiOnly = 2;
 // Stages 1..g_comp_stages of SMX_S8_COMP_BF16 are compensated.
 static int g_comp_stages = 5;
+// Tile geometry policy (smx_s8_tile_geometry): 0 automatic (pick_geo),
+// 1 256 x 256 tiles for every GEMM launch, 2 never 256 x 256.
+static int g_tile_policy = 0;
 
-constexpr int kThreads = 256;      // 4 waves, one per SIMD
-constexpr int kWaves = kThreads / 64;
-constexpr int kTileN = 128;         // block output tile columns
-constexpr int kSubN = 2;            // 32x32 MFMA column tiles per wave (waves 2 x 2)
+constexpr int kSubN = 2;            // 32x32 MFMA column tiles per wave (64 columns)
 constexpr int kBK = 16;             // K per pipeline stage
-constexpr int kOpB = kTileN * kBK * 4;  // B operand tile 128 x 16 (4 bytes per element)
 constexpr int kStages = 3;          // LDS ring depth (2 stages in flight)
-constexpr int kLoadsB = kOpB / 1024 / kWaves;  // 1 KB loads per wave
-constexpr int kKmRow = kTileN * 4;  // bytes per K row of the K-major B tile
 
-// Block tile geometry, by output rows TM: 256 x 128 (each wave 128 x 64,
-// two blocks per CU) or 128 x 128 (each wave 64 x 64, three blocks per CU).
-// The Gram and the apply use 256 x 128 tiles.  The square uses 128 x 128
-// tiles when they take fewer rounds of the CUs' block slots, allowing for
-// their lower rate (square_small): the smaller tile moves a third more
-// operand bytes per MFMA, and a round of it takes 0.9 of a round of the
-// larger one.  At 768 x 768 the square's 12 half-tiles per matrix need two
-// rounds of 512 slots, its 21 small tiles 1.5 rounds of 768 (cfg4: 104
-// against 117 us per launch); at 2048 x 2048 the larger tile wins.
-// (128 x 128 Gram tiles measured no faster at 768 x 3072.)
-template <int TM>
+// Block tile geometries.  Each wave computes 32 kSubM x 64 outputs
+// (kSubM x kSubN MFMA 32x32 tiles); the waves of a block are 2 x kWavesN.
+//   kGeoM  256 x 128, 4 waves of 128 x 64, two blocks per CU;
+//   kGeoS  128 x 128, 4 waves of 64 x 64, three blocks per CU;
+//   kGeoL  256 x 256, 8 waves of 128 x 64 (two per SIMD), one block per CU.
+// The wave tile, and so the LDS fragment reads per MFMA, is the same in M
+// and L; an L block moves a third fewer operand bytes into LDS per MFMA
+// (its 256 A rows serve 256 B rows), which is what bounds these loops: the
+// direct-to-LDS operand stream, not the MFMAs (a timing copy without the
+// refill loads ran the cfg5 S8 37% faster, one without the fragment reads
+// 11% faster).  A round of the device's block slots does the same work in
+// M and L; the host picks the geometry per launch (pick_geo).
+enum TileGeo { kGeoM = 0, kGeoS = 1, kGeoL = 2 };
+template <int TM, int TN>
 struct Geo {
-  static constexpr int kTileM = TM;
-  static constexpr int kSubM = TM / 64;           // 32x32 MFMA row tiles per wave
-  static constexpr int kOpA = TM * kBK * 4;       // A operand tile TM x 16
+  static constexpr int kTileM = TM, kTileN = TN;
+  static constexpr int kSubM = TM / 64;             // 32x32 MFMA row tiles per wave
+  static constexpr int kWavesN = TN / (32 * kSubN);
+  static constexpr int kWaves = 2 * kWavesN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kOpA = TM * kBK * 4;       // A operand tile TM x 16 (4 bytes per element)
+  static constexpr int kOpB = TN * kBK * 4;       // B operand tile TN x 16
   static constexpr int kStageBytes = kOpA + kOpB;
   static constexpr int kRingBytes = kStages * kStageBytes;
-  static constexpr int kLoadsA = kOpA / 1024 / kWaves;
+  static constexpr int kLoadsA = kOpA / 1024 / kWaves;  // 1 KB loads per wave
+  static constexpr int kLoadsB = kOpB / 1024 / kWaves;
   static constexpr int kLoadsPerStage = kLoadsA + kLoadsB;
-  static constexpr int kWavesPerEU = TM == 256 ? 2 : 3;
+  static constexpr int kKmRow = TN * 4;           // bytes per K row of the K-major B tile
+  static constexpr int kWavesPerEU = TM == 128 ? 3 : 2;
+  static constexpr int kGeo = TN == 256 ? kGeoL : TM == 128 ? kGeoS : kGeoM;
 };
+using GeoM = Geo<256, 128>;
+using GeoS = Geo<128, 128>;
+using GeoL = Geo<256, 256>;
+// (kGeoM: the Gram and the apply at 768 x 768, 128 x 128 Gram tiles measured
+// no faster at 768 x 3072.  kGeoS: the square when its tiles take fewer
+// rounds of the CUs' block slots, allowing for their lower rate: the
+// smaller tile moves a third more operand bytes per MFMA, and a round of it
+// takes 0.9 of a round of the larger one.  At 768 x 768 the square's 12
+// half-tiles per matrix need two rounds of 512 slots, its 21 small tiles
+// 1.5 rounds of 768 (cfg4: 104 against 117 us per launch); at 2048 x 2048
+// the larger tile wins.)
 
 struct StageArgs {
   S8Layout L;
@@ -130,7 +148,7 @@ struct StageArgs {
   int32_t seg_cnt[kMaxSeg];
   int32_t n_seg;
   int32_t stage;  // 1..5
-  int32_t sq_small;  // this run's square uses 128 x 128 tiles (else 256 x 128)
+  int32_t sq_geo;    // TileGeo of this run's square (the stage-1 Schatten partials are per square tile)
   float a, b, c;
   float b_over_c;
 };
@@ -193,20 +211,23 @@ __device__ __forceinline__ TileOffsets<N> tile_offsets(int64_t ld, int64_t row0,
   return t;
 }
 
-// K-major tile (16 K rows, N columns n0 .. n0 + kTileN - 1 of a row-major
-// operand with rows of `ld` elements; kKmRow bytes per K row): load i
-// covers K rows 2 (wave*N+i) and 2 (wave*N+i) + 1, lane l filling slot
-// l & 31 of its row k with logical chunk (l & 31) ^ swzk(k).  The scalar
-// base of a stage at K offset k0 moves by 4*k0*ld bytes.
-template <int N>
+// K-major tile (16 K rows, TN columns n0 .. n0 + TN - 1 of a row-major
+// operand with rows of `ld` elements; KMROW = 4 TN bytes per K row): with
+// 512-byte rows load i covers K rows 2 (wave*N+i) and 2 (wave*N+i) + 1,
+// lane l filling slot l & 31 of its row k; with 1 KB rows it covers K row
+// wave*N+i, lane l filling slot l.  The slot holds logical chunk
+// slot ^ swzk(k).  The scalar base of a stage at K offset k0 moves by
+// 4*k0*ld bytes.
+template <int N, int KMROW>
 __device__ __forceinline__ TileOffsets<N> tile_offsets_km(int64_t ld, int64_t n0, int wave) {
-  static_assert(kKmRow == 512, "two K rows per 1 KB load");
+  static_assert(KMROW == 512 || KMROW == 1024, "one or two K rows per 1 KB load");
+  constexpr int kRowsPerLoad = 1024 / KMROW, kSlots = KMROW / 16;
   const int lane = threadIdx.x & 63;
   TileOffsets<N> t;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    const int k = 2 * (wave * N + i) + (lane >> 5);
-    t.v[i] = static_cast<uint32_t>((k * ld + n0) * 4 + (((lane & 31) ^ swzk(k)) << 4));
+    const int k = kRowsPerLoad * (wave * N + i) + lane / kSlots;
+    t.v[i] = static_cast<uint32_t>((k * ld + n0) * 4 + (((lane % kSlots) ^ swzk(k)) << 4));
   }
   return t;
 }
@@ -299,11 +320,11 @@ struct BFrags<kS8HiOnly> : BFrags<SMX_S8_COMP_BF16> {};
 // LDS -> registers: A row block i, and the four B column blocks, of one
 // stage.  Lane (r, h) takes K = 8h .. 8h+7 of its row: chunks h (hi) and
 // 2 + h (lo) of the interleaved form, chunks 2h and 2h + 1 of FP32.
-template <int MODE, int TM>
+template <int MODE, class G>
 __device__ __forceinline__ void load_a(const char *st, int wm, int i, AFrag<MODE> &f) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
-  const int r = wm * (32 * Geo<TM>::kSubM) + i * 32 + lr;
+  const int r = wm * (32 * G::kSubM) + i * 32 + lr;
   if constexpr (MODE != SMX_S8_FP32) {
     f.h = read_b16(st, r, lh);
     if constexpr (MODE == SMX_S8_COMP_BF16) f.l = read_b16(st, r, 2 + lh);
@@ -312,11 +333,11 @@ __device__ __forceinline__ void load_a(const char *st, int wm, int i, AFrag<MODE
   }
 }
 
-template <int MODE, int TM>
+template <int MODE, class G>
 __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) {
   const int lane = threadIdx.x & 63;
   const int lr = lane & 31, lh = lane >> 5;
-  const char *bt = st + Geo<TM>::kOpA;
+  const char *bt = st + G::kOpA;
 #pragma unroll
   for (int j = 0; j < kSubN; ++j) {
     const int r = wn * (32 * kSubN) + j * 32 + lr;
@@ -343,6 +364,7 @@ __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) 
 struct BkmLane {
   uint32_t o[2][2];
 };
+template <int KMROW>
 __device__ __forceinline__ BkmLane bkm_lane() {
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, s = lane & 15;
@@ -353,14 +375,14 @@ __device__ __forceinline__ BkmLane bkm_lane() {
   for (int jl = 0; jl < 2; ++jl)
 #pragma unroll
     for (int pl = 0; pl < 2; ++pl)
-      L.o[jl][pl] = static_cast<uint32_t>(k * kKmRow + 8 * (s & 1) +
+      L.o[jl][pl] = static_cast<uint32_t>(k * KMROW + 8 * (s & 1) +
                                           (((8 * jl + 4 * (g & 1) + 2 * pl + ((s >> 1) & 1)) ^ sw) << 4));
   return L;
 }
 
-template <int MODE, int TM>
+template <int MODE, class G>
 __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &f, const BkmLane &L) {
-  constexpr int kOpA = Geo<TM>::kOpA;
+  constexpr int kOpA = G::kOpA, kKmRow = G::kKmRow;
   const int lane = threadIdx.x & 63;
   const char *bt = st + kOpA;
   if constexpr (MODE != SMX_S8_FP32) {
@@ -401,10 +423,10 @@ __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &
   }
 }
 
-template <int MODE, int TM, bool BKM>
+template <int MODE, class G, bool BKM>
 __device__ __forceinline__ void load_b_any(const char *st, int wn, BFrags<MODE> &f, const BkmLane &L) {
-  if constexpr (BKM) load_b_km<MODE, TM>(st, wn, f, L);
-  else load_b<MODE, TM>(st, wn, f);
+  if constexpr (BKM) load_b_km<MODE, G>(st, wn, f, L);
+  else load_b<MODE, G>(st, wn, f);
 }
 
 // MFMAs of row block i: acc[i][j] += A_i B_j^T over the stage's 16 K.
@@ -464,14 +486,14 @@ __device__ __forceinline__ AFrag<MODE> one_hot(float s, int r0) {
 // wave's B chunks start kOpA bytes later, less the difference of the
 // wave's A and B shares.  BKM: B is K-major (its stage is 16 rows further
 // down).
-template <int TM>
+template <class G>
 struct WaveOffsets {
-  TileOffsets<Geo<TM>::kLoadsA> a;
-  TileOffsets<kLoadsB> b;
+  TileOffsets<G::kLoadsA> a;
+  TileOffsets<G::kLoadsB> b;
   uint32_t b_lds;  // LDS byte offset of the wave's B chunks from its A chunks
 };
-template <int TM, bool BKM>
-__device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const WaveOffsets<TM> &o, int64_t k0,
+template <class G, bool BKM>
+__device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const WaveOffsets<G> &o, int64_t k0,
                                             uint32_t lds) {
   dma_tile(o.a, static_cast<const char *>(A.p) + 4 * k0, lds);
   dma_tile(o.b, static_cast<const char *>(B.p) + 4 * k0 * (BKM ? B.ld : 1), lds + o.b_lds);
@@ -479,9 +501,9 @@ __device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const 
 
 // Waits until at most `pending` stages of this wave's loads are in flight
 // (loads complete in issue order).
-template <int TM>
+template <class G>
 __device__ __forceinline__ void wait_stages(int pending) {
-  constexpr int L = Geo<TM>::kLoadsPerStage;
+  constexpr int L = G::kLoadsPerStage;
   static_assert(kStages == 3, "at most two stages in flight");
   if (pending >= 2) wait_vm<2 * L>();
   else if (pending == 1) wait_vm<L>();
@@ -494,8 +516,8 @@ __device__ __forceinline__ void wait_stages(int pending) {
 // lgkmcnt waits before later MFMAs that stall on unrelated newer reads.
 __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// C[256 x 128] = A[arow0.., :K] * B[brow0.., :K]^T (BKM: A[arow0.., :K] *
-// B[:K, brow0..]).
+// C[TM x TN] = A[arow0.., :K] * B[brow0.., :K]^T (BKM: A[arow0.., :K] *
+// B[:K, brow0..]), geometry G.
 //
 // Two pipelines overlap the MFMAs:
 //  * a ring of kStages LDS slots filled by direct-to-LDS loads, kStages
@@ -512,25 +534,24 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 // (rows 16 SEL .. 16 SEL + 15 of the wave, accumulator block SEL / 2).
 // STEADY: kt + kStages < nk, so a next stage exists, the refill is due and
 // kStages - 2 stages may stay in flight (no run-time conditions).
-template <int MODE, int TM, int SEL, int PAR, bool STEADY, bool BKM>
-__device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const WaveOffsets<TM> &o, const BkmLane &bl,
+template <int MODE, class G, int SEL, int PAR, bool STEADY, bool BKM>
+__device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const WaveOffsets<G> &o, const BkmLane &bl,
                                           uint32_t lds0, float sel_s, char *smem, int kt, int nk, int wm, int wn,
-                                          AFrag<MODE> (&af)[Geo<TM>::kSubM], BFrags<MODE> (&bf)[2],
-                                          f32x16 (&acc)[Geo<TM>::kSubM][kSubN]) {
-  using G = Geo<TM>;
+                                          AFrag<MODE> (&af)[G::kSubM], BFrags<MODE> (&bf)[2],
+                                          f32x16 (&acc)[G::kSubM][kSubN]) {
   constexpr int S = kStages;
   const bool more = STEADY || kt + 1 < nk;
   if constexpr (STEADY) {
     wait_vm<(S - 2) * G::kLoadsPerStage>();
   } else {
-    if (more) wait_stages<TM>(min(S - 2, nk - 2 - kt));
+    if (more) wait_stages<G>(min(S - 2, nk - 2 - kt));
   }
   wait_lds();
   block_barrier();
   if (STEADY || kt + S < nk)
-    issue_stage<TM, BKM>(A, B, o, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * G::kStageBytes);
+    issue_stage<G, BKM>(A, B, o, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * G::kStageBytes);
   const char *nxt = smem + ((kt + 1) % S) * G::kStageBytes;
-  if (more) load_b_any<MODE, TM, BKM>(nxt, wn, bf[PAR ^ 1], bl);
+  if (more) load_b_any<MODE, G, BKM>(nxt, wn, bf[PAR ^ 1], bl);
   // Raised wave priority while this wave issues its MFMAs, so the
   // arbiter favours it over the other block's wave on the SIMD that is
   // issuing LDS reads and loads (Gram launches 5% faster).
@@ -538,7 +559,7 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Wa
 #pragma unroll
   for (int i = 0; i < G::kSubM; ++i) {
     mma_row<MODE>(af[i], bf[PAR], acc[i]);
-    if (more) load_a<MODE, TM>(nxt, wm, i, af[i]);
+    if (more) load_a<MODE, G>(nxt, wm, i, af[i]);
   }
   if constexpr (SEL >= 0) mma_row<MODE>(one_hot<MODE>(sel_s, (SEL & 1) * 16), bf[PAR], acc[SEL >> 1]);
   __builtin_amdgcn_s_setprio(0);
@@ -547,15 +568,14 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Wa
 // ACCG: also accumulate sel_s * G over the wave's rows (square phase; A and
 // B are the same symmetric G, K = rows of G).  BKM: B is a K-major
 // row-major operand (C = A B, apply), brow0 its first column.
-template <int MODE, int TM, bool ACCG, bool BKM>
+template <int MODE, class G, bool ACCG, bool BKM>
 __device__ __forceinline__ void gemm_tile(const Opnd &A, const Opnd &B, int64_t K, int64_t arow0, int64_t brow0,
-                                          float sel_s, char *smem, f32x16 (&acc)[Geo<TM>::kSubM][kSubN]) {
-  using G = Geo<TM>;
+                                          float sel_s, char *smem, f32x16 (&acc)[G::kSubM][kSubN]) {
   constexpr int kSubM = G::kSubM;
   static_assert((kSubM == 4 || kSubM == 2) && kBK == 16, "the one_hot window is 2 kSubM stages of 16 rows");
   static_assert((8 * kSubN) % 16 == 0, "the wave's K-major column offset must be whole chunk groups");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves, each 128 x 64
+  const int wm = wave / G::kWavesN, wn = wave % G::kWavesN;  // 2 x kWavesN waves
 #pragma unroll
   for (int i = 0; i < kSubM; ++i)
 #pragma unroll
@@ -563,25 +583,25 @@ __device__ __forceinline__ void gemm_tile(const Opnd &A, const Opnd &B, int64_t 
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
   const int nk = static_cast<int>(K / kBK);
-  WaveOffsets<TM> o;
+  WaveOffsets<G> o;
   o.a = tile_offsets<G::kLoadsA>(A.ld, arow0, wave);
-  o.b = BKM ? tile_offsets_km<kLoadsB>(B.ld, brow0, wave) : tile_offsets<kLoadsB>(B.ld, brow0, wave);
-  o.b_lds = static_cast<uint32_t>(G::kOpA + wave * (kLoadsB - G::kLoadsA) * 1024);
-  const BkmLane bl = bkm_lane();  // used by the K-major B path only
+  o.b = BKM ? tile_offsets_km<G::kLoadsB, G::kKmRow>(B.ld, brow0, wave) : tile_offsets<G::kLoadsB>(B.ld, brow0, wave);
+  o.b_lds = static_cast<uint32_t>(G::kOpA + wave * (G::kLoadsB - G::kLoadsA) * 1024);
+  const BkmLane bl = bkm_lane<G::kKmRow>();  // used by the K-major B path only
   // LDS byte address of the ring plus this wave's first A chunk.
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * G::kLoadsA * 1024;
 #pragma unroll
   for (int s = 0; s < kStages; ++s)
-    if (s < nk) issue_stage<TM, BKM>(A, B, o, static_cast<int64_t>(s) * kBK, lds0 + s * G::kStageBytes);
-  wait_stages<TM>(min(kStages - 1, nk - 1));
+    if (s < nk) issue_stage<G, BKM>(A, B, o, static_cast<int64_t>(s) * kBK, lds0 + s * G::kStageBytes);
+  wait_stages<G>(min(kStages - 1, nk - 1));
   block_barrier();
   AFrag<MODE> af[kSubM];
   BFrags<MODE> bf[2];
-  load_b_any<MODE, TM, BKM>(smem, wn, bf[0], bl);
+  load_b_any<MODE, G, BKM>(smem, wn, bf[0], bl);
 #pragma unroll
-  for (int i = 0; i < kSubM; ++i) load_a<MODE, TM>(smem, wm, i, af[i]);
+  for (int i = 0; i < kSubM; ++i) load_a<MODE, G>(smem, wm, i, af[i]);
 #define SMX_PIPE(SEL, PAR, KT, STEADY) \
-  pipe_iter<MODE, TM, SEL, PAR, STEADY, BKM>(A, B, o, bl, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
+  pipe_iter<MODE, G, SEL, PAR, STEADY, BKM>(A, B, o, bl, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
   // Stages [kt, to) in pairs (kt and `to` even): branch-free while a refill
   // is due, then the general form.
   const int steady_end = nk - kStages;
@@ -642,14 +662,17 @@ struct Stage1Scalars {
   float s;
   bool ok;
 };
-__host__ __device__ inline int64_t square_tiles(const S8Class &k, bool small) {
-  return small ? sym_tiles(k.tiles_s) : 2 * sym_tiles(k.tiles_m);
+// Tiles of a symmetric r x r result (Gram, square, SYM) in a geometry: the
+// upper-triangle 256 x 256 blocks (kGeoL), each as two 128-column halves
+// (kGeoM), or the upper-triangle 128 x 128 tiles (kGeoS).
+__host__ __device__ inline int64_t square_tiles(const S8Class &k, int geo) {
+  return geo == kGeoS ? sym_tiles(k.tiles_s) : geo == kGeoL ? sym_tiles(k.tiles_m) : 2 * sym_tiles(k.tiles_m);
 }
 
-__device__ Stage1Scalars stage1_scalars(const S8Mat &M, bool sq_small, double *bcast) {
+__device__ Stage1Scalars stage1_scalars(const S8Mat &M, int sq_geo, double *bcast) {
   Stage1Scalars r;
   r.fro2 = M.cst()[kCstFro];
-  const double sq = sum_parts(M.sch(), static_cast<int>(square_tiles(*M.kp(), sq_small)), bcast);
+  const double sq = sum_parts(M.sch(), static_cast<int>(square_tiles(*M.kp(), sq_geo)), bcast);
   r.ok = r.fro2 > 0.0 && sq > 0.0;
   r.s = r.ok ? fmaxf(static_cast<float>(kS8Margin * pow(sq, 0.125)), 1e-30f) : 1.f;
   return r;
@@ -679,9 +702,13 @@ __device__ __forceinline__ TileRef tile_of(const StageArgs &args) {
 // padded to 36 floats (16-byte aligned row vectors).
 constexpr int kEpStride = 36;
 constexpr int kEpBlock = 32 * kEpStride;
-static_assert(kWaves * 2 * kEpBlock * 4 <= Geo<kSymTile>::kRingBytes, "epilogue staging must fit in the operand ring");
-static_assert((kWaves * 2 * kEpBlock + 2 * kTile) * 4 <= Geo<kTile>::kRingBytes,
-              "apply epilogue staging and the row-sum column vectors must fit in the operand ring");
+template <class G>
+constexpr bool epilogue_fits() {
+  // per wave two staging blocks; the apply adds the tile's a and z vectors
+  return (G::kWaves * 2 * kEpBlock + 2 * (G::kTileM > G::kTileN ? G::kTileM : G::kTileN)) * 4 <= G::kRingBytes;
+}
+static_assert(epilogue_fits<GeoM>() && epilogue_fits<GeoS>() && epilogue_fits<GeoL>(),
+              "epilogue staging and the row-sum column vectors must fit in the operand ring");
 
 __device__ __forceinline__ void ep_read8(const float *s, int row, int col, float (&w)[8]) {
   const f32x4 a = *reinterpret_cast<const f32x4 *>(s + row * kEpStride + col);
@@ -691,25 +718,26 @@ __device__ __forceinline__ void ep_read8(const float *s, int row, int col, float
 }
 
 // ------------------------------------------------------------ kernel ---
-// Output tiles are TM x 128: tm counts TM-row blocks, tn 128-column blocks.
-// The Gram and the square compute the upper triangle of their symmetric
-// result: with 256 x 128 tiles as the upper-triangle 256 x 256 blocks,
-// each as two 128-column halves (tix = 2 * block index + half); with
-// 128 x 128 tiles as the upper-triangle tiles (tn >= tm, row by row).  A
-// diagonal block or tile is computed whole; an off-diagonal one also
-// writes its mirror.
-// `small`: the launch's tiles are 128 x 128 (square and SYM launches).
-__host__ __device__ inline int64_t phase_tiles(const S8Class &k, int phase, bool small, int op = -1) {
-  if (phase == kApply) return static_cast<int64_t>(k.tiles_m) * ((op == kOpApplyQ ? k.rp : k.cp) / kTileN);
-  return phase == kSquare || phase == kSym ? square_tiles(k, small) : 2 * sym_tiles(k.tiles_m);
+// Output tiles are TM x TN: tm counts TM-row blocks, tn TN-column blocks.
+// The Gram, the square and the SYM products compute the upper triangle of
+// their symmetric result (square_tiles): 256 x 256 tiles are its
+// upper-triangle blocks (tn >= tm, row by row); 256 x 128 tiles the
+// halves of those blocks (tix = 2 * block index + half); 128 x 128 tiles
+// its upper-triangle 128 x 128 tiles.  A diagonal block or tile is
+// computed whole; an off-diagonal one also writes its mirror.
+__host__ __device__ inline int64_t phase_tiles(const S8Class &k, int phase, int geo, int op = -1) {
+  if (phase == kApply)
+    return static_cast<int64_t>(k.tiles_m) * ((op == kOpApplyQ ? k.rp : k.cp) / (geo == kGeoL ? 256 : 128));
+  return square_tiles(k, geo);
 }
 
-template <int MODE, int PHASE, int TM>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(Geo<TM>::kWavesPerEU, Geo<TM>::kWavesPerEU)))
+template <int MODE, int PHASE, int TM, int TN>
+__global__ void __launch_bounds__((Geo<TM, TN>::kThreads))
+__attribute__((amdgpu_waves_per_eu(Geo<TM, TN>::kWavesPerEU, Geo<TM, TN>::kWavesPerEU)))
 s8_stage_kernel(StageArgs args) {
-  static_assert(TM == kTile || PHASE == kSquare || PHASE == kSym, "128 x 128 tiles for the square and SYM only");
-  using Gm = Geo<TM>;
-  constexpr int kSubM = Gm::kSubM;
+  using Gm = Geo<TM, TN>;
+  static_assert(Gm::kGeo != kGeoS || PHASE == kSquare || PHASE == kSym, "128 x 128 tiles for the square and SYM only");
+  constexpr int kSubM = Gm::kSubM, kTileN = Gm::kTileN, kThreads = Gm::kThreads, kWaves = Gm::kWaves;
   __shared__ __attribute__((aligned(16))) char smem[Gm::kRingBytes];
   __shared__ double dscratch[16];
   __shared__ double bcast;
@@ -717,12 +745,12 @@ s8_stage_kernel(StageArgs args) {
 
   const TileRef ref = tile_of(args);
   const S8Class &K = *ref.k;
-  const int64_t tpm = phase_tiles(K, PHASE, TM == kSymTile, ref.op);
+  const int64_t tpm = phase_tiles(K, PHASE, Gm::kGeo, ref.op);
   if (ref.L >= tpm * ref.cnt) return;
   const int slot = ref.slot0 + static_cast<int>(ref.L / tpm);
   const int64_t tix = ref.L % tpm;
   int64_t tm, tn;
-  bool diag = false;  // Gram / square: a half of a diagonal 256 x 256 block
+  bool diag = false;  // symmetric result: a diagonal block or tile (or a half of one)
   if constexpr (PHASE == kApply) {
     // Column-major over the output: consecutive tiles (one XCD's L2) share
     // a column block of X and cycle through P's row blocks, so each X block
@@ -730,7 +758,7 @@ s8_stage_kernel(StageArgs args) {
     // row-major; the launch time is the same).
     tn = tix / K.tiles_m;
     tm = tix % K.tiles_m;
-  } else if constexpr (TM == kTile) {
+  } else if constexpr (Gm::kGeo == kGeoM) {
     int64_t rem = tix >> 1;
     tm = 0;
     while (rem >= K.tiles_m - tm) { rem -= K.tiles_m - tm; ++tm; }
@@ -738,9 +766,10 @@ s8_stage_kernel(StageArgs args) {
     tn = 2 * tb + (tix & 1);
     diag = tb == tm;
   } else {
+    const int64_t nt = Gm::kGeo == kGeoL ? K.tiles_m : K.tiles_s;  // tiles per row and column
     int64_t rem = tix;
     tm = 0;
-    while (rem >= K.tiles_s - tm) { rem -= K.tiles_s - tm; ++tm; }
+    while (rem >= nt - tm) { rem -= nt - tm; ++tm; }
     tn = tm + rem;
     diag = tn == tm;
   }
@@ -790,11 +819,11 @@ s8_stage_kernel(StageArgs args) {
       A = M.t(); B = pk; sym_out = M.g();
       if (stage == 1) {
         // G1 = P1 G0 P1 / s^2
-        const Stage1Scalars sc = stage1_scalars(M, args.sq_small != 0, &bcast);
+        const Stage1Scalars sc = stage1_scalars(M, args.sq_geo, &bcast);
         scale = sc.ok ? 1.0f / (sc.s * sc.s) : 0.f;
       }
     }
-    gemm_tile<MODE, TM, false, false>(Opnd{A, K.rp}, Opnd{B, K.rp}, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem,
+    gemm_tile<MODE, Gm, false, false>(Opnd{A, K.rp}, Opnd{B, K.rp}, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem,
                                       acc);
   } else if constexpr (PHASE == kGram) {
     if (stage == 1) {
@@ -803,15 +832,15 @@ s8_stage_kernel(StageArgs args) {
     }
     // A Gram-space class takes its stage-3 Gram of X2 from x1.
     const Opnd X{K.gs && stage == 3 ? M.x1() : x_in, K.cp};
-    gemm_tile<MODE, TM, false, false>(X, X, K.cp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
+    gemm_tile<MODE, Gm, false, false>(X, X, K.cp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
   } else if constexpr (PHASE == kSquare) {
     const Opnd G{M.g(), K.rp};
     if (stage == 1) {
-      gemm_tile<MODE, TM, false, false>(G, G, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
+      gemm_tile<MODE, Gm, false, false>(G, G, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
     } else {
       // acc = G G + (b/c) G; the epilogue forms P = c acc + a I.
       scale = args.c;
-      gemm_tile<MODE, TM, true, false>(G, G, K.rp, tm * Gm::kTileM, tn * kTileN, args.b_over_c, smem, acc);
+      gemm_tile<MODE, Gm, true, false>(G, G, K.rp, tm * Gm::kTileM, tn * kTileN, args.b_over_c, smem, acc);
     }
   } else {
     // X-space: X' = P X (stage 1: X' = P1 V / (||V|| s)).  Gram space:
@@ -819,13 +848,13 @@ s8_stage_kernel(StageArgs args) {
     const int op = ref.op;
     const bool gq = op == kOpApplyQ, mid = op == kOpApplyMid, fin = op == kOpApplyFinal;
     if (stage == 1 || mid) {
-      const Stage1Scalars sc = stage1_scalars(M, args.sq_small != 0, &bcast);
+      const Stage1Scalars sc = stage1_scalars(M, args.sq_geo, &bcast);
       scale = sc.ok ? static_cast<float>(1.0 / (sqrt(sc.fro2) * static_cast<double>(sc.s))) : 0.f;
     }
     const float *A = mid ? M.qb() : fin ? M.qa() : M.p();
     const Opnd B = gq ? Opnd{q_in, K.rp} : Opnd{mid ? M.x0() : fin ? M.x1() : x_in, K.cp};
     // B = X (or Q) rows k (K-major), columns of the tile.
-    gemm_tile<MODE, TM, false, true>(Opnd{A, K.rp}, B, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
+    gemm_tile<MODE, Gm, false, true>(Opnd{A, K.rp}, B, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
   }
 
   // ------------------------------------------------------- epilogue ---
@@ -836,7 +865,7 @@ s8_stage_kernel(StageArgs args) {
   //   SQUARE  stage 1: G2 (FP32) -> p; stage k: P = c acc + a I -> p
   //   APPLY   tile -> X' (stage 5, transposed parameter: transpose -> xf)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / Gm::kWavesN, wn = wave % Gm::kWavesN;
   const int lr = lane & 31, lh = lane >> 5;
   const int rr = lane >> 2, cc = (lane & 3) * 8;  // read-back: rows rr, rr + 16; cols cc..cc+7
   const int64_t R0 = tm * Gm::kTileM + wm * (32 * kSubM), C0 = tn * kTileN + wn * (32 * kSubN);
@@ -1038,7 +1067,7 @@ __global__ void __launch_bounds__(256) s8_poly1_kernel(StageArgs args) {
       g4[k][e] = reinterpret_cast<const uint4 *>(G + idx[k])[e];
     }
   }
-  const Stage1Scalars sc = stage1_scalars(M, args.sq_small != 0, &bcast);
+  const Stage1Scalars sc = stage1_scalars(M, args.sq_geo, &bcast);
   const float s2 = sc.s * sc.s;
   const float is2 = sc.ok ? 1.0f / s2 : 0.f, is4 = sc.ok ? 1.0f / (s2 * s2) : 0.f;
 #pragma unroll
@@ -1179,73 +1208,88 @@ static std::vector<Seg> launch_segments(const S8Layout &Lay, const SlotSet &set,
   return segs;
 }
 
-// MFMA FLOPs of one launch: computed tiles x 2 * TM * 128 * K (x3 for a
+// MFMA FLOPs of one launch: computed tiles x 2 * TM * TN * K (x3 for a
 // compensated stage), plus the square phase's one-hot MFMAs (2 kSubM stages
 // of kSubN 32x32x16 products per wave).
-static double launch_flops(const S8Layout &Lay, int phase, int stage, bool small, const std::vector<Seg> &segs) {
+static double launch_flops(const S8Layout &Lay, int phase, int stage, int geo, const std::vector<Seg> &segs) {
   if (phase == kPoly1) return 0.0;
   const double prod = stage_mode(Lay, stage) == SMX_S8_COMP_BF16 ? 3.0 : 1.0;
-  const int tm = (phase == kSquare || phase == kSym) && small ? kSymTile : kTile;
+  const int tm = geo == kGeoS ? 128 : 256, tn = geo == kGeoL ? 256 : 128, waves = geo == kGeoL ? 8 : 4;
   const int sub_m = tm / 64;
   double f = 0.0;
   for (const Seg &sg : segs) {
     const S8Class &k = Lay.cls[sg.cls];
-    const double tiles = static_cast<double>(phase_tiles(k, phase, small, sg.op));
+    const double tiles = static_cast<double>(phase_tiles(k, phase, geo, sg.op));
     const double K = phase == kGram ? static_cast<double>(k.cp) : static_cast<double>(k.rp);
     const double cnt = sg.hi - sg.lo;
-    f += cnt * tiles * 2.0 * tm * kTileN * K * prod;
+    f += cnt * tiles * 2.0 * tm * tn * K * prod;
     // one-hot: per wave 2 kSubM stages of kSubN MFMA tiles
     if (phase == kSquare && stage != 1)
-      f += cnt * tiles * kWaves * (2.0 * sub_m) * kSubN * 2.0 * 32 * 32 * kBK * prod;
+      f += cnt * tiles * waves * (2.0 * sub_m) * kSubN * 2.0 * 32 * 32 * kBK * prod;
   }
   return f;
 }
 
-// Whether a symmetric-output launch (square, SYM) over use(i) matrices of
-// each class i takes 128 x 128 tiles: rounds of the device's block slots
-// (two 256 x 128 or three 128 x 128 blocks per CU), a round of the smaller
-// tile counted as 0.9 of one of the larger.
-template <typename Use>
-static bool small_tiles(const S8Layout &Lay, Use use) {
+static int64_t device_cus() {
   static int cus[64] = {};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
   if (cus[dev] == 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return false;
-  int64_t big = 0, small = 0;
-  for (int i = 0; i < Lay.n_classes; ++i) {
-    const int64_t cnt = use(i);  // matrices of class i in the launches
-    big += cnt * square_tiles(Lay.cls[i], false);
-    small += cnt * square_tiles(Lay.cls[i], true);
-  }
-  const double r_big = static_cast<double>(ceil_div(big, 2 * static_cast<int64_t>(cus[dev])));
-  const double r_small = static_cast<double>(ceil_div(small, 3 * static_cast<int64_t>(cus[dev])));
-  return 0.9 * r_small < r_big;
+    return 256;
+  return cus[dev];
 }
 
-// One phase launch of a stage kernel (a square or SYM launch on 128 x 128
-// tiles when `small`).
+// The tile geometry of one launch over `segs`.  256 x 256 tiles when the
+// launch has at least 0.9 of one per CU: those blocks move a third fewer
+// operand bytes per MFMA (cfg5 S8 7% faster, the cfg4 applies 16%
+// faster).  With fewer, each CU has at most one block of a launch and
+// nothing of it to overlap a block's prologue and epilogue with (cfg4
+// Gram, square and SYM launches 15-60% slower).  Otherwise, for the square
+// and the SYM products (`small_ok`), 128 x 128 tiles when they take fewer
+// rounds of the CUs' block slots (three per CU, a round counted 0.9 of one
+// of two 256 x 128 blocks per CU), else 256 x 128.
+static int pick_geo(const S8Layout &Lay, int phase, const std::vector<Seg> &segs, bool small_ok) {
+  if (g_tile_policy == 1) return kGeoL;
+  const int64_t cus = device_cus();
+  int64_t tiles[3] = {0, 0, 0};
+  for (const Seg &sg : segs) {
+    const S8Class &k = Lay.cls[sg.cls];
+    const int64_t cnt = sg.hi - sg.lo;
+    for (int g = 0; g < 3; ++g) tiles[g] += cnt * phase_tiles(k, phase, g, sg.op);
+  }
+  if (g_tile_policy == 0 && 10 * tiles[kGeoL] >= 9 * cus) return kGeoL;
+  if (small_ok) {
+    const double r_m = static_cast<double>(ceil_div(tiles[kGeoM], 2 * cus));
+    const double r_s = static_cast<double>(ceil_div(tiles[kGeoS], 3 * cus));
+    if (0.9 * r_s < r_m) return kGeoS;
+  }
+  return kGeoM;
+}
+
+// One phase launch of a stage kernel in geometry `geo`.
 template <int MODE, int PHASE>
-static void launch_stage(bool small, int32_t blocks, const StageArgs &a, hipStream_t st) {
+static void launch_stage(int geo, int32_t blocks, const StageArgs &a, hipStream_t st) {
   if constexpr (PHASE == kSquare || PHASE == kSym) {
-    if (small) {
-      hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, kSymTile>), dim3(blocks), dim3(kThreads), 0, st, a);
+    if (geo == kGeoS) {
+      hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, 128, 128>), dim3(blocks), dim3(GeoS::kThreads), 0, st, a);
       return;
     }
   }
-  hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, kTile>), dim3(blocks), dim3(kThreads), 0, st, a);
+  if (geo == kGeoL)
+    hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, 256, 256>), dim3(blocks), dim3(GeoL::kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, 256, 128>), dim3(blocks), dim3(GeoM::kThreads), 0, st, a);
 }
 
-// sq_small: the run's square takes 128 x 128 tiles (the stage-1 Schatten
-// partials are per square tile); sym_small: its SYM launches do.
+// sq_geo: the geometry of the run's square launches (the stage-1 Schatten
+// partials are per square tile).
 template <int PHASE>
-static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, bool sq_small, bool sym_small, hipStream_t st,
-                        double &flops, const std::vector<int> &ops = {}) {
-  const bool small = PHASE == kSquare ? sq_small : PHASE == kSym ? sym_small : false;
+static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, int sq_geo, hipStream_t st, double &flops,
+                        const std::vector<int> &ops = {}) {
   StageArgs a{};
   a.L = Lay;
   a.stage = stage;
-  a.sq_small = sq_small ? 1 : 0;
+  a.sq_geo = sq_geo;
   const auto &co = kS8Coefficients[stage - 1];
   a.a = static_cast<float>(co[0]);
   a.b = static_cast<float>(co[1]);
@@ -1253,11 +1297,12 @@ static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, bool
   a.b_over_c = static_cast<float>(co[1] / co[2]);
   const std::vector<Seg> segs = launch_segments(Lay, set, PHASE, stage, ops);
   if (static_cast<int>(segs.size()) > kMaxSeg) return fail(SMX_EINVAL, "s8: too many launch segments");
+  const int geo = PHASE == kSquare ? sq_geo : PHASE == kPoly1 ? kGeoM : pick_geo(Lay, PHASE, segs, PHASE == kSym);
   int32_t off = 0;
   a.n_seg = 0;
   for (const Seg &sg : segs) {
     const S8Class &k = Lay.cls[sg.cls];
-    const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE, small, sg.op);
+    const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE, geo, sg.op);
     const int64_t nt = round_up(tpm * (sg.hi - sg.lo), 8);
     a.seg_off[a.n_seg] = off;
     a.seg_cls[a.n_seg] = sg.cls;
@@ -1280,14 +1325,14 @@ static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, bool
       hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_FP32>, dim3(off), dim3(256), 0, st, a);
     rc = check_launch("s8 stage-1 polynomial");
   } else {
-    if (mode == SMX_S8_COMP_BF16) launch_stage<SMX_S8_COMP_BF16, PHASE>(small, off, a, st);
-    else if (mode == kS8HiOnly) launch_stage<kS8HiOnly, PHASE>(small, off, a, st);
-    else launch_stage<SMX_S8_FP32, PHASE>(small, off, a, st);
+    if (mode == SMX_S8_COMP_BF16) launch_stage<SMX_S8_COMP_BF16, PHASE>(geo, off, a, st);
+    else if (mode == kS8HiOnly) launch_stage<kS8HiOnly, PHASE>(geo, off, a, st);
+    else launch_stage<SMX_S8_FP32, PHASE>(geo, off, a, st);
     rc = check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : PHASE == kSym ? "s8 sym"
                                                                                                 : "s8 apply");
   }
   if (rc) return rc;
-  const double f = launch_flops(Lay, PHASE, stage, small, segs);
+  const double f = launch_flops(Lay, PHASE, stage, geo, segs);
   flops += f;
   return timing_end(slot, st, PHASE, f);
 }
@@ -1298,32 +1343,34 @@ static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, bool
 // 2 (X2) and 5 (X5).
 static int run_s8_set_stage(const S8Layout &Lay, const SlotSet &set, int stage, hipStream_t st, double &flops) {
   auto cnt = [&](int i) { return static_cast<int64_t>(set.hi[i] - set.lo[i]); };
-  const bool sq_small = small_tiles(Lay, [&](int i) { return cnt(i); });
-  const bool sym_small = small_tiles(Lay, [&](int i) { return Lay.cls[i].gs ? cnt(i) : int64_t{0}; });
+  // The square covers every matrix of the set at every stage, so its
+  // geometry (and the stage-1 Schatten partials) is the same for the run.
+  const int sq_geo = pick_geo(Lay, kSquare, launch_segments(Lay, set, kSquare, stage, {}), true);
   bool any_gs = false;
   for (int i = 0; i < Lay.n_classes; ++i) any_gs = any_gs || (Lay.cls[i].gs && cnt(i) > 0);
   int rc = SMX_OK;
   {
-    rc = launch_phase<kGram>(Lay, set, stage, sq_small, sym_small, st, flops);
-    if (!rc) rc = launch_phase<kSquare>(Lay, set, stage, sq_small, sym_small, st, flops);
-    if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, set, stage, sq_small, sym_small, st, flops);
+    rc = launch_phase<kGram>(Lay, set, stage, sq_geo, st, flops);
+    if (!rc) rc = launch_phase<kSquare>(Lay, set, stage, sq_geo, st, flops);
+    if (!rc && stage == 1) rc = launch_phase<kPoly1>(Lay, set, stage, sq_geo, st, flops);
     if (!rc && any_gs && gs_sym(stage)) {
-      rc = launch_phase<kSym>(Lay, set, stage, sq_small, sym_small, st, flops, {kOpPG});
-      if (!rc) rc = launch_phase<kSym>(Lay, set, stage, sq_small, sym_small, st, flops, {kOpTP});
+      rc = launch_phase<kSym>(Lay, set, stage, sq_geo, st, flops, {kOpPG});
+      if (!rc) rc = launch_phase<kSym>(Lay, set, stage, sq_geo, st, flops, {kOpTP});
     }
-    if (!rc) rc = launch_phase<kApply>(Lay, set, stage, sq_small, sym_small, st, flops, {kOpApplyX, kOpApplyQ});
+    if (!rc) rc = launch_phase<kApply>(Lay, set, stage, sq_geo, st, flops, {kOpApplyX, kOpApplyQ});
     if (!rc && any_gs && (stage == 2 || stage == 5))
-      rc = launch_phase<kApply>(Lay, set, stage, sq_small, sym_small, st, flops,
-                                {stage == 2 ? kOpApplyMid : kOpApplyFinal});
+      rc = launch_phase<kApply>(Lay, set, stage, sq_geo, st, flops, {stage == 2 ? kOpApplyMid : kOpApplyFinal});
   }
   return rc;
 }
 
-// A second stream of the device (default priority) and the two events of a
-// fork and join, created once per device.
+// The launch chains of an S8 run beyond the first (which runs on the
+// caller's stream): further streams of the device (default priority), each
+// with the events of its fork and join, created once per device.
+constexpr int kChains = 2;
 struct ForkStream {
-  hipStream_t aux = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
+  hipStream_t aux[kChains - 1] = {};
+  hipEvent_t fork = nullptr, join[kChains - 1] = {};
 };
 static std::mutex g_fork_lock;
 static ForkStream g_fork[64];
@@ -1333,26 +1380,31 @@ static int fork_stream(ForkStream *&out) {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(SMX_ELAUNCH, "s8: no current HIP device");
   std::lock_guard<std::mutex> lock(g_fork_lock);
   ForkStream &f = g_fork[dev];
-  if (!f.aux) {
-    if (hipStreamCreateWithFlags(&f.aux, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&f.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&f.join, hipEventDisableTiming) != hipSuccess)
-      return fail(SMX_ELAUNCH, "s8: cannot create the second stream and its events");
+  if (!f.fork) {
+    bool ok = hipEventCreateWithFlags(&f.fork, hipEventDisableTiming) == hipSuccess;
+    for (int i = 0; ok && i < kChains - 1; ++i)
+      ok = hipStreamCreateWithFlags(&f.aux[i], hipStreamNonBlocking) == hipSuccess &&
+           hipEventCreateWithFlags(&f.join[i], hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+      f.fork = nullptr;
+      return fail(SMX_ELAUNCH, "s8: cannot create the launch chains' streams and events");
+    }
   }
   out = &f;
   return SMX_OK;
 }
 
 // The whole S8 run.  The matrices are independent until the run ends, so
-// they go to two launch chains: a class of at least kSplitCount matrices is
-// split in halves, one to each chain, and a smaller class whole to the
-// chain with less work so far (r^2 c per matrix, largest classes first).
-// One chain runs on the caller's stream, the other on a second stream
-// forked from it and joined back before the run ends: the blocks of one
-// chain's launches fill the CUs that the other's leave idle (a launch's
-// tail, tiles that take longer than the rest).  The launch recorder gets
-// one record for the run, on the caller's stream.
-constexpr int kSplitCount = 4;
+// they go to kChains launch chains: a class of at least kSplitCount
+// matrices is split into kChains near-equal parts, one to each chain, and a
+// smaller class whole to the chain with the least work so far (r^2 c per
+// matrix, largest classes first).  The first chain runs on the caller's
+// stream, the others on further streams forked from it and joined back
+// before the run ends: the blocks of one chain's launches fill the CUs
+// that the others' leave idle (a launch's tail, tiles that take longer than
+// the rest).  The launch recorder gets one record for the run, on the
+// caller's stream.
+constexpr int kSplitCount = 2 * kChains;
 
 int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
   int slot = -1;
@@ -1367,41 +1419,52 @@ int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
   };
   std::stable_sort(order.begin(), order.end(),
                    [&](int x, int y) { return work(x, Lay.cls[x].count) > work(y, Lay.cls[y].count); });
-  SlotSet set[2];
-  double load[2] = {0.0, 0.0};
+  SlotSet set[kChains];
+  double load[kChains] = {};
   for (int i : order) {
     const int c = Lay.cls[i].count;
     if (c >= kSplitCount) {
-      set[0].lo[i] = 0;
-      set[0].hi[i] = set[1].lo[i] = c - c / 2;
-      set[1].hi[i] = c;
-      load[0] += work(i, c - c / 2);
-      load[1] += work(i, c / 2);
+      int lo = 0;
+      for (int t = 0; t < kChains; ++t) {
+        const int n = c / kChains + (t < c % kChains ? 1 : 0);
+        set[t].lo[i] = lo;
+        set[t].hi[i] = lo + n;
+        load[t] += work(i, n);
+        lo += n;
+      }
     } else {
-      const int t = load[0] <= load[1] ? 0 : 1;
+      int t = 0;
+      for (int u = 1; u < kChains; ++u)
+        if (load[u] < load[t]) t = u;
       set[t].lo[i] = 0;
       set[t].hi[i] = c;
       load[t] += work(i, c);
     }
   }
+  int chains = 0;  // chains with work (the first always has some)
+  for (int t = 0; t < kChains; ++t)
+    if (!set[t].empty()) chains = t + 1;
   double flops = 0.0;
-  if (set[1].empty()) {
+  if (chains <= 1) {
     for (int stage = 1; stage <= 5 && !rc; ++stage) rc = run_s8_set_stage(Lay, set[0], stage, st, flops);
   } else {
     ForkStream *f = nullptr;
     rc = fork_stream(f);
-    if (!rc && (hipEventRecord(f->fork, st) != hipSuccess || hipStreamWaitEvent(f->aux, f->fork, 0) != hipSuccess))
-      rc = fail(SMX_ELAUNCH, "s8: fork to the second stream failed");
-    // The two chains are enqueued a stage at a time each, so that the
-    // second starts while the host is still enqueuing the first.
-    for (int stage = 1; stage <= 5 && !rc; ++stage) {
-      rc = run_s8_set_stage(Lay, set[1], stage, f->aux, flops);
-      if (!rc) rc = run_s8_set_stage(Lay, set[0], stage, st, flops);
-    }
+    if (!rc && hipEventRecord(f->fork, st) != hipSuccess) rc = fail(SMX_ELAUNCH, "s8: fork of the launch chains failed");
+    for (int t = 1; t < chains && !rc; ++t)
+      if (hipStreamWaitEvent(f->aux[t - 1], f->fork, 0) != hipSuccess)
+        rc = fail(SMX_ELAUNCH, "s8: fork of the launch chains failed");
+    // The chains are enqueued a stage at a time each, so that every chain
+    // starts while the host is still enqueuing the others.
+    for (int stage = 1; stage <= 5 && !rc; ++stage)
+      for (int t = chains - 1; t >= 0 && !rc; --t)
+        if (!set[t].empty()) rc = run_s8_set_stage(Lay, set[t], stage, t ? f->aux[t - 1] : st, flops);
     // Join even after a failed launch, so the caller's stream never runs
-    // ahead of work already on the second stream.
-    if (f && (hipEventRecord(f->join, f->aux) != hipSuccess || hipStreamWaitEvent(st, f->join, 0) != hipSuccess) && !rc)
-      rc = fail(SMX_ELAUNCH, "s8: join of the second stream failed");
+    // ahead of work already on the other streams.
+    for (int t = 1; f && t < chains; ++t)
+      if ((hipEventRecord(f->join[t - 1], f->aux[t - 1]) != hipSuccess ||
+           hipStreamWaitEvent(st, f->join[t - 1], 0) != hipSuccess) && !rc)
+        rc = fail(SMX_ELAUNCH, "s8: join of the launch chains failed");
   }
   if (rc) return rc;
   return timing_end(slot, st, kSpan, flops);
@@ -1484,6 +1547,13 @@ extern "C" int smx_s8_comp_stages(int32_t k) {
   SMX_REQUIRE(k >= 0 && k <= 5, SMX_EINVAL, "s8 compensated stages: k must be in [0, 5]");
   const int prev = smx::g_comp_stages;
   smx::g_comp_stages = k;
+  return prev;
+}
+
+extern "C" int smx_s8_tile_geometry(int32_t policy) {
+  SMX_REQUIRE(policy >= 0 && policy <= 2, SMX_EINVAL, "s8 tile geometry: policy must be 0, 1 or 2");
+  const int prev = smx::g_tile_policy;
+  smx::g_tile_policy = policy;
   return prev;
 }
 

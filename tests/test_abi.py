@@ -144,6 +144,16 @@ def test_compensated_stage_count_setting():
     assert lib.smx_s8_comp_stages(5) == 5
 
 
+def test_tile_geometry_setting():
+    lib = _native.lib()
+    assert lib.smx_s8_tile_geometry(3) == -1 and lib.smx_s8_tile_geometry(-1) == -1
+    assert lib.smx_s8_tile_geometry(1) == 0   # the automatic default is unchanged by the rejected calls
+    assert _native.s8_tile_geometry(2) == 1
+    with pytest.raises(ValueError):
+        _native.s8_tile_geometry(4)
+    assert lib.smx_s8_tile_geometry(0) == 2
+
+
 def test_stats_slot_rows():
     # Row chunks hold at least 512 rows and at most n_slots chunks are used.
     lib = _native.lib()

@@ -117,7 +117,7 @@ class Chain(nn.Module):
 
 
 @pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
-def test_odd_shapes_through_the_optimizer(device, mode):
+def test_odd_shapes_through_the_optimizer(device, tile_policy, mode):
     torch.manual_seed(41)
     model = Chain()
     g = torch.Generator().manual_seed(42)
@@ -126,7 +126,7 @@ def test_odd_shapes_through_the_optimizer(device, mode):
     hist, opt, ora = run_pair(device, model, batches, loss, RankOneAWeightedPE, mode, 1e-2, steps=2)
     assert len(opt.named_matrices) == 5
     worst = check_directions(hist, opt, 1e-2, mode)
-    print(f"odd shapes {mode}: worst direction rel err {worst:.3e}")
+    print(f"odd shapes {mode} tiles {tile_policy}: worst direction rel err {worst:.3e}")
     check_aux(hist, opt, ora)
 
 
@@ -154,7 +154,7 @@ class WideBranches(nn.Module):
 
 
 @pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
-def test_wide_rows_through_the_optimizer(device, mode):
+def test_wide_rows_through_the_optimizer(device, tile_policy, mode):
     torch.manual_seed(43)
     model = WideBranches()
     g = torch.Generator().manual_seed(44)
@@ -165,5 +165,5 @@ def test_wide_rows_through_the_optimizer(device, mode):
     hist, opt, ora = run_pair(device, model, batches, loss, RankOneAWeightedPE, mode, 1e-2, steps=2)
     assert len(opt.named_matrices) == 5
     worst = check_directions(hist, opt, 1e-2, mode)
-    print(f"wide rows {mode}: worst direction rel err {worst:.3e}")
+    print(f"wide rows {mode} tiles {tile_policy}: worst direction rel err {worst:.3e}")
     check_aux(hist, opt, ora)

@@ -149,6 +149,47 @@ def test_s8_timing_runs_only_records_one_span_per_run(device):
 
 
 @pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("shape", [(2, 7, 3), (3, 64, 96), (2, 300, 200), (1, 257, 513), (4, 512, 512), (3, 300, 520),
+                                   (1, 520, 300), (2, 768, 3072)])
+def test_s8_256x256_tiles(device, mode, shape):
+    """Every GEMM launch on 256 x 256 tiles of 8 waves (forced): X-space and
+    Gram-space classes, transposed inputs, a batch split over two launch
+    chains, against the oracle and the SVD closed form."""
+    prev = _native.s8_tile_geometry(1)
+    try:
+        torch.manual_seed(sum(shape) + 7)
+        x = torch.randn(*shape)
+        out = _s8_fp32(x.to(device), mode=mode)
+    finally:
+        _native.s8_tile_geometry(prev)
+    assert out.shape == x.shape and torch.isfinite(out).all()
+    assert max(per_matrix_rel(out, O.s8(x))) <= TOL[mode]
+    assert max(per_matrix_rel(out, O.s8_svd(x))) <= TOL[mode]
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+def test_s8_launch_timing_256x256_tiles(device, mode):
+    # oriented 300 x 500 padded to 512 x 512 with every launch forced to
+    # 256 x 256 tiles of 8 waves: the Gram and the square compute the 3
+    # upper-triangle blocks of their 512 x 512 results, the apply 2 x 2
+    # tiles; the one-hot term adds, per square tile and wave, 8 K stages of
+    # 2 MFMA tiles 32 x 32 x 16.
+    x = torch.randn(3, 300, 500, device=device)
+    prev = _native.s8_tile_geometry(1)
+    try:
+        out, phases, fl = _timed_s8(x, mode)
+    finally:
+        _native.s8_tile_geometry(prev)
+    assert phases == ["gram", "square", "poly1", "apply"] + ["gram", "square", "apply"] * 4
+    prod = 3 if mode == "comp_bf16" else 1
+    sym, apply = 3 * 3 * 2 * 256 * 256 * 512 * prod, 3 * 4 * 2 * 256 * 256 * 512 * prod
+    one_hot = 3 * 3 * 8 * 8 * 2 * 2 * 32 * 32 * 16 * prod
+    assert fl[:4] == [sym, sym, 0.0, apply]
+    assert fl[4:7] == [sym, sym + one_hot, apply]
+    assert max(per_matrix_rel(out, O.s8(x.cpu()))) <= TOL[mode]
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
 @pytest.mark.parametrize("batch,small", [(8, True), (160, False)])
 def test_s8_square_tile_geometries(device, mode, batch, small):
     """The square phase takes 128 x 128 tiles when they need fewer rounds of
