@@ -736,7 +736,7 @@ __global__ void __launch_bounds__((Geo<TM, TN>::kThreads))
 __attribute__((amdgpu_waves_per_eu(Geo<TM, TN>::kWavesPerEU, Geo<TM, TN>::kWavesPerEU)))
 s8_stage_kernel(StageArgs args) {
   using Gm = Geo<TM, TN>;
-  static_assert(Gm::kGeo != kGeoS || PHASE == kSquare || PHASE == kSym, "128 x 128 tiles for the square and SYM only");
+  static_assert(Gm::kGeo != kGeoS || PHASE != kApply, "no 128 x 128 tiles for the apply");
   constexpr int kSubM = Gm::kSubM, kTileN = Gm::kTileN, kThreads = Gm::kThreads, kWaves = Gm::kWaves;
   __shared__ __attribute__((aligned(16))) char smem[Gm::kRingBytes];
   __shared__ double dscratch[16];
@@ -1244,10 +1244,10 @@ static int64_t device_cus() {
 // operand bytes per MFMA (cfg5 S8 7% faster, the cfg4 applies 16%
 // faster).  With fewer, each CU has at most one block of a launch and
 // nothing of it to overlap a block's prologue and epilogue with (cfg4
-// Gram, square and SYM launches 15-60% slower).  Otherwise, for the square
-// and the SYM products (`small_ok`), 128 x 128 tiles when they take fewer
-// rounds of the CUs' block slots (three per CU, a round counted 0.9 of one
-// of two 256 x 128 blocks per CU), else 256 x 128.
+// Gram, square and SYM launches 15-60% slower).  Otherwise, for the
+// symmetric products (`small_ok`: Gram, square, SYM), 128 x 128 tiles when
+// they take fewer rounds of the CUs' block slots (three per CU, a round
+// counted 0.9 of one of two 256 x 128 blocks per CU), else 256 x 128.
 static int pick_geo(const S8Layout &Lay, int phase, const std::vector<Seg> &segs, bool small_ok) {
   if (g_tile_policy == 1) return kGeoL;
   const int64_t cus = device_cus();
@@ -1269,7 +1269,7 @@ static int pick_geo(const S8Layout &Lay, int phase, const std::vector<Seg> &segs
 // One phase launch of a stage kernel in geometry `geo`.
 template <int MODE, int PHASE>
 static void launch_stage(int geo, int32_t blocks, const StageArgs &a, hipStream_t st) {
-  if constexpr (PHASE == kSquare || PHASE == kSym) {
+  if constexpr (PHASE != kApply) {
     if (geo == kGeoS) {
       hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, 128, 128>), dim3(blocks), dim3(GeoS::kThreads), 0, st, a);
       return;
@@ -1297,7 +1297,7 @@ static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, int 
   a.b_over_c = static_cast<float>(co[1] / co[2]);
   const std::vector<Seg> segs = launch_segments(Lay, set, PHASE, stage, ops);
   if (static_cast<int>(segs.size()) > kMaxSeg) return fail(SMX_EINVAL, "s8: too many launch segments");
-  const int geo = PHASE == kSquare ? sq_geo : PHASE == kPoly1 ? kGeoM : pick_geo(Lay, PHASE, segs, PHASE == kSym);
+  const int geo = PHASE == kSquare ? sq_geo : PHASE == kPoly1 ? kGeoM : pick_geo(Lay, PHASE, segs, PHASE != kApply);
   int32_t off = 0;
   a.n_seg = 0;
   for (const Seg &sg : segs) {

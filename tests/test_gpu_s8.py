@@ -87,15 +87,16 @@ def _timed_s8(x, mode):
 @pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
 def test_s8_launch_timing_records_every_phase_x_space(device, mode):
     # oriented 300 x 500 padded to 512 x 512 (cp == rp): the stages run on
-    # the iterate.  The apply computes 2 x 4 tiles of 256 x 128, the Gram the
-    # 3 upper-triangle 256 x 256 blocks of its 512 x 512 result and the
-    # square its 10 upper-triangle 128 x 128 tiles; the one-hot term adds,
-    # per square tile and wave, 4 K stages of 2 MFMA tiles 32 x 32 x 16.
+    # the iterate.  The apply computes 2 x 4 tiles of 256 x 128, the Gram
+    # and the square the 10 upper-triangle 128 x 128 tiles of their 512 x 512
+    # results (three matrices take fewer rounds of the CUs' block slots in
+    # the smaller geometry); the one-hot term adds, per square tile and
+    # wave, 4 K stages of 2 MFMA tiles 32 x 32 x 16.
     x = torch.randn(3, 300, 500, device=device)
     _, phases, fl = _timed_s8(x, mode)
     assert phases == ["gram", "square", "poly1", "apply"] + ["gram", "square", "apply"] * 4
     prod = 3 if mode == "comp_bf16" else 1
-    gram, apply = 3 * 3 * 2 * 256 * 256 * 512 * prod, 3 * 8 * 2 * 256 * 128 * 512 * prod
+    gram, apply = 3 * 10 * 2 * 128 * 128 * 512 * prod, 3 * 8 * 2 * 256 * 128 * 512 * prod
     square1 = 3 * 10 * 2 * 128 * 128 * 512 * prod
     one_hot = 3 * 10 * 4 * 4 * 2 * 2 * 32 * 32 * 16 * prod
     assert fl[:4] == [gram, square1, 0.0, apply]
@@ -108,17 +109,17 @@ def test_s8_launch_timing_records_every_phase_gram_space(device, mode):
     # oriented 300 x 520 padded to 512 x 768 (cp > rp): Gram space, in two
     # segments.  Grams of X0 (stage 1) and X2 (stage 3), K = 768; applies of
     # Q2 to X0 and of Q5 to X2 over 2 x 6 tiles; symmetric r x r products
-    # T = P G and G = T P (stages 1, 3, 4) on the 10 upper-triangle
-    # 128 x 128 tiles (three matrices take fewer rounds of the CUs' block
-    # slots in the smaller geometry) and full products Q' = P Q (stages 2,
-    # 4, 5) over 2 x 4 apply tiles, all with K = 512.
+    # T = P G and G = T P (stages 1, 3, 4) and the Grams on the 10
+    # upper-triangle 128 x 128 tiles (three matrices take fewer rounds of
+    # the CUs' block slots in the smaller geometry) and full products
+    # Q' = P Q (stages 2, 4, 5) over 2 x 4 apply tiles, all with K = 512.
     x = torch.randn(3, 300, 520, device=device)
     out, phases, fl = _timed_s8(x, mode)
     assert phases == (["gram", "square", "poly1", "sym", "sym"] + ["square", "apply", "apply"]
                       + ["gram", "square", "sym", "sym"] + ["square", "sym", "sym", "apply"]
                       + ["square", "apply", "apply"])
     prod = 3 if mode == "comp_bf16" else 1
-    gram, x_apply = 3 * 3 * 2 * 256 * 256 * 768 * prod, 3 * 12 * 2 * 256 * 128 * 512 * prod
+    gram, x_apply = 3 * 10 * 2 * 128 * 128 * 768 * prod, 3 * 12 * 2 * 256 * 128 * 512 * prod
     sym, apply_q = 3 * 10 * 2 * 128 * 128 * 512 * prod, 3 * 8 * 2 * 256 * 128 * 512 * prod
     square1 = 3 * 10 * 2 * 128 * 128 * 512 * prod
     square = square1 + 3 * 10 * 4 * 4 * 2 * 2 * 32 * 32 * 16 * prod
@@ -189,25 +190,43 @@ def test_s8_launch_timing_256x256_tiles(device, mode):
     assert max(per_matrix_rel(out, O.s8(x.cpu()))) <= TOL[mode]
 
 
+# (tile rows, tile columns, waves) of each geometry
+GEOMETRY = {"128x128": (128, 128, 4), "256x128": (256, 128, 4), "256x256": (256, 256, 8)}
+
+
+def expected_square_geometry(n, size, cus):
+    """The square's geometry for a launch over n matrices of size x size:
+    256 x 256 tiles when there are at least 0.9 of one per CU, else 128 x 128
+    tiles when they take fewer rounds of the CUs' block slots (three per CU,
+    a round counted 0.9 of one of two 256 x 128 blocks), else 256 x 128."""
+    t256, ts = size // 256, size // 128
+    sym = lambda t: t * (t + 1) // 2
+    if 10 * n * sym(t256) >= 9 * cus:
+        return "256x256", sym(t256)
+    big_rounds = -(-n * 2 * sym(t256) // (2 * cus))
+    small_rounds = -(-n * sym(ts) // (3 * cus))
+    return ("128x128", sym(ts)) if 0.9 * small_rounds < big_rounds else ("256x128", 2 * sym(t256))
+
+
 @pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
-@pytest.mark.parametrize("batch,small", [(8, True), (160, False)])
-def test_s8_square_tile_geometries(device, mode, batch, small):
-    """The square phase takes 128 x 128 tiles when they need fewer rounds of
-    the CUs' block slots and 256 x 128 tiles otherwise.  A class of 4 or
-    more matrices runs as two launch chains of halves, and each chain's
-    launches decide for themselves: 4 matrices of 512 x 512 on 256 CUs give
-    40 small tiles against 24 large ones, one round each; 80 matrices give
-    480 large tiles in one round of two blocks per CU, while their 800 small
-    ones need two rounds of three, counted 0.9 each.  Both geometries meet
-    the gates; the recorded square FLOPs show which one ran."""
+@pytest.mark.parametrize("batch,size,geometry", [(8, 512, "128x128"), (74, 768, "256x128"), (160, 512, "256x256")])
+def test_s8_square_tile_geometries(device, mode, batch, size, geometry):
+    """The square phase takes 256 x 256 tiles when the launch has at least
+    0.9 of one per CU, else 128 x 128 tiles when they need fewer rounds of
+    the CUs' block slots, else 256 x 128 tiles.  A class of 4 or more
+    matrices runs as two launch chains of halves, and each chain's launches
+    decide for themselves: 4 matrices of 512 x 512 on 256 CUs give 40 small
+    tiles against 24 of 256 x 128, one round each; 37 of 768 x 768 give 777
+    small tiles (two rounds of three per CU) against 444 of 256 x 128 (one
+    round of two) and 222 of 256 x 256; 80 of 512 x 512 give 240 tiles of
+    256 x 256.  Every geometry meets the gates; the recorded square FLOPs
+    show which one ran."""
     cus = torch.cuda.get_device_properties(device).multi_processor_count
     chains = [batch - batch // 2, batch // 2] if batch >= 4 else [batch]
     for n in chains:
-        big_rounds = -(-n * 6 // (2 * cus))
-        small_rounds = -(-n * 10 // (3 * cus))
-        assert (0.9 * small_rounds < big_rounds) == small, "the case no longer selects the geometry it names"
+        assert expected_square_geometry(n, size, cus)[0] == geometry, "the case no longer selects the geometry it names"
     torch.manual_seed(batch)
-    x = torch.randn(batch, 512, 512)
+    x = torch.randn(batch, size, size)
     from sandmuon_amd import _native
     _native.s8_timing(True)
     try:
@@ -216,11 +235,12 @@ def test_s8_square_tile_geometries(device, mode, batch, small):
         _native.s8_timing(False)
     rec = _native.s8_timing_read()
     prod = 3 if mode == "comp_bf16" else 1
-    tiles, tm = (10, 128) if small else (6, 256)
+    tm, tn, waves = GEOMETRY[geometry]
+    tiles = expected_square_geometry(chains[0], size, cus)[1]
     # per matrix: stage 1 (G G) and stages 2-5 (G G plus the one-hot (b/c) G
     # MFMAs: per wave 2 tm/64 K stages of 2 32x32x16 products per tile)
-    f1 = tiles * 2 * tm * 128 * 512 * prod
-    f2 = f1 + tiles * 4 * (2 * tm // 64) * 2 * 2 * 32 * 32 * 16 * prod
+    f1 = tiles * 2 * tm * tn * size * prod
+    f2 = f1 + tiles * waves * (2 * tm // 64) * 2 * 2 * 32 * 32 * 16 * prod
     want = sorted(f for n in chains for f in [n * f1] + [n * f2] * 4)
     assert sorted(f for _, p, f in rec if p == "square") == want
     errs = per_matrix_rel(out, O.s8(x))
