@@ -867,7 +867,6 @@ s8_stage_kernel(StageArgs args) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wm = wave / Gm::kWavesN, wn = wave % Gm::kWavesN;
   const int lr = lane & 31, lh = lane >> 5;
-  const int rr = lane >> 2, cc = (lane & 3) * 8;  // read-back: rows rr, rr + 16; cols cc..cc+7
   const int64_t R0 = tm * Gm::kTileM + wm * (32 * kSubM), C0 = tn * kTileN + wn * (32 * kSubN);
   const bool last = stage == 5;
   float *dst_t, *dst_m;
@@ -913,7 +912,7 @@ s8_stage_kernel(StageArgs args) {
   // The stage-5 result of the matrix step: per parameter row, partial sums
   // of Q z, (a Q)^2 and (a Q)(a z) over the wave's strip of parameter
   // columns (its 64 output columns; its 128 output rows for a transposed
-  // parameter), reduced over the 4 lanes of the row and stored for the
+  // parameter), reduced over the 8 lanes of the row and stored for the
   // mapback (its row coefficients and graft norm), so no later pass reads Q
   // for them.
   static_assert(PHASE != kApply || (kStripT == 32 * kSubN && kStripM == 32 * kSubM),
@@ -931,42 +930,77 @@ s8_stage_kernel(StageArgs args) {
     }
     __syncthreads();
   }
-  float rs[kSubN][2][3];
+  // Read-back: 8 lanes per row of a 32 x 32 block, each the 16-byte chunk
+  // `ech` of the row's 128 bytes (32 columns), so that every store
+  // instruction writes 8 whole rows of the block: full 128-byte lines (a
+  // burst of such stores runs 25% faster than one of 32-byte pieces).  In
+  // operand form the chunk is plane (ech >> 1) & 1 of columns
+  // 16 (ech >> 2) + 8 (ech & 1) .. + 7; in FP32 columns 4 ech .. 4 ech + 3.
+  const int er = lane >> 3, ech = lane & 7;
+  const bool lo_plane = ((ech >> 1) & 1) != 0;
+  const int ec8 = 16 * (ech >> 2) + 8 * (ech & 1), ec4 = 4 * ech;
+  float rs[kSubN][4][3];
 #pragma unroll
   for (int j = 0; j < kSubN; ++j)
 #pragma unroll
-    for (int q = 0; q < 2; ++q) rs[j][q][0] = rs[j][q][1] = rs[j][q][2] = 0.f;
-  // a and z of parameter columns gc .. gc + 7 (zeros past the last column)
-  auto colv8 = [&](int64_t gc, float (&a8)[8], float (&z8)[8]) {
+    for (int q = 0; q < 4; ++q) rs[j][q][0] = rs[j][q][1] = rs[j][q][2] = 0.f;
+  // The row-sum partials of one row (FP32 output, four columns per lane),
+  // reduced over the row's 8 lanes and stored by the first.
+  auto accum4 = [&](const float (&w)[4], int64_t gc, float (&r)[3]) {
     const int o = static_cast<int>(gc - rs_c0);
-    ep_read8(colv_lds, 0, o, a8);
-    ep_read8(colv_lds, 0, rs_w + o, z8);
-  };
-  auto accum = [&](const float (&w)[8], const float (&a8)[8], const float (&z8)[8], float (&r)[3]) {
+    const f32x4 a4 = *reinterpret_cast<const f32x4 *>(colv_lds + o);
+    const f32x4 z4 = *reinterpret_cast<const f32x4 *>(colv_lds + rs_w + o);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float aw = a8[e] * w[e];
-      r[0] = fmaf(w[e], z8[e], r[0]);
+    for (int e = 0; e < 4; ++e) {
+      const float aw = a4[e] * w[e];
+      r[0] = fmaf(w[e], z4[e], r[0]);
       r[1] = fmaf(aw, aw, r[1]);
-      r[2] = fmaf(aw, a8[e] * z8[e], r[2]);
+      r[2] = fmaf(aw, a4[e] * z4[e], r[2]);
     }
   };
   auto emit = [&](int64_t prow, int64_t strip, float (&r)[3]) {
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-      r[k] += dpp_mov<0xB1>(r[k]);  // quad_perm [1,0,3,2]
-      r[k] += dpp_mov<0x4E>(r[k]);  // quad_perm [2,3,0,1]: the row's 4 lanes
+      r[k] += dpp_mov<0xB1>(r[k]);   // quad_perm [1,0,3,2]
+      r[k] += dpp_mov<0x4E>(r[k]);   // quad_perm [2,3,0,1]
+      r[k] += dpp_mov<0x141>(r[k]);  // row_half_mirror: the row's 8 lanes
     }
-    if ((lane & 3) == 0)
+    if (ech == 0)
 #pragma unroll
       for (int k = 0; k < 3; ++k) M.mrp(k)[strip * prows + prow] = r[k];
 #pragma unroll
     for (int k = 0; k < 3; ++k) r[k] = 0.f;
   };
-  auto add_eye = [&](int64_t row, int64_t col0, float(&w)[8]) {
+  // Row `row` of a staged block (S) to global row gr, columns gc0 .. gc0 + 31
+  // (gc0 a multiple of 32): one 16-byte store per lane.
+  auto put_row = [&](const float *S, int row, int64_t gr, int64_t gc0, float *dst, int64_t ld, bool pl,
+                     float (&r)[3], bool acc_r) {
+    char *out = reinterpret_cast<char *>(dst) + (gr * ld + gc0) * 4 + 16 * ech;
+    if (pl) {
+      float w[8];
+      ep_read8(S, row, ec8, w);
+      if (eye)
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (row == col0 + e && row < K.r) w[e] += args.a;
+        for (int e = 0; e < 8; ++e)
+          if (gr == gc0 + ec8 + e && gr < K.r) w[e] += args.a;
+      uint32_t b[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint16_t x0 = lo_plane ? bf16_lo_bits(w[2 * e]) : bf16_bits(w[2 * e]);
+        const uint16_t x1 = lo_plane ? bf16_lo_bits(w[2 * e + 1]) : bf16_bits(w[2 * e + 1]);
+        b[e] = x0 | (static_cast<uint32_t>(x1) << 16);
+      }
+      *reinterpret_cast<uint4 *>(out) = make_uint4(b[0], b[1], b[2], b[3]);
+    } else {
+      const f32x4 v4 = *reinterpret_cast<const f32x4 *>(S + row * kEpStride + ec4);
+      float w[4] = {v4.x, v4.y, v4.z, v4.w};
+      if (eye)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (gr == gc0 + ec4 + e && gr < K.r) w[e] += args.a;
+      *reinterpret_cast<float4 *>(out) = make_float4(w[0], w[1], w[2], w[3]);
+      if (acc_r) accum4(w, gc0 + ec4, r);
+    }
   };
 #pragma unroll
   for (int blk = 0; blk < kSubM * kSubN; ++blk) {
@@ -982,32 +1016,18 @@ s8_stage_kernel(StageArgs args) {
       }
       if (do_m) *reinterpret_cast<f32x4 *>(U + lr * kEpStride + 8 * k + 4 * lh) = v;
     }
-    float a8[8], z8[8];
-    if (rsum) colv8(do_m ? R0 + i * 32 + cc : C0 + j * 32 + cc, a8, z8);
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int row = rr + 16 * q;
+    for (int q = 0; q < 4; ++q) {
+      const int row = er + 8 * q;
       if (do_t) {
-        float w[8];
-        ep_read8(T, row, cc, w);
-        const int64_t gr = R0 + i * 32 + row, gc = C0 + j * 32 + cc;
-        if (eye) add_eye(gr, gc, w);
-        put_operand8(dst_t, gr * ld_t + gc, w, pl_t);
-        if (rsum) {
-          accum(w, a8, z8, rs[0][q]);
-          if (j == kSubN - 1) emit(gr, C0 / kStripT, rs[0][q]);
-        }
+        const int64_t gr = R0 + i * 32 + row;
+        put_row(T, row, gr, C0 + j * 32, dst_t, ld_t, pl_t, rs[0][q], rsum);
+        if (rsum && j == kSubN - 1) emit(gr, C0 / kStripT, rs[0][q]);
       }
       if (do_m) {
-        float w[8];
-        ep_read8(U, row, cc, w);
-        const int64_t gr = C0 + j * 32 + row, gc = R0 + i * 32 + cc;
-        if (eye) add_eye(gr, gc, w);
-        put_operand8(dst_m, gr * ld_m + gc, w, pl_m);
-        if (rsum) {
-          accum(w, a8, z8, rs[j][q]);
-          if (i == kSubM - 1) emit(gr, R0 / kStripM, rs[j][q]);
-        }
+        const int64_t gr = C0 + j * 32 + row;
+        put_row(U, row, gr, R0 + i * 32, dst_m, ld_m, pl_m, rs[j][q], rsum);
+        if (rsum && i == kSubM - 1) emit(gr, R0 / kStripM, rs[j][q]);
       }
     }
     // Keep the scheduler from hoisting every accumulator read to the top
