@@ -294,10 +294,11 @@ def log(msg):
 def train_bench(args, device):
     """Whole training steps of the cfg4 GPT: 8 microbatches of 16 x 1024
     random tokens, forward and backward under bf16 autocast, then step().
-    Three variants on the same model and optimizer: the statistics in the
-    hooks (the reference's design), fused into the Linear's input cast and
-    bias-gradient passes (sandmuon_amd.fused), and none at all (hooks
-    removed, forward/backward only) as the floor both are measured against."""
+    Four variants on the same model and optimizer: the statistics in the
+    hooks (the reference's design); fused into the Linear's input cast and
+    bias-gradient passes (sandmuon_amd.fused); those and the MLP's GELU
+    (the model passed to fuse_statistics); and none at all (hooks removed,
+    forward/backward only) as the floor they are measured against."""
     from sandmuon_amd import RankOneAWeightedPE
     from sandmuon_amd.fused import fuse_statistics
     from sandmuon_amd.workloads import GPT, GPT_103M, transformer_filter
@@ -346,6 +347,12 @@ def train_bench(args, device):
     fused = timed(True)
     log(f"train: fused {fused}")
     handle.close()
+    handle = fuse_statistics(opt, model)
+    log("train: fused statistics and GELU")
+    fused_gelu = timed(True)
+    gelu_per_step = handle.gelu_taken / (args.warmup + args.steps)
+    log(f"train: fused with GELU {fused_gelu} ({gelu_per_step:.0f} GELU outputs' statistics taken per step)")
+    handle.close()
     opt.close()
     log("train: no statistics (forward/backward only)")
     floor = timed(False)
@@ -360,8 +367,11 @@ def train_bench(args, device):
                    "matrices": len(opt.named_matrices), "microbatches": len(micro)},
         "variants_ms": {"hooks": {"total": hooks[0], "fwd_bwd": hooks[1], "step": hooks[2]},
                         "fused": {"total": fused[0], "fwd_bwd": fused[1], "step": fused[2]},
+                        "fused_with_gelu": {"total": fused_gelu[0], "fwd_bwd": fused_gelu[1], "step": fused_gelu[2],
+                                            "gelu_outputs_per_step": gelu_per_step},
                         "no_statistics_fwd_bwd": floor[1]},
-        "statistics_cost_ms": {"hooks": round(hooks[1] - floor[1], 3), "fused": round(fused[1] - floor[1], 3)},
+        "statistics_cost_ms": {"hooks": round(hooks[1] - floor[1], 3), "fused": round(fused[1] - floor[1], 3),
+                               "fused_with_gelu": round(fused_gelu[1] - floor[1], 3)},
     }
     print(json.dumps(out), flush=True)
 

@@ -115,6 +115,29 @@ int smx_stats_cast(const void *x, int dtype, int64_t rows, int64_t cols,
                    int32_t n_slots, void *out, int out_dtype,
                    int64_t out_stride, void *stream);
 
+/* smx_stats_gelu: out = GELU(x) (the exact form, x * 0.5 * (1 + erf(x /
+ * sqrt(2))) in FP32, rounded to the input dtype) with the A statistic of
+ * sandmuon/optimizer.py:156-168 of the output taken in the same pass, for
+ * the Linear the GELU feeds (no reference entry point; row 8f.1).  The
+ * statistic goes to per-chunk partials, not to slot rows: part_sq (and
+ * part_first, or NULL) receive smx_stats_slot_rows(rows, n_slots) rows of
+ * cols FP32 sums, which smx_stats_add_partials later adds into the Linear's
+ * slot rows; the result is the slot rows a smx_stats_accumulate of out
+ * would leave, bit for bit.  x and out are bf16 or f16 (out in x's dtype),
+ * with cols and row strides multiples of 8 elements and 16-byte aligned
+ * pointers (SMX_EALIGN otherwise). */
+int smx_stats_gelu(const void *x, int dtype, int64_t rows, int64_t cols,
+                   int64_t row_stride, void *out, int64_t out_stride,
+                   float *part_sq, float *part_first, int32_t n_slots,
+                   void *stream);
+
+/* slots[p*cols + c] += part[p*cols + c] for p < n_rows (FP32), for sq and,
+ * when both are given, first: the addition a statistics call makes into its
+ * slot rows, applied to the partials of smx_stats_gelu. */
+int smx_stats_add_partials(float *slots_sq, const float *part_sq,
+                           float *slots_first, const float *part_first,
+                           int64_t cols, int32_t n_rows, void *stream);
+
 /* smx_stats_colsum: the backward's bias gradient, colsum[c] = sum over the
  * rows of x, with the B statistic of sandmuon/optimizer.py:171-177 taken
  * from the same read.  The read writes one FP32 partial per row chunk into

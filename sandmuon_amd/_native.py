@@ -72,6 +72,9 @@ SIGNATURES = {
     "smx_stats_slot_rows": (c_int32, [c_int64, c_int32]),
     "smx_stats_cast": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int32,
                                c_void_p, c_int, c_int64, c_void_p]),
+    "smx_stats_gelu": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
+                               c_int32, c_void_p]),
+    "smx_stats_add_partials": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
     "smx_stats_colsum_workspace_bytes": (c_int64, [c_int64, c_int32]),
     "smx_stats_colsum": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_int32, c_void_p,
                                  c_void_p, c_int64, c_void_p]),
@@ -234,6 +237,24 @@ def stats_cast(rows2d: torch.Tensor, slots_sq: torch.Tensor, slots_first: Option
                               out2d.data_ptr(), dtype_code(out2d.dtype), out2d.stride(0),
                               stream_of(rows2d.device))
     _check(rc, "smx_stats_cast")
+
+
+def stats_gelu(rows2d: torch.Tensor, out2d: torch.Tensor, part_sq: torch.Tensor, part_first: Optional[torch.Tensor],
+               n_slots: int) -> None:
+    """out2d = GELU(rows2d) (bf16/f16) with the per-chunk partial sums of
+    out2d's statistic in part_sq / part_first ([chunks, cols] FP32)."""
+    rc = lib().smx_stats_gelu(rows2d.data_ptr(), dtype_code(rows2d.dtype), rows2d.shape[0], rows2d.shape[1],
+                              rows2d.stride(0), out2d.data_ptr(), out2d.stride(0), part_sq.data_ptr(),
+                              ptr(part_first), n_slots, stream_of(rows2d.device))
+    _check(rc, "smx_stats_gelu")
+
+
+def stats_add_partials(slots_sq: torch.Tensor, part_sq: torch.Tensor, slots_first: Optional[torch.Tensor],
+                       part_first: Optional[torch.Tensor]) -> None:
+    """slots[:chunks] += partials (FP32), chunks = part_sq.shape[0]."""
+    rc = lib().smx_stats_add_partials(slots_sq.data_ptr(), part_sq.data_ptr(), ptr(slots_first), ptr(part_first),
+                                      part_sq.shape[1], part_sq.shape[0], stream_of(part_sq.device))
+    _check(rc, "smx_stats_add_partials")
 
 
 def stats_colsum_workspace_bytes(cols: int, n_slots: int) -> int:

@@ -9,7 +9,10 @@
 //    job, so the result is deterministic, depends on the job alone (not on
 //    the other jobs of the launch), and no atomics or tail combine are
 //    needed.  The same kernel takes the statistic inside a Linear's input
-//    cast (CAST) and bias-gradient column sum (kSqColsum).
+//    cast (CAST) and bias-gradient column sum (kSqColsum), and the statistic
+//    of a GELU's output inside the GELU (XF, kSqDefer*): the A statistic of
+//    the Linear the GELU feeds, as per-chunk partials that the Linear's
+//    forward adds into its slot rows (stats_add_partials).
 //  * stats_fold: sum += sum over slot rows (FP64), slots zeroed.
 //  * stats_finish: _finish_a/_finish_b (sandmuon/optimizer.py:182-222) with
 //    rank1_inverse_sqrt (:27-35) and diagonal_inverse_sqrt (:19-24).
@@ -32,7 +35,22 @@ enum StatsMode : int {
   kSqOnly = 0,    // B side, diagonal A
   kSqFirst = 1,   // rank-one A: sum(x) into its own slot rows
   kSqColsum = 2,  // sum(x) of this call's rows into per-chunk partials (a bias gradient)
+  kSqDefer = 3,       // sum(x^2) into per-chunk partials (plain stores), added to slot rows later
+  kSqFirstDefer = 4,  // kSqDefer, and sum(x) into per-chunk partials too
 };
+constexpr int kStatsModes = 5;
+
+// Elementwise transform of the input before the statistic (XF): none, or
+// the exact GELU of the input, rounded to the input dtype and stored in
+// cast_out; the statistic is that of the stored (rounded) values.
+enum StatsXform : int { kXfNone = 0, kXfGelu = 1 };
+
+// torch's exact GELU in FP32 (x * 0.5 * (1 + erf(x / sqrt(2))), evaluated
+// left to right), without contraction.
+__device__ __forceinline__ float gelu_erf(float x) {
+  const float e = erff(__fmul_rn(x, static_cast<float>(M_SQRT1_2)));
+  return __fmul_rn(__fmul_rn(x, 0.5f), __fadd_rn(1.0f, e));
+}
 
 // Element access of one lane's VEC consecutive channels: `raw` loads their
 // bits (16 bytes for the vector forms, one element otherwise) and `cvt`
@@ -91,7 +109,12 @@ __device__ __forceinline__ void store_cast(void *out, int64_t i, const float *v)
     }
   }
   uint16_t *o = static_cast<uint16_t *>(out) + i;
-  if constexpr (VEC == 4) {
+  if constexpr (VEC == 8) {
+    *reinterpret_cast<uint4 *>(o) = make_uint4(h[0] | (static_cast<uint32_t>(h[1]) << 16),
+                                               h[2] | (static_cast<uint32_t>(h[3]) << 16),
+                                               h[4] | (static_cast<uint32_t>(h[5]) << 16),
+                                               h[6] | (static_cast<uint32_t>(h[7]) << 16));
+  } else if constexpr (VEC == 4) {
     *reinterpret_cast<uint2 *>(o) = make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16),
                                                h[2] | (static_cast<uint32_t>(h[3]) << 16));
   } else {
@@ -107,8 +130,8 @@ __device__ __forceinline__ void store_cast(void *out, int64_t i, const float *v)
 struct StatsJob {
   const void *x;
   float *sq;
-  float *first;     // kSqFirst: slot rows of sum(x); kSqColsum: per-chunk partials, plain stores
-  void *cast_out;   // CAST: low-precision copy of x
+  float *first;     // kSqFirst: slot rows of sum(x); kSqColsum, kSqFirstDefer: per-chunk partials, plain stores
+  void *cast_out;   // CAST: low-precision copy of x; XF: the transformed x
   int64_t rows, cols, row_stride, out_stride, rows_per_chunk;
   int32_t block_begin, tiles, code, pad_;
 };
@@ -124,15 +147,20 @@ static_assert(sizeof(StatsPack) <= 4000, "StatsPack is passed by value in the ke
 // U loads in flight and the next batch issued before the current one
 // is consumed; lanes holding the same channels are then added by xor
 // shuffles, the waves in wave order, and the sum is added to the slot row,
-// whose old value was loaded at the start of the block.  CAST (fp32 input
-// only) also writes x converted to bf16/f16, as the mixed-precision cast in
-// front of a Linear would.  MODE and CAST change nothing in how sum(x^2) is
-// formed, so every variant adds the same bits to the slots.
-template <int DT, int VEC, int CT, int U, int MODE, int CAST>
+// whose old value was loaded at the start of the block (the deferred modes
+// store the chunk's sum instead, to be added to the slot row later by one
+// FP32 addition, the same one).  CAST (fp32 input only) also writes x
+// converted to bf16/f16, as the mixed-precision cast in front of a Linear
+// would.  MODE and CAST change nothing in how sum(x^2) is formed, so every
+// variant adds the same bits to the slots; with XF the statistic is that of
+// the transformed values a later read of the output would load.
+template <int DT, int VEC, int CT, int U, int MODE, int CAST, int XF>
 __device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int64_t chunk, float *red) {
   using E = Elems<DT, VEC>;
   using Raw = typename E::Raw;
-  constexpr bool FIRST = MODE != kSqOnly;
+  constexpr bool FIRST = MODE != kSqOnly && MODE != kSqDefer;
+  constexpr bool DEFER = MODE == kSqDefer || MODE == kSqFirstDefer;
+  static_assert(XF == kXfNone || (CAST == 0 && DT != SMX_F32 && DEFER), "the GELU form: 16-bit input, deferred");
   constexpr int RPW = 64 / CT;
   constexpr int GROUPS = kStatsWaves * RPW;
   constexpr int TW = CT * VEC;
@@ -152,7 +180,7 @@ __device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int6
   const int c = threadIdx.x;
   const bool own = c < TW && tile_col0 + c < J.cols;
   float old_sq = 0.f, old_first = 0.f;
-  if (own && !empty) old_sq = J.sq[row_off + c];
+  if (!DEFER && own && !empty) old_sq = J.sq[row_off + c];
   if constexpr (MODE == kSqFirst)
     if (own) old_first = J.first[row_off + c];
 
@@ -171,6 +199,19 @@ __device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int6
     auto eat1 = [&](const Raw &q, int64_t row) {
       float v[VEC];
       E::cvt(q, v);
+      if constexpr (XF == kXfGelu) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          float g = gelu_erf(v[k]);
+          // The FP32 result is rounded to the 16-bit type as a separate step
+          // (torch rounds its FP32 result): the compiler would otherwise fold
+          // the last multiply into a mixed FMA that rounds to f16 once.
+          asm volatile("" : "+v"(g));
+          if constexpr (DT == SMX_BF16) v[k] = bf16_bits_to_f32(f32_to_bf16_bits(g));
+          else v[k] = f16_bits_to_f32(__builtin_bit_cast(uint16_t, static_cast<_Float16>(g)));
+        }
+        store_cast<DT, VEC>(J.cast_out, row * J.out_stride + col0, v);
+      }
 #pragma unroll
       for (int k = 0; k < VEC; ++k) {
         acc_sq[k] = fmaf(v[k], v[k], acc_sq[k]);
@@ -229,9 +270,9 @@ __device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int6
       s += red_sq[w * TW + c];
       if constexpr (FIRST) f += red_first[w * TW + c];
     }
-    if (!empty) J.sq[row_off + c] = old_sq + s;
+    if (!empty) J.sq[row_off + c] = DEFER ? s : old_sq + s;
     if constexpr (MODE == kSqFirst) J.first[row_off + c] = old_first + f;
-    if constexpr (MODE == kSqColsum) J.first[row_off + c] = f;
+    if constexpr (MODE == kSqColsum || MODE == kSqFirstDefer) J.first[row_off + c] = f;
   }
 }
 
@@ -239,7 +280,9 @@ __device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int6
 // scalar forms one element (64-lane tiles) for inputs whose width, row
 // stride or address is not 16-byte aligned.
 enum StatsForm : int { kF32V4 = 0, kBf16V8, kF16V8, kF32V1, kBf16V1, kF16V1, kNumForms };
-__host__ __device__ constexpr int stats_code(int form, int mode, int cast) { return (form * 3 + mode) * 3 + cast; }
+__host__ __device__ constexpr int stats_code(int form, int mode, int cast, int xf = kXfNone) {
+  return ((form * kStatsModes + mode) * 3 + cast) * 2 + xf;
+}
 
 // CT: lanes across a column tile (32 for the vector forms: 128 f32 or 256
 // 16-bit channels; 16 lanes measured 2% slower on the cfg4 hook inputs).
@@ -267,27 +310,35 @@ constexpr int64_t kTileChannels[kNumForms] = {tile_channels<kF32V4>(),  tile_cha
 // bits whether it is launched alone or with others.
 constexpr int64_t kStatsMinChunkRows = 512;
 
-template <int FORM, int MODE, int CAST>
+// The GELU form keeps two loads per batch: its erf evaluations need the
+// registers (it has a kernel of its own, so the hook kernel keeps its
+// register budget).
+template <int FORM, int MODE, int CAST, int XF>
 __device__ __forceinline__ void run_tile(const StatsJob &J, int64_t tile, int64_t chunk, float *red) {
   using F = FormTraits<FORM>;
-  stats_tile<F::DT, F::VEC, F::CT, F::U, MODE, CAST>(J, tile, chunk, red);
+  stats_tile<F::DT, F::VEC, F::CT, XF == kXfNone ? F::U : 2, MODE, CAST, XF>(J, tile, chunk, red);
+}
+
+// The job of block b of a launch: block_begin grows with the job index, so
+// the index is the count of later jobs that begin at or before the block
+// (unrolled, so the scalar loads of every begin are issued together).
+__device__ __forceinline__ int stats_job_of(const StatsPack &pack, int b) {
+  int j = 0;
+#pragma unroll
+  for (int i = 1; i < kStatsJobs; ++i) j += (i < pack.n && b >= pack.job[i].block_begin) ? 1 : 0;
+  return j;
 }
 
 // grid.x = sum over the jobs of tiles * n_chunks; block = kStatsThreads.
 __global__ void __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(6))) stats_accumulate_kernel(StatsPack pack) {
   __shared__ float red[2 * kStatsWaves * kStatsMaxTW];
-  // The job of this block: block_begin grows with the job index, so the
-  // index is the count of later jobs that begin at or before the block
-  // (unrolled, so the scalar loads of every begin are issued together).
   const int b = static_cast<int>(blockIdx.x);
-  int j = 0;
-#pragma unroll
-  for (int i = 1; i < kStatsJobs; ++i) j += (i < pack.n && b >= pack.job[i].block_begin) ? 1 : 0;
-  const StatsJob &J = pack.job[j];
+  const StatsJob &J = pack.job[stats_job_of(pack, b)];
   const int64_t local = b - J.block_begin;
   const int64_t tile = local % J.tiles, chunk = local / J.tiles;
 #define SMX_STATS_CASE(FORM, MODE, CAST) \
-  case stats_code(FORM, MODE, CAST): run_tile<FORM, MODE, CAST>(J, tile, chunk, red); break;
+  case stats_code(FORM, MODE, CAST): run_tile<FORM, MODE, CAST, kXfNone>(J, tile, chunk, red); break;
+
 #define SMX_STATS_MODES(FORM)          \
   SMX_STATS_CASE(FORM, kSqOnly, 0)     \
   SMX_STATS_CASE(FORM, kSqFirst, 0)    \
@@ -313,6 +364,28 @@ __global__ void __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per
 #undef SMX_STATS_CASE
 }
 
+// The GELU jobs (smx_stats_gelu), in a kernel of their own.
+__global__ void __launch_bounds__(kStatsThreads) stats_gelu_kernel(StatsPack pack) {
+  __shared__ float red[2 * kStatsWaves * kStatsMaxTW];
+  const int b = static_cast<int>(blockIdx.x);
+  const StatsJob &J = pack.job[stats_job_of(pack, b)];
+  const int64_t local = b - J.block_begin;
+  const int64_t tile = local % J.tiles, chunk = local / J.tiles;
+#define SMX_STATS_GELU(FORM)                                                                   \
+  case stats_code(FORM, kSqDefer, 0, kXfGelu):                                                 \
+    run_tile<FORM, kSqDefer, 0, kXfGelu>(J, tile, chunk, red);                                 \
+    break;                                                                                     \
+  case stats_code(FORM, kSqFirstDefer, 0, kXfGelu):                                            \
+    run_tile<FORM, kSqFirstDefer, 0, kXfGelu>(J, tile, chunk, red);                            \
+    break;
+  switch (J.code) {
+    SMX_STATS_GELU(kBf16V8)
+    SMX_STATS_GELU(kF16V8)
+    default: break;
+  }
+#undef SMX_STATS_GELU
+}
+
 // Host side: one job per input, launched in packs of kStatsJobs.
 struct StatsInput {
   const void *x;
@@ -323,6 +396,7 @@ struct StatsInput {
   int mode, cast;
   void *cast_out;
   int64_t out_stride;
+  int xf = kXfNone;
 };
 
 static int stats_form(const StatsInput &in) {
@@ -342,8 +416,11 @@ static int stats_launch(const StatsInput *in, int n, hipStream_t st, const char 
   int64_t blocks = 0;
   auto flush = [&]() -> int {
     if (pack.n == 0) return SMX_OK;
-    hipLaunchKernelGGL(stats_accumulate_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kStatsThreads), 0, st,
-                       pack);
+    if (pack.job[0].code % 2 == kXfGelu)
+      hipLaunchKernelGGL(stats_gelu_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kStatsThreads), 0, st, pack);
+    else
+      hipLaunchKernelGGL(stats_accumulate_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kStatsThreads), 0, st,
+                         pack);
     pack.n = 0;
     blocks = 0;
     return check_launch(who);
@@ -357,7 +434,7 @@ static int stats_launch(const StatsInput *in, int n, hipStream_t st, const char 
     // row, so it keeps one block per slot row.
     const int64_t chunks = s.mode == kSqColsum ? s.n_slots : std::max<int64_t>(ceil_div(s.rows, rows_per_chunk), 1);
     const int64_t nb = tiles * chunks;
-    if (pack.n == kStatsJobs || blocks + nb > INT32_MAX) {
+    if (pack.n == kStatsJobs || blocks + nb > INT32_MAX || (pack.n > 0 && pack.job[0].code % 2 != s.xf)) {
       int rc = flush();
       if (rc) return rc;
     }
@@ -373,7 +450,7 @@ static int stats_launch(const StatsInput *in, int n, hipStream_t st, const char 
     J.rows_per_chunk = rows_per_chunk;
     J.block_begin = static_cast<int32_t>(blocks);
     J.tiles = static_cast<int32_t>(tiles);
-    J.code = stats_code(form, s.mode, s.cast);
+    J.code = stats_code(form, s.mode, s.cast, s.xf);
     blocks += nb;
   }
   return flush();
@@ -642,6 +719,46 @@ extern "C" int smx_stats_cast(const void *x, int dtype, int64_t rows, int64_t co
   const StatsInput in{x, dtype, rows, cols, row_stride, slots_sq, slots_first, n_slots,
                       slots_first ? kSqFirst : kSqOnly, out_dtype, out, out_stride};
   return stats_launch(&in, 1, static_cast<hipStream_t>(stream), "stats_cast");
+}
+
+extern "C" int smx_stats_gelu(const void *x, int dtype, int64_t rows, int64_t cols, int64_t row_stride, void *out,
+                              int64_t out_stride, float *part_sq, float *part_first, int32_t n_slots, void *stream) {
+  int rc = check_rows("stats_gelu", x, dtype, rows, cols, row_stride, part_sq, n_slots);
+  if (rc) return rc;
+  SMX_REQUIRE(dtype == SMX_BF16 || dtype == SMX_F16, SMX_EDTYPE, "stats_gelu: the input must be bf16 or f16");
+  SMX_REQUIRE(rows == 0 || out, SMX_EINVAL, "stats_gelu: null output");
+  SMX_REQUIRE(out_stride >= cols || rows <= 1, SMX_ESHAPE, "stats_gelu: out_stride must be >= cols");
+  SMX_REQUIRE(cols % 8 == 0 && row_stride % 8 == 0 && out_stride % 8 == 0 &&
+                  reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+              SMX_EALIGN, "stats_gelu: cols and row strides must be multiples of 8 elements, x and out 16-byte aligned");
+  if (rows == 0) return SMX_OK;
+  StatsInput in{x, dtype, rows, cols, row_stride, part_sq, part_first, n_slots,
+                part_first ? kSqFirstDefer : kSqDefer, 0, out, out_stride};
+  in.xf = kXfGelu;
+  return stats_launch(&in, 1, static_cast<hipStream_t>(stream), "stats_gelu");
+}
+
+// slots[i] += part[i] over n elements (the FP32 addition a statistics call
+// makes into its slot rows), for sq and, when given, first.
+__global__ void __launch_bounds__(256) stats_add_partials_kernel(float *slots_sq, const float *part_sq, float *slots_first,
+                                                                 const float *part_first, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  slots_sq[i] = slots_sq[i] + part_sq[i];
+  if (slots_first) slots_first[i] = slots_first[i] + part_first[i];
+}
+
+extern "C" int smx_stats_add_partials(float *slots_sq, const float *part_sq, float *slots_first, const float *part_first,
+                                      int64_t cols, int32_t n_rows, void *stream) {
+  SMX_REQUIRE(cols >= 1 && n_rows >= 0, SMX_ESHAPE, "stats_add_partials: need cols >= 1 and n_rows >= 0");
+  SMX_REQUIRE(n_rows == 0 || (slots_sq && part_sq), SMX_EINVAL, "stats_add_partials: null slots_sq or part_sq");
+  SMX_REQUIRE((slots_first == nullptr) == (part_first == nullptr), SMX_EINVAL,
+              "stats_add_partials: slots_first and part_first must both be set or both NULL");
+  const int64_t n = cols * n_rows;
+  if (n == 0) return SMX_OK;
+  hipLaunchKernelGGL(stats_add_partials_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), slots_sq, part_sq, slots_first, part_first, n);
+  return check_launch("stats_add_partials");
 }
 
 extern "C" int64_t smx_stats_colsum_workspace_bytes(int64_t cols, int32_t n_slots) {

@@ -21,14 +21,24 @@ backward reduces the output cotangent over its rows for the bias gradient.
   dW = delta^T x are the matrix products torch's own backward of the layer
   runs (``mm_mat1_backward`` / ``mm_mat2_backward``).
 
+* activation, with the model passed to ``fuse_statistics``: an exact
+  ``F.gelu`` of a bf16/f16 tensor in the model's forward runs as one kernel
+  (``smx_stats_gelu``) that writes the GELU and takes the A statistic of its
+  output into per-chunk partials; the Linear that then receives that very
+  output adds the partials into its slot rows (``smx_stats_add_partials``)
+  instead of reading its input again.  The GELU is torch's formula in FP32
+  rounded to the input dtype, so its output equals ``F.gelu``'s bit for bit
+  (checked over every bf16 and f16 value); its backward is torch's
+  ``gelu_backward``.
+
 The statistics are the hooks' bit for bit (the same slot rows, the same
 summation order).  Two things differ from an unfused nn.Linear: the bias
 gradient is the FP32 column sum (FP32 chunk sums folded in FP64) where torch
 sums in the low precision and rounds to it, and the layer does not support
 double backward.  What the fused passes do not cover keeps its separate
-read: the A statistic of a bf16 input (there is no cast to fuse into) and
-the B statistic of a layer without a bias.  Modules other than plain
-``nn.Linear`` keep the hooks.
+read: the A statistic of a bf16 input that no fused GELU produced (the
+attention output of the GPT here) and the B statistic of a layer without a
+bias.  Modules other than plain ``nn.Linear`` keep the hooks.
 """
 from __future__ import annotations
 
@@ -40,6 +50,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 from torch.autograd.function import once_differentiable
+from torch.overrides import TorchFunctionMode
 
 from . import _native
 from .optimizer import _rows2d
@@ -116,7 +127,17 @@ class _FusedLinear(torch.autograd.Function):
                     site.cast_cache = (weakref.ref(x), x._version, x_lp, site.n_sharers)
         else:
             if site.capture_a:
-                opt._accumulate_a(p, x, state)
+                fused = opt._fused
+                entry = fused.take_gelu_output(x) if fused is not None else None
+                if entry is not None:
+                    part_sq, part_first, rows = entry
+                    sq, fs = opt._a_slots(p, part_sq.shape[1], x.device, state)
+                    opt._stats_barrier(sq)
+                    _native.stats_add_partials(sq, part_sq, fs, part_first)
+                    opt._note_slots(sq, rows)
+                    state["a_count"] += rows
+                else:
+                    opt._accumulate_a(p, x, state)
             x_lp = x if lp is None or x.dtype == lp else x.to(lp)
         w = weight if lp is None else weight.to(lp)
         b = None if bias is None else (bias if lp is None else bias.to(lp))
@@ -160,6 +181,48 @@ class _FusedLinear(torch.autograd.Function):
         return grad_x, grad_w, grad_b, None
 
 
+class _FusedGelu(torch.autograd.Function):
+    """F.gelu (exact) of a bf16/f16 tensor with the A statistic of its output
+    taken in the same pass, into per-chunk partials kept in `holder`."""
+
+    @staticmethod
+    def forward(ctx, h, optimizer, holder: list):
+        rows = _rows2d(h)
+        out = torch.empty(h.shape, dtype=h.dtype, device=h.device)
+        n_slots = optimizer.STAT_SLOTS
+        chunks = _native.stats_slot_rows(rows.shape[0], n_slots)
+        part_sq = torch.empty(chunks, rows.shape[1], dtype=torch.float32, device=h.device)
+        part_first = torch.empty_like(part_sq) if optimizer.rank_one_a else None
+        _native.stats_gelu(rows, out.view(rows.shape), part_sq, part_first, n_slots)
+        holder.extend([part_sq, part_first, rows.shape[0]])
+        ctx.save_for_backward(h)
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_y):
+        (h,) = ctx.saved_tensors
+        return torch.ops.aten.gelu_backward(grad_y, h, approximate="none"), None, None
+
+
+class _GeluStatistics(TorchFunctionMode):
+    """Active during the forward of the model given to ``fuse_statistics``:
+    runs each eligible ``F.gelu`` as ``_FusedGelu`` (other calls, and every
+    other function, pass through)."""
+
+    def __init__(self, fused: "FusedStatistics"):
+        super().__init__()
+        self.fused = fused
+
+    def __torch_function__(self, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        if func is F.gelu:
+            y = self.fused._gelu(args, kwargs)
+            if y is not None:
+                return y
+        return func(*args, **kwargs)
+
+
 def _fused_forward(site: _Site):
     def forward(module: nn.Linear, x: torch.Tensor) -> torch.Tensor:
         # The reference hook's gate (sandmuon/optimizer.py:153-155): training
@@ -175,9 +238,21 @@ def _fused_forward(site: _Site):
 class FusedStatistics:
     """Handle returned by ``fuse_statistics``; ``close()`` restores the hooks."""
 
-    def __init__(self, optimizer):
+    def __init__(self, optimizer, model: Optional[nn.Module] = None):
         self.optimizer = optimizer
         self.sites: Dict[str, _Site] = {}
+        # Fused GELU outputs of the running forward: id -> (weak reference,
+        # version, partials of sq, of first, rows); taken by the Linear that
+        # receives one, dropped when the forward ends.
+        self._gelu_outputs: Dict[int, tuple] = {}
+        self.gelu_calls = 0       # GELUs run fused
+        self.gelu_taken = 0       # of those, outputs whose statistic a Linear took
+        self._mode: Optional[_GeluStatistics] = None
+        self._depth = 0
+        self._model_handles = []
+        if model is not None:
+            self._model_handles = [model.register_forward_pre_hook(self._enter),
+                                   model.register_forward_hook(self._leave, always_call=True)]
         for name, module in optimizer._matrix_modules.items():
             if type(module) is not nn.Linear or "forward" in module.__dict__:
                 continue  # keeps its hooks
@@ -199,7 +274,52 @@ class FusedStatistics:
     def fused_names(self):
         return list(self.sites)
 
+    # ------------------------------------------------------ activations ---
+    def _enter(self, module, inputs):
+        if self._depth == 0:
+            self._mode = _GeluStatistics(self)
+            self._mode.__enter__()
+        self._depth += 1
+
+    def _leave(self, module, inputs, output):
+        self._depth -= 1
+        if self._depth == 0:
+            mode, self._mode = self._mode, None
+            mode.__exit__(None, None, None)
+            self._gelu_outputs.clear()
+
+    def _gelu(self, args, kwargs):
+        """The fused GELU of an eligible call, else None."""
+        h = args[0] if args else kwargs.get("input")
+        approximate = args[1] if len(args) > 1 else kwargs.get("approximate", "none")
+        if (approximate != "none" or not isinstance(h, torch.Tensor) or h.device.type != "cuda" or
+                h.dtype not in (torch.bfloat16, torch.float16) or h.dim() < 2 or h.numel() == 0 or
+                h.shape[-1] % 8 != 0 or not torch.is_grad_enabled() or not self.sites):
+            return None
+        holder: list = []
+        y = _FusedGelu.apply(h, self.optimizer, holder)
+        self._gelu_outputs[id(y)] = (weakref.ref(y), y._version, *holder)
+        self.gelu_calls += 1
+        return y
+
+    def take_gelu_output(self, x: torch.Tensor):
+        """(partials of sq, of first, rows) if x is an unmodified fused GELU
+        output of the running forward (removed from the registry), else None."""
+        entry = self._gelu_outputs.get(id(x))
+        if entry is None or entry[0]() is not x or entry[1] != x._version:
+            return None
+        del self._gelu_outputs[id(x)]
+        self.gelu_taken += 1
+        return entry[2], entry[3], entry[4]
+
     def close(self) -> None:
+        for h in self._model_handles:
+            h.remove()
+        self._model_handles = []
+        if self._mode is not None:
+            self._mode.__exit__(None, None, None)
+            self._mode, self._depth = None, 0
+        self._gelu_outputs.clear()
         opt = self.optimizer
         for name, site in self.sites.items():
             site.cast_cache = None
@@ -212,12 +332,14 @@ class FusedStatistics:
             opt._fused = None
 
 
-def fuse_statistics(optimizer) -> FusedStatistics:
+def fuse_statistics(optimizer, model: Optional[nn.Module] = None) -> FusedStatistics:
     """Fuse the hook statistics of every selected plain ``nn.Linear`` into
-    the layer's own input cast and bias-gradient passes.  Returns the handle
-    (the existing one if the optimizer is already fused)."""
+    the layer's own input cast and bias-gradient passes, and, when the model
+    is given, the A statistic of a GELU's output into the GELU (during
+    ``model``'s forward).  Returns the handle (the existing one if the
+    optimizer is already fused)."""
     if optimizer._fused is not None:
         return optimizer._fused
     if not optimizer.handles and optimizer._hook_handles == {}:
         raise RuntimeError("fuse_statistics: the optimizer is closed")
-    return FusedStatistics(optimizer)
+    return FusedStatistics(optimizer, model)

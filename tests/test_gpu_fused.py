@@ -8,8 +8,11 @@
 * a fused nn.Linear under bf16 autocast gives torch's output, input gradient
   and weight gradient bit for bit, and the bias gradient within the bf16
   rounding torch's own bias gradient carries;
-* a GPT step with fused statistics gives the hook path's statistics and
-  matrix updates bit for bit.
+* smx_stats_gelu: the GELU equals torch's F.gelu bit for bit over every
+  bf16 and f16 value, and its partials, added into slot rows, equal the
+  slot rows smx_stats_accumulate leaves for its output bit for bit;
+* a GPT step with fused statistics (with and without the GELU fused) gives
+  the hook path's statistics and matrix updates bit for bit.
 """
 import copy
 
@@ -53,6 +56,54 @@ def test_stats_cast_matches_torch_cast_and_hook_slots(device, rows, cols, out_dt
     assert torch.equal(sq, ref_sq)
     if first:
         assert torch.equal(fs, ref_fs)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_stats_gelu_equals_torch_gelu_on_every_value(device, dtype):
+    h = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(dtype).reshape(256, 256).to(device)
+    out = torch.empty_like(h)
+    chunks = _native.stats_slot_rows(256, SLOTS)
+    part = torch.empty(chunks, 256, device=device)
+    _native.stats_gelu(h, out, part, None, SLOTS)
+    want = torch.nn.functional.gelu(h)
+    torch.cuda.synchronize()
+    nan = torch.isnan(want)
+    assert torch.equal(torch.isnan(out), nan)
+    assert torch.equal(out[~nan].view(torch.int16), want[~nan].view(torch.int16))
+
+
+@pytest.mark.parametrize("rows,cols", [(16384, 3072), (16384 * 3 + 5, 768), (513, 8), (1, 16), (3, 1024)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("first", [True, False])
+def test_stats_gelu_partials_equal_hook_slots_of_its_output(device, rows, cols, dtype, first):
+    g = torch.Generator(device=device).manual_seed(rows + 3 * cols)
+    h = (torch.randn(rows, cols, generator=g, device=device) * 2).to(dtype)
+    # slot rows that already hold sums of earlier calls
+    base_sq = torch.rand(SLOTS, cols, generator=g, device=device)
+    base_fs = torch.randn(SLOTS, cols, generator=g, device=device) if first else None
+    ref_sq = base_sq.clone()
+    ref_fs = base_fs.clone() if first else None
+    _native.stats_accumulate(torch.nn.functional.gelu(h), ref_sq, ref_fs)
+    out = torch.empty_like(h)
+    chunks = _native.stats_slot_rows(rows, SLOTS)
+    part_sq = torch.empty(chunks, cols, device=device)
+    part_fs = torch.empty(chunks, cols, device=device) if first else None
+    _native.stats_gelu(h, out, part_sq, part_fs, SLOTS)
+    sq, fs = base_sq.clone(), base_fs.clone() if first else None
+    _native.stats_add_partials(sq, part_sq, fs, part_fs)
+    torch.cuda.synchronize()
+    # equal values: torch's own small-tensor path can give +0 where its
+    # vectorised path (and this kernel) give -0 for an underflowing negative
+    assert torch.equal(out, torch.nn.functional.gelu(h))
+    assert torch.equal(sq, ref_sq)
+    if first:
+        assert torch.equal(fs, ref_fs)
+
+
+def test_stats_gelu_refuses_unaligned_widths(device):
+    h = torch.randn(4, 12, device=device).to(torch.bfloat16)
+    with pytest.raises(ValueError, match="multiples of 8"):
+        _native.stats_gelu(h, torch.empty_like(h), torch.empty(1, 12, device=device), None, SLOTS)
 
 
 def test_stats_cast_strided_rows(device):
@@ -187,10 +238,11 @@ def _gpt_pair(device, cfg, seed, opt_cls):
 
 @pytest.mark.parametrize("opt_cls,amp", [(RankOneAWeightedPE, torch.bfloat16), (DiagonalWeightedPE, torch.bfloat16),
                                          (RankOneAWeightedPE, torch.float16)])
-def test_fused_gpt_step_equals_hook_step(device, opt_cls, amp):
+@pytest.mark.parametrize("gelu", [False, True], ids=["linears", "linears_and_gelu"])
+def test_fused_gpt_step_equals_hook_step(device, opt_cls, amp, gelu):
     cfg = GPTConfig(vocab=257, ctx=128, layers=2, width=256, heads=4, mlp=1024)
     model, twin, hooked, fused_opt = _gpt_pair(device, cfg, 11, opt_cls)
-    handle = fuse_statistics(fused_opt)
+    handle = fuse_statistics(fused_opt, twin if gelu else None)
     assert len(handle.fused_names) == 12 and fused_opt.handles == []
     g = torch.Generator().manual_seed(12)
     gm, gt = dict(model.named_parameters()), dict(twin.named_parameters())
@@ -221,6 +273,9 @@ def test_fused_gpt_step_equals_hook_step(device, opt_cls, amp):
                 loss.backward()
         for n in hooked.named_matrices:
             assert torch.equal(gm[n].grad, gt[n].grad), n
+        # every MLP's GELU ran fused and its output's statistic was taken by
+        # the MLP's c_proj
+        assert handle.gelu_calls == handle.gelu_taken == (3 * cfg.layers * (step + 1) if gelu else 0)
         # Linear biases: the fused gradient is the FP32 column sum of the
         # captured cotangents, torch's the bf16-rounded one.  Both are held
         # against the FP64 sum: the fused one within FP32 rounding of the
