@@ -118,7 +118,7 @@ int smx_stats_cast(const void *x, int dtype, int64_t rows, int64_t cols,
 /* smx_stats_gelu: out = GELU(x) (the exact form, x * 0.5 * (1 + erf(x /
  * sqrt(2))) in FP32, rounded to the input dtype) with the A statistic of
  * sandmuon/optimizer.py:156-168 of the output taken in the same pass, for
- * the Linear the GELU feeds (no reference entry point; row 8f.1).  The
+ * the Linear the GELU feeds (no reference entry point).  The
  * statistic goes to per-chunk partials, not to slot rows: part_sq (and
  * part_first, or NULL) receive smx_stats_slot_rows(rows, n_slots) rows of
  * cols FP32 sums, which smx_stats_add_partials later adds into the Linear's
