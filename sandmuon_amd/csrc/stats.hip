@@ -55,17 +55,26 @@ __device__ __forceinline__ float gelu_erf(float x) {
 // Element access of one lane's VEC consecutive channels: `raw` loads their
 // bits (16 bytes for the vector forms, one element otherwise) and `cvt`
 // widens them to FP32.  Keeping the raw bits in registers until they are
-// consumed lets the next batch of loads be issued first.
+// consumed lets the next batch of loads be issued first.  The loads are
+// non-temporal (the `nt` cache policy): every input byte is read once, and
+// a streaming read of HBM runs 13-15% faster with that hint on this part
+// (7.0-7.2 against 6.1-6.4 TB/s over 1-4 GiB).
 template <int DT, int VEC>
 struct Elems {
   using Raw = std::conditional_t<VEC == 1, uint32_t, uint4>;
   static constexpr int kSize = DT == SMX_F32 ? 4 : 2;
   static_assert(VEC == 1 || VEC * kSize == 16, "vector forms load 16 bytes");
   __device__ __forceinline__ static Raw raw(const void *p, int64_t i) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const char *b = static_cast<const char *>(p) + i * kSize;
-    if constexpr (VEC > 1) return *reinterpret_cast<const uint4 *>(b);
-    else if constexpr (kSize == 4) return *reinterpret_cast<const uint32_t *>(b);
-    else return *reinterpret_cast<const uint16_t *>(b);
+    if constexpr (VEC > 1) {
+      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(b));
+      return make_uint4(v.x, v.y, v.z, v.w);
+    } else if constexpr (kSize == 4) {
+      return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(b));
+    } else {
+      return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(b));
+    }
   }
   __device__ __forceinline__ static float one(uint32_t w) {
     if constexpr (DT == SMX_F32) return __uint_as_float(w);
@@ -219,9 +228,15 @@ __device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int6
       }
       if constexpr (CAST != 0) store_cast<CAST, VEC>(J.cast_out, row * J.out_stride + col0, v);
     };
+    // The scheduling barriers keep the batches in issue order: without them
+    // the compiler starts consuming the newest batch before issuing the
+    // next one, so each iteration waits for every load (vmcnt(0)) and a
+    // wave's loads run dry.
     auto eat = [&](const Raw (&q)[U], int64_t rq) {
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < U; ++u) eat1(q[u], rq + u * GROUPS);
+      __builtin_amdgcn_sched_barrier(0);
     };
     const int64_t n_rows = r < r_end ? (r_end - r + GROUPS - 1) / GROUPS : 0;
     const int64_t nb = n_rows / U;
