@@ -144,7 +144,9 @@ struct StatsJob {
   int64_t rows, cols, row_stride, out_stride, rows_per_chunk;
   int32_t block_begin, tiles, code, pad_;
 };
-constexpr int kStatsJobs = 24;  // jobs per launch, passed by value
+// Jobs per launch, passed by value: 44 takes a 1 GiB queue of 25 MB hook
+// inputs (768-wide bf16, 16384 rows) in one launch.
+constexpr int kStatsJobs = 44;
 struct StatsPack {
   StatsJob job[kStatsJobs];
   int32_t n;
@@ -348,7 +350,9 @@ __device__ __forceinline__ int stats_job_of(const StatsPack &pack, int b) {
 __global__ void __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(6))) stats_accumulate_kernel(StatsPack pack) {
   __shared__ float red[2 * kStatsWaves * kStatsMaxTW];
   const int b = static_cast<int>(blockIdx.x);
-  const StatsJob &J = pack.job[stats_job_of(pack, b)];
+  // A copy of the block's job (scalar registers): a reference into the pack
+  // makes the compiler copy the whole pack to scratch memory.
+  const StatsJob J = pack.job[stats_job_of(pack, b)];
   const int64_t local = b - J.block_begin;
   const int64_t tile = local % J.tiles, chunk = local / J.tiles;
 #define SMX_STATS_CASE(FORM, MODE, CAST) \
@@ -383,7 +387,9 @@ __global__ void __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per
 __global__ void __launch_bounds__(kStatsThreads) stats_gelu_kernel(StatsPack pack) {
   __shared__ float red[2 * kStatsWaves * kStatsMaxTW];
   const int b = static_cast<int>(blockIdx.x);
-  const StatsJob &J = pack.job[stats_job_of(pack, b)];
+  // A copy of the block's job (scalar registers): a reference into the pack
+  // makes the compiler copy the whole pack to scratch memory.
+  const StatsJob J = pack.job[stats_job_of(pack, b)];
   const int64_t local = b - J.block_begin;
   const int64_t tile = local % J.tiles, chunk = local / J.tiles;
 #define SMX_STATS_GELU(FORM)                                                                   \
