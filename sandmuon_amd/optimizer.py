@@ -227,17 +227,34 @@ class _StatsQueue:
     queue adds exactly what one launch per hook call would, in the same
     order per slot row.  The queue keeps its tensors alive until the launch
     is enqueued on the stream current at the first hook call.
+
+    The launch threshold ramps up after each step: the first launch takes
+    `first` bytes and each later one `growth` times more, up to `limit`.
+    Python queues hook inputs faster than the GPU reads them, so a phase of
+    hooks with nothing else on the GPU starts reading at once instead of
+    after a full batch is queued, and the batches still reach the full size.
     """
 
-    __slots__ = ("limit", "entries", "slot_ptrs", "nbytes", "stream", "device")
+    __slots__ = ("limit", "first", "growth", "threshold", "entries", "slot_ptrs", "nbytes", "stream", "device")
 
-    def __init__(self, limit: int):
+    def __init__(self, limit: int, first: int = 64 << 20, growth: float = 1.6):
         self.limit = int(limit)
+        self.first = int(first)
+        self.growth = float(growth)
+        self.threshold = min(self.limit, self.first)
         self.entries: List[Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor], int]] = []
         self.slot_ptrs = set()
         self.nbytes = 0
         self.stream = None
         self.device = None
+
+    def grow(self) -> None:
+        """The next launch threshold, after a launch."""
+        self.threshold = min(self.limit, int(self.threshold * self.growth))
+
+    def restart(self) -> None:
+        """Back to the first threshold (the statistics were consumed)."""
+        self.threshold = min(self.limit, self.first)
 
     def clear(self) -> None:
         self.entries = []
@@ -397,7 +414,7 @@ class DiagonalWeightedPE(Optimizer):
         q.entries.append((rows, sq, fs, rows._version))
         q.slot_ptrs.add(sq.data_ptr())
         q.nbytes += rows.numel() * rows.element_size()
-        if q.nbytes >= q.limit:
+        if q.nbytes >= q.threshold:
             self._flush_stats()
 
     def _stats_barrier(self, sq: torch.Tensor) -> None:
@@ -415,6 +432,7 @@ class DiagonalWeightedPE(Optimizer):
             return
         entries, stream, device = q.entries, q.stream, q.device
         q.clear()
+        q.grow()
         for rows, _, _, version in entries:
             if rows._version != version:
                 raise RuntimeError(
@@ -510,6 +528,7 @@ class DiagonalWeightedPE(Optimizer):
     def step(self, closure=None):
         loss = self._run_closure(closure)
         self._flush_stats()
+        self._queue.restart()
         matrix_items, auxiliary_items = [], []
         a_counts: Dict[int, int] = {}
         for group in self.param_groups:

@@ -60,6 +60,26 @@ def test_queue_launches_once_it_holds_the_limit(monkeypatch):
     assert len(rec.batches) == 2
 
 
+def test_launch_threshold_ramps_up_and_restarts(monkeypatch):
+    rec = Recorder()
+    rec.install(monkeypatch)
+    opt = object.__new__(DiagonalWeightedPE)
+    opt._queue = _StatsQueue(4000, first=800, growth=2.0)   # thresholds 800, 1600, 3200, 4000, 4000
+    opt._slot_rows = {}
+    x_bytes = 25 * 8 * 4                                     # 800 bytes per input
+    sizes = []
+    for k in range(17):                                      # 13600 bytes: exactly five launches
+        opt._enqueue_stats(rows(25), torch.zeros(4, 8), None)
+        if len(rec.batches) > len(sizes):
+            sizes.append(len(rec.batches[-1]) * x_bytes)
+    assert sizes == [800, 1600, 3200, 4000, 4000][:len(sizes)] and len(sizes) == 5
+    assert opt._queue.threshold == 4000
+    opt._flush_stats()
+    opt._queue.restart()                                     # what step() does after its flush
+    assert opt._queue.threshold == 800
+    assert _StatsQueue(100).threshold == 100                 # a limit below the first batch is the threshold
+
+
 def test_same_slot_rows_or_another_stream_launch_the_queue_first(monkeypatch):
     rec = Recorder()
     rec.install(monkeypatch)
