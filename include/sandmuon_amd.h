@@ -131,9 +131,30 @@ int smx_stats_gelu(const void *x, int dtype, int64_t rows, int64_t cols,
                    float *part_sq, float *part_first, int32_t n_slots,
                    void *stream);
 
+/* smx_stats_relayout: the row-major copy out[b*seq + t][h*head_dim + d] =
+ * x[b, t, h, d] of a [batch, seq, heads, head_dim] view with strides
+ * (batch_stride, seq_stride, head_stride, 1) (an attention output handed
+ * back from [batch, heads, seq, head_dim] to the Linear that projects it),
+ * with the A statistic of sandmuon/optimizer.py:156-168 of the copy taken
+ * in the same pass, for that Linear (no reference entry point).  The
+ * statistic goes to per-chunk partials as for smx_stats_gelu
+ * (smx_stats_slot_rows(batch*seq, n_slots) rows of heads*head_dim FP32
+ * sums; part_first may be NULL), equal bit for bit to what a
+ * smx_stats_accumulate of out would add.  x and out are bf16 or f16 (out
+ * in x's dtype, contiguous); head_dim and the strides are multiples of 8
+ * elements, x and out 16-byte aligned (SMX_EALIGN otherwise); seq must be a
+ * multiple of the statistic's row chunk, max(ceil(batch*seq / n_slots),
+ * 512) rows, so that no chunk crosses a sequence (SMX_ESHAPE otherwise). */
+int smx_stats_relayout(const void *x, int dtype, int64_t batch, int64_t seq,
+                       int64_t heads, int64_t head_dim, int64_t batch_stride,
+                       int64_t seq_stride, int64_t head_stride, void *out,
+                       float *part_sq, float *part_first, int32_t n_slots,
+                       void *stream);
+
 /* slots[p*cols + c] += part[p*cols + c] for p < n_rows (FP32), for sq and,
  * when both are given, first: the addition a statistics call makes into its
- * slot rows, applied to the partials of smx_stats_gelu. */
+ * slot rows, applied to the partials of smx_stats_gelu and
+ * smx_stats_relayout. */
 int smx_stats_add_partials(float *slots_sq, const float *part_sq,
                            float *slots_first, const float *part_first,
                            int64_t cols, int32_t n_rows, void *stream);

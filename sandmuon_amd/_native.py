@@ -74,6 +74,8 @@ SIGNATURES = {
                                c_void_p, c_int, c_int64, c_void_p]),
     "smx_stats_gelu": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
                                c_int32, c_void_p]),
+    "smx_stats_relayout": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                   c_void_p, c_void_p, c_void_p, c_int32, c_void_p]),
     "smx_stats_add_partials": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
     "smx_stats_colsum_workspace_bytes": (c_int64, [c_int64, c_int32]),
     "smx_stats_colsum": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_int32, c_void_p,
@@ -247,6 +249,20 @@ def stats_gelu(rows2d: torch.Tensor, out2d: torch.Tensor, part_sq: torch.Tensor,
                               rows2d.stride(0), out2d.data_ptr(), out2d.stride(0), part_sq.data_ptr(),
                               ptr(part_first), n_slots, stream_of(rows2d.device))
     _check(rc, "smx_stats_gelu")
+
+
+def stats_relayout(x4: torch.Tensor, out: torch.Tensor, part_sq: torch.Tensor, part_first: Optional[torch.Tensor],
+                   n_slots: int) -> None:
+    """out (contiguous, x4's numel) = the row-major copy of the [batch, seq,
+    heads, head_dim] view x4 (unit last stride), with the per-chunk partials
+    of out's statistic in part_sq / part_first ([chunks, heads*head_dim])."""
+    b, t, h, d = x4.shape
+    sb, st, sh, sd = x4.stride()
+    if sd != 1 and d > 1:
+        raise ValueError("stats_relayout: the last dimension must have unit stride")
+    rc = lib().smx_stats_relayout(x4.data_ptr(), dtype_code(x4.dtype), b, t, h, d, sb, st, sh, out.data_ptr(),
+                                  part_sq.data_ptr(), ptr(part_first), n_slots, stream_of(x4.device))
+    _check(rc, "smx_stats_relayout")
 
 
 def stats_add_partials(slots_sq: torch.Tensor, part_sq: torch.Tensor, slots_first: Optional[torch.Tensor],

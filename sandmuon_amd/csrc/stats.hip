@@ -40,10 +40,22 @@ enum StatsMode : int {
 };
 constexpr int kStatsModes = 5;
 
-// Elementwise transform of the input before the statistic (XF): none, or
-// the exact GELU of the input, rounded to the input dtype and stored in
-// cast_out; the statistic is that of the stored (rounded) values.
-enum StatsXform : int { kXfNone = 0, kXfGelu = 1 };
+// Elementwise transform of the input before the statistic (XF): none; the
+// exact GELU of the input, rounded to the input dtype and stored in
+// cast_out (the statistic is that of the stored, rounded values); or a copy
+// of the input into cast_out (a relayout: the input is read through an
+// InMap, the copy is row-major).
+enum StatsXform : int { kXfNone = 0, kXfGelu = 1, kXfCopy = 2 };
+constexpr int kStatsXforms = 3;
+
+// Where input element (row, col) of a job lives, relative to J.x:
+// (row - row0) * J.row_stride + col(col).  A row-major input has row0 = 0
+// and col(c) = c; a relayout input holds its columns as heads of hd
+// channels, hs elements apart (col(c) = (c / hd) * hs + c % hd).
+struct InMap {
+  int64_t row0 = 0, hd = 0, hs = 0;
+  __device__ __forceinline__ int64_t col(int64_t c) const { return hd ? (c / hd) * hs + c % hd : c; }
+};
 
 // torch's exact GELU in FP32 (x * 0.5 * (1 + erf(x / sqrt(2))), evaluated
 // left to right), without contraction.
@@ -166,12 +178,14 @@ static_assert(sizeof(StatsPack) <= 4000, "StatsPack is passed by value in the ke
 // variant adds the same bits to the slots; with XF the statistic is that of
 // the transformed values a later read of the output would load.
 template <int DT, int VEC, int CT, int U, int MODE, int CAST, int XF>
-__device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int64_t chunk, float *red) {
+__device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int64_t chunk, float *red,
+                                           const InMap &m = InMap{}) {
   using E = Elems<DT, VEC>;
   using Raw = typename E::Raw;
   constexpr bool FIRST = MODE != kSqOnly && MODE != kSqDefer;
   constexpr bool DEFER = MODE == kSqDefer || MODE == kSqFirstDefer;
-  static_assert(XF == kXfNone || (CAST == 0 && DT != SMX_F32 && DEFER), "the GELU form: 16-bit input, deferred");
+  static_assert(XF == kXfNone || (CAST == 0 && DT != SMX_F32 && DEFER && VEC == 8),
+                "the GELU and copy forms: 16-bit vector input, deferred");
   constexpr int RPW = 64 / CT;
   constexpr int GROUPS = kStatsWaves * RPW;
   constexpr int TW = CT * VEC;
@@ -201,13 +215,18 @@ __device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int6
 
   if (!empty && col0 < J.cols) {
     int64_t r = r_begin + group;
+    const int64_t colx = m.col(col0);  // the input offset of the lane's channels
     auto issue = [&](Raw (&q)[U], int64_t &rq) {
       rq = r;
 #pragma unroll
-      for (int u = 0; u < U; ++u) q[u] = E::raw(J.x, (r + u * GROUPS) * J.row_stride + col0);
+      for (int u = 0; u < U; ++u) q[u] = E::raw(J.x, (r + u * GROUPS - m.row0) * J.row_stride + colx);
       r += U * GROUPS;
     };
     auto eat1 = [&](const Raw &q, int64_t row) {
+      if constexpr (XF == kXfCopy) {
+        uint16_t *o = static_cast<uint16_t *>(J.cast_out) + row * J.out_stride + col0;
+        *reinterpret_cast<uint4 *>(o) = q;
+      }
       float v[VEC];
       E::cvt(q, v);
       if constexpr (XF == kXfGelu) {
@@ -261,7 +280,7 @@ __device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int6
         eat(A, ra);
       }
     }
-    for (; r < r_end; r += GROUPS) eat1(E::raw(J.x, r * J.row_stride + col0), r);
+    for (; r < r_end; r += GROUPS) eat1(E::raw(J.x, (r - m.row0) * J.row_stride + colx), r);
   }
   // Lanes l, l + CT, ... of a wave hold the same channels.
 #pragma unroll
@@ -298,7 +317,7 @@ __device__ __forceinline__ void stats_tile(const StatsJob &J, int64_t tile, int6
 // stride or address is not 16-byte aligned.
 enum StatsForm : int { kF32V4 = 0, kBf16V8, kF16V8, kF32V1, kBf16V1, kF16V1, kNumForms };
 __host__ __device__ constexpr int stats_code(int form, int mode, int cast, int xf = kXfNone) {
-  return ((form * kStatsModes + mode) * 3 + cast) * 2 + xf;
+  return ((form * kStatsModes + mode) * 3 + cast) * kStatsXforms + xf;
 }
 
 // CT: lanes across a column tile (32 for the vector forms: 128 f32 or 256
@@ -331,9 +350,10 @@ constexpr int64_t kStatsMinChunkRows = 512;
 // registers (it has a kernel of its own, so the hook kernel keeps its
 // register budget).
 template <int FORM, int MODE, int CAST, int XF>
-__device__ __forceinline__ void run_tile(const StatsJob &J, int64_t tile, int64_t chunk, float *red) {
+__device__ __forceinline__ void run_tile(const StatsJob &J, int64_t tile, int64_t chunk, float *red,
+                                         const InMap &m = InMap{}) {
   using F = FormTraits<FORM>;
-  stats_tile<F::DT, F::VEC, F::CT, XF == kXfNone ? F::U : 2, MODE, CAST, XF>(J, tile, chunk, red);
+  stats_tile<F::DT, F::VEC, F::CT, XF == kXfGelu ? 2 : F::U, MODE, CAST, XF>(J, tile, chunk, red, m);
 }
 
 // The job of block b of a launch: block_begin grows with the job index, so
@@ -407,6 +427,40 @@ __global__ void __launch_bounds__(kStatsThreads) stats_gelu_kernel(StatsPack pac
 #undef SMX_STATS_GELU
 }
 
+// A relayout job (smx_stats_relayout): a [batch, seq, heads, head_dim]
+// view with strides (sb, job.row_stride, hs, 1) copied row-major into
+// job.cast_out as [batch * seq, heads * head_dim], with the statistic of
+// the copy.  A row chunk lies inside one sequence (seq is a multiple of
+// job.rows_per_chunk), where consecutive rows are job.row_stride apart.
+struct RelayoutArgs {
+  StatsJob job;
+  int64_t seq, sb, hd, hs;
+};
+
+__global__ void __launch_bounds__(kStatsThreads) stats_relayout_kernel(RelayoutArgs a) {
+  __shared__ float red[2 * kStatsWaves * kStatsMaxTW];
+  StatsJob J = a.job;
+  const int64_t local = blockIdx.x;
+  const int64_t tile = local % J.tiles, chunk = local / J.tiles;
+  const int64_t r0 = chunk * J.rows_per_chunk;  // the chunk's first row: sequence b, position t0
+  const int64_t b = r0 / a.seq, t0 = r0 % a.seq;
+  J.x = static_cast<const char *>(J.x) + (b * a.sb + t0 * J.row_stride) * 2;  // 16-bit elements
+  const InMap m{r0, a.hd, a.hs};
+#define SMX_STATS_COPY(FORM)                                                                   \
+  case stats_code(FORM, kSqDefer, 0, kXfCopy):                                                 \
+    run_tile<FORM, kSqDefer, 0, kXfCopy>(J, tile, chunk, red, m);                              \
+    break;                                                                                     \
+  case stats_code(FORM, kSqFirstDefer, 0, kXfCopy):                                            \
+    run_tile<FORM, kSqFirstDefer, 0, kXfCopy>(J, tile, chunk, red, m);                         \
+    break;
+  switch (J.code) {
+    SMX_STATS_COPY(kBf16V8)
+    SMX_STATS_COPY(kF16V8)
+    default: break;
+  }
+#undef SMX_STATS_COPY
+}
+
 // Host side: one job per input, launched in packs of kStatsJobs.
 struct StatsInput {
   const void *x;
@@ -437,7 +491,7 @@ static int stats_launch(const StatsInput *in, int n, hipStream_t st, const char 
   int64_t blocks = 0;
   auto flush = [&]() -> int {
     if (pack.n == 0) return SMX_OK;
-    if (pack.job[0].code % 2 == kXfGelu)
+    if (pack.job[0].code % kStatsXforms == kXfGelu)
       hipLaunchKernelGGL(stats_gelu_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kStatsThreads), 0, st, pack);
     else
       hipLaunchKernelGGL(stats_accumulate_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kStatsThreads), 0, st,
@@ -455,7 +509,7 @@ static int stats_launch(const StatsInput *in, int n, hipStream_t st, const char 
     // row, so it keeps one block per slot row.
     const int64_t chunks = s.mode == kSqColsum ? s.n_slots : std::max<int64_t>(ceil_div(s.rows, rows_per_chunk), 1);
     const int64_t nb = tiles * chunks;
-    if (pack.n == kStatsJobs || blocks + nb > INT32_MAX || (pack.n > 0 && pack.job[0].code % 2 != s.xf)) {
+    if (pack.n == kStatsJobs || blocks + nb > INT32_MAX || (pack.n > 0 && pack.job[0].code % kStatsXforms != s.xf)) {
       int rc = flush();
       if (rc) return rc;
     }
@@ -757,6 +811,48 @@ extern "C" int smx_stats_gelu(const void *x, int dtype, int64_t rows, int64_t co
                 part_first ? kSqFirstDefer : kSqDefer, 0, out, out_stride};
   in.xf = kXfGelu;
   return stats_launch(&in, 1, static_cast<hipStream_t>(stream), "stats_gelu");
+}
+
+extern "C" int smx_stats_relayout(const void *x, int dtype, int64_t batch, int64_t seq, int64_t heads,
+                                  int64_t head_dim, int64_t batch_stride, int64_t seq_stride, int64_t head_stride,
+                                  void *out, float *part_sq, float *part_first, int32_t n_slots, void *stream) {
+  SMX_REQUIRE(dtype == SMX_BF16 || dtype == SMX_F16, SMX_EDTYPE, "stats_relayout: the input must be bf16 or f16");
+  SMX_REQUIRE(batch >= 1 && seq >= 1 && heads >= 1 && head_dim >= 1, SMX_ESHAPE,
+              "stats_relayout: batch, seq, heads and head_dim must be >= 1");
+  SMX_REQUIRE(x && out && part_sq, SMX_EINVAL, "stats_relayout: null input, output or partials");
+  SMX_REQUIRE(n_slots >= 1 && n_slots <= 65535, SMX_EINVAL, "stats_relayout: n_slots in [1, 65535]");
+  SMX_REQUIRE(head_dim % 8 == 0 && batch_stride % 8 == 0 && seq_stride % 8 == 0 && head_stride % 8 == 0 &&
+                  reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+              SMX_EALIGN,
+              "stats_relayout: head_dim and the strides must be multiples of 8 elements, x and out 16-byte aligned");
+  const int64_t rows = batch * seq, cols = heads * head_dim;
+  const int64_t rows_per_chunk = std::max<int64_t>(ceil_div(rows, n_slots), kStatsMinChunkRows);
+  SMX_REQUIRE(seq % rows_per_chunk == 0, SMX_ESHAPE,
+              "stats_relayout: seq must be a multiple of the row chunk (" + std::to_string(rows_per_chunk) + " rows)");
+  const int form = dtype == SMX_BF16 ? kBf16V8 : kF16V8;
+  RelayoutArgs a{};
+  StatsJob &J = a.job;
+  J.x = x;
+  J.sq = part_sq;
+  J.first = part_first;
+  J.cast_out = out;
+  J.rows = rows;
+  J.cols = cols;
+  J.row_stride = seq_stride;
+  J.out_stride = cols;
+  J.rows_per_chunk = rows_per_chunk;
+  J.block_begin = 0;
+  J.tiles = static_cast<int32_t>(ceil_div(cols, kTileChannels[form]));
+  J.code = stats_code(form, part_first ? kSqFirstDefer : kSqDefer, 0, kXfCopy);
+  a.seq = seq;
+  a.sb = batch_stride;
+  a.hd = head_dim;
+  a.hs = head_stride;
+  const int64_t blocks = static_cast<int64_t>(J.tiles) * (rows / rows_per_chunk);
+  SMX_REQUIRE(blocks < INT32_MAX, SMX_ESHAPE, "stats_relayout: too many blocks for one launch");
+  hipLaunchKernelGGL(stats_relayout_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kStatsThreads), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("stats_relayout");
 }
 
 // slots[i] += part[i] over n elements (the FP32 addition a statistics call

@@ -29,19 +29,32 @@ backward reduces the output cotangent over its rows for the bias gradient.
   instead of reading its input again.  The GELU is torch's formula in FP32
   rounded to the input dtype, so its output equals ``F.gelu``'s bit for bit
   (checked over every bf16 and f16 value); its backward is torch's
-  ``gelu_backward``.
+  ``gelu_backward``;
+* relayout, with the model passed: the copy that hands an attention output
+  from [batch, heads, seq, head_dim] back to the projection Linear
+  (``y.transpose(1, 2).reshape(b, t, c)``, or ``.contiguous()``, of a
+  bf16/f16 view) runs as one kernel (``smx_stats_relayout``) that writes the
+  row-major copy and takes the A statistic of it into per-chunk partials,
+  which the Linear receiving the copy adds into its slot rows.  The copy is
+  torch's bit for bit; its backward reshapes the gradient back.  It applies
+  when the sequence length is a multiple of the statistic's row chunk
+  (512 rows for up to 64K rows), so that no chunk crosses a sequence.  The
+  output of ``F.scaled_dot_product_attention`` on ROCm is seq-major already:
+  reshaping it is a view, with no copy to fuse into.
 
 The statistics are the hooks' bit for bit (the same slot rows, the same
 summation order).  Two things differ from an unfused nn.Linear: the bias
 gradient is the FP32 column sum (FP32 chunk sums folded in FP64) where torch
 sums in the low precision and rounds to it, and the layer does not support
 double backward.  What the fused passes do not cover keeps its separate
-read: the A statistic of a bf16 input that no fused GELU produced (the
-attention output of the GPT here) and the B statistic of a layer without a
-bias.  Modules other than plain ``nn.Linear`` keep the hooks.
+read: the A statistic of a bf16 input that no fused GELU or relayout
+produced, and the B statistic of a layer without a bias (its backward has
+no elementwise pass over the cotangent, only the two GEMMs).  Modules other
+than plain ``nn.Linear`` keep the hooks.
 """
 from __future__ import annotations
 
+import math
 import types
 import weakref
 from typing import Dict, Optional
@@ -128,7 +141,7 @@ class _FusedLinear(torch.autograd.Function):
         else:
             if site.capture_a:
                 fused = opt._fused
-                entry = fused.take_gelu_output(x) if fused is not None else None
+                entry = fused.take_output(x) if fused is not None else None
                 if entry is not None:
                     part_sq, part_first, rows = entry
                     sq, fs = opt._a_slots(p, part_sq.shape[1], x.device, state)
@@ -205,10 +218,41 @@ class _FusedGelu(torch.autograd.Function):
         return torch.ops.aten.gelu_backward(grad_y, h, approximate="none"), None, None
 
 
-class _GeluStatistics(TorchFunctionMode):
+class _FusedRelayout(torch.autograd.Function):
+    """The row-major copy of a [batch, seq, heads, head_dim] bf16/f16 view
+    (unit last stride) into `shape`, with the A statistic of the copy taken
+    in the same pass, into per-chunk partials kept in `holder`."""
+
+    @staticmethod
+    def forward(ctx, x, shape, optimizer, holder: list):
+        b, t, h, d = x.shape
+        out = torch.empty(shape, dtype=x.dtype, device=x.device)
+        n_slots = optimizer.STAT_SLOTS
+        chunks = _native.stats_slot_rows(b * t, n_slots)
+        part_sq = torch.empty(chunks, h * d, dtype=torch.float32, device=x.device)
+        part_first = torch.empty_like(part_sq) if optimizer.rank_one_a else None
+        _native.stats_relayout(x, out, part_sq, part_first, n_slots)
+        holder.extend([part_sq, part_first, b * t])
+        ctx.in_shape = x.shape
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_y):
+        return grad_y.reshape(ctx.in_shape), None, None, None
+
+
+_RESHAPES = (torch.Tensor.reshape, torch.reshape)
+# The producers whose output statistic a fused forward takes (the model
+# given to fuse_statistics): the GELU and the attention output's relayout.
+ACTIVATIONS = ("gelu", "relayout")
+
+
+class _ActivationStatistics(TorchFunctionMode):
     """Active during the forward of the model given to ``fuse_statistics``:
-    runs each eligible ``F.gelu`` as ``_FusedGelu`` (other calls, and every
-    other function, pass through)."""
+    runs each eligible ``F.gelu`` as ``_FusedGelu`` and each eligible
+    relayout copy of an attention output as ``_FusedRelayout`` (other calls,
+    and every other function, pass through)."""
 
     def __init__(self, fused: "FusedStatistics"):
         super().__init__()
@@ -216,10 +260,14 @@ class _GeluStatistics(TorchFunctionMode):
 
     def __torch_function__(self, func, types, args=(), kwargs=None):
         kwargs = kwargs or {}
-        if func is F.gelu:
-            y = self.fused._gelu(args, kwargs)
-            if y is not None:
-                return y
+        y = None
+        fused = self.fused
+        if func is F.gelu and "gelu" in fused.activations:
+            y = fused._gelu(args, kwargs)
+        elif (func in _RESHAPES or func is torch.Tensor.contiguous) and "relayout" in fused.activations:
+            y = fused._relayout(func, args, kwargs)
+        if y is not None:
+            return y
         return func(*args, **kwargs)
 
 
@@ -238,16 +286,24 @@ def _fused_forward(site: _Site):
 class FusedStatistics:
     """Handle returned by ``fuse_statistics``; ``close()`` restores the hooks."""
 
-    def __init__(self, optimizer, model: Optional[nn.Module] = None):
+    def __init__(self, optimizer, model: Optional[nn.Module] = None, activations=ACTIVATIONS):
+        unknown = set(activations) - set(ACTIVATIONS)
+        if unknown:
+            raise ValueError(f"fuse_statistics: unknown activations {sorted(unknown)}; expected a subset of "
+                             f"{ACTIVATIONS}")
         self.optimizer = optimizer
+        self.activations = frozenset(activations)
         self.sites: Dict[str, _Site] = {}
-        # Fused GELU outputs of the running forward: id -> (weak reference,
-        # version, partials of sq, of first, rows); taken by the Linear that
-        # receives one, dropped when the forward ends.
-        self._gelu_outputs: Dict[int, tuple] = {}
+        # Outputs of the running forward's fused GELUs and relayouts, by
+        # data pointer: (weak reference, version, kind, partials of sq, of
+        # first, rows); taken by the Linear that receives one (or a
+        # contiguous view of it), dropped when the forward ends.
+        self._outputs: Dict[int, tuple] = {}
         self.gelu_calls = 0       # GELUs run fused
         self.gelu_taken = 0       # of those, outputs whose statistic a Linear took
-        self._mode: Optional[_GeluStatistics] = None
+        self.relayout_calls = 0   # relayout copies run fused
+        self.relayout_taken = 0   # of those, copies whose statistic a Linear took
+        self._mode: Optional[_ActivationStatistics] = None
         self._depth = 0
         self._model_handles = []
         if model is not None:
@@ -277,7 +333,7 @@ class FusedStatistics:
     # ------------------------------------------------------ activations ---
     def _enter(self, module, inputs):
         if self._depth == 0:
-            self._mode = _GeluStatistics(self)
+            self._mode = _ActivationStatistics(self)
             self._mode.__enter__()
         self._depth += 1
 
@@ -286,7 +342,7 @@ class FusedStatistics:
         if self._depth == 0:
             mode, self._mode = self._mode, None
             mode.__exit__(None, None, None)
-            self._gelu_outputs.clear()
+            self._outputs.clear()
 
     def _gelu(self, args, kwargs):
         """The fused GELU of an eligible call, else None."""
@@ -298,19 +354,70 @@ class FusedStatistics:
             return None
         holder: list = []
         y = _FusedGelu.apply(h, self.optimizer, holder)
-        self._gelu_outputs[id(y)] = (weakref.ref(y), y._version, *holder)
+        self._register(y, "gelu", holder)
         self.gelu_calls += 1
         return y
 
-    def take_gelu_output(self, x: torch.Tensor):
-        """(partials of sq, of first, rows) if x is an unmodified fused GELU
-        output of the running forward (removed from the registry), else None."""
-        entry = self._gelu_outputs.get(id(x))
-        if entry is None or entry[0]() is not x or entry[1] != x._version:
+    def _relayout(self, func, args, kwargs):
+        """The fused relayout of an eligible reshape / contiguous call, else None."""
+        x = args[0] if args else kwargs.get("input")
+        if (not isinstance(x, torch.Tensor) or x.dim() != 4 or x.device.type != "cuda" or
+                x.dtype not in (torch.bfloat16, torch.float16) or x.is_contiguous() or x.stride(-1) != 1 or
+                not torch.is_grad_enabled() or not self.sites):
             return None
-        del self._gelu_outputs[id(x)]
-        self.gelu_taken += 1
-        return entry[2], entry[3], entry[4]
+        b, t, h, d = x.shape
+        if func is torch.Tensor.contiguous:
+            fmt = args[1] if len(args) > 1 else kwargs.get("memory_format", torch.contiguous_format)
+            if fmt is not torch.contiguous_format:
+                return None
+            shape = (b, t, h, d)
+        else:
+            dims = args[1:] if func is torch.Tensor.reshape else args[1:2]
+            if not dims:
+                dims = (kwargs.get("shape"),)
+            if len(dims) == 1 and isinstance(dims[0], (tuple, list, torch.Size)):
+                dims = tuple(dims[0])
+            if not dims or not all(isinstance(n, int) for n in dims):
+                return None
+            shape = tuple(dims)
+            if shape.count(-1) == 1:
+                known = math.prod(n for n in shape if n != -1)
+                if known <= 0 or x.numel() % known:
+                    return None
+                shape = tuple(x.numel() // known if n == -1 else n for n in shape)
+            if shape not in ((b, t, h * d), (b * t, h * d)):
+                return None
+        rows = b * t
+        chunk = max(-(-rows // self.optimizer.STAT_SLOTS), 512)
+        if (d % 8 or t % chunk or any(st % 8 for st in x.stride()[:3]) or x.data_ptr() % 16 or
+                x.numel() == 0):
+            return None
+        holder: list = []
+        y = _FusedRelayout.apply(x, shape, self.optimizer, holder)
+        self._register(y, "relayout", holder)
+        self.relayout_calls += 1
+        return y
+
+    def _register(self, y: torch.Tensor, kind: str, holder: list) -> None:
+        self._outputs[y.data_ptr()] = (weakref.ref(y), y._version, kind, *holder)
+
+    def take_output(self, x: torch.Tensor):
+        """(partials of sq, of first, rows) if x is an unmodified fused GELU or
+        relayout output of the running forward, or a contiguous view of all
+        of one (removed from the registry), else None."""
+        entry = self._outputs.get(x.data_ptr())
+        if entry is None:
+            return None
+        y = entry[0]()
+        if (y is None or entry[1] != x._version or x.numel() != y.numel() or not x.is_contiguous() or
+                x.shape[-1] != entry[3].shape[1]):
+            return None
+        del self._outputs[x.data_ptr()]
+        if entry[2] == "gelu":
+            self.gelu_taken += 1
+        else:
+            self.relayout_taken += 1
+        return entry[3], entry[4], entry[5]
 
     def close(self) -> None:
         for h in self._model_handles:
@@ -319,7 +426,7 @@ class FusedStatistics:
         if self._mode is not None:
             self._mode.__exit__(None, None, None)
             self._mode, self._depth = None, 0
-        self._gelu_outputs.clear()
+        self._outputs.clear()
         opt = self.optimizer
         for name, site in self.sites.items():
             site.cast_cache = None
@@ -332,14 +439,15 @@ class FusedStatistics:
             opt._fused = None
 
 
-def fuse_statistics(optimizer, model: Optional[nn.Module] = None) -> FusedStatistics:
+def fuse_statistics(optimizer, model: Optional[nn.Module] = None, activations=ACTIVATIONS) -> FusedStatistics:
     """Fuse the hook statistics of every selected plain ``nn.Linear`` into
     the layer's own input cast and bias-gradient passes, and, when the model
-    is given, the A statistic of a GELU's output into the GELU (during
-    ``model``'s forward).  Returns the handle (the existing one if the
-    optimizer is already fused)."""
+    is given, the A statistic of a GELU's output into the GELU and that of
+    an attention output into its relayout copy (during ``model``'s forward;
+    ``activations`` names which of the two).  Returns the handle (the
+    existing one if the optimizer is already fused)."""
     if optimizer._fused is not None:
         return optimizer._fused
     if not optimizer.handles and optimizer._hook_handles == {}:
         raise RuntimeError("fuse_statistics: the optimizer is closed")
-    return FusedStatistics(optimizer, model)
+    return FusedStatistics(optimizer, model, activations)

@@ -106,6 +106,19 @@ def test_validation_errors_return_before_gpu_work():
     assert lib.smx_stats_cast(ctypes.c_void_p(16), 0, 4, 4, 4, ctypes.c_void_p(16), None, 1, ctypes.c_void_p(16), 0,
                               4, None) == -3
     assert lib.smx_stats_cast(None, 0, 0, 4, 4, ctypes.c_void_p(16), None, 1, None, 1, 4, None) == 0
+    # relayout statistics: 16-bit input only, aligned strides, no row chunk
+    # across a sequence (chunks of 512 rows for 2 x 1024 rows and 128 slots)
+    v16 = ctypes.c_void_p(16)
+    ok_args = (1, 2, 1024, 12, 64, 12 * 1024 * 64, 64, 1024 * 64, v16, v16, None, 128, None)
+    assert lib.smx_stats_relayout(v16, 0, *ok_args[1:]) == -3
+    assert lib.smx_stats_relayout(v16, 1, 2, 1024, 12, 60, 12 * 1024 * 60, 60, 1024 * 60, v16, v16, None, 128,
+                                  None) == -4
+    assert lib.smx_stats_relayout(ctypes.c_void_p(24), *ok_args) == -4
+    assert lib.smx_stats_relayout(v16, 1, 2, 768, 12, 64, 12 * 768 * 64, 64, 768 * 64, v16, v16, None, 128,
+                                  None) == -2
+    assert b"multiple of the row chunk" in lib.smx_last_error()
+    assert lib.smx_stats_relayout(v16, 1, 2, 1024, 12, 64, 12 * 1024 * 64, 64, 1024 * 64, v16, None, None, 128,
+                                  None) == -1
     need = lib.smx_stats_colsum_workspace_bytes(768, 128)
     assert need >= 128 * 768 * 4 and need % 256 == 0
     assert lib.smx_stats_colsum_workspace_bytes(0, 128) == -1

@@ -11,8 +11,13 @@
 * smx_stats_gelu: the GELU equals torch's F.gelu bit for bit over every
   bf16 and f16 value, and its partials, added into slot rows, equal the
   slot rows smx_stats_accumulate leaves for its output bit for bit;
-* a GPT step with fused statistics (with and without the GELU fused) gives
-  the hook path's statistics and matrix updates bit for bit.
+* smx_stats_relayout: the row-major copy of a head-transposed attention
+  output equals torch's reshape bit for bit, and its partials, added into
+  slot rows, equal the slot rows smx_stats_accumulate leaves for the copy
+  bit for bit;
+* a GPT step with fused statistics (with and without the GELU and the
+  attention-output relayout fused) gives the hook path's statistics and
+  matrix updates bit for bit.
 """
 import copy
 
@@ -104,6 +109,44 @@ def test_stats_gelu_refuses_unaligned_widths(device):
     h = torch.randn(4, 12, device=device).to(torch.bfloat16)
     with pytest.raises(ValueError, match="multiples of 8"):
         _native.stats_gelu(h, torch.empty_like(h), torch.empty(1, 12, device=device), None, SLOTS)
+
+
+@pytest.mark.parametrize("b,h,t,d,pad", [(2, 12, 1024, 64, 0), (1, 16, 512, 128, 0), (4, 3, 512, 8, 0),
+                                         (2, 5, 1536, 24, 0), (2, 4, 1024, 64, 32)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("first", [True, False])
+def test_stats_relayout_copy_and_partials_equal_reshape_and_hook_slots(device, b, h, t, d, pad, dtype, first):
+    g = torch.Generator(device=device).manual_seed(b * h * t + d)
+    # [batch, heads, seq, head_dim] as attention returns it (pad: a view of
+    # a wider buffer, so the seq stride is not head_dim)
+    full = (torch.randn(b, h, t, d + pad, generator=g, device=device) * 3 - 0.25).to(dtype)
+    y = full[..., :d].transpose(1, 2)          # [batch, seq, heads, head_dim], not contiguous
+    want = y.reshape(b * t, h * d)
+    cols = h * d
+    base_sq = torch.rand(SLOTS, cols, generator=g, device=device)
+    base_fs = torch.randn(SLOTS, cols, generator=g, device=device) if first else None
+    ref_sq = base_sq.clone()
+    ref_fs = base_fs.clone() if first else None
+    _native.stats_accumulate(want, ref_sq, ref_fs)
+    out = torch.empty(b * t, cols, dtype=dtype, device=device)
+    chunks = _native.stats_slot_rows(b * t, SLOTS)
+    part_sq = torch.empty(chunks, cols, device=device)
+    part_fs = torch.empty(chunks, cols, device=device) if first else None
+    _native.stats_relayout(y, out, part_sq, part_fs, SLOTS)
+    sq, fs = base_sq.clone(), base_fs.clone() if first else None
+    _native.stats_add_partials(sq, part_sq, fs, part_fs)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(sq, ref_sq)
+    if first:
+        assert torch.equal(fs, ref_fs)
+
+
+def test_stats_relayout_refuses_chunks_across_sequences(device):
+    y = torch.randn(2, 4, 768, 64, device=device).to(torch.bfloat16).transpose(1, 2)
+    out = torch.empty(2 * 768, 256, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError, match="multiple of the row chunk"):
+        _native.stats_relayout(y, out, torch.empty(3, 256, device=device), None, SLOTS)
 
 
 def test_stats_cast_strided_rows(device):
@@ -300,5 +343,65 @@ def test_fused_gpt_step_equals_hook_step(device, opt_cls, amp, gelu):
             assert torch.equal(p, q), (step, n)
     handle.close()
     assert len(fused_opt.handles) == 12
+    hooked.close()
+    fused_opt.close()
+
+
+class _HeadsMajor(nn.Module):
+    """A projection pair around a heads-major activation, as a manual
+    attention (softmax(Q K^T) V) or any per-head op leaves it: the input of
+    c_proj is the relayout copy of a [batch, heads, seq, head_dim] tensor
+    (SDPA on this stack already returns its output seq-major, so the GPT's
+    reshape is a view with no copy to fuse into)."""
+
+    def __init__(self, width=256, heads=4):
+        super().__init__()
+        self.heads = heads
+        self.q_proj = nn.Linear(width, width)
+        self.c_proj = nn.Linear(width, width)
+
+    def forward(self, x):
+        b, t, c = x.shape
+        h = self.q_proj(x).view(b, t, self.heads, c // self.heads).transpose(1, 2).contiguous()
+        h = torch.nn.functional.silu(h) * 1.5
+        return self.c_proj(h.transpose(1, 2).reshape(b, t, c))
+
+
+@pytest.mark.parametrize("opt_cls,amp", [(RankOneAWeightedPE, torch.bfloat16), (DiagonalWeightedPE, torch.float16)])
+def test_fused_relayout_step_equals_hook_step(device, opt_cls, amp):
+    torch.manual_seed(3)
+    model = _HeadsMajor().to(device)
+    twin = copy.deepcopy(model)
+    hooked, fused_opt = opt_cls(model, 1e-2), opt_cls(twin, 1e-2)
+    with pytest.raises(ValueError, match="unknown activations"):
+        fuse_statistics(fused_opt, twin, activations=("gelu", "softmax"))
+    handle = fuse_statistics(fused_opt, twin, activations=("relayout",))
+    g = torch.Generator(device=device).manual_seed(4)
+    for step in range(2):
+        for opt in (hooked, fused_opt):
+            opt.zero_grad(set_to_none=True)
+        for mb in range(3):
+            x = torch.randn(2, 512, 256, generator=g, device=device)
+            for m in (model, twin):
+                with torch.autocast("cuda", dtype=amp):
+                    loss = m(x).float().square().mean() / 3
+                loss.backward()
+        assert handle.relayout_calls == handle.relayout_taken == 3 * (step + 1)
+        assert handle.gelu_calls == 0
+        hooked.step()
+        fused_opt.step()
+        torch.cuda.synchronize()
+        for n, p in hooked.named_matrices.items():
+            q = fused_opt.named_matrices[n]
+            for key in ("a_ema", "a_mean_ema", "b_ema"):
+                if key in hooked.state[p]:
+                    assert torch.equal(hooked.state[p][key], fused_opt.state[q][key]), (step, n, key)
+            assert torch.equal(p, q), (step, n)
+    # a sequence that is not a multiple of the 512-row chunk keeps the
+    # separate read (the copy is torch's)
+    with torch.autocast("cuda", dtype=amp):
+        twin(torch.randn(2, 384, 256, device=device)).float().sum().backward()
+    assert handle.relayout_calls == 6
+    handle.close()
     hooked.close()
     fused_opt.close()
