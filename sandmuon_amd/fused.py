@@ -409,8 +409,8 @@ class FusedStatistics:
         if entry is None:
             return None
         y = entry[0]()
-        if (y is None or entry[1] != x._version or x.numel() != y.numel() or not x.is_contiguous() or
-                x.shape[-1] != entry[3].shape[1]):
+        if (y is None or entry[1] != x._version or x.dtype != y.dtype or x.numel() != y.numel() or
+                not x.is_contiguous() or x.shape[-1] != entry[3].shape[1]):
             return None
         del self._outputs[x.data_ptr()]
         if entry[2] == "gelu":
