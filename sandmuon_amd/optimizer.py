@@ -306,6 +306,10 @@ class DiagonalWeightedPE(Optimizer):
         matrix_ids = {id(p) for p in matrices.values()}
         auxiliary = [p for p in model.parameters() if p.requires_grad and id(p) not in matrix_ids]
         matrix_names = {id(p): name for name, p in matrices.items()}
+        devices = {p.device for p in list(matrices.values()) + auxiliary}
+        if len(devices) > 1:
+            raise ValueError("sandmuon_amd runs one optimizer per GPU: every parameter must be on one device "
+                             f"(got {sorted(str(d) for d in devices)})")
         for p in list(matrices.values()) + auxiliary:
             if p.device.type != "cuda":
                 raise RuntimeError("sandmuon_amd runs on ROCm GPU parameters only; move the model to the GPU "
@@ -531,10 +535,16 @@ class DiagonalWeightedPE(Optimizer):
         self._queue.restart()
         matrix_items, auxiliary_items = [], []
         a_counts: Dict[int, int] = {}
+        device = None
         for group in self.param_groups:
             for parameter in group["params"]:
                 if parameter.grad is None:
                     continue
+                if parameter.device != device:
+                    if device is not None:
+                        raise ValueError("sandmuon_amd runs one optimizer per GPU: every parameter must be on one "
+                                         f"device (got {device} and {parameter.device})")
+                    device = parameter.device
                 if group.get("use_muon", True):
                     source = self.a_sources[id(parameter)]
                     if id(source) not in a_counts:

@@ -84,6 +84,9 @@ def test_constructor_errors():
         RankOneAWeightedPE(nn.Sequential(nn.Linear(4, 3)), 1e-3)  # CPU parameters: no fallback
     with pytest.raises(ValueError, match="s8_mode"):
         DiagonalWeightedPE(nn.Sequential(nn.Linear(4, 3)), 1e-3, s8_mode="fp16")
+    # parameters on more than one device: refused before any is used
+    with pytest.raises(ValueError, match="one device"):
+        RankOneAWeightedPE(nn.Sequential(nn.Linear(4, 3), nn.Linear(3, 2, device="meta")), 1e-3)
 
 
 def test_public_exports():
