@@ -367,7 +367,10 @@ __device__ __forceinline__ int stats_job_of(const StatsPack &pack, int b) {
 }
 
 // grid.x = sum over the jobs of tiles * n_chunks; block = kStatsThreads.
-__global__ void __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(6))) stats_accumulate_kernel(StatsPack pack) {
+// Four waves per SIMD (two blocks per CU): on the cfg4 hook inputs 0.3-0.7%
+// faster than six (three blocks per CU) with the same code and bits; three
+// waves per SIMD (one block) was 8% slower.
+__global__ void __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) stats_accumulate_kernel(StatsPack pack) {
   __shared__ float red[2 * kStatsWaves * kStatsMaxTW];
   const int b = static_cast<int>(blockIdx.x);
   // A copy of the block's job (scalar registers): a reference into the pack
