@@ -9,7 +9,9 @@ them, and the optimizer on shapes that take the kernels' scalar paths.
   path, to 1e-5 (fp32 mode) and 1e-4 (comp_bf16 mode).
 * odd shapes (columns not a multiple of 4, transposed parameters, sizes far
   from the 256 padding) through the whole optimizer against the CPU oracle,
-  at the north-star gates.
+  at the north-star gates;
+* seeded random shapes (widths 1-900, edge sizes around the padding and the
+  tiles, more distinct shapes than one S8 plan takes) the same way.
 """
 import math
 
@@ -166,4 +168,47 @@ def test_wide_rows_through_the_optimizer(device, tile_policy, mode):
     assert len(opt.named_matrices) == 5
     worst = check_directions(hist, opt, 1e-2, mode)
     print(f"wide rows {mode} tiles {tile_policy}: worst direction rel err {worst:.3e}")
+    check_aux(hist, opt, ora)
+
+
+class RandomBranches(nn.Module):
+    """Parallel Linears of seeded random widths, edge sizes included (1-3,
+    around the 256-element padding and the 512 and 768 tiles): tall, wide and
+    square matrices, transposed and not, more distinct shapes than one S8
+    plan takes (so the step runs in groups over one workspace)."""
+
+    def __init__(self, seed):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        edge = [1, 2, 3, 16, 255, 256, 257, 511, 512, 513, 767, 769]
+        dims = []
+        for k in range(14):
+            pick = lambda: (edge[int(torch.randint(0, len(edge), (1,), generator=g))] if k % 2 == 0
+                            else int(torch.randint(1, 901, (1,), generator=g)))
+            dims.append((pick(), pick()))
+        self.widths = dims
+        self.layers = nn.ModuleList([nn.Linear(a, b) for a, b in dims])
+
+    def forward(self, x):
+        parts = torch.split(x, [a for a, _ in self.widths], dim=-1)
+        return torch.cat([torch.tanh(layer(p)) for layer, p in zip(self.layers, parts)], dim=-1)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("seed", [7, 8])
+def test_random_shapes_through_the_optimizer(device, mode, seed):
+    torch.manual_seed(seed)
+    model = RandomBranches(seed)
+    width_in = sum(a for a, _ in model.widths)
+    width_out = sum(b for _, b in model.widths)
+    g = torch.Generator().manual_seed(seed + 100)
+    # more samples than any width, so every gradient has full rank
+    batches = [(torch.randn(2048, width_in, generator=g) + 0.1, torch.randn(2048, width_out, generator=g))
+               for _ in range(2)]
+    loss = lambda m, x, y: (m(x) - y).square().mean() / 2
+    hist, opt, ora = run_pair(device, model, batches, loss, RankOneAWeightedPE, mode, 1e-2, steps=2)
+    shapes = {tuple(sorted(p.shape)) for p in opt.named_matrices.values()}
+    assert len(opt.named_matrices) == 14 and len(shapes) > 8, model.widths
+    worst = check_directions(hist, opt, 1e-2, mode)
+    print(f"random shapes seed {seed} {mode}: {model.widths}; worst direction rel err {worst:.3e}")
     check_aux(hist, opt, ora)
