@@ -19,7 +19,7 @@ import pytest
 import torch
 from torch import nn
 
-from sandmuon_amd import RankOneAWeightedPE, _native
+from sandmuon_amd import DiagonalWeightedPE, RankOneAWeightedPE, _native
 
 from test_gpu_optimizer import check_aux, check_directions, rel, run_pair
 
@@ -195,8 +195,8 @@ class RandomBranches(nn.Module):
 
 
 @pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
-@pytest.mark.parametrize("seed", [7, 8])
-def test_random_shapes_through_the_optimizer(device, mode, seed):
+@pytest.mark.parametrize("seed,opt_cls", [(7, RankOneAWeightedPE), (8, RankOneAWeightedPE), (9, DiagonalWeightedPE)])
+def test_random_shapes_through_the_optimizer(device, mode, seed, opt_cls):
     torch.manual_seed(seed)
     model = RandomBranches(seed)
     width_in = sum(a for a, _ in model.widths)
@@ -206,9 +206,9 @@ def test_random_shapes_through_the_optimizer(device, mode, seed):
     batches = [(torch.randn(2048, width_in, generator=g) + 0.1, torch.randn(2048, width_out, generator=g))
                for _ in range(2)]
     loss = lambda m, x, y: (m(x) - y).square().mean() / 2
-    hist, opt, ora = run_pair(device, model, batches, loss, RankOneAWeightedPE, mode, 1e-2, steps=2)
+    hist, opt, ora = run_pair(device, model, batches, loss, opt_cls, mode, 1e-2, steps=2)
     shapes = {tuple(sorted(p.shape)) for p in opt.named_matrices.values()}
     assert len(opt.named_matrices) == 14 and len(shapes) > 8, model.widths
     worst = check_directions(hist, opt, 1e-2, mode)
-    print(f"random shapes seed {seed} {mode}: {model.widths}; worst direction rel err {worst:.3e}")
+    print(f"random shapes seed {seed} {opt_cls.__name__} {mode}: {model.widths}; worst direction rel err {worst:.3e}")
     check_aux(hist, opt, ora)
