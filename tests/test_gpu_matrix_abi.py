@@ -212,3 +212,37 @@ def test_random_shapes_through_the_optimizer(device, mode, seed, opt_cls):
     worst = check_directions(hist, opt, 1e-2, mode)
     print(f"random shapes seed {seed} {opt_cls.__name__} {mode}: {model.widths}; worst direction rel err {worst:.3e}")
     check_aux(hist, opt, ora)
+
+
+class Extremes(nn.Module):
+    """Linears far from square: a 40 x 12000 weight (a Gram-space class
+    whose Gram and apply run K = 12000), a 7000 x 33 weight (transposed, an
+    odd column count on the scalar statistics path) and a 300 x 4100 one."""
+
+    widths = [(12000, 40), (33, 7000), (4100, 300)]
+
+    def __init__(self):
+        super().__init__()
+        self.layers = nn.ModuleList([nn.Linear(a, b) for a, b in self.widths])
+
+    def forward(self, x):
+        parts = torch.split(x, [a for a, _ in self.widths], dim=-1)
+        return torch.cat([torch.tanh(layer(p)) for layer, p in zip(self.layers, parts)], dim=-1)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+def test_extreme_aspect_ratios_through_the_optimizer(device, mode):
+    torch.manual_seed(11)
+    model = Extremes()
+    width_in = sum(a for a, _ in model.widths)
+    width_out = sum(b for _, b in model.widths)
+    g = torch.Generator().manual_seed(111)
+    # 1024 samples: more than every matrix's smaller side, so each gradient has full rank
+    batches = [(torch.randn(1024, width_in, generator=g) + 0.1, torch.randn(1024, width_out, generator=g))
+               for _ in range(2)]
+    loss = lambda m, x, y: (m(x) - y).square().mean() / 2
+    hist, opt, ora = run_pair(device, model, batches, loss, RankOneAWeightedPE, mode, 1e-2, steps=2)
+    assert sorted(tuple(p.shape) for p in opt.named_matrices.values()) == [(40, 12000), (300, 4100), (7000, 33)]
+    worst = check_directions(hist, opt, 1e-2, mode)
+    print(f"extreme aspect ratios {mode}: worst direction rel err {worst:.3e}")
+    check_aux(hist, opt, ora)
