@@ -154,6 +154,12 @@ def dtype_code(dtype: torch.dtype) -> int:
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
+def stream_busy(device: torch.device) -> bool:
+    """True while work enqueued on the current stream of `device` has not
+    finished (hipStreamQuery through torch)."""
+    return not torch.cuda.current_stream(device).query()
+
+
 def stream_of(device: torch.device) -> int:
     """The current stream of `device` (the autograd device stream inside a
     backward hook) as a hipStream_t value."""

@@ -228,20 +228,27 @@ class _StatsQueue:
     order per slot row.  The queue keeps its tensors alive until the launch
     is enqueued on the stream current at the first hook call.
 
-    The launch threshold ramps up after each step: the first launch takes
-    `first` bytes and each later one `growth` times more, up to `limit`.
-    Python queues hook inputs faster than the GPU reads them, so a phase of
-    hooks with nothing else on the GPU starts reading at once instead of
-    after a full batch is queued, and the batches still reach the full size.
+    A phase of hooks (from construction or a step to the next step) starts
+    by asking whether the stream of its first hook call still has work.
+    If it has (the step itself, a forward pass), every launch takes `limit`
+    bytes: the GPU is busy while the queue fills.  If the stream is idle,
+    the launch threshold ramps up instead: the first launch takes `first`
+    bytes and each later one `growth` times more, up to `limit`, so the GPU
+    starts reading after a few hook calls rather than after a full batch
+    (Python queues hook inputs only somewhat faster than the GPU reads
+    them), and the batches still reach the full size.  Small launches
+    leave part of the device idle, so the ramp is only taken when it helps.
     """
 
-    __slots__ = ("limit", "first", "growth", "threshold", "entries", "slot_ptrs", "nbytes", "stream", "device")
+    __slots__ = ("limit", "first", "growth", "threshold", "fresh", "entries", "slot_ptrs", "nbytes", "stream",
+                 "device")
 
     def __init__(self, limit: int, first: int = 64 << 20, growth: float = 1.6):
         self.limit = int(limit)
         self.first = int(first)
         self.growth = float(growth)
         self.threshold = min(self.limit, self.first)
+        self.fresh = True  # the next hook call is the first of a phase
         self.entries: List[Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor], int]] = []
         self.slot_ptrs = set()
         self.nbytes = 0
@@ -253,8 +260,15 @@ class _StatsQueue:
         self.threshold = min(self.limit, int(self.threshold * self.growth))
 
     def restart(self) -> None:
-        """Back to the first threshold (the statistics were consumed)."""
+        """A new phase of hooks begins (the statistics were consumed)."""
         self.threshold = min(self.limit, self.first)
+        self.fresh = True
+
+    def start_phase(self, busy: bool) -> None:
+        """At the phase's first hook call: no ramp when the GPU is busy."""
+        self.fresh = False
+        if busy:
+            self.threshold = self.limit
 
     def clear(self) -> None:
         self.entries = []
@@ -415,6 +429,8 @@ class DiagonalWeightedPE(Optimizer):
             self._flush_stats()
         if not q.entries:
             q.stream, q.device = stream, rows.device
+            if q.fresh:
+                q.start_phase(_native.stream_busy(rows.device))
         q.entries.append((rows, sq, fs, rows._version))
         q.slot_ptrs.add(sq.data_ptr())
         q.nbytes += rows.numel() * rows.element_size()

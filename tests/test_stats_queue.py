@@ -16,6 +16,7 @@ class Recorder:
         self.batches = []   # list of [(rows data_ptr, slots data_ptr)], per launch
         self.single = []
         self.stream = 1
+        self.busy = False   # what the stream query answers at a phase's first hook call
 
     def install(self, monkeypatch):
         monkeypatch.setattr(_native, "stats_accumulate_batch",
@@ -24,6 +25,12 @@ class Recorder:
         monkeypatch.setattr(_native, "stats_accumulate",
                             lambda rows, sq, fs: self.single.append((rows.data_ptr(), sq.data_ptr())))
         monkeypatch.setattr(_native, "stream_of", lambda device: self.stream)
+        self.queries = 0
+
+        def busy(device):
+            self.queries += 1
+            return self.busy
+        monkeypatch.setattr(_native, "stream_busy", busy)
         self.waits = []
         monkeypatch.setattr(_native, "stream_wait", lambda waiter, signaler, device: self.waits.append((waiter, signaler)))
         monkeypatch.setattr(_native, "stats_slot_rows", lambda rows, n: min(n, max(1, -(-rows // 512))) if rows else 0)
@@ -78,6 +85,27 @@ def test_launch_threshold_ramps_up_and_restarts(monkeypatch):
     opt._queue.restart()                                     # what step() does after its flush
     assert opt._queue.threshold == 800
     assert _StatsQueue(100).threshold == 100                 # a limit below the first batch is the threshold
+    assert rec.queries == 1                                  # one stream query per phase of hooks
+
+
+def test_no_ramp_when_the_stream_is_busy_at_the_first_hook_call(monkeypatch):
+    rec = Recorder()
+    rec.install(monkeypatch)
+    rec.busy = True                                          # e.g. the step's kernels still running
+    opt = object.__new__(DiagonalWeightedPE)
+    opt._queue = _StatsQueue(4000, first=800, growth=2.0)
+    opt._slot_rows = {}
+    for k in range(10):                                      # 8000 bytes: two launches of the limit
+        opt._enqueue_stats(rows(25), torch.zeros(4, 8), None)
+    assert [len(b) for b in rec.batches] == [5, 5] and rec.queries == 1
+    opt._flush_stats()
+    opt._queue.restart()                                     # the next phase asks again
+    rec.busy = False
+    for k in range(2):
+        opt._enqueue_stats(rows(25), torch.zeros(4, 8), None)
+    # idle: the first launch takes 800 bytes, the next threshold is 1600
+    assert [len(b) for b in rec.batches] == [5, 5, 1] and len(opt._queue.entries) == 1
+    assert rec.queries == 2 and opt._queue.threshold == 1600
 
 
 def test_same_slot_rows_or_another_stream_launch_the_queue_first(monkeypatch):
