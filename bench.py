@@ -456,7 +456,7 @@ def main():
                   "frac": round(stats_gbs / (HBM_PEAK / 1e9), 4),
                   "traffic": traffic.get("stats_accumulate_kernel", {}).get("hbm_bytes_per_step"),
                   "kernel": "stats_accumulate_kernel (every statistics launch of the step's hooks: queued hook inputs, "
-                            "1 GiB of them per launch)",
+                            "up to 1 GiB of them per launch)",
                   "bytes_per_step": stat_bytes, "ms_per_step": round(hooks_ms, 3)}
     roof_s8 = {"bound": "mfma", "achieved": round(s8_tfs, 1), "peak": peak_mfma / 1e12, "unit": "TFLOP/s",
                "frac": round(s8_tfs / (peak_mfma / 1e12), 4),
