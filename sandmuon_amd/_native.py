@@ -156,8 +156,12 @@ _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 def stream_busy(device: torch.device) -> bool:
     """True while work enqueued on the current stream of `device` has not
-    finished (hipStreamQuery through torch)."""
-    return not torch.cuda.current_stream(device).query()
+    finished (hipStreamQuery through torch).  A stream under graph capture
+    cannot be queried and counts as busy."""
+    with torch.cuda.device(device):
+        if torch.cuda.is_current_stream_capturing():
+            return True
+        return not torch.cuda.current_stream(device).query()
 
 
 def stream_of(device: torch.device) -> int:

@@ -213,3 +213,45 @@ def test_queue_launched_on_the_hook_stream_orders_the_current_stream(device):
     torch.cuda.synchronize()
     assert ((got - want).norm() / want.norm()).item() <= 1e-6
     opt.close()
+
+
+def test_ramp_only_when_the_hook_stream_is_idle(device):
+    """The first hook call of a phase asks whether its stream still has work:
+    busy (here a bounded sleep kernel) -> every launch takes the full batch
+    size; idle -> the threshold ramps from the first size.  A stream under
+    graph capture counts as busy and is not queried."""
+    model = nn.Sequential(nn.Linear(256, 64)).to(device)
+    opt = DiagonalWeightedPE(model, 1e-2, hook_batch_bytes=64 << 20)
+    q = opt._queue
+    q.first = 1 << 20
+    p = model[0].weight
+    x = torch.randn(64, 256, device=device)           # 64 KB: stays queued
+    opt._accumulate_a(p, x)                           # allocates the slot rows (a fill kernel)
+    opt._flush_stats()
+    torch.cuda.synchronize()
+    q.restart()
+    opt._accumulate_a(p, x)                           # idle stream: ramp
+    assert q.threshold == 1 << 20 and not q.fresh
+    opt._flush_stats()
+    q.restart()
+    torch.cuda._sleep(50_000_000)
+    opt._accumulate_a(p, x)                           # busy stream: full size
+    assert q.threshold == 64 << 20
+    opt._flush_stats()
+    torch.cuda.synchronize()
+
+    g = torch.cuda.CUDAGraph()
+    y = torch.zeros(4, device=device)
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        y.add_(1)                                     # warm-up of the captured op
+    torch.cuda.current_stream(device).wait_stream(s)
+    with torch.cuda.graph(g):
+        busy = _native.stream_busy(y.device)
+        y.add_(1)
+    assert busy
+    g.replay()
+    torch.cuda.synchronize()
+    assert y.tolist() == [2.0] * 4
+    opt.close()
