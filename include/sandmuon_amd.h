@@ -16,6 +16,16 @@
  * kernel launch fails.  smx_last_error() returns a thread-local message for
  * the last failure on the calling thread.
  *
+ * Threads: entry points may be called from several host threads, also on
+ * one device and with different streams.  smx_matrix_step and smx_s8 fork
+ * part of their launches onto a second stream of the device that the
+ * library owns; the enqueue from that fork to its join is serialised by a
+ * process-wide lock, so concurrent callers never share a fork.  Calls whose
+ * device buffers overlap (the same workspace, slot rows or parameters)
+ * must be ordered by the caller, as for any kernels.  The S8 launch
+ * recorder (smx_s8_timing) and the test aids smx_s8_comp_stages and
+ * smx_s8_tile_geometry are process-wide settings, not thread-safe.
+ *
  * The reference interface each entry point replaces is cited as
  * path:line under pxike/SandMuon.
  */

@@ -1395,10 +1395,13 @@ struct ForkStream {
 static std::mutex g_fork_lock;
 static ForkStream g_fork[64];
 
+// The caller holds g_fork_lock from the fork record to the join wait: the
+// streams and events of a device are shared, so two host threads running
+// S8 on one device would otherwise interleave their fork and join records
+// (one chain waiting on the other caller's fork).
 static int fork_stream(ForkStream *&out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(SMX_ELAUNCH, "s8: no current HIP device");
-  std::lock_guard<std::mutex> lock(g_fork_lock);
   ForkStream &f = g_fork[dev];
   if (!f.fork) {
     bool ok = hipEventCreateWithFlags(&f.fork, hipEventDisableTiming) == hipSuccess;
@@ -1468,6 +1471,8 @@ int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
   if (chains <= 1) {
     for (int stage = 1; stage <= 5 && !rc; ++stage) rc = run_s8_set_stage(Lay, set[0], stage, st, flops);
   } else {
+    // Only enqueues happen under the lock.
+    std::lock_guard<std::mutex> lock(g_fork_lock);
     ForkStream *f = nullptr;
     rc = fork_stream(f);
     if (!rc && hipEventRecord(f->fork, st) != hipSuccess) rc = fail(SMX_ELAUNCH, "s8: fork of the launch chains failed");

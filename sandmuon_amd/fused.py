@@ -387,6 +387,12 @@ class FusedStatistics:
                 shape = tuple(x.numel() // known if n == -1 else n for n in shape)
             if shape not in ((b, t, h * d), (b * t, h * d)):
                 return None
+            # Only where torch's reshape copies: where it returns a view, the
+            # result must stay an alias of x (in-place writes reach x).
+            merges_hd = x.stride(2) == d
+            merges_bt = x.stride(0) == t * x.stride(1)
+            if merges_hd and (len(shape) == 3 or merges_bt):
+                return None
         rows = b * t
         chunk = max(-(-rows // self.optimizer.STAT_SLOTS), 512)
         if (d % 8 or t % chunk or any(st % 8 for st in x.stride()[:3]) or x.data_ptr() % 16 or

@@ -4,7 +4,8 @@ kernels of libsandmuon_amd.so.
 
 Drop-in surface (sandmuon/optimizer.py:96-328): DiagonalWeightedPE,
 RankOneAWeightedPE, module_filter, the forward/cotangent hooks, step(),
-state_dict()/load_state_dict() (inherited, same state keys and types) and
+state_dict()/load_state_dict() (same state keys and types; the load keeps
+the statistics, momentum and moments float32 for 16-bit parameters) and
 close().  The module-level helpers imported by the reference tests
 (_s8_fp32, diagonal_inverse_sqrt, _graft_direction, rank1_inverse_sqrt,
 rank1_mapback, rank1_whiten) are GPU-backed here as well.
@@ -140,6 +141,10 @@ def _s8_fp32(x: torch.Tensor, mode: str = "fp32") -> torch.Tensor:
 
 
 _PARAM_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+# Optimizer state kept in float32 whatever the parameter dtype (the kernels
+# read and write it as FP32; sandmuon/optimizer.py creates it float32).
+_FP32_STATE = ("a_sum", "a_first_sum", "b_sum", "a_ema", "a_mean_ema", "b_ema", "momentum_buffer",
+               "exp_avg", "exp_avg_sq")
 
 
 def _dense(t: torch.Tensor) -> bool:
@@ -165,6 +170,18 @@ def _check_layout(parameter: torch.Tensor, name: str, matrix: bool) -> None:
     if not matrix and not _dense(parameter):
         raise ValueError(f"sandmuon_amd needs parameters without gaps or overlap; {name} has strides "
                          f"{tuple(parameter.stride())}")
+
+
+def _require_f32(t: torch.Tensor, n: int, device, what: str) -> torch.Tensor:
+    """A state vector the kernels read and write as n contiguous FP32 values
+    on `device`; anything else is refused before a launch gets its pointer."""
+    if (not isinstance(t, torch.Tensor) or t.dtype != torch.float32 or t.numel() != n or
+            not t.is_contiguous() or t.device != device):
+        desc = (f"{t.dtype}, {t.numel()} elements, contiguous={t.is_contiguous()}, {t.device}"
+                if isinstance(t, torch.Tensor) else type(t).__name__)
+        raise ValueError(f"optimizer state {what} must be a contiguous float32 tensor of {n} elements on "
+                         f"{device} (got {desc})")
+    return t
 
 
 def _like(t: torch.Tensor, parameter: torch.Tensor, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
@@ -488,6 +505,10 @@ class DiagonalWeightedPE(Optimizer):
             if total is None:
                 continue
             first = state.get("a_first_sum") if side == "a" and fs is not None else None
+            name = self.parameter_names.get(pid, "a parameter")
+            _require_f32(total, sq.shape[1], sq.device, f"{side}_sum of {name}")
+            if first is not None:
+                _require_f32(first, sq.shape[1], sq.device, f"a_first_sum of {name}")
             n = self._take_slot_rows(sq)
             _native.stats_fold(total, sq[:n], first, fs[:n] if first is not None else None)
 
@@ -497,6 +518,39 @@ class DiagonalWeightedPE(Optimizer):
         self._queue.clear()
         self._slots.clear()
         self._slot_rows.clear()
+
+    def load_state_dict(self, state_dict: dict) -> None:
+        """torch's Optimizer.load_state_dict, keeping the FP32 state FP32.
+
+        torch casts every floating state tensor to its parameter's dtype, so
+        for a bf16/fp16 parameter the statistics, EMA, momentum and moment
+        tensors would come back 16-bit.  The reference creates them FP32
+        (sandmuon/optimizer.py:161,164,174,245,270-271) and the kernels read
+        and write them as FP32, so they are restored from the saved values
+        (not from the rounded copies) as contiguous float32 on the
+        parameter's device.
+        """
+        saved_state = state_dict["state"]
+        saved_ids = [i for g in state_dict["param_groups"] for i in g["params"]]
+        params = [p for g in self.param_groups for p in g["params"]]
+        keep = {}
+        for saved_id, parameter in zip(saved_ids, params):
+            entry = saved_state.get(saved_id)
+            if entry is None:
+                continue
+            for key in _FP32_STATE:
+                value = entry.get(key)
+                if isinstance(value, torch.Tensor) and value.is_floating_point():
+                    keep[(id(parameter), key)] = value
+        super().load_state_dict(state_dict)
+        for parameter in params:
+            state = self.state.get(parameter)
+            if not state:
+                continue
+            for key in _FP32_STATE:
+                value = keep.get((id(parameter), key))
+                if value is not None:
+                    state[key] = value.to(device=parameter.device, dtype=torch.float32, copy=True).contiguous()
 
     # ------------------------------------------------------------- step ---
     def _finish_a_check(self, parameter) -> int:
@@ -514,7 +568,7 @@ class DiagonalWeightedPE(Optimizer):
     def _finish_desc(self, parameter, side: str, count: int, out: Dict[str, torch.Tensor]) -> _native.FinishDesc:
         state = self.state[parameter]
         total = state[f"{side}_sum"]
-        n = total.numel()
+        n = parameter.shape[1] if side == "a" else parameter.shape[0]
         rank1 = side == "a" and self.rank_one_a
         sq, fs = self._slot_pair(parameter, side, n, total.device, rank1)
         ema_key = f"{side}_ema"
@@ -523,6 +577,10 @@ class DiagonalWeightedPE(Optimizer):
             state[ema_key] = torch.empty(n, dtype=torch.float32, device=total.device)
             if rank1:
                 state["a_mean_ema"] = torch.empty(n, dtype=torch.float32, device=total.device)
+        name = self.parameter_names[id(parameter)]
+        keys = [f"{side}_sum", ema_key] + (["a_first_sum", "a_mean_ema"] if rank1 else [])
+        for key in keys:
+            _require_f32(state[key], n, parameter.device, f"{key} of {name}")
         kind = _KIND_B if side == "b" else (_KIND_RANK1_A if rank1 else _KIND_DIAG_A)
         d = _native.FinishDesc(sum_sq=total.data_ptr(), slots_sq=sq.data_ptr(), ema=state[ema_key].data_ptr(),
                                inv=out["inv"].data_ptr(), n=n, count=int(count), n_slots=self._take_slot_rows(sq),

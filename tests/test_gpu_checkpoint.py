@@ -1,5 +1,5 @@
 """state_dict() / load_state_dict() of the GPU build (sandmuon/optimizer.py:
-96-321, inherited from torch.optim.Optimizer).
+96-321, torch.optim.Optimizer's, with the state kept float32 on load).
 
 * The saved structure (param groups, state keys, dtypes, shapes, int counts
   and int AdamW step) equals the reference's, recorded by the reference in
@@ -9,6 +9,9 @@
 * Hook statistics still pending in the slot buffers are folded into the
   saved a_sum / b_sum (checked against an FP64 brute force), and loading a
   checkpoint discards pending partials.
+* With bf16 parameters the loaded statistics, EMA, momentum and moment
+  tensors stay float32 (torch would cast them to bf16) and a resumed run
+  is bit-identical to an uninterrupted one.
 * A checkpoint whose AdamW `step` is a tensor (the historical trainer's
   format, reproduction/odl/optim/diagonal_weighted_pe.py:487-493) loads and
   continues exactly like the int form.
@@ -65,12 +68,12 @@ def params_of(model):
     return {n: p.detach().clone() for n, p in model.named_parameters()}
 
 
-def record(device, params, names, data):
+def record(device, params, names, data, dtype=torch.float32):
     """Hook inputs, output cotangents and gradients of one effective batch,
-    computed once on a separate copy of the model at `params`, so that two
-    optimizers can be fed bit-identical inputs (the model's own backward
-    is not bit-reproducible: the embedding backward uses atomics)."""
-    model = fresh(device)
+    computed once on a separate copy of the model at `params` (in `dtype`),
+    so that two optimizers can be fed bit-identical inputs (the model's own
+    backward is not bit-reproducible: the embedding backward uses atomics)."""
+    model = fresh(device).to(dtype)
     with torch.no_grad():
         for n, p in model.named_parameters():
             p.copy_(params[n])
@@ -236,3 +239,53 @@ def test_tensor_adamw_step_loads_like_int(device):
     for n in results[0]:
         assert torch.equal(results[0][n], results[1][n]), n
     opt.close()
+
+
+def test_bf16_parameters_resume_with_float32_state(device):
+    """torch's load_state_dict casts floating state to the parameter dtype;
+    the build keeps every statistic, EMA, momentum and moment float32 (the
+    kernels read and write FP32), restored from the saved values.  With bf16
+    parameters a resumed run is bit-identical to an uninterrupted one."""
+    def bf16_model(seed=11):
+        return fresh(device, seed).to(torch.bfloat16)
+
+    model_a = bf16_model()
+    opt_a = RankOneAWeightedPE(model_a, lr=3e-3, module_filter=transformer_filter)
+    names = list(opt_a.named_matrices)
+    replay_step(model_a, opt_a, *record(device, params_of(model_a), names, batches(device, 12), torch.bfloat16))
+    saved = cpu_copy(opt_a.state_dict())
+    float_keys = set()
+    for entry in saved["state"].values():
+        for key, value in entry.items():
+            if torch.is_tensor(value):
+                assert value.dtype == torch.float32, key
+                float_keys.add(key)
+    assert {"a_sum", "a_first_sum", "b_sum", "a_ema", "a_mean_ema", "b_ema", "momentum_buffer",
+            "exp_avg", "exp_avg_sq"} <= float_keys
+    saved_params = params_of(model_a)
+    step2 = record(device, saved_params, names, batches(device, 13), torch.bfloat16)
+    replay_step(model_a, opt_a, *step2)
+
+    model_b = bf16_model(seed=99)
+    with torch.no_grad():
+        for n, p in model_b.named_parameters():
+            p.copy_(saved_params[n])
+    opt_b = RankOneAWeightedPE(model_b, lr=3e-3, module_filter=transformer_filter)
+    opt_b.load_state_dict(saved)
+    for k, entry in opt_b.state_dict()["state"].items():
+        for key, value in entry.items():
+            if torch.is_tensor(value):
+                assert value.dtype == torch.float32 and value.is_contiguous(), (k, key)
+                assert torch.equal(value.cpu(), saved["state"][k][key]), (k, key)
+    replay_step(model_b, opt_b, *step2)
+    for (n, pa), (_, pb) in zip(model_a.named_parameters(), model_b.named_parameters()):
+        assert pa.dtype == torch.bfloat16
+        assert torch.equal(pa, pb), n
+    for pa, pb in zip(opt_a.state.values(), opt_b.state.values()):
+        for key in pa:
+            if torch.is_tensor(pa[key]):
+                assert pb[key].dtype == torch.float32, key
+                assert torch.equal(pa[key], pb[key]), key
+    opt_a.close()
+    opt_b.close()
+

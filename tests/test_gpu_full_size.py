@@ -16,8 +16,10 @@
 * cfg5: one step of the 2048-wide, 24-layer GPT (144 matrices, 105.7M AdamW
   parameters, the 16 GB workspace) with 4 microbatches of 8 x 1024-token
   synthetic hook inputs of the dtypes a bf16-autocast step hands the hooks;
-  the update norm of every matrix, the statistics against FP64, one matrix
-  of each shape class against the oracle in FP64, AdamW on wte.
+  every direction, momentum buffer and AdamW parameter against the FP32
+  oracle's step from the same weights, gradients and FP64 statistics, the
+  update norm of every matrix, the statistics against FP64, and one matrix
+  of each shape class against the exact map in FP64.
 * FP32 mode's error budget: the reference's eager FP32 path, the same path
   with its two Frobenius norms reduced in FP64, and this build's FP32 mode,
   each against the FP64 map.
@@ -443,9 +445,8 @@ def test_cfg5_gpt_step(device):
             opt._accumulate_a(p, x)
         for p, d in b:
             opt._accumulate_b(p, d)
+    names = {id(p): n for n, p in model.named_parameters()}
     before = {id(p): p.detach().clone() for p in model.parameters()}
-    cpu_wte = model.transformer.wte.weight.detach().cpu().clone()
-    cpu_wte_grad = model.transformer.wte.weight.grad.detach().cpu().clone()
     grads = {n: p.grad.detach().clone() for n, p in opt.named_matrices.items()}
     opt.step()
     torch.cuda.synchronize()
@@ -455,12 +456,15 @@ def test_cfg5_gpt_step(device):
         dw = (before[id(p)] - p.detach()).double() / lr
         assert torch.isfinite(dw).all(), n
         assert abs(dw.norm().item() - math.sqrt(p.shape[0])) <= 1e-4 * math.sqrt(p.shape[0]), n
-    # statistics against FP64 sums of the same inputs (each set used twice)
+    # statistics against FP64 sums of the same inputs (each set used twice),
+    # kept as the oracle's hook state
     worst_stats = 0.0
+    stats = {}
     for (pa, x), j in zip(sets[0][0], range(len(sets[0][0]))):
         x1 = sets[1][0][j][1]
         sq = sum(t.double().square().sum(0) for t in (x, x1)) * 2
         first = sum(t.double().sum(0) for t in (x, x1)) * 2
+        stats[(names[id(pa)], "a")] = (sq, first, 4 * rows)
         st = opt.state[pa]
         for key, want in (("a_ema", sq / (4 * rows)), ("a_mean_ema", first / (4 * rows))):
             e = rel(st[key], want)
@@ -468,23 +472,58 @@ def test_cfg5_gpt_step(device):
             assert e <= STATS_TOL, (key, e)
     for j, (pb, d) in enumerate(sets[0][1]):
         d1 = sets[1][1][j][1]
-        bsum = sum(t.double().square().sum(0) for t in (d, d1)) * 2 / (4 * rows)
+        bsq = sum(t.double().square().sum(0) for t in (d, d1)) * 2
+        stats[(names[id(pb)], "b")] = (bsq, None, 4 * rows)
+        bsum = bsq / (4 * rows)
         e = rel(opt.state[pb]["b_ema"], bsum / bsum.mean())
         worst_stats = max(worst_stats, e)
         assert e <= STATS_TOL, ("b_ema", e)
-    # one matrix of each shape class against the oracle's FP64 direction
+    del sets
+    # The FP32 oracle's step on the CPU from the same weights, gradients and
+    # FP64 statistics: all 144 directions, the momentum and every AdamW
+    # parameter.
+    with torch.device("meta"):
+        cpu_model = GPT(cfg)
+    cpu_model = cpu_model.to_empty(device="cpu")
+    gparams = dict(model.named_parameters())
+    with torch.no_grad():
+        for n, c in cpu_model.named_parameters():
+            gp = gparams[n]
+            c.copy_(before[id(gp)].cpu())
+            c.grad = gp.grad.detach().cpu()
+    ora = O.OracleOptimizer(cpu_model, lr, rank_one_a=True, module_filter=transformer_filter, hooks=False)
+    assert list(ora.matrices) == list(opt.named_matrices)
+    feed_oracle(ora, stats)
+    t2 = time.time()
+    print(f"cfg5: GPU step and statistics checked ({t2 - t0:.1f}s); oracle step on the CPU", flush=True)
+    ora.step()
+    t3 = time.time()
+    cparams = dict(cpu_model.named_parameters())
     errs = {}
+    for n, p in opt.named_matrices.items():
+        got = (before[id(p)] - p.detach()).double().cpu() / lr
+        want = (before[id(p)].cpu() - cparams[n].detach()).double() / lr
+        errs[n] = rel(got, want)
+        assert rel(opt.state[p]["momentum_buffer"], ora.st(ora.matrices[n])["momentum_buffer"]) <= 1e-6, n
+    worst = max(errs.values())
+    assert worst <= DIR_TOL["comp_bf16"], (max(errs, key=errs.get), worst)
+    worst_aux = 0.0
+    for n, p in model.named_parameters():
+        if n not in errs:
+            e = rel(p, cparams[n])
+            worst_aux = max(worst_aux, e)
+            assert e <= 1e-6, n
+    # one matrix of each shape class against the exact map (FP64, from the
+    # oracle's statistics and momentum)
+    exact = {}
     blk = "transformer.h.0."
     for n in (blk + "attn.q_proj.weight", blk + "mlp.c_fc.weight", blk + "mlp.c_proj.weight"):
-        p = opt.named_matrices[n]
+        p, pc = opt.named_matrices[n], ora.matrices[n]
         got = (before[id(p)] - p.detach()).double().cpu() / lr
-        errs[n] = rel(got, fp64_direction(opt.state[p], opt.state[p], p.shape, grads[n]))
-        assert errs[n] <= DIR_TOL["comp_bf16"], (n, errs[n])
-    # AdamW on wte
-    st = {}
-    O.adamw(cpu_wte, cpu_wte_grad, st, lr * .1)
-    assert rel(model.transformer.wte.weight, cpu_wte) <= 1e-6
-    print(f"cfg5 step: 144 matrices, statistics worst {worst_stats:.2e}, FP64 directions "
-          + ", ".join(f"{n.split('.', 3)[-1]} {e:.2e}" for n, e in errs.items())
-          + f"; GPU part {t1 - t0:.1f}s, checks {time.time() - t1:.1f}s")
+        exact[n] = rel(got, fp64_direction(ora.st(pc), ora.st(ora.a_source[id(pc)]), pc.shape, grads[n]))
+        assert exact[n] <= DIR_TOL["comp_bf16"], (n, exact[n])
+    print(f"cfg5 step: 144 matrices, worst direction rel err vs the FP32 oracle {worst:.3e} "
+          f"({max(errs, key=errs.get)}), statistics worst {worst_stats:.2e}, AdamW worst {worst_aux:.2e}; "
+          "FP64 directions " + ", ".join(f"{n.split('.', 3)[-1]} {e:.2e}" for n, e in exact.items())
+          + f"; GPU part {t1 - t0:.1f}s, oracle step {t3 - t2:.1f}s, total {time.time() - t0:.1f}s")
     opt.close()

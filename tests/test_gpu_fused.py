@@ -405,3 +405,37 @@ def test_fused_relayout_step_equals_hook_step(device, opt_cls, amp):
     handle.close()
     hooked.close()
     fused_opt.close()
+
+
+class _HeadSlice(nn.Module):
+    """A reshape that is a view in torch (a head slice of a packed qkv with
+    stride(h) == head_dim, flattened back)."""
+
+    def __init__(self, width=256, heads=4):
+        super().__init__()
+        self.heads = heads
+        self.qkv = nn.Linear(width, 3 * width)
+        self.c_proj = nn.Linear(width, width)
+        self.seen = []
+
+    def forward(self, x):
+        b, t, c = x.shape
+        qkv = self.qkv(x).view(b, t, 3 * self.heads, c // self.heads)
+        q = qkv[:, :, : self.heads]          # non-contiguous, stride(2) == head_dim
+        flat = q.reshape(b, t, c)            # torch: a view of qkv
+        self.seen.append((flat._base is not None, flat.data_ptr() == q.data_ptr()))
+        return self.c_proj(flat)
+
+
+def test_fused_relayout_keeps_reshape_views(device):
+    torch.manual_seed(5)
+    model = _HeadSlice().to(device)
+    opt = RankOneAWeightedPE(model, 1e-2)
+    handle = fuse_statistics(opt, model, activations=("relayout",))
+    x = torch.randn(2, 512, 256, device=device)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        model(x).float().square().mean().backward()
+    assert model.seen == [(True, True)]  # still a view of the same storage
+    assert handle.relayout_calls == 0
+    handle.close()
+    opt.close()

@@ -246,3 +246,39 @@ def test_extreme_aspect_ratios_through_the_optimizer(device, mode):
     worst = check_directions(hist, opt, 1e-2, mode)
     print(f"extreme aspect ratios {mode}: worst direction rel err {worst:.3e}")
     check_aux(hist, opt, ora)
+
+
+class ManyBranches(nn.Module):
+    """264 parallel Linears in four shape classes, half of them transposed
+    parameters: the row kernels of the matrix step take at most 128 jobs per
+    launch, so the whiten, the transposed whiten and both mapback kernels
+    each run a second launch whose jobs (table entries 128 and up) are
+    compared with the oracle like the first."""
+
+    WIDTHS = [(32, 48), (48, 32), (64, 64), (24, 80)] * 66  # (in, out): weights 48x32 (transposed), 32x48, ...
+
+    def __init__(self):
+        super().__init__()
+        self.layers = nn.ModuleList([nn.Linear(a, b) for a, b in self.WIDTHS])
+
+    def forward(self, x):
+        parts = torch.split(x, [a for a, _ in self.WIDTHS], dim=-1)
+        return torch.cat([torch.tanh(layer(p)) for layer, p in zip(self.layers, parts)], dim=-1)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+def test_more_matrices_than_one_row_launch_takes(device, mode):
+    torch.manual_seed(17)
+    model = ManyBranches()
+    d_in, d_out = sum(a for a, _ in ManyBranches.WIDTHS), sum(b for _, b in ManyBranches.WIDTHS)
+    g = torch.Generator().manual_seed(18)
+    # 256 samples: more than every matrix's smaller side (full-rank gradients)
+    batches = [(torch.randn(256, d_in, generator=g) + 0.1, torch.randn(256, d_out, generator=g)) for _ in range(2)]
+    loss = lambda m, x, y: (m(x) - y).square().mean() / 2
+    hist, opt, ora = run_pair(device, model, batches, loss, RankOneAWeightedPE, mode, 1e-2, steps=2)
+    mats = list(opt.named_matrices.values())
+    flipped = sum(p.shape[0] > p.shape[1] for p in mats)
+    assert len(mats) == 264 and flipped > 128 and len(mats) - flipped > 128
+    worst = check_directions(hist, opt, 1e-2, mode)  # every matrix, so every job of both launches
+    print(f"264 matrices ({flipped} transposed) {mode}: worst direction rel err {worst:.3e}")
+    check_aux(hist, opt, ora)

@@ -109,3 +109,48 @@ def test_helper_factor_batching(monkeypatch):
     assert bv.shape == (3, 5) and bc.shape == (3,)
     assert M._work_dtype(torch.zeros(2), torch.zeros(2, dtype=torch.float64)) == torch.float64
     assert M._work_dtype(torch.zeros(2, dtype=torch.bfloat16)) == torch.float32
+
+
+def _bare_optimizer(params):
+    """A DiagonalWeightedPE shell over CPU parameters: torch's Optimizer
+    state without the GPU constructor (no hooks, no library calls), enough
+    to run load_state_dict."""
+    from sandmuon_amd import optimizer as M
+    opt = M.DiagonalWeightedPE.__new__(M.DiagonalWeightedPE)
+    torch.optim.Optimizer.__init__(opt, [dict(params=params[:1], use_muon=True),
+                                         dict(params=params[1:], use_muon=False)], dict(lr=1e-3))
+    return opt
+
+
+def test_load_state_dict_keeps_float32_state_for_16bit_parameters():
+    # torch casts floating state to the parameter dtype on load; the build
+    # restores the saved float32 values (not their bf16 rounding).
+    w = nn.Parameter(torch.zeros(3, 5, dtype=torch.bfloat16))
+    b = nn.Parameter(torch.zeros(3, dtype=torch.bfloat16))
+    opt = _bare_optimizer([w, b])
+    g = torch.Generator().manual_seed(5)
+    fine = lambda *shape: 1 + torch.rand(*shape, generator=g) * 2 ** -12  # not bf16-representable
+    saved = {"state": {0: {"a_sum": fine(5), "a_first_sum": fine(5), "a_count": 0, "b_sum": fine(3),
+                           "b_count": 0, "a_ema": fine(5), "a_mean_ema": fine(5), "b_ema": fine(3),
+                           "momentum_buffer": fine(5, 3).t()},  # a transposed (non-contiguous) buffer
+                       1: {"exp_avg": fine(3), "exp_avg_sq": fine(3), "step": 4}},
+             "param_groups": [dict(opt.param_groups[0], params=[0]), dict(opt.param_groups[1], params=[1])]}
+    opt.load_state_dict(saved)
+    for i, p in enumerate((w, b)):
+        for key, value in saved["state"][i].items():
+            got = opt.state[p][key]
+            if torch.is_tensor(value):
+                assert got.dtype == torch.float32 and got.is_contiguous(), key
+                assert torch.equal(got, value), key
+                assert got.data_ptr() != value.data_ptr(), key  # a copy, not the caller's tensor
+            else:
+                assert got == value, key
+
+
+def test_state_vectors_are_checked_before_launch():
+    from sandmuon_amd.optimizer import _require_f32
+    ok = torch.zeros(4)
+    assert _require_f32(ok, 4, ok.device, "a_sum") is ok
+    for bad in (torch.zeros(4, dtype=torch.bfloat16), torch.zeros(5), torch.zeros(8)[::2]):
+        with pytest.raises(ValueError, match="contiguous float32"):
+            _require_f32(bad, 4, ok.device, "a_sum")

@@ -81,6 +81,9 @@ def test_static_step_refuses_matrices_beyond_its_array(device):
     fn = static_step()
     # two 8192 x 8192 matrices need several GB of workspace; the call must
     # return before touching the (never dereferenced) pointers
+    # The fake pointers are safe only while the size check refuses this set:
+    # fail on the host if the workspace estimate ever fits the array.
+    assert _native.matrix_step_workspace_bytes([(8192, 8192)] * 2, _native.S8_COMP_BF16) > 1 << 30
     d = _native.MatrixDesc(param=256, grad=256, momentum=256, inv_row=256, inv_col=256, rows=8192, cols=8192,
                            lr=1e-2, momentum_beta=.8)
     arr = (_native.MatrixDesc * 2)(d, d)
