@@ -39,7 +39,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="gpt103m", choices=["gpt103m", "gpt2048"])
-    ap.add_argument("--s8-mode", default="comp_bf16", choices=["comp_bf16", "fp32"])
+    ap.add_argument("--s8-mode", default="comp_bf16", choices=["comp_bf16", "mixed", "fp32"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: all cores in the affinity mask")
     ap.add_argument("--train", action="store_true",
@@ -446,7 +446,7 @@ def main():
     log(f"timed {args.steps} steps: {ms:.3f} ms/step (hooks {hooks_ms:.3f}, step {step_ms:.3f}, "
         f"S8 GEMM launches {s8_ms:.3f})")
 
-    peak_mfma = BF16_PEAK if args.s8_mode == "comp_bf16" else FP32_PEAK
+    peak_mfma = FP32_PEAK if args.s8_mode == "fp32" else BF16_PEAK  # FP16 and BF16 MFMA share the peak
     stats_gbs = stat_bytes / (hooks_ms * 1e-3) / 1e9
     s8_tfs = s8_issued / (s8_ms * 1e-3) / 1e12
     # The committed counter summary covers the cfg4 step in comp_bf16 mode;
@@ -470,7 +470,7 @@ def main():
     out = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16" if args.s8_mode == "comp_bf16" else "fp32", "data": "synthetic",
+        "vs_baseline": None, "dtype": {"comp_bf16": "bf16", "mixed": "bf16+fp16", "fp32": "fp32"}[args.s8_mode], "data": "synthetic",
         "config": {"workload": ("cfg4: 103M GPT SandMuon step = hook statistics of 8 microbatches x 16x1024 tokens + "
                                 "step() on 54 matrices + AdamW on 39.5M params") if args.config == "gpt103m" else
                    "cfg5: 2048-wide 24-layer GPT, 144 matrices, 4 microbatches x 8x1024 tokens",

@@ -23,8 +23,9 @@
  * process-wide lock, so concurrent callers never share a fork.  Calls whose
  * device buffers overlap (the same workspace, slot rows or parameters)
  * must be ordered by the caller, as for any kernels.  The S8 launch
- * recorder (smx_s8_timing) and the test aids smx_s8_comp_stages and
- * smx_s8_tile_geometry are process-wide settings, not thread-safe.
+ * recorder (smx_s8_timing) and the test aids smx_s8_comp_stages,
+ * smx_s8_comp_mask and smx_s8_tile_geometry are process-wide settings, not
+ * thread-safe.
  *
  * The reference interface each entry point replaces is cited as
  * path:line under pxike/SandMuon.
@@ -39,7 +40,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 2
+#define SMX_ABI_VERSION 3
 
 enum smx_status {
   SMX_OK = 0,
@@ -62,8 +63,19 @@ enum smx_dtype { SMX_F32 = 0, SMX_BF16 = 1, SMX_F16 = 2, SMX_F64 = 3 };
  *   (hi*lo + lo*hi + hi*hi, FP32 accumulation); intermediates are stored as
  *   the BF16 hi/lo pair.  The compensated-product scheme of
  *   reproduction/odl/ops/bf16_compensated_mm_fast.py:18-68, applied to all
- *   five stages. */
-enum smx_s8_mode { SMX_S8_FP32 = 0, SMX_S8_COMP_BF16 = 1 };
+ *   five stages.
+ * SMX_S8_MIXED: stage 1 as SMX_S8_COMP_BF16 (it maps the raw input, whose
+ *   range needs BF16's exponent); stages 2-5 on FP16 operands with FP32
+ *   accumulation (v_mfma_f32_32x32x16_f16, one product per 16 K), except
+ *   the two products of a wide matrix's stage 2 that reach back to the
+ *   input (Q2 = P2 Q1 and X2 = Q2 X0), which stay compensated.  From stage
+ *   2 on every operand is normalised, and FP16 rounds 8x finer than a plain
+ *   BF16 product: measured direction error about 2e-3 against the FP32 map,
+ *   at about half the MFMA work of SMX_S8_COMP_BF16.  No counterpart in the
+ *   reference (whose historical recipe,
+ *   reproduction/odl/ops/dense_s8_compensated_fast.py:53-85, runs stages
+ *   2-5 as plain BF16 products). */
+enum smx_s8_mode { SMX_S8_FP32 = 0, SMX_S8_COMP_BF16 = 1, SMX_S8_MIXED = 2 };
 
 int smx_abi_version(void);
 const char *smx_last_error(void);
@@ -394,6 +406,13 @@ int smx_graft(const float *x, float *out, int64_t n, int64_t output_rows,
  * outside [0, 5] (then nothing changes).
  * ------------------------------------------------------------------ */
 int smx_s8_comp_stages(int32_t k);
+
+/* smx_s8_comp_mask: the same choice per stage (no counterpart in the
+ * reference; a measurement aid): bit k-1 set compensates stage k, a clear
+ * bit makes it the plain BF16 product hi*hi (whose one-hot linear term
+ * keeps the scalar's hi and lo).  0x1f is the production recipe.  Returns
+ * the previous mask, or SMX_EINVAL outside [0, 0x1f]. */
+int smx_s8_comp_mask(int32_t mask);
 
 /* ------------------------------------------------------------------ *
  * Tile geometry of the S8 GEMM launches (no counterpart in the reference;

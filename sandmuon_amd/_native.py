@@ -17,11 +17,11 @@ from typing import Optional, Sequence
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsandmuon_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 SMX_F32, SMX_BF16, SMX_F16, SMX_F64 = 0, 1, 2, 3
-S8_FP32, S8_COMP_BF16 = 0, 1
-S8_MODES = {"fp32": S8_FP32, "comp_bf16": S8_COMP_BF16}
+S8_FP32, S8_COMP_BF16, S8_MIXED = 0, 1, 2
+S8_MODES = {"fp32": S8_FP32, "comp_bf16": S8_COMP_BF16, "mixed": S8_MIXED}
 
 _DTYPES = {torch.float32: SMX_F32, torch.bfloat16: SMX_BF16, torch.float16: SMX_F16}
 
@@ -97,6 +97,7 @@ SIGNATURES = {
                                 c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "smx_graft": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p]),
     "smx_s8_comp_stages": (c_int, [c_int32]),
+    "smx_s8_comp_mask": (c_int, [c_int32]),
     "smx_s8_tile_geometry": (c_int, [c_int32]),
     "smx_s8_timing": (c_int, [c_int32]),
     "smx_s8_timing_read": (c_int32, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(c_int32),
@@ -421,4 +422,13 @@ def s8_comp_stages(k: int) -> int:
     (a measurement aid; 5 is the production recipe); returns the old value."""
     prev = lib().smx_s8_comp_stages(int(k))
     _check(min(prev, 0), "smx_s8_comp_stages")
+    return prev
+
+
+def s8_comp_mask(mask: int) -> int:
+    """Sets which S8 stages of the compensated-BF16 mode are compensated (bit
+    k-1: stage k; the others are plain BF16 products; a measurement aid,
+    0x1f is the production recipe); returns the old mask."""
+    prev = lib().smx_s8_comp_mask(int(mask))
+    _check(min(prev, 0), "smx_s8_comp_mask")
     return prev

@@ -926,7 +926,8 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
   SMX_REQUIRE(n >= 0, SMX_EINVAL, "matrix_step: n < 0");
   if (n == 0) return SMX_OK;
   SMX_REQUIRE(descs && workspace, SMX_EINVAL, "matrix_step: null descriptor table or workspace");
-  SMX_REQUIRE(mode == SMX_S8_FP32 || mode == SMX_S8_COMP_BF16, SMX_EINVAL, "matrix_step: unknown S8 mode");
+  SMX_REQUIRE(mode == SMX_S8_FP32 || mode == SMX_S8_COMP_BF16 || mode == SMX_S8_MIXED, SMX_EINVAL,
+              "matrix_step: unknown S8 mode");
   std::vector<int64_t> rows(n), cols(n);
   for (int32_t i = 0; i < n; ++i) {
     const smx_matrix_desc &d = descs[i];
@@ -996,7 +997,7 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
         j.strips = static_cast<int32_t>(M.strips());
         j.prow_pad = static_cast<int32_t>(M.prow_pad());
         j.pcol_pad = static_cast<int32_t>(M.pcol_pad());
-        j.planes = mode == SMX_S8_COMP_BF16;
+        j.planes = mode != SMX_S8_FP32;  // stage 1 reads X0 compensated in both BF16 modes
         row_geometry(j.d.cols, j.wpr, j.slices);
         j.cvec = j.d.cols % 4 == 0 && aligned16(j.d.inv_col) && (!r1 || aligned16(j.d.z));
         j.wvec = j.cvec && j.d.grad_dtype == SMX_F32 && aligned16(j.d.grad) && aligned16(j.d.momentum);

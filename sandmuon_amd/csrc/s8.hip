@@ -42,9 +42,31 @@
 //                     v_mfma_f32_32x32x16_bf16 (the compensated product of
 //                     reproduction/odl/ops/bf16_compensated_mm_fast.py:
 //                     60-66, applied in all five stages with FP32
-//                     accumulation of every intermediate).  Stages past
-//                     smx_s8_comp_stages(k) (default 5, i.e. none) run as
-//                     kS8HiOnly: the same stored operands, acc += hi*hi.
+//                     accumulation of every intermediate).  Stages whose
+//                     bit is clear in smx_s8_comp_mask (default 0x1f: none)
+//                     run as kS8HiOnly: the same stored operands, acc +=
+//                     hi*hi.
+//   SMX_S8_MIXED      stage 1 (and the two products of a Gram-space class
+//                     that reach back to X0 at stage 2, Q2 = P2 Q1 and X2 =
+//                     Q2 X0) as SMX_S8_COMP_BF16; every other product of
+//                     stages 2-5 as kS8F16: operands stored as FP16 (2 bytes
+//                     per element) and v_mfma_f32_32x32x16_f16 with FP32
+//                     accumulation.  Stage 1 maps the raw input, whose range
+//                     only BF16's exponent holds; from stage 2 on every
+//                     operand is normalised (|X| <= 1, G and P bounded, Q up
+//                     to its eigenvalue range, far below the FP16 maximum),
+//                     where FP16's 11-bit significand rounds 8x finer than a
+//                     plain BF16 product, at a third of the compensated
+//                     MFMAs and half the operand bytes.
+//
+// Operand forms (what a producer writes, chosen by the mode of the product
+// that reads it, out_form): FP32, interleaved BF16 hi/lo ("planes"; the
+// byte size of FP32), or FP16.  An FP16 operand has the row pitch 2 ld
+// bytes; in units of 4 bytes (the unit of the load offsets) it is an
+// operand of ld / 2 columns whose 32-deep K stages move the 64 bytes per
+// row that a 16-deep stage of the 4-byte forms moves, so the row-major
+// loads, the LDS ring and the fragment reads are those of the planes form
+// (chunk h: K 8h .. 8h+7 of the first 16, chunk 2 + h: of the second 16).
 //
 // Block: 256x128 output tile, 4 waves (2 x 2, one per SIMD), each wave
 // 128x64 (4 x 2 MFMA 32x32 tiles, 128 accumulator registers), and two
@@ -59,6 +81,7 @@
 #include <algorithm>
 #include <cmath>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace smx {
@@ -83,11 +106,67 @@ __host__ __device__ constexpr bool gs_sym(int stage) { return stage == 1 || stag
 __host__ __device__ constexpr bool gs_apply_q(int stage) { return stage == 2 || stage == 4 || stage == 5; }
 constexpr int kMaxSeg = 2 * kMaxClasses;
 
-// Internal MFMA mode of a plain BF16 stage of the compensated recipe: the
-// operands in their stored hi/lo form, only the hi*hi product issued.
-constexpr int kS8HiOnly = 2;
-// Stages 1..g_comp_stages of SMX_S8_COMP_BF16 are compensated.
-static int g_comp_stages = 5;
+// Internal MFMA modes of one GEMM launch (the public modes are SMX_S8_FP32,
+// SMX_S8_COMP_BF16 and the recipe SMX_S8_MIXED):
+//   kS8HiOnly  a plain BF16 stage of the compensated recipe: the operands in
+//              their stored hi/lo form, only the hi*hi product issued;
+//   kS8F16     FP16 operands, two 32x32x16 FP16 MFMAs per 32-deep K stage.
+constexpr int kS8HiOnly = 3;
+constexpr int kS8F16 = 4;
+// Bit k-1 set: stage k of SMX_S8_COMP_BF16 is compensated.
+static int g_comp_mask = 0x1f;
+
+// Operand forms.
+enum Form { kFormF32 = 0, kFormPlanes = 1, kFormF16 = 2, kFormAny = 3 };  // kFormAny: an epilogue's run-time choice
+__host__ __device__ constexpr int form_of(int gemm_mode) {
+  return gemm_mode == SMX_S8_FP32 ? kFormF32 : gemm_mode == kS8F16 ? kFormF16 : kFormPlanes;
+}
+
+// The MFMA mode of one product of the map (phase, stage and, for SYM and
+// APPLY, its SegOp) under the run's public `mode` and compensation mask.
+__host__ __device__ constexpr int gemm_mode(int mode, int mask, int phase, int stage, int op) {
+  return mode == SMX_S8_FP32 ? SMX_S8_FP32
+         : mode == SMX_S8_COMP_BF16 ? (((mask >> (stage - 1)) & 1) ? SMX_S8_COMP_BF16 : kS8HiOnly)
+         : (stage == 1 || (phase == kApply && stage == 2 && (op == kOpApplyQ || op == kOpApplyMid)))
+             ? SMX_S8_COMP_BF16
+             : kS8F16;
+}
+
+// The output forms a GEMM kernel of MFMA mode `gm` and phase `phase`
+// compiles (each kernel keeps only these epilogues): a Gram feeds its
+// stage's square (same mode); a square writes FP32 G2 at stage 1, else P
+// for its stage's products (an FP16 square also Q2's compensated P2); the
+// SYM products feed products of their own mode, except the compensated TP
+// of SMX_S8_MIXED's stage 1 (the FP16 stage-2 square); an apply feeds the
+// next stage, X2 or the FP32 result.
+__host__ __device__ constexpr bool form_compiled(int gm, int phase, int form) {
+  return gm == SMX_S8_FP32 ? form == kFormF32
+         : gm == kS8F16 ? (form == kFormF16 || (form == kFormPlanes && phase == kSquare) ||
+                           (form == kFormF32 && phase == kApply))
+         : form == kFormPlanes || (form == kFormF32 && (phase == kSquare || phase == kApply)) ||
+               (form == kFormF16 && gm == SMX_S8_COMP_BF16 && (phase == kSym || phase == kApply));
+}
+
+// The form a product's output is stored in: that of the product that reads
+// it (the Gram feeds its stage's square; the square feeds its stage's apply
+// or Q' = P Q, and at stages 3 and 4 the SYM products of the same mode; PG
+// feeds TP, TP the next stage's square; an iterate feeds the next stage's
+// Gram and apply; Q2 feeds X2, Q4 and Q5 the next Q' and X5; X2 the
+// stage-3 Gram and X5).  The stage-1 square's G2 and the stage-5 result
+// are FP32.
+__host__ __device__ constexpr int out_form(int mode, int mask, int phase, int stage, int op, bool gs) {
+  return phase == kGram ? form_of(gemm_mode(mode, mask, kSquare, stage, -1))
+         : phase == kSquare ? (stage == 1 ? kFormF32
+                                          : form_of(gemm_mode(mode, mask, kApply, stage, gs ? kOpApplyQ : kOpApplyX)))
+         : phase == kPoly1 ? form_of(gemm_mode(mode, mask, kApply, 1, kOpApplyX))
+         : phase == kSym ? (op == kOpPG ? form_of(gemm_mode(mode, mask, kSym, stage, kOpTP))
+                                        : form_of(gemm_mode(mode, mask, kSquare, stage + 1, -1)))
+         : op == kOpApplyX ? (stage == 5 ? kFormF32 : form_of(gemm_mode(mode, mask, kGram, stage + 1, -1)))
+         : op == kOpApplyQ ? form_of(gemm_mode(mode, mask, kApply, stage == 2 ? 2 : 5,
+                                               stage == 2 ? kOpApplyMid : stage == 4 ? kOpApplyQ : kOpApplyFinal))
+         : op == kOpApplyMid ? form_of(gemm_mode(mode, mask, kGram, 3, -1))
+                             : kFormF32;
+}
 // Tile geometry policy (smx_s8_tile_geometry): 0 automatic (pick_geo),
 // 1 256 x 256 tiles for every GEMM launch, 2 never 256 x 256.
 static int g_tile_policy = 0;
@@ -124,6 +203,7 @@ struct Geo {
   static constexpr int kLoadsB = kOpB / 1024 / kWaves;
   static constexpr int kLoadsPerStage = kLoadsA + kLoadsB;
   static constexpr int kKmRow = TN * 4;           // bytes per K row of the K-major B tile
+  static constexpr int kKmRowH = TN * 2;          // the same for FP16 operands (32 K rows per stage)
   static constexpr int kWavesPerEU = TM == 128 ? 3 : 2;
   static constexpr int kGeo = TN == 256 ? kGeoL : TM == 128 ? kGeoS : kGeoM;
 };
@@ -149,6 +229,7 @@ struct StageArgs {
   int32_t n_seg;
   int32_t stage;  // 1..5
   int32_t sq_geo;    // TileGeo of this run's square (the stage-1 Schatten partials are per square tile)
+  int32_t mask;      // compensated stages of SMX_S8_COMP_BF16 (bit k-1: stage k)
   float a, b, c;
   float b_over_c;
 };
@@ -218,18 +299,42 @@ __device__ __forceinline__ TileOffsets<N> tile_offsets(int64_t ld, int64_t row0,
 // wave*N+i, lane l filling slot l.  The slot holds logical chunk
 // slot ^ swzk(k).  The scalar base of a stage at K offset k0 moves by
 // 4*k0*ld bytes.
-template <int N, int KMROW>
+// Chunk swizzle of an FP16 K-major tile (rows of 2 TN bytes, 32 K rows per
+// stage): 0, 6, 12 or 10 from bits 0 and 1 of the K row.  A transposed read
+// of 16 lanes takes 4 consecutive K rows (aligned to 4) and two adjacent
+// chunks of each, 32 lanes four aligned chunks of each; bits 1-2 of the
+// swizzle differ between the 4 rows (the 16 lanes' chunks at distinct
+// positions modulo 8: 32 banks) and so do bits 2-3 (the 32 lanes' chunk
+// groups at distinct positions modulo 16: 64 banks).
+__device__ __forceinline__ int swzh(int k) { return (0xAC60 >> (4 * (k & 3))) & 0xE; }
+
+// (F16: an FP16 operand; ld and n0 are in 4-byte units, i.e. half the
+// element counts, and a stage holds 32 K rows.)
+template <int N, int KMROW, bool F16 = false>
 __device__ __forceinline__ TileOffsets<N> tile_offsets_km(int64_t ld, int64_t n0, int wave) {
-  static_assert(KMROW == 512 || KMROW == 1024, "one or two K rows per 1 KB load");
+  static_assert(KMROW == 256 || KMROW == 512 || KMROW == 1024, "one, two or four K rows per 1 KB load");
   constexpr int kRowsPerLoad = 1024 / KMROW, kSlots = KMROW / 16;
   const int lane = threadIdx.x & 63;
   TileOffsets<N> t;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const int k = kRowsPerLoad * (wave * N + i) + lane / kSlots;
-    t.v[i] = static_cast<uint32_t>((k * ld + n0) * 4 + (((lane % kSlots) ^ swzk(k)) << 4));
+    const int sw = F16 ? swzh(k) : swzk(k);
+    t.v[i] = static_cast<uint32_t>((k * ld + n0) * 4 + (((lane % kSlots) ^ sw) << 4));
   }
   return t;
+}
+
+// A wave-uniform pointer in scalar registers: the direct-to-LDS loads take
+// their base from an SGPR pair, and in some kernels the compiler does not
+// prove a base built from the kernel arguments uniform (it is: every
+// pointer of a tile derives from the block index and kernel arguments).
+// Applied once per tile to the operand bases.
+__device__ __forceinline__ const void *uniform_ptr(const void *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const void *>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 template <int N>
@@ -287,8 +392,9 @@ __device__ __forceinline__ i16x4 read_tr16(lds_char *p) {
 }
 
 // ----------------------------------------------------------- compute ---
-// Register fragments of one 16-deep K stage for this wave's 128 x 128
-// sub-tile: BF16 hi/lo pairs (compensated mode) or FP32 (FP32 mode).  The
+// Register fragments of one K stage for this wave's 128 x 128 sub-tile:
+// BF16 hi/lo pairs (compensated mode, 16 K), FP16 values of K 0-15 and
+// 16-31 (kS8F16, 32 K) or FP32 (FP32 mode, 16 K).  The
 // A fragments of row block i are dead once row i's MFMAs are issued and are
 // reloaded in place with the next stage; the B fragments, used by every
 // row, are double-buffered.
@@ -304,6 +410,8 @@ struct AFrag<SMX_S8_FP32> {
 };
 template <>
 struct AFrag<kS8HiOnly> : AFrag<SMX_S8_COMP_BF16> {};
+template <>
+struct AFrag<kS8F16> : AFrag<SMX_S8_COMP_BF16> {};  // h: K 0-15, l: K 16-31 (FP16 bits)
 template <int MODE>
 struct BFrags;
 template <>
@@ -316,6 +424,13 @@ struct BFrags<SMX_S8_FP32> {
 };
 template <>
 struct BFrags<kS8HiOnly> : BFrags<SMX_S8_COMP_BF16> {};
+template <>
+struct BFrags<kS8F16> : BFrags<SMX_S8_COMP_BF16> {};
+
+// Both 16-byte chunks of a row's K slice are read (the lo plane, or FP16's
+// second 16 K).
+template <int MODE>
+constexpr bool two_chunks() { return MODE == SMX_S8_COMP_BF16 || MODE == kS8F16; }
 
 // LDS -> registers: A row block i, and the four B column blocks, of one
 // stage.  Lane (r, h) takes K = 8h .. 8h+7 of its row: chunks h (hi) and
@@ -327,7 +442,7 @@ __device__ __forceinline__ void load_a(const char *st, int wm, int i, AFrag<MODE
   const int r = wm * (32 * G::kSubM) + i * 32 + lr;
   if constexpr (MODE != SMX_S8_FP32) {
     f.h = read_b16(st, r, lh);
-    if constexpr (MODE == SMX_S8_COMP_BF16) f.l = read_b16(st, r, 2 + lh);
+    if constexpr (two_chunks<MODE>()) f.l = read_b16(st, r, 2 + lh);
   } else {
     read8(st, r, lh, f.v);
   }
@@ -343,7 +458,7 @@ __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) 
     const int r = wn * (32 * kSubN) + j * 32 + lr;
     if constexpr (MODE != SMX_S8_FP32) {
       f.h[j] = read_b16(bt, r, lh);
-      if constexpr (MODE == SMX_S8_COMP_BF16) f.l[j] = read_b16(bt, r, 2 + lh);
+      if constexpr (two_chunks<MODE>()) f.l[j] = read_b16(bt, r, 2 + lh);
     } else {
       read8(bt, r, lh, f.v[j]);
     }
@@ -380,12 +495,53 @@ __device__ __forceinline__ BkmLane bkm_lane() {
   return L;
 }
 
+// FP16 K-major tile (rows of KMROW = 2 TN bytes, 32 K rows per stage).
+// Lane (n, h) needs B[k = 8h .. 8h+7][n] for the first 16 K and B[16 + 8h
+// ..][n] for the second.  Lane s of the 16-lane group g addresses row
+// 8 (g >> 1) + (s >> 2) (+4 for the second read, +16 for the second 16 K)
+// and columns 16 (g & 1) + 4 (s & 3) .. + 3 of each 32-column block j of the
+// wave, i.e. chunk 8 wn + 4 j + 2 (g & 1) + ((s >> 1) & 1) and byte 8 (s & 1)
+// of it; the row's swizzle depends on s alone, so o[j][0] holds the whole
+// per-lane offset of block j (wn included) and the other reads add
+// constants.
+template <int KMROW>
+__device__ __forceinline__ BkmLane bkm_lane_f16(int wn) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, s = lane & 15;
+  const int k = 8 * (g >> 1) + (s >> 2);
+  const int sw = swzh(k);  // the same for rows k + 4, k + 16 and k + 20
+  BkmLane L;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    L.o[j][0] = static_cast<uint32_t>(k * KMROW + 8 * (s & 1) +
+                                      (((8 * wn + 4 * j + 2 * (g & 1) + ((s >> 1) & 1)) ^ sw) << 4));
+    L.o[j][1] = 0;
+  }
+  return L;
+}
+
 template <int MODE, class G>
 __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &f, const BkmLane &L) {
   constexpr int kOpA = G::kOpA, kKmRow = G::kKmRow;
   const int lane = threadIdx.x & 63;
   const char *bt = st + kOpA;
-  if constexpr (MODE != SMX_S8_FP32) {
+  if constexpr (MODE == kS8F16) {
+    static_assert(kSubN == 2, "one lane offset per 32-column block");
+    constexpr int kRow = G::kKmRowH;
+#pragma unroll
+    for (int j = 0; j < kSubN; ++j) {
+      lds_char *q = to_lds(st) + L.o[j][0];
+      asm volatile("" : "+v"(q));
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        lds_char *p = q + (kOpA + 16 * half * kRow);
+        const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * kRow);
+        const bf16x8 v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        if (half == 0) f.h[j] = v;
+        else f.l[j] = v;
+      }
+    }
+  } else if constexpr (MODE != SMX_S8_FP32) {
     // Four base addresses per stage; the empty asm keeps the compiler from
     // pre-adding every read's constant offset into a register of its own
     // (sixteen live registers and two VALU ops per read) instead of using
@@ -429,7 +585,10 @@ __device__ __forceinline__ void load_b_any(const char *st, int wn, BFrags<MODE> 
   else load_b<MODE, G>(st, wn, f);
 }
 
-// MFMAs of row block i: acc[i][j] += A_i B_j^T over the stage's 16 K.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f16x8 as_f16(bf16x8 v) { return __builtin_bit_cast(f16x8, v); }
+
+// MFMAs of row block i: acc[i][j] += A_i B_j^T over the stage's K.
 template <int MODE>
 __device__ __forceinline__ void mma_row(const AFrag<MODE> &a, const BFrags<MODE> &b, f32x16 (&acc)[kSubN]) {
   if constexpr (MODE == SMX_S8_COMP_BF16) {
@@ -443,6 +602,14 @@ __device__ __forceinline__ void mma_row(const AFrag<MODE> &a, const BFrags<MODE>
   } else if constexpr (MODE == kS8HiOnly) {
 #pragma unroll
     for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.h[j], acc[j], 0, 0, 0);
+  } else if constexpr (MODE == kS8F16) {
+    // K 0-15, then K 16-31 of the stage.
+#pragma unroll
+    for (int j = 0; j < kSubN; ++j)
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(a.h), as_f16(b.h[j]), acc[j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kSubN; ++j)
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(a.l), as_f16(b.l[j]), acc[j], 0, 0, 0);
   } else {
     // Lane half h supplies k = 8h + q to MFMA q (the same permutation for
     // both operands, so every k is paired exactly once).
@@ -465,7 +632,20 @@ __device__ __forceinline__ AFrag<MODE> one_hot(float s, int r0) {
   const int lane = threadIdx.x & 63;
   const int e = (lane & 31) - r0 - 8 * (lane >> 5);  // position of k = row - R in this lane's 8
   AFrag<MODE> f;
-  if constexpr (MODE != SMX_S8_FP32) {
+  if constexpr (MODE == kS8F16) {
+    // s as the FP16 pair hi + lo (22 bits), hi in h, lo in l.
+    const _Float16 sh = static_cast<_Float16>(s);
+    const _Float16 sl = static_cast<_Float16>(s - static_cast<float>(sh));
+    const _Float16 z = static_cast<_Float16>(0.f);
+    f16x8 h, l;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      h[q] = q == e ? sh : z;
+      l[q] = q == e ? sl : z;
+    }
+    f.h = __builtin_bit_cast(bf16x8, h);
+    f.l = __builtin_bit_cast(bf16x8, l);
+  } else if constexpr (MODE != SMX_S8_FP32) {
     const __bf16 sh = static_cast<__bf16>(s);
     const __bf16 sl = static_cast<__bf16>(s - static_cast<float>(sh));
     const __bf16 z = static_cast<__bf16>(0.f);
@@ -481,6 +661,35 @@ __device__ __forceinline__ AFrag<MODE> one_hot(float s, int r0) {
   return f;
 }
 
+// acc[i] += s G over the rows of the one-hot window stage: the compensated
+// recipe's three products of the (hi, lo) scalar and B planes; a plain BF16
+// stage the scalar's hi and lo against B's hi plane (a BF16 scalar alone
+// would misscale the linear term of P by up to 2^-9); FP16 the scalar's hi
+// and lo against the stage's first 16 K (rows r0 = 0 .. 15 of the block)
+// and its second 16 K (rows 16 .. 31); FP32 one product.
+template <int MODE>
+__device__ __forceinline__ void mma_one_hot(float s, int sel, const BFrags<MODE> &b, f32x16 (&acc)[kSubN]) {
+  if constexpr (MODE == kS8F16) {
+    const AFrag<MODE> o0 = one_hot<MODE>(s, 0), o1 = one_hot<MODE>(s, 16);
+#pragma unroll
+    for (int j = 0; j < kSubN; ++j) {
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(o0.h), as_f16(b.h[j]), acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(o0.l), as_f16(b.h[j]), acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(o1.h), as_f16(b.l[j]), acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(o1.l), as_f16(b.l[j]), acc[j], 0, 0, 0);
+    }
+  } else if constexpr (MODE == kS8HiOnly) {
+    const AFrag<MODE> o = one_hot<MODE>(s, (sel & 1) * 16);
+#pragma unroll
+    for (int j = 0; j < kSubN; ++j) {
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o.h, b.h[j], acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o.l, b.h[j], acc[j], 0, 0, 0);
+    }
+  } else {
+    mma_row<MODE>(one_hot<MODE>(s, (sel & 1) * 16), b, acc);
+  }
+}
+
 // Issues one stage (A and B tiles) into a ring slot.  `lds` is the slot's
 // LDS byte address plus this wave's first A chunk (wave-uniform); the
 // wave's B chunks start kOpA bytes later, less the difference of the
@@ -492,11 +701,13 @@ struct WaveOffsets {
   TileOffsets<G::kLoadsB> b;
   uint32_t b_lds;  // LDS byte offset of the wave's B chunks from its A chunks
 };
-template <class G, bool BKM>
+// KMSTEP: K rows of a K-major stage per 4-byte unit of k0 (2 for FP16,
+// whose 32-row stages advance k0 by 16).
+template <class G, bool BKM, int KMSTEP>
 __device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const WaveOffsets<G> &o, int64_t k0,
                                             uint32_t lds) {
   dma_tile(o.a, static_cast<const char *>(A.p) + 4 * k0, lds);
-  dma_tile(o.b, static_cast<const char *>(B.p) + 4 * k0 * (BKM ? B.ld : 1), lds + o.b_lds);
+  dma_tile(o.b, static_cast<const char *>(B.p) + 4 * k0 * (BKM ? B.ld * KMSTEP : 1), lds + o.b_lds);
 }
 
 // Waits until at most `pending` stages of this wave's loads are in flight
@@ -530,8 +741,9 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 // barrier makes every wave's loads of kt+1 visible and every wave's reads
 // of kt finished; refill slot kt with stage kt+kStages; MFMAs of stage kt
 // interleaved with the reads of stage kt+1.
-// SEL >= 0: this stage is stage SEL of the wave's 8-stage one_hot window
-// (rows 16 SEL .. 16 SEL + 15 of the wave, accumulator block SEL / 2).
+// SEL >= 0: this stage is stage SEL of the wave's one_hot window (rows
+// 16 SEL .. 16 SEL + 15 of the wave, accumulator block SEL / 2; FP16: rows
+// 32 SEL .. 32 SEL + 31, accumulator block SEL).
 // STEADY: kt + kStages < nk, so a next stage exists, the refill is due and
 // kStages - 2 stages may stay in flight (no run-time conditions).
 template <int MODE, class G, int SEL, int PAR, bool STEADY, bool BKM>
@@ -549,7 +761,8 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Wa
   wait_lds();
   block_barrier();
   if (STEADY || kt + S < nk)
-    issue_stage<G, BKM>(A, B, o, static_cast<int64_t>(kt + S) * kBK, lds0 + (kt % S) * G::kStageBytes);
+    issue_stage<G, BKM, MODE == kS8F16 ? 2 : 1>(A, B, o, static_cast<int64_t>(kt + S) * kBK,
+                                                lds0 + (kt % S) * G::kStageBytes);
   const char *nxt = smem + ((kt + 1) % S) * G::kStageBytes;
   if (more) load_b_any<MODE, G, BKM>(nxt, wn, bf[PAR ^ 1], bl);
   // Raised wave priority while this wave issues its MFMAs, so the
@@ -561,18 +774,23 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Wa
     mma_row<MODE>(af[i], bf[PAR], acc[i]);
     if (more) load_a<MODE, G>(nxt, wm, i, af[i]);
   }
-  if constexpr (SEL >= 0) mma_row<MODE>(one_hot<MODE>(sel_s, (SEL & 1) * 16), bf[PAR], acc[SEL >> 1]);
+  if constexpr (SEL >= 0) mma_one_hot<MODE>(sel_s, SEL, bf[PAR], acc[MODE == kS8F16 ? SEL : SEL >> 1]);
   __builtin_amdgcn_s_setprio(0);
 }
 
 // ACCG: also accumulate sel_s * G over the wave's rows (square phase; A and
 // B are the same symmetric G, K = rows of G).  BKM: B is a K-major
-// row-major operand (C = A B, apply), brow0 its first column.
+// row-major operand (C = A B, apply), brow0 its first column.  Row pitches
+// (ld), K and brow0 are in elements; an FP16 operand (MODE kS8F16) is
+// addressed in 4-byte units, half of each.
 template <int MODE, class G, bool ACCG, bool BKM>
-__device__ __forceinline__ void gemm_tile(const Opnd &A, const Opnd &B, int64_t K, int64_t arow0, int64_t brow0,
+__device__ __forceinline__ void gemm_tile(const Opnd &A_in, const Opnd &B_in, int64_t K, int64_t arow0, int64_t brow0,
                                           float sel_s, char *smem, f32x16 (&acc)[G::kSubM][kSubN]) {
   constexpr int kSubM = G::kSubM;
+  constexpr bool F16 = MODE == kS8F16;
+  constexpr int kU = F16 ? 2 : 1;  // elements per 4-byte unit
   static_assert((kSubM == 4 || kSubM == 2) && kBK == 16, "the one_hot window is 2 kSubM stages of 16 rows");
+  const Opnd A{uniform_ptr(A_in.p), A_in.ld / kU}, B{uniform_ptr(B_in.p), B_in.ld / kU};
   static_assert((8 * kSubN) % 16 == 0, "the wave's K-major column offset must be whole chunk groups");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int wm = wave / G::kWavesN, wn = wave % G::kWavesN;  // 2 x kWavesN waves
@@ -582,17 +800,19 @@ __device__ __forceinline__ void gemm_tile(const Opnd &A, const Opnd &B, int64_t 
     for (int j = 0; j < kSubN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-  const int nk = static_cast<int>(K / kBK);
+  const int nk = static_cast<int>(K / (kBK * kU));
   WaveOffsets<G> o;
   o.a = tile_offsets<G::kLoadsA>(A.ld, arow0, wave);
-  o.b = BKM ? tile_offsets_km<G::kLoadsB, G::kKmRow>(B.ld, brow0, wave) : tile_offsets<G::kLoadsB>(B.ld, brow0, wave);
+  o.b = BKM ? tile_offsets_km<G::kLoadsB, F16 ? G::kKmRowH : G::kKmRow, F16>(B.ld, brow0 / kU, wave)
+            : tile_offsets<G::kLoadsB>(B.ld, brow0, wave);
   o.b_lds = static_cast<uint32_t>(G::kOpA + wave * (G::kLoadsB - G::kLoadsA) * 1024);
-  const BkmLane bl = bkm_lane<G::kKmRow>();  // used by the K-major B path only
+  // used by the K-major B path only
+  const BkmLane bl = F16 ? bkm_lane_f16<G::kKmRowH>(wn) : bkm_lane<G::kKmRow>();
   // LDS byte address of the ring plus this wave's first A chunk.
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * G::kLoadsA * 1024;
 #pragma unroll
   for (int s = 0; s < kStages; ++s)
-    if (s < nk) issue_stage<G, BKM>(A, B, o, static_cast<int64_t>(s) * kBK, lds0 + s * G::kStageBytes);
+    if (s < nk) issue_stage<G, BKM, kU>(A, B, o, static_cast<int64_t>(s) * kBK, lds0 + s * G::kStageBytes);
   wait_stages<G>(min(kStages - 1, nk - 1));
   block_barrier();
   AFrag<MODE> af[kSubM];
@@ -617,22 +837,25 @@ __device__ __forceinline__ void gemm_tile(const Opnd &A, const Opnd &B, int64_t 
   };
   int kt = 0;
   if constexpr (ACCG) {
-    // The wave's rows are K stages kt0 .. kt0 + 2 kSubM - 1 (kt0 = first
-    // row / 16, a multiple of 4, so the stage parity matches the unrolled
+    // The wave's rows are K stages kt0 .. kt0 + kWin - 1 (kt0 = first row /
+    // 16, or / 32 for FP16: even, so the stage parity matches the unrolled
     // pairs).
-    const int kt0 = static_cast<int>((arow0 + wm * (32 * kSubM)) / kBK);
+    constexpr int kWin = (F16 ? 1 : 2) * kSubM;
+    const int kt0 = static_cast<int>((arow0 + wm * (32 * kSubM)) / (kBK * kU));
     run(kt, kt0);
     SMX_PIPE(0, 0, kt0, false);
     SMX_PIPE(1, 1, kt0 + 1, false);
-    SMX_PIPE(2, 0, kt0 + 2, false);
-    SMX_PIPE(3, 1, kt0 + 3, false);
-    if constexpr (kSubM == 4) {
+    if constexpr (kWin >= 4) {
+      SMX_PIPE(2, 0, kt0 + 2, false);
+      SMX_PIPE(3, 1, kt0 + 3, false);
+    }
+    if constexpr (kWin == 8) {
       SMX_PIPE(4, 0, kt0 + 4, false);
       SMX_PIPE(5, 1, kt0 + 5, false);
       SMX_PIPE(6, 0, kt0 + 6, false);
       SMX_PIPE(7, 1, kt0 + 7, false);
     }
-    kt = kt0 + 2 * kSubM;
+    kt = kt0 + kWin;
   }
   run(kt, nk);
 #undef SMX_PIPE
@@ -741,7 +964,6 @@ s8_stage_kernel(StageArgs args) {
   __shared__ __attribute__((aligned(16))) char smem[Gm::kRingBytes];
   __shared__ double dscratch[16];
   __shared__ double bcast;
-  constexpr bool PL = MODE != SMX_S8_FP32;  // operands stored as interleaved BF16
 
   const TileRef ref = tile_of(args);
   const S8Class &K = *ref.k;
@@ -871,28 +1093,25 @@ s8_stage_kernel(StageArgs args) {
   const bool last = stage == 5;
   float *dst_t, *dst_m;
   int64_t ld_t, ld_m;
-  bool pl_t, pl_m, do_t, do_m;
+  bool do_t, do_m;
+  // The output's form is that of the product that reads it (out_form); a
+  // transposed stage-5 result (dst_m) is FP32 as the stage-5 form is.
+  const int form = out_form(args.L.mode, args.mask, PHASE, stage, ref.op, K.gs != 0);
   if constexpr (PHASE == kApply) {
     if (ref.op == kOpApplyQ) {
       dst_t = q_out; ld_t = K.rp;
       dst_m = nullptr; ld_m = K.rp;
-      pl_t = PL;
-      pl_m = false;
       do_t = true;
       do_m = false;
     } else if (ref.op == kOpApplyMid) {
       dst_t = M.x1(); ld_t = K.cp;  // X2, an operand of the stage-3 Gram and the final apply
       dst_m = nullptr; ld_m = K.rp;
-      pl_t = PL;
-      pl_m = false;
       do_t = true;
       do_m = false;
     } else {
       const bool xf = last && M.flip();
       dst_t = ref.op == kOpApplyFinal ? M.x0() : x_out; ld_t = K.cp;
       dst_m = xf ? M.xf() : nullptr; ld_m = K.rp;
-      pl_t = PL && !last;
-      pl_m = false;
       do_t = !xf;
       do_m = xf;
     }
@@ -901,7 +1120,6 @@ s8_stage_kernel(StageArgs args) {
     float *sq_out = K.gs && stage == 3 ? M.qa() : M.p();
     dst_t = dst_m = PHASE == kSym ? sym_out : PHASE == kGram ? M.g() : sq_out;
     ld_t = ld_m = K.rp;
-    pl_t = pl_m = PL && (PHASE != kSquare || stage != 1);
     do_t = true;
     do_m = !diag;
   }
@@ -972,11 +1190,15 @@ s8_stage_kernel(StageArgs args) {
     for (int k = 0; k < 3; ++k) r[k] = 0.f;
   };
   // Row `row` of a staged block (S) to global row gr, columns gc0 .. gc0 + 31
-  // (gc0 a multiple of 32): one 16-byte store per lane.
-  auto put_row = [&](const float *S, int row, int64_t gr, int64_t gc0, float *dst, int64_t ld, bool pl,
+  // (gc0 a multiple of 32) in form FM: one 16-byte store per lane (FP32,
+  // planes), or one 8-byte store of the lane's four columns (FP16: the
+  // row's 64 bytes).
+  // (FM = kFormAny: planes or FP32 chosen at run time by `form`, one loop
+  // for both: the compensated square's stage-1 G2 and later P.)
+  auto put_row = [&](auto fm_c, const float *S, int row, int64_t gr, int64_t gc0, float *dst, int64_t ld,
                      float (&r)[3], bool acc_r) {
-    char *out = reinterpret_cast<char *>(dst) + (gr * ld + gc0) * 4 + 16 * ech;
-    if (pl) {
+    constexpr int FM = decltype(fm_c)::value;
+    if (FM == kFormPlanes || (FM == kFormAny && form == kFormPlanes)) {
       float w[8];
       ep_read8(S, row, ec8, w);
       if (eye)
@@ -990,7 +1212,8 @@ s8_stage_kernel(StageArgs args) {
         const uint16_t x1 = lo_plane ? bf16_lo_bits(w[2 * e + 1]) : bf16_bits(w[2 * e + 1]);
         b[e] = x0 | (static_cast<uint32_t>(x1) << 16);
       }
-      *reinterpret_cast<uint4 *>(out) = make_uint4(b[0], b[1], b[2], b[3]);
+      *reinterpret_cast<uint4 *>(reinterpret_cast<char *>(dst) + (gr * ld + gc0) * 4 + 16 * ech) =
+          make_uint4(b[0], b[1], b[2], b[3]);
     } else {
       const f32x4 v4 = *reinterpret_cast<const f32x4 *>(S + row * kEpStride + ec4);
       float w[4] = {v4.x, v4.y, v4.z, v4.w};
@@ -998,41 +1221,74 @@ s8_stage_kernel(StageArgs args) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (gr == gc0 + ec4 + e && gr < K.r) w[e] += args.a;
-      *reinterpret_cast<float4 *>(out) = make_float4(w[0], w[1], w[2], w[3]);
-      if (acc_r) accum4(w, gc0 + ec4, r);
+      if constexpr (FM == kFormF16) {
+        uint32_t b[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          b[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(w[2 * e]))) |
+                 (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(w[2 * e + 1]))) << 16);
+        *reinterpret_cast<uint2 *>(reinterpret_cast<char *>(dst) + (gr * ld + gc0 + ec4) * 2) =
+            make_uint2(b[0], b[1]);
+      } else {
+        *reinterpret_cast<float4 *>(reinterpret_cast<char *>(dst) + (gr * ld + gc0) * 4 + 16 * ech) =
+            make_float4(w[0], w[1], w[2], w[3]);
+        if (acc_r) accum4(w, gc0 + ec4, r);
+      }
     }
   };
+  // The block loop, specialised for the output form (one copy per form the
+  // launch's mode can produce, so that each keeps only its own registers).
+  auto epilogue = [&](auto fm_c) {
+    constexpr int FM = decltype(fm_c)::value;
+    const bool rs_on = FM == kFormF32 && rsum;  // the row sums come with the FP32 result only
 #pragma unroll
-  for (int blk = 0; blk < kSubM * kSubN; ++blk) {
-    const int i = blk / kSubN, j = blk % kSubN;
+    for (int blk = 0; blk < kSubM * kSubN; ++blk) {
+      const int i = blk / kSubN, j = blk % kSubN;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      f32x4 v;
+      for (int k = 0; k < 4; ++k) {
+        f32x4 v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v[q] = acc[i][j][4 * k + q] * scale;
+          // stage 1's FP32 G2: its squared entries feed the Schatten scale
+          if constexpr (PHASE == kSquare && (FM == kFormF32 || FM == kFormAny)) sq_local = fmaf(v[q], v[q], sq_local);
+          T[(8 * k + 4 * lh + q) * kEpStride + lr] = v[q];
+        }
+        if (do_m) *reinterpret_cast<f32x4 *>(U + lr * kEpStride + 8 * k + 4 * lh) = v;
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        v[q] = acc[i][j][4 * k + q] * scale;
-        if constexpr (PHASE == kSquare) sq_local = fmaf(v[q], v[q], sq_local);  // used in stage 1
-        T[(8 * k + 4 * lh + q) * kEpStride + lr] = v[q];
+        const int row = er + 8 * q;
+        if (do_t) {
+          const int64_t gr = R0 + i * 32 + row;
+          put_row(fm_c, T, row, gr, C0 + j * 32, dst_t, ld_t, rs[0][q], rs_on);
+          if (rs_on && j == kSubN - 1) emit(gr, C0 / kStripT, rs[0][q]);
+        }
+        if (do_m) {
+          const int64_t gr = C0 + j * 32 + row;
+          put_row(fm_c, U, row, gr, R0 + i * 32, dst_m, ld_m, rs[j][q], rs_on);
+          if (rs_on && i == kSubM - 1) emit(gr, R0 / kStripM, rs[j][q]);
+        }
       }
-      if (do_m) *reinterpret_cast<f32x4 *>(U + lr * kEpStride + 8 * k + 4 * lh) = v;
+      // Keep the scheduler from hoisting every accumulator read to the top
+      // of the epilogue (the values would not fit in the VGPRs).
+      __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int row = er + 8 * q;
-      if (do_t) {
-        const int64_t gr = R0 + i * 32 + row;
-        put_row(T, row, gr, C0 + j * 32, dst_t, ld_t, pl_t, rs[0][q], rsum);
-        if (rsum && j == kSubN - 1) emit(gr, C0 / kStripT, rs[0][q]);
-      }
-      if (do_m) {
-        const int64_t gr = C0 + j * 32 + row;
-        put_row(U, row, gr, R0 + i * 32, dst_m, ld_m, pl_m, rs[j][q], rsum);
-        if (rsum && i == kSubM - 1) emit(gr, R0 / kStripM, rs[j][q]);
-      }
-    }
-    // Keep the scheduler from hoisting every accumulator read to the top
-    // of the epilogue (the values would not fit in the VGPRs).
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Only the forms this launch kind can produce are compiled (the host
+  // checks every launch's forms against the same table, form_compiled).
+  constexpr bool kPlanes = form_compiled(MODE, PHASE, kFormPlanes);
+  constexpr bool kF16 = form_compiled(MODE, PHASE, kFormF16);
+  constexpr bool kF32 = form_compiled(MODE, PHASE, kFormF32);
+  if constexpr (PHASE == kSquare && kPlanes && kF32 && !kF16) {
+    epilogue(std::integral_constant<int, kFormAny>{});
+  } else if (kPlanes && form == kFormPlanes) {
+    if constexpr (kPlanes) epilogue(std::integral_constant<int, kFormPlanes>{});
+  } else if (kF16 && form == kFormF16) {
+    if constexpr (kF16) epilogue(std::integral_constant<int, kFormF16>{});
+  } else {
+    if constexpr (kF32) epilogue(std::integral_constant<int, kFormF32>{});
   }
   if constexpr (PHASE == kSquare) {
     if (stage == 1) {
@@ -1170,11 +1426,10 @@ static int timing_end(int slot, hipStream_t st, int phase, double flops) {
   return SMX_OK;
 }
 
-// The MFMA mode of a stage: FP32, compensated, or (compensated recipe,
-// stages past g_comp_stages) hi*hi only.
-static int stage_mode(const S8Layout &Lay, int stage) {
-  if (Lay.mode != SMX_S8_COMP_BF16) return SMX_S8_FP32;
-  return stage <= g_comp_stages ? SMX_S8_COMP_BF16 : kS8HiOnly;
+// The MFMA mode of one product of a launch (gemm_mode under the run's mode
+// and the process-wide compensation mask).
+static int seg_mode(const S8Layout &Lay, int phase, int stage, int op) {
+  return gemm_mode(Lay.mode, g_comp_mask, phase, stage, op);
 }
 
 // The segments of one launch, in class order by per-tile cost (K length,
@@ -1228,14 +1483,19 @@ static std::vector<Seg> launch_segments(const S8Layout &Lay, const SlotSet &set,
   return segs;
 }
 
-// MFMA FLOPs of one launch: computed tiles x 2 * TM * TN * K (x3 for a
-// compensated stage), plus the square phase's one-hot MFMAs (2 kSubM stages
-// of kSubN 32x32x16 products per wave).
-static double launch_flops(const S8Layout &Lay, int phase, int stage, int geo, const std::vector<Seg> &segs) {
+// MFMA FLOPs of one launch in MFMA mode `mode`: computed tiles x 2 * TM *
+// TN * K (x3 compensated), plus the square phase's one-hot MFMAs: per wave
+// and 32x32 column tile, 2 kSubM window stages of 3 (compensated), 2
+// (plain BF16: the scalar's hi and lo) or 1 (FP32) 16-deep products, or
+// kSubM stages of 4 (FP16: hi and lo over each 16 K of a 32-deep stage).
+static double launch_flops(int mode, int phase, int stage, int geo, const S8Layout &Lay,
+                           const std::vector<Seg> &segs) {
   if (phase == kPoly1) return 0.0;
-  const double prod = stage_mode(Lay, stage) == SMX_S8_COMP_BF16 ? 3.0 : 1.0;
+  const double prod = mode == SMX_S8_COMP_BF16 ? 3.0 : 1.0;
   const int tm = geo == kGeoS ? 128 : 256, tn = geo == kGeoL ? 256 : 128, waves = geo == kGeoL ? 8 : 4;
   const int sub_m = tm / 64;
+  const double onehot = mode == SMX_S8_COMP_BF16 ? 6.0 * sub_m : mode == kS8HiOnly ? 4.0 * sub_m
+                        : mode == kS8F16 ? 4.0 * sub_m : 2.0 * sub_m;
   double f = 0.0;
   for (const Seg &sg : segs) {
     const S8Class &k = Lay.cls[sg.cls];
@@ -1243,9 +1503,7 @@ static double launch_flops(const S8Layout &Lay, int phase, int stage, int geo, c
     const double K = phase == kGram ? static_cast<double>(k.cp) : static_cast<double>(k.rp);
     const double cnt = sg.hi - sg.lo;
     f += cnt * tiles * 2.0 * tm * tn * K * prod;
-    // one-hot: per wave 2 kSubM stages of kSubN MFMA tiles
-    if (phase == kSquare && stage != 1)
-      f += cnt * tiles * waves * (2.0 * sub_m) * kSubN * 2.0 * 32 * 32 * kBK * prod;
+    if (phase == kSquare && stage != 1) f += cnt * tiles * waves * onehot * kSubN * 2.0 * 32 * 32 * kBK;
   }
   return f;
 }
@@ -1302,59 +1560,79 @@ static void launch_stage(int geo, int32_t blocks, const StageArgs &a, hipStream_
 }
 
 // sq_geo: the geometry of the run's square launches (the stage-1 Schatten
-// partials are per square tile).
+// partials are per square tile).  The segments of a phase whose products
+// run in different MFMA modes (SMX_S8_MIXED at stage 2: X' = P X in FP16,
+// Q2 = P2 Q1 compensated) go to one launch per mode.
 template <int PHASE>
 static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, int sq_geo, hipStream_t st, double &flops,
                         const std::vector<int> &ops = {}) {
-  StageArgs a{};
-  a.L = Lay;
-  a.stage = stage;
-  a.sq_geo = sq_geo;
-  const auto &co = kS8Coefficients[stage - 1];
-  a.a = static_cast<float>(co[0]);
-  a.b = static_cast<float>(co[1]);
-  a.c = static_cast<float>(co[2]);
-  a.b_over_c = static_cast<float>(co[1] / co[2]);
-  const std::vector<Seg> segs = launch_segments(Lay, set, PHASE, stage, ops);
-  if (static_cast<int>(segs.size()) > kMaxSeg) return fail(SMX_EINVAL, "s8: too many launch segments");
-  const int geo = PHASE == kSquare ? sq_geo : PHASE == kPoly1 ? kGeoM : pick_geo(Lay, PHASE, segs, PHASE != kApply);
-  int32_t off = 0;
-  a.n_seg = 0;
-  for (const Seg &sg : segs) {
-    const S8Class &k = Lay.cls[sg.cls];
-    const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE, geo, sg.op);
-    const int64_t nt = round_up(tpm * (sg.hi - sg.lo), 8);
+  const std::vector<Seg> all = launch_segments(Lay, set, PHASE, stage, ops);
+  std::vector<int> modes;
+  for (const Seg &sg : all) {
+    const int m = seg_mode(Lay, PHASE, stage, sg.op);
+    if (std::find(modes.begin(), modes.end(), m) == modes.end()) modes.push_back(m);
+  }
+  for (const int mode : modes) {
+    std::vector<Seg> segs;
+    for (const Seg &sg : all)
+      if (seg_mode(Lay, PHASE, stage, sg.op) == mode) segs.push_back(sg);
+    StageArgs a{};
+    a.L = Lay;
+    a.stage = stage;
+    a.sq_geo = sq_geo;
+    a.mask = g_comp_mask;
+    const auto &co = kS8Coefficients[stage - 1];
+    a.a = static_cast<float>(co[0]);
+    a.b = static_cast<float>(co[1]);
+    a.c = static_cast<float>(co[2]);
+    a.b_over_c = static_cast<float>(co[1] / co[2]);
+    if (static_cast<int>(segs.size()) > kMaxSeg) return fail(SMX_EINVAL, "s8: too many launch segments");
+    if (PHASE != kPoly1)
+      for (const Seg &sg : segs)
+        if (!form_compiled(mode, PHASE, out_form(Lay.mode, g_comp_mask, PHASE, stage, sg.op, Lay.cls[sg.cls].gs != 0)))
+          return fail(SMX_EINVAL, "s8: no epilogue for the output form of this product");
+    const int geo =
+        PHASE == kSquare ? sq_geo : PHASE == kPoly1 ? kGeoM : pick_geo(Lay, PHASE, segs, PHASE != kApply);
+    int32_t off = 0;
+    a.n_seg = 0;
+    for (const Seg &sg : segs) {
+      const S8Class &k = Lay.cls[sg.cls];
+      const int64_t tpm = PHASE == kPoly1 ? poly_blocks_per_matrix(k) : phase_tiles(k, PHASE, geo, sg.op);
+      const int64_t nt = round_up(tpm * (sg.hi - sg.lo), 8);
+      a.seg_off[a.n_seg] = off;
+      a.seg_cls[a.n_seg] = sg.cls;
+      a.seg_op[a.n_seg] = sg.op;
+      a.seg_slot0[a.n_seg] = sg.lo;
+      a.seg_cnt[a.n_seg] = sg.hi - sg.lo;
+      ++a.n_seg;
+      off += static_cast<int32_t>(nt);
+    }
     a.seg_off[a.n_seg] = off;
-    a.seg_cls[a.n_seg] = sg.cls;
-    a.seg_op[a.n_seg] = sg.op;
-    a.seg_slot0[a.n_seg] = sg.lo;
-    a.seg_cnt[a.n_seg] = sg.hi - sg.lo;
-    ++a.n_seg;
-    off += static_cast<int32_t>(nt);
+    if (off == 0) continue;
+    int slot = -1;
+    int rc = timing_begin(st, slot, false);
+    if (rc) return rc;
+    if constexpr (PHASE == kPoly1) {
+      if (mode != SMX_S8_FP32)
+        hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_COMP_BF16>, dim3(off), dim3(256), 0, st, a);
+      else
+        hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_FP32>, dim3(off), dim3(256), 0, st, a);
+      rc = check_launch("s8 stage-1 polynomial");
+    } else {
+      if (mode == SMX_S8_COMP_BF16) launch_stage<SMX_S8_COMP_BF16, PHASE>(geo, off, a, st);
+      else if (mode == kS8HiOnly) launch_stage<kS8HiOnly, PHASE>(geo, off, a, st);
+      else if (mode == kS8F16) launch_stage<kS8F16, PHASE>(geo, off, a, st);
+      else launch_stage<SMX_S8_FP32, PHASE>(geo, off, a, st);
+      rc = check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : PHASE == kSym ? "s8 sym"
+                                                                                                  : "s8 apply");
+    }
+    if (rc) return rc;
+    const double f = launch_flops(mode, PHASE, stage, geo, Lay, segs);
+    flops += f;
+    rc = timing_end(slot, st, PHASE, f);
+    if (rc) return rc;
   }
-  a.seg_off[a.n_seg] = off;
-  if (off == 0) return SMX_OK;
-  const int mode = stage_mode(Lay, stage);
-  int slot = -1;
-  int rc = timing_begin(st, slot, false);
-  if (rc) return rc;
-  if constexpr (PHASE == kPoly1) {
-    if (mode != SMX_S8_FP32)
-      hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_COMP_BF16>, dim3(off), dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL(s8_poly1_kernel<SMX_S8_FP32>, dim3(off), dim3(256), 0, st, a);
-    rc = check_launch("s8 stage-1 polynomial");
-  } else {
-    if (mode == SMX_S8_COMP_BF16) launch_stage<SMX_S8_COMP_BF16, PHASE>(geo, off, a, st);
-    else if (mode == kS8HiOnly) launch_stage<kS8HiOnly, PHASE>(geo, off, a, st);
-    else launch_stage<SMX_S8_FP32, PHASE>(geo, off, a, st);
-    rc = check_launch(PHASE == kGram ? "s8 gram" : PHASE == kSquare ? "s8 square" : PHASE == kSym ? "s8 sym"
-                                                                                                : "s8 apply");
-  }
-  if (rc) return rc;
-  const double f = launch_flops(Lay, PHASE, stage, geo, segs);
-  flops += f;
-  return timing_end(slot, st, PHASE, f);
+  return SMX_OK;
 }
 
 // Stage `stage` of the S8 map over the matrices of `set`: one launch per
@@ -1570,8 +1848,16 @@ using smx::g_timing;
 
 extern "C" int smx_s8_comp_stages(int32_t k) {
   SMX_REQUIRE(k >= 0 && k <= 5, SMX_EINVAL, "s8 compensated stages: k must be in [0, 5]");
-  const int prev = smx::g_comp_stages;
-  smx::g_comp_stages = k;
+  int prev = 0;  // leading compensated stages of the previous mask
+  while (prev < 5 && ((smx::g_comp_mask >> prev) & 1)) ++prev;
+  smx::g_comp_mask = (1 << k) - 1;
+  return prev;
+}
+
+extern "C" int smx_s8_comp_mask(int32_t mask) {
+  SMX_REQUIRE(mask >= 0 && mask <= 0x1f, SMX_EINVAL, "s8 compensation mask: must be in [0, 0x1f]");
+  const int prev = smx::g_comp_mask;
+  smx::g_comp_mask = mask;
   return prev;
 }
 

@@ -104,7 +104,8 @@ extern "C" int smx_s8(const float *x, float *out, int64_t batch, int64_t rows, i
                       int64_t row_stride, int64_t col_stride, int mode, void *workspace, size_t workspace_bytes,
                       void *stream) {
   SMX_REQUIRE(x && out, SMX_EINVAL, "s8: null pointer");
-  SMX_REQUIRE(mode == SMX_S8_FP32 || mode == SMX_S8_COMP_BF16, SMX_EINVAL, "s8: unknown mode");
+  SMX_REQUIRE(mode == SMX_S8_FP32 || mode == SMX_S8_COMP_BF16 || mode == SMX_S8_MIXED, SMX_EINVAL,
+              "s8: unknown mode");
   SMX_REQUIRE(batch >= 0 && rows >= 0 && cols >= 0, SMX_ESHAPE, "s8: negative shape");
   SMX_REQUIRE(batch <= 65535, SMX_ESHAPE, "s8: batch must be <= 65535");
   if (batch == 0 || rows == 0 || cols == 0) return SMX_OK;
@@ -123,7 +124,7 @@ extern "C" int smx_s8(const float *x, float *out, int64_t batch, int64_t rows, i
   a.sb = batch_stride;
   a.sr = row_stride;
   a.sc = col_stride;
-  a.planes = mode == SMX_S8_COMP_BF16;
+  a.planes = mode != SMX_S8_FP32;  // stage 1 reads X0 compensated in both BF16 modes
   const S8Mat M0{a.k, 0};
   const unsigned tiles = static_cast<unsigned>((M0.prow_pad() / 64) * (M0.pcol_pad() / 64));
   hipLaunchKernelGGL(s8_load_norm_kernel, dim3(1, batch), dim3(256), 0, st, a);

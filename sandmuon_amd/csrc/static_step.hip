@@ -52,7 +52,8 @@ extern "C" int smx_matrix_step_static(const smx_matrix_desc *descs, int32_t n, i
   SMX_REQUIRE(n >= 0, SMX_EINVAL, "matrix_step_static: n < 0");
   if (n == 0) return SMX_OK;
   SMX_REQUIRE(descs, SMX_EINVAL, "matrix_step_static: null descriptor table");
-  SMX_REQUIRE(mode == SMX_S8_FP32 || mode == SMX_S8_COMP_BF16, SMX_EINVAL, "matrix_step_static: unknown S8 mode");
+  SMX_REQUIRE(mode == SMX_S8_FP32 || mode == SMX_S8_COMP_BF16 || mode == SMX_S8_MIXED, SMX_EINVAL,
+              "matrix_step_static: unknown S8 mode");
   std::vector<int64_t> rows(n), cols(n);
   for (int32_t i = 0; i < n; ++i) {
     SMX_REQUIRE(descs[i].rows >= 1 && descs[i].cols >= 1, SMX_ESHAPE,

@@ -52,7 +52,7 @@ def per_matrix_rel(a, b):
     return ((a - b).flatten(-2).norm(dim=-1) / b.flatten(-2).norm(dim=-1)).tolist()
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_s8_full_cfg2_batch(device, mode):
     worst = 0.0
     for seed, shape in ((1002, (36, 768, 768)), (1003, (9, 3072, 768)), (1004, (9, 768, 3072))):
@@ -65,7 +65,7 @@ def test_s8_full_cfg2_batch(device, mode):
     print(f"cfg2 {mode}: worst per-matrix rel err {worst:.3e}")
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 @pytest.mark.parametrize("shape", [(2, 2048, 2048), (1, 2048, 8192), (1, 8192, 2048)])
 def test_s8_cfg5_shapes(device, mode, shape):
     """At K = 2048 the eager FP32 path itself is 1.1e-4 to 1.6e-4 (relative
