@@ -46,6 +46,9 @@ def parse():
                     help="time whole training steps instead (model forward/backward of 8 microbatches under bf16 "
                          "autocast + step()), with the hook statistics, with the fused statistics, and with "
                          "no statistics; prints its own JSON line")
+    ap.add_argument("--mfma-peak", action="store_true",
+                    help="only run the MFMA peak probe (dense BF16, FP16 and FP32 MFMAs from registers on every "
+                         "SIMD; sustained TFLOP/s and the engine clock held) and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run 3 plain device copies of MB megabytes (the known-size reference for "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -73,6 +76,18 @@ def copy_calibration(mb):
     us = a.elapsed_time(b) / 20 * 1e3
     print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 3, "timed_copies": 20, "us_per_copy": round(us, 1),
                       "read_write_tb_s": round(2 * n * 4 / us / 1e6, 3)}), flush=True)
+
+
+def mfma_peak_probe(device) -> dict:
+    """Sustained dense MFMA rates (smx_mfma_peak: 4 blocks of 8 waves per CU,
+    register operands, about 30 ms per dtype) and the clock held: the
+    measured denominators beside the nominal 2.5 PFLOP/s (BF16/FP16) and
+    157.3 TFLOP/s (FP32) peaks, which assume 2.4 GHz."""
+    from sandmuon_amd import _native
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    return {name: _native.mfma_peak(dt, iters, device, blocks=4 * cus)
+            for name, dt, iters in (("bf16", torch.bfloat16, 40000), ("fp16", torch.float16, 40000),
+                                    ("fp32", torch.float32, 20000))}
 
 
 # ------------------------------------------------------------ workload ---
@@ -381,6 +396,10 @@ def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.mfma_peak:
+        sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+        print(json.dumps({"mfma_peak_probe": mfma_peak_probe(torch.device("cuda", 0))}), flush=True)
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -415,6 +415,22 @@ int smx_s8_comp_stages(int32_t k);
 int smx_s8_comp_mask(int32_t mask);
 
 /* ------------------------------------------------------------------ *
+ * MFMA peak probe (no counterpart in the reference; a measurement aid for
+ * the roofline denominators).  `blocks` blocks of 512 threads (8 waves,
+ * two per SIMD) each issue `iters` rounds of 4 independent dense MFMAs on
+ * register operands, no memory traffic: v_mfma_f32_32x32x16_bf16 (dtype
+ * SMX_BF16) or _f16 (SMX_F16), 32768 FLOP each, or
+ * v_mfma_f32_32x32x2_f32 (SMX_F32), 4096 FLOP each.  Lane 0 of each block
+ * writes times[4*b .. 4*b+3] = s_memtime at start and end (engine clock
+ * cycles), then s_memrealtime at start and end (a 100 MHz counter), from
+ * which the caller derives the clock held under the load; sink receives
+ * blocks*512 floats that depend on every MFMA.  Enqueues on `stream`; the
+ * caller times it (events).
+ * ------------------------------------------------------------------ */
+int smx_mfma_peak(int32_t dtype, int32_t blocks, int64_t iters,
+                  uint64_t *times, float *sink, void *stream);
+
+/* ------------------------------------------------------------------ *
  * Tile geometry of the S8 GEMM launches (no counterpart in the reference;
  * a test and measurement aid).  0 (the default): each launch picks its
  * tiles from its size (256 x 256 blocks of 8 waves for launches that fill

@@ -99,6 +99,7 @@ SIGNATURES = {
     "smx_s8_comp_stages": (c_int, [c_int32]),
     "smx_s8_comp_mask": (c_int, [c_int32]),
     "smx_s8_tile_geometry": (c_int, [c_int32]),
+    "smx_mfma_peak": (c_int, [c_int32, c_int32, c_int64, c_void_p, c_void_p, c_void_p]),
     "smx_s8_timing": (c_int, [c_int32]),
     "smx_s8_timing_read": (c_int32, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(c_int32),
                                      ctypes.POINTER(c_double), c_int32]),
@@ -432,3 +433,33 @@ def s8_comp_mask(mask: int) -> int:
     prev = lib().smx_s8_comp_mask(int(mask))
     _check(min(prev, 0), "smx_s8_comp_mask")
     return prev
+
+
+def mfma_peak(dtype: torch.dtype, iters: int, device, blocks: Optional[int] = None) -> dict:
+    """The MFMA peak probe (smx_mfma_peak): dense MFMAs from registers on
+    every SIMD of the device (blocks = one per CU by default), timed with
+    events on the current stream.  Returns the sustained TFLOP/s, the engine
+    clock held (GHz, from s_memtime against the 100 MHz s_memrealtime) and
+    the nominal rate at that clock (4096 BF16/FP16 or 256 FP32 FLOP per
+    clock per CU)."""
+    code = {torch.float32: SMX_F32, torch.bfloat16: SMX_BF16, torch.float16: SMX_F16}[dtype]
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    blocks = blocks or cus
+    times = torch.zeros(blocks * 4, dtype=torch.int64, device=device)
+    sink = torch.empty(blocks * 512, dtype=torch.float32, device=device)
+    st = stream_of(device)
+    _check(lib().smx_mfma_peak(code, blocks, 1, times.data_ptr(), sink.data_ptr(), st), "smx_mfma_peak")  # warm
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    _check(lib().smx_mfma_peak(code, blocks, int(iters), times.data_ptr(), sink.data_ptr(), st), "smx_mfma_peak")
+    b.record()
+    torch.cuda.synchronize(device)
+    ms = a.elapsed_time(b)
+    per_mfma = 4096 if code == SMX_F32 else 32768
+    flops = blocks * 8 * 4 * int(iters) * per_mfma
+    t = times.view(blocks, 4).cpu().double()
+    ghz = float(((t[:, 1] - t[:, 0]) / (t[:, 3] - t[:, 2])).median()) * 0.1
+    per_clk = 256 if code == SMX_F32 else 4096
+    return {"tflops": round(flops / (ms * 1e-3) / 1e12, 1), "clock_ghz": round(ghz, 3),
+            "nominal_tflops_at_clock": round(cus * per_clk * ghz * 1e9 / 1e12, 1), "ms": round(ms, 3),
+            "blocks": blocks, "iters": int(iters), "finite": bool(torch.isfinite(sink).all())}

@@ -157,6 +157,17 @@ def test_compensated_stage_count_setting():
     assert lib.smx_s8_comp_stages(5) == 5
 
 
+def test_compensation_mask_setting():
+    lib = _native.lib()
+    assert lib.smx_s8_comp_mask(0x20) == -1 and lib.smx_s8_comp_mask(-1) == -1
+    assert lib.smx_s8_comp_mask(0x15) == 0x1F  # the production default is unchanged by the rejected calls
+    assert lib.smx_s8_comp_stages(2) == 1      # leading compensated stages of 0x15: stage 1 only
+    assert _native.s8_comp_mask(0x1F) == 0x03
+    with pytest.raises(ValueError):
+        _native.s8_comp_mask(64)
+    assert lib.smx_s8_comp_stages(5) == 5
+
+
 def test_tile_geometry_setting():
     lib = _native.lib()
     assert lib.smx_s8_tile_geometry(3) == -1 and lib.smx_s8_tile_geometry(-1) == -1

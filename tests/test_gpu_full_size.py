@@ -23,12 +23,13 @@
 * FP32 mode's error budget: the reference's eager FP32 path, the same path
   with its two Frobenius norms reduced in FP64, and this build's FP32 mode,
   each against the FP64 map.
-* The compensated recipe: the worst error of the compensated-BF16 S8 when
-  only the first k stages are compensated, k = 1..5, on the cfg2 batch, the
-  cfg5 shapes and the cfg4 step (smx_s8_comp_stages).
+* The compensated recipe: the worst error of the compensated-BF16 S8 under
+  each compensation mask (which stages are compensated, the rest plain
+  BF16; smx_s8_comp_mask) and of the mixed mode (compensated stage 1, FP16
+  stages 2-5), on the cfg2 batch, the cfg5 shapes and the cfg4 step.
 
 Gates (north star): statistics/EMA rel. error <= 1e-6; per-matrix direction
-rel. Frobenius error <= 1e-4 (fp32 mode), <= 1e-2 (comp_bf16 mode).
+rel. Frobenius error <= 1e-4 (fp32 mode), <= 1e-2 (comp_bf16 and mixed).
 """
 import pytest
 import torch
@@ -305,7 +306,13 @@ def cfg4_run(device, mode):
     return model, cpu_model, opt, ora, stats.sums
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+# The compensation recipes compared: stages whose bit is set in the mask
+# are compensated, the others plain BF16 products (smx_s8_comp_mask).
+RECIPES = {"all five": 0x1F, "plain 5": 0x0F, "plain 4": 0x17, "plain 3": 0x1B, "plain 2": 0x1D,
+           "plain 2,4": 0x15, "plain 3,4": 0x13, "stage 1 only (historical)": 0x01}
+
+
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_cfg4_gpt_step_at_the_real_workload(device, mode):
     t0 = time.time()
     model, cpu_model, opt, ora, stats = cfg4_run(device, mode)
@@ -346,33 +353,38 @@ def test_cfg4_gpt_step_at_the_real_workload(device, mode):
             o64 = fp64_direction(ora.st(pc), ora.st(ora.a_source[id(pc)]), pc.shape, pc.grad)
             print(f"  {n}: gpu vs fp64 {rel(got[n], g64):.2e}, fp32 oracle vs fp64 {rel(want[n], o64):.2e}, "
                   f"fp64 from either side's statistics {rel(g64, o64):.2e}")
-    else:
-        # The recipe table: the same step from the same state with only the
-        # first k S8 stages compensated.
-        table = {5: worst}
+    elif mode == "comp_bf16":
+        # The recipe table: the same step from the same state with each
+        # compensation mask (plain stages: BF16 products hi*hi).
+        table = {}
         try:
-            for k in (4, 3, 2, 1):
+            for label, mask in RECIPES.items():
                 with torch.no_grad():
                     for n, p in model.named_parameters():
                         p.copy_(before[n])
                 opt.load_state_dict(copy.deepcopy(sd))
-                _native.s8_comp_stages(k)
+                _native.s8_comp_mask(mask)
                 opt.step()
                 torch.cuda.synchronize()
                 dk = directions(before, model, names, 1e-2)
-                table[k] = max(rel(dk[n], want[n]) for n in names)
+                table[label] = max(rel(dk[n], want[n]) for n in names)
         finally:
-            _native.s8_comp_stages(5)
-        print("cfg4 step, compensated stages k -> worst direction rel err vs the FP32 oracle: " +
-              ", ".join(f"k={k}: {e:.2e}" for k, e in sorted(table.items())))
+            _native.s8_comp_mask(0x1F)
+        print("cfg4 step, compensation recipe -> worst direction rel err vs the FP32 oracle: " +
+              ", ".join(f"{k}: {e:.2e}" for k, e in table.items()))
+        assert abs(table["all five"] - worst) <= 1e-6  # the reloaded state repeats the step
+    else:
+        assert worst <= 5e-3, worst  # the mixed recipe keeps half the gate in reserve
     opt.close()
 
 
 def test_compensated_stage_recipe_on_cfg2_and_cfg5_shapes(device):
-    """Worst per-matrix error of the compensated-BF16 S8 against the FP32
-    oracle with the first k stages compensated: the whole cfg2 batch and
-    the cfg5 shapes.  The production recipe (k = 5) must stay within half
-    the 1e-2 gate; the table is printed for the recipe decision."""
+    """Worst per-matrix error against the FP32 oracle of each compensation
+    recipe of the compensated-BF16 S8 (plain stages: BF16 products hi*hi)
+    and of the mixed mode (compensated stage 1, FP16 stages 2-5): the whole
+    cfg2 batch and the cfg5 shapes.  The production recipe (all five
+    stages) and the mixed mode must stay within half the 1e-2 gate; the
+    table is printed for the recipe decision."""
     cases = [((1002, (36, 768, 768)), "cfg2 768x768"), ((1003, (9, 3072, 768)), "cfg2 3072x768"),
              ((1004, (9, 768, 3072)), "cfg2 768x3072"), ((1009, (2, 2048, 2048)), "cfg5 2048x2048"),
              ((1015, (1, 2048, 8192)), "cfg5 2048x8192")]
@@ -382,16 +394,19 @@ def test_compensated_stage_recipe_on_cfg2_and_cfg5_shapes(device):
             x = s8_cfg2_batch(seed, *shape)
             ref = O.s8(x)
             xd = x.to(device)
-            for k in (5, 4, 3, 2, 1, 0):
-                _native.s8_comp_stages(k)
-                table[(label, k)] = max(per_matrix_rel(_s8_fp32(xd, mode="comp_bf16"), ref))
+            for recipe, mask in RECIPES.items():
+                _native.s8_comp_mask(mask)
+                table[(label, recipe)] = max(per_matrix_rel(_s8_fp32(xd, mode="comp_bf16"), ref))
+            _native.s8_comp_mask(0x1F)
+            table[(label, "mixed")] = max(per_matrix_rel(_s8_fp32(xd, mode="mixed"), ref))
     finally:
-        _native.s8_comp_stages(5)
-    for (label, _), _ in list(table.items())[::6]:
-        print(f"{label}: " + ", ".join(f"k={k}: {table[(label, k)]:.2e}" for k in (5, 4, 3, 2, 1, 0)))
-    for (label, k), e in table.items():
-        if k == 5:
-            assert e <= 5e-3, (label, e)
+        _native.s8_comp_mask(0x1F)
+    recipes = list(RECIPES) + ["mixed"]
+    for _, label in cases:
+        print(f"{label}: " + ", ".join(f"{r}: {table[(label, r)]:.2e}" for r in recipes))
+    for (label, recipe), e in table.items():
+        if recipe in ("all five", "mixed"):
+            assert e <= 5e-3, (label, recipe, e)
 
 
 def _init_on_device(model, seed, device):

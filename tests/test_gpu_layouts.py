@@ -36,19 +36,22 @@ from test_gpu_optimizer import DIR_TOL, Pair, check_directions, rel
 pytestmark = pytest.mark.gpu
 
 
-def ulp_close(a, b, before, dtype):
+def ulp_close(a, b, before, dtype, upd_tol=0.0):
     """Elements where |a - b| exceeds one unit in the last place of dtype at
     the scale of the update's operands (the parameter before and after):
     where p and lr*d nearly cancel, a fused and an unfused multiply-add
-    differ by far more than one ulp of the small result, but not of p."""
+    differ by far more than one ulp of the small result, but not of p.
+    upd_tol adds that fraction of the element's update |before - b| (the
+    mixed S8 mode's directions are ~2e-3 from the FP32 map, which on a
+    near-zero weight is more than two ulps of it)."""
     a, b, before = (t.detach().float().cpu() for t in (a, b, before))
     scale = torch.maximum(torch.maximum(a.abs(), b.abs()), before.abs())
-    bad = (a - b).abs() > 2 * torch.finfo(dtype).eps * scale
+    bad = (a - b).abs() > 2 * torch.finfo(dtype).eps * scale + upd_tol * (before - b).abs()
     return int(bad.sum()), a.numel()
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_low_precision_parameters_match_the_oracle(device, dtype, mode):
     torch.manual_seed(41)
     model = GPT(GPT_TINY)
@@ -64,7 +67,7 @@ def test_low_precision_parameters_match_the_oracle(device, dtype, mode):
         before, after_g, after_c = pair.step(batches, loss)
         for n, p in after_g.items():
             assert p.dtype == dtype
-            bad, total = ulp_close(p, after_c[n], before[n], dtype)
+            bad, total = ulp_close(p, after_c[n], before[n], dtype, 5e-2 if mode == "mixed" else 0.0)
             assert bad <= max(1, total // 200), (n, bad, total)
         for n in pair.opt.named_matrices:
             dg = (before[n] - after_g[n]).float().cpu()
@@ -156,7 +159,7 @@ class Branches(nn.Module):
 
 
 @pytest.mark.parametrize("opt_cls", [RankOneAWeightedPE, DiagonalWeightedPE])
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_more_than_eight_shape_classes(device, opt_cls, mode):
     torch.manual_seed(44)
     model = Branches()

@@ -36,7 +36,7 @@ def _factors(rows, cols, seed, device):
     return [t.float().to(device) for t in (inv_row, inv_col, z, kappa)]
 
 
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1, 2])
 @pytest.mark.parametrize("gdt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", [(96, 64), (64, 96), (37, 53), (130, 7)])
 def test_matrix_step_low_precision_gradients(device, mode, gdt, shape):
@@ -65,8 +65,9 @@ def test_matrix_step_low_precision_gradients(device, mode, gdt, shape):
     d_lp = (w0.to(device) - w_lp) / lr
     d_32 = (w0.to(device) - w_32) / lr
     # comp_bf16 rounds the iterate to 16-17 bits in every stage, so a
-    # last-bit difference in the whitening row sums moves it by a few 1e-5
-    assert rel(d_lp, d_32) <= (1e-5 if mode == 0 else 1e-4)
+    # last-bit difference in the whitening row sums moves it by a few 1e-5;
+    # the mixed mode's FP16 stages round it to 11 bits
+    assert rel(d_lp, d_32) <= (1e-5 if mode == 0 else 1e-4 if mode == 1 else 2e-3)
     # the graft: ||direction|| = sqrt(rows)
     assert abs(d_lp.double().norm().item() - math.sqrt(rows)) <= 1e-4 * math.sqrt(rows)
 
@@ -118,7 +119,7 @@ class Chain(nn.Module):
         return x
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_odd_shapes_through_the_optimizer(device, tile_policy, mode):
     torch.manual_seed(41)
     model = Chain()
@@ -155,7 +156,7 @@ class WideBranches(nn.Module):
         return torch.cat([torch.tanh(layer(p)) for layer, p in zip(self.layers, parts)], dim=-1)
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_wide_rows_through_the_optimizer(device, tile_policy, mode):
     torch.manual_seed(43)
     model = WideBranches()
@@ -194,7 +195,7 @@ class RandomBranches(nn.Module):
         return torch.cat([torch.tanh(layer(p)) for layer, p in zip(self.layers, parts)], dim=-1)
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 @pytest.mark.parametrize("seed,opt_cls", [(7, RankOneAWeightedPE), (8, RankOneAWeightedPE), (9, DiagonalWeightedPE)])
 def test_random_shapes_through_the_optimizer(device, mode, seed, opt_cls):
     torch.manual_seed(seed)
@@ -230,7 +231,7 @@ class Extremes(nn.Module):
         return torch.cat([torch.tanh(layer(p)) for layer, p in zip(self.layers, parts)], dim=-1)
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_extreme_aspect_ratios_through_the_optimizer(device, mode):
     torch.manual_seed(11)
     model = Extremes()
@@ -266,7 +267,7 @@ class ManyBranches(nn.Module):
         return torch.cat([torch.tanh(layer(p)) for layer, p in zip(self.layers, parts)], dim=-1)
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_more_matrices_than_one_row_launch_takes(device, mode):
     torch.manual_seed(17)
     model = ManyBranches()

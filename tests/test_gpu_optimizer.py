@@ -156,7 +156,7 @@ def mse(model, x, y):
     return (model(x) - y).square().mean()
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_cfg1_single_linear_768(device, mode):
     """BASELINE cfg1: fp32 Linear 768->768, W ~ N(0, .02), bias 0, lr 1e-2,
     4 microbatches of 16x1024 tokens, x = N(0,1) + mu_c (mu_c ~ N(0, .5)),
@@ -189,7 +189,7 @@ def test_cfg1_single_linear_768(device, mode):
 
 
 @pytest.mark.parametrize("opt_cls", [RankOneAWeightedPE, DiagonalWeightedPE])
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_tiny_gpt_two_steps(device, opt_cls, mode):
     torch.manual_seed(21)
     model = GPT(GPT_TINY)

@@ -84,28 +84,46 @@ def _timed_s8(x, mode):
     return out, [p for _, p, _ in rec], [f for _, _, f in rec]
 
 
+def prod(mode, stage, comp_op=False):
+    """MFMA FLOPs per logical FLOP of a product: 3 for the compensated
+    products (every stage of comp_bf16; stage 1 of mixed, and its stage-2
+    Q2 = P2 Q1 and X2 = Q2 X0), 1 for FP32 and FP16 products."""
+    return 3 if mode == "comp_bf16" or (mode == "mixed" and (stage == 1 or comp_op)) else 1
+
+
+def one_hot_flops(mode, stage, tiles, tm, waves):
+    """The square's one-hot (b/c) G MFMAs (32 x 32 x 16 each) per launch
+    matrix: per tile and wave, over its 2 column tiles, 2 tm/64 K stages of
+    3 (compensated) or 1 (FP32) products, or tm/64 FP16 stages of 4 (the
+    scalar's hi and lo against both 16-deep halves)."""
+    per = {"comp_bf16": 2 * (tm // 64) * 3, "fp32": 2 * (tm // 64)}.get(mode, (tm // 64) * 4)
+    if mode == "mixed" and stage == 1:
+        per = 2 * (tm // 64) * 3
+    return tiles * waves * per * 2 * 2 * 32 * 32 * 16
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_s8_launch_timing_records_every_phase_x_space(device, mode):
     # oriented 300 x 500 padded to 512 x 512 (cp == rp): the stages run on
     # the iterate.  The apply computes 2 x 4 tiles of 256 x 128, the Gram
     # and the square the 10 upper-triangle 128 x 128 tiles of their 512 x 512
     # results (three matrices take fewer rounds of the CUs' block slots in
-    # the smaller geometry); the one-hot term adds, per square tile and
-    # wave, 4 K stages of 2 MFMA tiles 32 x 32 x 16.
+    # the smaller geometry); the square of stages 2-5 adds the one-hot MFMAs.
     x = torch.randn(3, 300, 500, device=device)
     _, phases, fl = _timed_s8(x, mode)
     assert phases == ["gram", "square", "poly1", "apply"] + ["gram", "square", "apply"] * 4
-    prod = 3 if mode == "comp_bf16" else 1
-    gram, apply = 3 * 10 * 2 * 128 * 128 * 512 * prod, 3 * 8 * 2 * 256 * 128 * 512 * prod
-    square1 = 3 * 10 * 2 * 128 * 128 * 512 * prod
-    one_hot = 3 * 10 * 4 * 4 * 2 * 2 * 32 * 32 * 16 * prod
-    assert fl[:4] == [gram, square1, 0.0, apply]
-    assert fl[4:7] == [gram, square1 + one_hot, apply]
+    want = []
+    for stage in range(1, 6):
+        f = prod(mode, stage)
+        gram, apply = 3 * 10 * 2 * 128 * 128 * 512 * f, 3 * 8 * 2 * 256 * 128 * 512 * f
+        square = 3 * 10 * 2 * 128 * 128 * 512 * f + (0 if stage == 1 else 3 * one_hot_flops(mode, stage, 10, 128, 4))
+        want += [gram, square, 0.0, apply] if stage == 1 else [gram, square, apply]
+    assert fl == want
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_s8_launch_timing_records_every_phase_gram_space(device, mode):
     # oriented 300 x 520 padded to 512 x 768 (cp > rp): Gram space, in two
     # segments.  Grams of X0 (stage 1) and X2 (stage 3), K = 768; applies of
@@ -119,13 +137,14 @@ def test_s8_launch_timing_records_every_phase_gram_space(device, mode):
     assert phases == (["gram", "square", "poly1", "sym", "sym"] + ["square", "apply", "apply"]
                       + ["gram", "square", "sym", "sym"] + ["square", "sym", "sym", "apply"]
                       + ["square", "apply", "apply"])
-    prod = 3 if mode == "comp_bf16" else 1
-    gram, x_apply = 3 * 10 * 2 * 128 * 128 * 768 * prod, 3 * 12 * 2 * 256 * 128 * 512 * prod
-    sym, apply_q = 3 * 10 * 2 * 128 * 128 * 512 * prod, 3 * 8 * 2 * 256 * 128 * 512 * prod
-    square1 = 3 * 10 * 2 * 128 * 128 * 512 * prod
-    square = square1 + 3 * 10 * 4 * 4 * 2 * 2 * 32 * 32 * 16 * prod
-    assert fl == ([gram, square1, 0.0, sym, sym] + [square, apply_q, x_apply] + [gram, square, sym, sym]
-                  + [square, sym, sym, apply_q] + [square, apply_q, x_apply])
+    gram = lambda k: 3 * 10 * 2 * 128 * 128 * 768 * prod(mode, k)
+    sym = lambda k: 3 * 10 * 2 * 128 * 128 * 512 * prod(mode, k)
+    square = lambda k: sym(k) + (0 if k == 1 else 3 * one_hot_flops(mode, k, 10, 128, 4))
+    apply_q = lambda k: 3 * 8 * 2 * 256 * 128 * 512 * prod(mode, k, comp_op=k == 2)
+    x_apply = lambda k: 3 * 12 * 2 * 256 * 128 * 512 * prod(mode, k, comp_op=k == 2)
+    assert fl == ([gram(1), square(1), 0.0, sym(1), sym(1)] + [square(2), apply_q(2), x_apply(2)]
+                  + [gram(3), square(3), sym(3), sym(3)] + [square(4), sym(4), sym(4), apply_q(4)]
+                  + [square(5), apply_q(5), x_apply(5)])
     ref = O.s8(x.cpu())
     assert max(per_matrix_rel(out, ref)) <= TOL[mode]
 
@@ -150,7 +169,7 @@ def test_s8_timing_runs_only_records_one_span_per_run(device):
     assert rec[0][2] == rec[1][2] == full[0][2]
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 @pytest.mark.parametrize("shape", [(2, 7, 3), (3, 64, 96), (2, 300, 200), (1, 257, 513), (4, 512, 512), (3, 300, 520),
                                    (1, 520, 300), (2, 768, 3072)])
 def test_s8_256x256_tiles(device, mode, shape):
@@ -169,7 +188,7 @@ def test_s8_256x256_tiles(device, mode, shape):
     assert max(per_matrix_rel(out, O.s8_svd(x))) <= TOL[mode]
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 def test_s8_launch_timing_256x256_tiles(device, mode):
     # oriented 300 x 500 padded to 512 x 512 with every launch forced to
     # 256 x 256 tiles of 8 waves: the Gram and the square compute the 3
@@ -183,11 +202,13 @@ def test_s8_launch_timing_256x256_tiles(device, mode):
     finally:
         _native.s8_tile_geometry(prev)
     assert phases == ["gram", "square", "poly1", "apply"] + ["gram", "square", "apply"] * 4
-    prod = 3 if mode == "comp_bf16" else 1
-    sym, apply = 3 * 3 * 2 * 256 * 256 * 512 * prod, 3 * 4 * 2 * 256 * 256 * 512 * prod
-    one_hot = 3 * 3 * 8 * 8 * 2 * 2 * 32 * 32 * 16 * prod
-    assert fl[:4] == [sym, sym, 0.0, apply]
-    assert fl[4:7] == [sym, sym + one_hot, apply]
+    want = []
+    for stage in range(1, 6):
+        f = prod(mode, stage)
+        sym, apply = 3 * 3 * 2 * 256 * 256 * 512 * f, 3 * 4 * 2 * 256 * 256 * 512 * f
+        square = sym + (0 if stage == 1 else 3 * one_hot_flops(mode, stage, 3, 256, 8))
+        want += [sym, square, 0.0, apply] if stage == 1 else [sym, square, apply]
+    assert fl == want
     assert max(per_matrix_rel(out, O.s8(x.cpu()))) <= TOL[mode]
 
 
@@ -209,7 +230,7 @@ def expected_square_geometry(n, size, cus):
     return ("128x128", sym(ts)) if 0.9 * small_rounds < big_rounds else ("256x128", 2 * sym(t256))
 
 
-@pytest.mark.parametrize("mode", ["fp32", "comp_bf16"])
+@pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
 @pytest.mark.parametrize("batch,size,geometry", [(8, 512, "128x128"), (74, 768, "256x128"), (160, 512, "256x256")])
 def test_s8_square_tile_geometries(device, mode, batch, size, geometry):
     """The square phase takes 256 x 256 tiles when the launch has at least
@@ -235,13 +256,12 @@ def test_s8_square_tile_geometries(device, mode, batch, size, geometry):
     finally:
         _native.s8_timing(False)
     rec = _native.s8_timing_read()
-    prod = 3 if mode == "comp_bf16" else 1
     tm, tn, waves = GEOMETRY[geometry]
     tiles = expected_square_geometry(chains[0], size, cus)[1]
     # per matrix: stage 1 (G G) and stages 2-5 (G G plus the one-hot (b/c) G
-    # MFMAs: per wave 2 tm/64 K stages of 2 32x32x16 products per tile)
-    f1 = tiles * 2 * tm * tn * size * prod
-    f2 = f1 + tiles * waves * (2 * tm // 64) * 2 * 2 * 32 * 32 * 16 * prod
+    # MFMAs)
+    f1 = tiles * 2 * tm * tn * size * prod(mode, 1)
+    f2 = tiles * 2 * tm * tn * size * prod(mode, 2) + one_hot_flops(mode, 2, tiles, tm, waves)
     want = sorted(f for n in chains for f in [n * f1] + [n * f2] * 4)
     assert sorted(f for _, p, f in rec if p == "square") == want
     errs = per_matrix_rel(out, O.s8(x))
