@@ -40,6 +40,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="gpt103m", choices=["gpt103m", "gpt2048"])
     ap.add_argument("--s8-mode", default="comp_bf16", choices=["comp_bf16", "mixed", "fp32"])
+    ap.add_argument("--no-alt-mode", action="store_true",
+                    help="skip the second measurement of the other BF16-class S8 mode (comp_bf16 <-> mixed) "
+                         "that the line carries under `alt_mode`")
+    ap.add_argument("--no-peak-probe", action="store_true", help="skip the MFMA peak probe of the line")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: all cores in the affinity mask")
     ap.add_argument("--train", action="store_true",
@@ -430,6 +434,27 @@ def main():
         if ev:
             ev[2].record()
 
+    def timed_steps(steps):
+        """`steps` timed steps: total ms per step, hook-phase and step() ms,
+        host wall ms, and the library's whole-run S8 records."""
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        _native.s8_timing(True, runs_only=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        for k in range(steps):
+            one_step(evs[k])
+        end.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+        _native.s8_timing(False)
+        runs = _native.s8_timing_read()
+        ms = start.elapsed_time(end) / steps
+        hooks_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
+        step_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
+        return ms, hooks_ms, step_ms, wall, runs
+
     for _ in range(args.warmup):
         one_step()
     torch.cuda.synchronize()
@@ -438,28 +463,13 @@ def main():
     # Timed region: K steps between two events; inside it, event pairs around
     # the hook phase and step() of every step, and the library records an
     # event pair around each step's whole S8 run on the stream it uses.
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    _native.s8_timing(True, runs_only=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record()
-    for k in range(args.steps):
-        one_step(evs[k])
-    end.record()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3 / args.steps
-    _native.s8_timing(False)
-    runs = _native.s8_timing_read()
+    ms, hooks_ms, step_ms, wall, runs = timed_steps(args.steps)
     # One more step, untimed, with an event pair around every S8 launch for
     # the per-phase breakdown.
     _native.s8_timing(True)
     one_step()
     _native.s8_timing(False)
     launches = _native.s8_timing_read()
-    ms = start.elapsed_time(end) / args.steps
-    hooks_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
-    step_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
     s8_ms, s8_issued, s8_phases = summarize_s8(runs, launches, args.steps)
     s8_logical = logical_s8_flops(opt)
     log(f"timed {args.steps} steps: {ms:.3f} ms/step (hooks {hooks_ms:.3f}, step {step_ms:.3f}, "
@@ -485,6 +495,32 @@ def main():
                "logical_tflops": round(s8_logical / (s8_ms * 1e-3) / 1e12, 1), "ms_per_step": round(s8_ms, 3),
                "phases": s8_phases}
     roof_s8["vendor_bf16_gemm"] = vendor_gemm_rate(opt, device)
+    alt = None
+    alt_mode = {"comp_bf16": "mixed", "mixed": "comp_bf16"}.get(args.s8_mode)
+    if alt_mode and not args.no_alt_mode:
+        # The same workload and optimizer with the other BF16-class S8 mode:
+        # one warm-up step, then the same number of timed steps.
+        log(f"alternate mode {alt_mode}")
+        opt.s8_mode = alt_mode
+        one_step()
+        a_ms, a_hooks, a_step, _, a_runs = timed_steps(args.steps)
+        opt.s8_mode = args.s8_mode
+        a_s8 = sum(r[0] for r in a_runs) / args.steps
+        a_issued = sum(r[2] for r in a_runs) / args.steps
+        a_tfs = a_issued / (a_s8 * 1e-3) / 1e12
+        alt = {"s8_mode": alt_mode, "ms_per_step": round(a_ms, 4),
+               "phases_ms": {"hooks": round(a_hooks, 3), "step": round(a_step, 3)},
+               "s8": {"ms_per_step": round(a_s8, 3), "achieved_tflops": round(a_tfs, 1),
+                      "frac": round(a_tfs / (BF16_PEAK / 1e12), 4), "issued_flops_per_step": a_issued,
+                      "logical_tflops": round(s8_logical / (a_s8 * 1e-3) / 1e12, 1)}}
+    if not args.no_peak_probe:
+        probe = mfma_peak_probe(device)
+        roof_s8["mfma_peak_probe"] = probe
+        key = {"fp32": "fp32", "mixed": "fp16"}.get(args.s8_mode, "bf16")
+        roof_s8["frac_of_probe"] = round(s8_tfs / probe[key]["tflops"], 4)
+        if alt:
+            akey = "fp16" if alt["s8_mode"] == "mixed" else "bf16"
+            alt["s8"]["frac_of_probe"] = round(alt["s8"]["achieved_tflops"] / probe[akey]["tflops"], 4)
     dominant = roof_stats if hooks_ms >= s8_ms else roof_s8
     out = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
@@ -499,6 +535,8 @@ def main():
         "roofline_s8": roof_s8,
         "phases_ms": {"hooks": round(hooks_ms, 3), "step": round(step_ms, 3), "host_wall_per_step": round(wall, 3)},
     }
+    if alt:
+        out["alt_mode"] = alt
     if not args.no_cpu_baseline:
         log("cpu baseline")
         threads = args.cpu_threads or len(os.sched_getaffinity(0))

@@ -54,3 +54,11 @@ def test_bench_line_has_the_contract_fields(device):
     assert s8["logical_flops_per_step"] == 1223059046400
     assert 0 < s8["ms_per_step"] < phases["step"]
     assert set(s8["phases"]) >= {"gram", "square", "apply"}
+    # the same run's second BF16-class mode and the MFMA peak probe
+    alt = line["alt_mode"]
+    assert alt["s8_mode"] == "mixed" and 0 < alt["s8"]["ms_per_step"] < alt["phases_ms"]["step"]
+    probe = s8["mfma_peak_probe"]
+    for dt in ("bf16", "fp16", "fp32"):
+        assert probe[dt]["finite"] and probe[dt]["tflops"] > 0 and 1.0 < probe[dt]["clock_ghz"] < 3.0
+        assert probe[dt]["tflops"] <= 1.02 * probe[dt]["nominal_tflops_at_clock"]
+    assert 0 < s8["frac_of_probe"] <= 1

@@ -423,18 +423,20 @@ def _init_on_device(model, seed, device):
                 p.fill_(1.0)
 
 
-def test_cfg5_gpt_step(device):
-    """BASELINE cfg5: the 2048-wide GPT's step in compensated-BF16 mode with
-    4 microbatches of 8 x 1024-token hook inputs (LayerNorm-fed q/c_fc
-    inputs in fp32, the attention and GELU outputs and every cotangent in
-    bf16, as a bf16-autocast step hands them; two rotating input sets)."""
+@pytest.mark.parametrize("mode", ["comp_bf16", "mixed"])
+def test_cfg5_gpt_step(device, mode):
+    """BASELINE cfg5: the 2048-wide GPT's step in compensated-BF16 (and the
+    mixed) mode with 4 microbatches of 8 x 1024-token hook inputs
+    (LayerNorm-fed q/c_fc inputs in fp32, the attention and GELU outputs and
+    every cotangent in bf16, as a bf16-autocast step hands them; two
+    rotating input sets)."""
     t0 = time.time()
     cfg = GPT_2048
     with torch.device(device):
         model = GPT(cfg)
     _init_on_device(model, 2048, device)
     lr = 1e-2
-    opt = RankOneAWeightedPE(model, lr, module_filter=transformer_filter, s8_mode="comp_bf16")
+    opt = RankOneAWeightedPE(model, lr, module_filter=transformer_filter, s8_mode=mode)
     assert len(opt.named_matrices) == 144
     aux = [p for p in model.parameters() if id(p) not in {id(q) for q in opt.named_matrices.values()}]
     assert sum(p.numel() for p in aux) == 105_666_560
@@ -521,7 +523,7 @@ def test_cfg5_gpt_step(device):
         errs[n] = rel(got, want)
         assert rel(opt.state[p]["momentum_buffer"], ora.st(ora.matrices[n])["momentum_buffer"]) <= 1e-6, n
     worst = max(errs.values())
-    assert worst <= DIR_TOL["comp_bf16"], (max(errs, key=errs.get), worst)
+    assert worst <= DIR_TOL[mode], (max(errs, key=errs.get), worst)
     worst_aux = 0.0
     for n, p in model.named_parameters():
         if n not in errs:
@@ -536,8 +538,8 @@ def test_cfg5_gpt_step(device):
         p, pc = opt.named_matrices[n], ora.matrices[n]
         got = (before[id(p)] - p.detach()).double().cpu() / lr
         exact[n] = rel(got, fp64_direction(ora.st(pc), ora.st(ora.a_source[id(pc)]), pc.shape, grads[n]))
-        assert exact[n] <= DIR_TOL["comp_bf16"], (n, exact[n])
-    print(f"cfg5 step: 144 matrices, worst direction rel err vs the FP32 oracle {worst:.3e} "
+        assert exact[n] <= DIR_TOL[mode], (n, exact[n])
+    print(f"cfg5 step ({mode}): 144 matrices, worst direction rel err vs the FP32 oracle {worst:.3e} "
           f"({max(errs, key=errs.get)}), statistics worst {worst_stats:.2e}, AdamW worst {worst_aux:.2e}; "
           "FP64 directions " + ", ".join(f"{n.split('.', 3)[-1]} {e:.2e}" for n, e in exact.items())
           + f"; GPU part {t1 - t0:.1f}s, oracle step {t3 - t2:.1f}s, total {time.time() - t0:.1f}s")
