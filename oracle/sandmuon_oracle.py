@@ -312,53 +312,94 @@ def _mm_comp(a: torch.Tensor, b: torch.Tensor, comp: bool = True) -> torch.Tenso
     return acc.to(a.dtype)
 
 
-def s8_comp_bf16_model(x: torch.Tensor, comp_stages: int = 5, coefficients=S8_COEFFICIENTS,
-                       margin=S8_MARGIN) -> torch.Tensor:
-    """Rounding model of the compensated-BF16 S8 of the HIP build, with the
-    first ``comp_stages`` stages compensated and the rest plain BF16.
+def _f16(t: torch.Tensor) -> torch.Tensor:
+    """Round to FP16 (nearest even, gradual underflow) and back."""
+    return t.to(torch.float16).to(t.dtype)
 
-    Follows the build's dataflow: every GEMM operand is stored as the BF16
-    pair hi + lo (the whitened input, G, P and each stage's iterate); stage
-    1 scales the Gram by 1/||V||^2 and the apply by 1/(||V|| s); G2 of stage
-    1 and the last stage's output stay in the working dtype; stages 2-5 form
+
+def _mm_f16(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """A product of FP16 operands with a wide accumulator (the FP16 MFMA of
+    the mixed mode), rounded once to the working dtype.  Pinned by: the
+    elementwise bound |p - a b| <= 2^-10 (|a| |b|) and the identity case."""
+    return (_f16(a).double() @ _f16(b).double()).to(a.dtype)
+
+
+def s8_comp_bf16_model(x: torch.Tensor, comp_stages: int = 5, coefficients=S8_COEFFICIENTS,
+                       margin=S8_MARGIN, mask: Optional[int] = None, fp16_stages=()) -> torch.Tensor:
+    """Rounding model of the BF16-class S8 of the HIP build (X-space
+    schedule): each stage compensated, plain BF16 or FP16.
+
+    Stage k is FP16 if k is in ``fp16_stages`` (the mixed mode: stages
+    2-5), else compensated if bit k-1 of ``mask`` is set (default: the first
+    ``comp_stages`` stages), else plain BF16.  Follows the build's dataflow:
+    every GEMM operand is stored in the form of the stage that reads it (the
+    BF16 pair hi + lo, 16-17 significant bits, or FP16); stage 1 scales the
+    Gram by 1/||V||^2 and the apply by 1/(||V|| s); G2 of stage 1 and the
+    last stage's output stay in the working dtype; stages 2-5 form
     P = c (G G + (b/c) G) + a I with the (b/c) G term as a product of its
-    own.  A compensated stage uses hi*lo + lo*hi + hi*hi for every product, a
-    plain one hi*hi (so comp_stages = 1 is the recipe of
+    own, whose scalar keeps its hi and lo halves (BF16 or FP16) in every
+    form.  A compensated stage uses hi*lo + lo*hi + hi*hi for every product,
+    a plain one hi*hi (so comp_stages = 1 is the recipe of
     reproduction/odl/ops/dense_s8_compensated_fast.py:53-85: a BF16 input to
     the plain stages, a compensated stage 1).  The working dtype is the
-    input's (float32 models the build; float64 with BF16 rounding replaced
+    input's (float32 models the build; float64 with the roundings replaced
     by the identity reduces it to the exact map, which pins the stage
-    algebra against ``s8_svd``).  Used to budget the mode's error against
+    algebra against ``s8_svd``).  Used to budget the recipes' error against
     the 1e-2 gate; the GPU measurement is what decides the recipe.
-    Pinned by: tests/test_oracle_pins.py (identity case vs the SVD form in
-    every comp_stages setting, the product bound and a planted dropped
-    correction product).
+    Pinned by: tests/test_oracle_pins.py (identity case vs the SVD form for
+    several recipes, the product bounds and a planted dropped correction
+    product).
     """
     wd = x.dtype if x.dtype == torch.float64 else torch.float32
     x = x.to(wd)
     flip = x.shape[-2] > x.shape[-1]
     if flip:
         x = x.transpose(-2, -1)
-    comp = [k < comp_stages for k in range(len(coefficients))]
+    if mask is None:
+        mask = (1 << comp_stages) - 1
+    form = ["f16" if k + 1 in fp16_stages else "comp" if (mask >> k) & 1 else "plain"
+            for k in range(len(coefficients))]
+
+    def stored(t, f):
+        return _f16(t) if f == "f16" else _stored(t)
+
+    def mm(a, b, f):
+        return _mm_f16(a, b) if f == "f16" else _mm_comp(a, b, f == "comp")
+
+    def lin(scalar, g, f):
+        """scalar * G as the one-hot MFMAs form it: the scalar's hi and lo
+        halves against G (both halves of G when compensated)."""
+        if f == "f16":
+            sh = _f16(torch.tensor(scalar, dtype=wd))
+            sl = _f16(torch.tensor(scalar, dtype=wd) - sh)
+            return ((sh.double() + sl.double()) * _f16(g).double()).to(wd)
+        sh, sl = _split(torch.tensor(scalar, dtype=wd))
+        gh, gl = _split(g)
+        acc = sh.double() * gh.double() + sl.double() * gh.double()
+        if f == "comp":
+            acc = acc + sh.double() * gl.double()
+        return acc.to(wd)
+
     eye = torch.eye(x.shape[-2], dtype=wd)
     fro2 = (x.double() ** 2).sum((-2, -1), keepdim=True)
     xs = _stored(x)
     inv_n2 = torch.where(fro2 > 0, 1.0 / fro2.clamp_min(1e-300), torch.zeros_like(fro2)).to(wd)
-    g = _stored(_mm_comp(xs, xs.transpose(-2, -1), comp[0]) * inv_n2)
-    g2 = _mm_comp(g, g, comp[0])
+    g = _stored(mm(xs, xs.transpose(-2, -1), form[0]) * inv_n2)
+    g2 = mm(g, g, form[0])
     s = torch.clamp(margin * torch.linalg.matrix_norm(g2.double(), keepdim=True) ** 0.25, min=1e-30)
     a, b, c = coefficients[0]
     s2 = (s * s).to(wd)
     p = _stored(a * eye + (b * g) / s2 + (c * g2) / (s2 * s2))
     scale = torch.where(fro2 > 0, 1.0 / (fro2.sqrt() * s).clamp_min(1e-300), torch.zeros_like(fro2)).to(wd)
-    xk = _mm_comp(p, xs, comp[0]) * scale
+    xk = mm(p, xs, form[0]) * scale
     for k in range(1, len(coefficients)):
         a, b, c = coefficients[k]
-        xk = _stored(xk)
-        g = _stored(_mm_comp(xk, xk.transpose(-2, -1), comp[k]))
-        acc = _mm_comp(g, g, comp[k]) + _mm_comp((b / c) * eye.expand_as(g), g, comp[k])
-        p = _stored(c * acc + a * eye)
-        xk = _mm_comp(p, xk, comp[k])
+        f = form[k]
+        xk = stored(xk, f)
+        g = stored(mm(xk, xk.transpose(-2, -1), f), f)
+        acc = mm(g, g, f) + lin(b / c, g, f)
+        p = stored(c * acc + a * eye, f)
+        xk = mm(p, xk, f)
     if flip:
         xk = xk.transpose(-2, -1)
     return xk

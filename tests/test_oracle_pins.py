@@ -348,19 +348,39 @@ def test_planted_dropped_correction_product_is_caught():
     assert not bool((err <= 2.0 ** -16 * _bound(a, b)).all())
 
 
-@pytest.mark.parametrize("comp_stages", [0, 1, 3, 5])
+RECIPES = [dict(comp_stages=0), dict(comp_stages=1), dict(comp_stages=3), dict(comp_stages=5),
+           dict(mask=0x15), dict(fp16_stages=(2, 3, 4, 5))]
+
+
+@pytest.mark.parametrize("recipe", RECIPES, ids=lambda r: "-".join(f"{k}{v}" for k, v in r.items()))
 @pytest.mark.parametrize("shape", [(2, 7, 3), (2, 3, 7), (1, 40, 64)])
-def test_comp_model_without_rounding_is_the_exact_map(monkeypatch, shape, comp_stages):
-    # With BF16 rounding replaced by the identity every stored operand is
-    # exact (lo = 0) and the float64 model must reduce to the SVD closed form:
-    # this pins its scaling, orientation, stage order and the (b/c) G term.
+def test_comp_model_without_rounding_is_the_exact_map(monkeypatch, shape, recipe):
+    # With the BF16 and FP16 roundings replaced by the identity every stored
+    # operand is exact (lo = 0) and the float64 model must reduce to the SVD
+    # closed form: this pins its scaling, orientation, stage order and the
+    # (b/c) G term in every recipe.
     monkeypatch.setattr(O, "_bf16", lambda t: t)
+    monkeypatch.setattr(O, "_f16", lambda t: t)
     torch.manual_seed(17)
     x = torch.randn(*shape, dtype=torch.float64)
-    torch.testing.assert_close(O.s8_comp_bf16_model(x, comp_stages), O.s8_svd(x), atol=1e-10, rtol=1e-9)
+    torch.testing.assert_close(O.s8_comp_bf16_model(x, **recipe), O.s8_svd(x), atol=1e-10, rtol=1e-9)
     # A planted slip (the stage coefficients in the wrong order) is caught.
-    slipped = O.s8_comp_bf16_model(x, comp_stages, coefficients=O.S8_COEFFICIENTS[::-1])
+    slipped = O.s8_comp_bf16_model(x, coefficients=O.S8_COEFFICIENTS[::-1], **recipe)
     assert not torch.allclose(slipped, O.s8_svd(x), atol=1e-3)
+
+
+def test_mm_f16_is_within_2_to_minus_10_of_the_exact_product():
+    # FP16 operands (11-bit significands) and a wide accumulator: every
+    # element within 2^-10 (|a||b|) of the float64 product, and finer than a
+    # plain BF16 product on the same (normal-range) operands.
+    g = torch.Generator().manual_seed(9)
+    a = torch.randn(40, 64, generator=g) * torch.exp(torch.empty(40, 64).uniform_(-3, 3, generator=g))
+    b = torch.randn(64, 30, generator=g) * torch.exp(torch.empty(64, 30).uniform_(-3, 3, generator=g))
+    exact = a.double() @ b.double()
+    e16 = (O._mm_f16(a, b).double() - exact).abs()
+    assert bool((e16 <= 2.0 ** -10 * _bound(a, b)).all())
+    ebf = (O._mm_comp(a, b, comp=False).double() - exact).abs()
+    assert e16.norm() < ebf.norm() / 4
 
 
 def test_comp_bf16_model_is_within_gate_on_cfg2_like_input():
@@ -374,3 +394,6 @@ def test_comp_bf16_model_is_within_gate_on_cfg2_like_input():
     full, none = err(O.s8_comp_bf16_model(x, 5)), err(O.s8_comp_bf16_model(x, 0))
     assert full < 1e-3, full
     assert none > 10 * full, (none, full)
+    # the mixed recipe (compensated stage 1, FP16 stages 2-5) lies between
+    mixed = err(O.s8_comp_bf16_model(x, fp16_stages=(2, 3, 4, 5)))
+    assert full < mixed < none and mixed < 5e-3, (full, mixed, none)
