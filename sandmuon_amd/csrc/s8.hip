@@ -82,6 +82,7 @@
 #include <cmath>
 #include <mutex>
 #include <type_traits>
+#include <utility>
 #include <vector>
 
 namespace smx {
@@ -110,9 +111,15 @@ constexpr int kMaxSeg = 2 * kMaxClasses;
 // SMX_S8_COMP_BF16 and the recipe SMX_S8_MIXED):
 //   kS8HiOnly  a plain BF16 stage of the compensated recipe: the operands in
 //              their stored hi/lo form, only the hi*hi product issued;
-//   kS8F16     FP16 operands, two 32x32x16 FP16 MFMAs per 32-deep K stage.
+//   kS8F16     FP16 operands, two 32x32x16 FP16 MFMAs per 32-deep K stage;
+//   kS8CompMix the compensated products of SMX_S8_MIXED: the K loop of
+//              SMX_S8_COMP_BF16, whose kernels alone also compile an FP16
+//              epilogue (kept out of the compensated recipe's kernels, whose
+//              code would otherwise outgrow the instruction cache).
 constexpr int kS8HiOnly = 3;
 constexpr int kS8F16 = 4;
+constexpr int kS8CompMix = 5;
+__host__ __device__ constexpr bool is_comp(int m) { return m == SMX_S8_COMP_BF16 || m == kS8CompMix; }
 // Bit k-1 set: stage k of SMX_S8_COMP_BF16 is compensated.
 static int g_comp_mask = 0x1f;
 
@@ -128,7 +135,7 @@ __host__ __device__ constexpr int gemm_mode(int mode, int mask, int phase, int s
   return mode == SMX_S8_FP32 ? SMX_S8_FP32
          : mode == SMX_S8_COMP_BF16 ? (((mask >> (stage - 1)) & 1) ? SMX_S8_COMP_BF16 : kS8HiOnly)
          : (stage == 1 || (phase == kApply && stage == 2 && (op == kOpApplyQ || op == kOpApplyMid)))
-             ? SMX_S8_COMP_BF16
+             ? kS8CompMix
              : kS8F16;
 }
 
@@ -144,7 +151,7 @@ __host__ __device__ constexpr bool form_compiled(int gm, int phase, int form) {
          : gm == kS8F16 ? (form == kFormF16 || (form == kFormPlanes && phase == kSquare) ||
                            (form == kFormF32 && phase == kApply))
          : form == kFormPlanes || (form == kFormF32 && (phase == kSquare || phase == kApply)) ||
-               (form == kFormF16 && gm == SMX_S8_COMP_BF16 && (phase == kSym || phase == kApply));
+               (form == kFormF16 && gm == kS8CompMix && (phase == kSym || phase == kApply));
 }
 
 // The form a product's output is stored in: that of the product that reads
@@ -325,6 +332,17 @@ __device__ __forceinline__ TileOffsets<N> tile_offsets_km(int64_t ld, int64_t n0
   return t;
 }
 
+// f(std::integral_constant<int, 0>{}) .. f(std::integral_constant<int, N - 1>{}),
+// expanded at compile time.
+template <class F, int... I>
+__device__ __forceinline__ void static_for_seq(F &f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
 // A wave-uniform pointer in scalar registers: the direct-to-LDS loads take
 // their base from an SGPR pair, and in some kernels the compiler does not
 // prove a base built from the kernel arguments uniform (it is: every
@@ -412,6 +430,8 @@ template <>
 struct AFrag<kS8HiOnly> : AFrag<SMX_S8_COMP_BF16> {};
 template <>
 struct AFrag<kS8F16> : AFrag<SMX_S8_COMP_BF16> {};  // h: K 0-15, l: K 16-31 (FP16 bits)
+template <>
+struct AFrag<kS8CompMix> : AFrag<SMX_S8_COMP_BF16> {};
 template <int MODE>
 struct BFrags;
 template <>
@@ -426,11 +446,13 @@ template <>
 struct BFrags<kS8HiOnly> : BFrags<SMX_S8_COMP_BF16> {};
 template <>
 struct BFrags<kS8F16> : BFrags<SMX_S8_COMP_BF16> {};
+template <>
+struct BFrags<kS8CompMix> : BFrags<SMX_S8_COMP_BF16> {};
 
 // Both 16-byte chunks of a row's K slice are read (the lo plane, or FP16's
 // second 16 K).
 template <int MODE>
-constexpr bool two_chunks() { return MODE == SMX_S8_COMP_BF16 || MODE == kS8F16; }
+constexpr bool two_chunks() { return is_comp(MODE) || MODE == kS8F16; }
 
 // LDS -> registers: A row block i, and the four B column blocks, of one
 // stage.  Lane (r, h) takes K = 8h .. 8h+7 of its row: chunks h (hi) and
@@ -557,7 +579,7 @@ __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &
 #pragma unroll
     for (int j = 0; j < kSubN; ++j) {
 #pragma unroll
-      for (int pl = 0; pl < (MODE == SMX_S8_COMP_BF16 ? 2 : 1); ++pl) {
+      for (int pl = 0; pl < (is_comp(MODE) ? 2 : 1); ++pl) {
         lds_char *p = q[j & 1][pl] + (kOpA + ((8 * kSubN * wn + 16 * (j >> 1)) << 4));
         const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * kKmRow);
         const bf16x8 v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -591,7 +613,7 @@ __device__ __forceinline__ f16x8 as_f16(bf16x8 v) { return __builtin_bit_cast(f1
 // MFMAs of row block i: acc[i][j] += A_i B_j^T over the stage's K.
 template <int MODE>
 __device__ __forceinline__ void mma_row(const AFrag<MODE> &a, const BFrags<MODE> &b, f32x16 (&acc)[kSubN]) {
-  if constexpr (MODE == SMX_S8_COMP_BF16) {
+  if constexpr (is_comp(MODE)) {
     // Corrections first, then hi*hi.
 #pragma unroll
     for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.l[j], acc[j], 0, 0, 0);
@@ -783,14 +805,16 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Wa
 // row-major operand (C = A B, apply), brow0 its first column.  Row pitches
 // (ld), K and brow0 are in elements; an FP16 operand (MODE kS8F16) is
 // addressed in 4-byte units, half of each.
-template <int MODE, class G, bool ACCG, bool BKM>
+template <int MODE, class G, bool ACCG, bool BKM, bool UB = false>
 __device__ __forceinline__ void gemm_tile(const Opnd &A_in, const Opnd &B_in, int64_t K, int64_t arow0, int64_t brow0,
                                           float sel_s, char *smem, f32x16 (&acc)[G::kSubM][kSubN]) {
   constexpr int kSubM = G::kSubM;
   constexpr bool F16 = MODE == kS8F16;
   constexpr int kU = F16 ? 2 : 1;  // elements per 4-byte unit
   static_assert((kSubM == 4 || kSubM == 2) && kBK == 16, "the one_hot window is 2 kSubM stages of 16 rows");
-  const Opnd A{uniform_ptr(A_in.p), A_in.ld / kU}, B{uniform_ptr(B_in.p), B_in.ld / kU};
+  // (UB: pass the operand bases through readfirstlane, for the kernels in
+  // which the compiler keeps them in vector registers: see uniform_ptr.)
+  const Opnd A{UB ? uniform_ptr(A_in.p) : A_in.p, A_in.ld / kU}, B{UB ? uniform_ptr(B_in.p) : B_in.p, B_in.ld / kU};
   static_assert((8 * kSubN) % 16 == 0, "the wave's K-major column offset must be whole chunk groups");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int wm = wave / G::kWavesN, wn = wave % G::kWavesN;  // 2 x kWavesN waves
@@ -1045,8 +1069,8 @@ s8_stage_kernel(StageArgs args) {
         scale = sc.ok ? 1.0f / (sc.s * sc.s) : 0.f;
       }
     }
-    gemm_tile<MODE, Gm, false, false>(Opnd{A, K.rp}, Opnd{B, K.rp}, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem,
-                                      acc);
+    gemm_tile<MODE, Gm, false, false, MODE == kS8CompMix>(Opnd{A, K.rp}, Opnd{B, K.rp}, K.rp, tm * Gm::kTileM,
+                                                         tn * kTileN, 0.f, smem, acc);
   } else if constexpr (PHASE == kGram) {
     if (stage == 1) {
       const double f = M.cst()[kCstFro];
@@ -1057,12 +1081,15 @@ s8_stage_kernel(StageArgs args) {
     gemm_tile<MODE, Gm, false, false>(X, X, K.cp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
   } else if constexpr (PHASE == kSquare) {
     const Opnd G{M.g(), K.rp};
+    // (the square kernels run at the VGPR budget, where the compiler keeps
+    // the operand bases in vector registers)
+    constexpr bool kUB = true;
     if (stage == 1) {
-      gemm_tile<MODE, Gm, false, false>(G, G, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
+      gemm_tile<MODE, Gm, false, false, kUB>(G, G, K.rp, tm * Gm::kTileM, tn * kTileN, 0.f, smem, acc);
     } else {
       // acc = G G + (b/c) G; the epilogue forms P = c acc + a I.
       scale = args.c;
-      gemm_tile<MODE, Gm, true, false>(G, G, K.rp, tm * Gm::kTileM, tn * kTileN, args.b_over_c, smem, acc);
+      gemm_tile<MODE, Gm, true, false, kUB>(G, G, K.rp, tm * Gm::kTileM, tn * kTileN, args.b_over_c, smem, acc);
     }
   } else {
     // X-space: X' = P X (stage 1: X' = P1 V / (||V|| s)).  Gram space:
@@ -1194,11 +1221,28 @@ s8_stage_kernel(StageArgs args) {
   // planes), or one 8-byte store of the lane's four columns (FP16: the
   // row's 64 bytes).
   // (FM = kFormAny: planes or FP32 chosen at run time by `form`, one loop
-  // for both: the compensated square's stage-1 G2 and later P.)
+  // for both, in the kernels that produce no FP16.)
   auto put_row = [&](auto fm_c, const float *S, int row, int64_t gr, int64_t gc0, float *dst, int64_t ld,
                      float (&r)[3], bool acc_r) {
     constexpr int FM = decltype(fm_c)::value;
-    if (FM == kFormPlanes || (FM == kFormAny && form == kFormPlanes)) {
+    if constexpr (FM == kFormF16) {
+      const f32x4 v4 = *reinterpret_cast<const f32x4 *>(S + row * kEpStride + ec4);
+      float w[4] = {v4.x, v4.y, v4.z, v4.w};
+      if (eye)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (gr == gc0 + ec4 + e && gr < K.r) w[e] += args.a;
+      uint32_t b[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        b[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(w[2 * e]))) |
+               (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(w[2 * e + 1]))) << 16);
+      *reinterpret_cast<uint2 *>(reinterpret_cast<char *>(dst) + (gr * ld + gc0 + ec4) * 2) = make_uint2(b[0], b[1]);
+      return;
+    }
+    char *out = reinterpret_cast<char *>(dst) + (gr * ld + gc0) * 4 + 16 * ech;
+    const bool pl = FM == kFormPlanes || (FM == kFormAny && form == kFormPlanes);
+    if (pl) {
       float w[8];
       ep_read8(S, row, ec8, w);
       if (eye)
@@ -1212,8 +1256,7 @@ s8_stage_kernel(StageArgs args) {
         const uint16_t x1 = lo_plane ? bf16_lo_bits(w[2 * e + 1]) : bf16_bits(w[2 * e + 1]);
         b[e] = x0 | (static_cast<uint32_t>(x1) << 16);
       }
-      *reinterpret_cast<uint4 *>(reinterpret_cast<char *>(dst) + (gr * ld + gc0) * 4 + 16 * ech) =
-          make_uint4(b[0], b[1], b[2], b[3]);
+      *reinterpret_cast<uint4 *>(out) = make_uint4(b[0], b[1], b[2], b[3]);
     } else {
       const f32x4 v4 = *reinterpret_cast<const f32x4 *>(S + row * kEpStride + ec4);
       float w[4] = {v4.x, v4.y, v4.z, v4.w};
@@ -1221,29 +1264,20 @@ s8_stage_kernel(StageArgs args) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (gr == gc0 + ec4 + e && gr < K.r) w[e] += args.a;
-      if constexpr (FM == kFormF16) {
-        uint32_t b[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-          b[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(w[2 * e]))) |
-                 (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(w[2 * e + 1]))) << 16);
-        *reinterpret_cast<uint2 *>(reinterpret_cast<char *>(dst) + (gr * ld + gc0 + ec4) * 2) =
-            make_uint2(b[0], b[1]);
-      } else {
-        *reinterpret_cast<float4 *>(reinterpret_cast<char *>(dst) + (gr * ld + gc0) * 4 + 16 * ech) =
-            make_float4(w[0], w[1], w[2], w[3]);
-        if (acc_r) accum4(w, gc0 + ec4, r);
-      }
+      *reinterpret_cast<float4 *>(out) = make_float4(w[0], w[1], w[2], w[3]);
+      if (acc_r) accum4(w, gc0 + ec4, r);
     }
   };
   // The block loop, specialised for the output form (one copy per form the
   // launch's mode can produce, so that each keeps only its own registers).
   auto epilogue = [&](auto fm_c) {
     constexpr int FM = decltype(fm_c)::value;
-    const bool rs_on = FM == kFormF32 && rsum;  // the row sums come with the FP32 result only
-#pragma unroll
-    for (int blk = 0; blk < kSubM * kSubN; ++blk) {
-      const int i = blk / kSubN, j = blk % kSubN;
+    // the row sums come with the FP32 result only (rsum implies it)
+    const bool rs_on = (FM == kFormF32 || FM == kFormAny) && rsum;
+    // (expanded at compile time: a rolled block loop indexes acc at run
+    // time, which moves every accumulator of the kernel to scratch memory)
+    static_for<kSubM * kSubN>([&](auto blk_c) {
+      constexpr int blk = decltype(blk_c)::value, i = blk / kSubN, j = blk % kSubN;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         f32x4 v;
@@ -1274,7 +1308,7 @@ s8_stage_kernel(StageArgs args) {
       // Keep the scheduler from hoisting every accumulator read to the top
       // of the epilogue (the values would not fit in the VGPRs).
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
   };
   // Only the forms this launch kind can produce are compiled (the host
   // checks every launch's forms against the same table, form_compiled).
@@ -1282,6 +1316,7 @@ s8_stage_kernel(StageArgs args) {
   constexpr bool kF16 = form_compiled(MODE, PHASE, kFormF16);
   constexpr bool kF32 = form_compiled(MODE, PHASE, kFormF32);
   if constexpr (PHASE == kSquare && kPlanes && kF32 && !kF16) {
+    // one loop for both forms, as compact as a kernel of one form
     epilogue(std::integral_constant<int, kFormAny>{});
   } else if (kPlanes && form == kFormPlanes) {
     if constexpr (kPlanes) epilogue(std::integral_constant<int, kFormPlanes>{});
@@ -1491,10 +1526,10 @@ static std::vector<Seg> launch_segments(const S8Layout &Lay, const SlotSet &set,
 static double launch_flops(int mode, int phase, int stage, int geo, const S8Layout &Lay,
                            const std::vector<Seg> &segs) {
   if (phase == kPoly1) return 0.0;
-  const double prod = mode == SMX_S8_COMP_BF16 ? 3.0 : 1.0;
+  const double prod = is_comp(mode) ? 3.0 : 1.0;
   const int tm = geo == kGeoS ? 128 : 256, tn = geo == kGeoL ? 256 : 128, waves = geo == kGeoL ? 8 : 4;
   const int sub_m = tm / 64;
-  const double onehot = mode == SMX_S8_COMP_BF16 ? 6.0 * sub_m : mode == kS8HiOnly ? 4.0 * sub_m
+  const double onehot = is_comp(mode) ? 6.0 * sub_m : mode == kS8HiOnly ? 4.0 * sub_m
                         : mode == kS8F16 ? 4.0 * sub_m : 2.0 * sub_m;
   double f = 0.0;
   for (const Seg &sg : segs) {
@@ -1620,6 +1655,7 @@ static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, int 
       rc = check_launch("s8 stage-1 polynomial");
     } else {
       if (mode == SMX_S8_COMP_BF16) launch_stage<SMX_S8_COMP_BF16, PHASE>(geo, off, a, st);
+      else if (mode == kS8CompMix) launch_stage<kS8CompMix, PHASE>(geo, off, a, st);
       else if (mode == kS8HiOnly) launch_stage<kS8HiOnly, PHASE>(geo, off, a, st);
       else if (mode == kS8F16) launch_stage<kS8F16, PHASE>(geo, off, a, st);
       else launch_stage<SMX_S8_FP32, PHASE>(geo, off, a, st);
