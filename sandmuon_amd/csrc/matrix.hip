@@ -195,9 +195,18 @@ __global__ void __launch_bounds__(64) matrix_prep_kernel(PrepPack pack) {
 }
 
 // Blocks per matrix of the row kernels (host MatJob or device DevJob).
+// Row groups (4 / wpr rows, one per wave group) per whiten block: a job
+// whose row fits the lanes' registers takes kWhitenGroups of them in turn,
+// the next group's loads in flight while the current one is reduced and
+// stored; the other jobs take one.
+constexpr int kWhitenGroups = 4;
+template <typename Job>
+__host__ __device__ inline bool whiten_pipelined(const Job &j) {
+  return !j.flip && j.wvec && j.slices <= kMaxSlices;
+}
 template <typename Job>
 __host__ __device__ inline int64_t whiten_blocks(const Job &j) {
-  return j.flip ? j.prow_pad / kFlipRows : j.prow_pad / (4 / j.wpr);
+  return j.flip ? j.prow_pad / kFlipRows : j.prow_pad / (4 / j.wpr) / (whiten_pipelined(j) ? kWhitenGroups : 1);
 }
 template <typename Job>
 __host__ __device__ inline int64_t mapback_blocks(const Job &j) { return ceil_div(j.d.rows, 4 / j.wpr); }
@@ -345,14 +354,178 @@ __device__ __forceinline__ void block_part(const DevJob &J, double vy, double vu
   }
 }
 
+// Operand-form store of four consecutive elements per lane, lanes in pairs
+// (lane ^ 1 holds the next four): in BF16 planes the even lane writes the
+// pair's 8 hi values and the odd lane their 8 lo values, 16 bytes each, so
+// that the 4 lanes of a 16-element group fill its 64 bytes in one store
+// instruction (as FP32 does); each lane writes alone where its partner's
+// columns lie outside the row.  idx = the lane's first element (idx % 4 == 0).
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void put_operand4_paired(SMX_GLOBAL float *base, int64_t idx, const float (&v)[4],
+                                                    bool planes, bool pair) {
+  if (!planes) {
+    *reinterpret_cast<SMX_GLOBAL f32x4v *>(base + idx) = f32x4v{v[0], v[1], v[2], v[3]};
+    return;
+  }
+  const uint32_t h0 = bf16_bits(v[0]) | (uint32_t(bf16_bits(v[1])) << 16);
+  const uint32_t h1 = bf16_bits(v[2]) | (uint32_t(bf16_bits(v[3])) << 16);
+  const uint32_t l0 = bf16_lo_bits(v[0]) | (uint32_t(bf16_lo_bits(v[1])) << 16);
+  const uint32_t l1 = bf16_lo_bits(v[2]) | (uint32_t(bf16_lo_bits(v[3])) << 16);
+  const bool odd = (threadIdx.x & 1) != 0;
+  // the partner's hi (to an even lane) or lo (to an odd lane)
+  const uint32_t x0 = dpp_mov<0xB1>(odd ? h0 : l0), x1 = dpp_mov<0xB1>(odd ? h1 : l1);
+  SMX_GLOBAL uint16_t *h = reinterpret_cast<SMX_GLOBAL uint16_t *>(base) + plane_hi(idx);
+  if (pair) {
+    if (odd)  // lo of the pair: the even lane's four, then this lane's
+      *reinterpret_cast<SMX_GLOBAL u32x4v *>(h + 16 - 4) = u32x4v{x0, x1, l0, l1};
+    else
+      *reinterpret_cast<SMX_GLOBAL u32x4v *>(h) = u32x4v{h0, h1, x0, x1};
+  } else {
+    *reinterpret_cast<SMX_GLOBAL u32x2v *>(h) = u32x2v{h0, h1};
+    *reinterpret_cast<SMX_GLOBAL u32x2v *>(h + 16) = u32x2v{l0, l1};
+  }
+}
+
+// Rows whose float4 fit kMaxSlices per lane (the float4 path): the block
+// takes kWhitenGroups row groups in turn.  a and z are the same for every
+// row a lane sees and are loaded once; the g and m' of group k + 1 are
+// loaded while group k is reduced and stored.
 template <bool R1>
-__global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
-  __shared__ double red[4][4];  // row_sums
-  __shared__ double rp[2][4];
-  const int jid = find_job(range, blockIdx.x);
-  const DevJob J = load_job(range.jobs, jid);
+__device__ __forceinline__ void whiten_rows_pipelined(const DevJob &J, int blk, double (*red)[4][4],
+                                                      double (*rp)[4]) {
   const DevDesc &d = J.d;
-  const int blk = blockIdx.x - range.start[jid];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = J.wpr, rib = wave / W, wr = wave % W, rpg = 4 / W;
+  const int q0 = wr * 64 + lane, span = 64 * W;
+  const int n4 = static_cast<int>(d.cols / 4), pc4 = static_cast<int>(J.pcol_pad / 4);
+  const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
+  const float kappa = R1 ? d.kappa[0] : 0.f;
+  const bool planes = J.planes != 0;
+  const int64_t row0 = static_cast<int64_t>(blk) * kWhitenGroups * rpg + rib;
+  float4 a[kMaxSlices], z[kMaxSlices];
+  float bb[kWhitenGroups];
+#pragma unroll
+  for (int t = 0; t < kMaxSlices; ++t) {
+    const int q = q0 + span * t;
+    a[t] = z[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < J.slices && q < n4) {
+      a[t] = ld4(d.inv_col, q);
+      if constexpr (R1) z[t] = ld4(d.z, q);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kWhitenGroups; ++k) {
+    const int64_t i = row0 + k * rpg;
+    bb[k] = i < d.rows ? d.inv_row[i] : 0.f;
+  }
+  float4 g[2][kMaxSlices], m[2][kMaxSlices];
+  auto load_rows = [&](int k, float4 (&gg)[kMaxSlices], float4 (&mm)[kMaxSlices]) {
+    const int64_t i = row0 + k * rpg;
+    if (i >= d.rows) return;
+    const SMX_GLOBAL float *grow = (const SMX_GLOBAL float *)d.grad + i * d.cols;
+    const SMX_GLOBAL float *mrow = d.momentum + i * d.cols;
+#pragma unroll
+    for (int t = 0; t < kMaxSlices; ++t) {
+      const int q = q0 + span * t;
+      if (t < J.slices && q < n4) {
+        gg[t] = ld4(grow, q);
+        mm[t] = ld4(mrow, q);
+      }
+    }
+  };
+  load_rows(0, g[0], m[0]);
+  double vy = 0.0, vu = 0.0;  // the b^2 |S a|^2 and u^2 of the wave group's rows, in order
+#pragma unroll
+  for (int k = 0; k < kWhitenGroups; ++k) {
+    const int c = k & 1;
+    if (k + 1 < kWhitenGroups) load_rows(k + 1, g[c ^ 1], m[c ^ 1]);
+    const int64_t i = row0 + k * rpg;
+    const bool live = i < d.rows;
+    SMX_GLOBAL float *mrow = d.momentum + i * d.cols;
+    float y2 = 0.f, yz = 0.f;
+    float4 y[kMaxSlices];
+#pragma unroll
+    for (int t = 0; t < kMaxSlices; ++t) {
+      const int q = q0 + span * t;
+      y[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (live && t < J.slices && q < n4) {
+        const float4 gg = g[c][t], aa = a[t];
+        float4 mm = m[c][t];
+        mm.x = fmaf(mm.x, beta, gg.x * omb); mm.y = fmaf(mm.y, beta, gg.y * omb);
+        mm.z = fmaf(mm.z, beta, gg.z * omb); mm.w = fmaf(mm.w, beta, gg.w * omb);
+        st4(mrow, q, mm);
+        float4 yy;
+        yy.x = fmaf(mm.x, beta, gg.x * omb) * aa.x; yy.y = fmaf(mm.y, beta, gg.y * omb) * aa.y;
+        yy.z = fmaf(mm.z, beta, gg.z * omb) * aa.z; yy.w = fmaf(mm.w, beta, gg.w * omb) * aa.w;
+        y2 = fmaf(yy.x, yy.x, fmaf(yy.y, yy.y, fmaf(yy.z, yy.z, fmaf(yy.w, yy.w, y2))));
+        if constexpr (R1) {
+          const float4 zz = z[t];
+          yz = fmaf(yy.x, zz.x, fmaf(yy.y, zz.y, fmaf(yy.z, zz.z, fmaf(yy.w, zz.w, yz))));
+        }
+        y[t] = yy;
+      }
+    }
+    double v[2] = {static_cast<double>(wave_sum(y2)), static_cast<double>(wave_sum(yz))};
+    if (W > 1) {  // uniform per block; red[k & 1] alternates, so one barrier per group suffices
+      if (lane == 0) {
+        red[k & 1][wave][0] = v[0];
+        red[k & 1][wave][1] = v[1];
+      }
+      __syncthreads();
+      v[0] = v[1] = 0.0;
+      for (int w = 0; w < W; ++w) {
+        v[0] += red[k & 1][rib * W + w][0];
+        v[1] += red[k & 1][rib * W + w][1];
+      }
+    }
+    const float b = bb[k];
+    float ku = 0.f;
+    if (live) {
+      const double bd = b;
+      const double u = bd * v[1];
+      ku = R1 ? kappa * static_cast<float>(u) : 0.f;
+      vy += bd * bd * v[0];
+      vu += u * u;
+      if (lane == 0 && wr == 0) J.u[i] = static_cast<float>(u);
+    }
+    // V_ij = b_i y_j + kappa u_i z_j, zeros in padding rows and columns
+    SMX_GLOBAL float *xrow = J.x + i * J.pcol_pad;
+#pragma unroll
+    for (int t = 0; t < kMaxSlices; ++t) {
+      const int q = q0 + span * t;
+      if (t < J.slices && q < pc4) {
+        float w[4] = {0.f, 0.f, 0.f, 0.f};
+        if (live && q < n4) {
+          const float4 yy = y[t], zz = z[t];
+          w[0] = fmaf(ku, zz.x, b * yy.x); w[1] = fmaf(ku, zz.y, b * yy.y);
+          w[2] = fmaf(ku, zz.z, b * yy.z); w[3] = fmaf(ku, zz.w, b * yy.w);
+        }
+        // pc4 is a multiple of 4 and q0 + span t steps by lanes, so both
+        // lanes of a pair are inside the row or both outside
+        put_operand4_paired(xrow, 4 * static_cast<int64_t>(q), w, planes, true);
+      }
+    }
+  }
+  if (lane == 0 && wr == 0) {
+    rp[0][rib] = vy;
+    rp[1][rib] = vu;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    double t = 0.0;
+    for (int r = 0; r < rpg; ++r) t += rp[threadIdx.x][r];
+    J.fro[threadIdx.x * whiten_blocks(J) + blk] = t;
+  }
+}
+
+// The other rows (wide rows in passes of kMaxSlices float4, or a
+// gradient without the float4 path): one row group per block.
+template <bool R1>
+__device__ __forceinline__ void whiten_rows_single(const DevJob &J, int blk, double (*red)[4], double (*rp)[4]) {
+  const DevDesc &d = J.d;
   const RowPos p = row_pos(J, blk);
   const int lane = threadIdx.x & 63;
   const bool live = p.i < d.rows;
@@ -366,12 +539,10 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
   // ---- pass 1: m' (stored), y = S a of the lane's columns, and the row's
   // sum y^2 and y.z.
   float y2 = 0.f, yz = 0.f;
-  float4 yk[kMaxSlices];
-  const bool kept = J.wvec && J.slices <= kMaxSlices;  // uniform per block
   if (J.wvec) {
     const int n4 = static_cast<int>(d.cols / 4);
     const SMX_GLOBAL float *grow = live ? (const SMX_GLOBAL float *)d.grad + p.i * d.cols : nullptr;
-    // Slices [t0, t0 + kMaxSlices) of the row; y goes to yk.
+    // Slices [t0, t0 + kMaxSlices) of the row.
     auto pass1 = [&](int t0) {
       float4 g[kMaxSlices], m[kMaxSlices], a[kMaxSlices], z[kMaxSlices];
 #pragma unroll
@@ -405,7 +576,6 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
             if constexpr (R1) yz = fmaf(y.x, zz4.x, fmaf(y.y, zz4.y, fmaf(y.z, zz4.z, fmaf(y.w, zz4.w, yz))));
           }
         }
-        yk[t] = y;
       }
     };
     for (int t0 = 0; t0 < J.slices; t0 += kMaxSlices) pass1(t0);
@@ -440,29 +610,7 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
 
   // ---- pass 2: V_ij = b_i y_j + kappa u_i z_j (zeros in padding rows and
   // columns) in operand form.
-  if (kept) {
-    // z again (a cached vector) rather than held through the row sums
-    const int n4 = static_cast<int>(d.cols / 4);
-    float4 zk[kMaxSlices];
-#pragma unroll
-    for (int t = 0; t < kMaxSlices; ++t) {
-      const int q = p.q0 + p.span * t;
-      zk[t] = R1 && live && t < J.slices && q < n4 ? ld4(d.z, q) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int t = 0; t < kMaxSlices; ++t) {
-      const int q = p.q0 + p.span * t;
-      if (t < J.slices && q < pc4) {
-        float w[4] = {0.f, 0.f, 0.f, 0.f};
-        if (live && q < n4) {
-          const float4 y = yk[t], z = zk[t];
-          w[0] = fmaf(ku, z.x, b * y.x); w[1] = fmaf(ku, z.y, b * y.y);
-          w[2] = fmaf(ku, z.z, b * y.z); w[3] = fmaf(ku, z.w, b * y.w);
-        }
-        put_operand4((float *)xrow, 4 * q, w, planes);
-      }
-    }
-  } else if (J.wvec) {
+  if (J.wvec) {
     // Wide rows: m' and g again (the row was just read and written).
     const int n4 = static_cast<int>(d.cols / 4);
     const SMX_GLOBAL float *grow = live ? (const SMX_GLOBAL float *)d.grad + p.i * d.cols : nullptr;
@@ -509,6 +657,19 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
     }
   }
   block_part(J, vy, vu, p, blk, static_cast<int>(whiten_blocks(J)), J.fro, rp);
+}
+
+template <bool R1>
+__global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
+  __shared__ double red[2][4][4];  // row sums over the waves of a row
+  __shared__ double rp[2][4];
+  const int jid = find_job(range, blockIdx.x);
+  const DevJob J = load_job(range.jobs, jid);
+  const int blk = blockIdx.x - range.start[jid];
+  if (whiten_pipelined(J))
+    whiten_rows_pipelined<R1>(J, blk, red, rp);
+  else
+    whiten_rows_single<R1>(J, blk, red[0], rp);
 }
 
 // Transposed parameters: one wave per row, kFlipRows rows per block, the
