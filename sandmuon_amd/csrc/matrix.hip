@@ -95,11 +95,10 @@ __device__ __forceinline__ int find_job(const JobRange &r, int b) {
 }
 
 // The job as the row kernels hold it, with every pointer in the global
-// address space: a pointer read from memory (the job table) is a generic
-// pointer to the compiler, and accesses through it would be FLAT
+// address space (SMX_GLOBAL): a pointer read from memory (the job table) is
+// a generic pointer to the compiler, and accesses through it would be FLAT
 // instructions, which also count against the LDS / scalar wait counter and
 // address with a 64-bit VGPR pair per access.
-#define SMX_GLOBAL __attribute__((address_space(1)))
 struct DevDesc {
   SMX_GLOBAL void *param;
   const SMX_GLOBAL void *grad;
@@ -351,40 +350,6 @@ __device__ __forceinline__ void block_part(const DevJob &J, double vy, double vu
     double t = 0.0;
     for (int r = 0; r < 4 / J.wpr; ++r) t += rp[threadIdx.x][r];
     parts[threadIdx.x * nblk + blk] = t;
-  }
-}
-
-// Operand-form store of four consecutive elements per lane, lanes in pairs
-// (lane ^ 1 holds the next four): in BF16 planes the even lane writes the
-// pair's 8 hi values and the odd lane their 8 lo values, 16 bytes each, so
-// that the 4 lanes of a 16-element group fill its 64 bytes in one store
-// instruction (as FP32 does); each lane writes alone where its partner's
-// columns lie outside the row.  idx = the lane's first element (idx % 4 == 0).
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-typedef float f32x4v __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void put_operand4_paired(SMX_GLOBAL float *base, int64_t idx, const float (&v)[4],
-                                                    bool planes, bool pair) {
-  if (!planes) {
-    *reinterpret_cast<SMX_GLOBAL f32x4v *>(base + idx) = f32x4v{v[0], v[1], v[2], v[3]};
-    return;
-  }
-  const uint32_t h0 = bf16_bits(v[0]) | (uint32_t(bf16_bits(v[1])) << 16);
-  const uint32_t h1 = bf16_bits(v[2]) | (uint32_t(bf16_bits(v[3])) << 16);
-  const uint32_t l0 = bf16_lo_bits(v[0]) | (uint32_t(bf16_lo_bits(v[1])) << 16);
-  const uint32_t l1 = bf16_lo_bits(v[2]) | (uint32_t(bf16_lo_bits(v[3])) << 16);
-  const bool odd = (threadIdx.x & 1) != 0;
-  // the partner's hi (to an even lane) or lo (to an odd lane)
-  const uint32_t x0 = dpp_mov<0xB1>(odd ? h0 : l0), x1 = dpp_mov<0xB1>(odd ? h1 : l1);
-  SMX_GLOBAL uint16_t *h = reinterpret_cast<SMX_GLOBAL uint16_t *>(base) + plane_hi(idx);
-  if (pair) {
-    if (odd)  // lo of the pair: the even lane's four, then this lane's
-      *reinterpret_cast<SMX_GLOBAL u32x4v *>(h + 16 - 4) = u32x4v{x0, x1, l0, l1};
-    else
-      *reinterpret_cast<SMX_GLOBAL u32x4v *>(h) = u32x4v{h0, h1, x0, x1};
-  } else {
-    *reinterpret_cast<SMX_GLOBAL u32x2v *>(h) = u32x2v{h0, h1};
-    *reinterpret_cast<SMX_GLOBAL u32x2v *>(h + 16) = u32x2v{l0, l1};
   }
 }
 

@@ -1337,13 +1337,15 @@ s8_stage_kernel(StageArgs args) {
 // matrices of a class: P1 = a I + (b G)/s^2 + (c G2)/s^4 from the
 // normalised G and the FP32 G2 of the square phase, written over G2 in the
 // p buffer in operand form (into qa, as Q1, for a Gram-space class).  A
-// block takes kPolyChunk consecutive
-// 16-element groups of one matrix (64 KB of each buffer, contiguous), a
-// thread kPolyGroups of them; whole groups keep the FP32 and interleaved
-// BF16 forms in the same 64 bytes.  The loads are issued before the block
-// sums the stage-1 scalars, which they do not depend on.
-constexpr int kPolyGroups = 4;
-constexpr int kPolyChunk = 256 * kPolyGroups;  // groups per block
+// block takes kPolyChunk consecutive 16-element groups of one matrix, four
+// lanes per group, each lane a quarter (4 elements: 16 bytes of FP32, 8 of
+// each BF16 half), so that every load and store instruction of a wave
+// covers 16 whole groups (1 KB); a thread takes kPolyUnits quarters.  All
+// loads are issued before the block sums the stage-1 scalars, which they do
+// not depend on.  (In place for an X-space class: the lanes of a group are
+// one wave's, and a group's loads complete before any of its stores.)
+constexpr int kPolyUnits = 4;
+constexpr int kPolyChunk = 256 * kPolyUnits / 4;  // groups per block
 
 __host__ __device__ inline int64_t poly_blocks_per_matrix(const S8Class &k) {
   return k.rp * k.rp / 16 / kPolyChunk;  // rp is a multiple of 256
@@ -1360,62 +1362,54 @@ __global__ void __launch_bounds__(256) s8_poly1_kernel(StageArgs args) {
   const S8Mat M{K, ref.slot0 + static_cast<int>(ref.L / tpm)};
   const int64_t g0 = (ref.L % tpm) * kPolyChunk;  // first group of the block
   const int64_t gpr = K.rp / 16;                   // groups per row
+  const int qt = threadIdx.x & 3;                  // the lane's quarter of its groups
   const float *G = M.g();
-  float *P = M.p();                       // FP32 G2 in, and P1 out for an X-space class
-  float *Pout = K.gs ? M.qa() : M.p();    // Gram space: P1 is Q1
-  int64_t row[kPolyGroups], col[kPolyGroups], idx[kPolyGroups];
-  float4 w4[kPolyGroups][4];
-  uint4 g4[kPolyGroups][4];  // FP32 G, or its 16 hi then 16 lo BF16 values
+  const float *P = M.p();                                           // FP32 G2
+  SMX_GLOBAL float *Pout = (SMX_GLOBAL float *)(K.gs ? M.qa() : M.p());  // Gram space: P1 is Q1
+  int64_t grp[kPolyUnits];
+  float4 w4[kPolyUnits];
+  uint2 gh[kPolyUnits], gl[kPolyUnits];  // BF16 hi and lo of the quarter, or its FP32 G
 #pragma unroll
-  for (int k = 0; k < kPolyGroups; ++k) {
-    const int64_t q = g0 + threadIdx.x + 256 * k;
-    row[k] = q / gpr;
-    col[k] = (q % gpr) * 16;
-    idx[k] = q * 16;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      w4[k][e] = reinterpret_cast<const float4 *>(P + idx[k])[e];
-      g4[k][e] = reinterpret_cast<const uint4 *>(G + idx[k])[e];
+  for (int k = 0; k < kPolyUnits; ++k) {
+    grp[k] = g0 + (threadIdx.x + 256 * k) / 4;
+    const int64_t idx = grp[k] * 16 + 4 * qt;
+    w4[k] = *reinterpret_cast<const float4 *>(P + idx);
+    if constexpr (PL) {
+      const char *gb = reinterpret_cast<const char *>(G + grp[k] * 16);
+      gh[k] = *reinterpret_cast<const uint2 *>(gb + 8 * qt);
+      gl[k] = *reinterpret_cast<const uint2 *>(gb + 32 + 8 * qt);
+    } else {
+      const uint4 g = *reinterpret_cast<const uint4 *>(G + idx);
+      gh[k] = make_uint2(g.x, g.y);
+      gl[k] = make_uint2(g.z, g.w);
     }
   }
   const Stage1Scalars sc = stage1_scalars(M, args.sq_geo, &bcast);
   const float s2 = sc.s * sc.s;
   const float is2 = sc.ok ? 1.0f / s2 : 0.f, is4 = sc.ok ? 1.0f / (s2 * s2) : 0.f;
 #pragma unroll
-  for (int k = 0; k < kPolyGroups; ++k) {
-    float g[16], w[16];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      w[4 * e] = w4[k][e].x; w[4 * e + 1] = w4[k][e].y; w[4 * e + 2] = w4[k][e].z; w[4 * e + 3] = w4[k][e].w;
-    }
+  for (int k = 0; k < kPolyUnits; ++k) {
+    const float w[4] = {w4[k].x, w4[k].y, w4[k].z, w4[k].w};
+    float g[4];
     if constexpr (PL) {
-      const uint32_t hw[8] = {g4[k][0].x, g4[k][0].y, g4[k][0].z, g4[k][0].w,
-                              g4[k][1].x, g4[k][1].y, g4[k][1].z, g4[k][1].w};
-      const uint32_t lw[8] = {g4[k][2].x, g4[k][2].y, g4[k][2].z, g4[k][2].w,
-                              g4[k][3].x, g4[k][3].y, g4[k][3].z, g4[k][3].w};
+      const uint32_t hw[2] = {gh[k].x, gh[k].y}, lw[2] = {gl[k].x, gl[k].y};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < 2; ++e) {
         g[2 * e] = __uint_as_float(hw[e] << 16) + __uint_as_float(lw[e] << 16);
         g[2 * e + 1] = __uint_as_float(hw[e] & 0xffff0000u) + __uint_as_float(lw[e] & 0xffff0000u);
       }
     } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        g[4 * e] = __uint_as_float(g4[k][e].x); g[4 * e + 1] = __uint_as_float(g4[k][e].y);
-        g[4 * e + 2] = __uint_as_float(g4[k][e].z); g[4 * e + 3] = __uint_as_float(g4[k][e].w);
-      }
+      g[0] = __uint_as_float(gh[k].x); g[1] = __uint_as_float(gh[k].y);
+      g[2] = __uint_as_float(gl[k].x); g[3] = __uint_as_float(gl[k].y);
     }
-    float v[16];
+    const int64_t row = grp[k] / gpr, col = (grp[k] % gpr) * 16 + 4 * qt;
+    float v[4];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float eye = (row[k] == col[k] + e && row[k] < K.r) ? args.a : 0.f;
+    for (int e = 0; e < 4; ++e) {
+      const float eye = (row == col + e && row < K.r) ? args.a : 0.f;
       v[e] = (eye + (args.b * g[e]) * is2) + (args.c * w[e]) * is4;
     }
-    float lo8[8], hi8[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) { lo8[e] = v[e]; hi8[e] = v[8 + e]; }
-    put_operand8(Pout, idx[k], lo8, PL);
-    put_operand8(Pout, idx[k] + 8, hi8, PL);
+    put_operand4_paired(Pout, grp[k] * 16 + 4 * qt, v, PL, true);
   }
 }
 
