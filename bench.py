@@ -56,6 +56,20 @@ def parse():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run 3 plain device copies of MB megabytes (the known-size reference for "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
+    g = ap.add_argument_group("profile summaries (no GPU: text summaries of rocprofv3 --output-format csv runs "
+                              "of this script, as committed under profiles/)")
+    g.add_argument("--summarize", choices=["trace", "counters", "traffic"],
+                   help="trace: a --kernel-trace run; counters: a --pmc run; traffic: the FETCH_SIZE and "
+                        "WRITE_SIZE runs of the workload and of --copy-calibration (four --prof-dir, in that order)")
+    g.add_argument("--prof-dir", action="append", default=[], help="rocprofv3 output directory (-d)")
+    g.add_argument("--prof-command", action="append", default=[],
+                   help="the command that made each --prof-dir (quoted in the summary)")
+    g.add_argument("--title", default="", help="first line of the summary")
+    g.add_argument("--run-steps", type=int, default=3,
+                   help="optimizer steps in the profiled run (per-step figures = run totals / this)")
+    g.add_argument("--copy-mb", type=int, default=512, help="the --copy-calibration size of the traffic runs")
+    g.add_argument("--out", help="summary text file (default: stdout)")
+    g.add_argument("--json-out", help="traffic: the per-kernel bytes as JSON (bench.py reads profiles/traffic_cfg4.json)")
     return ap.parse_args()
 
 
@@ -395,9 +409,253 @@ def train_bench(args, device):
     print(json.dumps(out), flush=True)
 
 
+# ------------------------------------------------------- profile summaries ---
+# Text summaries of the rocprofv3 runs of this script (CSV output), the form
+# committed under profiles/.  Counter values are per dispatch, summed over
+# the hardware instances by rocprofv3 (SQ counters over the shader engines,
+# GRBM counters over the 8 XCDs).
+S8_PHASE_NAMES = {"0": "gram", "1": "square", "2": "apply", "5": "sym"}
+
+
+def _prof_rows(d, stem):
+    import csv
+    import glob
+    import gzip
+    files = sorted(glob.glob(os.path.join(d, "**", f"*{stem}.csv"), recursive=True) +
+                   glob.glob(os.path.join(d, "**", f"*{stem}.csv.gz"), recursive=True))
+    if not files:
+        sys.exit(f"no *{stem}.csv(.gz) under {d}")
+    rows = []
+    for f in files:
+        with (gzip.open(f, "rt") if f.endswith(".gz") else open(f)) as fh:
+            rows += list(csv.DictReader(fh))
+    return rows
+
+
+def _kname(name):
+    """Kernel name without namespace and argument list, template arguments kept."""
+    n = name.replace("void ", "").replace("smx::", "").replace("(anonymous namespace)::", "")
+    if n.startswith("Cijk_"):  # hipBLASLt: its macro tile names the kernel
+        tile = [t for t in n.split("_") if t.startswith("MT")]
+        return "hipBLASLt " + (tile[0] if tile else n[:24])
+    return n.split("(")[0] if "(" in n else n
+
+
+def _git_head():
+    import subprocess
+    try:
+        here = os.path.dirname(os.path.abspath(__file__))
+        return subprocess.run(["git", "-C", here, "rev-parse", "--short", "HEAD"], capture_output=True,
+                              text=True, check=True).stdout.strip()
+    except Exception:
+        return "unknown"
+
+
+def _header(args, lines):
+    out = [f"# {args.title}" if args.title else "# rocprofv3 summary", ""]
+    cmds = args.prof_command or []
+    out.append("command:" if len(cmds) == 1 else "commands:")
+    out += [f"  {c}" for c in cmds]
+    out.append(f"summary: python bench.py --summarize {args.summarize} " +
+               " ".join(f"--prof-dir {d}" for d in args.prof_dir) + f" --run-steps {args.run_steps}")
+    out.append(f"code: git {_git_head()}")
+    out.append("")
+    return out + lines + [""]
+
+
+def _steps_of(trace):
+    """Start indices of step(): the first finish_fold launch after any other kernel."""
+    return [i for i, r in enumerate(trace) if "finish_fold_kernel" in r["name"] and
+            (i == 0 or "finish_fold_kernel" not in trace[i - 1]["name"] and "finish_kernel" not in trace[i - 1]["name"])]
+
+
+def summarize_trace(args):
+    rows = _prof_rows(args.prof_dir[0], "kernel_trace")
+    trace = sorted(({"name": r["Kernel_Name"], "q": int(r["Queue_Id"]), "t0": int(r["Start_Timestamp"]),
+                     "t1": int(r["End_Timestamp"])} for r in rows), key=lambda r: r["t0"])
+    agg = {}
+    for r in trace:
+        a = agg.setdefault(_kname(r["name"]), [0, 0.0])
+        a[0] += 1
+        a[1] += (r["t1"] - r["t0"]) / 1e3
+    total = sum(v[1] for v in agg.values())
+    lines = ["Durations are rocprofv3 per-dispatch GPU times over the whole run (warm-up, timed and per-launch",
+             "timing steps of bench.py, plus the synthetic-input setup: at::native kernels).  The S8 launches",
+             "run as two chains on two streams (two HW queues), so their durations overlap in time.", "",
+             f"{'kernel':<60}{'calls':>7}{'total_ms':>11}{'avg_us':>10}{'pct':>7}"]
+    for n, (c, us) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        lines.append(f"{n[:59]:<60}{c:>7}{us / 1e3:>11.2f}{us / c:>10.1f}{100 * us / total:>7.2f}")
+    st = _steps_of(trace)
+    lines += ["", "## Statistics launches before each step()"]
+    prev = 0
+    for i in st:
+        lines.append(f"  {sum('stats_accumulate_kernel' in r['name'] for r in trace[prev:i])} launches")
+        prev = i
+    if len(st) >= 2:
+        # the last timed step (the run's last step carries per-launch timing events)
+        a, b = st[-2], st[-1]
+        b = next((k for k in range(a + 1, b) if "stats_accumulate_kernel" in trace[k]["name"]), b)
+        step = trace[a:b]
+        t0 = step[0]["t0"]
+        span = (max(r["t1"] for r in step) - t0) / 1e3
+        lines += ["", f"## One timed step(), in launch order (start offset, duration, HW queue): span {span:.1f} us"]
+        for r in step:
+            lines.append(f"  {(r['t0'] - t0) / 1e3:9.1f} us {(r['t1'] - r['t0']) / 1e3:8.1f} us  q{r['q']}  "
+                         f"{_kname(r['name'])}")
+        per = {}
+        for r in step:
+            per[_kname(r["name"])] = per.get(_kname(r["name"]), 0.0) + (r["t1"] - r["t0"]) / 1e3
+        lines += ["", "## GPU time of that step() by kernel (us; the two S8 chains overlap)"]
+        for n, us in sorted(per.items(), key=lambda kv: -kv[1]):
+            lines.append(f"  {us:9.1f}  {n}")
+    return "\n".join(_header(args, lines))
+
+
+def _dispatches(d):
+    """{dispatch id: {"name", "dur_ns", counter: value}} of a --pmc run."""
+    out = {}
+    for r in _prof_rows(d, "counter_collection"):
+        e = out.setdefault(r["Dispatch_Id"], {"name": r["Kernel_Name"],
+                                              "dur_ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+        e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return out
+
+
+def summarize_counters(args):
+    disp = _dispatches(args.prof_dir[0])
+    groups = {}
+    for e in disp.values():
+        groups.setdefault(_kname(e["name"]), []).append(e)
+    counters = sorted({k for e in disp.values() for k in e if k not in ("name", "dur_ns")})
+    lines = ["Per kernel: launches in the profiled run, average launch time (counter runs serialise the",
+             "launches, so the two S8 chains do not overlap here) and the run totals of each counter per launch.",
+             "Derived, where the counters are present:",
+             "  clock_GHz = GRBM_GUI_ACTIVE / 8 XCDs / launch time (launches under 30 us: '-', their counter",
+             "  window is longer than the launch);",
+             "  issued TFLOP/s = SQ_VALU_MFMA_BUSY_CYCLES x 1024 FLOP / launch time, %nom against 2.5 PFLOP/s,",
+             "  %clk against 2.5 PFLOP/s x clock / 2.4 GHz;",
+             "  fractions of SQ_WAVE_CYCLES: wait_issue = SQ_WAIT_INST_ANY (waiting to issue the next",
+             "  instruction), wait_any = SQ_WAIT_ANY (memory counters, barriers), wait_lds = SQ_WAIT_INST_LDS,",
+             "  valu / lds = SQ_ACTIVE_INST_VALU / _LDS, vmem_cyc = SQ_INST_CYCLES_VMEM;",
+             "  MOPS/LDS = (SQ_INSTS_VALU_MFMA_MOPS_BF16 + _F16) per SQ_INSTS_LDS (one MOP = 512 FLOP).", ""]
+    hdr = f"{'kernel':<44}{'calls':>6}{'avg_us':>9}"
+    have = set(counters)
+    if "GRBM_GUI_ACTIVE" in have:
+        hdr += f"{'clk_GHz':>9}"
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in have:
+        hdr += f"{'TFLOP/s':>9}{'%nom':>7}{'%clk':>7}"
+    labels = {"SQ_WAIT_INST_ANY": "wait_issue", "SQ_WAIT_ANY": "wait_any", "SQ_WAIT_INST_LDS": "wait_lds",
+              "SQ_ACTIVE_INST_VALU": "valu", "SQ_ACTIVE_INST_LDS": "lds", "SQ_INST_CYCLES_VMEM": "vmem_cyc"}
+    waits = [c for c in labels if c in have and "SQ_WAVE_CYCLES" in have]
+    hdr += "".join(f"{labels[c]:>11}" for c in waits)
+    lds = "SQ_INSTS_LDS" in have
+    if lds:
+        hdr += f"{'LDS_insts':>11}{'conflict':>11}{'MOPS/LDS':>9}"
+    lines.append(hdr)
+    for n, es in sorted(groups.items(), key=lambda kv: -sum(e["dur_ns"] for e in kv[1])):
+        if n.startswith("at::") or n.startswith("__amd"):
+            continue
+        c = len(es)
+        dur = sum(e["dur_ns"] for e in es)
+        tot = lambda k: sum(e.get(k, 0.0) for e in es)
+        row = f"{n[:43]:<44}{c:>6}{dur / c / 1e3:>9.1f}"
+        clk = None
+        if "GRBM_GUI_ACTIVE" in have:
+            if dur / c >= 30e3:
+                clk = tot("GRBM_GUI_ACTIVE") / 8 / dur
+                row += f"{clk:>9.2f}"
+            else:
+                row += f"{'-':>9}"
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in have:
+            tf = tot("SQ_VALU_MFMA_BUSY_CYCLES") * 1024 / dur / 1e3
+            row += f"{tf:>9.1f}{100 * tf / 2500:>7.1f}"
+            row += f"{100 * tf / (2500 * clk / 2.4):>7.1f}" if clk else f"{'':>7}"
+        wc = tot("SQ_WAVE_CYCLES") if waits else 0.0
+        row += "".join(f"{tot(w) / wc:>11.3f}" if wc else f"{'':>11}" for w in waits)
+        if lds:
+            li = tot("SQ_INSTS_LDS")
+            mops = tot("SQ_INSTS_VALU_MFMA_MOPS_BF16") + tot("SQ_INSTS_VALU_MFMA_MOPS_F16")
+            row += f"{li / c:>11.3g}{tot('SQ_LDS_BANK_CONFLICT') / c:>11.3g}" + (f"{mops / li:>9.1f}" if li else "")
+        lines.append(row)
+    return "\n".join(_header(args, lines))
+
+
+def summarize_traffic(args):
+    fetch, write, cfetch, cwrite = (_dispatches(d) for d in args.prof_dir[:4])
+    copy_bytes = args.copy_mb * (1 << 20)
+
+    def copies(disp, counter):
+        v = [e[counter] for e in disp.values() if "copyBuffer" in e["name"] and e.get(counter)]
+        v.sort()
+        return v[len(v) // 2]  # the median copy of the calibration run (KiB)
+
+    cf, cw = copies(cfetch, "FETCH_SIZE"), copies(cwrite, "WRITE_SIZE")
+    fscale, wscale = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
+
+    def group(name):
+        k = _kname(name)
+        if k.startswith("s8_stage_kernel<"):
+            return ["s8_stage_kernel", "s8_stage_kernel " + S8_PHASE_NAMES.get(k.split("<")[1].split(",")[1].strip(), "?")]
+        return [k.split("<")[0]]
+
+    per = {}
+    for disp, key, scale, counter in ((fetch, "hbm_read_bytes_per_step", fscale, "FETCH_SIZE"),
+                                      (write, "hbm_write_bytes_per_step", wscale, "WRITE_SIZE")):
+        for e in disp.values():
+            if e["name"].startswith("void at::") or "__amd" in e["name"] or "Cijk" in e["name"]:
+                continue
+            for g in group(e["name"]):
+                d = per.setdefault(g, {"launches_per_step": 0.0, "hbm_read_bytes_per_step": 0.0,
+                                       "hbm_write_bytes_per_step": 0.0})
+                d[key] += e.get(counter, 0.0) * 1024 * scale / args.run_steps
+                if counter == "FETCH_SIZE":
+                    d["launches_per_step"] += 1 / args.run_steps
+    for d in per.values():
+        d["hbm_bytes_per_step"] = d["hbm_read_bytes_per_step"] + d["hbm_write_bytes_per_step"]
+        for k in d:
+            d[k] = round(d[k], 2) if k == "launches_per_step" else int(d[k])
+    js = {"calibration": {"copy_bytes": copy_bytes, "FETCH_SIZE_KiB": cf, "WRITE_SIZE_KiB": cw,
+                          "fetch_scale": fscale, "write_scale": wscale},
+          "commands": args.prof_command, "code": _git_head(), **per}
+    lines = [f"Calibration: a plain device copy of {copy_bytes} bytes reads FETCH_SIZE = {cf:.0f} KiB and "
+             f"WRITE_SIZE = {cw:.0f} KiB per dispatch,",
+             f"so fetch counts are scaled by {fscale:.3f} and write counts by {wscale:.3f}.",
+             f"Per step = counter totals of the profiled run / {args.run_steps} steps.", "",
+             f"{'kernel':<32}{'launches/step':>14}{'read GB':>10}{'write GB':>10}{'total GB':>10}"]
+    for n, d in sorted(per.items(), key=lambda kv: -kv[1]["hbm_bytes_per_step"]):
+        lines.append(f"{n:<32}{d['launches_per_step']:>14.2f}{d['hbm_read_bytes_per_step'] / 1e9:>10.3f}"
+                     f"{d['hbm_write_bytes_per_step'] / 1e9:>10.3f}{d['hbm_bytes_per_step'] / 1e9:>10.3f}")
+    return "\n".join(_header(args, lines)), js
+
+
+def summarize(args):
+    need = 4 if args.summarize == "traffic" else 1
+    if len(args.prof_dir) != need:
+        sys.exit(f"--summarize {args.summarize} takes {need} --prof-dir")
+    js = None
+    if args.summarize == "trace":
+        text = summarize_trace(args)
+    elif args.summarize == "counters":
+        text = summarize_counters(args)
+    else:
+        text, js = summarize_traffic(args)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(text)
+    else:
+        print(text)
+    if js is not None and args.json_out:
+        with open(args.json_out, "w") as f:
+            json.dump(js, f, indent=1)
+            f.write("\n")
+
+
 # ---------------------------------------------------------------- main ---
 def main():
     args = parse()
+    if args.summarize:
+        summarize(args)
+        return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
