@@ -62,3 +62,62 @@ def test_bench_line_has_the_contract_fields(device):
         assert probe[dt]["finite"] and probe[dt]["tflops"] > 0 and 1.0 < probe[dt]["clock_ghz"] < 3.0
         assert probe[dt]["tflops"] <= 1.02 * probe[dt]["nominal_tflops_at_clock"]
     assert 0 < s8["frac_of_probe"] <= 1
+
+
+def _write_csv(path, header, rows):
+    import csv
+    path.parent.mkdir(parents=True, exist_ok=True)
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f, quoting=csv.QUOTE_NONNUMERIC)
+        w.writerow(header)
+        w.writerows(rows)
+
+
+def test_profile_summaries_of_synthetic_rocprof_output(tmp_path):
+    """bench.py --summarize on hand-made rocprofv3 CSVs: a kernel trace of
+    two steps, a counter run, and the four traffic runs, whose figures are
+    known in closed form."""
+    trace = ["Kind", "Agent_Id", "Queue_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"]
+    rows, t = [], 0
+    for step in range(3):
+        for name, us in (("smx::stats_accumulate_kernel(smx::StatsPack)", 100), ("smx::finish_fold_kernel(x)", 5),
+                         ("smx::finish_kernel(x)", 5), ("void smx::s8_stage_kernel<1, 2, 256, 256>(smx::StageArgs)", 40)):
+            rows.append(["KERNEL_DISPATCH", "Agent 1", 1, name, t, t + us * 1000])
+            t += us * 1000 + 1000
+    _write_csv(tmp_path / "tr" / "run_kernel_trace.csv", trace, rows)
+    res = run_bench("--summarize", "trace", "--prof-dir", str(tmp_path / "tr"), "--prof-command", "cmd-t")
+    assert res.returncode == 0, res.stderr
+    out = res.stdout
+    assert "cmd-t" in out and "s8_stage_kernel<1, 2, 256, 256>" in out
+    stats = [l.split() for l in out.splitlines() if l.startswith("stats_accumulate_kernel")][0]
+    assert stats[1:4] == ["3", "0.30", "100.0"], stats
+    assert out.count("1 launches") == 3 and "span 52.0 us" in out  # fold 5 + 1 + finish 5 + 1 + S8 40
+
+    cc = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+    # a 100 us launch: 8 XCDs x 2.0 GHz, and 1.0e8 MFMA-busy cycles -> 1024 TFLOP/s
+    _write_csv(tmp_path / "pmc" / "run_counter_collection.csv", cc,
+               [[1, "void smx::s8_stage_kernel<1, 0, 128, 128>(smx::StageArgs)", "GRBM_GUI_ACTIVE", 8 * 2.0e5, 0,
+                 100000],
+                [1, "void smx::s8_stage_kernel<1, 0, 128, 128>(smx::StageArgs)", "SQ_VALU_MFMA_BUSY_CYCLES", 1.0e8, 0,
+                 100000]])
+    res = run_bench("--summarize", "counters", "--prof-dir", str(tmp_path / "pmc"), "--prof-command", "cmd-c")
+    assert res.returncode == 0, res.stderr
+    row = [l for l in res.stdout.splitlines() if l.startswith("s8_stage_kernel<1, 0, 128, 128>")][0].split()
+    assert row[-6:] == ["1", "100.0", "2.00", "1024.0", "41.0", "49.2"], row
+
+    # traffic: the copy of 1 MiB reads 512 KiB and writes 1024 KiB per dispatch
+    for d, counter, name, kib in (("f", "FETCH_SIZE", "smx::adamw_kernel(smx::AdamPack)", 300.0),
+                                  ("w", "WRITE_SIZE", "smx::adamw_kernel(smx::AdamPack)", 600.0),
+                                  ("cf", "FETCH_SIZE", "__amd_rocclr_copyBuffer", 512.0),
+                                  ("cw", "WRITE_SIZE", "__amd_rocclr_copyBuffer", 1024.0)):
+        _write_csv(tmp_path / d / "run_counter_collection.csv", cc, [[1, name, counter, kib, 0, 1000]])
+    js = tmp_path / "t.json"
+    args = ["--summarize", "traffic", "--run-steps", "1", "--copy-mb", "1", "--json-out", str(js)]
+    for d in ("f", "w", "cf", "cw"):
+        args += ["--prof-dir", str(tmp_path / d), "--prof-command", f"cmd-{d}"]
+    res = run_bench(*args)
+    assert res.returncode == 0, res.stderr
+    data = json.loads(js.read_text())
+    assert data["calibration"]["fetch_scale"] == 2.0 and data["calibration"]["write_scale"] == 1.0
+    assert data["adamw_kernel"] == {"launches_per_step": 1.0, "hbm_read_bytes_per_step": 600 * 1024,
+                                    "hbm_write_bytes_per_step": 600 * 1024, "hbm_bytes_per_step": 1200 * 1024}
