@@ -64,15 +64,16 @@ enum smx_dtype { SMX_F32 = 0, SMX_BF16 = 1, SMX_F16 = 2, SMX_F64 = 3 };
  *   the BF16 hi/lo pair.  The compensated-product scheme of
  *   reproduction/odl/ops/bf16_compensated_mm_fast.py:18-68, applied to all
  *   five stages.
- * SMX_S8_MIXED: stage 1 as SMX_S8_COMP_BF16 (it maps the raw input, whose
- *   range needs BF16's exponent); stages 2-5 on FP16 operands with FP32
- *   accumulation (v_mfma_f32_32x32x16_f16, one product per 16 K), except
- *   the two products of a wide matrix's stage 2 that reach back to the
- *   input (Q2 = P2 Q1 and X2 = Q2 X0), which stay compensated.  From stage
- *   2 on every operand is normalised, and FP16 rounds 8x finer than a plain
- *   BF16 product: measured direction error about 2e-3 against the FP32 map,
- *   at about half the MFMA work of SMX_S8_COMP_BF16.  No counterpart in the
- *   reference (whose historical recipe,
+ * SMX_S8_MIXED: stages 1 and 2 as SMX_S8_COMP_BF16 (stage 1 maps the raw
+ *   input, whose range needs BF16's exponent; stage 2's rounding is the
+ *   one the later stages amplify most); stages 3-5 of a matrix with
+ *   rows == cols after padding (run on the iterate, X-space) on FP16
+ *   operands with FP32 accumulation (v_mfma_f32_32x32x16_f16, one product
+ *   per 16 K).  A wider matrix (run on r x r Gram products) stays
+ *   compensated in every stage: its Gram has the square of the iterate's
+ *   spectrum, which FP16 does not hold.  Direction error up to about 3e-3
+ *   against the FP32 map; the S8 time falls with the share of square
+ *   matrices.  No counterpart in the reference (whose historical recipe,
  *   reproduction/odl/ops/dense_s8_compensated_fast.py:53-85, runs stages
  *   2-5 as plain BF16 products). */
 enum smx_s8_mode { SMX_S8_FP32 = 0, SMX_S8_COMP_BF16 = 1, SMX_S8_MIXED = 2 };

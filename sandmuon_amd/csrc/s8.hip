@@ -46,18 +46,24 @@
 //                     bit is clear in smx_s8_comp_mask (default 0x1f: none)
 //                     run as kS8HiOnly: the same stored operands, acc +=
 //                     hi*hi.
-//   SMX_S8_MIXED      stage 1 (and the two products of a Gram-space class
-//                     that reach back to X0 at stage 2, Q2 = P2 Q1 and X2 =
-//                     Q2 X0) as SMX_S8_COMP_BF16; every other product of
-//                     stages 2-5 as kS8F16: operands stored as FP16 (2 bytes
-//                     per element) and v_mfma_f32_32x32x16_f16 with FP32
-//                     accumulation.  Stage 1 maps the raw input, whose range
-//                     only BF16's exponent holds; from stage 2 on every
-//                     operand is normalised (|X| <= 1, G and P bounded, Q up
-//                     to its eigenvalue range, far below the FP16 maximum),
-//                     where FP16's 11-bit significand rounds 8x finer than a
-//                     plain BF16 product, at a third of the compensated
-//                     MFMAs and half the operand bytes.
+//   SMX_S8_MIXED      stages 1 and 2 as SMX_S8_COMP_BF16 (kernels of
+//                     mode kS8CompMix); stages 3-5 of an X-space class as
+//                     kS8F16: operands stored as FP16 (2 bytes per element)
+//                     and v_mfma_f32_32x32x16_f16 with FP32 accumulation.
+//                     Stage 1 maps the raw input, whose range only BF16's
+//                     exponent holds; from stage 2 on every operand is
+//                     normalised (|X| <= 1, G and P bounded, far below the
+//                     FP16 maximum), where FP16's 11-bit significand rounds
+//                     8x finer than a plain BF16 product, at a third of the
+//                     compensated MFMAs and half the operand bytes.  Stage
+//                     2 stays compensated: FP16 rounding there is what the
+//                     later stages amplify most.  A Gram-space class stays
+//                     compensated in every stage: its stages 3-5 carry the
+//                     Gram G = X X^T, whose spectrum is the square of the
+//                     iterate's, and an FP16 G loses the small eigenvalues
+//                     (1.1e-2 from the FP32 map on matrices whose singular
+//                     values decay as i^-1.5, against 3.4e-3 for the same
+//                     stages on an X-space class).
 //
 // Operand forms (what a producer writes, chosen by the mode of the product
 // that reads it, out_form): FP32, interleaved BF16 hi/lo ("planes"; the
@@ -131,27 +137,25 @@ __host__ __device__ constexpr int form_of(int gemm_mode) {
 
 // The MFMA mode of one product of the map (phase, stage and, for SYM and
 // APPLY, its SegOp) under the run's public `mode` and compensation mask.
-__host__ __device__ constexpr int gemm_mode(int mode, int mask, int phase, int stage, int op) {
+__host__ __device__ constexpr int gemm_mode(int mode, int mask, int phase, int stage, int op, bool gs) {
   return mode == SMX_S8_FP32 ? SMX_S8_FP32
          : mode == SMX_S8_COMP_BF16 ? (((mask >> (stage - 1)) & 1) ? SMX_S8_COMP_BF16 : kS8HiOnly)
-         : (stage == 1 || (phase == kApply && stage == 2 && (op == kOpApplyQ || op == kOpApplyMid)))
-             ? kS8CompMix
-             : kS8F16;
+         : (stage <= 2 || gs) ? kS8CompMix
+                              : kS8F16;
 }
 
 // The output forms a GEMM kernel of MFMA mode `gm` and phase `phase`
 // compiles (each kernel keeps only these epilogues): a Gram feeds its
 // stage's square (same mode); a square writes FP32 G2 at stage 1, else P
-// for its stage's products (an FP16 square also Q2's compensated P2); the
-// SYM products feed products of their own mode, except the compensated TP
-// of SMX_S8_MIXED's stage 1 (the FP16 stage-2 square); an apply feeds the
-// next stage, X2 or the FP32 result.
+// for its stage's products; the SYM products feed products of their own
+// mode; an apply feeds the next stage (in SMX_S8_MIXED the stage-2 apply,
+// compensated, writes the FP16 X2 or X-space iterate of stage 3), Q2 / X2,
+// or the FP32 result.
 __host__ __device__ constexpr bool form_compiled(int gm, int phase, int form) {
   return gm == SMX_S8_FP32 ? form == kFormF32
-         : gm == kS8F16 ? (form == kFormF16 || (form == kFormPlanes && phase == kSquare) ||
-                           (form == kFormF32 && phase == kApply))
+         : gm == kS8F16 ? (form == kFormF16 || (form == kFormF32 && phase == kApply))
          : form == kFormPlanes || (form == kFormF32 && (phase == kSquare || phase == kApply)) ||
-               (form == kFormF16 && gm == kS8CompMix && (phase == kSym || phase == kApply));
+               (form == kFormF16 && gm == kS8CompMix && phase == kApply);
 }
 
 // The form a product's output is stored in: that of the product that reads
@@ -162,16 +166,16 @@ __host__ __device__ constexpr bool form_compiled(int gm, int phase, int form) {
 // stage-3 Gram and X5).  The stage-1 square's G2 and the stage-5 result
 // are FP32.
 __host__ __device__ constexpr int out_form(int mode, int mask, int phase, int stage, int op, bool gs) {
-  return phase == kGram ? form_of(gemm_mode(mode, mask, kSquare, stage, -1))
+  return phase == kGram ? form_of(gemm_mode(mode, mask, kSquare, stage, -1, gs))
          : phase == kSquare ? (stage == 1 ? kFormF32
-                                          : form_of(gemm_mode(mode, mask, kApply, stage, gs ? kOpApplyQ : kOpApplyX)))
-         : phase == kPoly1 ? form_of(gemm_mode(mode, mask, kApply, 1, kOpApplyX))
-         : phase == kSym ? (op == kOpPG ? form_of(gemm_mode(mode, mask, kSym, stage, kOpTP))
-                                        : form_of(gemm_mode(mode, mask, kSquare, stage + 1, -1)))
-         : op == kOpApplyX ? (stage == 5 ? kFormF32 : form_of(gemm_mode(mode, mask, kGram, stage + 1, -1)))
+                                          : form_of(gemm_mode(mode, mask, kApply, stage, gs ? kOpApplyQ : kOpApplyX, gs)))
+         : phase == kPoly1 ? form_of(gemm_mode(mode, mask, kApply, 1, kOpApplyX, gs))
+         : phase == kSym ? (op == kOpPG ? form_of(gemm_mode(mode, mask, kSym, stage, kOpTP, gs))
+                                        : form_of(gemm_mode(mode, mask, kSquare, stage + 1, -1, gs)))
+         : op == kOpApplyX ? (stage == 5 ? kFormF32 : form_of(gemm_mode(mode, mask, kGram, stage + 1, -1, gs)))
          : op == kOpApplyQ ? form_of(gemm_mode(mode, mask, kApply, stage == 2 ? 2 : 5,
-                                               stage == 2 ? kOpApplyMid : stage == 4 ? kOpApplyQ : kOpApplyFinal))
-         : op == kOpApplyMid ? form_of(gemm_mode(mode, mask, kGram, 3, -1))
+                                               stage == 2 ? kOpApplyMid : stage == 4 ? kOpApplyQ : kOpApplyFinal, gs))
+         : op == kOpApplyMid ? form_of(gemm_mode(mode, mask, kGram, 3, -1, gs))
                              : kFormF32;
 }
 // Tile geometry policy (smx_s8_tile_geometry): 0 automatic (pick_geo),
@@ -1455,11 +1459,6 @@ static int timing_end(int slot, hipStream_t st, int phase, double flops) {
   return SMX_OK;
 }
 
-// The MFMA mode of one product of a launch (gemm_mode under the run's mode
-// and the process-wide compensation mask).
-static int seg_mode(const S8Layout &Lay, int phase, int stage, int op) {
-  return gemm_mode(Lay.mode, g_comp_mask, phase, stage, op);
-}
 
 // The segments of one launch, in class order by per-tile cost (K length,
 // most expensive first, so long-K tiles start first and short tiles fill
@@ -1472,6 +1471,13 @@ struct Seg {
   int op;
   int lo, hi;  // slots
 };
+
+// The MFMA mode of one product of a launch (gemm_mode under the run's mode
+// and the process-wide compensation mask).
+static int seg_mode(const S8Layout &Lay, int phase, int stage, const Seg &sg) {
+  return gemm_mode(Lay.mode, g_comp_mask, phase, stage, sg.op, Lay.cls[sg.cls].gs != 0);
+}
+
 // The matrices of one launch chain: slots lo[c] .. hi[c] - 1 of class c.
 struct SlotSet {
   int32_t lo[kMaxClasses] = {}, hi[kMaxClasses] = {};
@@ -1598,13 +1604,13 @@ static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, int 
   const std::vector<Seg> all = launch_segments(Lay, set, PHASE, stage, ops);
   std::vector<int> modes;
   for (const Seg &sg : all) {
-    const int m = seg_mode(Lay, PHASE, stage, sg.op);
+    const int m = seg_mode(Lay, PHASE, stage, sg);
     if (std::find(modes.begin(), modes.end(), m) == modes.end()) modes.push_back(m);
   }
   for (const int mode : modes) {
     std::vector<Seg> segs;
     for (const Seg &sg : all)
-      if (seg_mode(Lay, PHASE, stage, sg.op) == mode) segs.push_back(sg);
+      if (seg_mode(Lay, PHASE, stage, sg) == mode) segs.push_back(sg);
     StageArgs a{};
     a.L = Lay;
     a.stage = stage;

@@ -14,8 +14,8 @@ Added keywords (defaults keep the production recipe and the reference's
 results):
 * ``s8_mode`` selects the arithmetic of the S8 products: "comp_bf16"
   (compensated BF16 MFMA in all five stages), "mixed" (compensated BF16
-  stage 1, FP16 MFMA stages 2-5: about 2e-3 from the FP32 map at a third
-  less S8 time) or "fp32" (FP32 MFMA);
+  stages 1-2, FP16 MFMA stages 3-5: about 1e-3 from the FP32 map at a
+  quarter less S8 time) or "fp32" (FP32 MFMA);
 * ``hook_batch_bytes``: the hooks queue their inputs and take the
   statistics of the queue in one launch once it holds this many bytes (and
   at step(), state_dict() and close()); 0 launches in every hook call.  The

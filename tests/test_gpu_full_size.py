@@ -25,8 +25,8 @@
   each against the FP64 map.
 * The compensated recipe: the worst error of the compensated-BF16 S8 under
   each compensation mask (which stages are compensated, the rest plain
-  BF16; smx_s8_comp_mask) and of the mixed mode (compensated stage 1, FP16
-  stages 2-5), on the cfg2 batch, the cfg5 shapes and the cfg4 step.
+  BF16; smx_s8_comp_mask) and of the mixed mode (compensated stages 1-2,
+  FP16 stages 3-5), on the cfg2 batch, the cfg5 shapes and the cfg4 step.
 
 Gates (north star): statistics/EMA rel. error <= 1e-6; per-matrix direction
 rel. Frobenius error <= 1e-4 (fp32 mode), <= 1e-2 (comp_bf16 and mixed).
@@ -381,7 +381,7 @@ def test_cfg4_gpt_step_at_the_real_workload(device, mode):
 def test_compensated_stage_recipe_on_cfg2_and_cfg5_shapes(device):
     """Worst per-matrix error against the FP32 oracle of each compensation
     recipe of the compensated-BF16 S8 (plain stages: BF16 products hi*hi)
-    and of the mixed mode (compensated stage 1, FP16 stages 2-5): the whole
+    and of the mixed mode (compensated stages 1-2, FP16 stages 3-5): the whole
     cfg2 batch and the cfg5 shapes.  The production recipe (all five
     stages) and the mixed mode must stay within half the 1e-2 gate; the
     table is printed for the recipe decision."""
