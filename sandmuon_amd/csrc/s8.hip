@@ -1596,8 +1596,9 @@ static void launch_stage(int geo, int32_t blocks, const StageArgs &a, hipStream_
 
 // sq_geo: the geometry of the run's square launches (the stage-1 Schatten
 // partials are per square tile).  The segments of a phase whose products
-// run in different MFMA modes (SMX_S8_MIXED at stage 2: X' = P X in FP16,
-// Q2 = P2 Q1 compensated) go to one launch per mode.
+// run in different MFMA modes (SMX_S8_MIXED at stages 3-5: an X-space
+// class in FP16, a Gram-space class compensated) go to one launch per
+// mode.
 template <int PHASE>
 static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, int sq_geo, hipStream_t st, double &flops,
                         const std::vector<int> &ops = {}) {
