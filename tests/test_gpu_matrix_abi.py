@@ -135,17 +135,18 @@ def test_odd_shapes_through_the_optimizer(device, tile_policy, mode):
 
 class WideBranches(nn.Module):
     """Linears whose parameter rows take each path of the whiten kernel:
-    in-widths 2048 and 4096 keep 2 and 4 column chunks of S in registers,
-    4100 is wider than 4096 and re-reads g and m'; 64 -> 700 is a transposed
-    parameter with one kept chunk, 1100 -> 1300 a transposed one whose 1100
-    columns re-read.  The batches hold more samples (4096) than the widest
+    in-widths 1000 and 2048 are taken by 2 and 4 waves per row with 2
+    float4 per lane kept in registers (blocks of 4 row groups, 44 and 48
+    rows: padding rows in the last block), 4096 and 4100 are wider and
+    re-read g and m'; 64 -> 700 is a transposed parameter with one kept
+    chunk, 1100 -> 1300 a transposed one whose 1100 columns re-read.  The batches hold more samples (4096) than the widest
     parameter has rows or columns: with fewer, the gradients of the 1100 x
     1300 parameter are rank-deficient, and the polar map of a rank-deficient
     matrix amplifies the rounding in its null space (two FP32 evaluations of
     such a matrix already differ by about 1.2e-4), which no FP32 gate can
     hold to 1e-4."""
 
-    WIDTHS = [(2048, 48), (4096, 40), (4100, 36), (64, 700), (1100, 1300)]
+    WIDTHS = [(1000, 44), (2048, 48), (4096, 40), (4100, 36), (64, 700), (1100, 1300)]
 
     def __init__(self):
         super().__init__()
@@ -166,7 +167,7 @@ def test_wide_rows_through_the_optimizer(device, tile_policy, mode):
                for _ in range(2)]
     loss = lambda m, x, y: (m(x) - y).square().mean() / 2
     hist, opt, ora = run_pair(device, model, batches, loss, RankOneAWeightedPE, mode, 1e-2, steps=2)
-    assert len(opt.named_matrices) == 5
+    assert len(opt.named_matrices) == 6
     worst = check_directions(hist, opt, 1e-2, mode)
     print(f"wide rows {mode} tiles {tile_policy}: worst direction rel err {worst:.3e}")
     check_aux(hist, opt, ora)
