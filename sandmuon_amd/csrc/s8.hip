@@ -148,9 +148,9 @@ __host__ __device__ constexpr int gemm_mode(int mode, int mask, int phase, int s
 // compiles (each kernel keeps only these epilogues): a Gram feeds its
 // stage's square (same mode); a square writes FP32 G2 at stage 1, else P
 // for its stage's products; the SYM products feed products of their own
-// mode; an apply feeds the next stage (in SMX_S8_MIXED the stage-2 apply,
-// compensated, writes the FP16 X2 or X-space iterate of stage 3), Q2 / X2,
-// or the FP32 result.
+// mode; an apply feeds the next stage (in SMX_S8_MIXED the compensated
+// stage-2 apply of an X-space class writes the FP16 iterate of stage 3),
+// Q2 / X2, or the FP32 result.
 __host__ __device__ constexpr bool form_compiled(int gm, int phase, int form) {
   return gm == SMX_S8_FP32 ? form == kFormF32
          : gm == kS8F16 ? (form == kFormF16 || (form == kFormF32 && phase == kApply))
