@@ -464,9 +464,9 @@ def _header(args, lines):
 
 
 def _steps_of(trace):
-    """Start indices of step(): the first finish_fold launch after any other kernel."""
-    return [i for i, r in enumerate(trace) if "finish_fold_kernel" in r["name"] and
-            (i == 0 or "finish_fold_kernel" not in trace[i - 1]["name"] and "finish_kernel" not in trace[i - 1]["name"])]
+    """Start indices of step(): the first finish-fold launch after any other kernel."""
+    fin = lambda n: "finish_fold" in n or "finish_kernel" in n or "finish_table_kernel" in n
+    return [i for i, r in enumerate(trace) if "finish_fold" in r["name"] and (i == 0 or not fin(trace[i - 1]["name"]))]
 
 
 def summarize_trace(args):

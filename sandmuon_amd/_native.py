@@ -17,7 +17,7 @@ from typing import Optional, Sequence
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsandmuon_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 SMX_F32, SMX_BF16, SMX_F16, SMX_F64 = 0, 1, 2, 3
 S8_FP32, S8_COMP_BF16, S8_MIXED = 0, 1, 2
@@ -82,8 +82,14 @@ SIGNATURES = {
                                  c_void_p, c_int64, c_void_p]),
     "smx_stats_fold": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
     "smx_stats_finish": (c_int, [ctypes.POINTER(FinishDesc), c_int32, c_double, c_void_p]),
+    "smx_stats_finish_table_bytes": (c_size_t, [c_int32]),
+    "smx_stats_finish_staged": (c_int, [ctypes.POINTER(FinishDesc), c_int32, c_double, c_void_p, c_void_p,
+                                        c_size_t, c_void_p]),
     "smx_adamw": (c_int, [ctypes.POINTER(AdamwDesc), c_int32, c_int64, c_double, c_double, c_double, c_double,
                           c_double, c_void_p]),
+    "smx_adamw_table_bytes": (c_size_t, [c_int32, c_int64]),
+    "smx_adamw_staged": (c_int, [ctypes.POINTER(AdamwDesc), c_int32, c_int64, c_double, c_double, c_double,
+                                 c_double, c_double, c_void_p, c_void_p, c_size_t, c_void_p]),
     "smx_matrix_step_workspace_bytes": (c_size_t, [ctypes.POINTER(c_int64), ctypes.POINTER(c_int64),
                                                    c_int32, c_int]),
     "smx_matrix_step": (c_int, [ctypes.POINTER(MatrixDesc), c_int32, c_int, c_void_p, c_size_t, c_void_p]),
@@ -307,20 +313,75 @@ def stats_fold(sum_sq, slots_sq, sum_first, slots_first) -> None:
     _check(rc, "smx_stats_fold")
 
 
-def stats_finish(descs: Sequence[FinishDesc], beta: float, device: torch.device) -> None:
+# Descriptors per launch of the by-value entry points (kernel arguments);
+# longer tables go through the staged ones.
+FINISH_BATCH = 32
+ADAMW_BATCH = 56
+
+
+class DescriptorStage:
+    """Device tables for the staged entry points (smx_stats_finish_staged,
+    smx_adamw_staged) and the pinned host memory they are copied from: a
+    ring of two, each with an event recorded on the stream after its call.
+    A slot is reused only once its event has completed, so the host never
+    rewrites pinned memory whose copy is still queued, and the device table
+    of a call stays untouched until that call's kernels have run."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.slots = [[None, None, None] for _ in range(2)]  # device table, pinned stage, event
+        self.next = 0
+
+    def take(self, nbytes: int):
+        slot = self.slots[self.next]
+        self.next = (self.next + 1) % len(self.slots)
+        if slot[2] is not None:
+            slot[2].synchronize()
+        if slot[0] is None or slot[0].numel() < nbytes:
+            size = max(nbytes, 4096)
+            slot[0] = torch.empty(size, dtype=torch.uint8, device=self.device)
+            slot[1] = torch.empty(size, dtype=torch.uint8, pin_memory=True)
+        return slot
+
+    def done(self, slot) -> None:
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        slot[2] = ev
+
+
+def stats_finish(descs: Sequence[FinishDesc], beta: float, device: torch.device,
+                 stage: Optional[DescriptorStage] = None) -> None:
+    """Finish of every vector: one fold and one finish launch per FINISH_BATCH
+    descriptors, or one of each for the whole table through `stage`."""
     if not descs:
         return
     arr = (FinishDesc * len(descs))(*descs)
-    _check(lib().smx_stats_finish(arr, len(descs), beta, stream_of(device)), "smx_stats_finish")
+    if stage is None or len(descs) <= FINISH_BATCH:
+        _check(lib().smx_stats_finish(arr, len(descs), beta, stream_of(device)), "smx_stats_finish")
+        return
+    nbytes = int(lib().smx_stats_finish_table_bytes(len(descs)))
+    slot = stage.take(nbytes)
+    _check(lib().smx_stats_finish_staged(arr, len(descs), beta, slot[0].data_ptr(), slot[1].data_ptr(),
+                                         slot[0].numel(), stream_of(device)), "smx_stats_finish_staged")
+    stage.done(slot)
 
 
 def adamw(descs: Sequence[AdamwDesc], total: int, lr: float, beta1: float, beta2: float, eps: float,
-          weight_decay: float, device: torch.device) -> None:
+          weight_decay: float, device: torch.device, stage: Optional[DescriptorStage] = None) -> None:
+    """AdamW over every tensor: one launch per ADAMW_BATCH descriptors, or one
+    for the whole table through `stage`."""
     if not descs:
         return
     arr = (AdamwDesc * len(descs))(*descs)
-    _check(lib().smx_adamw(arr, len(descs), total, lr, beta1, beta2, eps, weight_decay, stream_of(device)),
-           "smx_adamw")
+    if stage is None or len(descs) <= ADAMW_BATCH:
+        _check(lib().smx_adamw(arr, len(descs), total, lr, beta1, beta2, eps, weight_decay, stream_of(device)),
+               "smx_adamw")
+        return
+    nbytes = int(lib().smx_adamw_table_bytes(len(descs), total))
+    slot = stage.take(nbytes)
+    _check(lib().smx_adamw_staged(arr, len(descs), total, lr, beta1, beta2, eps, weight_decay, slot[0].data_ptr(),
+                                  slot[1].data_ptr(), slot[0].numel(), stream_of(device)), "smx_adamw_staged")
+    stage.done(slot)
 
 
 def matrix_step_workspace_bytes(shapes: Sequence[tuple], mode: int) -> int:

@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <climits>
 #include <cmath>
+#include <cstring>
 
 namespace smx {
 
@@ -19,43 +20,54 @@ constexpr int kAdamMaxChunk = 2048;  // elements per block (large launches)
 constexpr int kAdamUnroll = 4;
 constexpr int kAdamVec = 2;  // float4 per thread per pass (FP32 tensors)
 
-struct AdamPack {
-  int32_t first_blk[kAdamBatch];  // ceil(offset / chunk); INT32_MAX past the last
-  smx_adamw_desc d[kAdamBatch];
+// The scalars of one launch: its element count and block chunk, and the
+// FP32 coefficients.
+struct AdamScalars {
   int32_t n;
   int64_t total;
   int64_t chunk;
   float neg_lr, decay, b1, omb1, b2, omb2, eps;
 };
+struct AdamPack {
+  int32_t first_blk[kAdamBatch];  // ceil(offset / chunk); INT32_MAX past the last
+  smx_adamw_desc d[kAdamBatch];
+  AdamScalars sc;
+};
 static_assert(sizeof(AdamPack) <= 4000, "AdamPack is passed by value in the kernel arguments");
+
+// Elements per block: short chunks for small launches (the biases and norms
+// left after the embeddings), so they spread over more CUs instead of
+// queueing behind each other in a few blocks.
+static int64_t adam_chunk(int64_t total) {
+  return std::min<int64_t>(kAdamMaxChunk, std::max<int64_t>(256, ceil_div(ceil_div(total, 2048), 256) * 256));
+}
 
 __device__ __forceinline__ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // The moments and the step of one element, with explicit fused
 // multiply-adds so that every code path rounds the same way.
-__device__ __forceinline__ float adam_step(const AdamPack &pk, const smx_adamw_desc &d, float g, float &m, float &v) {
+__device__ __forceinline__ float adam_step(const AdamScalars &pk, const smx_adamw_desc &d, float g, float &m, float &v) {
   m = fmaf(m, pk.b1, g * pk.omb1);
   v = fmaf(v, pk.b2, (g * g) * pk.omb2);
   return (m / d.bias1) / (sqrtf(v / d.bias2) + pk.eps);
 }
 
 // One element of the FP32 update.
-__device__ __forceinline__ void adam_f32(const AdamPack &pk, const smx_adamw_desc &d, float g, float &m, float &v,
+__device__ __forceinline__ void adam_f32(const AdamScalars &pk, const smx_adamw_desc &d, float g, float &m, float &v,
                                          float &p) {
   const float step = adam_step(pk, d, g, m, v);
   p = fmaf(pk.neg_lr, step, p * pk.decay);
 }
 
-__global__ void __launch_bounds__(256) adamw_kernel(AdamPack pk) {
+// The block's elements [e0, e1) of the flattened tensors, from tensor k (the
+// last whose offset is <= e0) on; desc(k) gives tensor k's descriptor.
+template <class Desc>
+__device__ __forceinline__ void adamw_block(const AdamScalars &pk, Desc desc, int k) {
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * pk.chunk;
   const int64_t e1 = min(pk.total, e0 + pk.chunk);
-  // Tensor holding e0, the last with offset <= e0 (offsets are ascending):
-  // independent compares, no chain of dependent descriptor loads.
-  int k = 0;
-#pragma unroll
-  for (int t = 1; t < kAdamBatch; ++t) k += static_cast<int>(blockIdx.x) >= pk.first_blk[t] ? 1 : 0;
-  for (; k < pk.n && pk.d[k].offset < e1; ++k) {
-    const smx_adamw_desc &d = pk.d[k];
+  for (; k < pk.n; ++k) {
+    const smx_adamw_desc d = desc(k);
+    if (d.offset >= e1) break;
     int64_t lo = max(e0, d.offset) - d.offset;
     const int64_t hi = min(e1, d.offset + d.n) - d.offset;
     // FP32 tensors whose block range starts on a 16-byte boundary: float4
@@ -137,12 +149,30 @@ __global__ void __launch_bounds__(256) adamw_kernel(AdamPack pk) {
   }
 }
 
+__global__ void __launch_bounds__(256) adamw_kernel(AdamPack pk) {
+  // Tensor holding the block's first element, the last with offset <= e0
+  // (offsets are ascending): independent compares, no chain of dependent
+  // descriptor loads.
+  int k = 0;
+#pragma unroll
+  for (int t = 1; t < kAdamBatch; ++t) k += static_cast<int>(blockIdx.x) >= pk.first_blk[t] ? 1 : 0;
+  adamw_block(pk.sc, [&](int i) { return pk.d[i]; }, k);
+}
+
+// The same over a table in device memory: descriptors, then the first
+// tensor of every block (one load per block).
+__global__ void __launch_bounds__(256) adamw_table_kernel(AdamScalars sc, const smx_adamw_desc *__restrict__ table,
+                                                          const int32_t *__restrict__ block_first) {
+  // (the index is block-uniform: the descriptor loads are scalar loads)
+  adamw_block(sc, [&](int i) { return table[__builtin_amdgcn_readfirstlane(i)]; },
+              __builtin_amdgcn_readfirstlane(block_first[blockIdx.x]));
+}
+
 }  // namespace smx
 
 using namespace smx;
 
-extern "C" int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t total, double lr, double beta1,
-                         double beta2, double eps, double weight_decay, void *stream) {
+static int check_adamw_descs(const smx_adamw_desc *descs, int32_t n_desc, int64_t total) {
   SMX_REQUIRE(n_desc >= 0 && (n_desc == 0 || descs), SMX_EINVAL, "adamw: bad descriptor table");
   int64_t sum = 0;
   for (int32_t i = 0; i < n_desc; ++i) {
@@ -157,37 +187,88 @@ extern "C" int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t to
     sum += d.n;
   }
   SMX_REQUIRE(sum == total, SMX_ESHAPE, "adamw: total != sum of n");
+  return SMX_OK;
+}
+
+// Each FP32 coefficient is rounded from the double the reference computes
+// in Python (1 - lr*wd, 1 - beta, -lr).
+static AdamScalars adam_scalars(int32_t n, int64_t total, double lr, double beta1, double beta2, double eps,
+                                double weight_decay) {
+  AdamScalars sc{};
+  sc.n = n;
+  sc.total = total;
+  sc.chunk = adam_chunk(total);
+  sc.neg_lr = static_cast<float>(-lr);
+  sc.decay = static_cast<float>(1.0 - lr * weight_decay);
+  sc.b1 = static_cast<float>(beta1);
+  sc.omb1 = static_cast<float>(1.0 - beta1);
+  sc.b2 = static_cast<float>(beta2);
+  sc.omb2 = static_cast<float>(1.0 - beta2);
+  sc.eps = static_cast<float>(eps);
+  return sc;
+}
+
+extern "C" int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t total, double lr, double beta1,
+                         double beta2, double eps, double weight_decay, void *stream) {
+  if (const int rc = check_adamw_descs(descs, n_desc, total)) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   for (int32_t b = 0; b < n_desc; b += kAdamBatch) {
     AdamPack pk{};
-    pk.n = std::min<int32_t>(kAdamBatch, n_desc - b);
+    const int32_t n = std::min<int32_t>(kAdamBatch, n_desc - b);
     const int64_t base = descs[b].offset;
-    for (int i = 0; i < pk.n; ++i) {
+    for (int i = 0; i < n; ++i) {
       pk.d[i] = descs[b + i];
       pk.d[i].offset -= base;
     }
-    pk.total = pk.d[pk.n - 1].offset + pk.d[pk.n - 1].n;
-    // Each FP32 coefficient is rounded from the double the reference
-    // computes in Python (1 - lr*wd, 1 - beta, -lr).
-    pk.neg_lr = static_cast<float>(-lr);
-    pk.decay = static_cast<float>(1.0 - lr * weight_decay);
-    pk.b1 = static_cast<float>(beta1);
-    pk.omb1 = static_cast<float>(1.0 - beta1);
-    pk.b2 = static_cast<float>(beta2);
-    pk.omb2 = static_cast<float>(1.0 - beta2);
-    pk.eps = static_cast<float>(eps);
-    if (pk.total == 0) continue;
-    // Small launches (the biases and norms left after the embeddings) use
-    // short chunks, so they spread over more CUs instead of queueing behind
-    // each other in a few blocks.
-    pk.chunk = std::min<int64_t>(kAdamMaxChunk, std::max<int64_t>(256, ceil_div(ceil_div(pk.total, 2048), 256) * 256));
-    const int64_t blocks = ceil_div(pk.total, pk.chunk);
+    pk.sc = adam_scalars(n, pk.d[n - 1].offset + pk.d[n - 1].n, lr, beta1, beta2, eps, weight_decay);
+    if (pk.sc.total == 0) continue;
+    const int64_t blocks = ceil_div(pk.sc.total, pk.sc.chunk);
     SMX_REQUIRE(blocks < INT32_MAX, SMX_ESHAPE, "adamw: too many elements for one launch");
     for (int i = 0; i < kAdamBatch; ++i)
-      pk.first_blk[i] = i < pk.n ? static_cast<int32_t>(ceil_div(pk.d[i].offset, pk.chunk)) : INT32_MAX;
+      pk.first_blk[i] = i < n ? static_cast<int32_t>(ceil_div(pk.d[i].offset, pk.sc.chunk)) : INT32_MAX;
     hipLaunchKernelGGL(adamw_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, pk);
     const int rc = check_launch("adamw");
     if (rc) return rc;
   }
   return SMX_OK;
+}
+
+// Table of smx_adamw_staged: the descriptors, then each block's first
+// tensor (int32).
+static size_t adamw_table_bytes(int32_t n_desc, int64_t total) {
+  if (n_desc <= 0 || total <= 0) return 0;
+  return static_cast<size_t>(n_desc) * sizeof(smx_adamw_desc) +
+         static_cast<size_t>(ceil_div(total, adam_chunk(total))) * sizeof(int32_t);
+}
+
+extern "C" size_t smx_adamw_table_bytes(int32_t n_desc, int64_t total) { return adamw_table_bytes(n_desc, total); }
+
+extern "C" int smx_adamw_staged(const smx_adamw_desc *descs, int32_t n_desc, int64_t total, double lr, double beta1,
+                                double beta2, double eps, double weight_decay, void *dev_table, void *host_stage,
+                                size_t table_bytes, void *stream) {
+  if (const int rc = check_adamw_descs(descs, n_desc, total)) return rc;
+  if (n_desc == 0 || total == 0) return SMX_OK;
+  const size_t need = adamw_table_bytes(n_desc, total);
+  SMX_REQUIRE(dev_table && host_stage && table_bytes >= need, SMX_EWORKSPACE,
+              "adamw_staged: dev_table and host_stage need smx_adamw_table_bytes(n_desc, total) bytes");
+  const AdamScalars sc = adam_scalars(n_desc, total, lr, beta1, beta2, eps, weight_decay);
+  const int64_t blocks = ceil_div(total, sc.chunk);
+  SMX_REQUIRE(blocks < INT32_MAX, SMX_ESHAPE, "adamw: too many elements for one launch");
+  auto *d = static_cast<smx_adamw_desc *>(host_stage);
+  std::memcpy(d, descs, static_cast<size_t>(n_desc) * sizeof(smx_adamw_desc));
+  // Block b starts at element b * chunk: its first tensor is the last one
+  // whose offset is <= that (the same tensor adamw_kernel's compares find).
+  auto *first = reinterpret_cast<int32_t *>(d + n_desc);
+  int32_t k = 0;
+  for (int64_t b = 0; b < blocks; ++b) {
+    while (k + 1 < n_desc && descs[k + 1].offset <= b * sc.chunk) ++k;
+    first[b] = k;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  SMX_REQUIRE(hipMemcpyAsync(dev_table, host_stage, need, hipMemcpyHostToDevice, st) == hipSuccess, SMX_ELAUNCH,
+              "adamw_staged: copy of the descriptor table failed");
+  const auto *table = static_cast<const smx_adamw_desc *>(dev_table);
+  hipLaunchKernelGGL(adamw_table_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, sc, table,
+                     reinterpret_cast<const int32_t *>(table + n_desc));
+  return check_launch("adamw_staged");
 }

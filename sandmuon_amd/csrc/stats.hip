@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <cfloat>
 #include <climits>
+#include <cstring>
 #include <type_traits>
 #include <vector>
 
@@ -599,9 +600,8 @@ static_assert(sizeof(FinishPack) <= 4000, "FinishPack is passed by value in the 
 // are combined in a fixed order (FP64).
 constexpr int kFoldWaves = 8;
 
-__global__ void __launch_bounds__(64 * kFoldWaves) finish_fold_kernel(FinishPack pack) {
+__device__ __forceinline__ void finish_fold(const smx_finish_desc &d) {
   __shared__ double part[2][kFoldWaves][64];
-  const smx_finish_desc &d = pack.d[blockIdx.y];
   if (static_cast<int64_t>(blockIdx.x) * 64 >= d.n) return;  // uniform per block
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
@@ -632,6 +632,17 @@ __global__ void __launch_bounds__(64 * kFoldWaves) finish_fold_kernel(FinishPack
   }
 }
 
+__global__ void __launch_bounds__(64 * kFoldWaves) finish_fold_kernel(FinishPack pack) {
+  finish_fold(pack.d[blockIdx.y]);
+}
+
+// The same over a descriptor table in device memory (any number of
+// descriptors in one launch), the block's descriptor copied to registers.
+__global__ void __launch_bounds__(64 * kFoldWaves) finish_fold_table_kernel(const smx_finish_desc *table) {
+  const smx_finish_desc d = table[blockIdx.y];
+  finish_fold(d);
+}
+
 __device__ __forceinline__ float ema_update(float e, float x, float beta, float omb) {
   // e.mul_(beta).add_(x, alpha=1-beta), both coefficients rounded from double
   return e * beta + x * omb;
@@ -640,9 +651,8 @@ __device__ __forceinline__ float ema_update(float e, float x, float beta, float 
 // One block of kFinishThreads per descriptor.
 constexpr int kFinishThreads = 1024;
 
-__global__ void __launch_bounds__(kFinishThreads) finish_kernel(FinishPack pack, float beta, float omb) {
+__device__ __forceinline__ void finish_one(const smx_finish_desc &d, float beta, float omb) {
   __shared__ double scratch[16];
-  const smx_finish_desc &d = pack.d[blockIdx.x];
   const int64_t n = d.n;
   const float cnt = static_cast<float>(d.count);
   const int t = threadIdx.x;
@@ -711,6 +721,16 @@ __global__ void __launch_bounds__(kFinishThreads) finish_kernel(FinishPack pack,
     const float rho = sqrtf(1.0f + static_cast<float>(zz));
     d.kappa[0] = -1.0f / (rho * (rho + 1.0f));
   }
+}
+
+__global__ void __launch_bounds__(kFinishThreads) finish_kernel(FinishPack pack, float beta, float omb) {
+  finish_one(pack.d[blockIdx.x], beta, omb);
+}
+
+__global__ void __launch_bounds__(kFinishThreads) finish_table_kernel(const smx_finish_desc *table, float beta,
+                                                                      float omb) {
+  const smx_finish_desc d = table[blockIdx.x];
+  finish_one(d, beta, omb);
 }
 
 }  // namespace smx
@@ -920,8 +940,7 @@ extern "C" int smx_stats_fold(float *sum_sq, float *slots_sq, float *sum_first, 
   return check_launch("stats_fold");
 }
 
-extern "C" int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc, double beta,
-                                void *stream) {
+static int check_finish_descs(const smx_finish_desc *descs, int32_t n_desc) {
   SMX_REQUIRE(n_desc >= 0, SMX_EINVAL, "stats_finish: n_desc < 0");
   SMX_REQUIRE(n_desc == 0 || descs, SMX_EINVAL, "stats_finish: null descriptor table");
   for (int32_t i = 0; i < n_desc; ++i) {
@@ -935,6 +954,12 @@ extern "C" int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc, do
       SMX_REQUIRE(d.sum_first && d.slots_first && d.mean_ema && d.z && d.kappa, SMX_EINVAL,
                   "stats_finish: rank-one descriptor needs sum_first, slots_first, mean_ema, z, kappa");
   }
+  return SMX_OK;
+}
+
+extern "C" int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc, double beta,
+                                void *stream) {
+  if (const int rc = check_finish_descs(descs, n_desc)) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   for (int32_t b = 0; b < n_desc; b += kFinishBatch) {
     FinishPack pack{};
@@ -954,4 +979,33 @@ extern "C" int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc, do
     if (rc) return rc;
   }
   return SMX_OK;
+}
+
+extern "C" size_t smx_stats_finish_table_bytes(int32_t n_desc) {
+  return n_desc > 0 ? static_cast<size_t>(n_desc) * sizeof(smx_finish_desc) : 0;
+}
+
+extern "C" int smx_stats_finish_staged(const smx_finish_desc *descs, int32_t n_desc, double beta, void *dev_table,
+                                       void *host_stage, size_t table_bytes, void *stream) {
+  if (const int rc = check_finish_descs(descs, n_desc)) return rc;
+  if (n_desc == 0) return SMX_OK;
+  SMX_REQUIRE(n_desc <= 65535, SMX_EINVAL, "stats_finish_staged: at most 65535 descriptors");
+  const size_t need = smx_stats_finish_table_bytes(n_desc);
+  SMX_REQUIRE(dev_table && host_stage && table_bytes >= need, SMX_EWORKSPACE,
+              "stats_finish_staged: dev_table and host_stage need smx_stats_finish_table_bytes(n_desc) bytes");
+  int64_t nmax = 1;
+  for (int32_t i = 0; i < n_desc; ++i) nmax = std::max<int64_t>(nmax, descs[i].n);
+  SMX_REQUIRE(ceil_div(nmax, 64) <= INT32_MAX, SMX_ESHAPE, "stats_finish_staged: vector too long");
+  std::memcpy(host_stage, descs, need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  SMX_REQUIRE(hipMemcpyAsync(dev_table, host_stage, need, hipMemcpyHostToDevice, st) == hipSuccess, SMX_ELAUNCH,
+              "stats_finish_staged: copy of the descriptor table failed");
+  const auto *table = static_cast<const smx_finish_desc *>(dev_table);
+  hipLaunchKernelGGL(finish_fold_table_kernel, dim3(static_cast<unsigned>(ceil_div(nmax, 64)), n_desc),
+                     dim3(64 * kFoldWaves), 0, st, table);
+  int rc = check_launch("stats_finish_staged(fold)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(finish_table_kernel, dim3(n_desc), dim3(kFinishThreads), 0, st, table, static_cast<float>(beta),
+                     static_cast<float>(1.0 - beta));
+  return check_launch("stats_finish_staged");
 }

@@ -364,6 +364,9 @@ class DiagonalWeightedPE(Optimizer):
         # slot buffer (data pointer): the fold and finish read only those.
         self._slot_rows: Dict[int, int] = {}
         self._workspace: Optional[torch.Tensor] = None
+        # Device tables for the finish and AdamW launches of a step with more
+        # descriptors than one by-value launch takes (created on first use).
+        self._stage: Optional[_native.DescriptorStage] = None
         self.register_state_dict_pre_hook(DiagonalWeightedPE._flush_slots)
         self.register_load_state_dict_post_hook(DiagonalWeightedPE._drop_slots)
         self.handles = []
@@ -593,6 +596,11 @@ class DiagonalWeightedPE(Optimizer):
             d.z, d.kappa = out["z"].data_ptr(), out["kappa"].data_ptr()
         return d
 
+    def _descriptor_stage(self, device) -> "_native.DescriptorStage":
+        if self._stage is None or self._stage.device != device:
+            self._stage = _native.DescriptorStage(device)
+        return self._stage
+
     def _run_closure(self, closure):
         """sandmuon/optimizer.py:226-230: the closure runs with gradients enabled."""
         if closure is None:
@@ -664,7 +672,7 @@ class DiagonalWeightedPE(Optimizer):
             out = {"inv": next(views)}
             b_out[id(parameter)] = out
             descs.append(self._finish_desc(parameter, "b", a_counts[id(source)], out))
-        _native.stats_finish(descs, self.statistic_beta, device)
+        _native.stats_finish(descs, self.statistic_beta, device, self._descriptor_stage(device))
         for s in sources:
             self.state[s]["a_count"] = 0
         for parameter, _, _ in items:
@@ -740,7 +748,8 @@ class DiagonalWeightedPE(Optimizer):
                     grad_dtype=_native.dtype_code(grad.dtype), param_dtype=_native.dtype_code(parameter.dtype)))
                 offset += n
             lr = group["lr"] * group["adamw_lr_ratio"]
-            _native.adamw(descs, offset, lr, b1, b2, group["adamw_eps"], group["weight_decay"], device)
+            _native.adamw(descs, offset, lr, b1, b2, group["adamw_eps"], group["weight_decay"], device,
+                          self._descriptor_stage(device))
             del keep
 
     def close(self):
