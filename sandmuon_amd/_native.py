@@ -325,7 +325,9 @@ class DescriptorStage:
     ring of two, each with an event recorded on the stream after its call.
     A slot is reused only once its event has completed, so the host never
     rewrites pinned memory whose copy is still queued, and the device table
-    of a call stays untouched until that call's kernels have run."""
+    of a call stays untouched until that call's kernels have run.  (Under
+    graph capture, where the host cannot wait on an event, the by-value
+    calls are used.)"""
 
     def __init__(self, device: torch.device):
         self.device = device
@@ -356,7 +358,7 @@ def stats_finish(descs: Sequence[FinishDesc], beta: float, device: torch.device,
     if not descs:
         return
     arr = (FinishDesc * len(descs))(*descs)
-    if stage is None or len(descs) <= FINISH_BATCH:
+    if stage is None or len(descs) <= FINISH_BATCH or torch.cuda.is_current_stream_capturing():
         _check(lib().smx_stats_finish(arr, len(descs), beta, stream_of(device)), "smx_stats_finish")
         return
     nbytes = int(lib().smx_stats_finish_table_bytes(len(descs)))
@@ -373,7 +375,7 @@ def adamw(descs: Sequence[AdamwDesc], total: int, lr: float, beta1: float, beta2
     if not descs:
         return
     arr = (AdamwDesc * len(descs))(*descs)
-    if stage is None or len(descs) <= ADAMW_BATCH:
+    if stage is None or len(descs) <= ADAMW_BATCH or torch.cuda.is_current_stream_capturing():
         _check(lib().smx_adamw(arr, len(descs), total, lr, beta1, beta2, eps, weight_decay, stream_of(device)),
                "smx_adamw")
         return
