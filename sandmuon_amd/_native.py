@@ -12,7 +12,7 @@ import functools
 import threading
 from ctypes import c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
 from pathlib import Path
-from typing import Optional, Sequence
+from typing import List, Optional, Sequence
 
 import torch
 
@@ -321,24 +321,33 @@ ADAMW_BATCH = 56
 
 class DescriptorStage:
     """Device tables for the staged entry points (smx_stats_finish_staged,
-    smx_adamw_staged) and the pinned host memory they are copied from: a
-    ring of two, each with an event recorded on the stream after its call.
-    A slot is reused only once its event has completed, so the host never
-    rewrites pinned memory whose copy is still queued, and the device table
-    of a call stays untouched until that call's kernels have run.  (Under
-    graph capture, where the host cannot wait on an event, the by-value
-    calls are used.)"""
+    smx_adamw_staged) and the pinned host memory they are copied from, each
+    slot with an event recorded on the stream after its call.  A slot is
+    reused only once its event has completed, so the host never rewrites
+    pinned memory whose copy is still queued, and the device table of a
+    call stays untouched until that call's kernels have run.  A call takes
+    the first free slot; while every slot is still in flight a new one is
+    added (up to MAX_SLOTS, then the host waits for the oldest), so several
+    staged calls of one step (the finish, an AdamW call per parameter group)
+    never wait on each other.  (Under graph capture, where the host cannot
+    wait on an event, the by-value calls are used.)"""
+
+    MAX_SLOTS = 8
 
     def __init__(self, device: torch.device):
         self.device = device
-        self.slots = [[None, None, None] for _ in range(2)]  # device table, pinned stage, event
-        self.next = 0
+        self.slots: List[list] = []  # [device table, pinned stage, event], oldest use first
 
     def take(self, nbytes: int):
-        slot = self.slots[self.next]
-        self.next = (self.next + 1) % len(self.slots)
-        if slot[2] is not None:
+        free = [i for i, sl in enumerate(self.slots) if sl[2] is None or sl[2].query()]
+        if free:
+            slot = self.slots.pop(free[0])
+        elif len(self.slots) < self.MAX_SLOTS:
+            slot = [None, None, None]
+        else:
+            slot = self.slots.pop(0)
             slot[2].synchronize()
+        self.slots.append(slot)  # most recent use last
         if slot[0] is None or slot[0].numel() < nbytes:
             size = max(nbytes, 4096)
             slot[0] = torch.empty(size, dtype=torch.uint8, device=self.device)

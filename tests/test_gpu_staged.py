@@ -87,3 +87,35 @@ def test_staged_adamw_equals_the_batched_calls(device, n_desc):
         for ta, tb in zip(a, b):
             for x, y in zip(ta, tb):
                 assert torch.equal(x, y), rep
+
+
+def test_staged_calls_in_flight_take_their_own_slots(device):
+    # Several staged calls enqueued back to back behind a busy stream (a
+    # finish and AdamW calls of two parameter groups per step, three steps),
+    # so that none has run when the next is staged: each in-flight call keeps
+    # its own pinned stage and device table, and every result equals the
+    # by-value calls'.
+    stage = _native.DescriptorStage(device)
+    cases = []
+    for rep in range(3):
+        fa, a = _finish_case(device, 40 + rep, 20 + rep)
+        fb, b = _finish_case(device, 40 + rep, 20 + rep)
+        wa, wta, tot = _adamw_case(device, 60 + rep, 30 + rep)
+        wb, wtb, _ = _adamw_case(device, 60 + rep, 30 + rep)
+        cases.append((fa, fb, a, b, wa, wb, wta, wtb, tot))
+    torch.cuda.synchronize()
+    torch.cuda._sleep(100_000_000)  # a bounded spin (tens of ms) ahead of the calls
+    for fa, fb, a, b, wa, wb, wta, wtb, tot in cases:
+        _native.stats_finish(fa, 0.97, device)
+        _native.adamw(wa, tot, 1e-3, 0.9, 0.95, 1e-8, 0.1, device)
+        _native.stats_finish(fb, 0.97, device, stage)
+        _native.adamw(wb, tot, 1e-3, 0.9, 0.95, 1e-8, 0.1, device, stage)
+    assert len(stage.slots) == 6  # every staged call still in flight took a slot of its own
+    torch.cuda.synchronize()
+    for fa, fb, a, b, wa, wb, wta, wtb, tot in cases:
+        for ta, tb in zip(a, b):
+            for key in ta:
+                assert torch.equal(ta[key], tb[key]), key
+        for ta, tb in zip(wta, wtb):
+            for x, y in zip(ta, tb):
+                assert torch.equal(x, y)
