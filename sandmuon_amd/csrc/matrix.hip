@@ -53,8 +53,8 @@ constexpr int kFlipChunk = 256 * kMaxSlices;  // transposed whiten: columns per 
 
 struct MatJob {
   smx_matrix_desc d;
-  float *x;          // whiten: the oriented iterate ([prow_pad][pcol_pad], or for a transposed
-                     // parameter [pcol_pad][prow_pad])
+  float *x;          // whiten: the oriented iterate, a tiled S8 operand ([prow_pad][pcol_pad], or
+                     // for a transposed parameter [pcol_pad][prow_pad])
   const float *q;    // mapback: the S8 result in parameter layout ([prow_pad][pcol_pad])
   float *u;          // [prow_pad] rank-one row coefficients
   double *fro;       // whiten per-block partials of ||V||^2
@@ -457,7 +457,7 @@ __device__ __forceinline__ void whiten_rows_pipelined(const DevJob &J, int blk, 
       if (lane == 0 && wr == 0) J.u[i] = static_cast<float>(u);
     }
     // V_ij = b_i y_j + kappa u_i z_j, zeros in padding rows and columns
-    SMX_GLOBAL float *xrow = J.x + i * J.pcol_pad;
+    // (the S8 operand: tiled, row i's K group 4 q / 16 in its piece)
 #pragma unroll
     for (int t = 0; t < kMaxSlices; ++t) {
       const int q = q0 + span * t;
@@ -470,7 +470,7 @@ __device__ __forceinline__ void whiten_rows_pipelined(const DevJob &J, int blk, 
         }
         // pc4 is a multiple of 4 and q0 + span t steps by lanes, so both
         // lanes of a pair are inside the row or both outside
-        put_operand4_paired(xrow, 4 * static_cast<int64_t>(q), w, planes, true);
+        put_operand4_paired(J.x, tiled_index(i, 4 * static_cast<int64_t>(q), J.pcol_pad), w, planes, true);
       }
     }
   }
@@ -498,7 +498,6 @@ __device__ __forceinline__ void whiten_rows_single(const DevJob &J, int blk, dou
   const float kappa = R1 ? d.kappa[0] : 0.f;
   const bool planes = J.planes != 0;
   SMX_GLOBAL float *mrow = live ? d.momentum + p.i * d.cols : nullptr;
-  SMX_GLOBAL float *xrow = J.x + p.i * J.pcol_pad;
   const int pc4 = static_cast<int>(J.pcol_pad / 4);
 
   // ---- pass 1: m' (stored), y = S a of the lane's columns, and the row's
@@ -606,7 +605,7 @@ __device__ __forceinline__ void whiten_rows_single(const DevJob &J, int blk, dou
 #pragma unroll
           for (int e = 0; e < 4; ++e) w[e] = fmaf(ku, zs[e], b * (fmaf(ms[e], beta, gs[e] * omb) * as[e]));
         }
-        put_operand4((float *)xrow, 4 * q, w, planes);
+        put_operand4((float *)J.x, tiled_index(p.i, 4 * q, J.pcol_pad), w, planes);
       }
     }
   } else {
@@ -618,7 +617,7 @@ __device__ __forceinline__ void whiten_rows_single(const DevJob &J, int blk, dou
         x = b * y;
         if constexpr (R1) x = fmaf(ku, d.z[j], x);
       }
-      put_operand((float *)xrow, j, x, planes);
+      put_operand((float *)J.x, tiled_index(p.i, j, J.pcol_pad), x, planes);
     }
   }
   block_part(J, vy, vu, p, blk, static_cast<int>(whiten_blocks(J)), J.fro, rp);
@@ -641,8 +640,8 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
 // row in chunks of kFlipChunk columns (kMaxSlices float4 per lane); pass 1
 // keeps y = S a when the row is one chunk (KEPT, a launch of its own), else
 // pass 2 reads g and m' again.  Pass 2 stages each chunk of V in LDS: the block's 16 rows are
-// one 16-element K group of every X row of the chunk, written as 64-byte
-// runs (4 lanes per X row).
+// one 16-element K group of every X row of the chunk, so each 64 lanes
+// write one whole 1 KB piece of the tiled X (16 X rows, 4 lanes per row).
 template <bool R1, bool KEPT>
 __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange range) {
   __shared__ float tile[kFlipRows][kFlipChunk + 4];
@@ -651,9 +650,9 @@ __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange rang
   const DevJob J = load_job(range.jobs, jid);
   const DevDesc &d = J.d;
   // Row group of the block: the hardware deals blocks to the 8 XCDs in
-  // turn, and the blocks of one XCD take consecutive groups, so the two
-  // 64-byte halves of a 128-byte line of X (adjacent K groups) meet in one
-  // L2.  (Every job's first block and block count are multiples of 8.)
+  // turn, and the blocks of one XCD take consecutive groups (adjacent K
+  // pieces of X).  (Every job's first block and block count are multiples
+  // of 8.)
   const int jb = blockIdx.x - range.start[jid];
   const int blk = (jb & 7) * static_cast<int>(J.prow_pad / kFlipRows / 8) + (jb >> 3);
   const int lane = threadIdx.x & 63;
@@ -814,7 +813,7 @@ __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange rang
       const int jj = (threadIdx.x >> 2) + 256 * r;  // X row in the chunk
       if (c0 + jj < J.pcol_pad) {
         const float w[4] = {tile[4 * qq][jj], tile[4 * qq + 1][jj], tile[4 * qq + 2][jj], tile[4 * qq + 3][jj]};
-        put_operand4((float *)J.x, (c0 + jj) * J.prow_pad + i0 + 4 * qq, w, planes);
+        put_operand4((float *)J.x, tiled_index(c0 + jj, i0 + 4 * qq, J.prow_pad), w, planes);
       }
     }
     __syncthreads();

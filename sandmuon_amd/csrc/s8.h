@@ -55,15 +55,16 @@ struct S8Class {
   int32_t tiles_s;     // rp / kSymTile
   int32_t gs;          // Gram-space iteration (cp > rp): the stages run on r x r
                        // products and X0 is applied once, at stage 5
-  // Iterate buffers (4 bytes per element), oriented layout only.  In
-  // SMX_S8_FP32 mode they hold FP32; in SMX_S8_COMP_BF16 mode interleaved
-  // BF16 hi/lo (put_operand), except the stage-5 result, which is FP32.
+  // Iterate buffers (4 bytes per element), oriented layout only: tiled
+  // operands (tiled_index), FP32 in SMX_S8_FP32 mode and interleaved BF16
+  // hi/lo (put_operand) or FP16 in the others, except the stage-5 result,
+  // which is a row-major FP32 matrix.
   float *x0, *x1;      // [count][rp][cp] ping, pong (Gram space: X0, then X2)
   float *xf;           // [n_flip][cp][rp] stage-5 result of transposed parameters
                        // (parameter layout); the others end in x1 (X-space)
                        // or x0 (Gram space)
-  float *g;            // [count][rp][rp] Gram (FP32, or planes in comp mode)
-  float *p;            // [count][rp][rp] stage 1: FP32 G2; later: P (planes in comp mode)
+  float *g;            // [count][rp][rp] Gram (tiled operand)
+  float *p;            // [count][rp][rp] stage 1: FP32 G2; later: P (tiled, like every operand)
   float *t, *qa, *qb;  // Gram-space classes only, [count][rp][rp] each (operand
                        // form): T = P G, and the accumulated product Q of a
                        // segment's stage polynomials (qa, qb: ping-pong)
@@ -128,13 +129,27 @@ struct S8Mat {
   __host__ __device__ int64_t pcol_pad() const { return flip() ? kp()->rp : kp()->cp; }
 };
 
-// GEMM operand buffers are row-major with K contiguous and rows padded to
-// multiples of kTile.  In compensated mode an element v is stored as two
-// BF16 values, hi = bf16(v) and lo = bf16(v - hi) (round to nearest even),
-// interleaved per 16-element K group: 16 hi values, then the 16 matching lo
-// values.  The buffer has the byte size of its FP32 form and a 16-deep K
-// slice of a row is one contiguous 64-byte run in both forms.  `idx` is the
-// FP32 element index (row * ld + k).
+// GEMM operand buffers hold ld K columns per row (ld a multiple of 16 for
+// the 4-byte forms, of 32 for FP16) and rows padded to multiples of kTile.
+// In compensated mode an element v is stored as two BF16 values, hi =
+// bf16(v) and lo = bf16(v - hi) (round to nearest even), interleaved per
+// 16-element K group: 16 hi values, then the 16 matching lo values.  The
+// buffer has the byte size of its FP32 form and the 16-element K group of a
+// row is one contiguous 64-byte run in both forms (32 elements in FP16).
+// Those runs are tiled: the runs of group k of 16 consecutive rows
+// (16 i .. 16 i + 15) form one contiguous 1 KB piece, and the pieces of a
+// row block follow each other in K order, so every 1 KB direct-to-LDS load
+// of a 16-deep K stage reads one piece, 8 whole 128-byte lines, and the K
+// groups of a K-major stage (16 rows, many columns) are consecutive pieces.
+// A 16-row block takes the bytes of 16 rows, so whole row blocks sit where
+// they would in a row-major buffer.  The stage-5 result of the map is not an
+// operand: it is a plain row-major FP32 matrix.
+// tiled_index: the FP32 element index of (row, col) in a tiled operand of
+// ld columns.  plane_hi: the BF16 index of the hi half of an element at FP32
+// index idx (its lo half is 16 further).
+__host__ __device__ inline int64_t tiled_index(int64_t row, int64_t col, int64_t ld) {
+  return ((((row >> 4) * (ld >> 4)) + (col >> 4)) << 8) + ((row & 15) << 4) + (col & 15);
+}
 __device__ __forceinline__ int64_t plane_hi(int64_t idx) { return 2 * (idx & ~int64_t{15}) + (idx & 15); }
 
 __device__ __forceinline__ uint16_t bf16_bits(float v) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v)); }
@@ -142,6 +157,8 @@ __device__ __forceinline__ uint16_t bf16_lo_bits(float v) {
   return bf16_bits(v - static_cast<float>(static_cast<__bf16>(v)));
 }
 
+// Operand-form stores at the FP32 element index idx (tiled_index of the
+// element; the elements of one store lie in one 16-element group).
 __device__ __forceinline__ void put_operand(float *base, int64_t idx, float v, bool planes) {
   if (planes) {
     uint16_t *h = reinterpret_cast<uint16_t *>(base) + plane_hi(idx);

@@ -26,10 +26,14 @@
 // range's precision, so Q' is the full product with Q as the K-major
 // operand of an apply tile (a mirrored Q' costs ~6x in accuracy).
 // The Gram (C = X X^T) and the square (C = G G, G symmetric) read both
-// operands as row-major K-contiguous rows.  The apply (C = P X) reads P the
-// same way and X itself as a K-major operand: its LDS tile holds 16 rows of
-// X and the MFMA fragments are gathered with the 16-bit transposed LDS read
+// operands as K-contiguous rows.  The apply (C = P X) reads P the same way
+// and X itself as a K-major operand: its LDS tile holds 16 rows of X and
+// the MFMA fragments are gathered with the 16-bit transposed LDS read
 // (ds_read_b64_tr_b16), so the iterate is only ever stored in one layout.
+// Every operand is tiled (s8.h: 1 KB pieces of 16 rows x one 64-byte K
+// group), so each 1 KB direct-to-LDS load of either kind reads one piece:
+// 8 whole 128-byte lines, where the rows' 64-byte runs of a row-major layout
+// touched 16 lines (cfg4 S8 10% faster).
 // Gram and square only compute upper-triangle tiles and store each
 // off-diagonal tile twice (tile and mirror).  The (b/c) G term of the square
 // is accumulated by extra MFMAs from the B fragments (one_hot), so no
@@ -67,12 +71,13 @@
 //
 // Operand forms (what a producer writes, chosen by the mode of the product
 // that reads it, out_form): FP32, interleaved BF16 hi/lo ("planes"; the
-// byte size of FP32), or FP16.  An FP16 operand has the row pitch 2 ld
-// bytes; in units of 4 bytes (the unit of the load offsets) it is an
-// operand of ld / 2 columns whose 32-deep K stages move the 64 bytes per
-// row that a 16-deep stage of the 4-byte forms moves, so the row-major
-// loads, the LDS ring and the fragment reads are those of the planes form
-// (chunk h: K 8h .. 8h+7 of the first 16, chunk 2 + h: of the second 16).
+// byte size of FP32), or FP16.  An FP16 operand has 2 ld bytes per row;
+// in units of 4 bytes (the unit of the load offsets) it is an operand of
+// ld / 2 columns whose 32-deep K stages move the 64 bytes per row that a
+// 16-deep stage of the 4-byte forms moves (its pieces: 16 rows x 32 K), so
+// the row-major loads, the LDS ring and the fragment reads are those of the
+// planes form (chunk h: K 8h .. 8h+7 of the first 16, chunk 2 + h: of the
+// second 16).
 //
 // Block: 256x128 output tile, 4 waves (2 x 2, one per SIMD), each wave
 // 128x64 (4 x 2 MFMA 32x32 tiles, 128 accumulator registers), and two
@@ -213,7 +218,7 @@ struct Geo {
   static constexpr int kLoadsA = kOpA / 1024 / kWaves;  // 1 KB loads per wave
   static constexpr int kLoadsB = kOpB / 1024 / kWaves;
   static constexpr int kLoadsPerStage = kLoadsA + kLoadsB;
-  static constexpr int kKmRow = TN * 4;           // bytes per K row of the K-major B tile
+  static constexpr int kKmRow = TN * 4;           // bytes of a K row of the K-major B tile
   static constexpr int kKmRowH = TN * 2;          // the same for FP16 operands (32 K rows per stage)
   static constexpr int kWavesPerEU = TM == 128 ? 3 : 2;
   static constexpr int kGeo = TN == 256 ? kGeoL : TM == 128 ? kGeoS : kGeoM;
@@ -260,13 +265,6 @@ struct Opnd {
 // 64-bank LDS.
 __device__ __forceinline__ int swz4(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 __device__ __forceinline__ int f32_off(int r, int kc) { return (r * 4 + (kc ^ swz4(r))) << 4; }
-// Chunk swizzle of the K-major operand tile (apply's B): 0, 2, 12 or 14
-// from bits 0 and 1 of the K row.  A transposed read takes 4 consecutive K
-// rows per 16 lanes, two chunks of each; the swizzle puts the 16 chunks that
-// 32 consecutive lanes read at distinct positions modulo 16 (and the 8 of
-// 16 lanes at distinct positions modulo 8), so each read is conflict-free
-// for 64 banks serving 32 lanes per cycle and for 32 banks serving 16.
-__device__ __forceinline__ int swzk(int k) { return 2 * (k & 1) + 12 * ((k >> 1) & 1); }
 
 // One 16-byte direct-to-LDS load per lane from sbase + voff (scalar base,
 // per-lane 32-bit byte offset): lane l writes LDS[m0 + 16 l].  Issued from
@@ -286,52 +284,60 @@ struct TileOffsets {
   uint32_t v[N];
 };
 
-// Row-major operand tile (rows row0.., 16 K columns): LDS chunk
-// p = (wave*N+i)*64 + lane is stored slot p&3 of row p>>2; the scalar base
-// of a stage at K offset k0 moves by 4*k0 bytes.
+// Row-major operand tile (rows row0.. of a tiled operand with ld columns,
+// one 16-deep K stage): load q = wave*N + i reads the stage's 1 KB piece of
+// rows row0 + 16 q .. + 15, lane l filling LDS slot l & 3 of tile row
+// 16 q + (l >> 2) with logical chunk (l & 3) ^ swz4(row) of that row
+// (swz4 only sees bits 1-3 of the row).  The scalar base of a stage at K
+// offset k0 (4-byte units) moves by 64 k0 bytes: k0 / 16 pieces.
 template <int N>
 __device__ __forceinline__ TileOffsets<N> tile_offsets(int64_t ld, int64_t row0, int wave) {
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, m = lane >> 2;
+  const uint32_t in_piece = static_cast<uint32_t>(m * 64 + (((lane & 3) ^ swz4(m)) << 4));
   TileOffsets<N> t;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    const int p = (wave * N + i) * 64 + lane;
-    const int row = p >> 2;
-    const int kc = (p & 3) ^ swz4(row);
-    t.v[i] = static_cast<uint32_t>(((row0 + row) * ld + kc * 4) * 4);
+    const int64_t blk = (row0 >> 4) + wave * N + i;  // 16-row block
+    t.v[i] = static_cast<uint32_t>(blk * (ld >> 4) * 1024) + in_piece;
   }
   return t;
 }
 
-// K-major tile (16 K rows, TN columns n0 .. n0 + TN - 1 of a row-major
-// operand with rows of `ld` elements; KMROW = 4 TN bytes per K row): with
-// 512-byte rows load i covers K rows 2 (wave*N+i) and 2 (wave*N+i) + 1,
-// lane l filling slot l & 31 of its row k; with 1 KB rows it covers K row
-// wave*N+i, lane l filling slot l.  The slot holds logical chunk
-// slot ^ swzk(k).  The scalar base of a stage at K offset k0 moves by
-// 4*k0*ld bytes.
-// Chunk swizzle of an FP16 K-major tile (rows of 2 TN bytes, 32 K rows per
-// stage): 0, 6, 12 or 10 from bits 0 and 1 of the K row.  A transposed read
-// of 16 lanes takes 4 consecutive K rows (aligned to 4) and two adjacent
-// chunks of each, 32 lanes four aligned chunks of each; bits 1-2 of the
-// swizzle differ between the 4 rows (the 16 lanes' chunks at distinct
-// positions modulo 8: 32 banks) and so do bits 2-3 (the 32 lanes' chunk
-// groups at distinct positions modulo 16: 64 banks).
-__device__ __forceinline__ int swzh(int k) { return (0xAC60 >> (4 * (k & 3))) & 0xE; }
+// K-major tile (the apply's B: the stage's K rows, columns n0 .. n0 + TN - 1
+// of a tiled operand with ld columns; KMROW = 4 TN bytes, 2 TN for FP16):
+// TN / 16 pieces, [piece][16 rows][64 bytes] in LDS.  Load q = wave*N + i
+// reads piece q: K group n0 / 16 + q of the stage's 16-row block (FP16, 32
+// K rows and 32 columns per group: pieces q < TN / 32 from the first row
+// block, the others from the second), lane l filling slot l & 3 of the
+// piece's row l >> 2 with logical chunk (l & 3) ^ swzt.  The scalar base of
+// a stage at K offset k0 moves by 4 k0 ld bytes (whole row blocks).
+// swzt: 2 ((row >> 1 ^ piece) & 1) (FP16: 2 ((row >> 1) & 1); FP32, whose
+// 4-byte reads are not on the MFMA-bound path's critical side, none, which
+// leaves its fragment addresses one register and constants).  A transposed
+// read of 16 lanes takes two chunks of each of 4 consecutive rows of one
+// piece: rows 4t and 4t + 2 share their bank positions modulo 128 bytes, and
+// the swizzle puts their chunks on different halves of the row (32 banks
+// serving 16 lanes); 32 lanes read the same rows of two adjacent pieces
+// (FP16: the other two chunks of the same piece), which the piece term puts
+// on different halves too (64 banks serving 32 lanes).
+__device__ __forceinline__ int swzt(int row, int piece) { return 2 * (((row >> 1) ^ piece) & 1); }
+__device__ __forceinline__ int swzt_h(int row) { return 2 * ((row >> 1) & 1); }
 
 // (F16: an FP16 operand; ld and n0 are in 4-byte units, i.e. half the
 // element counts, and a stage holds 32 K rows.)
-template <int N, int KMROW, bool F16 = false>
+enum KmSwz { kKmSwzNone = 0, kKmSwzT = 1, kKmSwzH = 2 };
+template <int N, int KMROW, int SWZ>
 __device__ __forceinline__ TileOffsets<N> tile_offsets_km(int64_t ld, int64_t n0, int wave) {
-  static_assert(KMROW == 256 || KMROW == 512 || KMROW == 1024, "one, two or four K rows per 1 KB load");
-  constexpr int kRowsPerLoad = 1024 / KMROW, kSlots = KMROW / 16;
-  const int lane = threadIdx.x & 63;
+  constexpr bool F16 = SWZ == kKmSwzH;
+  constexpr int kBlockPieces = KMROW / 64;  // pieces per 16-row block: TN / 16, FP16 TN / 32
+  const int lane = threadIdx.x & 63, m = lane >> 2;
   TileOffsets<N> t;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    const int k = kRowsPerLoad * (wave * N + i) + lane / kSlots;
-    const int sw = F16 ? swzh(k) : swzk(k);
-    t.v[i] = static_cast<uint32_t>((k * ld + n0) * 4 + (((lane % kSlots) ^ sw) << 4));
+    const int q = wave * N + i;
+    const int hb = F16 ? q / kBlockPieces : 0, jj = F16 ? q % kBlockPieces : q;
+    const int sw = SWZ == kKmSwzH ? swzt_h(m) : SWZ == kKmSwzT ? swzt(m, q) : 0;
+    t.v[i] = static_cast<uint32_t>((hb * (ld >> 4) + (n0 >> 4) + jj) * 1024 + m * 64 + (((lane & 3) ^ sw) << 4));
   }
   return t;
 }
@@ -391,11 +397,12 @@ __device__ __forceinline__ bf16x8 read_b16(const char *tile, int r, int kc) {
 }
 
 // ------------------------------------------- K-major operand tile (apply) ---
-// [16 K rows][kTileN N columns] of a row-major operand (the iterate X), one
-// row per K, in chunks of 16 bytes, logical chunk c at slot c ^ swzk(k).
-// Logical chunks follow the global bytes: interleaved BF16 4 G + 2 plane +
-// half (16-column group G, plane 0 hi / 1 lo, columns 8 half .. 8 half + 7
-// of the group); FP32 n / 4.  (swzk is defined with the row-major swizzle.)
+// [piece][16 K rows][64 bytes] (tile_offsets_km): piece j holds the
+// columns 16 j .. 16 j + 15 of the tile (FP16: 32 j .. 32 j + 31 of 16 K
+// rows, the stage's second 16 rows after the first), a 64-byte row of it in
+// 16-byte chunks, logical chunk c at slot c ^ swzt.  Logical chunks follow
+// the global bytes: interleaved BF16 2 plane + half (plane 0 hi / 1 lo,
+// columns 8 half .. 8 half + 7 of the piece); FP32 and FP16 in column order.
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
@@ -496,51 +503,44 @@ __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) 
 // transposed reads of 4 K rows each; lane s of a 16-lane group g addresses
 // row 8 (g >> 1) + 4 r + (s >> 2), columns 16 (g & 1) + 4 (s & 3) .. + 3 of
 // the 32-column block, so lane 16 (g & 1) + s of the block receives its
-// column at the 4 rows.  FP32: eight 4-byte reads.
-// The per-lane part of those addresses, fixed for a tile: the logical chunk
-// 8 kSubN wn + 8 j + 4 (g & 1) + 2 plane + ((s >> 1) & 1) is XORed with
-// swzk(k) < 16, which only touches bits 1..3, so bits 4 and up (16 (j >> 1)
-// and 8 kSubN wn) add to the chunk index; the rest takes one offset per
-// (j & 1, plane).
+// column at the 4 rows.  Column block j of wave wn is pieces 4 wn + 2 j and
+// 4 wn + 2 j + 1 (g & 1 picks one), logical chunk 2 plane + ((s >> 1) & 1),
+// byte 8 (s & 1) of it.  The swizzle of rows k and k + 4 is the same, and
+// its piece term is g & 1, so the per-lane offsets (wn included) are one per
+// plane (o[plane][0]) and every read adds a constant.  FP16: lane s of group
+// g addresses row 8 (g >> 1) + (s >> 2) (+4 for the second read, + the
+// second row block's pieces for the second 16 K), columns 16 (g & 1) +
+// 4 (s & 3) .. + 3 of piece 2 wn + j (32 columns), i.e. chunk 2 (g & 1) +
+// ((s >> 1) & 1); o[j][0] holds the offset of block j.  FP32: eight
+// 4-byte reads.
 struct BkmLane {
   uint32_t o[2][2];
 };
-template <int KMROW>
-__device__ __forceinline__ BkmLane bkm_lane() {
+__device__ __forceinline__ BkmLane bkm_lane(int wn) {
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, s = lane & 15;
   const int k = 8 * (g >> 1) + (s >> 2);
-  const int sw = swzk(k);  // the same for rows k and k + 4
+  const int sw = swzt(k, g & 1);  // the same for rows k and k + 4
   BkmLane L;
 #pragma unroll
-  for (int jl = 0; jl < 2; ++jl)
-#pragma unroll
-    for (int pl = 0; pl < 2; ++pl)
-      L.o[jl][pl] = static_cast<uint32_t>(k * KMROW + 8 * (s & 1) +
-                                          (((8 * jl + 4 * (g & 1) + 2 * pl + ((s >> 1) & 1)) ^ sw) << 4));
+  for (int pl = 0; pl < 2; ++pl) {
+    L.o[pl][0] = static_cast<uint32_t>((4 * wn + (g & 1)) * 1024 + k * 64 + 8 * (s & 1) +
+                                       (((2 * pl + ((s >> 1) & 1)) ^ sw) << 4));
+    L.o[pl][1] = 0;
+  }
   return L;
 }
 
-// FP16 K-major tile (rows of KMROW = 2 TN bytes, 32 K rows per stage).
-// Lane (n, h) needs B[k = 8h .. 8h+7][n] for the first 16 K and B[16 + 8h
-// ..][n] for the second.  Lane s of the 16-lane group g addresses row
-// 8 (g >> 1) + (s >> 2) (+4 for the second read, +16 for the second 16 K)
-// and columns 16 (g & 1) + 4 (s & 3) .. + 3 of each 32-column block j of the
-// wave, i.e. chunk 8 wn + 4 j + 2 (g & 1) + ((s >> 1) & 1) and byte 8 (s & 1)
-// of it; the row's swizzle depends on s alone, so o[j][0] holds the whole
-// per-lane offset of block j (wn included) and the other reads add
-// constants.
-template <int KMROW>
 __device__ __forceinline__ BkmLane bkm_lane_f16(int wn) {
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, s = lane & 15;
   const int k = 8 * (g >> 1) + (s >> 2);
-  const int sw = swzh(k);  // the same for rows k + 4, k + 16 and k + 20
+  const int sw = swzt_h(k);  // the same for rows k + 4 and the second row block
   BkmLane L;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    L.o[j][0] = static_cast<uint32_t>(k * KMROW + 8 * (s & 1) +
-                                      (((8 * wn + 4 * j + 2 * (g & 1) + ((s >> 1) & 1)) ^ sw) << 4));
+    L.o[j][0] = static_cast<uint32_t>((2 * wn + j) * 1024 + k * 64 + 8 * (s & 1) +
+                                      (((2 * (g & 1) + ((s >> 1) & 1)) ^ sw) << 4));
     L.o[j][1] = 0;
   }
   return L;
@@ -548,60 +548,55 @@ __device__ __forceinline__ BkmLane bkm_lane_f16(int wn) {
 
 template <int MODE, class G>
 __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &f, const BkmLane &L) {
-  constexpr int kOpA = G::kOpA, kKmRow = G::kKmRow;
+  constexpr int kOpA = G::kOpA;
   const int lane = threadIdx.x & 63;
   const char *bt = st + kOpA;
   if constexpr (MODE == kS8F16) {
     static_assert(kSubN == 2, "one lane offset per 32-column block");
-    constexpr int kRow = G::kKmRowH;
+    constexpr int kBlockBytes = G::kKmRowH / 64 * 1024;  // the pieces of one 16-row block
 #pragma unroll
     for (int j = 0; j < kSubN; ++j) {
       lds_char *q = to_lds(st) + L.o[j][0];
       asm volatile("" : "+v"(q));
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        lds_char *p = q + (kOpA + 16 * half * kRow);
-        const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * kRow);
+        lds_char *p = q + (kOpA + half * kBlockBytes);
+        const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * 64);
         const bf16x8 v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         if (half == 0) f.h[j] = v;
         else f.l[j] = v;
       }
     }
   } else if constexpr (MODE != SMX_S8_FP32) {
-    // Four base addresses per stage; the empty asm keeps the compiler from
+    // Two base addresses per stage; the empty asm keeps the compiler from
     // pre-adding every read's constant offset into a register of its own
-    // (sixteen live registers and two VALU ops per read) instead of using
-    // the instructions' offset field.
-    lds_char *q[2][2];
+    // instead of using the instructions' offset field.
+    lds_char *q[2];
 #pragma unroll
-    for (int jl = 0; jl < 2; ++jl)
-#pragma unroll
-      for (int pl = 0; pl < 2; ++pl) {
-        q[jl][pl] = to_lds(st) + L.o[jl][pl];
-        asm volatile("" : "+v"(q[jl][pl]));
-      }
+    for (int pl = 0; pl < 2; ++pl) {
+      q[pl] = to_lds(st) + L.o[pl][0];
+      asm volatile("" : "+v"(q[pl]));
+    }
 #pragma unroll
     for (int j = 0; j < kSubN; ++j) {
 #pragma unroll
       for (int pl = 0; pl < (is_comp(MODE) ? 2 : 1); ++pl) {
-        lds_char *p = q[j & 1][pl] + (kOpA + ((8 * kSubN * wn + 16 * (j >> 1)) << 4));
-        const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * kKmRow);
+        lds_char *p = q[pl] + (kOpA + 2 * j * 1024);
+        const i16x4 lo = read_tr16(p), hi = read_tr16(p + 4 * 64);
         const bf16x8 v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         if (pl == 0) f.h[j] = v;
         else f.l[j] = v;
       }
     }
   } else {
-    const int h = lane >> 5;
+    // Lane (n, h), n = 64 wn + 32 j + (lane & 31): piece 4 wn + 2 j +
+    // ((lane >> 4) & 1), element 4 ((lane >> 2) & 3) + (lane & 3) of rows
+    // 8 h + q (no swizzle).
+    const char *base = bt + (4 * wn + ((lane >> 4) & 1)) * 1024 + 512 * (lane >> 5) + 4 * (lane & 15);
 #pragma unroll
-    for (int j = 0; j < kSubN; ++j) {
-      const int n = wn * (32 * kSubN) + j * 32 + (lane & 31);
+    for (int j = 0; j < kSubN; ++j)
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int k = 8 * h + q;
-        f.v[j][q] = *reinterpret_cast<const float *>(bt + k * kKmRow + (((n >> 2) ^ swzk(k)) << 4) + (n & 3) * 4);
-      }
-    }
+      for (int q = 0; q < 8; ++q) f.v[j][q] = *reinterpret_cast<const float *>(base + 2048 * j + 64 * q);
   }
 }
 
@@ -732,8 +727,8 @@ struct WaveOffsets {
 template <class G, bool BKM, int KMSTEP>
 __device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const WaveOffsets<G> &o, int64_t k0,
                                             uint32_t lds) {
-  dma_tile(o.a, static_cast<const char *>(A.p) + 4 * k0, lds);
-  dma_tile(o.b, static_cast<const char *>(B.p) + 4 * k0 * (BKM ? B.ld * KMSTEP : 1), lds + o.b_lds);
+  dma_tile(o.a, static_cast<const char *>(A.p) + 64 * k0, lds);
+  dma_tile(o.b, static_cast<const char *>(B.p) + (BKM ? 4 * k0 * B.ld * KMSTEP : 64 * k0), lds + o.b_lds);
 }
 
 // Waits until at most `pending` stages of this wave's loads are in flight
@@ -831,11 +826,12 @@ __device__ __forceinline__ void gemm_tile(const Opnd &A_in, const Opnd &B_in, in
   const int nk = static_cast<int>(K / (kBK * kU));
   WaveOffsets<G> o;
   o.a = tile_offsets<G::kLoadsA>(A.ld, arow0, wave);
-  o.b = BKM ? tile_offsets_km<G::kLoadsB, F16 ? G::kKmRowH : G::kKmRow, F16>(B.ld, brow0 / kU, wave)
+  o.b = BKM ? tile_offsets_km<G::kLoadsB, F16 ? G::kKmRowH : G::kKmRow,
+                              F16 ? kKmSwzH : MODE == SMX_S8_FP32 ? kKmSwzNone : kKmSwzT>(B.ld, brow0 / kU, wave)
             : tile_offsets<G::kLoadsB>(B.ld, brow0, wave);
   o.b_lds = static_cast<uint32_t>(G::kOpA + wave * (G::kLoadsB - G::kLoadsA) * 1024);
   // used by the K-major B path only
-  const BkmLane bl = F16 ? bkm_lane_f16<G::kKmRowH>(wn) : bkm_lane<G::kKmRow>();
+  const BkmLane bl = F16 ? bkm_lane_f16(wn) : bkm_lane(wn);
   // LDS byte address of the ring plus this wave's first A chunk.
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * G::kLoadsA * 1024;
 #pragma unroll
@@ -1154,6 +1150,10 @@ s8_stage_kernel(StageArgs args) {
     do_t = true;
     do_m = !diag;
   }
+  // Every output is a tiled operand except the stage-5 result (row-major
+  // FP32: the mapback's and the stand-alone map's input).
+  const bool tiled_t = !(PHASE == kApply && last && (ref.op == kOpApplyX || ref.op == kOpApplyFinal));
+  const bool tiled_m = PHASE != kApply;
   const bool eye = PHASE == kSquare && stage != 1;  // add a I on the diagonal
   float *const T = reinterpret_cast<float *>(smem) + wave * 2 * kEpBlock;
   float *const U = T + kEpBlock;
@@ -1186,6 +1186,9 @@ s8_stage_kernel(StageArgs args) {
   // operand form the chunk is plane (ech >> 1) & 1 of columns
   // 16 (ech >> 2) + 8 (ech & 1) .. + 7; in FP32 columns 4 ech .. 4 ech + 3.
   const int er = lane >> 3, ech = lane & 7;
+  // the lane's chunk: tiled, byte 16 (ech & 3) of the row's K group ech >> 2;
+  // row-major, byte 16 ech of the row's 128 bytes
+  const int ech_t = ((ech >> 2) << 10) + ((ech & 3) << 4), ech_r = ech << 4;
   const bool lo_plane = ((ech >> 1) & 1) != 0;
   const int ec8 = 16 * (ech >> 2) + 8 * (ech & 1), ec4 = 4 * ech;
   float rs[kSubN][4][3];
@@ -1223,10 +1226,12 @@ s8_stage_kernel(StageArgs args) {
   // Row `row` of a staged block (S) to global row gr, columns gc0 .. gc0 + 31
   // (gc0 a multiple of 32) in form FM: one 16-byte store per lane (FP32,
   // planes), or one 8-byte store of the lane's four columns (FP16: the
-  // row's 64 bytes).
+  // row's 64 bytes).  A tiled output (`tl`; planes and FP16 always are)
+  // puts the row's two 64-byte K groups (one for FP16) in their pieces, so
+  // the 8 rows of a store instruction fill two 512-byte halves of pieces.
   // (FM = kFormAny: planes or FP32 chosen at run time by `form`, one loop
   // for both, in the kernels that produce no FP16.)
-  auto put_row = [&](auto fm_c, const float *S, int row, int64_t gr, int64_t gc0, float *dst, int64_t ld,
+  auto put_row = [&](auto fm_c, const float *S, int row, int64_t gr, int64_t gc0, float *dst, int64_t ld, bool tl,
                      float (&r)[3], bool acc_r) {
     constexpr int FM = decltype(fm_c)::value;
     if constexpr (FM == kFormF16) {
@@ -1241,11 +1246,19 @@ s8_stage_kernel(StageArgs args) {
       for (int e = 0; e < 2; ++e)
         b[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(w[2 * e]))) |
                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(w[2 * e + 1]))) << 16);
-      *reinterpret_cast<uint2 *>(reinterpret_cast<char *>(dst) + (gr * ld + gc0 + ec4) * 2) = make_uint2(b[0], b[1]);
+      // (32-column pieces: group gc0 / 32 at 32 gc0 bytes of the row block)
+      const int64_t off = (gr & ~int64_t{15}) * (2 * ld) + ((gr & 15) << 6) + 32 * gc0 + 8 * ech;
+      *reinterpret_cast<uint2 *>(reinterpret_cast<char *>(dst) + off) = make_uint2(b[0], b[1]);
       return;
     }
-    char *out = reinterpret_cast<char *>(dst) + (gr * ld + gc0) * 4 + 16 * ech;
     const bool pl = FM == kFormPlanes || (FM == kFormAny && form == kFormPlanes);
+    // Row block, row in it, columns: (gr & ~15) 4 ld + (gr & 15) rs + gc0 cs
+    // + the lane's chunk, rs = 64 and cs = 64 tiled (group gc0 / 16 at
+    // 1024 gc0 / 16 bytes of the row block), rs = 4 ld and cs = 4 row-major.
+    const bool t = pl || tl;
+    const int64_t off = (gr & ~int64_t{15}) * (4 * ld) + (gr & 15) * (t ? 64 : 4 * ld) + gc0 * (t ? 64 : 4) +
+                        (t ? ech_t : ech_r);
+    char *out = reinterpret_cast<char *>(dst) + off;
     if (pl) {
       float w[8];
       ep_read8(S, row, ec8, w);
@@ -1300,12 +1313,12 @@ s8_stage_kernel(StageArgs args) {
         const int row = er + 8 * q;
         if (do_t) {
           const int64_t gr = R0 + i * 32 + row;
-          put_row(fm_c, T, row, gr, C0 + j * 32, dst_t, ld_t, rs[0][q], rs_on);
+          put_row(fm_c, T, row, gr, C0 + j * 32, dst_t, ld_t, tiled_t, rs[0][q], rs_on);
           if (rs_on && j == kSubN - 1) emit(gr, C0 / kStripT, rs[0][q]);
         }
         if (do_m) {
           const int64_t gr = C0 + j * 32 + row;
-          put_row(fm_c, U, row, gr, R0 + i * 32, dst_m, ld_m, rs[j][q], rs_on);
+          put_row(fm_c, U, row, gr, R0 + i * 32, dst_m, ld_m, tiled_m, rs[j][q], rs_on);
           if (rs_on && i == kSubM - 1) emit(gr, R0 / kStripM, rs[j][q]);
         }
       }
@@ -1340,8 +1353,10 @@ s8_stage_kernel(StageArgs args) {
 // Stage-1 polynomial operand (sandmuon/optimizer.py:84-86) over the r x r
 // matrices of a class: P1 = a I + (b G)/s^2 + (c G2)/s^4 from the
 // normalised G and the FP32 G2 of the square phase, written over G2 in the
-// p buffer in operand form (into qa, as Q1, for a Gram-space class).  A
-// block takes kPolyChunk consecutive 16-element groups of one matrix, four
+// p buffer in operand form (into qa, as Q1, for a Gram-space class).  G,
+// G2 and P1 are tiled alike, so the pass runs over their 64-byte runs in
+// memory order, and only the diagonal term needs an element's row and
+// column.  A block takes kPolyChunk consecutive runs of one matrix, four
 // lanes per group, each lane a quarter (4 elements: 16 bytes of FP32, 8 of
 // each BF16 half), so that every load and store instruction of a wave
 // covers 16 whole groups (1 KB); a thread takes kPolyUnits quarters.  All
@@ -1406,7 +1421,9 @@ __global__ void __launch_bounds__(256) s8_poly1_kernel(StageArgs args) {
       g[0] = __uint_as_float(gh[k].x); g[1] = __uint_as_float(gh[k].y);
       g[2] = __uint_as_float(gl[k].x); g[3] = __uint_as_float(gl[k].y);
     }
-    const int64_t row = grp[k] / gpr, col = (grp[k] % gpr) * 16 + 4 * qt;
+    // (tiled: run u is row 16 (u / 16 / gpr) + u % 16 of K group (u / 16) % gpr)
+    const int64_t pc = grp[k] >> 4;
+    const int64_t row = (pc / gpr) * 16 + (grp[k] & 15), col = (pc % gpr) * 16 + 4 * qt;
     float v[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -1701,11 +1718,13 @@ static int run_s8_set_stage(const S8Layout &Lay, const SlotSet &set, int stage, 
 
 // The launch chains of an S8 run beyond the first (which runs on the
 // caller's stream): further streams of the device (default priority), each
-// with the events of its fork and join, created once per device.
+// with the events of its fork and join, and an event per chain for the end
+// of each of stages 1-4, created once per device.
 constexpr int kChains = 2;
 struct ForkStream {
   hipStream_t aux[kChains - 1] = {};
   hipEvent_t fork = nullptr, join[kChains - 1] = {};
+  hipEvent_t stage_end[kChains][4] = {};
 };
 static std::mutex g_fork_lock;
 static ForkStream g_fork[64];
@@ -1723,6 +1742,9 @@ static int fork_stream(ForkStream *&out) {
     for (int i = 0; ok && i < kChains - 1; ++i)
       ok = hipStreamCreateWithFlags(&f.aux[i], hipStreamNonBlocking) == hipSuccess &&
            hipEventCreateWithFlags(&f.join[i], hipEventDisableTiming) == hipSuccess;
+    for (int t = 0; ok && t < kChains; ++t)
+      for (int k = 0; ok && k < 4; ++k)
+        ok = hipEventCreateWithFlags(&f.stage_end[t][k], hipEventDisableTiming) == hipSuccess;
     if (!ok) {
       f.fork = nullptr;
       return fail(SMX_ELAUNCH, "s8: cannot create the launch chains' streams and events");
@@ -1740,8 +1762,12 @@ static int fork_stream(ForkStream *&out) {
 // stream, the others on further streams forked from it and joined back
 // before the run ends: the blocks of one chain's launches fill the CUs
 // that the others' leave idle (a launch's tail, tiles that take longer than
-// the rest).  The launch recorder gets one record for the run, on the
-// caller's stream.
+// the rest).  Each chain starts a stage only once the others have finished
+// the one before: left alone, the chain whose launches reach the hardware
+// queues first keeps the CUs first and pulls ahead, and the other then runs
+// its last stage alone (cfg4 S8 2.37-2.46 ms with 2.7-3.0 ms in 3 runs of 7;
+// with the stage waits 2.41-2.42 ms in every run).  The launch recorder
+// gets one record for the run, on the caller's stream.
 constexpr int kSplitCount = 2 * kChains;
 
 int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
@@ -1796,9 +1822,20 @@ int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
         rc = fail(SMX_ELAUNCH, "s8: fork of the launch chains failed");
     // The chains are enqueued a stage at a time each, so that every chain
     // starts while the host is still enqueuing the others.
-    for (int stage = 1; stage <= 5 && !rc; ++stage)
-      for (int t = chains - 1; t >= 0 && !rc; --t)
-        if (!set[t].empty()) rc = run_s8_set_stage(Lay, set[t], stage, t ? f->aux[t - 1] : st, flops);
+    auto chain_stream = [&](int t) { return t ? f->aux[t - 1] : st; };
+    for (int stage = 1; stage <= 5 && !rc; ++stage) {
+      for (int t = chains - 1; t >= 0 && !rc; --t) {
+        if (set[t].empty()) continue;
+        for (int u = 0; stage > 1 && u < chains && !rc; ++u)
+          if (u != t && !set[u].empty() &&
+              hipStreamWaitEvent(chain_stream(t), f->stage_end[u][stage - 2], 0) != hipSuccess)
+            rc = fail(SMX_ELAUNCH, "s8: stage wait between the launch chains failed");
+        if (!rc) rc = run_s8_set_stage(Lay, set[t], stage, chain_stream(t), flops);
+      }
+      for (int t = 0; stage < 5 && t < chains && !rc; ++t)
+        if (!set[t].empty() && hipEventRecord(f->stage_end[t][stage - 1], chain_stream(t)) != hipSuccess)
+          rc = fail(SMX_ELAUNCH, "s8: stage wait between the launch chains failed");
+    }
     // Join even after a failed launch, so the caller's stream never runs
     // ahead of work already on the other streams.
     for (int t = 1; f && t < chains; ++t)

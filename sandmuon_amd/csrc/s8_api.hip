@@ -33,8 +33,8 @@ __global__ void __launch_bounds__(256) s8_load_norm_kernel(S8IoArgs a) {
 }
 
 // Tile pass: 64x64 tiles of the padded parameter layout (input layout)
-// into the oriented iterate x0: directly, or transposed through LDS for
-// transposed parameters.  grid = (tiles, batch), block 256.
+// into the oriented iterate x0 (a tiled operand): directly, or transposed
+// through LDS for transposed parameters.  grid = (tiles, batch), block 256.
 __global__ void __launch_bounds__(256) s8_load_tiles_kernel(S8IoArgs a) {
   __shared__ float tile[64][65];
   const S8Mat M{a.k, static_cast<int32_t>(blockIdx.y)};
@@ -56,7 +56,7 @@ __global__ void __launch_bounds__(256) s8_load_tiles_kernel(S8IoArgs a) {
       v[e] = (i < a.rows && j < a.cols) ? x[i * a.sr + j * a.sc] : 0.f;
       tile[lr][lc + e] = v[e];
     }
-    if (pl) put_operand4(pl, i * ppad + j0 + lc, v, a.planes != 0);
+    if (pl) put_operand4(pl, tiled_index(i, j0 + lc, ppad), v, a.planes != 0);
   }
   if (!tl) return;  // uniform per block
   __syncthreads();
@@ -64,7 +64,7 @@ __global__ void __launch_bounds__(256) s8_load_tiles_kernel(S8IoArgs a) {
   for (int q = 0; q < 4; ++q) {
     const int lr = (t >> 4) + 16 * q;
     const float v[4] = {tile[lc][lr], tile[lc + 1][lr], tile[lc + 2][lr], tile[lc + 3][lr]};
-    put_operand4(tl, (j0 + lr) * rpad + i0 + lc, v, a.planes != 0);
+    put_operand4(tl, tiled_index(j0 + lr, i0 + lc, rpad), v, a.planes != 0);
   }
 }
 
