@@ -353,13 +353,43 @@ __device__ __forceinline__ void block_part(const DevJob &J, double vy, double vu
   }
 }
 
+// Operand-form bytes of a row group staged in LDS before they go to the
+// tiled X: rows of up to 768 columns four at a time (up to 1536 two, up to
+// 3072 one at a time), each row's bytes in row-major operand form at a pitch
+// of 64 bytes more than the row, so that the 16 lanes reading 16-byte
+// chunks of 4 rows hit distinct banks.
+constexpr int kWhitenStageBytes = 4 * (768 * 4 + 64);
+
+// The 16 bytes a lane of put_operand4_paired's lane pairs writes, and their
+// byte offset in the row: FP32 the lane's four values; BF16 planes the
+// pair's eight hi values (even lane) or lo values (odd lane).  col = the
+// lane's first column (a multiple of 4).
+__device__ __forceinline__ u32x4v operand_chunk(const float (&v)[4], bool planes, int64_t col, int64_t &off) {
+  if (!planes) {
+    off = 4 * col;
+    return u32x4v{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+  }
+  const uint32_t h0 = bf16_bits(v[0]) | (uint32_t(bf16_bits(v[1])) << 16);
+  const uint32_t h1 = bf16_bits(v[2]) | (uint32_t(bf16_bits(v[3])) << 16);
+  const uint32_t l0 = bf16_lo_bits(v[0]) | (uint32_t(bf16_lo_bits(v[1])) << 16);
+  const uint32_t l1 = bf16_lo_bits(v[2]) | (uint32_t(bf16_lo_bits(v[3])) << 16);
+  const bool odd = (threadIdx.x & 1) != 0;
+  const uint32_t x0 = dpp_mov<0xB1>(odd ? h0 : l0), x1 = dpp_mov<0xB1>(odd ? h1 : l1);
+  off = 2 * (plane_hi(col) + (odd ? 16 - 4 : 0));
+  return odd ? u32x4v{x0, x1, l0, l1} : u32x4v{h0, h1, x0, x1};
+}
+
 // Rows whose float4 fit kMaxSlices per lane (the float4 path): the block
 // takes kWhitenGroups row groups in turn.  a and z are the same for every
 // row a lane sees and are loaded once; the g and m' of group k + 1 are
-// loaded while group k is reduced and stored.
+// loaded while group k is reduced and stored.  The group's X goes through
+// LDS (`xs`, one buffer per group parity) and is stored as the rows'
+// consecutive 64-byte runs of each K group: with two or four rows per group
+// whole 128-byte lines of the tiled X, where each wave's own row would leave
+// half lines.
 template <bool R1>
 __device__ __forceinline__ void whiten_rows_pipelined(const DevJob &J, int blk, double (*red)[4][4],
-                                                      double (*rp)[4]) {
+                                                      double (*rp)[4], char (*xs)[kWhitenStageBytes]) {
   const DevDesc &d = J.d;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -370,6 +400,7 @@ __device__ __forceinline__ void whiten_rows_pipelined(const DevJob &J, int blk, 
   const float kappa = R1 ? d.kappa[0] : 0.f;
   const bool planes = J.planes != 0;
   const int64_t row0 = static_cast<int64_t>(blk) * kWhitenGroups * rpg + rib;
+  const int pitch = 4 * static_cast<int>(J.pcol_pad) + 64;
   float4 a[kMaxSlices], z[kMaxSlices];
   float bb[kWhitenGroups];
 #pragma unroll
@@ -470,7 +501,24 @@ __device__ __forceinline__ void whiten_rows_pipelined(const DevJob &J, int blk, 
         }
         // pc4 is a multiple of 4 and q0 + span t steps by lanes, so both
         // lanes of a pair are inside the row or both outside
-        put_operand4_paired(J.x, tiled_index(i, 4 * static_cast<int64_t>(q), J.pcol_pad), w, planes, true);
+        int64_t off;
+        const u32x4v c = operand_chunk(w, planes, 4 * static_cast<int64_t>(q), off);
+        *reinterpret_cast<u32x4v *>(xs[k & 1] + rib * pitch + off) = c;
+      }
+    }
+    {
+      // (one barrier per group: a buffer is rewritten two groups later,
+      // after every thread has passed the next group's barrier)
+      __syncthreads();
+      // The group's rows lie in one 16-row block of the tiled X: K group g
+      // at 1 KB g from the group's first run, row r 64 r bytes further.
+      const int64_t first = row0 - rib + k * rpg;
+      SMX_GLOBAL char *gp = reinterpret_cast<SMX_GLOBAL char *>(J.x) + 4 * tiled_index(first, 0, J.pcol_pad);
+      const int lg = W == 1 ? 2 : W == 2 ? 1 : 0;  // log2 rpg
+      for (int ci = threadIdx.x; ci < (pc4 << lg); ci += kRowThreads) {
+        const int c = ci & 3, r = (ci >> 2) & (rpg - 1), g = ci >> (2 + lg);
+        const u32x4v v = *reinterpret_cast<const u32x4v *>(xs[k & 1] + r * pitch + 64 * g + 16 * c);
+        *reinterpret_cast<SMX_GLOBAL u32x4v *>(gp + (1024 * g + 64 * r + 16 * c)) = v;
       }
     }
   }
@@ -627,11 +675,12 @@ template <bool R1>
 __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
   __shared__ double red[2][4][4];  // row sums over the waves of a row
   __shared__ double rp[2][4];
+  __shared__ __attribute__((aligned(16))) char xs[2][kWhitenStageBytes];
   const int jid = find_job(range, blockIdx.x);
   const DevJob J = load_job(range.jobs, jid);
   const int blk = blockIdx.x - range.start[jid];
   if (whiten_pipelined(J))
-    whiten_rows_pipelined<R1>(J, blk, red, rp);
+    whiten_rows_pipelined<R1>(J, blk, red, rp, xs);
   else
     whiten_rows_single<R1>(J, blk, red[0], rp);
 }
