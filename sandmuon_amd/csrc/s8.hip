@@ -1570,11 +1570,12 @@ static int64_t device_cus() {
 }
 
 // The tile geometry of one launch over `segs`.  256 x 256 tiles when the
-// launch has at least 0.9 of one per CU: those blocks move a third fewer
-// operand bytes per MFMA (cfg5 S8 7% faster, the cfg4 applies 16%
-// faster).  With fewer, each CU has at most one block of a launch and
-// nothing of it to overlap a block's prologue and epilogue with (cfg4
-// Gram, square and SYM launches 15-60% slower).  Otherwise, for the
+// launch has at least 1.5 of them per CU: those blocks move a third fewer
+// operand bytes per MFMA (cfg5 S8 7% faster).  With fewer, each CU holds
+// one or two blocks of the launch and nothing of it to overlap a block's
+// prologue and epilogue with (cfg4 Gram, square and SYM launches 15-60%
+// slower; with tiled operands the cfg4 applies, 0.6-2.2 tiles per CU, are
+// 1-2% faster as 256 x 128 tiles, two blocks per CU).  Otherwise, for the
 // symmetric products (`small_ok`: Gram, square, SYM), 128 x 128 tiles when
 // they take fewer rounds of the CUs' block slots (three per CU, a round
 // counted 0.9 of one of two 256 x 128 blocks per CU), else 256 x 128.
@@ -1587,7 +1588,7 @@ static int pick_geo(const S8Layout &Lay, int phase, const std::vector<Seg> &segs
     const int64_t cnt = sg.hi - sg.lo;
     for (int g = 0; g < 3; ++g) tiles[g] += cnt * phase_tiles(k, phase, g, sg.op);
   }
-  if (g_tile_policy == 0 && 10 * tiles[kGeoL] >= 9 * cus) return kGeoL;
+  if (g_tile_policy == 0 && 2 * tiles[kGeoL] >= 3 * cus) return kGeoL;
   if (small_ok) {
     const double r_m = static_cast<double>(ceil_div(tiles[kGeoM], 2 * cus));
     const double r_s = static_cast<double>(ceil_div(tiles[kGeoS], 3 * cus));

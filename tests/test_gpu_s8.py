@@ -252,12 +252,12 @@ GEOMETRY = {"128x128": (128, 128, 4), "256x128": (256, 128, 4), "256x256": (256,
 
 def expected_square_geometry(n, size, cus):
     """The square's geometry for a launch over n matrices of size x size:
-    256 x 256 tiles when there are at least 0.9 of one per CU, else 128 x 128
+    256 x 256 tiles when there are at least 1.5 of them per CU, else 128 x 128
     tiles when they take fewer rounds of the CUs' block slots (three per CU,
     a round counted 0.9 of one of two 256 x 128 blocks), else 256 x 128."""
     t256, ts = size // 256, size // 128
     sym = lambda t: t * (t + 1) // 2
-    if 10 * n * sym(t256) >= 9 * cus:
+    if 2 * n * sym(t256) >= 3 * cus:
         return "256x256", sym(t256)
     big_rounds = -(-n * 2 * sym(t256) // (2 * cus))
     small_rounds = -(-n * sym(ts) // (3 * cus))
@@ -265,16 +265,16 @@ def expected_square_geometry(n, size, cus):
 
 
 @pytest.mark.parametrize("mode", ["fp32", "comp_bf16", "mixed"])
-@pytest.mark.parametrize("batch,size,geometry", [(8, 512, "128x128"), (74, 768, "256x128"), (160, 512, "256x256")])
+@pytest.mark.parametrize("batch,size,geometry", [(8, 512, "128x128"), (74, 768, "256x128"), (800, 256, "256x256")])
 def test_s8_square_tile_geometries(device, mode, batch, size, geometry):
     """The square phase takes 256 x 256 tiles when the launch has at least
-    0.9 of one per CU, else 128 x 128 tiles when they need fewer rounds of
+    1.5 of them per CU, else 128 x 128 tiles when they need fewer rounds of
     the CUs' block slots, else 256 x 128 tiles.  A class of 4 or more
     matrices runs as two launch chains of halves, and each chain's launches
     decide for themselves: 4 matrices of 512 x 512 on 256 CUs give 40 small
     tiles against 24 of 256 x 128, one round each; 37 of 768 x 768 give 777
     small tiles (two rounds of three per CU) against 444 of 256 x 128 (one
-    round of two) and 222 of 256 x 256; 80 of 512 x 512 give 240 tiles of
+    round of two) and 222 of 256 x 256; 400 of 256 x 256 give 400 tiles of
     256 x 256.  Every geometry meets the gates; the recorded square FLOPs
     show which one ran."""
     cus = torch.cuda.get_device_properties(device).multi_processor_count
