@@ -1719,13 +1719,11 @@ static int run_s8_set_stage(const S8Layout &Lay, const SlotSet &set, int stage, 
 
 // The launch chains of an S8 run beyond the first (which runs on the
 // caller's stream): further streams of the device (default priority), each
-// with the events of its fork and join, and an event per chain for the end
-// of each of stages 1-4, created once per device.
+// with the events of its fork and join, created once per device.
 constexpr int kChains = 2;
 struct ForkStream {
   hipStream_t aux[kChains - 1] = {};
   hipEvent_t fork = nullptr, join[kChains - 1] = {};
-  hipEvent_t stage_end[kChains][4] = {};
 };
 static std::mutex g_fork_lock;
 static ForkStream g_fork[64];
@@ -1743,9 +1741,6 @@ static int fork_stream(ForkStream *&out) {
     for (int i = 0; ok && i < kChains - 1; ++i)
       ok = hipStreamCreateWithFlags(&f.aux[i], hipStreamNonBlocking) == hipSuccess &&
            hipEventCreateWithFlags(&f.join[i], hipEventDisableTiming) == hipSuccess;
-    for (int t = 0; ok && t < kChains; ++t)
-      for (int k = 0; ok && k < 4; ++k)
-        ok = hipEventCreateWithFlags(&f.stage_end[t][k], hipEventDisableTiming) == hipSuccess;
     if (!ok) {
       f.fork = nullptr;
       return fail(SMX_ELAUNCH, "s8: cannot create the launch chains' streams and events");
@@ -1763,12 +1758,11 @@ static int fork_stream(ForkStream *&out) {
 // stream, the others on further streams forked from it and joined back
 // before the run ends: the blocks of one chain's launches fill the CUs
 // that the others' leave idle (a launch's tail, tiles that take longer than
-// the rest).  Each chain starts a stage only once the others have finished
-// the one before: left alone, the chain whose launches reach the hardware
-// queues first keeps the CUs first and pulls ahead, and the other then runs
-// its last stage alone (cfg4 S8 2.37-2.46 ms with 2.7-3.0 ms in 3 runs of 7;
-// with the stage waits 2.41-2.42 ms in every run).  The launch recorder
-// gets one record for the run, on the caller's stream.
+// the rest).  The chains do not wait for each other between stages: such
+// waits kept them in step but cost about 12 us per stage boundary on each
+// chain plus the faster chain's idle time (cfg4 S8 2.35 against 2.25 ms,
+// the median over 8 processes of 18 steps each).  The launch recorder gets
+// one record for the run, on the caller's stream.
 constexpr int kSplitCount = 2 * kChains;
 
 int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
@@ -1823,20 +1817,9 @@ int run_s8_stages(const S8Layout &Lay, hipStream_t st) {
         rc = fail(SMX_ELAUNCH, "s8: fork of the launch chains failed");
     // The chains are enqueued a stage at a time each, so that every chain
     // starts while the host is still enqueuing the others.
-    auto chain_stream = [&](int t) { return t ? f->aux[t - 1] : st; };
-    for (int stage = 1; stage <= 5 && !rc; ++stage) {
-      for (int t = chains - 1; t >= 0 && !rc; --t) {
-        if (set[t].empty()) continue;
-        for (int u = 0; stage > 1 && u < chains && !rc; ++u)
-          if (u != t && !set[u].empty() &&
-              hipStreamWaitEvent(chain_stream(t), f->stage_end[u][stage - 2], 0) != hipSuccess)
-            rc = fail(SMX_ELAUNCH, "s8: stage wait between the launch chains failed");
-        if (!rc) rc = run_s8_set_stage(Lay, set[t], stage, chain_stream(t), flops);
-      }
-      for (int t = 0; stage < 5 && t < chains && !rc; ++t)
-        if (!set[t].empty() && hipEventRecord(f->stage_end[t][stage - 1], chain_stream(t)) != hipSuccess)
-          rc = fail(SMX_ELAUNCH, "s8: stage wait between the launch chains failed");
-    }
+    for (int stage = 1; stage <= 5 && !rc; ++stage)
+      for (int t = chains - 1; t >= 0 && !rc; --t)
+        if (!set[t].empty()) rc = run_s8_set_stage(Lay, set[t], stage, t ? f->aux[t - 1] : st, flops);
     // Join even after a failed launch, so the caller's stream never runs
     // ahead of work already on the other streams.
     for (int t = 1; f && t < chains; ++t)

@@ -110,7 +110,8 @@ def test_staged_calls_in_flight_take_their_own_slots(device):
         _native.adamw(wa, tot, 1e-3, 0.9, 0.95, 1e-8, 0.1, device)
         _native.stats_finish(fb, 0.97, device, stage)
         _native.adamw(wb, tot, 1e-3, 0.9, 0.95, 1e-8, 0.1, device, stage)
-    assert len(stage.slots) == 6  # every staged call still in flight took a slot of its own
+    # every staged call is still in flight, each in a slot of its own
+    assert sum(1 for sl in stage.slots if sl[2] is not None and not sl[2].query()) == 6
     torch.cuda.synchronize()
     for fa, fb, a, b, wa, wb, wta, wtb, tot in cases:
         for ta, tb in zip(a, b):
@@ -119,3 +120,27 @@ def test_staged_calls_in_flight_take_their_own_slots(device):
         for ta, tb in zip(wta, wtb):
             for x, y in zip(ta, tb):
                 assert torch.equal(x, y)
+
+
+@pytest.mark.gpu
+def test_descriptor_stage_allocates_once_for_tables_that_fit(device):
+    # All slots are allocated at the first staged call, at one size (a
+    # power of two of at least 256 KiB); later calls whose tables fit take
+    # those slots and allocate nothing; a larger table replaces all slots by
+    # larger ones once.
+    stage = _native.DescriptorStage(device)
+    slot = stage.take(10_000)
+    stage.done(slot)
+    assert len(stage.slots) == stage.MAX_SLOTS and stage.size == 1 << 18
+    tables = {sl[0].data_ptr() for sl in stage.slots}
+    pinned = {sl[1].data_ptr() for sl in stage.slots}
+    for n in (100, 90_000, 1 << 18, 5000) * 5:
+        slot = stage.take(n)
+        stage.done(slot)
+    assert {sl[0].data_ptr() for sl in stage.slots} == tables
+    assert {sl[1].data_ptr() for sl in stage.slots} == pinned
+    slot = stage.take((1 << 18) + 1)
+    stage.done(slot)
+    assert stage.size == 1 << 19 and len(stage.slots) == stage.MAX_SLOTS
+    assert all(sl[0].numel() == 1 << 19 and sl[1].numel() == 1 << 19 for sl in stage.slots)
+    torch.cuda.synchronize()
