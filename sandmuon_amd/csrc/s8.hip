@@ -189,7 +189,6 @@ static int g_tile_policy = 0;
 
 constexpr int kSubN = 2;            // 32x32 MFMA column tiles per wave (64 columns)
 constexpr int kBK = 16;             // K per pipeline stage
-constexpr int kStages = 3;          // LDS ring depth (2 stages in flight)
 
 // Block tile geometries.  Each wave computes 32 kSubM x 64 outputs
 // (kSubM x kSubN MFMA 32x32 tiles); the waves of a block are 2 x kWavesN.
@@ -214,6 +213,9 @@ struct Geo {
   static constexpr int kOpA = TM * kBK * 4;       // A operand tile TM x 16 (4 bytes per element)
   static constexpr int kOpB = TN * kBK * 4;       // B operand tile TN x 16
   static constexpr int kStageBytes = kOpA + kOpB;
+  // LDS ring depth (kStages - 1 stages in flight): 3 where two or three
+  // blocks share a CU's LDS, 4 for the one 256 x 256 block per CU.
+  static constexpr int kStages = TN == 256 ? 4 : 3;
   static constexpr int kRingBytes = kStages * kStageBytes;
   static constexpr int kLoadsA = kOpA / 1024 / kWaves;  // 1 KB loads per wave
   static constexpr int kLoadsB = kOpB / 1024 / kWaves;
@@ -736,7 +738,13 @@ __device__ __forceinline__ void issue_stage(const Opnd &A, const Opnd &B, const 
 template <class G>
 __device__ __forceinline__ void wait_stages(int pending) {
   constexpr int L = G::kLoadsPerStage;
-  static_assert(kStages == 3, "at most two stages in flight");
+  static_assert(G::kStages == 3 || G::kStages == 4, "at most three stages in flight");
+  if constexpr (G::kStages == 4) {
+    if (pending >= 3) {
+      wait_vm<3 * L>();
+      return;
+    }
+  }
   if (pending >= 2) wait_vm<2 * L>();
   else if (pending == 1) wait_vm<L>();
   else wait_vm<0>();
@@ -752,7 +760,7 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 // B[:K, brow0..]), geometry G.
 //
 // Two pipelines overlap the MFMAs:
-//  * a ring of kStages LDS slots filled by direct-to-LDS loads, kStages
+//  * a ring of G::kStages LDS slots filled by direct-to-LDS loads, kStages
 //    stages ahead of the fragment reads;
 //  * register fragments: while the MFMAs of stage kt run, the fragments of
 //    stage kt+1 are read from LDS (B into the other buffer up front, each A
@@ -772,7 +780,7 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Wa
                                           uint32_t lds0, float sel_s, char *smem, int kt, int nk, int wm, int wn,
                                           AFrag<MODE> (&af)[G::kSubM], BFrags<MODE> (&bf)[2],
                                           f32x16 (&acc)[G::kSubM][kSubN]) {
-  constexpr int S = kStages;
+  constexpr int S = G::kStages;
   const bool more = STEADY || kt + 1 < nk;
   if constexpr (STEADY) {
     wait_vm<(S - 2) * G::kLoadsPerStage>();
@@ -835,9 +843,9 @@ __device__ __forceinline__ void gemm_tile(const Opnd &A_in, const Opnd &B_in, in
   // LDS byte address of the ring plus this wave's first A chunk.
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * G::kLoadsA * 1024;
 #pragma unroll
-  for (int s = 0; s < kStages; ++s)
+  for (int s = 0; s < G::kStages; ++s)
     if (s < nk) issue_stage<G, BKM, kU>(A, B, o, static_cast<int64_t>(s) * kBK, lds0 + s * G::kStageBytes);
-  wait_stages<G>(min(kStages - 1, nk - 1));
+  wait_stages<G>(min(G::kStages - 1, nk - 1));
   block_barrier();
   AFrag<MODE> af[kSubM];
   BFrags<MODE> bf[2];
@@ -848,7 +856,7 @@ __device__ __forceinline__ void gemm_tile(const Opnd &A_in, const Opnd &B_in, in
   pipe_iter<MODE, G, SEL, PAR, STEADY, BKM>(A, B, o, bl, lds0, sel_s, smem, KT, nk, wm, wn, af, bf, acc)
   // Stages [kt, to) in pairs (kt and `to` even): branch-free while a refill
   // is due, then the general form.
-  const int steady_end = nk - kStages;
+  const int steady_end = nk - G::kStages;
   auto run = [&](int &kt, int to) {
     for (; kt + 1 < min(to, steady_end); kt += 2) {
       SMX_PIPE(-1, 0, kt, true);
