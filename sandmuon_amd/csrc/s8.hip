@@ -268,6 +268,15 @@ struct Opnd {
 __device__ __forceinline__ int swz4(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 __device__ __forceinline__ int f32_off(int r, int kc) { return (r * 4 + (kc ^ swz4(r))) << 4; }
 
+// Bits 2 and 3 of a row (or column) index within a 32-row fragment block,
+// swapped.  The B fragments are read with this permutation of their 32 rows,
+// so that in the accumulator of C^T = B A^T (the operands of every MFMA
+// are passed B first) register 4 k + q of lane (r, h) holds column
+// 16 (k >> 1) + 8 h + 4 (k & 1) + q of row r: each lane holds 8
+// consecutive columns of each 16-column K group of its row, which the
+// epilogue stores directly as row vectors.
+__device__ __forceinline__ int sw23(int p) { return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1); }
+
 // One 16-byte direct-to-LDS load per lane from sbase + voff (scalar base,
 // per-lane 32-bit byte offset): lane l writes LDS[m0 + 16 l].  Issued from
 // asm so the compiler does not treat later LDS reads as aliasing the
@@ -490,7 +499,7 @@ __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) 
   const char *bt = st + G::kOpA;
 #pragma unroll
   for (int j = 0; j < kSubN; ++j) {
-    const int r = wn * (32 * kSubN) + j * 32 + lr;
+    const int r = wn * (32 * kSubN) + j * 32 + sw23(lr);
     if constexpr (MODE != SMX_S8_FP32) {
       f.h[j] = read_b16(bt, r, lh);
       if constexpr (two_chunks<MODE>()) f.l[j] = read_b16(bt, r, 2 + lh);
@@ -501,20 +510,24 @@ __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) 
 }
 
 // The four B column blocks of one stage from a K-major tile (apply).  Lane
-// (n, h) needs B[k = 8h .. 8h+7][n].  Interleaved BF16: per plane, two
-// transposed reads of 4 K rows each; lane s of a 16-lane group g addresses
-// row 8 (g >> 1) + 4 r + (s >> 2), columns 16 (g & 1) + 4 (s & 3) .. + 3 of
-// the 32-column block, so lane 16 (g & 1) + s of the block receives its
-// column at the 4 rows.  Column block j of wave wn is pieces 4 wn + 2 j and
-// 4 wn + 2 j + 1 (g & 1 picks one), logical chunk 2 plane + ((s >> 1) & 1),
-// byte 8 (s & 1) of it.  The swizzle of rows k and k + 4 is the same, and
-// its piece term is g & 1, so the per-lane offsets (wn included) are one per
-// plane (o[plane][0]) and every read adds a constant.  FP16: lane s of group
-// g addresses row 8 (g >> 1) + (s >> 2) (+4 for the second read, + the
-// second row block's pieces for the second 16 K), columns 16 (g & 1) +
-// 4 (s & 3) .. + 3 of piece 2 wn + j (32 columns), i.e. chunk 2 (g & 1) +
-// ((s >> 1) & 1); o[j][0] holds the offset of block j.  FP32: eight
-// 4-byte reads.
+// (n, h) needs B[k = 8h .. 8h+7][sw23(n)] (the permuted fragment rows of
+// sw23).  Interleaved BF16: per plane, two transposed reads of 4 K rows
+// each; lane s of a 16-lane group g addresses row 8 (g >> 1) + 4 r +
+// (s >> 2), columns 16 (g & 1) + 4 c .. + 3 of the 32-column block with
+// c = sw23(4 (s & 3)) / 4 (the two bits of s & 3 swapped), so lane
+// 16 (g & 1) + 4 a + b of the block receives column 16 (g & 1) + 4 c(a) + b
+// = sw23 of its index at the 4 rows.  Column block j of wave wn is pieces
+// 4 wn + 2 j and 4 wn + 2 j + 1 (g & 1 picks one), logical chunk 2 plane +
+// (c >> 1) = 2 plane + (s & 1), byte 8 (c & 1) = 8 ((s >> 1) & 1) of it.
+// The swizzle of rows k and k + 4 is the same, and its piece term is g & 1,
+// so the per-lane offsets (wn included) are one per plane (o[plane][0]) and
+// every read adds a constant.  FP16: lane s of group g addresses row
+// 8 (g >> 1) + (s >> 2) (+4 for the second read, + the second row block's
+// pieces for the second 16 K), columns 16 (g & 1) + 4 c .. + 3 of piece
+// 2 wn + j (32 columns), i.e. chunk 2 (g & 1) + (s & 1), byte
+// 8 ((s >> 1) & 1); o[j][0] holds the offset of block j.  FP32: eight
+// 4-byte reads.  (The 16 lanes of a read address the same bytes as with
+// unpermuted columns, in another lane order: the same banks.)
 struct BkmLane {
   uint32_t o[2][2];
 };
@@ -526,8 +539,8 @@ __device__ __forceinline__ BkmLane bkm_lane(int wn) {
   BkmLane L;
 #pragma unroll
   for (int pl = 0; pl < 2; ++pl) {
-    L.o[pl][0] = static_cast<uint32_t>((4 * wn + (g & 1)) * 1024 + k * 64 + 8 * (s & 1) +
-                                       (((2 * pl + ((s >> 1) & 1)) ^ sw) << 4));
+    L.o[pl][0] = static_cast<uint32_t>((4 * wn + (g & 1)) * 1024 + k * 64 + 8 * ((s >> 1) & 1) +
+                                       (((2 * pl + (s & 1)) ^ sw) << 4));
     L.o[pl][1] = 0;
   }
   return L;
@@ -541,8 +554,8 @@ __device__ __forceinline__ BkmLane bkm_lane_f16(int wn) {
   BkmLane L;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    L.o[j][0] = static_cast<uint32_t>((2 * wn + j) * 1024 + k * 64 + 8 * (s & 1) +
-                                      (((2 * (g & 1) + ((s >> 1) & 1)) ^ sw) << 4));
+    L.o[j][0] = static_cast<uint32_t>((2 * wn + j) * 1024 + k * 64 + 8 * ((s >> 1) & 1) +
+                                      (((2 * (g & 1) + (s & 1)) ^ sw) << 4));
     L.o[j][1] = 0;
   }
   return L;
@@ -591,10 +604,10 @@ __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &
       }
     }
   } else {
-    // Lane (n, h), n = 64 wn + 32 j + (lane & 31): piece 4 wn + 2 j +
-    // ((lane >> 4) & 1), element 4 ((lane >> 2) & 3) + (lane & 3) of rows
-    // 8 h + q (no swizzle).
-    const char *base = bt + (4 * wn + ((lane >> 4) & 1)) * 1024 + 512 * (lane >> 5) + 4 * (lane & 15);
+    // Lane (n, h), n = 64 wn + 32 j + sw23(lane & 31): piece 4 wn + 2 j +
+    // ((lane >> 4) & 1), element sw23(lane & 15) of rows 8 h + q (no
+    // swizzle).
+    const char *base = bt + (4 * wn + ((lane >> 4) & 1)) * 1024 + 512 * (lane >> 5) + 4 * sw23(lane & 15);
 #pragma unroll
     for (int j = 0; j < kSubN; ++j)
 #pragma unroll
@@ -614,25 +627,26 @@ __device__ __forceinline__ f16x8 as_f16(bf16x8 v) { return __builtin_bit_cast(f1
 // MFMAs of row block i: acc[i][j] += A_i B_j^T over the stage's K.
 template <int MODE>
 __device__ __forceinline__ void mma_row(const AFrag<MODE> &a, const BFrags<MODE> &b, f32x16 (&acc)[kSubN]) {
+  // (B first: the accumulator holds C^T = B A^T, lane r of it row r of C.)
   if constexpr (is_comp(MODE)) {
     // Corrections first, then hi*hi.
 #pragma unroll
-    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.l[j], acc[j], 0, 0, 0);
+    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b.l[j], a.h, acc[j], 0, 0, 0);
 #pragma unroll
-    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.l, b.h[j], acc[j], 0, 0, 0);
+    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b.h[j], a.l, acc[j], 0, 0, 0);
 #pragma unroll
-    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.h[j], acc[j], 0, 0, 0);
+    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b.h[j], a.h, acc[j], 0, 0, 0);
   } else if constexpr (MODE == kS8HiOnly) {
 #pragma unroll
-    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.h, b.h[j], acc[j], 0, 0, 0);
+    for (int j = 0; j < kSubN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b.h[j], a.h, acc[j], 0, 0, 0);
   } else if constexpr (MODE == kS8F16) {
     // K 0-15, then K 16-31 of the stage.
 #pragma unroll
     for (int j = 0; j < kSubN; ++j)
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(a.h), as_f16(b.h[j]), acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(b.h[j]), as_f16(a.h), acc[j], 0, 0, 0);
 #pragma unroll
     for (int j = 0; j < kSubN; ++j)
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(a.l), as_f16(b.l[j]), acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(b.l[j]), as_f16(a.l), acc[j], 0, 0, 0);
   } else {
     // Lane half h supplies k = 8h + q to MFMA q (the same permutation for
     // both operands, so every k is paired exactly once).
@@ -640,7 +654,7 @@ __device__ __forceinline__ void mma_row(const AFrag<MODE> &a, const BFrags<MODE>
     for (int q = 0; q < 8; ++q)
 #pragma unroll
       for (int j = 0; j < kSubN; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.v[q], b.v[j][q], acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b.v[j][q], a.v[q], acc[j], 0, 0, 0);
   }
 }
 
@@ -696,17 +710,17 @@ __device__ __forceinline__ void mma_one_hot(float s, int sel, const BFrags<MODE>
     const AFrag<MODE> o0 = one_hot<MODE>(s, 0), o1 = one_hot<MODE>(s, 16);
 #pragma unroll
     for (int j = 0; j < kSubN; ++j) {
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(o0.h), as_f16(b.h[j]), acc[j], 0, 0, 0);
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(o0.l), as_f16(b.h[j]), acc[j], 0, 0, 0);
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(o1.h), as_f16(b.l[j]), acc[j], 0, 0, 0);
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(o1.l), as_f16(b.l[j]), acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(b.h[j]), as_f16(o0.h), acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(b.h[j]), as_f16(o0.l), acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(b.l[j]), as_f16(o1.h), acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16(b.l[j]), as_f16(o1.l), acc[j], 0, 0, 0);
     }
   } else if constexpr (MODE == kS8HiOnly) {
     const AFrag<MODE> o = one_hot<MODE>(s, (sel & 1) * 16);
 #pragma unroll
     for (int j = 0; j < kSubN; ++j) {
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o.h, b.h[j], acc[j], 0, 0, 0);
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o.l, b.h[j], acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b.h[j], o.h, acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b.h[j], o.l, acc[j], 0, 0, 0);
     }
   } else {
     mma_row<MODE>(one_hot<MODE>(s, (sel & 1) * 16), b, acc);
@@ -1115,9 +1129,13 @@ s8_stage_kernel(StageArgs args) {
   }
 
   // ------------------------------------------------------- epilogue ---
-  // Each 32x32 accumulator block goes through wave-private LDS in both
-  // orientations (T row-major, U column-major), so that the tile and its
-  // transpose are written as row vectors of 8 elements per lane.
+  // Each lane holds, per 32x32 accumulator block, 8 consecutive columns of
+  // each 16-column K group of one row (sw23), which it stores directly as
+  // row vectors: 16 bytes per store, the two lanes of a row 32 contiguous
+  // bytes of it.  A transposed output (the mirror of an off-diagonal
+  // symmetric tile, the stage-5 result of a transposed parameter) goes
+  // through wave-private LDS: written by column, read back as rows of 8
+  // elements per lane.
   //   GRAM    tile -> G, transpose -> G (halves of off-diagonal blocks)
   //   SQUARE  stage 1: G2 (FP32) -> p; stage k: P = c acc + a I -> p
   //   APPLY   tile -> X' (stage 5, transposed parameter: transpose -> xf)
@@ -1163,8 +1181,8 @@ s8_stage_kernel(StageArgs args) {
   const bool tiled_t = !(PHASE == kApply && last && (ref.op == kOpApplyX || ref.op == kOpApplyFinal));
   const bool tiled_m = PHASE != kApply;
   const bool eye = PHASE == kSquare && stage != 1;  // add a I on the diagonal
-  float *const T = reinterpret_cast<float *>(smem) + wave * 2 * kEpBlock;
-  float *const U = T + kEpBlock;
+  // the wave's staging block of a transposed output: [column][row]
+  float *const U = reinterpret_cast<float *>(smem) + wave * 2 * kEpBlock;
   float sq_local = 0.f;
   // The stage-5 result of the matrix step: per parameter row, partial sums
   // of Q z, (a Q)^2 and (a Q)(a z) over the wave's strip of parameter
@@ -1187,7 +1205,8 @@ s8_stage_kernel(StageArgs args) {
     }
     __syncthreads();
   }
-  // Read-back: 8 lanes per row of a 32 x 32 block, each the 16-byte chunk
+  // Read-back of a staged (transposed) block: 8 lanes per row of a 32 x 32
+  // block, each the 16-byte chunk
   // `ech` of the row's 128 bytes (32 columns), so that every store
   // instruction writes 8 whole rows of the block: full 128-byte lines (a
   // burst of such stores runs 25% faster than one of 32-byte pieces).  In
@@ -1293,41 +1312,123 @@ s8_stage_kernel(StageArgs args) {
       if (acc_r) accum4(w, gc0 + ec4, r);
     }
   };
+  // The lane's 16 values w of row gr, columns cb + col16(e) (cb a multiple
+  // of 32), stored in form FM: tiled FP32, planes and FP16 put each K group's
+  // 8 columns of the lane at their place in the group's row (planes: 16
+  // bytes of hi at 16 lh, 16 of lo at 32 + 16 lh; FP16: 16 bytes at
+  // 16 lh of the 32-column piece's half g); row-major FP32 (the stage-5
+  // result) as 16-byte column quads.
+  auto put_direct = [&](auto fm_c, const float (&w)[16], int64_t gr, int64_t cb, float *dst, int64_t ld, bool tl) {
+    constexpr int FM = decltype(fm_c)::value;
+    char *const out = reinterpret_cast<char *>(dst);
+    if constexpr (FM == kFormF16) {
+      const int64_t base = (gr & ~int64_t{15}) * (2 * ld) + ((gr & 15) << 6) + 32 * cb + 16 * lh;
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        uint32_t b[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          b[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(w[8 * g + 2 * e]))) |
+                 (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(w[8 * g + 2 * e + 1])))
+                  << 16);
+        *reinterpret_cast<uint4 *>(out + base + 32 * g) = make_uint4(b[0], b[1], b[2], b[3]);
+      }
+      return;
+    }
+    const bool pl = FM == kFormPlanes || (FM == kFormAny && form == kFormPlanes);
+    if (pl) {
+      const int64_t base = (gr & ~int64_t{15}) * (4 * ld) + ((gr & 15) << 6) + 64 * cb + 16 * lh;
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          h[e] = bf16_bits(w[8 * g + 2 * e]) | (static_cast<uint32_t>(bf16_bits(w[8 * g + 2 * e + 1])) << 16);
+          l[e] = bf16_lo_bits(w[8 * g + 2 * e]) | (static_cast<uint32_t>(bf16_lo_bits(w[8 * g + 2 * e + 1])) << 16);
+        }
+        *reinterpret_cast<uint4 *>(out + base + 1024 * g) = make_uint4(h[0], h[1], h[2], h[3]);
+        *reinterpret_cast<uint4 *>(out + base + 1024 * g + 32) = make_uint4(l[0], l[1], l[2], l[3]);
+      }
+    } else {
+      // column 16 g + 8 lh + 4 h: tiled, byte 64 (that column & 15) of its
+      // K group's row; row-major, byte 4 column of the row
+      const int64_t base = tl ? (gr & ~int64_t{15}) * (4 * ld) + ((gr & 15) << 6) + 64 * cb + 32 * lh
+                              : gr * (4 * ld) + 4 * (cb + 8 * lh);
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int e = 8 * g + 4 * h;
+          *reinterpret_cast<float4 *>(out + base + (tl ? 1024 * g + 16 * h : 4 * (16 * g + 4 * h))) =
+              make_float4(w[e], w[e + 1], w[e + 2], w[e + 3]);
+        }
+    }
+  };
+  // Register e of a block holds column col16(e) of the lane's row.
+  auto col16 = [&](int e) { return 16 * (e >> 3) + 8 * lh + (e & 7); };
   // The block loop, specialised for the output form (one copy per form the
   // launch's mode can produce, so that each keeps only its own registers).
   auto epilogue = [&](auto fm_c) {
     constexpr int FM = decltype(fm_c)::value;
     // the row sums come with the FP32 result only (rsum implies it)
     const bool rs_on = (FM == kFormF32 || FM == kFormAny) && rsum;
+    // Row sums of the lane's row over the wave's strip (its kSubN blocks),
+    // for a parameter that is not transposed.
+    float rsd[3] = {0.f, 0.f, 0.f};
     // (expanded at compile time: a rolled block loop indexes acc at run
     // time, which moves every accumulator of the kernel to scratch memory)
     static_for<kSubM * kSubN>([&](auto blk_c) {
       constexpr int blk = decltype(blk_c)::value, i = blk / kSubN, j = blk % kSubN;
+      const int64_t gr = R0 + i * 32 + lr, cb = C0 + j * 32;
+      float w[16];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        f32x4 v;
+      for (int e = 0; e < 16; ++e) {
+        w[e] = acc[i][j][e] * scale;
+        // stage 1's FP32 G2: its squared entries feed the Schatten scale
+        if constexpr (PHASE == kSquare && (FM == kFormF32 || FM == kFormAny)) sq_local = fmaf(w[e], w[e], sq_local);
+        if (do_m) U[col16(e) * kEpStride + lr] = w[e];
+      }
+      if (do_t) {
+        if (eye)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (gr == cb + col16(e) && gr < K.r) w[e] += args.a;
+        put_direct(fm_c, w, gr, cb, dst_t, ld_t, tiled_t);
+        if (rs_on) {
+          // a and z of the lane's columns, then the row's two lanes (lh)
+          const int o = static_cast<int>(cb - rs_c0) + 8 * lh;
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4) {
+            const int oc = o + 16 * (e4 >> 1) + 4 * (e4 & 1);
+            const f32x4 a4 = *reinterpret_cast<const f32x4 *>(colv_lds + oc);
+            const f32x4 z4 = *reinterpret_cast<const f32x4 *>(colv_lds + rs_w + oc);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float x = w[4 * e4 + e], aw = a4[e] * x;
+              rsd[0] = fmaf(x, z4[e], rsd[0]);
+              rsd[1] = fmaf(aw, aw, rsd[1]);
+              rsd[2] = fmaf(aw, a4[e] * z4[e], rsd[2]);
+            }
+          }
+          if (j == kSubN - 1) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) rsd[k] += __shfl_xor(rsd[k], 32);
+            if (lh == 0)
+#pragma unroll
+              for (int k = 0; k < 3; ++k) M.mrp(k)[(C0 / kStripT) * prows + gr] = rsd[k];
+#pragma unroll
+            for (int k = 0; k < 3; ++k) rsd[k] = 0.f;
+          }
+        }
+      }
+      if (do_m) {
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          v[q] = acc[i][j][4 * k + q] * scale;
-          // stage 1's FP32 G2: its squared entries feed the Schatten scale
-          if constexpr (PHASE == kSquare && (FM == kFormF32 || FM == kFormAny)) sq_local = fmaf(v[q], v[q], sq_local);
-          T[(8 * k + 4 * lh + q) * kEpStride + lr] = v[q];
-        }
-        if (do_m) *reinterpret_cast<f32x4 *>(U + lr * kEpStride + 8 * k + 4 * lh) = v;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int row = er + 8 * q;
-        if (do_t) {
-          const int64_t gr = R0 + i * 32 + row;
-          put_row(fm_c, T, row, gr, C0 + j * 32, dst_t, ld_t, tiled_t, rs[0][q], rs_on);
-          if (rs_on && j == kSubN - 1) emit(gr, C0 / kStripT, rs[0][q]);
-        }
-        if (do_m) {
-          const int64_t gr = C0 + j * 32 + row;
-          put_row(fm_c, U, row, gr, R0 + i * 32, dst_m, ld_m, tiled_m, rs[j][q], rs_on);
-          if (rs_on && i == kSubM - 1) emit(gr, R0 / kStripM, rs[j][q]);
+          const int row = er + 8 * q;
+          const int64_t gm = cb + row;
+          put_row(fm_c, U, row, gm, R0 + i * 32, dst_m, ld_m, tiled_m, rs[j][q], rs_on);
+          if (rs_on && i == kSubM - 1) emit(gm, R0 / kStripM, rs[j][q]);
         }
       }
       // Keep the scheduler from hoisting every accumulator read to the top
@@ -1596,7 +1697,12 @@ static int pick_geo(const S8Layout &Lay, int phase, const std::vector<Seg> &segs
     const int64_t cnt = sg.hi - sg.lo;
     for (int g = 0; g < 3; ++g) tiles[g] += cnt * phase_tiles(k, phase, g, sg.op);
   }
-  if (g_tile_policy == 0 && 2 * tiles[kGeoL] >= 3 * cus) return kGeoL;
+  {
+    static int thr_apply = getenv("SMX_XL_APPLY") ? atoi(getenv("SMX_XL_APPLY")) : 15;
+    static int thr_other = getenv("SMX_XL_OTHER") ? atoi(getenv("SMX_XL_OTHER")) : 15;
+    const int thr = phase == kApply ? thr_apply : thr_other;
+    if (g_tile_policy == 0 && 10 * tiles[kGeoL] >= thr * cus) return kGeoL;
+  }
   if (small_ok) {
     const double r_m = static_cast<double>(ceil_div(tiles[kGeoM], 2 * cus));
     const double r_s = static_cast<double>(ceil_div(tiles[kGeoS], 3 * cus));

@@ -32,6 +32,11 @@ def swzt_h(row):
     return 2 * ((row >> 1) & 1)
 
 
+def sw23(p):
+    """s8.hip sw23: bits 2 and 3 of a fragment row index swapped."""
+    return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1)
+
+
 def plane_hi(idx):
     return 2 * (idx & ~15) + (idx & 15)
 
@@ -164,14 +169,14 @@ def test_k_major_planes_reads(tn, waves):
         def lane_off(lane, pl):
             g, s = lane >> 4, lane & 15
             k = 8 * (g >> 1) + (s >> 2)
-            return (4 * wn + (g & 1)) * 1024 + k * 64 + 8 * (s & 1) + (((2 * pl + ((s >> 1) & 1)) ^ swzt(k, g & 1)) << 4)
+            return (4 * wn + (g & 1)) * 1024 + k * 64 + 8 * ((s >> 1) & 1) + (((2 * pl + (s & 1)) ^ swzt(k, g & 1)) << 4)
         for j in range(2):
             for pl in range(2):
                 for second in range(2):
                     addr_of = lambda sl: lane_off(sl, pl) + 2048 * j + 256 * second
                     got = tr16(lds, addr_of)
                     for lane in range(64):
-                        n, h = 64 * wn + 32 * j + (lane & 31), lane >> 5
+                        n, h = 64 * wn + 32 * j + sw23(lane & 31), lane >> 5
                         want = [("hi" if pl == 0 else "lo", k0 + 8 * h + 4 * second + t, n0 + n) for t in range(4)]
                         assert got[lane] == want
                     assert conflicts(addr_of, 16, 32) == 0 and conflicts(addr_of, 32, 64) == 0
@@ -188,14 +193,14 @@ def test_k_major_f16_reads(tn, waves):
         def lane_off(lane, j):
             g, s = lane >> 4, lane & 15
             k = 8 * (g >> 1) + (s >> 2)
-            return (2 * wn + j) * 1024 + k * 64 + 8 * (s & 1) + (((2 * (g & 1) + ((s >> 1) & 1)) ^ swzt_h(k)) << 4)
+            return (2 * wn + j) * 1024 + k * 64 + 8 * ((s >> 1) & 1) + (((2 * (g & 1) + (s & 1)) ^ swzt_h(k)) << 4)
         for j in range(2):
             for half in range(2):
                 for second in range(2):
                     addr_of = lambda sl: lane_off(sl, j) + half * block_bytes + 256 * second
                     got = tr16(lds, addr_of)
                     for lane in range(64):
-                        n, h = 64 * wn + 32 * j + (lane & 31), lane >> 5
+                        n, h = 64 * wn + 32 * j + sw23(lane & 31), lane >> 5
                         want = [("x", k0 + 16 * half + 8 * h + 4 * second + t, n0 + n) for t in range(4)]
                         assert got[lane] == want
                     assert conflicts(addr_of, 16, 32) == 0 and conflicts(addr_of, 32, 64) == 0
@@ -203,22 +208,23 @@ def test_k_major_f16_reads(tn, waves):
 
 @pytest.mark.parametrize("tn,waves", [(128, 4), (256, 8)])
 def test_k_major_f32_reads(tn, waves):
-    """load_b_km (FP32): lane (n, h) reads B[k0 + 8h + q][n] at
-    (4 wn + pp) KB + 512 h + 4 (lane & 15) + 2 KB j + 64 q."""
+    """load_b_km (FP32): lane (n, h) reads B[k0 + 8h + q][n] (n the
+    permuted column sw23) at (4 wn + pp) KB + 512 h + 4 sw23(lane & 15) +
+    2 KB j + 64 q."""
     ld, k0, n0 = 512, 32, tn
     lds = km_stage("f32", tn, waves, ld, k0, n0)
     for wn in range(tn // 64):
         for lane in range(64):
-            base = (4 * wn + ((lane >> 4) & 1)) * 1024 + 512 * (lane >> 5) + 4 * (lane & 15)
+            base = (4 * wn + ((lane >> 4) & 1)) * 1024 + 512 * (lane >> 5) + 4 * sw23(lane & 15)
             for j in range(2):
                 for q in range(8):
-                    n, k = 64 * wn + 32 * j + (lane & 31), 8 * (lane >> 5) + q
+                    n, k = 64 * wn + 32 * j + sw23(lane & 31), 8 * (lane >> 5) + q
                     assert lds[base + 2048 * j + 64 * q] == ("f", k0 + k, n0 + n)
 
 
 @pytest.mark.parametrize("form", ["planes", "f32", "f16"])
-def test_epilogue_stores_address_tiled_elements(form):
-    """put_row: lane ech of the 8 lanes of output row gr writes chunk ech of
+def test_epilogue_staged_stores_address_tiled_elements(form):
+    """put_row (transposed outputs, staged in LDS): lane ech of the 8 lanes of output row gr writes chunk ech of
     columns gc0 .. gc0 + 31 at (gr & ~15) 4 ld + (gr & 15) 64 + 64 gc0 +
     1024 (ech >> 2) + 16 (ech & 3) (FP16: (gr & ~15) 2 ld + (gr & 15) 64 +
     32 gc0 + 8 ech); those are the bytes tiled_index gives its elements, and
@@ -247,3 +253,80 @@ def test_epilogue_stores_address_tiled_elements(form):
                         assert [mem[off + 2 * e] for e in range(8)] == [(plane, gr, c) for c in cols]
                     spans.add(off // 512)
             assert len(spans) == (1 if form == "f16" else 2)
+
+
+def col16(e, lh):
+    """s8.hip col16: the column of register e of a lane of half lh."""
+    return 16 * (e >> 3) + 8 * lh + (e & 7)
+
+
+def test_swapped_mfma_layout_puts_consecutive_columns_in_a_lane():
+    """The MFMAs take the B fragment first, so the accumulator is
+    D = Bfrag A^T: register e of lane l holds D[8 (e >> 2) + 4 (l >> 5) +
+    (e & 3)][l & 31] (the 32x32 MFMA output layout), and D[p][m] =
+    C[m][sw23(p)] because lane p of the B fragment holds B row sw23(p).
+    So register e of lane (r, h) holds C[r][col16(e)]: 8 consecutive columns
+    of each 16-column K group per lane, every column of the block once
+    per row."""
+    for lane in range(64):
+        r, lh = lane & 31, lane >> 5
+        cols = []
+        for e in range(16):
+            p = 8 * (e >> 2) + 4 * lh + (e & 3)
+            assert sw23(p) == col16(e, lh)
+            cols.append(sw23(p))
+        assert cols[:8] == list(range(8 * lh, 8 * lh + 8))
+        assert cols[8:] == list(range(16 + 8 * lh, 16 + 8 * lh + 8))
+    assert sorted(col16(e, h) for h in range(2) for e in range(16)) == list(range(32))
+
+
+@pytest.mark.parametrize("form", ["planes", "f32", "f32_rowmajor", "f16"])
+def test_epilogue_direct_stores_address_tiled_elements(form):
+    """put_direct: lane (r, h) stores its 16 values of row gr = R + r,
+    columns cb + col16(e); every store writes 16 bytes that are exactly the
+    bytes of those elements (tiled_index, planes hi/lo, FP16 32-column
+    pieces, or row-major FP32), and the block's 32 x 32 elements are each
+    written once."""
+    ld = 256
+    mem = memory(form if form != "f32_rowmajor" else "f32", 64, ld)
+    if form == "f32_rowmajor":
+        mem = {}
+        for row in range(64):
+            for c in range(ld):
+                for b in range(4):
+                    mem[4 * (row * ld + c) + b] = ("f", row, c)
+    for R in (0, 32):
+        for cb in (0, 32, 224):
+            seen = {}
+            for lane in range(64):
+                r, lh = lane & 31, lane >> 5
+                gr = R + r
+                val = {e: (gr, cb + col16(e, lh)) for e in range(16)}
+                stores = []  # (byte offset, [elements], bytes per element, plane)
+                if form == "f16":
+                    base = (gr & ~15) * 2 * ld + ((gr & 15) << 6) + 32 * cb + 16 * lh
+                    for g in range(2):
+                        stores.append((base + 32 * g, [val[8 * g + e] for e in range(8)], 2, "x"))
+                elif form == "planes":
+                    base = (gr & ~15) * 4 * ld + ((gr & 15) << 6) + 64 * cb + 16 * lh
+                    for g in range(2):
+                        stores.append((base + 1024 * g, [val[8 * g + e] for e in range(8)], 2, "hi"))
+                        stores.append((base + 1024 * g + 32, [val[8 * g + e] for e in range(8)], 2, "lo"))
+                else:
+                    tl = form == "f32"
+                    base = ((gr & ~15) * 4 * ld + ((gr & 15) << 6) + 64 * cb + 32 * lh) if tl else \
+                        gr * 4 * ld + 4 * (cb + 8 * lh)
+                    for g in range(2):
+                        for h in range(2):
+                            e = 8 * g + 4 * h
+                            off = base + (1024 * g + 16 * h if tl else 4 * (16 * g + 4 * h))
+                            stores.append((off, [val[e + t] for t in range(4)], 4, "f"))
+                for off, elems, size, plane in stores:
+                    assert len(elems) * size == 16
+                    for t, (row, col) in enumerate(elems):
+                        assert mem[off + size * t] == (plane, row, col)
+                        key = (plane, row, col)
+                        assert key not in seen
+                        seen[key] = True
+            planes = ("hi", "lo") if form == "planes" else ("x",) if form == "f16" else ("f",)
+            assert sorted(seen) == sorted((p, R + r, cb + c) for p in planes for r in range(32) for c in range(32))
