@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 4
+#define SMX_ABI_VERSION 5
 
 enum smx_status {
   SMX_OK = 0,
@@ -233,19 +233,20 @@ int smx_stats_finish(const smx_finish_desc *descs, int32_t n_desc,
 
 /* smx_stats_finish in one fold and one finish launch for any n_desc (the
  * call above launches one pair per 32 descriptors, which travel by value in
- * the kernel arguments).  The descriptors are checked as there, written to
- * `host_stage` (pinned host memory, e.g. from hipHostMalloc) and copied on
- * `stream` to `dev_table` (device memory), which the kernels read; both
- * hold table_bytes >= smx_stats_finish_table_bytes(n_desc) bytes.  The
- * caller keeps host_stage unchanged until that copy has run (an event
- * recorded on `stream` after the call marks it) and dev_table until the
- * launches have.  No counterpart in the reference (the same
+ * the kernel arguments).  The descriptors are checked as there and written
+ * in order on `stream` to `dev_table` (device memory of table_bytes >=
+ * smx_stats_finish_table_bytes(n_desc) bytes), which the kernels read:
+ * they travel in the kernel arguments of small upload launches (3840 bytes
+ * each), so `descs` may be reused when the call returns and the call never
+ * waits for the device.  The caller keeps dev_table for this call until its
+ * launches have run (an event recorded on `stream` after the call marks
+ * it).  No counterpart in the reference (the same
  * sandmuon/optimizer.py:182-222); for callers with more vectors than one
  * launch of smx_stats_finish takes. */
 size_t smx_stats_finish_table_bytes(int32_t n_desc);
 int smx_stats_finish_staged(const smx_finish_desc *descs, int32_t n_desc,
-                            double beta, void *dev_table, void *host_stage,
-                            size_t table_bytes, void *stream);
+                            double beta, void *dev_table, size_t table_bytes,
+                            void *stream);
 
 /* ------------------------------------------------------------------ *
  * AdamW on the auxiliary parameters: sandmuon/optimizer.py:268-281.
@@ -273,17 +274,17 @@ int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t total,
               double weight_decay, void *stream);
 
 /* smx_adamw in one launch for any n_desc (the call above launches once per
- * 56 descriptors): the descriptors and each block's first tensor are
- * written to `host_stage` (pinned host memory) and copied on `stream` to
- * `dev_table`, both of table_bytes >= smx_adamw_table_bytes(n_desc, total)
- * bytes, with the lifetimes of smx_stats_finish_staged.  No counterpart in
- * the reference (the same sandmuon/optimizer.py:268-281); for models with
- * more auxiliary tensors than one launch of smx_adamw takes. */
+ * 56 descriptors): the descriptors are written to `dev_table` (table_bytes
+ * >= smx_adamw_table_bytes(n_desc, total) bytes) as in
+ * smx_stats_finish_staged, with the same lifetimes, and each block finds
+ * its first tensor in the table.  No counterpart in the reference (the same
+ * sandmuon/optimizer.py:268-281); for models with more auxiliary tensors
+ * than one launch of smx_adamw takes. */
 size_t smx_adamw_table_bytes(int32_t n_desc, int64_t total);
 int smx_adamw_staged(const smx_adamw_desc *descs, int32_t n_desc,
                      int64_t total, double lr, double beta1, double beta2,
                      double eps, double weight_decay, void *dev_table,
-                     void *host_stage, size_t table_bytes, void *stream);
+                     size_t table_bytes, void *stream);
 
 /* ------------------------------------------------------------------ *
  * Matrix update: Nesterov momentum -> whiten -> S8 -> mapback -> graft ->

@@ -17,7 +17,7 @@ from typing import List, Optional, Sequence
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsandmuon_amd.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 SMX_F32, SMX_BF16, SMX_F16, SMX_F64 = 0, 1, 2, 3
 S8_FP32, S8_COMP_BF16, S8_MIXED = 0, 1, 2
@@ -83,13 +83,13 @@ SIGNATURES = {
     "smx_stats_fold": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
     "smx_stats_finish": (c_int, [ctypes.POINTER(FinishDesc), c_int32, c_double, c_void_p]),
     "smx_stats_finish_table_bytes": (c_size_t, [c_int32]),
-    "smx_stats_finish_staged": (c_int, [ctypes.POINTER(FinishDesc), c_int32, c_double, c_void_p, c_void_p,
-                                        c_size_t, c_void_p]),
+    "smx_stats_finish_staged": (c_int, [ctypes.POINTER(FinishDesc), c_int32, c_double, c_void_p, c_size_t,
+                                        c_void_p]),
     "smx_adamw": (c_int, [ctypes.POINTER(AdamwDesc), c_int32, c_int64, c_double, c_double, c_double, c_double,
                           c_double, c_void_p]),
     "smx_adamw_table_bytes": (c_size_t, [c_int32, c_int64]),
     "smx_adamw_staged": (c_int, [ctypes.POINTER(AdamwDesc), c_int32, c_int64, c_double, c_double, c_double,
-                                 c_double, c_double, c_void_p, c_void_p, c_size_t, c_void_p]),
+                                 c_double, c_double, c_void_p, c_size_t, c_void_p]),
     "smx_matrix_step_workspace_bytes": (c_size_t, [ctypes.POINTER(c_int64), ctypes.POINTER(c_int64),
                                                    c_int32, c_int]),
     "smx_matrix_step": (c_int, [ctypes.POINTER(MatrixDesc), c_int32, c_int, c_void_p, c_size_t, c_void_p]),
@@ -321,55 +321,50 @@ ADAMW_BATCH = 56
 
 class DescriptorStage:
     """Device tables for the staged entry points (smx_stats_finish_staged,
-    smx_adamw_staged) and the pinned host memory they are copied from, each
-    slot with an event recorded on the stream after its call.  A slot is
-    reused only once its event has completed, so the host never rewrites
-    pinned memory whose copy is still queued, and the device table of a
-    call stays untouched until that call's kernels have run.  A call takes
-    the first free slot, or waits for the oldest when all MAX_SLOTS are in
+    smx_adamw_staged), each slot with an event recorded on the stream after
+    its call.  The library writes a table in order on the call's stream (the
+    descriptors travel in kernel arguments), so on one stream a table could
+    be reused at once; the events keep a table whose kernels have not run
+    from being rewritten by a call on another stream.  A call takes the
+    first free slot, or waits for the oldest when all MAX_SLOTS are in
     flight, so several staged calls of one step (the finish, an AdamW call
     per parameter group) never wait on each other.
 
     The slots are allocated together and all of one size, a power of two of
-    at least MIN_BYTES that covers the largest table staged so far: a pinned
-    host allocation can wait for the device, and one inside a step stalls
-    the host while the GPU drains its queue, after which the GPU waits for
-    the step's launches (measured: a step whose host work took 7-11 ms
-    instead of 1.6 ms, its S8 run 3.2 ms instead of 2.3).  So a step whose
-    tables fit allocates nothing.  (Under graph capture, where the host
-    cannot wait on an event, the by-value calls are used.)"""
+    at least MIN_BYTES that covers the largest table staged so far, so a
+    step whose tables fit allocates nothing.  (Under graph capture, where the
+    host cannot wait on an event, the by-value calls are used.)"""
 
     MAX_SLOTS = 8
-    MIN_BYTES = 1 << 18
+    MIN_BYTES = 1 << 16
 
     def __init__(self, device: torch.device):
         self.device = device
         self.size = 0
-        self.slots: List[list] = []  # [device table, pinned stage, event], oldest use first
+        self.slots: List[list] = []  # [device table, event], oldest use first
 
     def _grow(self, nbytes: int) -> None:
         for sl in self.slots:  # queued kernels still read these tables
-            if sl[2] is not None:
-                sl[2].synchronize()
+            if sl[1] is not None:
+                sl[1].synchronize()
         self.size = max(self.MIN_BYTES, 1 << (int(nbytes) - 1).bit_length())
-        self.slots = [[torch.empty(self.size, dtype=torch.uint8, device=self.device),
-                       torch.empty(self.size, dtype=torch.uint8, pin_memory=True), None]
+        self.slots = [[torch.empty(self.size, dtype=torch.uint8, device=self.device), None]
                       for _ in range(self.MAX_SLOTS)]
 
     def take(self, nbytes: int):
         if nbytes > self.size:
             self._grow(nbytes)
-        free = [i for i, sl in enumerate(self.slots) if sl[2] is None or sl[2].query()]
+        free = [i for i, sl in enumerate(self.slots) if sl[1] is None or sl[1].query()]
         slot = self.slots.pop(free[0] if free else 0)
         if not free:
-            slot[2].synchronize()
+            slot[1].synchronize()
         self.slots.append(slot)  # most recent use last
         return slot
 
     def done(self, slot) -> None:
         ev = torch.cuda.Event()
         ev.record(torch.cuda.current_stream(self.device))
-        slot[2] = ev
+        slot[1] = ev
 
 
 def stats_finish(descs: Sequence[FinishDesc], beta: float, device: torch.device,
@@ -384,8 +379,8 @@ def stats_finish(descs: Sequence[FinishDesc], beta: float, device: torch.device,
         return
     nbytes = int(lib().smx_stats_finish_table_bytes(len(descs)))
     slot = stage.take(nbytes)
-    _check(lib().smx_stats_finish_staged(arr, len(descs), beta, slot[0].data_ptr(), slot[1].data_ptr(),
-                                         slot[0].numel(), stream_of(device)), "smx_stats_finish_staged")
+    _check(lib().smx_stats_finish_staged(arr, len(descs), beta, slot[0].data_ptr(), slot[0].numel(),
+                                         stream_of(device)), "smx_stats_finish_staged")
     stage.done(slot)
 
 
@@ -403,7 +398,7 @@ def adamw(descs: Sequence[AdamwDesc], total: int, lr: float, beta1: float, beta2
     nbytes = int(lib().smx_adamw_table_bytes(len(descs), total))
     slot = stage.take(nbytes)
     _check(lib().smx_adamw_staged(arr, len(descs), total, lr, beta1, beta2, eps, weight_decay, slot[0].data_ptr(),
-                                  slot[1].data_ptr(), slot[0].numel(), stream_of(device)), "smx_adamw_staged")
+                                  slot[0].numel(), stream_of(device)), "smx_adamw_staged")
     stage.done(slot)
 
 

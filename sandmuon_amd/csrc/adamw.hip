@@ -159,13 +159,20 @@ __global__ void __launch_bounds__(256) adamw_kernel(AdamPack pk) {
   adamw_block(pk.sc, [&](int i) { return pk.d[i]; }, k);
 }
 
-// The same over a table in device memory: descriptors, then the first
-// tensor of every block (one load per block).
-__global__ void __launch_bounds__(256) adamw_table_kernel(AdamScalars sc, const smx_adamw_desc *__restrict__ table,
-                                                          const int32_t *__restrict__ block_first) {
-  // (the index is block-uniform: the descriptor loads are scalar loads)
-  adamw_block(sc, [&](int i) { return table[__builtin_amdgcn_readfirstlane(i)]; },
-              __builtin_amdgcn_readfirstlane(block_first[blockIdx.x]));
+// The same over a descriptor table in device memory.  The block's first
+// tensor is the last one whose offset is <= its first element (offsets are
+// ascending, the first is 0): a binary search over the table, the tensor
+// adamw_kernel's compares find.
+__global__ void __launch_bounds__(256) adamw_table_kernel(AdamScalars sc, const smx_adamw_desc *__restrict__ table) {
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * sc.chunk;
+  int lo = 0, hi = sc.n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    // (the index is block-uniform: the descriptor loads are scalar loads)
+    if (table[__builtin_amdgcn_readfirstlane(mid)].offset <= e0) lo = mid;
+    else hi = mid - 1;
+  }
+  adamw_block(sc, [&](int i) { return table[__builtin_amdgcn_readfirstlane(i)]; }, __builtin_amdgcn_readfirstlane(lo));
 }
 
 }  // namespace smx
@@ -233,42 +240,29 @@ extern "C" int smx_adamw(const smx_adamw_desc *descs, int32_t n_desc, int64_t to
   return SMX_OK;
 }
 
-// Table of smx_adamw_staged: the descriptors, then each block's first
-// tensor (int32).
+// Table of smx_adamw_staged: the descriptors.
 static size_t adamw_table_bytes(int32_t n_desc, int64_t total) {
   if (n_desc <= 0 || total <= 0) return 0;
-  return static_cast<size_t>(n_desc) * sizeof(smx_adamw_desc) +
-         static_cast<size_t>(ceil_div(total, adam_chunk(total))) * sizeof(int32_t);
+  return static_cast<size_t>(n_desc) * sizeof(smx_adamw_desc);
 }
 
 extern "C" size_t smx_adamw_table_bytes(int32_t n_desc, int64_t total) { return adamw_table_bytes(n_desc, total); }
 
 extern "C" int smx_adamw_staged(const smx_adamw_desc *descs, int32_t n_desc, int64_t total, double lr, double beta1,
-                                double beta2, double eps, double weight_decay, void *dev_table, void *host_stage,
-                                size_t table_bytes, void *stream) {
+                                double beta2, double eps, double weight_decay, void *dev_table, size_t table_bytes,
+                                void *stream) {
   if (const int rc = check_adamw_descs(descs, n_desc, total)) return rc;
   if (n_desc == 0 || total == 0) return SMX_OK;
   const size_t need = adamw_table_bytes(n_desc, total);
-  SMX_REQUIRE(dev_table && host_stage && table_bytes >= need, SMX_EWORKSPACE,
-              "adamw_staged: dev_table and host_stage need smx_adamw_table_bytes(n_desc, total) bytes");
+  SMX_REQUIRE(dev_table && table_bytes >= need, SMX_EWORKSPACE,
+              "adamw_staged: dev_table needs smx_adamw_table_bytes(n_desc, total) bytes");
   const AdamScalars sc = adam_scalars(n_desc, total, lr, beta1, beta2, eps, weight_decay);
   const int64_t blocks = ceil_div(total, sc.chunk);
   SMX_REQUIRE(blocks < INT32_MAX, SMX_ESHAPE, "adamw: too many elements for one launch");
-  auto *d = static_cast<smx_adamw_desc *>(host_stage);
-  std::memcpy(d, descs, static_cast<size_t>(n_desc) * sizeof(smx_adamw_desc));
-  // Block b starts at element b * chunk: its first tensor is the last one
-  // whose offset is <= that (the same tensor adamw_kernel's compares find).
-  auto *first = reinterpret_cast<int32_t *>(d + n_desc);
-  int32_t k = 0;
-  for (int64_t b = 0; b < blocks; ++b) {
-    while (k + 1 < n_desc && descs[k + 1].offset <= b * sc.chunk) ++k;
-    first[b] = k;
-  }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  SMX_REQUIRE(hipMemcpyAsync(dev_table, host_stage, need, hipMemcpyHostToDevice, st) == hipSuccess, SMX_ELAUNCH,
-              "adamw_staged: copy of the descriptor table failed");
+  static_assert(sizeof(smx_adamw_desc) % 4 == 0, "the table is uploaded as 32-bit words");
+  if (const int rc = upload_table(dev_table, descs, need, st)) return rc;
   const auto *table = static_cast<const smx_adamw_desc *>(dev_table);
-  hipLaunchKernelGGL(adamw_table_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, sc, table,
-                     reinterpret_cast<const int32_t *>(table + n_desc));
+  hipLaunchKernelGGL(adamw_table_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, sc, table);
   return check_launch("adamw_staged");
 }

@@ -13,6 +13,13 @@ namespace smx {
 void set_error(const std::string &msg);
 int fail(int code, const std::string &msg);
 int check_launch(const char *what);
+// Writes `bytes` (a multiple of 4) from host memory `src` to device memory
+// `dst` in order on `st`, through the kernel arguments of one small launch
+// per 3840 bytes: no host memory is read after the call returns, and the
+// host never waits for the device (a hipMemcpyAsync from pinned memory was
+// seen to block the calling thread for milliseconds, long enough to leave
+// the GPU idle behind it).
+int upload_table(void *dst, const void *src, size_t bytes, hipStream_t st);
 
 #define SMX_REQUIRE(cond, code, msg)                                        \
   do {                                                                      \

@@ -276,6 +276,11 @@ __device__ __forceinline__ int f32_off(int r, int kc) { return (r * 4 + (kc ^ sw
 // consecutive columns of each 16-column K group of its row, which the
 // epilogue stores directly as row vectors.
 __device__ __forceinline__ int sw23(int p) { return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1); }
+// FP32 mode keeps the natural order: its outputs are FP32, whose 16-byte
+// quads of columns 8 k + 4 h .. + 3 already give the two lanes of a row 32
+// contiguous bytes per store.
+template <int MODE>
+__device__ __forceinline__ int frag_row(int p) { return MODE == SMX_S8_FP32 ? p : sw23(p); }
 
 // One 16-byte direct-to-LDS load per lane from sbase + voff (scalar base,
 // per-lane 32-bit byte offset): lane l writes LDS[m0 + 16 l].  Issued from
@@ -499,7 +504,7 @@ __device__ __forceinline__ void load_b(const char *st, int wn, BFrags<MODE> &f) 
   const char *bt = st + G::kOpA;
 #pragma unroll
   for (int j = 0; j < kSubN; ++j) {
-    const int r = wn * (32 * kSubN) + j * 32 + sw23(lr);
+    const int r = wn * (32 * kSubN) + j * 32 + frag_row<MODE>(lr);
     if constexpr (MODE != SMX_S8_FP32) {
       f.h[j] = read_b16(bt, r, lh);
       if constexpr (two_chunks<MODE>()) f.l[j] = read_b16(bt, r, 2 + lh);
@@ -604,10 +609,10 @@ __device__ __forceinline__ void load_b_km(const char *st, int wn, BFrags<MODE> &
       }
     }
   } else {
-    // Lane (n, h), n = 64 wn + 32 j + sw23(lane & 31): piece 4 wn + 2 j +
-    // ((lane >> 4) & 1), element sw23(lane & 15) of rows 8 h + q (no
-    // swizzle).
-    const char *base = bt + (4 * wn + ((lane >> 4) & 1)) * 1024 + 512 * (lane >> 5) + 4 * sw23(lane & 15);
+    // (FP32 mode, natural column order: frag_row.)  Lane (n, h), n =
+    // 64 wn + 32 j + (lane & 31): piece 4 wn + 2 j + ((lane >> 4) & 1),
+    // element 4 ((lane >> 2) & 3) + (lane & 3) of rows 8 h + q (no swizzle).
+    const char *base = bt + (4 * wn + ((lane >> 4) & 1)) * 1024 + 512 * (lane >> 5) + 4 * (lane & 15);
 #pragma unroll
     for (int j = 0; j < kSubN; ++j)
 #pragma unroll
@@ -1130,9 +1135,10 @@ s8_stage_kernel(StageArgs args) {
 
   // ------------------------------------------------------- epilogue ---
   // Each lane holds, per 32x32 accumulator block, 8 consecutive columns of
-  // each 16-column K group of one row (sw23), which it stores directly as
-  // row vectors: 16 bytes per store, the two lanes of a row 32 contiguous
-  // bytes of it.  A transposed output (the mirror of an off-diagonal
+  // each 16-column K group of one row (sw23; FP32 mode: four quads of 4
+  // columns), which it stores directly as row vectors: 16 bytes per store,
+  // the two lanes of a row 32 contiguous bytes of it (FP32 row-major
+  // results of the other modes: 16).  A transposed output (the mirror of an off-diagonal
   // symmetric tile, the stage-5 result of a transposed parameter) goes
   // through wave-private LDS: written by column, read back as rows of 8
   // elements per lane.
@@ -1312,12 +1318,17 @@ s8_stage_kernel(StageArgs args) {
       if (acc_r) accum4(w, gc0 + ec4, r);
     }
   };
+  // Register e of a block holds column col16(e) of the lane's row (FP32
+  // mode: the natural MFMA order, 8 (e >> 2) + 4 lh + (e & 3)).
+  auto col16 = [&](int e) {
+    return MODE == SMX_S8_FP32 ? 8 * (e >> 2) + 4 * lh + (e & 3) : 16 * (e >> 3) + 8 * lh + (e & 7);
+  };
   // The lane's 16 values w of row gr, columns cb + col16(e) (cb a multiple
-  // of 32), stored in form FM: tiled FP32, planes and FP16 put each K group's
-  // 8 columns of the lane at their place in the group's row (planes: 16
-  // bytes of hi at 16 lh, 16 of lo at 32 + 16 lh; FP16: 16 bytes at
-  // 16 lh of the 32-column piece's half g); row-major FP32 (the stage-5
-  // result) as 16-byte column quads.
+  // of 32), stored in form FM: planes and FP16 put each K group's 8 columns
+  // of the lane at their place in the group's row (planes: 16 bytes of hi at
+  // 16 lh, 16 of lo at 32 + 16 lh; FP16: 16 bytes at 16 lh of the 32-column
+  // piece's half g); FP32 (tiled, or row-major for the stage-5 result) as
+  // 16-byte quads of columns.
   auto put_direct = [&](auto fm_c, const float (&w)[16], int64_t gr, int64_t cb, float *dst, int64_t ld, bool tl) {
     constexpr int FM = decltype(fm_c)::value;
     char *const out = reinterpret_cast<char *>(dst);
@@ -1350,22 +1361,17 @@ s8_stage_kernel(StageArgs args) {
         *reinterpret_cast<uint4 *>(out + base + 1024 * g + 32) = make_uint4(l[0], l[1], l[2], l[3]);
       }
     } else {
-      // column 16 g + 8 lh + 4 h: tiled, byte 64 (that column & 15) of its
-      // K group's row; row-major, byte 4 column of the row
-      const int64_t base = tl ? (gr & ~int64_t{15}) * (4 * ld) + ((gr & 15) << 6) + 64 * cb + 32 * lh
-                              : gr * (4 * ld) + 4 * (cb + 8 * lh);
+      // each quad of 4 consecutive columns c = col16(4 e4) .. + 3: tiled,
+      // byte 4 (c & 15) of the row of K group c >> 4; row-major, byte 4 c
+      const int64_t base = tl ? (gr & ~int64_t{15}) * (4 * ld) + ((gr & 15) << 6) + 64 * cb : gr * (4 * ld) + 4 * cb;
 #pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int e = 8 * g + 4 * h;
-          *reinterpret_cast<float4 *>(out + base + (tl ? 1024 * g + 16 * h : 4 * (16 * g + 4 * h))) =
-              make_float4(w[e], w[e + 1], w[e + 2], w[e + 3]);
-        }
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int c = col16(4 * e4), e = 4 * e4;
+        *reinterpret_cast<float4 *>(out + base + (tl ? 1024 * (c >> 4) + 4 * (c & 15) : 4 * c)) =
+            make_float4(w[e], w[e + 1], w[e + 2], w[e + 3]);
+      }
     }
   };
-  // Register e of a block holds column col16(e) of the lane's row.
-  auto col16 = [&](int e) { return 16 * (e >> 3) + 8 * lh + (e & 7); };
   // The block loop, specialised for the output form (one copy per form the
   // launch's mode can produce, so that each keeps only its own registers).
   auto epilogue = [&](auto fm_c) {
@@ -1396,10 +1402,10 @@ s8_stage_kernel(StageArgs args) {
         put_direct(fm_c, w, gr, cb, dst_t, ld_t, tiled_t);
         if (rs_on) {
           // a and z of the lane's columns, then the row's two lanes (lh)
-          const int o = static_cast<int>(cb - rs_c0) + 8 * lh;
+          const int o = static_cast<int>(cb - rs_c0);
 #pragma unroll
           for (int e4 = 0; e4 < 4; ++e4) {
-            const int oc = o + 16 * (e4 >> 1) + 4 * (e4 & 1);
+            const int oc = o + col16(4 * e4);
             const f32x4 a4 = *reinterpret_cast<const f32x4 *>(colv_lds + oc);
             const f32x4 z4 = *reinterpret_cast<const f32x4 *>(colv_lds + rs_w + oc);
 #pragma unroll

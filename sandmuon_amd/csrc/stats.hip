@@ -986,20 +986,19 @@ extern "C" size_t smx_stats_finish_table_bytes(int32_t n_desc) {
 }
 
 extern "C" int smx_stats_finish_staged(const smx_finish_desc *descs, int32_t n_desc, double beta, void *dev_table,
-                                       void *host_stage, size_t table_bytes, void *stream) {
+                                       size_t table_bytes, void *stream) {
   if (const int rc = check_finish_descs(descs, n_desc)) return rc;
   if (n_desc == 0) return SMX_OK;
   SMX_REQUIRE(n_desc <= 65535, SMX_EINVAL, "stats_finish_staged: at most 65535 descriptors");
   const size_t need = smx_stats_finish_table_bytes(n_desc);
-  SMX_REQUIRE(dev_table && host_stage && table_bytes >= need, SMX_EWORKSPACE,
-              "stats_finish_staged: dev_table and host_stage need smx_stats_finish_table_bytes(n_desc) bytes");
+  SMX_REQUIRE(dev_table && table_bytes >= need, SMX_EWORKSPACE,
+              "stats_finish_staged: dev_table needs smx_stats_finish_table_bytes(n_desc) bytes");
   int64_t nmax = 1;
   for (int32_t i = 0; i < n_desc; ++i) nmax = std::max<int64_t>(nmax, descs[i].n);
   SMX_REQUIRE(ceil_div(nmax, 64) <= INT32_MAX, SMX_ESHAPE, "stats_finish_staged: vector too long");
-  std::memcpy(host_stage, descs, need);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  SMX_REQUIRE(hipMemcpyAsync(dev_table, host_stage, need, hipMemcpyHostToDevice, st) == hipSuccess, SMX_ELAUNCH,
-              "stats_finish_staged: copy of the descriptor table failed");
+  static_assert(sizeof(smx_finish_desc) % 4 == 0, "the table is uploaded as 32-bit words");
+  if (const int rc = upload_table(dev_table, descs, need, st)) return rc;
   const auto *table = static_cast<const smx_finish_desc *>(dev_table);
   hipLaunchKernelGGL(finish_fold_table_kernel, dim3(static_cast<unsigned>(ceil_div(nmax, 64)), n_desc),
                      dim3(64 * kFoldWaves), 0, st, table);

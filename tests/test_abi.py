@@ -132,25 +132,28 @@ def test_validation_errors_return_before_gpu_work():
     a.offset, a.param_dtype = 0, 3
     assert lib.smx_adamw((_native.AdamwDesc * 1)(a), 1, 4, 1e-3, .9, .999, 1e-8, .01, None) == -3
     # staged finish and AdamW: the descriptor checks of the by-value calls,
-    # then the sizes of the device table and the pinned stage
+    # then the size of the device table
     f.kind = 0
     fs = (_native.FinishDesc * 3)(f, f, f)
     assert lib.smx_stats_finish_table_bytes(3) == 3 * ctypes.sizeof(_native.FinishDesc)
     assert lib.smx_stats_finish_table_bytes(0) == 0
     v16 = ctypes.c_void_p(16)
-    assert lib.smx_stats_finish_staged(fs, 3, .97, None, v16, 1 << 20, None) == -5
-    assert lib.smx_stats_finish_staged(fs, 3, .97, v16, v16, 3 * ctypes.sizeof(_native.FinishDesc) - 1, None) == -5
+    assert lib.smx_stats_finish_staged(fs, 3, .97, None, 1 << 20, None) == -5
+    assert lib.smx_stats_finish_staged(fs, 3, .97, v16, 3 * ctypes.sizeof(_native.FinishDesc) - 1, None) == -5
     f.kind = 5
-    assert lib.smx_stats_finish_staged((_native.FinishDesc * 1)(f), 1, .97, v16, v16, 1 << 20, None) == -1
-    assert lib.smx_stats_finish_staged(fs, 0, .97, None, None, 0, None) == 0
+    assert lib.smx_stats_finish_staged((_native.FinishDesc * 1)(f), 1, .97, v16, 1 << 20, None) == -1
+    assert lib.smx_stats_finish_staged(fs, 0, .97, None, 0, None) == 0
     a = _native.AdamwDesc(param=16, grad=16, exp_avg=16, exp_avg_sq=16, n=4, offset=0, bias1=.1, bias2=.1)
-    # 4 elements: one block of the minimum 256-element chunk
-    assert lib.smx_adamw_table_bytes(1, 4) == ctypes.sizeof(_native.AdamwDesc) + 4
-    assert lib.smx_adamw_table_bytes(2, 10 ** 6) == 2 * ctypes.sizeof(_native.AdamwDesc) + 4 * -(-10 ** 6 // 512)
-    assert lib.smx_adamw_staged((_native.AdamwDesc * 1)(a), 1, 4, 1e-3, .9, .999, 1e-8, .01, v16, None, 1 << 20,
+    # the table holds the descriptors (each block finds its first tensor)
+    assert lib.smx_adamw_table_bytes(1, 4) == ctypes.sizeof(_native.AdamwDesc)
+    assert lib.smx_adamw_table_bytes(2, 10 ** 6) == 2 * ctypes.sizeof(_native.AdamwDesc)
+    assert lib.smx_adamw_table_bytes(0, 0) == 0
+    assert lib.smx_adamw_staged((_native.AdamwDesc * 1)(a), 1, 4, 1e-3, .9, .999, 1e-8, .01, None, 1 << 20,
                                 None) == -5
+    assert lib.smx_adamw_staged((_native.AdamwDesc * 1)(a), 1, 4, 1e-3, .9, .999, 1e-8, .01, v16,
+                                ctypes.sizeof(_native.AdamwDesc) - 1, None) == -5
     a.offset = 3
-    assert lib.smx_adamw_staged((_native.AdamwDesc * 1)(a), 1, 4, 1e-3, .9, .999, 1e-8, .01, v16, v16, 1 << 20,
+    assert lib.smx_adamw_staged((_native.AdamwDesc * 1)(a), 1, 4, 1e-3, .9, .999, 1e-8, .01, v16, 1 << 20,
                                 None) == -2
     # matrix step: f64 parameters are not a step dtype
     d = _native.MatrixDesc(param=16, grad=16, momentum=16, inv_row=16, inv_col=16, rows=64, cols=32,

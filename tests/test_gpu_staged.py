@@ -1,5 +1,6 @@
 """The staged finish and AdamW entry points (one launch for a whole
-descriptor table in device memory, copied from pinned host memory) against
+descriptor table in device memory, written on the stream through the kernel
+arguments of 3840-byte upload launches) against
 the by-value calls (one launch per 32 finish / 56 AdamW descriptors):
 bit-identical results, on tables longer than one by-value launch takes and
 on consecutive calls that cycle the staging ring with tables of different
@@ -93,8 +94,7 @@ def test_staged_calls_in_flight_take_their_own_slots(device):
     # Several staged calls enqueued back to back behind a busy stream (a
     # finish and AdamW calls of two parameter groups per step, three steps),
     # so that none has run when the next is staged: each in-flight call keeps
-    # its own pinned stage and device table, and every result equals the
-    # by-value calls'.
+    # its own device table, and every result equals the by-value calls'.
     stage = _native.DescriptorStage(device)
     cases = []
     for rep in range(3):
@@ -111,7 +111,7 @@ def test_staged_calls_in_flight_take_their_own_slots(device):
         _native.stats_finish(fb, 0.97, device, stage)
         _native.adamw(wb, tot, 1e-3, 0.9, 0.95, 1e-8, 0.1, device, stage)
     # every staged call is still in flight, each in a slot of its own
-    assert sum(1 for sl in stage.slots if sl[2] is not None and not sl[2].query()) == 6
+    assert sum(1 for sl in stage.slots if sl[1] is not None and not sl[1].query()) == 6
     torch.cuda.synchronize()
     for fa, fb, a, b, wa, wb, wta, wtb, tot in cases:
         for ta, tb in zip(a, b):
@@ -125,22 +125,20 @@ def test_staged_calls_in_flight_take_their_own_slots(device):
 @pytest.mark.gpu
 def test_descriptor_stage_allocates_once_for_tables_that_fit(device):
     # All slots are allocated at the first staged call, at one size (a
-    # power of two of at least 256 KiB); later calls whose tables fit take
+    # power of two of at least 64 KiB); later calls whose tables fit take
     # those slots and allocate nothing; a larger table replaces all slots by
     # larger ones once.
     stage = _native.DescriptorStage(device)
     slot = stage.take(10_000)
     stage.done(slot)
-    assert len(stage.slots) == stage.MAX_SLOTS and stage.size == 1 << 18
+    assert len(stage.slots) == stage.MAX_SLOTS and stage.size == 1 << 16
     tables = {sl[0].data_ptr() for sl in stage.slots}
-    pinned = {sl[1].data_ptr() for sl in stage.slots}
-    for n in (100, 90_000, 1 << 18, 5000) * 5:
+    for n in (100, 30_000, 1 << 16, 5000) * 5:
         slot = stage.take(n)
         stage.done(slot)
     assert {sl[0].data_ptr() for sl in stage.slots} == tables
-    assert {sl[1].data_ptr() for sl in stage.slots} == pinned
-    slot = stage.take((1 << 18) + 1)
+    slot = stage.take((1 << 16) + 1)
     stage.done(slot)
-    assert stage.size == 1 << 19 and len(stage.slots) == stage.MAX_SLOTS
-    assert all(sl[0].numel() == 1 << 19 and sl[1].numel() == 1 << 19 for sl in stage.slots)
+    assert stage.size == 1 << 17 and len(stage.slots) == stage.MAX_SLOTS
+    assert all(sl[0].numel() == 1 << 17 for sl in stage.slots)
     torch.cuda.synchronize()

@@ -208,17 +208,17 @@ def test_k_major_f16_reads(tn, waves):
 
 @pytest.mark.parametrize("tn,waves", [(128, 4), (256, 8)])
 def test_k_major_f32_reads(tn, waves):
-    """load_b_km (FP32): lane (n, h) reads B[k0 + 8h + q][n] (n the
-    permuted column sw23) at (4 wn + pp) KB + 512 h + 4 sw23(lane & 15) +
-    2 KB j + 64 q."""
+    """load_b_km (FP32 mode, natural column order): lane (n, h) reads
+    B[k0 + 8h + q][n] at (4 wn + pp) KB + 512 h + 4 (lane & 15) + 2 KB j +
+    64 q."""
     ld, k0, n0 = 512, 32, tn
     lds = km_stage("f32", tn, waves, ld, k0, n0)
     for wn in range(tn // 64):
         for lane in range(64):
-            base = (4 * wn + ((lane >> 4) & 1)) * 1024 + 512 * (lane >> 5) + 4 * sw23(lane & 15)
+            base = (4 * wn + ((lane >> 4) & 1)) * 1024 + 512 * (lane >> 5) + 4 * (lane & 15)
             for j in range(2):
                 for q in range(8):
-                    n, k = 64 * wn + 32 * j + sw23(lane & 31), 8 * (lane >> 5) + q
+                    n, k = 64 * wn + 32 * j + (lane & 31), 8 * (lane >> 5) + q
                     assert lds[base + 2048 * j + 64 * q] == ("f", k0 + k, n0 + n)
 
 
@@ -255,9 +255,10 @@ def test_epilogue_staged_stores_address_tiled_elements(form):
             assert len(spans) == (1 if form == "f16" else 2)
 
 
-def col16(e, lh):
-    """s8.hip col16: the column of register e of a lane of half lh."""
-    return 16 * (e >> 3) + 8 * lh + (e & 7)
+def col16(e, lh, natural=False):
+    """s8.hip col16: the column of register e of a lane of half lh (FP32
+    mode reads its B fragments unpermuted: the natural MFMA order)."""
+    return 8 * (e >> 2) + 4 * lh + (e & 3) if natural else 16 * (e >> 3) + 8 * lh + (e & 7)
 
 
 def test_swapped_mfma_layout_puts_consecutive_columns_in_a_lane():
@@ -267,7 +268,7 @@ def test_swapped_mfma_layout_puts_consecutive_columns_in_a_lane():
     C[m][sw23(p)] because lane p of the B fragment holds B row sw23(p).
     So register e of lane (r, h) holds C[r][col16(e)]: 8 consecutive columns
     of each 16-column K group per lane, every column of the block once
-    per row."""
+    per row.  (FP32 mode reads B unpermuted: C[r][8 (e >> 2) + 4 h + (e & 3)].)"""
     for lane in range(64):
         r, lh = lane & 31, lane >> 5
         cols = []
@@ -278,10 +279,14 @@ def test_swapped_mfma_layout_puts_consecutive_columns_in_a_lane():
         assert cols[:8] == list(range(8 * lh, 8 * lh + 8))
         assert cols[8:] == list(range(16 + 8 * lh, 16 + 8 * lh + 8))
     assert sorted(col16(e, h) for h in range(2) for e in range(16)) == list(range(32))
+    for lane in range(64):
+        r, lh = lane & 31, lane >> 5
+        assert [8 * (e >> 2) + 4 * lh + (e & 3) for e in range(16)] == [col16(e, lh, True) for e in range(16)]
 
 
-@pytest.mark.parametrize("form", ["planes", "f32", "f32_rowmajor", "f16"])
-def test_epilogue_direct_stores_address_tiled_elements(form):
+@pytest.mark.parametrize("form,natural", [("planes", False), ("f32", False), ("f32", True),
+                                          ("f32_rowmajor", False), ("f32_rowmajor", True), ("f16", False)])
+def test_epilogue_direct_stores_address_tiled_elements(form, natural):
     """put_direct: lane (r, h) stores its 16 values of row gr = R + r,
     columns cb + col16(e); every store writes 16 bytes that are exactly the
     bytes of those elements (tiled_index, planes hi/lo, FP16 32-column
@@ -301,7 +306,7 @@ def test_epilogue_direct_stores_address_tiled_elements(form):
             for lane in range(64):
                 r, lh = lane & 31, lane >> 5
                 gr = R + r
-                val = {e: (gr, cb + col16(e, lh)) for e in range(16)}
+                val = {e: (gr, cb + col16(e, lh, natural)) for e in range(16)}
                 stores = []  # (byte offset, [elements], bytes per element, plane)
                 if form == "f16":
                     base = (gr & ~15) * 2 * ld + ((gr & 15) << 6) + 32 * cb + 16 * lh
@@ -314,13 +319,11 @@ def test_epilogue_direct_stores_address_tiled_elements(form):
                         stores.append((base + 1024 * g + 32, [val[8 * g + e] for e in range(8)], 2, "lo"))
                 else:
                     tl = form == "f32"
-                    base = ((gr & ~15) * 4 * ld + ((gr & 15) << 6) + 64 * cb + 32 * lh) if tl else \
-                        gr * 4 * ld + 4 * (cb + 8 * lh)
-                    for g in range(2):
-                        for h in range(2):
-                            e = 8 * g + 4 * h
-                            off = base + (1024 * g + 16 * h if tl else 4 * (16 * g + 4 * h))
-                            stores.append((off, [val[e + t] for t in range(4)], 4, "f"))
+                    base = ((gr & ~15) * 4 * ld + ((gr & 15) << 6) + 64 * cb) if tl else gr * 4 * ld + 4 * cb
+                    for e4 in range(4):
+                        c = col16(4 * e4, lh, natural)
+                        off = base + (1024 * (c >> 4) + 4 * (c & 15) if tl else 4 * c)
+                        stores.append((off, [val[4 * e4 + t] for t in range(4)], 4, "f"))
                 for off, elems, size, plane in stores:
                     assert len(elems) * size == 16
                     for t, (row, col) in enumerate(elems):
