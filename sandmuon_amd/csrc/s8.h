@@ -24,8 +24,9 @@ constexpr int kTile = 256;        // apply tile rows and buffer padding
 constexpr int kSymTile = 128;     // Gram / square output tile edge
 constexpr int kMaxClasses = 8;    // shape classes per GEMM launch
 // Parameter columns per stage-5 row-sum partial: a wave's 64 output columns
-// of an apply tile, or (transposed parameter) its 128 output rows.
-constexpr int kStripT = 64, kStripM = 128;
+// of an apply tile, or (transposed parameter) 64 of its output rows (two
+// strips per wave of a 256-row tile, one per wave of a 128-row tile).
+constexpr int kStripT = 64, kStripM = 64;
 
 // Fixed S8 recipe: sandmuon/coefficients.py:3-11.
 constexpr double kS8Margin = 1.35;

@@ -197,11 +197,9 @@ constexpr int kBK = 16;             // K per pipeline stage
 //   kGeoL  256 x 256, 8 waves of 128 x 64 (two per SIMD), one block per CU.
 // The wave tile, and so the LDS fragment reads per MFMA, is the same in M
 // and L; an L block moves a third fewer operand bytes into LDS per MFMA
-// (its 256 A rows serve 256 B rows), which is what bounds these loops: the
-// direct-to-LDS operand stream, not the MFMAs (a timing copy without the
-// refill loads ran the cfg5 S8 37% faster, one without the fragment reads
-// 11% faster).  A round of the device's block slots does the same work in
-// M and L; the host picks the geometry per launch (pick_geo).
+// (its 256 A rows serve 256 B rows: cfg5 S8 7% faster).  A round of the
+// device's block slots does the same work in M and L; the host picks the
+// geometry per launch (pick_geo).
 enum TileGeo { kGeoM = 0, kGeoS = 1, kGeoL = 2 };
 template <int TM, int TN>
 struct Geo {
@@ -228,11 +226,11 @@ struct Geo {
 using GeoM = Geo<256, 128>;
 using GeoS = Geo<128, 128>;
 using GeoL = Geo<256, 256>;
-// (kGeoM: the Gram and the apply at 768 x 768, 128 x 128 Gram tiles measured
-// no faster at 768 x 3072.  kGeoS: the square when its tiles take fewer
-// rounds of the CUs' block slots, allowing for their lower rate: the
-// smaller tile moves a third more operand bytes per MFMA, and a round of it
-// takes 0.9 of a round of the larger one.  At 768 x 768 the square's 12
+// (kGeoS: the Gram, the square, the SYM products and the applies at cfg4,
+// and generally a launch whose small tiles take fewer rounds of the CUs'
+// block slots, allowing for their lower rate: the smaller tile moves a
+// third more operand bytes per MFMA, and a round of it takes 0.9 of a round
+// of the larger one.  At 768 x 768 the square's 12
 // half-tiles per matrix need two rounds of 512 slots, its 21 small tiles
 // 1.5 rounds of 768 (cfg4: 104 against 117 us per launch); at 2048 x 2048
 // the larger tile wins.)
@@ -1001,7 +999,8 @@ __device__ __forceinline__ void ep_read8(const float *s, int row, int col, float
 // computed whole; an off-diagonal one also writes its mirror.
 __host__ __device__ inline int64_t phase_tiles(const S8Class &k, int phase, int geo, int op = -1) {
   if (phase == kApply)
-    return static_cast<int64_t>(k.tiles_m) * ((op == kOpApplyQ ? k.rp : k.cp) / (geo == kGeoL ? 256 : 128));
+    return static_cast<int64_t>(geo == kGeoS ? k.tiles_s : k.tiles_m) *
+           ((op == kOpApplyQ ? k.rp : k.cp) / (geo == kGeoL ? 256 : 128));
   return square_tiles(k, geo);
 }
 
@@ -1010,7 +1009,6 @@ __global__ void __launch_bounds__((Geo<TM, TN>::kThreads))
 __attribute__((amdgpu_waves_per_eu(Geo<TM, TN>::kWavesPerEU, Geo<TM, TN>::kWavesPerEU)))
 s8_stage_kernel(StageArgs args) {
   using Gm = Geo<TM, TN>;
-  static_assert(Gm::kGeo != kGeoS || PHASE != kApply, "no 128 x 128 tiles for the apply");
   constexpr int kSubM = Gm::kSubM, kTileN = Gm::kTileN, kThreads = Gm::kThreads, kWaves = Gm::kWaves;
   __shared__ __attribute__((aligned(16))) char smem[Gm::kRingBytes];
   __shared__ double dscratch[16];
@@ -1029,8 +1027,9 @@ s8_stage_kernel(StageArgs args) {
     // a column block of X and cycle through P's row blocks, so each X block
     // is fetched once (0.54 GB per cfg4 apply launch against 0.77 GB
     // row-major; the launch time is the same).
-    tn = tix / K.tiles_m;
-    tm = tix % K.tiles_m;
+    const int64_t nrow = Gm::kGeo == kGeoS ? K.tiles_s : K.tiles_m;  // row tiles
+    tn = tix / nrow;
+    tm = tix % nrow;
   } else if constexpr (Gm::kGeo == kGeoM) {
     int64_t rem = tix >> 1;
     tm = 0;
@@ -1196,7 +1195,7 @@ s8_stage_kernel(StageArgs args) {
   // parameter), reduced over the 8 lanes of the row and stored for the
   // mapback (its row coefficients and graft norm), so no later pass reads Q
   // for them.
-  static_assert(PHASE != kApply || (kStripT == 32 * kSubN && kStripM == 32 * kSubM),
+  static_assert(PHASE != kApply || (kStripT == 32 * kSubN && (32 * kSubM) % kStripM == 0),
                 "a row-sum strip is one wave's share of an apply tile");
   const int64_t strips = M.strips(), prows = M.prow_pad();
   // a and z of the tile's parameter columns in LDS past the staging blocks
@@ -1434,7 +1433,7 @@ s8_stage_kernel(StageArgs args) {
           const int row = er + 8 * q;
           const int64_t gm = cb + row;
           put_row(fm_c, U, row, gm, R0 + i * 32, dst_m, ld_m, tiled_m, rs[j][q], rs_on);
-          if (rs_on && i == kSubM - 1) emit(gm, R0 / kStripM, rs[j][q]);
+          if (rs_on && (i + 1) % (kStripM / 32) == 0) emit(gm, (R0 + 32 * (i + 1) - kStripM) / kStripM, rs[j][q]);
         }
       }
       // Keep the scheduler from hoisting every accumulator read to the top
@@ -1690,11 +1689,12 @@ static int64_t device_cus() {
 // one or two blocks of the launch and nothing of it to overlap a block's
 // prologue and epilogue with (cfg4 Gram, square and SYM launches 15-60%
 // slower; with tiled operands the cfg4 applies, 0.6-2.2 tiles per CU, are
-// 1-2% faster as 256 x 128 tiles, two blocks per CU).  Otherwise, for the
-// symmetric products (`small_ok`: Gram, square, SYM), 128 x 128 tiles when
-// they take fewer rounds of the CUs' block slots (three per CU, a round
-// counted 0.9 of one of two 256 x 128 blocks per CU), else 256 x 128.
-static int pick_geo(const S8Layout &Lay, int phase, const std::vector<Seg> &segs, bool small_ok) {
+// 1-2% faster as 256 x 128 tiles, two blocks per CU).  Otherwise 128 x 128
+// tiles when they take fewer rounds of the CUs' block slots (three per CU,
+// a round counted 0.9 of one of two 256 x 128 blocks per CU), else
+// 256 x 128 (the cfg4 applies take 128 x 128 tiles: S8 runs 2% shorter
+// than with 256 x 128).
+static int pick_geo(const S8Layout &Lay, int phase, const std::vector<Seg> &segs) {
   if (g_tile_policy == 1) return kGeoL;
   const int64_t cus = device_cus();
   int64_t tiles[3] = {0, 0, 0};
@@ -1709,7 +1709,7 @@ static int pick_geo(const S8Layout &Lay, int phase, const std::vector<Seg> &segs
     const int thr = phase == kApply ? thr_apply : thr_other;
     if (g_tile_policy == 0 && 10 * tiles[kGeoL] >= thr * cus) return kGeoL;
   }
-  if (small_ok) {
+  {
     const double r_m = static_cast<double>(ceil_div(tiles[kGeoM], 2 * cus));
     const double r_s = static_cast<double>(ceil_div(tiles[kGeoS], 3 * cus));
     if (0.9 * r_s < r_m) return kGeoS;
@@ -1720,11 +1720,9 @@ static int pick_geo(const S8Layout &Lay, int phase, const std::vector<Seg> &segs
 // One phase launch of a stage kernel in geometry `geo`.
 template <int MODE, int PHASE>
 static void launch_stage(int geo, int32_t blocks, const StageArgs &a, hipStream_t st) {
-  if constexpr (PHASE != kApply) {
-    if (geo == kGeoS) {
-      hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, 128, 128>), dim3(blocks), dim3(GeoS::kThreads), 0, st, a);
-      return;
-    }
+  if (geo == kGeoS) {
+    hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, 128, 128>), dim3(blocks), dim3(GeoS::kThreads), 0, st, a);
+    return;
   }
   if (geo == kGeoL)
     hipLaunchKernelGGL((s8_stage_kernel<MODE, PHASE, 256, 256>), dim3(blocks), dim3(GeoL::kThreads), 0, st, a);
@@ -1766,7 +1764,7 @@ static int launch_phase(const S8Layout &Lay, const SlotSet &set, int stage, int 
         if (!form_compiled(mode, PHASE, out_form(Lay.mode, g_comp_mask, PHASE, stage, sg.op, Lay.cls[sg.cls].gs != 0)))
           return fail(SMX_EINVAL, "s8: no epilogue for the output form of this product");
     const int geo =
-        PHASE == kSquare ? sq_geo : PHASE == kPoly1 ? kGeoM : pick_geo(Lay, PHASE, segs, PHASE != kApply);
+        PHASE == kSquare ? sq_geo : PHASE == kPoly1 ? kGeoM : pick_geo(Lay, PHASE, segs);
     int32_t off = 0;
     a.n_seg = 0;
     for (const Seg &sg : segs) {
@@ -1818,7 +1816,7 @@ static int run_s8_set_stage(const S8Layout &Lay, const SlotSet &set, int stage, 
   auto cnt = [&](int i) { return static_cast<int64_t>(set.hi[i] - set.lo[i]); };
   // The square covers every matrix of the set at every stage, so its
   // geometry (and the stage-1 Schatten partials) is the same for the run.
-  const int sq_geo = pick_geo(Lay, kSquare, launch_segments(Lay, set, kSquare, stage, {}), true);
+  const int sq_geo = pick_geo(Lay, kSquare, launch_segments(Lay, set, kSquare, stage, {}));
   bool any_gs = false;
   for (int i = 0; i < Lay.n_classes; ++i) any_gs = any_gs || (Lay.cls[i].gs && cnt(i) > 0);
   int rc = SMX_OK;
