@@ -811,17 +811,15 @@ __device__ __forceinline__ void pipe_iter(const Opnd &A, const Opnd &B, const Wa
                                                 lds0 + (kt % S) * G::kStageBytes);
   const char *nxt = smem + ((kt + 1) % S) * G::kStageBytes;
   if (more) load_b_any<MODE, G, BKM>(nxt, wn, bf[PAR ^ 1], bl);
-  // Raised wave priority while this wave issues its MFMAs, so the
-  // arbiter favours it over the other block's wave on the SIMD that is
-  // issuing LDS reads and loads (Gram launches 5% faster).
-  __builtin_amdgcn_s_setprio(1);
+  // (Raising the wave's priority around its MFMAs, s_setprio 1, made the
+  // Gram launches 5% faster with 256 x 128 tiles; with the current tiles it
+  // made the S8 runs 0.5-1% slower, so the waves keep the default.)
 #pragma unroll
   for (int i = 0; i < G::kSubM; ++i) {
     mma_row<MODE>(af[i], bf[PAR], acc[i]);
     if (more) load_a<MODE, G>(nxt, wm, i, af[i]);
   }
   if constexpr (SEL >= 0) mma_one_hot<MODE>(sel_s, SEL, bf[PAR], acc[MODE == kS8F16 ? SEL : SEL >> 1]);
-  __builtin_amdgcn_s_setprio(0);
 }
 
 // ACCG: also accumulate sel_s * G over the wave's rows (square phase; A and
