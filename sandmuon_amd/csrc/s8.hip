@@ -1188,14 +1188,15 @@ s8_stage_kernel(StageArgs args) {
   float *const U = reinterpret_cast<float *>(smem) + wave * 2 * kEpBlock;
   float sq_local = 0.f;
   // The stage-5 result of the matrix step: per parameter row, partial sums
-  // of Q z, (a Q)^2 and (a Q)(a z) over the wave's strip of parameter
-  // columns (its 64 output columns; its 128 output rows for a transposed
-  // parameter), reduced over the 8 lanes of the row and stored for the
-  // mapback (its row coefficients and graft norm), so no later pass reads Q
-  // for them.
+  // of Q z, (a Q)^2 and (a Q)(a z) over a strip of parameter columns (the
+  // wave's 64 output columns; for a transposed parameter, 64 of its output
+  // rows), reduced over the lanes that hold the row (the two lanes of a
+  // directly stored row, the 8 of a staged transposed one) and stored for
+  // the mapback (its row coefficients and graft norm), so no later pass
+  // reads Q for them.
   static_assert(PHASE != kApply || (kStripT == 32 * kSubN && (32 * kSubM) % kStripM == 0),
                 "a row-sum strip is one wave's share of an apply tile");
-  const int64_t strips = M.strips(), prows = M.prow_pad();
+  const int64_t prows = M.prow_pad();
   // a and z of the tile's parameter columns in LDS past the staging blocks
   // (the operand ring is free once the K loop is done).
   float *const colv_lds = reinterpret_cast<float *>(smem) + kWaves * 2 * kEpBlock;
