@@ -47,7 +47,7 @@ int upload_table(void *dst, const void *src, size_t bytes, hipStream_t st) {
   auto *d = static_cast<uint32_t *>(dst);
   const size_t words = bytes / 4;
   for (size_t o = 0; o < words; o += kUploadWords) {
-    UploadPack p;
+    UploadPack p{};  // (the unused tail of the payload is zeros, not stale host bytes)
     p.words = static_cast<int32_t>(std::min<size_t>(kUploadWords, words - o));
     std::memcpy(p.w, s + o, static_cast<size_t>(p.words) * 4);
     p.dst = d + o;
