@@ -197,8 +197,10 @@ __global__ void __launch_bounds__(64) matrix_prep_kernel(PrepPack pack) {
 // Row groups (4 / wpr rows, one per wave group) per whiten block: a job
 // whose row fits the lanes' registers takes kWhitenGroups of them in turn,
 // the next group's loads in flight while the current one is reduced and
-// stored; the other jobs take one.
-constexpr int kWhitenGroups = 4;
+// stored; the other jobs take one.  One group per block is the fastest on
+// the cfg4 shapes (more blocks, each issuing all its loads at once): 139 us
+// per step against 147 with two groups and 153 with four.
+constexpr int kWhitenGroups = 1;
 template <typename Job>
 __host__ __device__ inline bool whiten_pipelined(const Job &j) {
   return !j.flip && j.wvec && j.slices <= kMaxSlices;
@@ -685,13 +687,125 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
     whiten_rows_single<R1>(J, blk, red[0], rp);
 }
 
-// Transposed parameters: one wave per row, kFlipRows rows per block, the
-// row in chunks of kFlipChunk columns (kMaxSlices float4 per lane); pass 1
-// keeps y = S a when the row is one chunk (KEPT, a launch of its own), else
-// pass 2 reads g and m' again.  Pass 2 stages each chunk of V in LDS: the block's 16 rows are
-// one 16-element K group of every X row of the chunk, so each 64 lanes
-// write one whole 1 KB piece of the tiled X (16 X rows, 4 lanes per row).
-template <bool R1, bool KEPT>
+// Transposed parameters whose row is one chunk (the float4 path, at most
+// kFlipChunk columns): one wave per row, kFlipRows rows per block.  a and z
+// (the same for every row) are loaded once into LDS, which leaves every g
+// and m load of a lane in flight together (6 float4) within the 64 VGPRs
+// that let a CU hold two 1024-thread blocks.  The LDS tile row of a wave
+// holds b y = b S a, then V = b y + kappa u z; the block's 16 rows are one
+// 16-element K group of every X row, so each 64 lanes write one whole 1 KB
+// piece of the tiled X (16 X rows, 4 lanes per row).
+template <bool R1>
+__global__ void __launch_bounds__(kFlipThreads) whiten_flip_kept_kernel(JobRange range) {
+  __shared__ float tile[kFlipRows][kFlipChunk + 4];
+  __shared__ double rp[2][kFlipRows];
+  __shared__ float4 colv[2][kFlipChunk / 4];  // a, z
+  const int jid = find_job(range, blockIdx.x);
+  const DevJob J = load_job(range.jobs, jid);
+  const DevDesc &d = J.d;
+  // (blocks of one XCD take consecutive groups, as in whiten_flip_kernel)
+  const int nb = static_cast<int>(whiten_blocks(J));
+  const int jb = blockIdx.x - range.start[jid];
+  const int blk = (jb & 7) * (nb / 8) + (jb >> 3);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the row: wave-uniform
+  const int64_t i0 = static_cast<int64_t>(blk) * kFlipRows;
+  const int64_t i = i0 + wave;
+  const bool live = i < d.rows;
+  const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
+  const float kappa = R1 ? d.kappa[0] : 0.f;
+  const bool planes = J.planes != 0;
+  const int n4 = static_cast<int>(d.cols / 4);
+  SMX_GLOBAL float *mrow = d.momentum + i * d.cols;
+  const SMX_GLOBAL float *grow = (const SMX_GLOBAL float *)d.grad + i * d.cols;
+  {
+    const int t = threadIdx.x, h = kFlipChunk / 4;
+    if (t < n4) colv[0][t] = ld4(d.inv_col, t);
+    if (R1 && t >= h && t - h < n4) colv[1][t - h] = ld4(d.z, t - h);
+  }
+  float4 g[kMaxSlices], m[kMaxSlices];
+#pragma unroll
+  for (int t = 0; t < kMaxSlices; ++t) {
+    const int q = lane + 64 * t;
+    if (live && q < n4) {
+      g[t] = ld4(grow, q);
+      m[t] = ld4(mrow, q);
+    }
+  }
+  const float b = live ? d.inv_row[i] : 0.f;
+  __syncthreads();
+  float y2 = 0.f, yz = 0.f;
+#pragma unroll
+  for (int t = 0; t < kMaxSlices; ++t) {
+    const int q = lane + 64 * t;
+    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live && q < n4) {
+      const float4 aa = colv[0][q], gg = g[t];
+      float4 mm = m[t];
+      mm.x = fmaf(mm.x, beta, gg.x * omb); mm.y = fmaf(mm.y, beta, gg.y * omb);
+      mm.z = fmaf(mm.z, beta, gg.z * omb); mm.w = fmaf(mm.w, beta, gg.w * omb);
+      st4(mrow, q, mm);
+      y.x = fmaf(mm.x, beta, gg.x * omb) * aa.x; y.y = fmaf(mm.y, beta, gg.y * omb) * aa.y;
+      y.z = fmaf(mm.z, beta, gg.z * omb) * aa.z; y.w = fmaf(mm.w, beta, gg.w * omb) * aa.w;
+      y2 = fmaf(y.x, y.x, fmaf(y.y, y.y, fmaf(y.z, y.z, fmaf(y.w, y.w, y2))));
+      if constexpr (R1) {
+        const float4 zz4 = colv[1][q];
+        yz = fmaf(y.x, zz4.x, fmaf(y.y, zz4.y, fmaf(y.z, zz4.z, fmaf(y.w, zz4.w, yz))));
+      }
+    }
+    *reinterpret_cast<float4 *>(&tile[wave][4 * q]) = make_float4(b * y.x, b * y.y, b * y.z, b * y.w);
+  }
+  const double Y2 = wave_sum(y2), YZ = wave_sum(yz);
+  double vy = 0.0, vu = 0.0;  // the row's b^2 |S a|^2 and u^2
+  if (live) {
+    const double bd = b;
+    const double u = bd * YZ;
+    vy = bd * bd * Y2;
+    vu = u * u;
+    if (lane == 0) J.u[i] = static_cast<float>(u);
+    if constexpr (R1) {
+      const float ku = kappa * static_cast<float>(u);
+#pragma unroll
+      for (int t = 0; t < kMaxSlices; ++t) {
+        const int q = lane + 64 * t;
+        if (q < n4) {
+          float4 *v = reinterpret_cast<float4 *>(&tile[wave][4 * q]);
+          const float4 z = colv[1][q];
+          float4 w = *v;
+          w.x = fmaf(ku, z.x, w.x); w.y = fmaf(ku, z.y, w.y); w.z = fmaf(ku, z.z, w.z); w.w = fmaf(ku, z.w, w.w);
+          *v = w;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int qq = threadIdx.x & 3;  // 4-row quarter of the K group
+#pragma unroll
+  for (int r = 0; r < kFlipChunk / 256; ++r) {
+    const int jj = (threadIdx.x >> 2) + 256 * r;  // X row
+    if (jj < J.pcol_pad) {
+      const float w[4] = {tile[4 * qq][jj], tile[4 * qq + 1][jj], tile[4 * qq + 2][jj], tile[4 * qq + 3][jj]};
+      // (the 4 lanes of an X row are in it together, so lane pairs are whole)
+      put_operand4_paired(J.x, tiled_index(jj, i0 + 4 * qq, J.prow_pad), w, planes, true);
+    }
+  }
+  if (lane == 0) {
+    rp[0][wave] = vy;
+    rp[1][wave] = vu;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    double t = 0.0;
+    for (int r = 0; r < kFlipRows; ++r) t += rp[threadIdx.x][r];
+    J.fro[threadIdx.x * nb + blk] = t;
+  }
+}
+
+// Transposed parameters, the other rows: one wave per row, kFlipRows rows
+// per block, the row in chunks of kFlipChunk columns (kMaxSlices float4 per
+// lane); pass 2 reads g and m' again.  Pass 2 stages each chunk of V in LDS
+// as whiten_flip_kept_kernel does.
+template <bool R1>
 __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange range) {
   __shared__ float tile[kFlipRows][kFlipChunk + 4];
   __shared__ double rp[2][kFlipRows];
@@ -714,13 +828,10 @@ __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange rang
   const bool planes = J.planes != 0;
   SMX_GLOBAL float *mrow = live ? d.momentum + i * d.cols : nullptr;
   const bool vec = J.wvec != 0;
-  constexpr bool kept = KEPT;  // the host's bucket: vec && cols <= kFlipChunk
   const int n4 = static_cast<int>(d.cols / 4);
   const SMX_GLOBAL float *grow = live && vec ? (const SMX_GLOBAL float *)d.grad + i * d.cols : nullptr;
   const float b = live ? d.inv_row[i] : 0.f;
   // Slice t of chunk c of this lane: float4 c * kFlipChunk / 4 + lane + 64 t.
-  // KEPT: pass 1 leaves b y = b S a of its row in the LDS tile, and pass 2
-  // adds kappa u z there.
   float y2 = 0.f, yz = 0.f;
   if (vec) {
     // Two slices' loads in flight at a time: with kMaxSlices at once the
@@ -763,9 +874,6 @@ __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange rang
             yz = fmaf(y.x, zz4.x, fmaf(y.y, zz4.y, fmaf(y.z, zz4.z, fmaf(y.w, zz4.w, yz))));
           }
         }
-        if constexpr (KEPT)
-          *reinterpret_cast<float4 *>(&tile[wave][4 * (lane + 64 * t)]) =
-              make_float4(b * y.x, b * y.y, b * y.z, b * y.w);
       }
       }
     }
@@ -800,22 +908,7 @@ __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange rang
   const int qq = threadIdx.x & 3;  // 4-row quarter of the K group
   for (int c0 = 0; c0 < J.pcol_pad; c0 += kFlipChunk) {
     const int c4 = c0 / 4;
-    if constexpr (KEPT) {
-      // one chunk (pcol_pad <= kFlipChunk): the tile row holds b y
-      if constexpr (R1) {
-#pragma unroll
-        for (int t = 0; t < kMaxSlices; ++t) {
-          const int q = lane + 64 * t;
-          if (live && q < n4) {
-            float4 *v = reinterpret_cast<float4 *>(&tile[wave][4 * q]);
-            const float4 z = ld4(d.z, q);
-            float4 w = *v;
-            w.x = fmaf(ku, z.x, w.x); w.y = fmaf(ku, z.y, w.y); w.z = fmaf(ku, z.z, w.z); w.w = fmaf(ku, z.w, w.w);
-            *v = w;
-          }
-        }
-      }
-    } else {
+    {
     float4 g[kMaxSlices], m[kMaxSlices], a[kMaxSlices], z[kMaxSlices];
 #pragma unroll
     for (int t = 0; t < kMaxSlices; ++t) {
@@ -862,7 +955,8 @@ __global__ void __launch_bounds__(kFlipThreads) whiten_flip_kernel(JobRange rang
       const int jj = (threadIdx.x >> 2) + 256 * r;  // X row in the chunk
       if (c0 + jj < J.pcol_pad) {
         const float w[4] = {tile[4 * qq][jj], tile[4 * qq + 1][jj], tile[4 * qq + 2][jj], tile[4 * qq + 3][jj]};
-        put_operand4((float *)J.x, tiled_index(c0 + jj, i0 + 4 * qq, J.prow_pad), w, planes);
+        // (the 4 lanes of an X row are in it together, so lane pairs are whole)
+        put_operand4_paired(J.x, tiled_index(c0 + jj, i0 + 4 * qq, J.prow_pad), w, planes, true);
       }
     }
     __syncthreads();
@@ -1196,14 +1290,14 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
     int rc = r1 ? launch_range(h, table, 0, n_plain, whiten_blocks, whiten_kernel<true>, kRowThreads, "whiten", st)
                 : launch_range(h, table, 0, n_plain, whiten_blocks, whiten_kernel<false>, kRowThreads, "whiten", st);
     if (!rc && n_kept > n_plain)
-      rc = r1 ? launch_range(h, table, n_plain, n_kept - n_plain, whiten_blocks, whiten_flip_kernel<true, true>,
+      rc = r1 ? launch_range(h, table, n_plain, n_kept - n_plain, whiten_blocks, whiten_flip_kept_kernel<true>,
                              kFlipThreads, "whiten", st)
-              : launch_range(h, table, n_plain, n_kept - n_plain, whiten_blocks, whiten_flip_kernel<false, true>,
+              : launch_range(h, table, n_plain, n_kept - n_plain, whiten_blocks, whiten_flip_kept_kernel<false>,
                              kFlipThreads, "whiten", st);
     if (!rc && m > n_kept)
-      rc = r1 ? launch_range(h, table, n_kept, m - n_kept, whiten_blocks, whiten_flip_kernel<true, false>,
+      rc = r1 ? launch_range(h, table, n_kept, m - n_kept, whiten_blocks, whiten_flip_kernel<true>,
                              kFlipThreads, "whiten", st)
-              : launch_range(h, table, n_kept, m - n_kept, whiten_blocks, whiten_flip_kernel<false, false>,
+              : launch_range(h, table, n_kept, m - n_kept, whiten_blocks, whiten_flip_kernel<false>,
                              kFlipThreads, "whiten", st);
     if (!rc) rc = matrix_totals(table, m, kCstFro, st);
     plan.layout.rowsums = 1;
