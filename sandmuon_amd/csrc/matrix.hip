@@ -18,10 +18,11 @@
 // by `wpr` waves (1, 2 or 4, so that a lane holds at most kMaxSlices float4
 // of it), a 256-thread block by 4 / wpr rows.  Sums over a matrix (||V||^2
 // for the S8 normalisation, ||U||^2 for the graft) are per-block FP64
-// partials, added in a fixed order by a one-block-per-matrix launch after
-// the row kernel.  (Adding them in the matrix's last block instead needs a
-// device-scope release per block, which on this part writes back the L2:
-// that made the whiten launch six times slower.)
+// partials, added in a fixed order: ||V||^2 by a one-block-per-matrix
+// launch after the whiten, ||U||^2 (a few dozen partials) by every block of
+// mapback_apply for itself.  (Adding them in the matrix's last block
+// instead needs a device-scope release per block, which on this part
+// writes back the L2: that made the whiten launch six times slower.)
 //
 // whiten        two passes per row: momentum update, u_i = b_i sum_j S_ij a_j z_j
 //               and the row's ||V_i||^2 in closed form
@@ -214,11 +215,10 @@ __host__ __device__ inline int64_t mapback_blocks(const Job &j) { return ceil_di
 template <typename Job>
 __host__ __device__ inline int64_t norm_blocks(const Job &j) { return ceil_div(j.d.rows, kRowThreads / 4); }
 
-// One block per job, after the whiten (which = kCstFro) or mapback_norm
-// (kCstU): the FP64 sums of the job's per-block partials (thread t takes
-// partials t, t + 256, ..., then a fixed-order block sum).  After the
-// whiten it also forms the rank-one constants sum z^2 and sum (a z)^2, and
-// ||V||^2 = sum b^2 |S a|^2 + (2 kappa + kappa^2 sum z^2) sum u^2 from the
+// One block per job, after the whiten: the FP64 sums of the job's
+// per-block partials (thread t takes partials t, t + 256, ..., then a
+// fixed-order block sum), the rank-one constants sum z^2 and sum (a z)^2,
+// and ||V||^2 = sum b^2 |S a|^2 + (2 kappa + kappa^2 sum z^2) sum u^2 from the
 // whiten's two partials.
 constexpr int kTotalThreads = 256;
 constexpr int kTotalUnroll = 12;  // column loads in flight per thread (3072 columns in one pass)
@@ -243,14 +243,13 @@ __device__ __forceinline__ void block_sums(double (&v)[N], double (*scratch)[kTo
   }
 }
 
-__global__ void __launch_bounds__(kTotalThreads) matrix_total_kernel(const MatJob *jobs, int which) {
+__global__ void __launch_bounds__(kTotalThreads) matrix_total_kernel(const MatJob *jobs) {
   __shared__ double scratch[4][kTotalThreads / 64];
   const DevJob J = load_job(jobs, blockIdx.x);
   const DevDesc &d = J.d;
-  const bool fro = which == kCstFro;
-  const SMX_GLOBAL double *parts = fro ? J.fro : J.mb;
-  const int64_t nblk = fro ? whiten_blocks(J) : norm_blocks(J);
-  const bool r1 = fro && d.z != nullptr;  // uniform per block
+  const SMX_GLOBAL double *parts = J.fro;
+  const int64_t nblk = whiten_blocks(J);
+  const bool r1 = d.z != nullptr;  // uniform per block
   // Every load of the thread first (partials, then z and a), then the sums.
   double s[4] = {0.0, 0.0, 0.0, 0.0};  // partials (kind 0, kind 1), sum z^2, sum (a z)^2
   for (int64_t k0 = threadIdx.x; k0 < nblk; k0 += kTotalThreads * 4) {
@@ -259,7 +258,7 @@ __global__ void __launch_bounds__(kTotalThreads) matrix_total_kernel(const MatJo
     for (int u = 0; u < 4; ++u) {
       const int64_t k = k0 + kTotalThreads * u;
       v[0][u] = k < nblk ? parts[k] : 0.0;
-      v[1][u] = fro && k < nblk ? parts[nblk + k] : 0.0;
+      v[1][u] = k < nblk ? parts[nblk + k] : 0.0;
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -286,10 +285,6 @@ __global__ void __launch_bounds__(kTotalThreads) matrix_total_kernel(const MatJo
   }
   block_sums<4>(s, scratch);
   if (threadIdx.x != 0) return;
-  if (!fro) {
-    J.cst[kCstU] = s[0];
-    return;
-  }
   // s[0] = sum b^2 |S a|^2, s[1] = sum u^2
   const double kappa = r1 ? d.kappa[0] : 0.0;
   J.cst[kCstZZ] = s[2];
@@ -1043,7 +1038,17 @@ __global__ void __launch_bounds__(kRowThreads) mapback_apply_kernel(JobRange ran
   if (p.i >= d.rows) return;
   const int pdt = d.param_dtype;
   const SMX_GLOBAL float *q = J.q + p.i * J.pcol_pad;
-  const double n2 = J.cst[kCstU];
+  // ||U||^2 from mapback_norm's per-block partials, added by every wave in
+  // the same fixed order (lane l takes partials l, l + 64, ..., then the
+  // wave sum), so that every block of the matrix scales by the same value
+  // (a separate one-block-per-matrix launch for this sum cost more than
+  // these few cached loads).
+  double n2 = 0.0;
+  {
+    const int64_t nb = norm_blocks(J);
+    for (int64_t k = threadIdx.x & 63; k < nb; k += 64) n2 += J.mb[k];
+    n2 = wave_sum(n2);
+  }
   const float norm = static_cast<float>(sqrt(n2));
   // _graft_direction: sqrt(rows) / max(||U||, FLT_MIN); a zero direction
   // gives a zero update.
@@ -1172,8 +1177,8 @@ static int launch_range(const MatJob *host, MatJob *table, int32_t first, int32_
   return SMX_OK;
 }
 
-static int matrix_totals(MatJob *table, int32_t m, int which, hipStream_t st) {
-  hipLaunchKernelGGL(matrix_total_kernel, dim3(static_cast<unsigned>(m)), dim3(kTotalThreads), 0, st, table, which);
+static int matrix_totals(MatJob *table, int32_t m, hipStream_t st) {
+  hipLaunchKernelGGL(matrix_total_kernel, dim3(static_cast<unsigned>(m)), dim3(kTotalThreads), 0, st, table);
   return check_launch("matrix_total");
 }
 
@@ -1299,13 +1304,12 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
                              kFlipThreads, "whiten", st)
               : launch_range(h, table, n_kept, m - n_kept, whiten_blocks, whiten_flip_kernel<false>,
                              kFlipThreads, "whiten", st);
-    if (!rc) rc = matrix_totals(table, m, kCstFro, st);
+    if (!rc) rc = matrix_totals(table, m, st);
     plan.layout.rowsums = 1;
     if (!rc) rc = run_s8_stages(plan.layout, st);
     if (!rc)
       rc = r1 ? launch_range(h, table, 0, m, norm_blocks, mapback_norm_kernel<true>, kRowThreads, "mapback_norm", st)
               : launch_range(h, table, 0, m, norm_blocks, mapback_norm_kernel<false>, kRowThreads, "mapback_norm", st);
-    if (!rc) rc = matrix_totals(table, m, kCstU, st);
     if (!rc)
       rc = r1 ? launch_range(h, table, 0, m, mapback_blocks, mapback_apply_kernel<true>, kRowThreads, "mapback_apply",
                              st)
