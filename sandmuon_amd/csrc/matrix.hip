@@ -48,6 +48,8 @@ namespace smx {
 
 constexpr int kRowThreads = 256;   // row kernels: 4 waves
 constexpr int kMaxSlices = 3;      // float4 per lane per row kept in registers
+constexpr int kKeptSlices = 8;     // whiten_rows_kept: float4 of y per lane (4 waves: 8192 columns)
+constexpr int kKeptBatch = 4;      // whiten_rows_kept: slices' loads in flight together
 constexpr int kFlipRows = 16;      // transposed whiten: rows per block (one K group)
 constexpr int kFlipThreads = 64 * kFlipRows;
 constexpr int kFlipChunk = 256 * kMaxSlices;  // transposed whiten: columns per LDS chunk
@@ -668,7 +670,91 @@ __device__ __forceinline__ void whiten_rows_single(const DevJob &J, int blk, dou
   block_part(J, vy, vu, p, blk, static_cast<int>(whiten_blocks(J)), J.fro, rp);
 }
 
+// Rows of more than kMaxSlices float4 per lane with the float4 path whose
+// padded row is at most kKeptSlices float4 per lane (4 waves per row: up
+// to 8192 columns): pass 1 keeps y = S a of every slice in registers, so
+// pass 2 forms V without reading g and m' again (24 -> 16 bytes per
+// element).  Loads go kKeptBatch slices at a time.
 template <bool R1>
+__device__ __forceinline__ void whiten_rows_kept(const DevJob &J, int blk, double (*red)[4], double (*rp)[4]) {
+  const DevDesc &d = J.d;
+  const RowPos p = row_pos(J, blk);
+  const bool live = p.i < d.rows;
+  const float beta = static_cast<float>(d.momentum_beta), omb = static_cast<float>(1.0 - d.momentum_beta);
+  const float kappa = R1 ? d.kappa[0] : 0.f;
+  const bool planes = J.planes != 0;
+  const int n4 = static_cast<int>(d.cols / 4), pc4 = static_cast<int>(J.pcol_pad / 4);
+  SMX_GLOBAL float *mrow = d.momentum + p.i * d.cols;
+  const SMX_GLOBAL float *grow = (const SMX_GLOBAL float *)d.grad + p.i * d.cols;
+  float4 y[kKeptSlices];
+  float y2 = 0.f, yz = 0.f;
+#pragma unroll
+  for (int t0 = 0; t0 < kKeptSlices; t0 += kKeptBatch) {
+    float4 g[kKeptBatch], m[kKeptBatch], a[kKeptBatch], z[kKeptBatch];
+#pragma unroll
+    for (int tb = 0; tb < kKeptBatch; ++tb) {
+      const int q = p.q0 + p.span * (t0 + tb);
+      if (live && q < n4) {
+        g[tb] = ld4(grow, q);
+        m[tb] = ld4(mrow, q);
+        a[tb] = ld4(d.inv_col, q);
+        if constexpr (R1) z[tb] = ld4(d.z, q);
+      }
+    }
+#pragma unroll
+    for (int tb = 0; tb < kKeptBatch; ++tb) {
+      const int q = p.q0 + p.span * (t0 + tb);
+      float4 yy = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (live && q < n4) {
+        const float4 gg = g[tb], aa = a[tb];
+        float4 mm = m[tb];
+        mm.x = fmaf(mm.x, beta, gg.x * omb); mm.y = fmaf(mm.y, beta, gg.y * omb);
+        mm.z = fmaf(mm.z, beta, gg.z * omb); mm.w = fmaf(mm.w, beta, gg.w * omb);
+        st4(mrow, q, mm);
+        yy.x = fmaf(mm.x, beta, gg.x * omb) * aa.x; yy.y = fmaf(mm.y, beta, gg.y * omb) * aa.y;
+        yy.z = fmaf(mm.z, beta, gg.z * omb) * aa.z; yy.w = fmaf(mm.w, beta, gg.w * omb) * aa.w;
+        y2 = fmaf(yy.x, yy.x, fmaf(yy.y, yy.y, fmaf(yy.z, yy.z, fmaf(yy.w, yy.w, y2))));
+        if constexpr (R1) {
+          const float4 zz = z[tb];
+          yz = fmaf(yy.x, zz.x, fmaf(yy.y, zz.y, fmaf(yy.z, zz.z, fmaf(yy.w, zz.w, yz))));
+        }
+      }
+      y[t0 + tb] = yy;
+    }
+  }
+  double v[2] = {static_cast<double>(wave_sum(y2)), static_cast<double>(wave_sum(yz))};
+  row_sums<2>(v, red, p, J.wpr);
+  double vy = 0.0, vu = 0.0;  // the row's b^2 |S a|^2 and u^2
+  float b = 0.f, ku = 0.f;
+  if (live) {
+    const double bd = d.inv_row[p.i];
+    const double u = bd * v[1];
+    b = d.inv_row[p.i];
+    ku = R1 ? kappa * static_cast<float>(u) : 0.f;
+    vy = bd * bd * v[0];
+    vu = u * u;
+    if ((threadIdx.x & 63) == 0 && p.wr == 0) J.u[p.i] = static_cast<float>(u);
+  }
+  // V_ij = b_i y_j + kappa u_i z_j, zeros in padding rows and columns.  q
+  // has the parity of the lane and pc4 is even, so both lanes of a pair
+  // are inside the padded row or both outside.
+#pragma unroll
+  for (int t = 0; t < kKeptSlices; ++t) {
+    const int q = p.q0 + p.span * t;
+    if (q >= pc4) continue;
+    float w[4] = {0.f, 0.f, 0.f, 0.f};
+    if (live && q < n4) {
+      float4 zz = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (R1) zz = ld4(d.z, q);
+      w[0] = fmaf(ku, zz.x, b * y[t].x); w[1] = fmaf(ku, zz.y, b * y[t].y);
+      w[2] = fmaf(ku, zz.z, b * y[t].z); w[3] = fmaf(ku, zz.w, b * y[t].w);
+    }
+    put_operand4_paired(J.x, tiled_index(p.i, 4 * static_cast<int64_t>(q), J.pcol_pad), w, planes, true);
+  }
+  block_part(J, vy, vu, p, blk, static_cast<int>(whiten_blocks(J)), J.fro, rp);
+}
+
+template <bool R1, bool WIDE>
 __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
   __shared__ double red[2][4][4];  // row sums over the waves of a row
   __shared__ double rp[2][4];
@@ -676,7 +762,9 @@ __global__ void __launch_bounds__(kRowThreads) whiten_kernel(JobRange range) {
   const int jid = find_job(range, blockIdx.x);
   const DevJob J = load_job(range.jobs, jid);
   const int blk = blockIdx.x - range.start[jid];
-  if (whiten_pipelined(J))
+  if constexpr (WIDE)
+    whiten_rows_kept<R1>(J, blk, red[0], rp);
+  else if (whiten_pipelined(J))
     whiten_rows_pipelined<R1>(J, blk, red, rp, xs);
   else
     whiten_rows_single<R1>(J, blk, red[0], rp);
@@ -1239,21 +1327,33 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
                  slot.data()))
       return fail(SMX_EINVAL, "matrix_step: internal shape grouping error");
     MatJob *table = reinterpret_cast<MatJob *>(static_cast<char *>(workspace) + plan.bytes);
-    // Table order: parameters kept as they are, then transposed ones whose
-    // rows fit one LDS chunk with the float4 path, then the other transposed
-    // ones (one whiten launch each); both mapback launches take the whole
-    // table.
+    // Table order (one whiten launch each): parameters kept as they are,
+    // except those of the next bucket; parameters kept as they are whose
+    // wide rows leave y in registers (whiten_rows_kept); transposed ones
+    // whose rows fit one LDS chunk with the float4 path; the other
+    // transposed ones.  Both mapback launches take the whole table.
     std::vector<MatJob> jobs;
     jobs.reserve(m);
     int32_t n_plain = 0, n_kept = 0;
-    auto flip_kept = [&](int32_t k) {
+    auto vec_path = [&](int32_t k) {  // the float4 path of the whiten kernels
       const smx_matrix_desc &d = descs[g[k]];
-      return d.cols % 4 == 0 && d.cols <= kFlipChunk && d.grad_dtype == SMX_F32 && aligned16(d.grad) &&
-             aligned16(d.momentum) && aligned16(d.inv_col) && (!r1 || aligned16(d.z));
+      return d.cols % 4 == 0 && d.grad_dtype == SMX_F32 && aligned16(d.grad) && aligned16(d.momentum) &&
+             aligned16(d.inv_col) && (!r1 || aligned16(d.z));
     };
-    for (int pass = 0; pass < 3; ++pass) {
+    auto plain_kept = [&](int32_t k) {  // whiten_rows_kept: y of the padded row fits the registers
+      int32_t wpr, slices;
+      row_geometry(descs[g[k]].cols, wpr, slices);
+      const S8Mat M{plan.layout.cls[cls[k]], slot[k]};
+      return vec_path(k) && slices > kMaxSlices && ceil_div(M.pcol_pad() / 4, 64 * wpr) <= kKeptSlices;
+    };
+    auto bucket = [&](int32_t k) {
+      if (!fl[k]) return plain_kept(k) ? 1 : 0;
+      return vec_path(k) && descs[g[k]].cols <= kFlipChunk ? 2 : 3;
+    };
+    int32_t n_wide = 0;
+    for (int pass = 0; pass < 4; ++pass) {
       for (int32_t k = 0; k < m; ++k) {
-        if (pass != (!fl[k] ? 0 : flip_kept(k) ? 1 : 2)) continue;
+        if (pass != bucket(k)) continue;
         const S8Mat M{plan.layout.cls[cls[k]], slot[k]};
         MatJob j{};
         j.d = descs[g[k]];
@@ -1277,7 +1377,8 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
         j.mvec = j.cvec && j.d.param_dtype == SMX_F32 && aligned16(j.d.param);
         jobs.push_back(j);
         n_plain += pass == 0;
-        n_kept += pass <= 1;
+        n_wide += pass <= 1;
+        n_kept += pass <= 2;
       }
     }
     for (int32_t b = 0; b < m; b += kPrepBatch) {
@@ -1292,12 +1393,19 @@ extern "C" int smx_matrix_step(const smx_matrix_desc *descs, int32_t n, int mode
     // The kernels are specialised on whether the matrices carry a rank-one
     // term (all of a call or none, checked above).
     const MatJob *h = jobs.data();
-    int rc = r1 ? launch_range(h, table, 0, n_plain, whiten_blocks, whiten_kernel<true>, kRowThreads, "whiten", st)
-                : launch_range(h, table, 0, n_plain, whiten_blocks, whiten_kernel<false>, kRowThreads, "whiten", st);
-    if (!rc && n_kept > n_plain)
-      rc = r1 ? launch_range(h, table, n_plain, n_kept - n_plain, whiten_blocks, whiten_flip_kept_kernel<true>,
+    int rc = r1 ? launch_range(h, table, 0, n_plain, whiten_blocks, whiten_kernel<true, false>, kRowThreads,
+                               "whiten", st)
+                : launch_range(h, table, 0, n_plain, whiten_blocks, whiten_kernel<false, false>, kRowThreads,
+                               "whiten", st);
+    if (!rc && n_wide > n_plain)
+      rc = r1 ? launch_range(h, table, n_plain, n_wide - n_plain, whiten_blocks, whiten_kernel<true, true>,
+                             kRowThreads, "whiten", st)
+              : launch_range(h, table, n_plain, n_wide - n_plain, whiten_blocks, whiten_kernel<false, true>,
+                             kRowThreads, "whiten", st);
+    if (!rc && n_kept > n_wide)
+      rc = r1 ? launch_range(h, table, n_wide, n_kept - n_wide, whiten_blocks, whiten_flip_kept_kernel<true>,
                              kFlipThreads, "whiten", st)
-              : launch_range(h, table, n_plain, n_kept - n_plain, whiten_blocks, whiten_flip_kept_kernel<false>,
+              : launch_range(h, table, n_wide, n_kept - n_wide, whiten_blocks, whiten_flip_kept_kernel<false>,
                              kFlipThreads, "whiten", st);
     if (!rc && m > n_kept)
       rc = r1 ? launch_range(h, table, n_kept, m - n_kept, whiten_blocks, whiten_flip_kernel<true>,
