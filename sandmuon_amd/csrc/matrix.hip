@@ -49,7 +49,8 @@ namespace smx {
 constexpr int kRowThreads = 256;   // row kernels: 4 waves
 constexpr int kMaxSlices = 3;      // float4 per lane per row kept in registers
 constexpr int kKeptSlices = 8;     // whiten_rows_kept: float4 of y per lane (4 waves: 8192 columns)
-constexpr int kKeptBatch = 4;      // whiten_rows_kept: slices' loads in flight together
+constexpr int kKeptBatch = 8;      // whiten_rows_kept: slices' loads in flight together (all: 1756 us per
+                                   // cfg5 launch at 161 VGPRs, against 1881 with 4 and 1963 with 2)
 constexpr int kFlipRows = 16;      // transposed whiten: rows per block (one K group)
 constexpr int kFlipThreads = 64 * kFlipRows;
 constexpr int kFlipChunk = 256 * kMaxSlices;  // transposed whiten: columns per LDS chunk
@@ -674,7 +675,7 @@ __device__ __forceinline__ void whiten_rows_single(const DevJob &J, int blk, dou
 // padded row is at most kKeptSlices float4 per lane (4 waves per row: up
 // to 8192 columns): pass 1 keeps y = S a of every slice in registers, so
 // pass 2 forms V without reading g and m' again (24 -> 16 bytes per
-// element).  Loads go kKeptBatch slices at a time.
+// element).  Loads go kKeptBatch slices at a time (every slice at once).
 template <bool R1>
 __device__ __forceinline__ void whiten_rows_kept(const DevJob &J, int blk, double (*red)[4], double (*rp)[4]) {
   const DevDesc &d = J.d;
